@@ -1,0 +1,372 @@
+/*
+ * sgl_rocm_kv.h -- C ABI of the MI355X (gfx950) KV-cache transfer path.
+ *
+ * The library (libsgl_rocm_kv.so) is the ROCm backend of sglang-rs's KV
+ * copy path. It has two groups of entry points:
+ *
+ *  1. Host mirror of the reference's KV layout arithmetic and copy plan
+ *     (no GPU needed). The reference keeps these in Rust; they are exported
+ *     here so that the C++ launcher, the Python binding and the tests share
+ *     one implementation of the validation rules the kernels rely on.
+ *  2. Kernel entry points. Kernels are hand-written HIP, compiled ahead of
+ *     time into a gfx950 code object (sgl_rocm_kv_gfx950.co) and loaded with
+ *     hipModuleLoad. libamdhip64 is resolved with dlopen at sgl_rocm_kv_init,
+ *     so the library loads (and group 1 works) on a host without a GPU.
+ *
+ * Conventions
+ *  - Every function returns an sgl_kv_status. On failure, the calling
+ *    thread's detail record (sgl_kv_last_error) holds the reference error
+ *    variant's fields. No exception, panic or abort crosses the ABI.
+ *  - All buffers are borrowed: the caller owns every device allocation and
+ *    passes plain device pointers with their byte lengths. The context owns
+ *    only the loaded module and a 4-byte device error flag.
+ *  - Streams are explicit (hipStream_t passed as void*; NULL is the null
+ *    stream). The pair scatter/gather drop-ins synchronise the stream and
+ *    read the error flag like the reference; the per-layer transfer calls are
+ *    asynchronous and report device-side errors through
+ *    sgl_rocm_kv_check_errors.
+ *  - One context per device. Calls on one context must not overlap in time
+ *    from different host threads (the reference takes &mut self).
+ */
+#ifndef SGL_ROCM_KV_H
+#define SGL_ROCM_KV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SGL_ROCM_KV_ABI_VERSION 1
+
+/* ------------------------------------------------------------------------ */
+/* Status codes                                                             */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * 1..12 mirror CudaKvPairCopyError (crates/sglang-kernel/src/cuda_kv_kernels.rs:304-338)
+ * plus the allocation range check of CudaDeviceAllocation::device_ptr_at
+ * (crates/sglang-kernel/src/cuda.rs:895-916). 20..36 mirror
+ * PagedKvCacheLayoutError (crates/sglang-srt/src/kv_cache.rs:256-318). 40..45
+ * mirror KvCacheTransferPlanError (crates/sglang-srt/src/transfer.rs:722-750).
+ * 50.. are device-side conditions of the per-layer transfer kernels.
+ */
+typedef enum sgl_kv_status {
+    SGL_KV_OK = 0,
+    SGL_KV_ZERO_DIMENSION = 1,                  /* name = dimension */
+    SGL_KV_SHAPE_OVERFLOW = 2,
+    SGL_KV_DIMENSION_TOO_LARGE = 3,             /* name, a = value, b = maximum */
+    SGL_KV_ROW_STRIDE_TOO_SMALL = 4,            /* name = tensor, a = row_bytes, b = row_stride_bytes */
+    SGL_KV_TENSOR_PAGE_REGION_OUT_OF_BOUNDS = 5,/* name = tensor, a = offset, b = tensor_page_bytes, c = page_stride_bytes */
+    SGL_KV_TENSOR_PAGE_REGIONS_OVERLAP = 6,     /* a = key_offset, b = value_offset, c = tensor_page_bytes */
+    SGL_KV_DEVICE_MISMATCH = 7,                 /* name = allocation, a = expected, b = actual ordinal */
+    SGL_KV_DEVICE_SLOT_INDEX_OUT_OF_RANGE = 8,  /* a = slot_count */
+    SGL_KV_HIP = 9,                             /* a = hipError_t, name = HIP call */
+    SGL_KV_MODULE = 10,                         /* code object / libamdhip64 could not be loaded or resolved */
+    SGL_KV_ALLOCATION_OUT_OF_BOUNDS = 11,       /* name = buffer, a = offset, b = byte_len, c = allocation_byte_len */
+    SGL_KV_INVALID_ARGUMENT = 12,               /* name = argument */
+
+    SGL_KV_LAYOUT_ZERO_PAGE_COUNT = 20,
+    SGL_KV_LAYOUT_ZERO_FIELD = 21,              /* name = field */
+    SGL_KV_LAYOUT_RUNTIME_PAGE_SIZE_MISMATCH = 22, /* a = expected, b = actual */
+    SGL_KV_LAYOUT_UNEVEN_LAYER = 23,            /* a = bytes_per_token, b = num_layers */
+    SGL_KV_LAYOUT_UNEVEN_TENSOR = 24,           /* a = bytes_per_token_per_layer, b = kv_tensors_per_token */
+    SGL_KV_LAYOUT_SIZE_OVERFLOW = 25,
+    SGL_KV_LAYOUT_PAGE_OUT_OF_RANGE = 26,       /* a = page_index, b = page_count */
+    SGL_KV_LAYOUT_LAYER_OUT_OF_RANGE = 27,      /* a = layer_index, b = layer_count */
+    SGL_KV_LAYOUT_TENSOR_OUT_OF_RANGE = 28,     /* a = tensor_index, b = tensor_count */
+    SGL_KV_LAYOUT_TOKEN_OUT_OF_RANGE = 29,      /* a = token_index, b = page_size */
+    SGL_KV_LAYOUT_SLOT_OUT_OF_RANGE = 30,       /* a = slot_index, b = slot_count */
+    SGL_KV_LAYOUT_EMPTY_SLOT_MAP = 31,
+    SGL_KV_LAYOUT_BATCH_SLOT_OUT_OF_RANGE = 32, /* a = batch_index, b = slot_index, c = slot_count */
+    SGL_KV_LAYOUT_KV_PAIR_REQUIRES_TWO_TENSORS = 33,     /* a = tensor_count */
+    SGL_KV_LAYOUT_TENSOR_PAIR_REQUIRES_TWO_TENSORS = 34, /* a = tensor_count */
+    SGL_KV_LAYOUT_TENSOR_PAIR_SIZE_MISMATCH = 35, /* a = bytes_per_token_per_layer, b = key, c = value token bytes */
+    SGL_KV_LAYOUT_UNEVEN_KV_PAIR_COPY = 36,     /* a = key_token_bytes, b = value_token_bytes */
+
+    SGL_KV_PLAN_ZERO_PAGE_SIZE = 40,
+    SGL_KV_PLAN_CACHE_PAGE_COUNT_MISMATCH = 41, /* a = request index, b = input_token_count, c = cache_page_count */
+    SGL_KV_PLAN_TRAILING_CACHE_PAGES = 42,      /* a = consumed, b = cache_page_count */
+    SGL_KV_PLAN_UNALIGNED_TOKEN_OFFSET = 43,    /* a = request index, b = token_offset, c = page_size */
+    SGL_KV_PLAN_UNALIGNED_CACHE_SLOT = 44,      /* a = request index, b = cache_slot, c = page_size */
+    SGL_KV_PLAN_NON_CONTIGUOUS_CACHE_SLOTS = 45,/* a = request index, b = expected, c = actual */
+
+    SGL_KV_DEVICE_PAGE_INDEX_OUT_OF_RANGE = 50, /* a page-table entry is negative, past the table or past the pool */
+    SGL_KV_DEVICE_SPAN_OUT_OF_RANGE = 51        /* a row is not covered by its span list */
+} sgl_kv_status;
+
+/* Detail of the calling thread's most recent failure. */
+typedef struct sgl_kv_error_detail {
+    int32_t code;          /* sgl_kv_status */
+    int32_t reserved;
+    uint64_t a, b, c;      /* variant fields, in the order listed above */
+    char name[64];         /* dimension / tensor / field / allocation / call name */
+    char message[320];     /* human-readable text, as the reference's Display impl */
+} sgl_kv_error_detail;
+
+void sgl_kv_last_error(sgl_kv_error_detail *out);
+const char *sgl_kv_status_name(int32_t code);
+
+/* ------------------------------------------------------------------------ */
+/* Group 1: layout and plan (host only)                                      */
+/* ------------------------------------------------------------------------ */
+
+/* KvCacheDtype (crates/sglang-srt/src/kv_cache.rs:7-14). */
+typedef enum sgl_kv_dtype {
+    SGL_KV_DTYPE_AUTO = 0,
+    SGL_KV_DTYPE_FLOAT32 = 1,
+    SGL_KV_DTYPE_BFLOAT16 = 2,
+    SGL_KV_DTYPE_FP8_E4M3 = 3,
+    SGL_KV_DTYPE_FP8_E5M2 = 4,
+    SGL_KV_DTYPE_FP4_E2M1 = 5
+} sgl_kv_dtype;
+
+/* KvCacheDtype::bytes_per_element (kv_cache.rs:39-46): 0 when the width
+ * needs model metadata (fp4). */
+size_t sgl_kv_dtype_bytes_per_element(int32_t dtype);
+
+/* KvCacheRuntimeLayout (kv_cache.rs:57-66). */
+typedef struct sgl_kv_runtime_layout {
+    int32_t dtype;
+    int32_t reserved;
+    uint64_t page_size;
+    uint64_t num_layers;
+    uint64_t kv_heads;
+    uint64_t head_dim;
+    uint64_t kv_tensors_per_token;
+    uint64_t bytes_per_token;
+    uint64_t page_size_bytes;
+} sgl_kv_runtime_layout;
+
+/* PagedKvCacheLayout (kv_cache.rs:437-445): page -> layer -> tensor -> token. */
+typedef struct sgl_kv_paged_layout {
+    sgl_kv_runtime_layout runtime;
+    uint64_t page_count;
+    uint64_t bytes_per_token_per_layer;
+    uint64_t bytes_per_layer_page;
+    uint64_t tensor_pair;          /* 0 = Uniform geometry, 1 = explicit Pair */
+    uint64_t token_bytes[2];       /* per-tensor token width; Uniform: both = token_bytes */
+    uint64_t tensor_page_bytes;    /* Uniform: page_bytes; Pair: key_page_bytes */
+    uint64_t total_byte_len;
+    uint64_t slot_count;
+} sgl_kv_paged_layout;
+
+/* PagedKvCacheLayout::new (kv_cache.rs:448-478). */
+int32_t sgl_kv_paged_layout_new(const sgl_kv_runtime_layout *runtime, uint64_t page_count,
+                                sgl_kv_paged_layout *out);
+/* PagedKvCacheLayout::new_with_tensor_pair (kv_cache.rs:480-529). */
+int32_t sgl_kv_paged_layout_new_with_tensor_pair(const sgl_kv_runtime_layout *runtime,
+                                                 uint64_t page_count, uint64_t key_token_bytes,
+                                                 uint64_t value_token_bytes,
+                                                 sgl_kv_paged_layout *out);
+/* PagedKvCacheLayout::page_byte_range (kv_cache.rs:639-651); [start, end). */
+int32_t sgl_kv_paged_layout_page_byte_range(const sgl_kv_paged_layout *layout, uint64_t page_index,
+                                            uint64_t *start, uint64_t *end);
+/* PagedKvCacheLayout::tensor_token_byte_range (kv_cache.rs:653-700). */
+int32_t sgl_kv_paged_layout_tensor_token_byte_range(const sgl_kv_paged_layout *layout,
+                                                    uint64_t page_index, uint64_t layer_index,
+                                                    uint64_t tensor_index, uint64_t token_index,
+                                                    uint64_t *start, uint64_t *end);
+/* PagedKvCacheLayout::tensor_slot_byte_range (kv_cache.rs:702-720). */
+int32_t sgl_kv_paged_layout_tensor_slot_byte_range(const sgl_kv_paged_layout *layout,
+                                                   uint64_t layer_index, uint64_t tensor_index,
+                                                   uint64_t slot_index, uint64_t *start,
+                                                   uint64_t *end);
+/* PagedKvCacheLayout::validate_slot_indices (kv_cache.rs:722-736); host slots. */
+int32_t sgl_kv_paged_layout_validate_slot_indices(const sgl_kv_paged_layout *layout,
+                                                  const uint64_t *slots, uint64_t slot_len);
+
+/* CudaKvPairCopyLayout (crates/sglang-kernel/src/cuda_kv_kernels.rs:106-128). */
+typedef struct sgl_kv_pair_copy_layout {
+    uint64_t page_size;
+    uint64_t page_stride_bytes;
+    uint64_t key_in_page_offset;
+    uint64_t value_in_page_offset;
+    uint64_t row_bytes;
+} sgl_kv_pair_copy_layout;
+
+/* PagedKvCacheLayout::kv_pair_copy_geometry (kv_cache.rs:738-777), returned
+ * directly as the copy layout it feeds (cuda_kv_cache.rs:510-532). */
+int32_t sgl_kv_paged_layout_kv_pair_copy_geometry(const sgl_kv_paged_layout *layout,
+                                                  uint64_t layer_index,
+                                                  sgl_kv_pair_copy_layout *out);
+
+/* CudaKvPairCopyPlan (cuda_kv_kernels.rs:153-164). grid_x / rows_per_tile
+ * describe this library's launch, not the reference's byte-per-thread grid. */
+typedef struct sgl_kv_pair_copy_plan {
+    uint64_t row_count;
+    uint64_t slot_count;
+    sgl_kv_pair_copy_layout layout;
+    uint64_t key_row_stride_bytes;
+    uint64_t value_row_stride_bytes;
+    uint64_t key_rows_required_bytes;
+    uint64_t value_rows_required_bytes;
+    uint64_t slot_indices_required_bytes;
+    uint64_t pool_required_bytes;
+} sgl_kv_pair_copy_plan;
+
+/* CudaKvPairCopyPlan::new (cuda_kv_kernels.rs:167-264): same validation
+ * order, same errors, same required-byte arithmetic. */
+int32_t sgl_kv_pair_copy_plan_new(uint64_t row_count, uint64_t slot_count,
+                                  const sgl_kv_pair_copy_layout *layout,
+                                  uint64_t key_row_stride_bytes, uint64_t value_row_stride_bytes,
+                                  sgl_kv_pair_copy_plan *out);
+
+/* transfer_page_indices (crates/sglang-srt/src/transfer.rs:679-720): splits
+ * one request's cache slots into pages. `out_pages` needs
+ * ceil(slot_len / page_size) entries; *out_len receives the count.
+ * `request_index` is echoed in error details (the reference carries the
+ * request id). */
+int32_t sgl_kv_transfer_page_indices(uint64_t request_index, uint64_t token_offset,
+                                     const uint64_t *cache_slots, uint64_t slot_len,
+                                     uint64_t page_size, uint64_t *out_pages, uint64_t *out_len);
+
+/* ------------------------------------------------------------------------ */
+/* Group 2: kernels                                                         */
+/* ------------------------------------------------------------------------ */
+
+typedef struct sgl_rocm_kv_ctx sgl_rocm_kv_ctx;
+
+/* Replaces CudaKvPairCopyKernels::compile (cuda_kv_kernels.rs:447-469):
+ * no runtime compilation; loads the prebuilt gfx950 code object from
+ * `code_object_path` (NULL: sgl_rocm_kv_gfx950.co beside the library) on
+ * `device`, resolves every kernel and allocates + zeroes the error flag.
+ * The library holds no per-process HIP state beyond the dlopen handle. */
+int32_t sgl_rocm_kv_init(int32_t device, const char *code_object_path, sgl_rocm_kv_ctx **out);
+/* Replaces the Drop of CudaKvPairCopyKernels / CudaModule (cuda.rs:693-708,
+ * 933-939): unloads the module and frees the flag. NULL is accepted. */
+int32_t sgl_rocm_kv_destroy(sgl_rocm_kv_ctx *ctx);
+/* CudaContext::device_ordinal for the context. */
+int32_t sgl_rocm_kv_device(const sgl_rocm_kv_ctx *ctx);
+/* Number of compute units of the context's device (launch sizing, tests). */
+int32_t sgl_rocm_kv_cu_count(const sgl_rocm_kv_ctx *ctx);
+
+/* CudaDeviceAllocation's (device_ptr, byte_len) pair (cuda.rs:611-620). */
+typedef struct sgl_kv_device_buffer {
+    void *ptr;
+    uint64_t byte_len;
+} sgl_kv_device_buffer;
+
+/* CudaKvPairScatter / CudaKvPairGather (cuda_kv_kernels.rs:424-444). */
+typedef struct sgl_kv_pair_copy_buffers {
+    sgl_kv_device_buffer keys;
+    uint64_t keys_offset;
+    sgl_kv_device_buffer values;
+    uint64_t values_offset;
+    sgl_kv_device_buffer slot_indices; /* u64 physical slots, one per row */
+    uint64_t slot_indices_offset;
+    sgl_kv_device_buffer pool;
+    uint64_t pool_offset;
+} sgl_kv_pair_copy_buffers;
+
+/* CudaKvPairCopyKernels::scatter (cuda_kv_kernels.rs:471-504, launch
+ * :541-623): strided K/V rows -> pool slots. Checks each buffer's device and
+ * range, clears the flag, launches on `stream`, synchronises `stream` and
+ * returns SGL_KV_DEVICE_SLOT_INDEX_OUT_OF_RANGE when any slot was >=
+ * slot_count (those rows are skipped, as in the reference). */
+int32_t sgl_rocm_kv_pair_scatter(sgl_rocm_kv_ctx *ctx, const sgl_kv_pair_copy_plan *plan,
+                                 const sgl_kv_pair_copy_buffers *buffers, void *stream);
+/* CudaKvPairCopyKernels::gather (cuda_kv_kernels.rs:506-539): pool slots ->
+ * strided K/V rows. Same contract as sgl_rocm_kv_pair_scatter. */
+int32_t sgl_rocm_kv_pair_gather(sgl_rocm_kv_ctx *ctx, const sgl_kv_pair_copy_plan *plan,
+                                const sgl_kv_pair_copy_buffers *buffers, void *stream);
+
+/* --- per-layer PD transfer (pack / unpack) ------------------------------ */
+
+typedef enum sgl_kv_head_layout {
+    SGL_KV_NHD = 0, /* token-major: a (page, layer, tensor) region is [page_size][heads][dim] */
+    SGL_KV_HND = 1  /* head-major:  a (page, layer, tensor) region is [heads][page_size][dim] */
+} sgl_kv_head_layout;
+
+/* One layer of a page-major pool. The page -> layer -> tensor nesting and
+ * the byte offsets follow PagedKvCacheLayout::tensor_token_byte_range
+ * (kv_cache.rs:653-700); head_layout = HND only reorders bytes inside each
+ * (page, layer, tensor) region. Build it with sgl_kv_pool_view_for_layer. */
+typedef struct sgl_kv_pool_view {
+    void *base;                 /* device pointer to byte 0 of the pool */
+    uint64_t byte_len;          /* pool allocation length */
+    uint64_t page_size;         /* tokens per page */
+    uint64_t page_stride_bytes; /* page_size_bytes */
+    uint64_t page_count;
+    uint64_t tensor_offset[2];  /* in-page offset of this layer's tensor regions */
+    uint64_t row_bytes;         /* bytes per (token, tensor): heads * head_dim * element bytes */
+    uint32_t tensor_count;      /* 2 = K/V pair, 1 = single tensor (MLA latent row) */
+    uint32_t heads;             /* KV heads; HND splits a row into `heads` chunks */
+    uint32_t head_layout;       /* sgl_kv_head_layout */
+    uint32_t reserved;
+    float *scale;               /* optional device pointer to this layer's scale (fp8), or NULL */
+} sgl_kv_pool_view;
+
+/* Builds the view of `layer` for tensors [first_tensor, first_tensor +
+ * tensor_count). Errors: layer/tensor out of range; UnevenKvPairCopy when a
+ * two-tensor view spans unequal widths (kv_cache.rs:758-763). */
+int32_t sgl_kv_pool_view_for_layer(const sgl_kv_paged_layout *layout, void *base,
+                                   uint64_t byte_len, uint32_t head_layout, uint64_t layer_index,
+                                   uint64_t first_tensor, uint64_t tensor_count,
+                                   sgl_kv_pool_view *out);
+
+/* Contiguous transfer rows: row r of tensor t at planes[t] + r * row_stride[t]. */
+typedef struct sgl_kv_rows_view {
+    void *planes[2];
+    uint64_t plane_bytes[2];    /* allocation bytes available from planes[t] */
+    uint64_t row_stride[2];
+    float *scale;               /* optional device pointer to the transferred scale, or NULL */
+} sgl_kv_rows_view;
+
+/* A request's run of rows (transfer.rs:495-505, KvCacheTransferSpan):
+ * rows [row_start, row_start + token_count) hold request tokens
+ * [token_offset, token_offset + token_count); token k lives in page
+ * page_table[page_table_start + k / page_size] at in-page position
+ * k % page_size. */
+typedef struct sgl_kv_span {
+    uint32_t row_start;
+    uint32_t token_offset;
+    uint32_t token_count;
+    uint32_t page_table_start;
+} sgl_kv_span;
+
+/* How the rows of a transfer find their physical slots on one pool. Either
+ * a per-row slot map (the scheduler's out_cache_pages, model_executor.rs:
+ * 158-175) or spans + a page table (the decode side's dst_kv_indices,
+ * pd_bootstrap.rs:416-494). All pointers are device pointers. */
+typedef struct sgl_kv_token_map {
+    const uint64_t *slots;      /* one physical slot per row, or NULL to use spans */
+    uint64_t slots_len;
+    const int32_t *page_table;  /* physical page indices */
+    uint64_t page_table_len;
+    const sgl_kv_span *spans;   /* sorted by row_start */
+    uint32_t span_count;
+    uint32_t reserved;
+} sgl_kv_token_map;
+
+/* Pack (new; generalises sglang_gather_kv_pair_bytes,
+ * cuda_kv_kernels.rs:54-99): rows [0, row_count) of one layer, pool ->
+ * transfer rows. Asynchronous on `stream`. Device-side range failures skip
+ * the affected rows and set the context's error flag. */
+int32_t sgl_rocm_kv_pack_layer(sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src,
+                               const sgl_kv_token_map *src_map, uint64_t row_count,
+                               const sgl_kv_rows_view *dst, void *stream);
+/* Unpack (new; generalises sglang_scatter_kv_pair_bytes,
+ * cuda_kv_kernels.rs:11-52): transfer rows -> the decode pool under its own
+ * page size, head layout and page table. Asynchronous. */
+int32_t sgl_rocm_kv_unpack_layer(sgl_rocm_kv_ctx *ctx, const sgl_kv_rows_view *src,
+                                 uint64_t row_count, const sgl_kv_pool_view *dst,
+                                 const sgl_kv_token_map *dst_map, void *stream);
+/* Pool -> pool in one pass, for prefill and decode pools co-resident on one
+ * GPU (the composition unpack(pack(.)) without the transfer rows). */
+int32_t sgl_rocm_kv_transfer_layer(sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src,
+                                   const sgl_kv_token_map *src_map, uint64_t row_count,
+                                   const sgl_kv_pool_view *dst, const sgl_kv_token_map *dst_map,
+                                   void *stream);
+/* Synchronises `stream`, reads and clears the error flag, and maps it to
+ * SGL_KV_DEVICE_SLOT_INDEX_OUT_OF_RANGE / _PAGE_INDEX_ / _SPAN_ (the first
+ * raised in that order). Replaces the flag readback of
+ * cuda_kv_kernels.rs:613-621 for the asynchronous calls. */
+int32_t sgl_rocm_kv_check_errors(sgl_rocm_kv_ctx *ctx, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SGL_ROCM_KV_H */

@@ -10,8 +10,9 @@
  *     one implementation of the validation rules the kernels rely on.
  *  2. Kernel entry points. Kernels are hand-written HIP, compiled ahead of
  *     time into a gfx950 code object (sgl_rocm_kv_gfx950.co) and loaded with
- *     hipModuleLoad. libamdhip64 is resolved with dlopen at sgl_rocm_kv_init,
- *     so the library loads (and group 1 works) on a host without a GPU.
+ *     hipModuleLoad. The library links libamdhip64.so.7 but makes no HIP
+ *     call before sgl_rocm_kv_init, so it loads (and group 1 works) on a
+ *     host without a GPU.
  *
  * Conventions
  *  - Every function returns an sgl_kv_status. On failure, the calling
@@ -232,7 +233,9 @@ typedef struct sgl_rocm_kv_ctx sgl_rocm_kv_ctx;
  * no runtime compilation; loads the prebuilt gfx950 code object from
  * `code_object_path` (NULL: sgl_rocm_kv_gfx950.co beside the library) on
  * `device`, resolves every kernel and allocates + zeroes the error flag.
- * The library holds no per-process HIP state beyond the dlopen handle. */
+ * The library holds no per-process HIP state outside its contexts. Every
+ * call on a context makes its device current for the call's duration and
+ * restores the caller's device afterwards. */
 int32_t sgl_rocm_kv_init(int32_t device, const char *code_object_path, sgl_rocm_kv_ctx **out);
 /* Replaces the Drop of CudaKvPairCopyKernels / CudaModule (cuda.rs:693-708,
  * 933-939): unloads the module and frees the flag. NULL is accepted. */
@@ -282,7 +285,8 @@ typedef enum sgl_kv_head_layout {
 /* One layer of a page-major pool. The page -> layer -> tensor nesting and
  * the byte offsets follow PagedKvCacheLayout::tensor_token_byte_range
  * (kv_cache.rs:653-700); head_layout = HND only reorders bytes inside each
- * (page, layer, tensor) region. Build it with sgl_kv_pool_view_for_layer. */
+ * (page, layer, tensor) region. Build it with sgl_kv_pool_view_for_layer,
+ * or fill it directly for pools this library did not describe. */
 typedef struct sgl_kv_pool_view {
     void *base;                 /* device pointer to byte 0 of the pool */
     uint64_t byte_len;          /* pool allocation length */
@@ -295,30 +299,58 @@ typedef struct sgl_kv_pool_view {
     uint32_t heads;             /* KV heads; HND splits a row into `heads` chunks */
     uint32_t head_layout;       /* sgl_kv_head_layout */
     uint32_t reserved;
-    float *scale;               /* optional device pointer to this layer's scale (fp8), or NULL */
+    float *scale;               /* optional device pointer to this layer's tensor_count
+                                   quantisation scales (fp8), or NULL */
 } sgl_kv_pool_view;
 
 /* Builds the view of `layer` for tensors [first_tensor, first_tensor +
- * tensor_count). Errors: layer/tensor out of range; UnevenKvPairCopy when a
+ * tensor_count). Errors: layer/tensor out of range (LayerOutOfRange,
+ * TensorOutOfRange, kv_cache.rs:672-685); UnevenKvPairCopy when a
  * two-tensor view spans unequal widths (kv_cache.rs:758-763). */
 int32_t sgl_kv_pool_view_for_layer(const sgl_kv_paged_layout *layout, void *base,
-                                   uint64_t byte_len, uint32_t head_layout, uint64_t layer_index,
-                                   uint64_t first_tensor, uint64_t tensor_count,
-                                   sgl_kv_pool_view *out);
+                                   uint64_t byte_len, uint32_t head_layout, uint64_t heads,
+                                   uint64_t layer_index, uint64_t first_tensor,
+                                   uint64_t tensor_count, sgl_kv_pool_view *out);
 
-/* Contiguous transfer rows: row r of tensor t at planes[t] + r * row_stride[t]. */
+/* Contiguous transfer rows: row r of tensor t at planes[t] + r * row_stride[t],
+ * token-major ([token][heads][dim]). */
 typedef struct sgl_kv_rows_view {
     void *planes[2];
     uint64_t plane_bytes[2];    /* allocation bytes available from planes[t] */
     uint64_t row_stride[2];
-    float *scale;               /* optional device pointer to the transferred scale, or NULL */
+    float *scale;               /* optional device pointer receiving / supplying the
+                                   layer's tensor_count scales, or NULL */
 } sgl_kv_rows_view;
 
-/* A request's run of rows (transfer.rs:495-505, KvCacheTransferSpan):
+/* Pack (generalises sglang_gather_kv_pair_bytes, cuda_kv_kernels.rs:54-99):
+ * row r of the transfer <- the pool row at physical slot slots[r], for
+ * r in [0, row_count). `slots` is the per-row u64 slot map the reference
+ * uploads with CudaKvStorage::upload_slot_map (cuda_kv_cache.rs:199-222);
+ * it must hold row_count entries. Asynchronous on `stream` (NULL: null
+ * stream); a slot outside the pool skips that row and raises the context's
+ * error word (read it with sgl_rocm_kv_check_errors). row_count 0 is a
+ * no-op. Scales are copied when both views carry a pointer. */
+int32_t sgl_rocm_kv_pack_layer(sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src,
+                               const sgl_kv_device_buffer *slots, uint64_t row_count,
+                               const sgl_kv_rows_view *dst, void *stream);
+/* Unpack (generalises sglang_scatter_kv_pair_bytes, cuda_kv_kernels.rs:
+ * 11-52): the pool row at slots[r] <- transfer row r, into the decode pool
+ * with its own page size and head layout. Asynchronous. */
+int32_t sgl_rocm_kv_unpack_layer(sgl_rocm_kv_ctx *ctx, const sgl_kv_rows_view *src,
+                                 uint64_t row_count, const sgl_kv_pool_view *dst,
+                                 const sgl_kv_device_buffer *slots, void *stream);
+/* Pool -> pool in one pass for co-resident prefill and decode pools:
+ * the composition unpack(pack(.)) without the transfer rows. */
+int32_t sgl_rocm_kv_transfer_layer(sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src,
+                                   const sgl_kv_device_buffer *src_slots, uint64_t row_count,
+                                   const sgl_kv_pool_view *dst,
+                                   const sgl_kv_device_buffer *dst_slots, void *stream);
+
+/* A request's run of transfer rows (KvCacheTransferSpan, transfer.rs:495-505):
  * rows [row_start, row_start + token_count) hold request tokens
  * [token_offset, token_offset + token_count); token k lives in page
- * page_table[page_table_start + k / page_size] at in-page position
- * k % page_size. */
+ * page_table[page_table_start + k / page_size] at position k % page_size.
+ * token_offset > 0 is a prefix already cached on the decode side. */
 typedef struct sgl_kv_span {
     uint32_t row_start;
     uint32_t token_offset;
@@ -326,42 +358,36 @@ typedef struct sgl_kv_span {
     uint32_t page_table_start;
 } sgl_kv_span;
 
-/* How the rows of a transfer find their physical slots on one pool. Either
- * a per-row slot map (the scheduler's out_cache_pages, model_executor.rs:
- * 158-175) or spans + a page table (the decode side's dst_kv_indices,
- * pd_bootstrap.rs:416-494). All pointers are device pointers. */
-typedef struct sgl_kv_token_map {
-    const uint64_t *slots;      /* one physical slot per row, or NULL to use spans */
-    uint64_t slots_len;
-    const int32_t *page_table;  /* physical page indices */
-    uint64_t page_table_len;
-    const sgl_kv_span *spans;   /* sorted by row_start */
-    uint32_t span_count;
-    uint32_t reserved;
-} sgl_kv_token_map;
+/* Expands spans + a page table (the decode side's dst_kv_indices,
+ * pd_bootstrap.rs:416-494) into the per-row slot map taken by the calls
+ * above, on the device. `spans` (device) must be sorted by row_start with
+ * row_start[i] + token_count[i] <= row_start[i + 1]. Rows no span covers and
+ * rows whose page entry is negative, past the table or >= page_count get
+ * slot UINT64_MAX and raise the error word (SPAN / PAGE); the copy calls
+ * then skip them. Asynchronous. */
+int32_t sgl_rocm_kv_resolve_spans(sgl_rocm_kv_ctx *ctx, uint64_t page_size, uint64_t page_count,
+                                  const sgl_kv_device_buffer *spans, uint64_t span_count,
+                                  const sgl_kv_device_buffer *page_table, uint64_t page_table_len,
+                                  uint64_t row_count, const sgl_kv_device_buffer *out_slots,
+                                  void *stream);
 
-/* Pack (new; generalises sglang_gather_kv_pair_bytes,
- * cuda_kv_kernels.rs:54-99): rows [0, row_count) of one layer, pool ->
- * transfer rows. Asynchronous on `stream`. Device-side range failures skip
- * the affected rows and set the context's error flag. */
-int32_t sgl_rocm_kv_pack_layer(sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src,
-                               const sgl_kv_token_map *src_map, uint64_t row_count,
-                               const sgl_kv_rows_view *dst, void *stream);
-/* Unpack (new; generalises sglang_scatter_kv_pair_bytes,
- * cuda_kv_kernels.rs:11-52): transfer rows -> the decode pool under its own
- * page size, head layout and page table. Asynchronous. */
-int32_t sgl_rocm_kv_unpack_layer(sgl_rocm_kv_ctx *ctx, const sgl_kv_rows_view *src,
-                                 uint64_t row_count, const sgl_kv_pool_view *dst,
-                                 const sgl_kv_token_map *dst_map, void *stream);
-/* Pool -> pool in one pass, for prefill and decode pools co-resident on one
- * GPU (the composition unpack(pack(.)) without the transfer rows). */
-int32_t sgl_rocm_kv_transfer_layer(sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src,
-                                   const sgl_kv_token_map *src_map, uint64_t row_count,
-                                   const sgl_kv_pool_view *dst, const sgl_kv_token_map *dst_map,
-                                   void *stream);
-/* Synchronises `stream`, reads and clears the error flag, and maps it to
- * SGL_KV_DEVICE_SLOT_INDEX_OUT_OF_RANGE / _PAGE_INDEX_ / _SPAN_ (the first
- * raised in that order). Replaces the flag readback of
+/* Synthetic-input generator for benchmarks and tests; it has no counterpart
+ * in the reference. Fills `buffer` (byte_len a multiple of 8) word by word:
+ * word i (8 bytes) derives from z = splitmix64(seed + (i + 1) *
+ * 0x9E3779B97F4A7C15). kind 0: the word is z (reproducible on the host);
+ * kind 1: four bf16 N(0,1) values (Box-Muller); kind 2: four bf16 U(-1,1)
+ * values. Asynchronous. */
+typedef enum sgl_kv_fill_kind {
+    SGL_KV_FILL_BITS = 0,
+    SGL_KV_FILL_BF16_NORMAL = 1,
+    SGL_KV_FILL_BF16_UNIFORM = 2
+} sgl_kv_fill_kind;
+int32_t sgl_rocm_kv_fill_synthetic(sgl_rocm_kv_ctx *ctx, const sgl_kv_device_buffer *buffer,
+                                   uint64_t seed, uint32_t kind, void *stream);
+
+/* Synchronises `stream`, reads and clears the error word, and maps it to
+ * SGL_KV_DEVICE_SLOT_INDEX_OUT_OF_RANGE, _PAGE_INDEX_ or _SPAN_ (the first
+ * raised, in that order). Replaces the flag readback of
  * cuda_kv_kernels.rs:613-621 for the asynchronous calls. */
 int32_t sgl_rocm_kv_check_errors(sgl_rocm_kv_ctx *ctx, void *stream);
 

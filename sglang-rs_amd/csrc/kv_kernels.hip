@@ -1,0 +1,278 @@
+// kv_kernels.hip -- gfx950 kernels of the KV-cache transfer path.
+//
+// Built ahead of time into a code object (sgl_rocm_kv_gfx950.co) and loaded
+// with hipModuleLoad by kv_runtime.cpp; every entry point is extern "C" so
+// the launcher resolves it by its plain name.
+//
+// The work is pure byte movement (no arithmetic on the payload), so the
+// design goal is HBM bandwidth:
+//  - A workgroup owns a tile of consecutive transfer rows. Before copying,
+//    it resolves each tile row's physical slot into a byte offset once
+//    (slot -> page, position -> offset) and stages the offsets in LDS, so
+//    the per-vector work is one LDS read and one 64-bit add.
+//  - Threads are laid out (x = vector index inside a row, y = row). Thread
+//    x keeps the same position in every row it copies, so which tensor and
+//    which head chunk it touches is decided once per thread, not per byte
+//    as in the reference's byte-per-thread kernels
+//    (crates/sglang-kernel/src/cuda_kv_kernels.rs:11-99).
+//  - Each thread issues the loads of SGLKV_ROWS_PER_THREAD rows before any
+//    store, so a 64-lane wavefront keeps up to 8 KiB in flight.
+//  - Accesses are VB-byte vectors (16 B = global_load/store_dwordx4 on the
+//    common shapes); consecutive lanes touch consecutive vectors of one row
+//    or one head chunk, so every wavefront access is a run of >= 256
+//    contiguous bytes for the shapes of this path.
+// A slot outside the pool skips the row and raises SGLKV_FLAG_SLOT in the
+// device error word, as the reference's kernels do with error_flag.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kv_params.h"
+
+typedef unsigned int sglkv_v4u __attribute__((ext_vector_type(4)));
+typedef unsigned int sglkv_v2u __attribute__((ext_vector_type(2)));
+
+// Global-address-space pointers: built from integer addresses, a plain
+// pointer would be flat, and flat accesses share the LDS wait counter, which
+// would serialise the loads behind the LDS reads of the row offsets.
+typedef __attribute__((address_space(1))) const char sglkv_gsrc;
+typedef __attribute__((address_space(1))) char sglkv_gdst;
+
+template <int VB> struct sglkv_vec;
+template <> struct sglkv_vec<16> { typedef sglkv_v4u type; };
+template <> struct sglkv_vec<8> { typedef sglkv_v2u type; };
+template <> struct sglkv_vec<4> { typedef uint32_t type; };
+template <> struct sglkv_vec<2> { typedef uint16_t type; };
+template <> struct sglkv_vec<1> { typedef uint8_t type; };
+
+// Byte offset (relative to plane[t]) of `row`'s data in a POOL side, or
+// SGLKV_INVALID_OFFSET after flagging a slot outside the pool. The host
+// guarantees slot_count < 2^32, so the page split runs in 32 bits.
+__device__ __forceinline__ uint64_t sglkv_pool_row_offset(const sglkv_side &s, uint32_t row,
+                                                         uint32_t *flag) {
+    const uint64_t slot = s.slots[row];
+    if (slot >= s.slot_count) {
+        atomicOr(flag, SGLKV_FLAG_SLOT);
+        return SGLKV_INVALID_OFFSET;
+    }
+    const uint32_t sl = static_cast<uint32_t>(slot);
+    const uint32_t page = sl / s.page_size;
+    const uint32_t pos = sl - page * s.page_size;
+    return static_cast<uint64_t>(page) * s.stride[0] + static_cast<uint64_t>(pos) * s.pos_mult;
+}
+
+template <int VB, uint32_t SK, uint32_t DK>
+__device__ __forceinline__ void sglkv_copy_rows(const sglkv_copy_params &p) {
+    typedef typename sglkv_vec<VB>::type V;
+    constexpr uint32_t RU = SGLKV_ROWS_PER_THREAD;
+    __shared__ uint64_t s_src[SGLKV_MAX_TILE_ROWS];
+    __shared__ uint64_t s_dst[SGLKV_MAX_TILE_ROWS];
+
+    const uint32_t tile = p.tile_rows;
+    const uint32_t row0 = blockIdx.x * tile;
+    const uint32_t nthreads = blockDim.x * blockDim.y;
+    const uint32_t tid = threadIdx.y * blockDim.x + threadIdx.x;
+
+    // A tile is "clean" when every one of its rows exists and resolved to a
+    // valid offset; clean tiles (all but the last tile, unless a slot is bad)
+    // copy without per-row predicates, so the compiler can pipeline the
+    // stores behind the loads instead of draining the memory counter at
+    // every branch.
+    int bad = row0 + tile > p.rows;
+    if (SK == SGLKV_SIDE_POOL || DK == SGLKV_SIDE_POOL) {
+        for (uint32_t i = tid; i < tile; i += nthreads) {
+            const uint32_t r = row0 + i;
+            if (r < p.rows) {
+                if (SK == SGLKV_SIDE_POOL) {
+                    s_src[i] = sglkv_pool_row_offset(p.src, r, p.flag);
+                    bad |= s_src[i] == SGLKV_INVALID_OFFSET;
+                }
+                if (DK == SGLKV_SIDE_POOL) {
+                    s_dst[i] = sglkv_pool_row_offset(p.dst, r, p.flag);
+                    bad |= s_dst[i] == SGLKV_INVALID_OFFSET;
+                }
+            }
+        }
+    }
+    const bool clean = !__syncthreads_or(bad);
+    // Per-layer quantisation scales ride along bit-exactly.
+    if (blockIdx.x == 0 && tid < p.scale_count) {
+        reinterpret_cast<uint32_t *>(p.scale_dst)[tid] =
+            reinterpret_cast<const uint32_t *>(p.scale_src)[tid];
+    }
+
+    for (uint32_t j = threadIdx.x; j < p.vpr; j += blockDim.x) {
+        const uint32_t t = j / p.vpt;
+        const uint32_t jt = j - t * p.vpt;
+        const uint32_t h = jt / p.vpc;
+        const uint32_t jc = jt - h * p.vpc;
+        // Select rather than index the kernel-argument arrays: a dynamic
+        // index would copy the struct to scratch.
+        const uint64_t src_plane = t ? p.src.plane[1] : p.src.plane[0];
+        const uint64_t dst_plane = t ? p.dst.plane[1] : p.dst.plane[0];
+        const uint64_t src_stride = t ? p.src.stride[1] : p.src.stride[0];
+        const uint64_t dst_stride = t ? p.dst.stride[1] : p.dst.stride[0];
+        sglkv_gsrc *sb = reinterpret_cast<sglkv_gsrc *>(src_plane +
+                                                       static_cast<uint64_t>(h) * p.src.head_stride +
+                                                       static_cast<uint64_t>(jc) * VB);
+        sglkv_gdst *db = reinterpret_cast<sglkv_gdst *>(dst_plane +
+                                                       static_cast<uint64_t>(h) * p.dst.head_stride +
+                                                       static_cast<uint64_t>(jc) * VB);
+
+        typedef __attribute__((address_space(1))) const V gload_t;
+        typedef __attribute__((address_space(1))) V gstore_t;
+        V buf[RU];
+        if (clean) {
+#pragma unroll
+            for (uint32_t k = 0; k < RU; ++k) {
+                const uint32_t i = threadIdx.y + k * blockDim.y;
+                const uint64_t so =
+                    SK == SGLKV_SIDE_POOL ? s_src[i] : static_cast<uint64_t>(row0 + i) * src_stride;
+                buf[k] = *reinterpret_cast<gload_t *>(sb + so);
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < RU; ++k) {
+                const uint32_t i = threadIdx.y + k * blockDim.y;
+                const uint64_t dof =
+                    DK == SGLKV_SIDE_POOL ? s_dst[i] : static_cast<uint64_t>(row0 + i) * dst_stride;
+                *reinterpret_cast<gstore_t *>(db + dof) = buf[k];
+            }
+            continue;
+        }
+        // Ragged or faulty tile: offsets of this thread's rows first, then
+        // every load, then every store, each row predicated.
+        uint64_t soff[RU];
+        uint64_t doff[RU];
+#pragma unroll
+        for (uint32_t k = 0; k < RU; ++k) {
+            const uint32_t i = threadIdx.y + k * blockDim.y;
+            const uint32_t r = row0 + i;
+            uint64_t so = SGLKV_INVALID_OFFSET;
+            uint64_t dof = SGLKV_INVALID_OFFSET;
+            if (r < p.rows) {
+                so = SK == SGLKV_SIDE_POOL ? s_src[i] : static_cast<uint64_t>(r) * src_stride;
+                dof = DK == SGLKV_SIDE_POOL ? s_dst[i] : static_cast<uint64_t>(r) * dst_stride;
+                if (so == SGLKV_INVALID_OFFSET) dof = SGLKV_INVALID_OFFSET;
+            }
+            soff[k] = so;
+            doff[k] = dof;
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < RU; ++k) {
+            if (doff[k] != SGLKV_INVALID_OFFSET) buf[k] = *reinterpret_cast<gload_t *>(sb + soff[k]);
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < RU; ++k) {
+            if (doff[k] != SGLKV_INVALID_OFFSET) *reinterpret_cast<gstore_t *>(db + doff[k]) = buf[k];
+        }
+    }
+}
+
+#define SGLKV_COPY_KERNEL(VB, SK, DK, NAME)                                            \
+    extern "C" __global__ __launch_bounds__(SGLKV_BLOCK_THREADS) void NAME(           \
+        const sglkv_copy_params p) {                                                   \
+        sglkv_copy_rows<VB, SK, DK>(p);                                                \
+    }
+
+#define SGLKV_COPY_KERNELS(VB)                                                                  \
+    SGLKV_COPY_KERNEL(VB, SGLKV_SIDE_POOL, SGLKV_SIDE_ROWS, sglkv_copy_pool_rows_v##VB)         \
+    SGLKV_COPY_KERNEL(VB, SGLKV_SIDE_ROWS, SGLKV_SIDE_POOL, sglkv_copy_rows_pool_v##VB)         \
+    SGLKV_COPY_KERNEL(VB, SGLKV_SIDE_POOL, SGLKV_SIDE_POOL, sglkv_copy_pool_pool_v##VB)
+
+SGLKV_COPY_KERNELS(16)
+SGLKV_COPY_KERNELS(8)
+SGLKV_COPY_KERNELS(4)
+SGLKV_COPY_KERNELS(2)
+SGLKV_COPY_KERNELS(1)
+
+// Spans + page table -> one physical slot per row (the decode side's
+// dst_kv_indices, crates/sglang-srt/src/pd_bootstrap.rs:416-494, expanded to
+// the per-row slot map the copy kernels take). One thread per row; the
+// row's span is the last one whose row_start <= row (binary search over
+// spans sorted by row_start). Rows no span covers, and rows whose page
+// entry is outside the table or the pool, get SGLKV_INVALID_OFFSET and
+// raise SGLKV_FLAG_SPAN / SGLKV_FLAG_PAGE.
+extern "C" __global__ __launch_bounds__(SGLKV_BLOCK_THREADS) void sglkv_resolve_spans(
+    const sglkv_resolve_params p) {
+    const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= p.rows) return;
+    uint32_t lo = 0, hi = p.span_count;
+    while (lo < hi) {
+        const uint32_t mid = lo + (hi - lo) / 2;
+        if (p.spans[mid].row_start <= r)
+            lo = mid + 1;
+        else
+            hi = mid;
+    }
+    uint64_t out = SGLKV_INVALID_OFFSET;
+    if (lo == 0) {
+        atomicOr(p.flag, SGLKV_FLAG_SPAN);
+    } else {
+        const sglkv_span s = p.spans[lo - 1];
+        const uint32_t k = r - s.row_start;
+        if (k >= s.token_count) {
+            atomicOr(p.flag, SGLKV_FLAG_SPAN);
+        } else {
+            const uint64_t token = static_cast<uint64_t>(s.token_offset) + k;
+            const uint64_t index = static_cast<uint64_t>(s.page_table_start) + token / p.page_size;
+            const int32_t page = index < p.page_table_len ? p.page_table[index] : -1;
+            if (page < 0 || static_cast<uint64_t>(page) >= p.page_count) {
+                atomicOr(p.flag, SGLKV_FLAG_PAGE);
+            } else {
+                out = static_cast<uint64_t>(page) * p.page_size + token % p.page_size;
+            }
+        }
+    }
+    p.out_slots[r] = out;
+}
+
+// Synthetic-input generator for benchmarks and tests (no reference
+// counterpart). Word i (8 bytes) of the buffer derives from
+// z = splitmix64(seed + (i + 1) * 0x9E3779B97F4A7C15):
+//   kind 0: the word is z itself (reproducible on the host for checks);
+//   kind 1: four bf16 N(0, 1) values, Box-Muller on (z, splitmix64(z));
+//   kind 2: four bf16 U(-1, 1) values from the four 16-bit fields of z.
+// Grid-stride loop; every thread exits after its last word.
+__device__ __forceinline__ uint64_t sglkv_mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__device__ __forceinline__ uint32_t sglkv_bf16_bits(float f) {
+    const uint32_t bits = __float_as_uint(f);
+    return (bits + 0x7FFFu + ((bits >> 16) & 1u)) >> 16;
+}
+
+extern "C" __global__ __launch_bounds__(SGLKV_BLOCK_THREADS) void sglkv_fill_synthetic(
+    uint64_t *out, uint64_t words, uint64_t seed, uint32_t kind) {
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < words;
+         i += stride) {
+        const uint64_t z = sglkv_mix64(seed + (i + 1) * 0x9E3779B97F4A7C15ull);
+        uint64_t w = z;
+        if (kind == 1) {
+            const uint64_t z2 = sglkv_mix64(z);
+            uint32_t v[4];
+            for (int k = 0; k < 2; ++k) {
+                const uint64_t src = k ? z2 : z;
+                // 24-bit uniforms; u1 in (0, 1] keeps the logarithm finite.
+                const float u1 = (static_cast<float>(src & 0xFFFFFFu) + 1.0f) * (1.0f / 16777216.0f);
+                const float u2 = static_cast<float>((src >> 32) & 0xFFFFFFu) * (1.0f / 16777216.0f);
+                const float r = sqrtf(-2.0f * logf(u1));
+                float sn, cs;
+                sincosf(6.283185307179586f * u2, &sn, &cs);
+                v[2 * k] = sglkv_bf16_bits(r * cs);
+                v[2 * k + 1] = sglkv_bf16_bits(r * sn);
+            }
+            w = v[0] | (static_cast<uint64_t>(v[1]) << 16) | (static_cast<uint64_t>(v[2]) << 32) |
+                (static_cast<uint64_t>(v[3]) << 48);
+        } else if (kind == 2) {
+            w = 0;
+            for (int k = 0; k < 4; ++k) {
+                const float u = static_cast<float>((z >> (16 * k)) & 0xFFFFu) * (2.0f / 65536.0f) - 1.0f;
+                w |= static_cast<uint64_t>(sglkv_bf16_bits(u)) << (16 * k);
+            }
+        }
+        out[i] = w;
+    }
+}

@@ -1,0 +1,551 @@
+// kv_layout.cpp -- host mirror of the reference's KV layout arithmetic and
+// copy plan (group 1 of sgl_rocm_kv.h). No HIP calls: these run on any host.
+//
+// Each function follows the reference item cited beside it: the same
+// validation order, the same error variants (as sgl_kv_status codes with the
+// variant's fields in a/b/c) and the same checked arithmetic.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "kv_internal.h"
+
+namespace sglkv {
+
+static thread_local sgl_kv_error_detail t_last;
+
+int32_t fail(int32_t code, const char *name, uint64_t a, uint64_t b, uint64_t c, const char *fmt,
+             ...) {
+    memset(&t_last, 0, sizeof t_last);
+    t_last.code = code;
+    t_last.a = a;
+    t_last.b = b;
+    t_last.c = c;
+    if (name) snprintf(t_last.name, sizeof t_last.name, "%s", name);
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(t_last.message, sizeof t_last.message, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int32_t ok() {
+    memset(&t_last, 0, sizeof t_last);
+    return SGL_KV_OK;
+}
+
+}  // namespace sglkv
+
+using namespace sglkv;
+
+extern "C" void sgl_kv_last_error(sgl_kv_error_detail *out) {
+    if (out) *out = t_last;
+}
+
+extern "C" const char *sgl_kv_status_name(int32_t code) {
+    switch (code) {
+    case SGL_KV_OK: return "Ok";
+    case SGL_KV_ZERO_DIMENSION: return "ZeroDimension";
+    case SGL_KV_SHAPE_OVERFLOW: return "ShapeOverflow";
+    case SGL_KV_DIMENSION_TOO_LARGE: return "DimensionTooLarge";
+    case SGL_KV_ROW_STRIDE_TOO_SMALL: return "RowStrideTooSmall";
+    case SGL_KV_TENSOR_PAGE_REGION_OUT_OF_BOUNDS: return "TensorPageRegionOutOfBounds";
+    case SGL_KV_TENSOR_PAGE_REGIONS_OVERLAP: return "TensorPageRegionsOverlap";
+    case SGL_KV_DEVICE_MISMATCH: return "DeviceMismatch";
+    case SGL_KV_DEVICE_SLOT_INDEX_OUT_OF_RANGE: return "DeviceSlotIndexOutOfRange";
+    case SGL_KV_HIP: return "Hip";
+    case SGL_KV_MODULE: return "Module";
+    case SGL_KV_ALLOCATION_OUT_OF_BOUNDS: return "AllocationOutOfBounds";
+    case SGL_KV_INVALID_ARGUMENT: return "InvalidArgument";
+    case SGL_KV_LAYOUT_ZERO_PAGE_COUNT: return "ZeroPageCount";
+    case SGL_KV_LAYOUT_ZERO_FIELD: return "ZeroLayoutField";
+    case SGL_KV_LAYOUT_RUNTIME_PAGE_SIZE_MISMATCH: return "RuntimePageSizeMismatch";
+    case SGL_KV_LAYOUT_UNEVEN_LAYER: return "UnevenLayerLayout";
+    case SGL_KV_LAYOUT_UNEVEN_TENSOR: return "UnevenTensorLayout";
+    case SGL_KV_LAYOUT_SIZE_OVERFLOW: return "SizeOverflow";
+    case SGL_KV_LAYOUT_PAGE_OUT_OF_RANGE: return "PageOutOfRange";
+    case SGL_KV_LAYOUT_LAYER_OUT_OF_RANGE: return "LayerOutOfRange";
+    case SGL_KV_LAYOUT_TENSOR_OUT_OF_RANGE: return "TensorOutOfRange";
+    case SGL_KV_LAYOUT_TOKEN_OUT_OF_RANGE: return "TokenOutOfRange";
+    case SGL_KV_LAYOUT_SLOT_OUT_OF_RANGE: return "SlotOutOfRange";
+    case SGL_KV_LAYOUT_EMPTY_SLOT_MAP: return "EmptySlotMap";
+    case SGL_KV_LAYOUT_BATCH_SLOT_OUT_OF_RANGE: return "BatchSlotOutOfRange";
+    case SGL_KV_LAYOUT_KV_PAIR_REQUIRES_TWO_TENSORS: return "KvPairRequiresTwoTensors";
+    case SGL_KV_LAYOUT_TENSOR_PAIR_REQUIRES_TWO_TENSORS: return "TensorPairRequiresTwoTensors";
+    case SGL_KV_LAYOUT_TENSOR_PAIR_SIZE_MISMATCH: return "TensorPairSizeMismatch";
+    case SGL_KV_LAYOUT_UNEVEN_KV_PAIR_COPY: return "UnevenKvPairCopy";
+    case SGL_KV_PLAN_ZERO_PAGE_SIZE: return "ZeroPageSize";
+    case SGL_KV_PLAN_CACHE_PAGE_COUNT_MISMATCH: return "CachePageCountMismatch";
+    case SGL_KV_PLAN_TRAILING_CACHE_PAGES: return "TrailingCachePages";
+    case SGL_KV_PLAN_UNALIGNED_TOKEN_OFFSET: return "UnalignedTokenOffset";
+    case SGL_KV_PLAN_UNALIGNED_CACHE_SLOT: return "UnalignedCacheSlot";
+    case SGL_KV_PLAN_NON_CONTIGUOUS_CACHE_SLOTS: return "NonContiguousCacheSlots";
+    case SGL_KV_DEVICE_PAGE_INDEX_OUT_OF_RANGE: return "DevicePageIndexOutOfRange";
+    case SGL_KV_DEVICE_SPAN_OUT_OF_RANGE: return "DeviceSpanOutOfRange";
+    default: return "Unknown";
+    }
+}
+
+// KvCacheDtype::bytes_per_element (crates/sglang-srt/src/kv_cache.rs:39-46).
+extern "C" size_t sgl_kv_dtype_bytes_per_element(int32_t dtype) {
+    switch (dtype) {
+    case SGL_KV_DTYPE_AUTO:
+    case SGL_KV_DTYPE_BFLOAT16: return 2;
+    case SGL_KV_DTYPE_FLOAT32: return 4;
+    case SGL_KV_DTYPE_FP8_E4M3:
+    case SGL_KV_DTYPE_FP8_E5M2: return 1;
+    default: return 0;
+    }
+}
+
+static int32_t layout_overflow() {
+    return fail(SGL_KV_LAYOUT_SIZE_OVERFLOW, nullptr, 0, 0, 0, "KV cache layout size overflowed");
+}
+
+// PagedKvCacheLayout::validate_runtime (kv_cache.rs:531-586).
+static int32_t validate_runtime(const sgl_kv_runtime_layout *rt, uint64_t page_count,
+                                sgl_kv_paged_layout *out) {
+    if (page_count == 0)
+        return fail(SGL_KV_LAYOUT_ZERO_PAGE_COUNT, nullptr, 0, 0, 0,
+                    "KV cache page count must be non-zero");
+    const struct {
+        const char *field;
+        uint64_t value;
+    } fields[] = {{"page_size", rt->page_size},
+                  {"num_layers", rt->num_layers},
+                  {"kv_heads", rt->kv_heads},
+                  {"head_dim", rt->head_dim},
+                  {"kv_tensors_per_token", rt->kv_tensors_per_token},
+                  {"bytes_per_token", rt->bytes_per_token},
+                  {"page_size_bytes", rt->page_size_bytes}};
+    for (const auto &f : fields)
+        if (f.value == 0)
+            return fail(SGL_KV_LAYOUT_ZERO_FIELD, f.field, 0, 0, 0,
+                        "KV cache layout field %s must be non-zero", f.field);
+    uint64_t expected;
+    if (mul_ovf(rt->page_size, rt->bytes_per_token, &expected)) return layout_overflow();
+    if (rt->page_size_bytes != expected)
+        return fail(SGL_KV_LAYOUT_RUNTIME_PAGE_SIZE_MISMATCH, nullptr, expected, rt->page_size_bytes, 0,
+                    "KV cache runtime page size is %llu bytes but page_size * bytes_per_token "
+                    "requires %llu bytes",
+                    (unsigned long long)rt->page_size_bytes, (unsigned long long)expected);
+    if (rt->bytes_per_token % rt->num_layers)
+        return fail(SGL_KV_LAYOUT_UNEVEN_LAYER, nullptr, rt->bytes_per_token, rt->num_layers, 0,
+                    "KV cache token size %llu bytes is not divisible by %llu layers",
+                    (unsigned long long)rt->bytes_per_token, (unsigned long long)rt->num_layers);
+    memset(out, 0, sizeof *out);
+    out->runtime = *rt;
+    out->page_count = page_count;
+    out->bytes_per_token_per_layer = rt->bytes_per_token / rt->num_layers;
+    if (mul_ovf(rt->page_size, out->bytes_per_token_per_layer, &out->bytes_per_layer_page) ||
+        mul_ovf(page_count, rt->page_size_bytes, &out->total_byte_len) ||
+        mul_ovf(page_count, rt->page_size, &out->slot_count))
+        return layout_overflow();
+    return SGL_KV_OK;
+}
+
+// PagedKvCacheLayout::new (kv_cache.rs:448-478): Uniform geometry.
+extern "C" int32_t sgl_kv_paged_layout_new(const sgl_kv_runtime_layout *runtime,
+                                           uint64_t page_count, sgl_kv_paged_layout *out) {
+    if (!runtime || !out)
+        return fail(SGL_KV_INVALID_ARGUMENT, "runtime/out", 0, 0, 0, "null argument");
+    sgl_kv_paged_layout l;
+    int32_t rc = validate_runtime(runtime, page_count, &l);
+    if (rc) return rc;
+    if (l.bytes_per_token_per_layer % runtime->kv_tensors_per_token)
+        return fail(SGL_KV_LAYOUT_UNEVEN_TENSOR, nullptr, l.bytes_per_token_per_layer,
+                    runtime->kv_tensors_per_token, 0,
+                    "KV cache per-layer token size %llu bytes is not divisible by %llu KV tensors",
+                    (unsigned long long)l.bytes_per_token_per_layer,
+                    (unsigned long long)runtime->kv_tensors_per_token);
+    const uint64_t token_bytes = l.bytes_per_token_per_layer / runtime->kv_tensors_per_token;
+    if (mul_ovf(runtime->page_size, token_bytes, &l.tensor_page_bytes)) return layout_overflow();
+    l.tensor_pair = 0;
+    l.token_bytes[0] = l.token_bytes[1] = token_bytes;
+    *out = l;
+    return ok();
+}
+
+// PagedKvCacheLayout::new_with_tensor_pair (kv_cache.rs:480-529).
+extern "C" int32_t sgl_kv_paged_layout_new_with_tensor_pair(const sgl_kv_runtime_layout *runtime,
+                                                            uint64_t page_count,
+                                                            uint64_t key_token_bytes,
+                                                            uint64_t value_token_bytes,
+                                                            sgl_kv_paged_layout *out) {
+    if (!runtime || !out)
+        return fail(SGL_KV_INVALID_ARGUMENT, "runtime/out", 0, 0, 0, "null argument");
+    sgl_kv_paged_layout l;
+    int32_t rc = validate_runtime(runtime, page_count, &l);
+    if (rc) return rc;
+    if (runtime->kv_tensors_per_token != 2)
+        return fail(SGL_KV_LAYOUT_TENSOR_PAIR_REQUIRES_TWO_TENSORS, nullptr,
+                    runtime->kv_tensors_per_token, 0, 0,
+                    "explicit KV tensor-pair layout requires exactly two tensors per token, layout "
+                    "has %llu",
+                    (unsigned long long)runtime->kv_tensors_per_token);
+    if (key_token_bytes == 0)
+        return fail(SGL_KV_LAYOUT_ZERO_FIELD, "key_token_bytes", 0, 0, 0,
+                    "KV cache layout field key_token_bytes must be non-zero");
+    if (value_token_bytes == 0)
+        return fail(SGL_KV_LAYOUT_ZERO_FIELD, "value_token_bytes", 0, 0, 0,
+                    "KV cache layout field value_token_bytes must be non-zero");
+    uint64_t pair;
+    if (add_ovf(key_token_bytes, value_token_bytes, &pair)) return layout_overflow();
+    if (pair != l.bytes_per_token_per_layer)
+        return fail(SGL_KV_LAYOUT_TENSOR_PAIR_SIZE_MISMATCH, nullptr, l.bytes_per_token_per_layer,
+                    key_token_bytes, value_token_bytes,
+                    "KV tensor-pair widths (%llu key bytes + %llu value bytes) do not match the "
+                    "runtime per-layer token size of %llu bytes",
+                    (unsigned long long)key_token_bytes, (unsigned long long)value_token_bytes,
+                    (unsigned long long)l.bytes_per_token_per_layer);
+    if (mul_ovf(runtime->page_size, key_token_bytes, &l.tensor_page_bytes)) return layout_overflow();
+    l.tensor_pair = 1;
+    l.token_bytes[0] = key_token_bytes;
+    l.token_bytes[1] = value_token_bytes;
+    *out = l;
+    return ok();
+}
+
+static int32_t validate_page(const sgl_kv_paged_layout *l, uint64_t page) {
+    if (page >= l->page_count)
+        return fail(SGL_KV_LAYOUT_PAGE_OUT_OF_RANGE, nullptr, page, l->page_count, 0,
+                    "KV cache page index %llu is outside %llu pages", (unsigned long long)page,
+                    (unsigned long long)l->page_count);
+    return SGL_KV_OK;
+}
+
+static int32_t tensor_out_of_range(const sgl_kv_paged_layout *l, uint64_t tensor) {
+    return fail(SGL_KV_LAYOUT_TENSOR_OUT_OF_RANGE, nullptr, tensor,
+                l->runtime.kv_tensors_per_token, 0,
+                "KV cache tensor index %llu is outside %llu tensors per token",
+                (unsigned long long)tensor, (unsigned long long)l->runtime.kv_tensors_per_token);
+}
+
+// tensor_token_bytes / tensor_page_offset (kv_cache.rs:780-818).
+static int32_t tensor_geometry(const sgl_kv_paged_layout *l, uint64_t tensor, uint64_t *token_bytes,
+                               uint64_t *page_offset) {
+    if (!l->tensor_pair) {
+        *token_bytes = l->token_bytes[0];
+        if (mul_ovf(tensor, l->tensor_page_bytes, page_offset)) return layout_overflow();
+        return SGL_KV_OK;
+    }
+    if (tensor > 1) return tensor_out_of_range(l, tensor);
+    *token_bytes = l->token_bytes[tensor];
+    *page_offset = tensor == 0 ? 0 : l->tensor_page_bytes;
+    return SGL_KV_OK;
+}
+
+// PagedKvCacheLayout::page_byte_range (kv_cache.rs:639-651).
+extern "C" int32_t sgl_kv_paged_layout_page_byte_range(const sgl_kv_paged_layout *layout,
+                                                       uint64_t page_index, uint64_t *start,
+                                                       uint64_t *end) {
+    if (!layout || !start || !end)
+        return fail(SGL_KV_INVALID_ARGUMENT, "layout/start/end", 0, 0, 0, "null argument");
+    int32_t rc = validate_page(layout, page_index);
+    if (rc) return rc;
+    uint64_t s, e;
+    if (mul_ovf(page_index, layout->runtime.page_size_bytes, &s) ||
+        add_ovf(s, layout->runtime.page_size_bytes, &e))
+        return layout_overflow();
+    *start = s;
+    *end = e;
+    return ok();
+}
+
+// PagedKvCacheLayout::tensor_token_byte_range (kv_cache.rs:653-700).
+extern "C" int32_t sgl_kv_paged_layout_tensor_token_byte_range(const sgl_kv_paged_layout *layout,
+                                                               uint64_t page_index,
+                                                               uint64_t layer_index,
+                                                               uint64_t tensor_index,
+                                                               uint64_t token_index,
+                                                               uint64_t *start, uint64_t *end) {
+    if (!layout || !start || !end)
+        return fail(SGL_KV_INVALID_ARGUMENT, "layout/start/end", 0, 0, 0, "null argument");
+    int32_t rc = validate_page(layout, page_index);
+    if (rc) return rc;
+    const sgl_kv_runtime_layout &rt = layout->runtime;
+    if (layer_index >= rt.num_layers)
+        return fail(SGL_KV_LAYOUT_LAYER_OUT_OF_RANGE, nullptr, layer_index, rt.num_layers, 0,
+                    "KV cache layer index %llu is outside %llu layers",
+                    (unsigned long long)layer_index, (unsigned long long)rt.num_layers);
+    if (tensor_index >= rt.kv_tensors_per_token) return tensor_out_of_range(layout, tensor_index);
+    if (token_index >= rt.page_size)
+        return fail(SGL_KV_LAYOUT_TOKEN_OUT_OF_RANGE, nullptr, token_index, rt.page_size, 0,
+                    "KV cache token index %llu is outside page size %llu",
+                    (unsigned long long)token_index, (unsigned long long)rt.page_size);
+    uint64_t page_off, layer_off, tensor_off, token_bytes, token_off, s, e;
+    if (mul_ovf(page_index, rt.page_size_bytes, &page_off) ||
+        mul_ovf(layer_index, layout->bytes_per_layer_page, &layer_off))
+        return layout_overflow();
+    rc = tensor_geometry(layout, tensor_index, &token_bytes, &tensor_off);
+    if (rc) return rc;
+    if (mul_ovf(token_index, token_bytes, &token_off) || add_ovf(page_off, layer_off, &s) ||
+        add_ovf(s, tensor_off, &s) || add_ovf(s, token_off, &s) || add_ovf(s, token_bytes, &e))
+        return layout_overflow();
+    *start = s;
+    *end = e;
+    return ok();
+}
+
+// PagedKvCacheLayout::tensor_slot_byte_range (kv_cache.rs:702-720).
+extern "C" int32_t sgl_kv_paged_layout_tensor_slot_byte_range(const sgl_kv_paged_layout *layout,
+                                                              uint64_t layer_index,
+                                                              uint64_t tensor_index,
+                                                              uint64_t slot_index, uint64_t *start,
+                                                              uint64_t *end) {
+    if (!layout || !start || !end)
+        return fail(SGL_KV_INVALID_ARGUMENT, "layout/start/end", 0, 0, 0, "null argument");
+    if (slot_index >= layout->slot_count)
+        return fail(SGL_KV_LAYOUT_SLOT_OUT_OF_RANGE, nullptr, slot_index, layout->slot_count, 0,
+                    "KV cache slot index %llu is outside %llu token slots",
+                    (unsigned long long)slot_index, (unsigned long long)layout->slot_count);
+    const uint64_t ps = layout->runtime.page_size;
+    return sgl_kv_paged_layout_tensor_token_byte_range(layout, slot_index / ps, layer_index,
+                                                       tensor_index, slot_index % ps, start, end);
+}
+
+// PagedKvCacheLayout::validate_slot_indices (kv_cache.rs:722-736).
+extern "C" int32_t sgl_kv_paged_layout_validate_slot_indices(const sgl_kv_paged_layout *layout,
+                                                             const uint64_t *slots,
+                                                             uint64_t slot_len) {
+    if (!layout) return fail(SGL_KV_INVALID_ARGUMENT, "layout", 0, 0, 0, "null argument");
+    if (slot_len == 0)
+        return fail(SGL_KV_LAYOUT_EMPTY_SLOT_MAP, nullptr, 0, 0, 0,
+                    "KV cache slot map must not be empty");
+    if (!slots) return fail(SGL_KV_INVALID_ARGUMENT, "slots", 0, 0, 0, "null argument");
+    for (uint64_t i = 0; i < slot_len; ++i)
+        if (slots[i] >= layout->slot_count)
+            return fail(SGL_KV_LAYOUT_BATCH_SLOT_OUT_OF_RANGE, nullptr, i, slots[i],
+                        layout->slot_count,
+                        "KV cache batch slot %llu references physical slot %llu, outside %llu "
+                        "token slots",
+                        (unsigned long long)i, (unsigned long long)slots[i],
+                        (unsigned long long)layout->slot_count);
+    return ok();
+}
+
+// PagedKvCacheLayout::kv_pair_copy_geometry (kv_cache.rs:738-777), returned as
+// the CudaKvPairCopyLayout it feeds (crates/sglang-srt/src/cuda_kv_cache.rs:510-532).
+extern "C" int32_t sgl_kv_paged_layout_kv_pair_copy_geometry(const sgl_kv_paged_layout *layout,
+                                                             uint64_t layer_index,
+                                                             sgl_kv_pair_copy_layout *out) {
+    if (!layout || !out)
+        return fail(SGL_KV_INVALID_ARGUMENT, "layout/out", 0, 0, 0, "null argument");
+    const sgl_kv_runtime_layout &rt = layout->runtime;
+    if (layer_index >= rt.num_layers)
+        return fail(SGL_KV_LAYOUT_LAYER_OUT_OF_RANGE, nullptr, layer_index, rt.num_layers, 0,
+                    "KV cache layer index %llu is outside %llu layers",
+                    (unsigned long long)layer_index, (unsigned long long)rt.num_layers);
+    if (rt.kv_tensors_per_token < 2)
+        return fail(SGL_KV_LAYOUT_KV_PAIR_REQUIRES_TWO_TENSORS, nullptr, rt.kv_tensors_per_token, 0,
+                    0,
+                    "KV cache K/V pair layout requires at least two tensors per token, layout has "
+                    "%llu",
+                    (unsigned long long)rt.kv_tensors_per_token);
+    uint64_t layer_off, kb, vb, ko, vo;
+    if (mul_ovf(layer_index, layout->bytes_per_layer_page, &layer_off)) return layout_overflow();
+    int32_t rc = tensor_geometry(layout, 0, &kb, &ko);
+    if (rc) return rc;
+    rc = tensor_geometry(layout, 1, &vb, &vo);
+    if (rc) return rc;
+    if (kb != vb)
+        return fail(SGL_KV_LAYOUT_UNEVEN_KV_PAIR_COPY, nullptr, kb, vb, 0,
+                    "the selected KV copy/attention kernel requires equal key and value widths, "
+                    "but the layout has %llu key bytes and %llu value bytes per token",
+                    (unsigned long long)kb, (unsigned long long)vb);
+    if (add_ovf(layer_off, ko, &ko) || add_ovf(layer_off, vo, &vo)) return layout_overflow();
+    out->page_size = rt.page_size;
+    out->page_stride_bytes = rt.page_size_bytes;
+    out->key_in_page_offset = ko;
+    out->value_in_page_offset = vo;
+    out->row_bytes = kb;
+    return ok();
+}
+
+// CudaKvPairCopyPlan::new (crates/sglang-kernel/src/cuda_kv_kernels.rs:167-264).
+extern "C" int32_t sgl_kv_pair_copy_plan_new(uint64_t row_count, uint64_t slot_count,
+                                             const sgl_kv_pair_copy_layout *layout,
+                                             uint64_t key_row_stride_bytes,
+                                             uint64_t value_row_stride_bytes,
+                                             sgl_kv_pair_copy_plan *out) {
+    if (!layout || !out)
+        return fail(SGL_KV_INVALID_ARGUMENT, "layout/out", 0, 0, 0, "null argument");
+    const struct {
+        const char *dimension;
+        uint64_t value;
+    } dims[] = {{"row_count", row_count},
+                {"slot_count", slot_count},
+                {"page_size", layout->page_size},
+                {"page_stride_bytes", layout->page_stride_bytes},
+                {"row_bytes", layout->row_bytes}};
+    for (const auto &d : dims)
+        if (d.value == 0)
+            return fail(SGL_KV_ZERO_DIMENSION, d.dimension, 0, 0, 0,
+                        "KV copy dimension %s must be non-zero", d.dimension);
+    const struct {
+        const char *tensor;
+        uint64_t stride;
+    } strides[] = {{"key", key_row_stride_bytes}, {"value", value_row_stride_bytes}};
+    for (const auto &s : strides)
+        if (s.stride < layout->row_bytes)
+            return fail(SGL_KV_ROW_STRIDE_TOO_SMALL, s.tensor, layout->row_bytes, s.stride, 0,
+                        "KV copy %s row stride %llu bytes is smaller than row width %llu bytes",
+                        s.tensor, (unsigned long long)s.stride,
+                        (unsigned long long)layout->row_bytes);
+    auto overflow = [] {
+        return fail(SGL_KV_SHAPE_OVERFLOW, nullptr, 0, 0, 0, "KV copy tensor shape overflowed");
+    };
+    uint64_t tensor_page_bytes;
+    if (mul_ovf(layout->page_size, layout->row_bytes, &tensor_page_bytes)) return overflow();
+    const struct {
+        const char *tensor;
+        uint64_t offset;
+    } regions[] = {{"key", layout->key_in_page_offset}, {"value", layout->value_in_page_offset}};
+    uint64_t ends[2];
+    for (int i = 0; i < 2; ++i) {
+        if (add_ovf(regions[i].offset, tensor_page_bytes, &ends[i])) return overflow();
+        if (ends[i] > layout->page_stride_bytes) {
+            uint64_t shown;
+            if (add_ovf(regions[i].offset, tensor_page_bytes, &shown)) shown = UINT64_MAX;
+            return fail(SGL_KV_TENSOR_PAGE_REGION_OUT_OF_BOUNDS, regions[i].tensor,
+                        regions[i].offset, tensor_page_bytes, layout->page_stride_bytes,
+                        "KV copy %s page region [%llu, %llu) exceeds page stride %llu",
+                        regions[i].tensor, (unsigned long long)regions[i].offset,
+                        (unsigned long long)shown, (unsigned long long)layout->page_stride_bytes);
+        }
+    }
+    if (layout->key_in_page_offset < ends[1] && layout->value_in_page_offset < ends[0])
+        return fail(SGL_KV_TENSOR_PAGE_REGIONS_OVERLAP, nullptr, layout->key_in_page_offset,
+                    layout->value_in_page_offset, tensor_page_bytes,
+                    "KV copy key/value page regions overlap: key offset %llu, value offset %llu, "
+                    "tensor page size %llu bytes",
+                    (unsigned long long)layout->key_in_page_offset,
+                    (unsigned long long)layout->value_in_page_offset,
+                    (unsigned long long)tensor_page_bytes);
+    sgl_kv_pair_copy_plan p;
+    memset(&p, 0, sizeof p);
+    // strided_rows_required_bytes: (rows - 1) * stride + row_bytes.
+    if (mul_ovf(row_count - 1, key_row_stride_bytes, &p.key_rows_required_bytes) ||
+        add_ovf(p.key_rows_required_bytes, layout->row_bytes, &p.key_rows_required_bytes) ||
+        mul_ovf(row_count - 1, value_row_stride_bytes, &p.value_rows_required_bytes) ||
+        add_ovf(p.value_rows_required_bytes, layout->row_bytes, &p.value_rows_required_bytes) ||
+        mul_ovf(row_count, 8, &p.slot_indices_required_bytes))
+        return overflow();
+    // The pool must reach the end of the last slot's later tensor row.
+    const uint64_t last_slot = slot_count - 1;
+    const uint64_t last_page = last_slot / layout->page_size;
+    const uint64_t last_token = last_slot % layout->page_size;
+    const uint64_t last_tensor_end = ends[0] > ends[1] ? ends[0] : ends[1];
+    uint64_t page_off, token_off, tail;
+    if (mul_ovf(last_page, layout->page_stride_bytes, &page_off) ||
+        last_tensor_end < tensor_page_bytes ||
+        mul_ovf(last_token, layout->row_bytes, &token_off) ||
+        add_ovf(last_tensor_end - tensor_page_bytes, token_off, &tail) ||
+        add_ovf(tail, layout->row_bytes, &tail) || add_ovf(page_off, tail, &p.pool_required_bytes))
+        return overflow();
+    // The reference sizes a byte-per-thread grid here (2 * rows * row_bytes
+    // threads); this library's launch is sized per row, so only the overflow
+    // check of that product is kept.
+    uint64_t threads;
+    if (mul_ovf(row_count, layout->row_bytes, &threads) || mul_ovf(threads, 2, &threads))
+        return overflow();
+    p.row_count = row_count;
+    p.slot_count = slot_count;
+    p.layout = *layout;
+    p.key_row_stride_bytes = key_row_stride_bytes;
+    p.value_row_stride_bytes = value_row_stride_bytes;
+    *out = p;
+    return ok();
+}
+
+// transfer_page_indices (crates/sglang-srt/src/transfer.rs:679-720).
+extern "C" int32_t sgl_kv_transfer_page_indices(uint64_t request_index, uint64_t token_offset,
+                                                const uint64_t *cache_slots, uint64_t slot_len,
+                                                uint64_t page_size, uint64_t *out_pages,
+                                                uint64_t *out_len) {
+    if (!out_len) return fail(SGL_KV_INVALID_ARGUMENT, "out_len", 0, 0, 0, "null argument");
+    *out_len = 0;
+    if (slot_len == 0) return ok();
+    if (page_size == 0)
+        return fail(SGL_KV_PLAN_ZERO_PAGE_SIZE, nullptr, 0, 0, 0,
+                    "KV transfer page size must be non-zero");
+    if (!cache_slots || !out_pages)
+        return fail(SGL_KV_INVALID_ARGUMENT, "cache_slots/out_pages", 0, 0, 0, "null argument");
+    if (token_offset % page_size)
+        return fail(SGL_KV_PLAN_UNALIGNED_TOKEN_OFFSET, nullptr, request_index, token_offset,
+                    page_size, "KV transfer token offset %llu is not aligned to page size %llu",
+                    (unsigned long long)token_offset, (unsigned long long)page_size);
+    uint64_t n = 0;
+    for (uint64_t first = 0; first < slot_len; first += page_size) {
+        const uint64_t head = cache_slots[first];
+        if (head % page_size)
+            return fail(SGL_KV_PLAN_UNALIGNED_CACHE_SLOT, nullptr, request_index, head, page_size,
+                        "KV transfer cache slot %llu is not aligned to page size %llu",
+                        (unsigned long long)head, (unsigned long long)page_size);
+        const uint64_t stop = slot_len - first < page_size ? slot_len : first + page_size;
+        for (uint64_t i = first; i < stop; ++i)
+            if (cache_slots[i] != head + (i - first))
+                return fail(SGL_KV_PLAN_NON_CONTIGUOUS_CACHE_SLOTS, nullptr, request_index,
+                            head + (i - first), cache_slots[i],
+                            "KV transfer cache slots are not contiguous: expected %llu, got %llu",
+                            (unsigned long long)(head + (i - first)),
+                            (unsigned long long)cache_slots[i]);
+        out_pages[n++] = head / page_size;
+    }
+    *out_len = n;
+    return ok();
+}
+
+// View of one layer of a paged pool for the per-layer copies.
+extern "C" int32_t sgl_kv_pool_view_for_layer(const sgl_kv_paged_layout *layout, void *base,
+                                              uint64_t byte_len, uint32_t head_layout,
+                                              uint64_t heads, uint64_t layer_index,
+                                              uint64_t first_tensor, uint64_t tensor_count,
+                                              sgl_kv_pool_view *out) {
+    if (!layout || !out) return fail(SGL_KV_INVALID_ARGUMENT, "layout/out", 0, 0, 0, "null argument");
+    const sgl_kv_runtime_layout &rt = layout->runtime;
+    if (layer_index >= rt.num_layers)
+        return fail(SGL_KV_LAYOUT_LAYER_OUT_OF_RANGE, nullptr, layer_index, rt.num_layers, 0,
+                    "KV cache layer index %llu is outside %llu layers",
+                    (unsigned long long)layer_index, (unsigned long long)rt.num_layers);
+    if (tensor_count == 0 || tensor_count > 2)
+        return fail(SGL_KV_INVALID_ARGUMENT, "tensor_count", tensor_count, 2, 0,
+                    "a pool view holds one or two tensors, not %llu",
+                    (unsigned long long)tensor_count);
+    if (first_tensor + tensor_count > rt.kv_tensors_per_token)
+        return tensor_out_of_range(layout, first_tensor + tensor_count - 1);
+    if (head_layout > SGL_KV_HND)
+        return fail(SGL_KV_INVALID_ARGUMENT, "head_layout", head_layout, 0, 0,
+                    "unknown head layout %u", head_layout);
+    uint64_t tb[2] = {0, 0}, to[2] = {0, 0}, layer_off;
+    if (mul_ovf(layer_index, layout->bytes_per_layer_page, &layer_off)) return layout_overflow();
+    for (uint64_t t = 0; t < tensor_count; ++t) {
+        int32_t rc = tensor_geometry(layout, first_tensor + t, &tb[t], &to[t]);
+        if (rc) return rc;
+        if (add_ovf(to[t], layer_off, &to[t])) return layout_overflow();
+    }
+    if (tensor_count == 2 && tb[0] != tb[1])
+        return fail(SGL_KV_LAYOUT_UNEVEN_KV_PAIR_COPY, nullptr, tb[0], tb[1], 0,
+                    "the selected KV copy/attention kernel requires equal key and value widths, "
+                    "but the layout has %llu key bytes and %llu value bytes per token",
+                    (unsigned long long)tb[0], (unsigned long long)tb[1]);
+    if (heads == 0 || heads > UINT32_MAX || tb[0] % heads)
+        return fail(SGL_KV_INVALID_ARGUMENT, "heads", heads, tb[0], 0,
+                    "%llu heads do not split a %llu-byte row evenly", (unsigned long long)heads,
+                    (unsigned long long)tb[0]);
+    sgl_kv_pool_view v;
+    memset(&v, 0, sizeof v);
+    v.base = base;
+    v.byte_len = byte_len;
+    v.page_size = rt.page_size;
+    v.page_stride_bytes = rt.page_size_bytes;
+    v.page_count = layout->page_count;
+    v.tensor_offset[0] = to[0];
+    v.tensor_offset[1] = to[1];
+    v.row_bytes = tb[0];
+    v.tensor_count = (uint32_t)tensor_count;
+    v.heads = (uint32_t)heads;
+    v.head_layout = head_layout;
+    *out = v;
+    return ok();
+}

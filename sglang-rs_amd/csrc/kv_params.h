@@ -1,0 +1,99 @@
+/*
+ * kv_params.h -- launch parameters shared by the host launcher
+ * (kv_runtime.cpp) and the gfx950 kernels (kv_kernels.hip).
+ *
+ * Every copy on this path moves whole "rows": the bytes one token owns in
+ * one layer for each of its tensors (K and V, or the single MLA latent row).
+ * A copy has a source side and a destination side, each of one of two kinds:
+ *
+ *  ROWS  contiguous transfer rows: row r of tensor t starts at
+ *        plane[t] + r * stride[t]; the row is token-major (heads then dim).
+ *  POOL  one layer of a page-major pool: row r lives in physical slot
+ *        slots[r]; page = slot / page_size, pos = slot % page_size and the
+ *        row's tensor-t bytes start at
+ *            plane[t] + page * stride + pos * pos_mult
+ *        where plane[t] already includes the layer's in-page tensor offset
+ *        (PagedKvCacheLayout::tensor_token_byte_range,
+ *        crates/sglang-srt/src/kv_cache.rs:653-700). Head chunk h of the row
+ *        sits head_stride bytes after chunk h-1: NHD pages keep the row
+ *        contiguous (head_stride = chunk bytes, pos_mult = row bytes), HND
+ *        pages put each head's page_size chunks together (head_stride =
+ *        page_size * chunk bytes, pos_mult = chunk bytes).
+ *
+ * Vectors: the host picks the widest access width VB in {16, 8, 4, 2, 1}
+ * that divides every base, stride and chunk size, so every access is
+ * naturally aligned. Sizes below are in units of VB.
+ */
+#ifndef SGLKV_PARAMS_H
+#define SGLKV_PARAMS_H
+
+#include <stdint.h>
+
+#define SGLKV_SIDE_ROWS 0u
+#define SGLKV_SIDE_POOL 1u
+
+/* Threads per workgroup and the largest row tile one workgroup stages. */
+#define SGLKV_BLOCK_THREADS 256u
+#define SGLKV_MAX_TILE_ROWS 512u
+/* Rows each thread keeps in flight (loads issued before the stores). */
+#define SGLKV_ROWS_PER_THREAD 8u
+
+/* Bits of the device error word. */
+#define SGLKV_FLAG_SLOT 1u /* a slot map entry >= slot_count (reference flag value) */
+#define SGLKV_FLAG_PAGE 2u /* a page-table entry out of range while resolving spans */
+#define SGLKV_FLAG_SPAN 4u /* a row not covered by any span */
+
+/* A resolved row offset that must not be touched. */
+#define SGLKV_INVALID_OFFSET 0xFFFFFFFFFFFFFFFFull
+
+typedef struct sglkv_side {
+    uint64_t plane[2];      /* byte address of tensor t's data (see above) */
+    uint64_t stride[2];     /* ROWS: row stride of tensor t; POOL: page stride (both) */
+    const uint64_t *slots;  /* POOL: physical slot of each row */
+    uint64_t pos_mult;      /* POOL: bytes between adjacent in-page positions */
+    uint64_t head_stride;   /* bytes between head chunks of one row */
+    uint64_t slot_count;    /* POOL: valid slots are [0, slot_count) */
+    uint32_t page_size;     /* POOL: tokens per page */
+    uint32_t reserved;
+} sglkv_side;
+
+typedef struct sglkv_copy_params {
+    sglkv_side src;
+    sglkv_side dst;
+    uint32_t *flag;         /* device error word (OR of SGLKV_FLAG_*) */
+    float *scale_src;       /* optional per-layer scales copied bit-exactly */
+    float *scale_dst;
+    uint32_t scale_count;   /* number of floats to copy (0: none) */
+    uint32_t rows;          /* rows in this launch */
+    uint32_t vpr;           /* vectors per row, all tensors */
+    uint32_t vpt;           /* vectors per tensor row */
+    uint32_t vpc;           /* vectors per head chunk */
+    uint32_t tile_rows;     /* rows per workgroup = blockDim.y * SGLKV_ROWS_PER_THREAD */
+} sglkv_copy_params;
+
+/* One request's run of rows (KvCacheTransferSpan,
+ * crates/sglang-srt/src/transfer.rs:495-505): rows [row_start, row_start +
+ * token_count) hold request tokens [token_offset, token_offset +
+ * token_count); token k is in page page_table[page_table_start + k /
+ * page_size] at position k % page_size. */
+typedef struct sglkv_span {
+    uint32_t row_start;
+    uint32_t token_offset;
+    uint32_t token_count;
+    uint32_t page_table_start;
+} sglkv_span;
+
+typedef struct sglkv_resolve_params {
+    const sglkv_span *spans;  /* sorted by row_start, non-overlapping */
+    const int32_t *page_table;
+    uint64_t *out_slots;      /* one slot per row; SGLKV_INVALID_OFFSET on failure */
+    uint32_t *flag;
+    uint64_t page_table_len;
+    uint64_t page_count;      /* pages of the pool the table indexes */
+    uint32_t span_count;
+    uint32_t page_size;
+    uint32_t rows;
+    uint32_t reserved;
+} sglkv_resolve_params;
+
+#endif

@@ -1,0 +1,617 @@
+// kv_runtime.cpp -- kernel entry points of libsgl_rocm_kv (group 2 of
+// sgl_rocm_kv.h): context set-up, host validation and launches of the
+// gfx950 kernels in sgl_rocm_kv_gfx950.co.
+//
+// Validation happens on the host before any launch, with the reference's
+// error variants (CudaKvPairCopyError, crates/sglang-kernel/src/
+// cuda_kv_kernels.rs:304-338, and CudaError::AllocationOutOfBounds,
+// crates/sglang-kernel/src/cuda.rs:895-916). What only the device can see
+// (a slot or page-table entry outside the pool) is reported through the
+// context's error word.
+#include <dlfcn.h>
+#include <hip/hip_runtime.h>
+#include <string.h>
+
+#include <string>
+
+#include "kv_internal.h"
+#include "kv_params.h"
+
+using namespace sglkv;
+
+namespace {
+
+constexpr int kWidths[5] = {16, 8, 4, 2, 1};
+constexpr int kPoolRows = 0, kRowsPool = 1, kPoolPool = 2;
+const char *const kKindNames[3] = {"pool_rows", "rows_pool", "pool_pool"};
+
+int32_t hip_fail(hipError_t err, const char *call) {
+    return fail(SGL_KV_HIP, call, (uint64_t)err, 0, 0, "%s failed: %s (%d)", call,
+                hipGetErrorString(err), (int)err);
+}
+
+#define SGLKV_HIP(call)                                     \
+    do {                                                    \
+        hipError_t e_ = (call);                             \
+        if (e_ != hipSuccess) return hip_fail(e_, #call);   \
+    } while (0)
+
+// Makes the context's device current for one call and restores the
+// caller's device afterwards (the reference pushes and pops its CUDA
+// context around every call, crates/sglang-kernel/src/cuda.rs:559-586).
+class DeviceScope {
+  public:
+    explicit DeviceScope(int device) : prev_(-1), err_(hipSuccess) {
+        err_ = hipGetDevice(&prev_);
+        if (err_ == hipSuccess && prev_ != device) err_ = hipSetDevice(device);
+        device_ = device;
+    }
+    ~DeviceScope() {
+        if (prev_ >= 0 && prev_ != device_) (void)hipSetDevice(prev_);
+    }
+    hipError_t status() const { return err_; }
+
+  private:
+    int prev_, device_;
+    hipError_t err_;
+};
+
+int32_t out_of_bounds(const char *name, uint64_t offset, uint64_t len, uint64_t have) {
+    return fail(SGL_KV_ALLOCATION_OUT_OF_BOUNDS, name, offset, len, have,
+                "allocation %s range [%llu, +%llu) exceeds its %llu bytes", name,
+                (unsigned long long)offset, (unsigned long long)len, (unsigned long long)have);
+}
+
+int32_t too_large(const char *name, uint64_t value, uint64_t maximum) {
+    return fail(SGL_KV_DIMENSION_TOO_LARGE, name, value, maximum, 0,
+                "KV copy dimension %s=%llu exceeds maximum %llu", name, (unsigned long long)value,
+                (unsigned long long)maximum);
+}
+
+int32_t shape_overflow() {
+    return fail(SGL_KV_SHAPE_OVERFLOW, nullptr, 0, 0, 0, "KV copy tensor shape overflowed");
+}
+
+// Geometry common to both sides of a copy.
+struct RowShape {
+    uint64_t row_bytes;
+    uint32_t tensors;
+    uint32_t heads;  // > 1 only when a side is head-major
+    bool split;      // some side is HND: copy head chunk by head chunk
+};
+
+// Validates one pool side and fills its kernel description.
+int32_t pool_side(const sgl_kv_pool_view *v, const sgl_kv_device_buffer *slots, uint64_t rows,
+                  const RowShape &shape, sglkv_side *out) {
+    if (!v || !v->base) return fail(SGL_KV_INVALID_ARGUMENT, "pool", 0, 0, 0, "null pool view");
+    if (!slots || !slots->ptr)
+        return fail(SGL_KV_INVALID_ARGUMENT, "slot_indices", 0, 0, 0, "null slot map");
+    uint64_t need;
+    if (mul_ovf(rows, 8, &need)) return shape_overflow();
+    if (need > slots->byte_len) return out_of_bounds("slot_indices", 0, need, slots->byte_len);
+    uint64_t slot_count, tensor_page_bytes;
+    if (mul_ovf(v->page_size, v->page_count, &slot_count) ||
+        mul_ovf(v->page_size, v->row_bytes, &tensor_page_bytes))
+        return shape_overflow();
+    if (slot_count > UINT32_MAX) return too_large("slot_count", slot_count, UINT32_MAX);
+    const char *names[2] = {v->tensor_count == 2 ? "key" : "latent", "value"};
+    uint64_t ends[2] = {0, 0};
+    for (uint32_t t = 0; t < v->tensor_count; ++t) {
+        if (add_ovf(v->tensor_offset[t], tensor_page_bytes, &ends[t])) return shape_overflow();
+        if (ends[t] > v->page_stride_bytes)
+            return fail(SGL_KV_TENSOR_PAGE_REGION_OUT_OF_BOUNDS, names[t], v->tensor_offset[t],
+                        tensor_page_bytes, v->page_stride_bytes,
+                        "KV copy %s page region [%llu, %llu) exceeds page stride %llu", names[t],
+                        (unsigned long long)v->tensor_offset[t], (unsigned long long)ends[t],
+                        (unsigned long long)v->page_stride_bytes);
+    }
+    if (v->tensor_count == 2 && v->tensor_offset[0] < ends[1] && v->tensor_offset[1] < ends[0])
+        return fail(SGL_KV_TENSOR_PAGE_REGIONS_OVERLAP, nullptr, v->tensor_offset[0],
+                    v->tensor_offset[1], tensor_page_bytes,
+                    "KV copy key/value page regions overlap: key offset %llu, value offset %llu, "
+                    "tensor page size %llu bytes",
+                    (unsigned long long)v->tensor_offset[0], (unsigned long long)v->tensor_offset[1],
+                    (unsigned long long)tensor_page_bytes);
+    // The pool must reach the end of the last slot's last tensor row
+    // (CudaKvPairCopyPlan's pool_required_bytes, cuda_kv_kernels.rs:220-234).
+    const uint64_t last_end = ends[0] > ends[1] ? ends[0] : ends[1];
+    uint64_t required;
+    if (mul_ovf(v->page_count - 1, v->page_stride_bytes, &required) ||
+        add_ovf(required, last_end, &required))
+        return shape_overflow();
+    if (required > v->byte_len) return out_of_bounds("pool", 0, required, v->byte_len);
+
+    const uint64_t chunk = shape.split ? shape.row_bytes / shape.heads : shape.row_bytes;
+    const bool hnd = v->head_layout == SGL_KV_HND;
+    memset(out, 0, sizeof *out);
+    const uint64_t base = (uint64_t)(uintptr_t)v->base;
+    out->plane[0] = base + v->tensor_offset[0];
+    out->plane[1] = base + (v->tensor_count == 2 ? v->tensor_offset[1] : v->tensor_offset[0]);
+    out->stride[0] = out->stride[1] = v->page_stride_bytes;
+    out->slots = static_cast<const uint64_t *>(slots->ptr);
+    out->pos_mult = hnd ? chunk : v->row_bytes;
+    out->head_stride = hnd ? v->page_size * chunk : chunk;
+    out->slot_count = slot_count;
+    out->page_size = (uint32_t)v->page_size;
+    return SGL_KV_OK;
+}
+
+int32_t check_pool_shape(const sgl_kv_pool_view *v) {
+    if (!v || !v->base) return fail(SGL_KV_INVALID_ARGUMENT, "pool", 0, 0, 0, "null pool view");
+    const struct {
+        const char *name;
+        uint64_t value;
+    } dims[] = {{"page_size", v->page_size},
+                {"page_stride_bytes", v->page_stride_bytes},
+                {"page_count", v->page_count},
+                {"row_bytes", v->row_bytes},
+                {"tensor_count", v->tensor_count},
+                {"heads", v->heads}};
+    for (const auto &d : dims)
+        if (d.value == 0)
+            return fail(SGL_KV_ZERO_DIMENSION, d.name, 0, 0, 0, "KV copy dimension %s must be non-zero",
+                        d.name);
+    if (v->tensor_count > 2)
+        return fail(SGL_KV_INVALID_ARGUMENT, "tensor_count", v->tensor_count, 2, 0,
+                    "a pool view holds one or two tensors, not %u", v->tensor_count);
+    if (v->head_layout > SGL_KV_HND)
+        return fail(SGL_KV_INVALID_ARGUMENT, "head_layout", v->head_layout, 0, 0,
+                    "unknown head layout %u", v->head_layout);
+    if (v->page_size > UINT32_MAX) return too_large("page_size", v->page_size, UINT32_MAX);
+    if (v->head_layout == SGL_KV_HND && v->row_bytes % v->heads)
+        return fail(SGL_KV_INVALID_ARGUMENT, "heads", v->heads, v->row_bytes, 0,
+                    "%u heads do not split a %llu-byte row evenly", v->heads,
+                    (unsigned long long)v->row_bytes);
+    return SGL_KV_OK;
+}
+
+// Validates a transfer-rows side; `names` label the planes in errors.
+int32_t rows_side(const sgl_kv_rows_view *v, uint64_t rows, const RowShape &shape,
+                  const char *const names[2], sglkv_side *out) {
+    if (!v) return fail(SGL_KV_INVALID_ARGUMENT, "rows", 0, 0, 0, "null rows view");
+    memset(out, 0, sizeof *out);
+    for (uint32_t t = 0; t < shape.tensors; ++t) {
+        if (!v->planes[t]) return fail(SGL_KV_INVALID_ARGUMENT, names[t], 0, 0, 0, "null plane");
+        if (v->row_stride[t] < shape.row_bytes)
+            return fail(SGL_KV_ROW_STRIDE_TOO_SMALL, names[t], shape.row_bytes, v->row_stride[t], 0,
+                        "KV copy %s row stride %llu bytes is smaller than row width %llu bytes",
+                        names[t], (unsigned long long)v->row_stride[t],
+                        (unsigned long long)shape.row_bytes);
+        uint64_t need;
+        if (mul_ovf(rows - 1, v->row_stride[t], &need) || add_ovf(need, shape.row_bytes, &need))
+            return shape_overflow();
+        if (need > v->plane_bytes[t]) return out_of_bounds(names[t], 0, need, v->plane_bytes[t]);
+        out->plane[t] = (uint64_t)(uintptr_t)v->planes[t];
+        out->stride[t] = v->row_stride[t];
+    }
+    if (shape.tensors == 1) {
+        out->plane[1] = out->plane[0];
+        out->stride[1] = out->stride[0];
+    }
+    out->head_stride = shape.split ? shape.row_bytes / shape.heads : shape.row_bytes;
+    return SGL_KV_OK;
+}
+
+// Widest power-of-two access (<= 16 bytes) that divides every address and
+// stride either side computes.
+int vector_bytes(const sglkv_side &s, const sglkv_side &d, uint64_t chunk) {
+    uint64_t bits = chunk;
+    for (const sglkv_side *x : {&s, &d})
+        bits |= x->plane[0] | x->plane[1] | x->stride[0] | x->stride[1] | x->pos_mult |
+                x->head_stride;
+    int vb = 16;
+    while (vb > 1 && (bits & (uint64_t)(vb - 1))) vb >>= 1;
+    return vb;
+}
+
+}  // namespace
+
+struct sgl_rocm_kv_ctx {
+    int device;
+    int cu_count;
+    hipModule_t module;
+    hipFunction_t copy[5][3];
+    hipFunction_t resolve;
+    hipFunction_t fill;
+    uint32_t *flag;
+};
+
+namespace {
+
+std::string default_code_object() {
+    Dl_info info;
+    if (dladdr(reinterpret_cast<void *>(&sgl_rocm_kv_init), &info) && info.dli_fname) {
+        std::string path(info.dli_fname);
+        const size_t slash = path.rfind('/');
+        return (slash == std::string::npos ? std::string(".") : path.substr(0, slash)) +
+               "/sgl_rocm_kv_gfx950.co";
+    }
+    return "sgl_rocm_kv_gfx950.co";
+}
+
+int32_t launch_copy(sgl_rocm_kv_ctx *ctx, int kind, sglkv_copy_params &p, const RowShape &shape,
+                    uint64_t rows, hipStream_t stream) {
+    if (rows > UINT32_MAX) return too_large("row_count", rows, UINT32_MAX);
+    const uint64_t chunk = shape.split ? shape.row_bytes / shape.heads : shape.row_bytes;
+    const int vb = vector_bytes(p.src, p.dst, chunk);
+    uint64_t row_vectors = shape.row_bytes / vb * shape.tensors;
+    if (row_vectors > (1ull << 31)) return too_large("row_bytes", shape.row_bytes, 1ull << 30);
+    int wi = 0;
+    while (kWidths[wi] != vb) ++wi;
+    p.flag = ctx->flag;
+    p.rows = (uint32_t)rows;
+    p.vpr = (uint32_t)row_vectors;
+    p.vpt = (uint32_t)(shape.row_bytes / vb);
+    p.vpc = (uint32_t)(chunk / vb);
+    const uint32_t bx = p.vpr < SGLKV_BLOCK_THREADS ? p.vpr : SGLKV_BLOCK_THREADS;
+    uint32_t by = SGLKV_BLOCK_THREADS / bx;
+    if (by > SGLKV_MAX_TILE_ROWS / SGLKV_ROWS_PER_THREAD) by = SGLKV_MAX_TILE_ROWS / SGLKV_ROWS_PER_THREAD;
+    p.tile_rows = by * SGLKV_ROWS_PER_THREAD;
+    const uint64_t grid = (rows + p.tile_rows - 1) / p.tile_rows;
+    if (grid > INT32_MAX) return too_large("grid blocks", grid, INT32_MAX);
+    void *args[] = {&p};
+    SGLKV_HIP(hipModuleLaunchKernel(ctx->copy[wi][kind], (unsigned)grid, 1, 1, bx, by, 1, 0, stream,
+                                    args, nullptr));
+    return SGL_KV_OK;
+}
+
+void attach_scales(sglkv_copy_params &p, float *src, float *dst, uint32_t tensors) {
+    if (src && dst) {
+        p.scale_src = src;
+        p.scale_dst = dst;
+        p.scale_count = tensors;
+    }
+}
+
+int32_t check_ctx(sgl_rocm_kv_ctx *ctx) {
+    if (!ctx) return fail(SGL_KV_INVALID_ARGUMENT, "ctx", 0, 0, 0, "null context");
+    return SGL_KV_OK;
+}
+
+int32_t device_of(const void *ptr, int *device) {
+    hipPointerAttribute_t attr;
+    memset(&attr, 0, sizeof attr);
+    hipError_t err = hipPointerGetAttributes(&attr, ptr);
+    if (err != hipSuccess) {
+        (void)hipGetLastError();
+        *device = -1;
+        return SGL_KV_OK;
+    }
+    *device = attr.type == hipMemoryTypeHost ? -1 : attr.device;
+    return SGL_KV_OK;
+}
+
+// CudaKvPairCopyKernels::validate_device (cuda_kv_kernels.rs:625-642).
+int32_t validate_device(const sgl_rocm_kv_ctx *ctx, const char *name, const sgl_kv_device_buffer &b) {
+    int dev;
+    device_of(b.ptr, &dev);
+    if (dev != ctx->device)
+        return fail(SGL_KV_DEVICE_MISMATCH, name, (uint64_t)ctx->device, (uint64_t)(int64_t)dev, 0,
+                    "KV copy allocation %s is on device %d, expected device %d", name, dev,
+                    ctx->device);
+    return SGL_KV_OK;
+}
+
+// CudaDeviceAllocation::device_ptr_at (cuda.rs:895-916).
+int32_t ptr_at(const char *name, const sgl_kv_device_buffer &b, uint64_t offset, uint64_t len,
+               uint64_t *out) {
+    uint64_t end;
+    if (add_ovf(offset, len, &end) || end > b.byte_len) return out_of_bounds(name, offset, len, b.byte_len);
+    *out = (uint64_t)(uintptr_t)b.ptr + offset;
+    return SGL_KV_OK;
+}
+
+// Launch, synchronise, read the error word (CudaKvPairCopyKernels::launch,
+// cuda_kv_kernels.rs:541-623).
+int32_t pair_copy(sgl_rocm_kv_ctx *ctx, const sgl_kv_pair_copy_plan *plan,
+                  const sgl_kv_pair_copy_buffers *b, hipStream_t stream, bool scatter) {
+    int32_t rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!plan || !b) return fail(SGL_KV_INVALID_ARGUMENT, "plan/buffers", 0, 0, 0, "null argument");
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    // Same check order as the reference: scatter validates keys, values,
+    // slots, pool; gather validates pool, slots, keys, values.
+    struct Buf {
+        const char *name;
+        const sgl_kv_device_buffer *buf;
+        uint64_t offset, required;
+        uint64_t *addr;
+    };
+    uint64_t keys = 0, values = 0, slots = 0, pool = 0;
+    const Buf k{"keys", &b->keys, b->keys_offset, plan->key_rows_required_bytes, &keys};
+    const Buf v{"values", &b->values, b->values_offset, plan->value_rows_required_bytes, &values};
+    const Buf s{"slot_indices", &b->slot_indices, b->slot_indices_offset,
+                plan->slot_indices_required_bytes, &slots};
+    const Buf q{"pool", &b->pool, b->pool_offset, plan->pool_required_bytes, &pool};
+    const Buf scatter_order[4] = {k, v, s, q};
+    const Buf gather_order[4] = {q, s, k, v};
+    const Buf *order = scatter ? scatter_order : gather_order;
+    for (int i = 0; i < 4; ++i)
+        if ((rc = validate_device(ctx, order[i].name, *order[i].buf))) return rc;
+    for (int i = 0; i < 4; ++i)
+        if ((rc = ptr_at(order[i].name, *order[i].buf, order[i].offset, order[i].required,
+                         order[i].addr)))
+            return rc;
+    if (plan->slot_count > UINT32_MAX) return too_large("slot_count", plan->slot_count, UINT32_MAX);
+    if (plan->layout.page_size > UINT32_MAX)
+        return too_large("page_size", plan->layout.page_size, UINT32_MAX);
+
+    RowShape shape{plan->layout.row_bytes, 2, 1, false};
+    sglkv_copy_params p;
+    memset(&p, 0, sizeof p);
+    sglkv_side &ps = scatter ? p.dst : p.src;
+    sglkv_side &rs = scatter ? p.src : p.dst;
+    ps.plane[0] = pool + plan->layout.key_in_page_offset;
+    ps.plane[1] = pool + plan->layout.value_in_page_offset;
+    ps.stride[0] = ps.stride[1] = plan->layout.page_stride_bytes;
+    ps.slots = reinterpret_cast<const uint64_t *>(slots);
+    ps.pos_mult = plan->layout.row_bytes;
+    ps.head_stride = plan->layout.row_bytes;
+    ps.slot_count = plan->slot_count;
+    ps.page_size = (uint32_t)plan->layout.page_size;
+    rs.plane[0] = keys;
+    rs.plane[1] = values;
+    rs.stride[0] = plan->key_row_stride_bytes;
+    rs.stride[1] = plan->value_row_stride_bytes;
+    rs.head_stride = plan->layout.row_bytes;
+
+    SGLKV_HIP(hipMemsetAsync(ctx->flag, 0, sizeof(uint32_t), stream));
+    rc = launch_copy(ctx, scatter ? kRowsPool : kPoolRows, p, shape, plan->row_count, stream);
+    if (rc) return rc;
+    SGLKV_HIP(hipStreamSynchronize(stream));
+    uint32_t flag = 0;
+    SGLKV_HIP(hipMemcpy(&flag, ctx->flag, sizeof flag, hipMemcpyDeviceToHost));
+    if (flag)
+        return fail(SGL_KV_DEVICE_SLOT_INDEX_OUT_OF_RANGE, nullptr, plan->slot_count, 0, 0,
+                    "KV copy device slot map contains an index outside %llu slots",
+                    (unsigned long long)plan->slot_count);
+    return ok();
+}
+
+}  // namespace
+
+extern "C" int32_t sgl_rocm_kv_init(int32_t device, const char *code_object_path,
+                                    sgl_rocm_kv_ctx **out) {
+    if (!out) return fail(SGL_KV_INVALID_ARGUMENT, "out", 0, 0, 0, "null argument");
+    *out = nullptr;
+    int count = 0;
+    hipError_t err = hipGetDeviceCount(&count);
+    if (err != hipSuccess) return hip_fail(err, "hipGetDeviceCount");
+    if (device < 0 || device >= count)
+        return fail(SGL_KV_INVALID_ARGUMENT, "device", (uint64_t)(int64_t)device, (uint64_t)count, 0,
+                    "device %d is not one of the %d visible devices", device, count);
+    DeviceScope scope(device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    const std::string path = code_object_path ? std::string(code_object_path) : default_code_object();
+    sgl_rocm_kv_ctx *ctx = new sgl_rocm_kv_ctx();
+    ctx->device = device;
+    err = hipModuleLoad(&ctx->module, path.c_str());
+    if (err != hipSuccess) {
+        delete ctx;
+        return fail(SGL_KV_MODULE, "hipModuleLoad", (uint64_t)err, 0, 0,
+                    "cannot load code object %s: %s", path.c_str(), hipGetErrorString(err));
+    }
+    for (int w = 0; w < 5; ++w)
+        for (int k = 0; k < 3; ++k) {
+            char name[64];
+            snprintf(name, sizeof name, "sglkv_copy_%s_v%d", kKindNames[k], kWidths[w]);
+            err = hipModuleGetFunction(&ctx->copy[w][k], ctx->module, name);
+            if (err != hipSuccess) {
+                (void)hipModuleUnload(ctx->module);
+                delete ctx;
+                return fail(SGL_KV_MODULE, name, (uint64_t)err, 0, 0,
+                            "code object %s lacks kernel %s", path.c_str(), name);
+            }
+        }
+    err = hipModuleGetFunction(&ctx->resolve, ctx->module, "sglkv_resolve_spans");
+    if (err == hipSuccess) err = hipModuleGetFunction(&ctx->fill, ctx->module, "sglkv_fill_synthetic");
+    if (err == hipSuccess) err = hipDeviceGetAttribute(&ctx->cu_count, hipDeviceAttributeMultiprocessorCount, device);
+    if (err == hipSuccess) err = hipMalloc(reinterpret_cast<void **>(&ctx->flag), sizeof(uint32_t));
+    if (err == hipSuccess) err = hipMemset(ctx->flag, 0, sizeof(uint32_t));
+    if (err != hipSuccess) {
+        if (ctx->flag) (void)hipFree(ctx->flag);
+        (void)hipModuleUnload(ctx->module);
+        delete ctx;
+        return hip_fail(err, "sgl_rocm_kv_init");
+    }
+    *out = ctx;
+    return ok();
+}
+
+extern "C" int32_t sgl_rocm_kv_destroy(sgl_rocm_kv_ctx *ctx) {
+    if (!ctx) return ok();
+    DeviceScope scope(ctx->device);
+    hipError_t e1 = hipFree(ctx->flag);
+    hipError_t e2 = hipModuleUnload(ctx->module);
+    delete ctx;
+    if (e1 != hipSuccess) return hip_fail(e1, "hipFree");
+    if (e2 != hipSuccess) return hip_fail(e2, "hipModuleUnload");
+    return ok();
+}
+
+extern "C" int32_t sgl_rocm_kv_device(const sgl_rocm_kv_ctx *ctx) { return ctx ? ctx->device : -1; }
+
+extern "C" int32_t sgl_rocm_kv_cu_count(const sgl_rocm_kv_ctx *ctx) { return ctx ? ctx->cu_count : 0; }
+
+extern "C" int32_t sgl_rocm_kv_pair_scatter(sgl_rocm_kv_ctx *ctx, const sgl_kv_pair_copy_plan *plan,
+                                            const sgl_kv_pair_copy_buffers *buffers, void *stream) {
+    return pair_copy(ctx, plan, buffers, static_cast<hipStream_t>(stream), true);
+}
+
+extern "C" int32_t sgl_rocm_kv_pair_gather(sgl_rocm_kv_ctx *ctx, const sgl_kv_pair_copy_plan *plan,
+                                           const sgl_kv_pair_copy_buffers *buffers, void *stream) {
+    return pair_copy(ctx, plan, buffers, static_cast<hipStream_t>(stream), false);
+}
+
+extern "C" int32_t sgl_rocm_kv_pack_layer(sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src,
+                                          const sgl_kv_device_buffer *slots, uint64_t row_count,
+                                          const sgl_kv_rows_view *dst, void *stream) {
+    int32_t rc = check_ctx(ctx);
+    if (!rc) rc = check_pool_shape(src);
+    if (rc) return rc;
+    if (!dst) return fail(SGL_KV_INVALID_ARGUMENT, "rows", 0, 0, 0, "null rows view");
+    if (row_count == 0) return ok();
+    const bool split = src->head_layout == SGL_KV_HND;
+    RowShape shape{src->row_bytes, src->tensor_count, split ? src->heads : 1u, split};
+    sglkv_copy_params p;
+    memset(&p, 0, sizeof p);
+    const char *names[2] = {src->tensor_count == 2 ? "keys" : "rows", "values"};
+    if ((rc = pool_side(src, slots, row_count, shape, &p.src)) ||
+        (rc = rows_side(dst, row_count, shape, names, &p.dst)))
+        return rc;
+    attach_scales(p, src->scale, dst->scale, src->tensor_count);
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    rc = launch_copy(ctx, kPoolRows, p, shape, row_count, static_cast<hipStream_t>(stream));
+    return rc ? rc : ok();
+}
+
+extern "C" int32_t sgl_rocm_kv_unpack_layer(sgl_rocm_kv_ctx *ctx, const sgl_kv_rows_view *src,
+                                            uint64_t row_count, const sgl_kv_pool_view *dst,
+                                            const sgl_kv_device_buffer *slots, void *stream) {
+    int32_t rc = check_ctx(ctx);
+    if (!rc) rc = check_pool_shape(dst);
+    if (rc) return rc;
+    if (!src) return fail(SGL_KV_INVALID_ARGUMENT, "rows", 0, 0, 0, "null rows view");
+    if (row_count == 0) return ok();
+    const bool split = dst->head_layout == SGL_KV_HND;
+    RowShape shape{dst->row_bytes, dst->tensor_count, split ? dst->heads : 1u, split};
+    sglkv_copy_params p;
+    memset(&p, 0, sizeof p);
+    const char *names[2] = {dst->tensor_count == 2 ? "keys" : "rows", "values"};
+    if ((rc = rows_side(src, row_count, shape, names, &p.src)) ||
+        (rc = pool_side(dst, slots, row_count, shape, &p.dst)))
+        return rc;
+    attach_scales(p, src->scale, dst->scale, dst->tensor_count);
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    rc = launch_copy(ctx, kRowsPool, p, shape, row_count, static_cast<hipStream_t>(stream));
+    return rc ? rc : ok();
+}
+
+extern "C" int32_t sgl_rocm_kv_transfer_layer(sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src,
+                                              const sgl_kv_device_buffer *src_slots,
+                                              uint64_t row_count, const sgl_kv_pool_view *dst,
+                                              const sgl_kv_device_buffer *dst_slots, void *stream) {
+    int32_t rc = check_ctx(ctx);
+    if (!rc) rc = check_pool_shape(src);
+    if (!rc) rc = check_pool_shape(dst);
+    if (rc) return rc;
+    if (src->row_bytes != dst->row_bytes || src->tensor_count != dst->tensor_count)
+        return fail(SGL_KV_INVALID_ARGUMENT, "dst", dst->row_bytes, src->row_bytes, 0,
+                    "destination rows (%llu bytes x %u tensors) differ from source rows (%llu x %u)",
+                    (unsigned long long)dst->row_bytes, dst->tensor_count,
+                    (unsigned long long)src->row_bytes, src->tensor_count);
+    const bool split = src->head_layout == SGL_KV_HND || dst->head_layout == SGL_KV_HND;
+    if (split && src->heads != dst->heads)
+        return fail(SGL_KV_INVALID_ARGUMENT, "heads", dst->heads, src->heads, 0,
+                    "head-major relayout needs equal head counts (%u vs %u)", dst->heads, src->heads);
+    if (split && src->row_bytes % src->heads)
+        return fail(SGL_KV_INVALID_ARGUMENT, "heads", src->heads, src->row_bytes, 0,
+                    "%u heads do not split a %llu-byte row evenly", src->heads,
+                    (unsigned long long)src->row_bytes);
+    if (row_count == 0) return ok();
+    RowShape shape{src->row_bytes, src->tensor_count, split ? src->heads : 1u, split};
+    sglkv_copy_params p;
+    memset(&p, 0, sizeof p);
+    if ((rc = pool_side(src, src_slots, row_count, shape, &p.src)) ||
+        (rc = pool_side(dst, dst_slots, row_count, shape, &p.dst)))
+        return rc;
+    attach_scales(p, src->scale, dst->scale, src->tensor_count);
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    rc = launch_copy(ctx, kPoolPool, p, shape, row_count, static_cast<hipStream_t>(stream));
+    return rc ? rc : ok();
+}
+
+extern "C" int32_t sgl_rocm_kv_resolve_spans(sgl_rocm_kv_ctx *ctx, uint64_t page_size,
+                                             uint64_t page_count, const sgl_kv_device_buffer *spans,
+                                             uint64_t span_count,
+                                             const sgl_kv_device_buffer *page_table,
+                                             uint64_t page_table_len, uint64_t row_count,
+                                             const sgl_kv_device_buffer *out_slots, void *stream) {
+    int32_t rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (page_size == 0) return fail(SGL_KV_ZERO_DIMENSION, "page_size", 0, 0, 0, "KV copy dimension page_size must be non-zero");
+    if (page_size > UINT32_MAX) return too_large("page_size", page_size, UINT32_MAX);
+    if (span_count > UINT32_MAX) return too_large("span_count", span_count, UINT32_MAX);
+    if (row_count > UINT32_MAX) return too_large("row_count", row_count, UINT32_MAX);
+    if (row_count == 0) return ok();
+    if (!spans || !page_table || !out_slots || !out_slots->ptr || (span_count && !spans->ptr) ||
+        (page_table_len && !page_table->ptr))
+        return fail(SGL_KV_INVALID_ARGUMENT, "spans/page_table/out_slots", 0, 0, 0, "null buffer");
+    uint64_t need;
+    if (mul_ovf(span_count, sizeof(sgl_kv_span), &need)) return shape_overflow();
+    if (need > spans->byte_len) return out_of_bounds("spans", 0, need, spans->byte_len);
+    if (mul_ovf(page_table_len, 4, &need)) return shape_overflow();
+    if (need > page_table->byte_len) return out_of_bounds("page_table", 0, need, page_table->byte_len);
+    if (mul_ovf(row_count, 8, &need)) return shape_overflow();
+    if (need > out_slots->byte_len) return out_of_bounds("out_slots", 0, need, out_slots->byte_len);
+    static_assert(sizeof(sgl_kv_span) == sizeof(sglkv_span), "span layouts differ");
+    sglkv_resolve_params p;
+    memset(&p, 0, sizeof p);
+    p.spans = static_cast<const sglkv_span *>(spans->ptr);
+    p.page_table = static_cast<const int32_t *>(page_table->ptr);
+    p.out_slots = static_cast<uint64_t *>(out_slots->ptr);
+    p.flag = ctx->flag;
+    p.page_table_len = page_table_len;
+    p.page_count = page_count;
+    p.span_count = (uint32_t)span_count;
+    p.page_size = (uint32_t)page_size;
+    p.rows = (uint32_t)row_count;
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    void *args[] = {&p};
+    const uint64_t grid = (row_count + SGLKV_BLOCK_THREADS - 1) / SGLKV_BLOCK_THREADS;
+    SGLKV_HIP(hipModuleLaunchKernel(ctx->resolve, (unsigned)grid, 1, 1, SGLKV_BLOCK_THREADS, 1, 1, 0,
+                                    static_cast<hipStream_t>(stream), args, nullptr));
+    return ok();
+}
+
+extern "C" int32_t sgl_rocm_kv_check_errors(sgl_rocm_kv_ctx *ctx, void *stream) {
+    int32_t rc = check_ctx(ctx);
+    if (rc) return rc;
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    SGLKV_HIP(hipStreamSynchronize(s));
+    uint32_t flag = 0;
+    SGLKV_HIP(hipMemcpy(&flag, ctx->flag, sizeof flag, hipMemcpyDeviceToHost));
+    if (flag) SGLKV_HIP(hipMemset(ctx->flag, 0, sizeof(uint32_t)));
+    if (flag & SGLKV_FLAG_SLOT)
+        return fail(SGL_KV_DEVICE_SLOT_INDEX_OUT_OF_RANGE, nullptr, 0, flag, 0,
+                    "KV copy device slot map contains an index outside the pool's slots");
+    if (flag & SGLKV_FLAG_PAGE)
+        return fail(SGL_KV_DEVICE_PAGE_INDEX_OUT_OF_RANGE, nullptr, 0, flag, 0,
+                    "KV transfer page table holds an entry outside the table or the pool");
+    if (flag & SGLKV_FLAG_SPAN)
+        return fail(SGL_KV_DEVICE_SPAN_OUT_OF_RANGE, nullptr, 0, flag, 0,
+                    "KV transfer row is not covered by any span");
+    return ok();
+}
+
+extern "C" int32_t sgl_rocm_kv_fill_synthetic(sgl_rocm_kv_ctx *ctx, const sgl_kv_device_buffer *buffer,
+                                              uint64_t seed, uint32_t kind, void *stream) {
+    int32_t rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!buffer || !buffer->ptr) return fail(SGL_KV_INVALID_ARGUMENT, "buffer", 0, 0, 0, "null buffer");
+    if (buffer->byte_len % 8)
+        return fail(SGL_KV_INVALID_ARGUMENT, "buffer", buffer->byte_len, 8, 0,
+                    "fill length %llu is not a multiple of 8 bytes",
+                    (unsigned long long)buffer->byte_len);
+    if (kind > SGL_KV_FILL_BF16_UNIFORM)
+        return fail(SGL_KV_INVALID_ARGUMENT, "kind", kind, 0, 0, "unknown fill kind %u", kind);
+    uint64_t words = buffer->byte_len / 8;
+    if (words == 0) return ok();
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    uint64_t blocks = (words + SGLKV_BLOCK_THREADS - 1) / SGLKV_BLOCK_THREADS;
+    const uint64_t cap = (uint64_t)(ctx->cu_count > 0 ? ctx->cu_count : 1) * 32;
+    if (blocks > cap) blocks = cap;
+    void *ptr = buffer->ptr;
+    void *args[] = {&ptr, &words, &seed, &kind};
+    SGLKV_HIP(hipModuleLaunchKernel(ctx->fill, (unsigned)blocks, 1, 1, SGLKV_BLOCK_THREADS, 1, 1, 0,
+                                    static_cast<hipStream_t>(stream), args, nullptr));
+    return ok();
+}

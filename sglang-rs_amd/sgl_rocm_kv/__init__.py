@@ -1,0 +1,566 @@
+"""Python binding of libsgl_rocm_kv, the MI355X (gfx950) backend of
+sglang-rs's KV-cache copy / PD-transfer path.
+
+The names mirror the reference's Rust API so that code and tests read the
+same way:
+
+========================================  =====================================================
+here                                      reference
+========================================  =====================================================
+``KvCacheRuntimeLayout``                  ``KvCacheRuntimeLayout`` (crates/sglang-srt/src/kv_cache.rs:57-66)
+``PagedKvCacheLayout``                    ``PagedKvCacheLayout`` (kv_cache.rs:436-823)
+``KvPairCopyLayout`` / ``KvPairCopyPlan`` ``CudaKvPairCopyLayout`` / ``CudaKvPairCopyPlan`` (crates/sglang-kernel/src/cuda_kv_kernels.rs:105-301)
+``RocmKvPairCopyKernels``                 ``CudaKvPairCopyKernels`` (cuda_kv_kernels.rs:416-642)
+``transfer_page_indices``                 ``transfer_page_indices`` (crates/sglang-srt/src/transfer.rs:679-720)
+``KvError``                               ``CudaKvPairCopyError`` / ``PagedKvCacheLayoutError`` / ``KvCacheTransferPlanError``
+========================================  =====================================================
+
+``RocmKvPairCopyKernels`` adds the per-layer PD transfer calls (pack,
+unpack, pool-to-pool transfer, span resolution) that the reference does not
+have. Every call goes to the native library; there is no Python or CPU
+fallback, and a missing library raises ``ExtensionMissing``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libsgl_rocm_kv.so")
+CODE_OBJECT_PATH = os.path.join(_HERE, "sgl_rocm_kv_gfx950.co")
+
+# --- status codes (sgl_kv_status) ---------------------------------------------------------
+OK = 0
+ZERO_DIMENSION = 1
+SHAPE_OVERFLOW = 2
+DIMENSION_TOO_LARGE = 3
+ROW_STRIDE_TOO_SMALL = 4
+TENSOR_PAGE_REGION_OUT_OF_BOUNDS = 5
+TENSOR_PAGE_REGIONS_OVERLAP = 6
+DEVICE_MISMATCH = 7
+DEVICE_SLOT_INDEX_OUT_OF_RANGE = 8
+HIP = 9
+MODULE = 10
+ALLOCATION_OUT_OF_BOUNDS = 11
+INVALID_ARGUMENT = 12
+LAYOUT_ZERO_PAGE_COUNT = 20
+LAYOUT_ZERO_FIELD = 21
+LAYOUT_RUNTIME_PAGE_SIZE_MISMATCH = 22
+LAYOUT_UNEVEN_LAYER = 23
+LAYOUT_UNEVEN_TENSOR = 24
+LAYOUT_SIZE_OVERFLOW = 25
+LAYOUT_PAGE_OUT_OF_RANGE = 26
+LAYOUT_LAYER_OUT_OF_RANGE = 27
+LAYOUT_TENSOR_OUT_OF_RANGE = 28
+LAYOUT_TOKEN_OUT_OF_RANGE = 29
+LAYOUT_SLOT_OUT_OF_RANGE = 30
+LAYOUT_EMPTY_SLOT_MAP = 31
+LAYOUT_BATCH_SLOT_OUT_OF_RANGE = 32
+LAYOUT_KV_PAIR_REQUIRES_TWO_TENSORS = 33
+LAYOUT_TENSOR_PAIR_REQUIRES_TWO_TENSORS = 34
+LAYOUT_TENSOR_PAIR_SIZE_MISMATCH = 35
+LAYOUT_UNEVEN_KV_PAIR_COPY = 36
+PLAN_ZERO_PAGE_SIZE = 40
+PLAN_UNALIGNED_TOKEN_OFFSET = 43
+PLAN_UNALIGNED_CACHE_SLOT = 44
+PLAN_NON_CONTIGUOUS_CACHE_SLOTS = 45
+DEVICE_PAGE_INDEX_OUT_OF_RANGE = 50
+DEVICE_SPAN_OUT_OF_RANGE = 51
+
+DTYPES = {"auto": 0, "float32": 1, "bf16": 2, "bfloat16": 2, "fp8_e4m3": 3, "fp8_e5m2": 4,
+          "fp4_e2m1": 5}
+NHD, HND = 0, 1
+FILL_BITS, FILL_BF16_NORMAL, FILL_BF16_UNIFORM = 0, 1, 2
+
+
+class ExtensionMissing(RuntimeError):
+    """The native library or its gfx950 code object has not been built."""
+
+
+class KvError(Exception):
+    """A failed call: ``code`` (sgl_kv_status), ``variant`` (the reference's
+    error variant name), ``name`` and ``fields`` (a, b, c) of the variant."""
+
+    def __init__(self, code, variant, name, fields, message):
+        super().__init__(f"{variant}: {message}")
+        self.code, self.variant, self.name, self.fields, self.message = (
+            code, variant, name, fields, message)
+
+
+# --- C structs (field for field as include/sgl_rocm_kv.h) ------------------------------------
+_u64 = ctypes.c_uint64
+
+
+class _ErrorDetail(ctypes.Structure):
+    _fields_ = [("code", ctypes.c_int32), ("reserved", ctypes.c_int32), ("a", _u64), ("b", _u64),
+                ("c", _u64), ("name", ctypes.c_char * 64), ("message", ctypes.c_char * 320)]
+
+
+class _RuntimeLayout(ctypes.Structure):
+    _fields_ = [("dtype", ctypes.c_int32), ("reserved", ctypes.c_int32)] + [
+        (n, _u64) for n in ("page_size", "num_layers", "kv_heads", "head_dim",
+                            "kv_tensors_per_token", "bytes_per_token", "page_size_bytes")]
+
+
+class _PagedLayout(ctypes.Structure):
+    _fields_ = [("runtime", _RuntimeLayout), ("page_count", _u64),
+                ("bytes_per_token_per_layer", _u64), ("bytes_per_layer_page", _u64),
+                ("tensor_pair", _u64), ("token_bytes", _u64 * 2), ("tensor_page_bytes", _u64),
+                ("total_byte_len", _u64), ("slot_count", _u64)]
+
+
+class _PairCopyLayout(ctypes.Structure):
+    _fields_ = [(n, _u64) for n in ("page_size", "page_stride_bytes", "key_in_page_offset",
+                                    "value_in_page_offset", "row_bytes")]
+
+
+class _PairCopyPlan(ctypes.Structure):
+    _fields_ = [("row_count", _u64), ("slot_count", _u64), ("layout", _PairCopyLayout)] + [
+        (n, _u64) for n in ("key_row_stride_bytes", "value_row_stride_bytes",
+                            "key_rows_required_bytes", "value_rows_required_bytes",
+                            "slot_indices_required_bytes", "pool_required_bytes")]
+
+
+class _DeviceBuffer(ctypes.Structure):
+    _fields_ = [("ptr", ctypes.c_void_p), ("byte_len", _u64)]
+
+
+class _PairCopyBuffers(ctypes.Structure):
+    _fields_ = [("keys", _DeviceBuffer), ("keys_offset", _u64), ("values", _DeviceBuffer),
+                ("values_offset", _u64), ("slot_indices", _DeviceBuffer),
+                ("slot_indices_offset", _u64), ("pool", _DeviceBuffer), ("pool_offset", _u64)]
+
+
+class PoolView(ctypes.Structure):
+    """sgl_kv_pool_view: one layer of a page-major pool on the device."""
+    _fields_ = [("base", ctypes.c_void_p), ("byte_len", _u64), ("page_size", _u64),
+                ("page_stride_bytes", _u64), ("page_count", _u64), ("tensor_offset", _u64 * 2),
+                ("row_bytes", _u64), ("tensor_count", ctypes.c_uint32),
+                ("heads", ctypes.c_uint32), ("head_layout", ctypes.c_uint32),
+                ("reserved", ctypes.c_uint32), ("scale", ctypes.c_void_p)]
+
+
+class RowsView(ctypes.Structure):
+    """sgl_kv_rows_view: contiguous transfer rows, planes[t] + r * row_stride[t]."""
+    _fields_ = [("planes", ctypes.c_void_p * 2), ("plane_bytes", _u64 * 2),
+                ("row_stride", _u64 * 2), ("scale", ctypes.c_void_p)]
+
+
+SPAN_DTYPE = np.dtype([("row_start", "<u4"), ("token_offset", "<u4"), ("token_count", "<u4"),
+                       ("page_table_start", "<u4")])
+
+_EXPORTS = {
+    "sgl_kv_last_error": (None, [ctypes.POINTER(_ErrorDetail)]),
+    "sgl_kv_status_name": (ctypes.c_char_p, [ctypes.c_int32]),
+    "sgl_kv_dtype_bytes_per_element": (ctypes.c_size_t, [ctypes.c_int32]),
+    "sgl_kv_paged_layout_new": (ctypes.c_int32, [ctypes.POINTER(_RuntimeLayout), _u64,
+                                                 ctypes.POINTER(_PagedLayout)]),
+    "sgl_kv_paged_layout_new_with_tensor_pair": (
+        ctypes.c_int32, [ctypes.POINTER(_RuntimeLayout), _u64, _u64, _u64,
+                         ctypes.POINTER(_PagedLayout)]),
+    "sgl_kv_paged_layout_page_byte_range": (
+        ctypes.c_int32, [ctypes.POINTER(_PagedLayout), _u64, ctypes.POINTER(_u64),
+                         ctypes.POINTER(_u64)]),
+    "sgl_kv_paged_layout_tensor_token_byte_range": (
+        ctypes.c_int32, [ctypes.POINTER(_PagedLayout), _u64, _u64, _u64, _u64,
+                         ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
+    "sgl_kv_paged_layout_tensor_slot_byte_range": (
+        ctypes.c_int32, [ctypes.POINTER(_PagedLayout), _u64, _u64, _u64, ctypes.POINTER(_u64),
+                         ctypes.POINTER(_u64)]),
+    "sgl_kv_paged_layout_validate_slot_indices": (
+        ctypes.c_int32, [ctypes.POINTER(_PagedLayout), ctypes.POINTER(_u64), _u64]),
+    "sgl_kv_paged_layout_kv_pair_copy_geometry": (
+        ctypes.c_int32, [ctypes.POINTER(_PagedLayout), _u64, ctypes.POINTER(_PairCopyLayout)]),
+    "sgl_kv_pair_copy_plan_new": (
+        ctypes.c_int32, [_u64, _u64, ctypes.POINTER(_PairCopyLayout), _u64, _u64,
+                         ctypes.POINTER(_PairCopyPlan)]),
+    "sgl_kv_transfer_page_indices": (
+        ctypes.c_int32, [_u64, _u64, ctypes.POINTER(_u64), _u64, _u64, ctypes.POINTER(_u64),
+                         ctypes.POINTER(_u64)]),
+    "sgl_kv_pool_view_for_layer": (
+        ctypes.c_int32, [ctypes.POINTER(_PagedLayout), ctypes.c_void_p, _u64, ctypes.c_uint32,
+                         _u64, _u64, _u64, _u64, ctypes.POINTER(PoolView)]),
+    "sgl_rocm_kv_init": (ctypes.c_int32, [ctypes.c_int32, ctypes.c_char_p,
+                                          ctypes.POINTER(ctypes.c_void_p)]),
+    "sgl_rocm_kv_destroy": (ctypes.c_int32, [ctypes.c_void_p]),
+    "sgl_rocm_kv_device": (ctypes.c_int32, [ctypes.c_void_p]),
+    "sgl_rocm_kv_cu_count": (ctypes.c_int32, [ctypes.c_void_p]),
+    "sgl_rocm_kv_pair_scatter": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_PairCopyPlan),
+                                                  ctypes.POINTER(_PairCopyBuffers),
+                                                  ctypes.c_void_p]),
+    "sgl_rocm_kv_pair_gather": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_PairCopyPlan),
+                                                 ctypes.POINTER(_PairCopyBuffers),
+                                                 ctypes.c_void_p]),
+    "sgl_rocm_kv_pack_layer": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(PoolView),
+                                                ctypes.POINTER(_DeviceBuffer), _u64,
+                                                ctypes.POINTER(RowsView), ctypes.c_void_p]),
+    "sgl_rocm_kv_unpack_layer": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(RowsView), _u64,
+                                                  ctypes.POINTER(PoolView),
+                                                  ctypes.POINTER(_DeviceBuffer), ctypes.c_void_p]),
+    "sgl_rocm_kv_transfer_layer": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(PoolView),
+                                                    ctypes.POINTER(_DeviceBuffer), _u64,
+                                                    ctypes.POINTER(PoolView),
+                                                    ctypes.POINTER(_DeviceBuffer),
+                                                    ctypes.c_void_p]),
+    "sgl_rocm_kv_resolve_spans": (ctypes.c_int32, [ctypes.c_void_p, _u64, _u64,
+                                                   ctypes.POINTER(_DeviceBuffer), _u64,
+                                                   ctypes.POINTER(_DeviceBuffer), _u64, _u64,
+                                                   ctypes.POINTER(_DeviceBuffer),
+                                                   ctypes.c_void_p]),
+    "sgl_rocm_kv_check_errors": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_void_p]),
+    "sgl_rocm_kv_fill_synthetic": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_DeviceBuffer),
+                                                    _u64, ctypes.c_uint32, ctypes.c_void_p]),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded native library; raises ExtensionMissing when it is not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ExtensionMissing(
+                f"{LIB_PATH} is not built: run `python -c 'import __graft_entry__ as g; g.build()'`")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _EXPORTS.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def exported_names():
+    return list(_EXPORTS)
+
+
+def status_name(code: int) -> str:
+    return lib().sgl_kv_status_name(code).decode()
+
+
+def _raise(code: int):
+    d = _ErrorDetail()
+    lib().sgl_kv_last_error(ctypes.byref(d))
+    raise KvError(code, status_name(code), d.name.decode(), (d.a, d.b, d.c), d.message.decode())
+
+
+def _call(fn, *args):
+    code = fn(*args)
+    if code != OK:
+        _raise(code)
+
+
+def _u64_array(values) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(values, dtype=np.uint64))
+
+
+def _pu64(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.POINTER(_u64))
+
+
+# --- group 1: layout and plan ----------------------------------------------------------------
+
+@dataclass
+class KvCacheRuntimeLayout:
+    dtype: str
+    page_size: int
+    num_layers: int
+    kv_heads: int
+    head_dim: int
+    kv_tensors_per_token: int
+    bytes_per_token: int
+    page_size_bytes: int
+
+    def _c(self) -> _RuntimeLayout:
+        return _RuntimeLayout(DTYPES[self.dtype], 0, self.page_size, self.num_layers,
+                              self.kv_heads, self.head_dim, self.kv_tensors_per_token,
+                              self.bytes_per_token, self.page_size_bytes)
+
+    @classmethod
+    def for_model(cls, dtype: str, page_size: int, num_layers: int, kv_heads: int, head_dim: int,
+                  kv_tensors_per_token: int = 2) -> "KvCacheRuntimeLayout":
+        """Uniform K/V geometry (KvCacheModelLayout::multi_tensor)."""
+        elt = lib().sgl_kv_dtype_bytes_per_element(DTYPES[dtype])
+        bpt = num_layers * kv_tensors_per_token * kv_heads * head_dim * elt
+        return cls(dtype, page_size, num_layers, kv_heads, head_dim, kv_tensors_per_token, bpt,
+                   bpt * page_size)
+
+
+class PagedKvCacheLayout:
+    """PagedKvCacheLayout (kv_cache.rs:436-823): page -> layer -> tensor -> token."""
+
+    def __init__(self, c: _PagedLayout):
+        self._c = c
+
+    @classmethod
+    def new(cls, runtime: KvCacheRuntimeLayout, page_count: int) -> "PagedKvCacheLayout":
+        out = _PagedLayout()
+        rt = runtime._c()
+        _call(lib().sgl_kv_paged_layout_new, ctypes.byref(rt), page_count, ctypes.byref(out))
+        return cls(out)
+
+    @classmethod
+    def new_with_tensor_pair(cls, runtime: KvCacheRuntimeLayout, page_count: int,
+                             key_token_bytes: int, value_token_bytes: int) -> "PagedKvCacheLayout":
+        out = _PagedLayout()
+        rt = runtime._c()
+        _call(lib().sgl_kv_paged_layout_new_with_tensor_pair, ctypes.byref(rt), page_count,
+              key_token_bytes, value_token_bytes, ctypes.byref(out))
+        return cls(out)
+
+    page_count = property(lambda self: self._c.page_count)
+    total_byte_len = property(lambda self: self._c.total_byte_len)
+    slot_count = property(lambda self: self._c.slot_count)
+    bytes_per_token_per_layer = property(lambda self: self._c.bytes_per_token_per_layer)
+    bytes_per_layer_page = property(lambda self: self._c.bytes_per_layer_page)
+
+    @property
+    def bytes_per_token_per_tensor(self):
+        return None if self._c.tensor_pair else self._c.token_bytes[0]
+
+    @property
+    def bytes_per_tensor_page(self):
+        return None if self._c.tensor_pair else self._c.tensor_page_bytes
+
+    def _range(self, fn, *args):
+        s, e = _u64(), _u64()
+        _call(fn, ctypes.byref(self._c), *args, ctypes.byref(s), ctypes.byref(e))
+        return (s.value, e.value)
+
+    def page_byte_range(self, page):
+        return self._range(lib().sgl_kv_paged_layout_page_byte_range, page)
+
+    def tensor_token_byte_range(self, page, layer, tensor, token):
+        return self._range(lib().sgl_kv_paged_layout_tensor_token_byte_range, page, layer, tensor,
+                           token)
+
+    def tensor_slot_byte_range(self, layer, tensor, slot):
+        return self._range(lib().sgl_kv_paged_layout_tensor_slot_byte_range, layer, tensor, slot)
+
+    def validate_slot_indices(self, slots):
+        a = _u64_array(slots)
+        _call(lib().sgl_kv_paged_layout_validate_slot_indices, ctypes.byref(self._c), _pu64(a),
+              len(a))
+
+    def kv_pair_copy_geometry(self, layer) -> "KvPairCopyLayout":
+        out = _PairCopyLayout()
+        _call(lib().sgl_kv_paged_layout_kv_pair_copy_geometry, ctypes.byref(self._c), layer,
+              ctypes.byref(out))
+        return KvPairCopyLayout(out.page_size, out.page_stride_bytes, out.key_in_page_offset,
+                                out.value_in_page_offset, out.row_bytes)
+
+    def pool_view(self, base: int, byte_len: int, layer: int, head_layout: int = NHD,
+                  heads: int = 1, first_tensor: int = 0, tensor_count: int | None = None,
+                  scale: int | None = None) -> PoolView:
+        if tensor_count is None:
+            tensor_count = min(2, self._c.runtime.kv_tensors_per_token - first_tensor)
+        v = PoolView()
+        _call(lib().sgl_kv_pool_view_for_layer, ctypes.byref(self._c), base, byte_len,
+              head_layout, heads, layer, first_tensor, tensor_count, ctypes.byref(v))
+        v.scale = scale
+        return v
+
+
+@dataclass(frozen=True)
+class KvPairCopyLayout:
+    page_size: int
+    page_stride_bytes: int
+    key_in_page_offset: int
+    value_in_page_offset: int
+    row_bytes: int
+
+    def _c(self):
+        return _PairCopyLayout(self.page_size, self.page_stride_bytes, self.key_in_page_offset,
+                               self.value_in_page_offset, self.row_bytes)
+
+
+class KvPairCopyPlan:
+    """CudaKvPairCopyPlan (cuda_kv_kernels.rs:153-264)."""
+
+    def __init__(self, c: _PairCopyPlan):
+        self._c = c
+
+    @classmethod
+    def new(cls, row_count, slot_count, layout: KvPairCopyLayout, key_row_stride_bytes,
+            value_row_stride_bytes) -> "KvPairCopyPlan":
+        out = _PairCopyPlan()
+        lay = layout._c()
+        _call(lib().sgl_kv_pair_copy_plan_new, row_count, slot_count, ctypes.byref(lay),
+              key_row_stride_bytes, value_row_stride_bytes, ctypes.byref(out))
+        return cls(out)
+
+    row_count = property(lambda self: self._c.row_count)
+    slot_count = property(lambda self: self._c.slot_count)
+    key_row_stride_bytes = property(lambda self: self._c.key_row_stride_bytes)
+    value_row_stride_bytes = property(lambda self: self._c.value_row_stride_bytes)
+    key_rows_required_bytes = property(lambda self: self._c.key_rows_required_bytes)
+    value_rows_required_bytes = property(lambda self: self._c.value_rows_required_bytes)
+    slot_indices_required_bytes = property(lambda self: self._c.slot_indices_required_bytes)
+    pool_required_bytes = property(lambda self: self._c.pool_required_bytes)
+
+    @property
+    def layout(self) -> KvPairCopyLayout:
+        lay = self._c.layout
+        return KvPairCopyLayout(lay.page_size, lay.page_stride_bytes, lay.key_in_page_offset,
+                                lay.value_in_page_offset, lay.row_bytes)
+
+
+def transfer_page_indices(request_index: int, token_offset: int, cache_slots, page_size: int):
+    """transfer_page_indices (transfer.rs:679-720): page index of each page-sized
+    run of a request's cache slots."""
+    a = _u64_array(cache_slots)
+    out = np.zeros(max(1, -(-len(a) // max(page_size, 1))), dtype=np.uint64)
+    n = _u64()
+    _call(lib().sgl_kv_transfer_page_indices, request_index, token_offset, _pu64(a), len(a),
+          page_size, _pu64(out), ctypes.byref(n))
+    return out[: n.value].tolist()
+
+
+# --- group 2: device calls -------------------------------------------------------------------
+
+def device_buffer(ptr: int, byte_len: int) -> _DeviceBuffer:
+    return _DeviceBuffer(ptr, byte_len)
+
+
+def rows_view(planes, plane_bytes, row_stride, scale: int | None = None) -> RowsView:
+    planes, plane_bytes, row_stride = list(planes), list(plane_bytes), list(row_stride)
+    while len(planes) < 2:
+        planes.append(None)
+        plane_bytes.append(0)
+        row_stride.append(0)
+    v = RowsView()
+    v.planes[0], v.planes[1] = planes[0], planes[1]
+    v.plane_bytes[0], v.plane_bytes[1] = plane_bytes
+    v.row_stride[0], v.row_stride[1] = row_stride
+    v.scale = scale
+    return v
+
+
+def pool_view(base: int, byte_len: int, *, page_size: int, page_stride_bytes: int,
+              page_count: int, tensor_offset, row_bytes: int, tensor_count: int, heads: int = 1,
+              head_layout: int = NHD, scale: int | None = None) -> PoolView:
+    """A pool view filled directly (for pools this library did not describe)."""
+    v = PoolView()
+    v.base, v.byte_len, v.page_size = base, byte_len, page_size
+    v.page_stride_bytes, v.page_count = page_stride_bytes, page_count
+    offs = list(tensor_offset) + [0, 0]
+    v.tensor_offset[0], v.tensor_offset[1] = offs[0], offs[1]
+    v.row_bytes, v.tensor_count, v.heads, v.head_layout = row_bytes, tensor_count, heads, head_layout
+    v.scale = scale
+    return v
+
+
+def _stream(stream) -> int | None:
+    if stream is None:
+        return None
+    return getattr(stream, "handle", stream)
+
+
+class RocmKvPairCopyKernels:
+    """CudaKvPairCopyKernels (cuda_kv_kernels.rs:416-642) on MI355X, plus the
+    per-layer PD transfer calls. ``RocmKvPairCopyKernels.compile(device)``
+    loads the prebuilt gfx950 code object (no runtime compilation)."""
+
+    def __init__(self, device: int = 0, code_object: str | None = None):
+        if code_object is None and not os.path.exists(CODE_OBJECT_PATH):
+            raise ExtensionMissing(f"{CODE_OBJECT_PATH} is not built")
+        h = ctypes.c_void_p()
+        _call(lib().sgl_rocm_kv_init, device,
+              code_object.encode() if code_object else None, ctypes.byref(h))
+        self._h = h.value
+
+    compile = classmethod(lambda cls, device=0, code_object=None: cls(device, code_object))
+
+    @property
+    def device(self) -> int:
+        return lib().sgl_rocm_kv_device(self._h)
+
+    @property
+    def cu_count(self) -> int:
+        return lib().sgl_rocm_kv_cu_count(self._h)
+
+    def close(self):
+        if self._h:
+            _call(lib().sgl_rocm_kv_destroy, self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @staticmethod
+    def _buffers(keys, keys_offset, values, values_offset, slot_indices, slot_indices_offset,
+                 pool, pool_offset) -> _PairCopyBuffers:
+        def db(b):
+            return _DeviceBuffer(b.ptr, b.nbytes) if hasattr(b, "nbytes") else b
+        return _PairCopyBuffers(db(keys), keys_offset, db(values), values_offset,
+                                db(slot_indices), slot_indices_offset, db(pool), pool_offset)
+
+    def scatter(self, plan: KvPairCopyPlan, *, keys, values, slot_indices, pool, keys_offset=0,
+                values_offset=0, slot_indices_offset=0, pool_offset=0, stream=None):
+        """CudaKvPairCopyKernels::scatter: strided K/V rows -> pool slots; synchronous."""
+        b = self._buffers(keys, keys_offset, values, values_offset, slot_indices,
+                          slot_indices_offset, pool, pool_offset)
+        _call(lib().sgl_rocm_kv_pair_scatter, self._h, ctypes.byref(plan._c), ctypes.byref(b),
+              _stream(stream))
+
+    def gather(self, plan: KvPairCopyPlan, *, pool, slot_indices, keys, values, pool_offset=0,
+               slot_indices_offset=0, keys_offset=0, values_offset=0, stream=None):
+        """CudaKvPairCopyKernels::gather: pool slots -> strided K/V rows; synchronous."""
+        b = self._buffers(keys, keys_offset, values, values_offset, slot_indices,
+                          slot_indices_offset, pool, pool_offset)
+        _call(lib().sgl_rocm_kv_pair_gather, self._h, ctypes.byref(plan._c), ctypes.byref(b),
+              _stream(stream))
+
+    def pack_layer(self, src: PoolView, slots: _DeviceBuffer, row_count: int, dst: RowsView,
+                   stream=None):
+        _call(lib().sgl_rocm_kv_pack_layer, self._h, ctypes.byref(src), ctypes.byref(slots),
+              row_count, ctypes.byref(dst), _stream(stream))
+
+    def unpack_layer(self, src: RowsView, row_count: int, dst: PoolView, slots: _DeviceBuffer,
+                     stream=None):
+        _call(lib().sgl_rocm_kv_unpack_layer, self._h, ctypes.byref(src), row_count,
+              ctypes.byref(dst), ctypes.byref(slots), _stream(stream))
+
+    def transfer_layer(self, src: PoolView, src_slots: _DeviceBuffer, row_count: int,
+                       dst: PoolView, dst_slots: _DeviceBuffer, stream=None):
+        _call(lib().sgl_rocm_kv_transfer_layer, self._h, ctypes.byref(src),
+              ctypes.byref(src_slots), row_count, ctypes.byref(dst), ctypes.byref(dst_slots),
+              _stream(stream))
+
+    def resolve_spans(self, page_size: int, page_count: int, spans: _DeviceBuffer,
+                      span_count: int, page_table: _DeviceBuffer, page_table_len: int,
+                      row_count: int, out_slots: _DeviceBuffer, stream=None):
+        _call(lib().sgl_rocm_kv_resolve_spans, self._h, page_size, page_count,
+              ctypes.byref(spans), span_count, ctypes.byref(page_table), page_table_len,
+              row_count, ctypes.byref(out_slots), _stream(stream))
+
+    def check_errors(self, stream=None):
+        _call(lib().sgl_rocm_kv_check_errors, self._h, _stream(stream))
+
+    def fill_synthetic(self, buffer: _DeviceBuffer, seed: int, kind: int = FILL_BITS, stream=None):
+        _call(lib().sgl_rocm_kv_fill_synthetic, self._h, ctypes.byref(buffer), seed, kind,
+              _stream(stream))
+
+
+def synthetic_words(seed: int, word_index) -> np.ndarray:
+    """Host copy of the words at `word_index` (8-byte word indices) of a
+    FILL_BITS buffer: the splitmix64 stream the device fill writes."""
+    i = np.asarray(word_index, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        z = np.uint64(seed) + (i + np.uint64(1)) * np.uint64(0x9E3779B97F4A7C15)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        return z ^ (z >> np.uint64(31))

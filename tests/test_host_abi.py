@@ -1,0 +1,243 @@
+"""The product library on the CPU: it loads, exports every function the
+C-ABI header declares, and its host mirror of the reference's layout and
+plan arithmetic (group 1 of include/sgl_rocm_kv.h) returns the reference's
+own golden values and error variants. No kernel is launched here.
+"""
+import os
+import re
+
+import numpy as np
+import pytest
+
+import sgl_rocm_kv as kv
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_functions():
+    names = []
+    for fn in sorted(os.listdir(os.path.join(ROOT, "include"))):
+        if fn.endswith(".h"):
+            text = open(os.path.join(ROOT, "include", fn)).read()
+            text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+            names += re.findall(r"^\s*[A-Za-z_][\w \*]*?\b(sgl_\w+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def test_library_exports_every_declared_function():
+    import ctypes
+    names = _declared_functions()
+    assert len(names) >= 20, names
+    handle = ctypes.CDLL(kv.LIB_PATH)
+    missing = [n for n in names if not hasattr(handle, n)]
+    assert not missing, f"declared in include/ but not exported: {missing}"
+    # and the binding knows every one of them
+    assert sorted(kv.exported_names()) == names
+
+
+def test_code_object_is_built_for_gfx950():
+    with open(kv.CODE_OBJECT_PATH, "rb") as f:
+        head = f.read(64)
+    assert head[:4] == b"\x7fELF"
+    assert int.from_bytes(head[18:20], "little") == 224  # EM_AMDGPU
+    # e_flags: EF_AMDGPU_MACH in the low byte; gfx950 = 0x4f
+    assert int.from_bytes(head[48:52], "little") & 0xFF == 0x4F
+
+
+def _runtime(d, **patch):
+    r = dict(d)
+    r.update(patch)
+    return kv.KvCacheRuntimeLayout(r["dtype"], r["page_size"], r["num_layers"], r["kv_heads"],
+                                   r["head_dim"], r["kv_tensors_per_token"], r["bytes_per_token"],
+                                   r["page_size_bytes"])
+
+
+def test_paged_layout_goldens(goldens):
+    g = goldens["kv_cache_layout"]
+    lay = kv.PagedKvCacheLayout.new(_runtime(g["runtime"]), g["page_count"])
+    assert lay.bytes_per_token_per_layer == g["bytes_per_token_per_layer"]
+    assert lay.bytes_per_token_per_tensor == g["bytes_per_token_per_tensor"]
+    assert lay.bytes_per_layer_page == g["bytes_per_layer_page"]
+    assert lay.bytes_per_tensor_page == g["bytes_per_tensor_page"]
+    assert lay.total_byte_len == g["total_byte_len"]
+    assert lay.slot_count == g["slot_count"]
+    assert lay.page_byte_range(1) == tuple(g["page_byte_range_1"])
+    assert lay.tensor_token_byte_range(1, 1, 1, 3) == tuple(g["tensor_token_byte_range_1_1_1_3"])
+    assert lay.tensor_slot_byte_range(1, 1, 7) == tuple(g["tensor_slot_byte_range_1_1_7"])
+    for e in g["errors"]:
+        with pytest.raises(kv.KvError) as ei:
+            getattr(lay, e["call"])(*e["args"])
+        assert ei.value.variant == e["variant"] and list(ei.value.fields[:2]) == e["fields"], e
+    geo = lay.kv_pair_copy_geometry(1)
+    want = g["kv_pair_copy_geometry_layer_1"]
+    assert (geo.page_size, geo.page_stride_bytes, geo.key_in_page_offset,
+            geo.value_in_page_offset, geo.row_bytes) == (
+        want["page_size"], want["page_stride_bytes"], want["key_offset_bytes"],
+        want["value_offset_bytes"], want["token_bytes"])
+    lay.validate_slot_indices(g["validate_slot_indices_ok"])
+    bad = g["validate_slot_indices_bad"]
+    with pytest.raises(kv.KvError) as ei:
+        lay.validate_slot_indices(bad["slots"])
+    assert ei.value.variant == bad["variant"] and list(ei.value.fields) == bad["fields"]
+    with pytest.raises(kv.KvError) as ei:
+        lay.validate_slot_indices([])
+    assert ei.value.variant == "EmptySlotMap"
+
+
+def test_paged_layout_runtime_errors(goldens):
+    g = goldens["kv_cache_layout"]
+    for e in g["runtime_errors"]:
+        with pytest.raises(kv.KvError) as ei:
+            kv.PagedKvCacheLayout.new(_runtime(g["runtime"], **e["patch"]), e["page_count"])
+        assert ei.value.variant == e["variant"] and list(ei.value.fields[:2]) == e["fields"], e
+    with pytest.raises(kv.KvError) as ei:
+        kv.PagedKvCacheLayout.new(_runtime(g["runtime"]), 0)
+    assert ei.value.variant == "ZeroPageCount"
+    with pytest.raises(kv.KvError) as ei:
+        kv.PagedKvCacheLayout.new(_runtime(g["runtime"], head_dim=0), 1)
+    assert ei.value.variant == "ZeroLayoutField" and ei.value.name == "head_dim"
+
+
+def test_tensor_pair_layout_goldens(goldens):
+    g = goldens["asymmetric_pair"]
+    lay = kv.PagedKvCacheLayout.new_with_tensor_pair(_runtime(g["runtime"]), g["page_count"],
+                                                     g["key_token_bytes"], g["value_token_bytes"])
+    assert lay.total_byte_len == g["total_byte_len"]
+    assert lay.bytes_per_token_per_tensor is None and lay.bytes_per_tensor_page is None
+    for r in g["ranges"]:
+        assert lay.tensor_token_byte_range(*r["args"]) == tuple(r["range"]), r
+    with pytest.raises(kv.KvError) as ei:
+        lay.kv_pair_copy_geometry(0)
+    want = g["kv_pair_copy_geometry_layer_0"]
+    assert ei.value.variant == want["variant"] and list(ei.value.fields[:2]) == want["fields"]
+    base = goldens[g["pair_errors"][0]["base"]]["runtime"]
+    for e in g["pair_errors"]:
+        with pytest.raises(kv.KvError) as ei:
+            kv.PagedKvCacheLayout.new_with_tensor_pair(_runtime(base, **e["patch"]), 1, e["key"],
+                                                       e["value"])
+        n = len(e["fields"])
+        assert ei.value.variant == e["variant"] and list(ei.value.fields[:n]) == e["fields"], e
+
+
+def test_cuda_backend_slot_location_golden(goldens):
+    g = goldens["cuda_backend_slot_location"]
+    lay = kv.PagedKvCacheLayout.new(_runtime(g["runtime"]), g["page_count"])
+    s, e = lay.tensor_slot_byte_range(1, 1, 63)
+    want = g["slot_location_layer_1_tensor_1_slot_63"]
+    assert (s, e - s) == (want["byte_offset"], want["byte_len"])
+    assert lay.total_byte_len == g["pool_byte_len"]
+
+
+def test_layout_agrees_with_the_oracle_on_random_shapes():
+    """The product's byte ranges equal the (independently pinned) oracle's."""
+    import oracle
+    rng = np.random.default_rng(0)
+    for _ in range(20):
+        P, L, T = int(rng.choice([1, 4, 16, 64])), int(rng.integers(1, 5)), int(rng.integers(1, 3))
+        H, D, pages = int(rng.integers(1, 5)), int(rng.choice([8, 64, 128])), int(rng.integers(1, 6))
+        bpt = L * T * H * D * 2
+        rt = kv.KvCacheRuntimeLayout("bf16", P, L, H, D, T, bpt, P * bpt)
+        lay = kv.PagedKvCacheLayout.new(rt, pages)
+        olay = oracle.layout(P, L, T, bpt, P * bpt, pages)
+        for _ in range(10):
+            slot, layer, t = int(rng.integers(0, pages * P)), int(rng.integers(0, L)), int(rng.integers(0, T))
+            rc, rngo = oracle.tensor_slot_byte_range(olay, layer, t, slot)
+            assert rc == 0 and lay.tensor_slot_byte_range(layer, t, slot) == rngo
+
+
+def test_pair_copy_plan_goldens(goldens):
+    g = goldens["pair_copy_plan"]
+    lay = kv.KvPairCopyLayout(**g["layout"])
+    plan = kv.KvPairCopyPlan.new(3, 12, lay, 40, 48)
+    want = g["new_3_12_40_48"]
+    assert (plan.key_rows_required_bytes, plan.value_rows_required_bytes,
+            plan.slot_indices_required_bytes, plan.pool_required_bytes) == (
+        want["key_rows_required_bytes"], want["value_rows_required_bytes"],
+        want["slot_indices_required_bytes"], want["pool_required_bytes"])
+    assert plan.layout == lay and plan.row_count == 3 and plan.slot_count == 12
+    umax = 2**64 - 1
+    for e in g["errors"]:
+        args = [umax if a == "usize::MAX" else a for a in e["args"]]
+        lay_args = [umax if a == "usize::MAX" else a for a in args[2]]
+        with pytest.raises(kv.KvError) as ei:
+            kv.KvPairCopyPlan.new(args[0], args[1], kv.KvPairCopyLayout(*lay_args), args[3], args[4])
+        assert ei.value.variant == e["variant"], e
+        if "name" in e:
+            assert ei.value.name == e["name"]
+        n = len(e["fields"])
+        assert list(ei.value.fields[:n]) == e["fields"], e
+
+
+def test_transfer_page_indices(goldens):
+    g = goldens["transfer_plan"]
+    assert kv.transfer_page_indices(0, g["span_token_offset"], [20, 21], 1) == [20, 21]
+    assert kv.transfer_page_indices(0, 0, [8, 9, 10, 11, 4, 5], 4) == [2, 1]
+    assert kv.transfer_page_indices(0, 0, [], 4) == []
+    for args, variant in [((7, 2, [8, 9], 4), "UnalignedTokenOffset"),
+                          ((7, 0, [9, 10], 4), "UnalignedCacheSlot"),
+                          ((7, 0, [8, 10], 4), "NonContiguousCacheSlots"),
+                          ((7, 0, [8], 0), "ZeroPageSize")]:
+        with pytest.raises(kv.KvError) as ei:
+            kv.transfer_page_indices(*args)
+        assert ei.value.variant == variant
+    with pytest.raises(kv.KvError) as ei:
+        kv.transfer_page_indices(7, 0, [8, 10], 4)
+    assert ei.value.fields == (7, 9, 10)
+
+
+def test_transfer_page_indices_agrees_with_oracle():
+    import oracle
+    rng = np.random.default_rng(1)
+    for _ in range(50):
+        P = int(rng.choice([1, 2, 4, 16]))
+        pages = rng.permutation(40)[: int(rng.integers(0, 6))]
+        slots = np.concatenate([p * P + np.arange(P) for p in pages]).astype(np.uint64) if len(pages) else np.zeros(0, np.uint64)
+        if len(slots) and rng.random() < 0.3:
+            slots = slots[: int(rng.integers(1, len(slots) + 1))]
+        if len(slots) and rng.random() < 0.3:
+            slots[int(rng.integers(0, len(slots)))] += 1
+        rc, want = oracle.transfer_page_indices(0, slots, P)
+        if rc == 0:
+            assert kv.transfer_page_indices(0, 0, slots, P) == want
+        else:
+            with pytest.raises(kv.KvError) as ei:
+                kv.transfer_page_indices(0, 0, slots, P)
+            assert ei.value.code == rc
+
+
+def test_pool_view_for_layer():
+    rt = kv.KvCacheRuntimeLayout.for_model("bf16", 64, 32, 8, 128)
+    lay = kv.PagedKvCacheLayout.new(rt, 4)
+    v = lay.pool_view(0x1000, lay.total_byte_len, 3, kv.HND, 8)
+    assert v.page_size == 64 and v.page_stride_bytes == 64 * 32 * 2 * 2048
+    assert list(v.tensor_offset) == [3 * 64 * 2 * 2048, 3 * 64 * 2 * 2048 + 64 * 2048]
+    assert v.row_bytes == 2048 and v.tensor_count == 2 and v.heads == 8 and v.head_layout == kv.HND
+    with pytest.raises(kv.KvError) as ei:
+        lay.pool_view(0x1000, lay.total_byte_len, 32)
+    assert ei.value.variant == "LayerOutOfRange"
+    with pytest.raises(kv.KvError) as ei:
+        lay.pool_view(0x1000, lay.total_byte_len, 0, kv.HND, 3)
+    assert ei.value.variant == "InvalidArgument" and ei.value.name == "heads"
+    mla = kv.PagedKvCacheLayout.new(kv.KvCacheRuntimeLayout.for_model("bf16", 64, 61, 1, 576, 1), 2)
+    mv = mla.pool_view(0x1000, mla.total_byte_len, 60)
+    assert mv.tensor_count == 1 and mv.row_bytes == 1152 and mv.tensor_offset[0] == 60 * 64 * 1152
+
+
+def test_device_calls_fail_loudly_without_a_gpu():
+    """On a host with no GPU the context cannot be created, and the error is
+    a typed failure, not a silent fallback."""
+    from sgl_rocm_kv import hip
+    if hip.device_count() > 0:
+        pytest.skip("a GPU is visible")
+    with pytest.raises(kv.KvError) as ei:
+        kv.RocmKvPairCopyKernels(0)
+    assert ei.value.variant in ("Hip", "InvalidArgument")
+
+
+def test_synthetic_words_is_splitmix64():
+    """The host copy of the fill stream against splitmix64's published
+    first outputs for seed 0 (Vigna's reference implementation: state += the
+    golden gamma, then the two xor-shift-multiply rounds)."""
+    got = kv.synthetic_words(0, np.arange(3))
+    assert [hex(int(x)) for x in got] == ["0xe220a8397b1dcdaf", "0x6e789e6aa1b965f4",
+                                          "0x6c45d188009454f"]

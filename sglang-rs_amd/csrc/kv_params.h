@@ -32,11 +32,18 @@
 #define SGLKV_SIDE_ROWS 0u
 #define SGLKV_SIDE_POOL 1u
 
-/* Threads per workgroup and the largest row tile one workgroup stages. */
+/* Threads per workgroup. */
 #define SGLKV_BLOCK_THREADS 256u
+/* Largest row tile one workgroup stages, and the rows each thread keeps in
+ * flight (loads issued before the stores). The code object exports the
+ * values it was built with (sglkv_max_tile_rows, sglkv_rows_per_thread);
+ * the launcher reads them at load time and sizes its tiles from them. */
+#ifndef SGLKV_MAX_TILE_ROWS
 #define SGLKV_MAX_TILE_ROWS 512u
-/* Rows each thread keeps in flight (loads issued before the stores). */
+#endif
+#ifndef SGLKV_ROWS_PER_THREAD
 #define SGLKV_ROWS_PER_THREAD 8u
+#endif
 
 /* Bits of the device error word. */
 #define SGLKV_FLAG_SLOT 1u /* a slot map entry >= slot_count (reference flag value) */
@@ -68,7 +75,7 @@ typedef struct sglkv_copy_params {
     uint32_t vpr;           /* vectors per row, all tensors */
     uint32_t vpt;           /* vectors per tensor row */
     uint32_t vpc;           /* vectors per head chunk */
-    uint32_t tile_rows;     /* rows per workgroup = blockDim.y * SGLKV_ROWS_PER_THREAD */
+    uint32_t tile_rows;     /* rows per workgroup = blockDim.y * rows per thread */
 } sglkv_copy_params;
 
 /* One request's run of rows (KvCacheTransferSpan,

@@ -214,6 +214,8 @@ struct sgl_rocm_kv_ctx {
     hipFunction_t resolve;
     hipFunction_t fill;
     uint32_t *flag;
+    uint32_t rows_per_thread;  // from the code object
+    uint32_t max_tile_rows;
 };
 
 namespace {
@@ -245,8 +247,8 @@ int32_t launch_copy(sgl_rocm_kv_ctx *ctx, int kind, sglkv_copy_params &p, const 
     p.vpc = (uint32_t)(chunk / vb);
     const uint32_t bx = p.vpr < SGLKV_BLOCK_THREADS ? p.vpr : SGLKV_BLOCK_THREADS;
     uint32_t by = SGLKV_BLOCK_THREADS / bx;
-    if (by > SGLKV_MAX_TILE_ROWS / SGLKV_ROWS_PER_THREAD) by = SGLKV_MAX_TILE_ROWS / SGLKV_ROWS_PER_THREAD;
-    p.tile_rows = by * SGLKV_ROWS_PER_THREAD;
+    if (by > ctx->max_tile_rows / ctx->rows_per_thread) by = ctx->max_tile_rows / ctx->rows_per_thread;
+    p.tile_rows = by * ctx->rows_per_thread;
     const uint64_t grid = (rows + p.tile_rows - 1) / p.tile_rows;
     if (grid > INT32_MAX) return too_large("grid blocks", grid, INT32_MAX);
     void *args[] = {&p};
@@ -407,6 +409,18 @@ extern "C" int32_t sgl_rocm_kv_init(int32_t device, const char *code_object_path
     err = hipModuleGetFunction(&ctx->resolve, ctx->module, "sglkv_resolve_spans");
     if (err == hipSuccess) err = hipModuleGetFunction(&ctx->fill, ctx->module, "sglkv_fill_synthetic");
     if (err == hipSuccess) err = hipDeviceGetAttribute(&ctx->cu_count, hipDeviceAttributeMultiprocessorCount, device);
+    // The tile constants the kernels were compiled with.
+    const char *const constants[2] = {"sglkv_rows_per_thread", "sglkv_max_tile_rows"};
+    uint32_t *const values[2] = {&ctx->rows_per_thread, &ctx->max_tile_rows};
+    for (int i = 0; i < 2 && err == hipSuccess; ++i) {
+        hipDeviceptr_t addr = nullptr;
+        size_t bytes = 0;
+        err = hipModuleGetGlobal(&addr, &bytes, ctx->module, constants[i]);
+        if (err == hipSuccess && bytes != sizeof(uint32_t)) err = hipErrorInvalidSymbol;
+        if (err == hipSuccess) err = hipMemcpyDtoH(values[i], addr, sizeof(uint32_t));
+    }
+    if (err == hipSuccess && (ctx->rows_per_thread == 0 || ctx->rows_per_thread > ctx->max_tile_rows))
+        err = hipErrorInvalidImage;
     if (err == hipSuccess) err = hipMalloc(reinterpret_cast<void **>(&ctx->flag), sizeof(uint32_t));
     if (err == hipSuccess) err = hipMemset(ctx->flag, 0, sizeof(uint32_t));
     if (err != hipSuccess) {

@@ -339,6 +339,24 @@ int32_t sgl_rocm_kv_pack_layer(sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src
 int32_t sgl_rocm_kv_unpack_layer(sgl_rocm_kv_ctx *ctx, const sgl_kv_rows_view *src,
                                  uint64_t row_count, const sgl_kv_pool_view *dst,
                                  const sgl_kv_device_buffer *slots, void *stream);
+/* Multi-layer forms: one launch covers `layer_count` consecutive layers
+ * (no counterpart in the reference, which launches per layer). Layer i's
+ * pool view is `src`/`dst` with every tensor_offset advanced by
+ * i * pool_layer_stride (PagedKvCacheLayout::bytes_per_layer_page for a
+ * paged pool); layer i's rows sit i * rows_layer_stride bytes after the
+ * given planes. Scales, when given, are layer_count consecutive groups of
+ * tensor_count floats. The first and last layers are validated like a
+ * single-layer call, and the destination's layers must not overlap. */
+int32_t sgl_rocm_kv_pack_layers(sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src,
+                                uint64_t pool_layer_stride, uint32_t layer_count,
+                                const sgl_kv_device_buffer *slots, uint64_t row_count,
+                                const sgl_kv_rows_view *dst, uint64_t rows_layer_stride,
+                                void *stream);
+int32_t sgl_rocm_kv_unpack_layers(sgl_rocm_kv_ctx *ctx, const sgl_kv_rows_view *src,
+                                  uint64_t rows_layer_stride, uint32_t layer_count,
+                                  uint64_t row_count, const sgl_kv_pool_view *dst,
+                                  uint64_t pool_layer_stride, const sgl_kv_device_buffer *slots,
+                                  void *stream);
 /* Pool -> pool in one pass for co-resident prefill and decode pools:
  * the composition unpack(pack(.)) without the transfer rows. */
 int32_t sgl_rocm_kv_transfer_layer(sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src,
@@ -370,6 +388,56 @@ int32_t sgl_rocm_kv_resolve_spans(sgl_rocm_kv_ctx *ctx, uint64_t page_size, uint
                                   const sgl_kv_device_buffer *page_table, uint64_t page_table_len,
                                   uint64_t row_count, const sgl_kv_device_buffer *out_slots,
                                   void *stream);
+
+/* --- layer pipeline (pack -> hop -> unpack, overlapped across layers) ---- */
+
+/* A whole-request transfer, layer by layer: the device-side half of a PD
+ * transfer backend (KvTransferBackend::submit, transfer.rs:1145-1151, driven
+ * by execute_kv_cache_transfer_plan, transfer.rs:1205-1231). For each layer l:
+ *   pack(src_layers[l]) -> send[l % 2]
+ *   [staged]  D2H send -> host[l % 2] (pinned), then H2D host -> recv[l % 2]
+ *   unpack(recv[l % 2], or send[l % 2] when not staged) -> dst_layers[l]
+ * on four streams (pack, D2H, H2D, unpack) so that layer l + 1 packs while
+ * layer l crosses the hop and layer l - 1 unpacks. The staged hop stands in
+ * for the inter-node link on one GPU. Buffers are double-buffered; events
+ * order every reuse. Each send/recv/host buffer holds one layer's rows as
+ * [tensor][row][row_bytes] (tensor_count * row_count * row_bytes bytes).
+ * All buffers are the caller's; host buffers must be pinned (hipHostMalloc)
+ * for the copies to be asynchronous. */
+typedef struct sgl_kv_pipeline_desc {
+    uint32_t layers;
+    uint32_t staged;                       /* 1: host hop; 0: unpack reads send[] directly */
+    const sgl_kv_pool_view *src_layers;    /* host array of `layers` views (copied) */
+    const sgl_kv_pool_view *dst_layers;    /* host array of `layers` views (copied) */
+    sgl_kv_device_buffer src_slots;        /* u64 slot per row, source pool */
+    sgl_kv_device_buffer dst_slots;        /* u64 slot per row, destination pool */
+    uint64_t row_count;
+    sgl_kv_device_buffer send[2];          /* device */
+    sgl_kv_device_buffer recv[2];          /* device; unused when not staged */
+    void *host[2];                         /* pinned host; unused when not staged */
+    uint64_t host_bytes;                   /* bytes available at each host[i] */
+} sgl_kv_pipeline_desc;
+
+typedef struct sgl_rocm_kv_pipeline sgl_rocm_kv_pipeline;
+
+/* Validates the description (every layer view against row_count and the
+ * staging sizes), creates the four streams (default priority) and the
+ * per-layer events. */
+int32_t sgl_rocm_kv_pipeline_create(sgl_rocm_kv_ctx *ctx, const sgl_kv_pipeline_desc *desc,
+                                    sgl_rocm_kv_pipeline **out);
+/* Enqueues every layer and returns; `after` (a hipEvent_t or NULL) gates the
+ * first pack. */
+int32_t sgl_rocm_kv_pipeline_run(sgl_rocm_kv_pipeline *pipe, void *after);
+/* Waits for the last unpack and reports device errors (check_errors). */
+int32_t sgl_rocm_kv_pipeline_wait(sgl_rocm_kv_pipeline *pipe);
+/* Durations in ms of layer `layer`'s last run: ms[0] pack, ms[1] D2H,
+ * ms[2] H2D, ms[3] unpack (hop entries 0 when not staged), and ms[4] the
+ * layer's latency from pack start to unpack end. */
+int32_t sgl_rocm_kv_pipeline_layer_times(const sgl_rocm_kv_pipeline *pipe, uint32_t layer,
+                                         float *ms);
+/* Elapsed ms from the first pack start to the last unpack end of the last run. */
+int32_t sgl_rocm_kv_pipeline_elapsed(const sgl_rocm_kv_pipeline *pipe, float *ms);
+int32_t sgl_rocm_kv_pipeline_destroy(sgl_rocm_kv_pipeline *pipe);
 
 /* Synthetic-input generator for benchmarks and tests; it has no counterpart
  * in the reference. Fills `buffer` (byte_len a multiple of 8) word by word:

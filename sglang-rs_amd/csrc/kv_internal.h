@@ -2,7 +2,10 @@
 #ifndef SGLKV_INTERNAL_H
 #define SGLKV_INTERNAL_H
 
+#include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "kv_params.h"
 
 // The C ABI is the library's only exported surface (built with
 // -fvisibility=hidden); the declarations carry default visibility.
@@ -18,8 +21,81 @@ int32_t fail(int32_t code, const char *name, uint64_t a, uint64_t b, uint64_t c,
 // Clears the detail record and returns SGL_KV_OK.
 int32_t ok();
 
+// Geometry common to both sides of a copy.
+struct RowShape {
+    uint64_t row_bytes;
+    uint32_t tensors;
+    uint32_t heads;  // > 1 only when a side is head-major
+    bool split;      // some side is HND: copy head chunk by head chunk
+};
+
+// A validated copy launch: kernel parameters plus launch geometry.
+struct Launch {
+    sglkv_copy_params params;
+    RowShape shape;
+    int kind;         // 0 pool->rows, 1 rows->pool, 2 pool->pool
+    int width_index;  // vector width 16, 8, 4, 2, 1
+    uint64_t rows;
+    uint64_t grid;
+    uint32_t layers;  // grid y: one layer per row of workgroups
+    uint32_t block_x, block_y;
+};
+
+// Layer span of a multi-layer launch: `count` layers, each side's data
+// `pool_stride` / `rows_stride` bytes after the previous layer's.
+struct LayerSpan {
+    uint32_t count;
+    uint64_t pool_stride;
+    uint64_t rows_stride;
+};
+
+int32_t prepare_pack(const sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src,
+                     const sgl_kv_device_buffer *slots, uint64_t row_count,
+                     const sgl_kv_rows_view *dst, Launch *l, LayerSpan span = {1, 0, 0});
+int32_t prepare_unpack(const sgl_rocm_kv_ctx *ctx, const sgl_kv_rows_view *src, uint64_t row_count,
+                       const sgl_kv_pool_view *dst, const sgl_kv_device_buffer *slots, Launch *l,
+                       LayerSpan span = {1, 0, 0});
+int32_t submit_launch(sgl_rocm_kv_ctx *ctx, Launch &l, hipStream_t stream);
+int32_t hip_fail(hipError_t err, const char *call);
+
 inline bool mul_ovf(uint64_t a, uint64_t b, uint64_t *out) { return __builtin_mul_overflow(a, b, out); }
 inline bool add_ovf(uint64_t a, uint64_t b, uint64_t *out) { return __builtin_add_overflow(a, b, out); }
+
+}  // namespace sglkv
+
+// The per-device context (opaque in the C ABI).
+struct sgl_rocm_kv_ctx {
+    int device;
+    int cu_count;
+    hipModule_t module;
+    hipFunction_t copy[5][3];
+    hipFunction_t resolve;
+    hipFunction_t fill;
+    uint32_t *flag;
+    uint32_t rows_per_thread;  // from the code object
+    uint32_t max_tile_rows;
+};
+
+namespace sglkv {
+
+// Makes the context's device current for one call and restores the
+// caller's device afterwards (the reference pushes and pops its CUDA
+// context around every call, crates/sglang-kernel/src/cuda.rs:559-586).
+class DeviceScope {
+  public:
+    explicit DeviceScope(int device) : prev_(-1), device_(device), err_(hipSuccess) {
+        err_ = hipGetDevice(&prev_);
+        if (err_ == hipSuccess && prev_ != device) err_ = hipSetDevice(device);
+    }
+    ~DeviceScope() {
+        if (prev_ >= 0 && prev_ != device_) (void)hipSetDevice(prev_);
+    }
+    hipError_t status() const { return err_; }
+
+  private:
+    int prev_, device_;
+    hipError_t err_;
+};
 
 }  // namespace sglkv
 

@@ -150,9 +150,10 @@ __device__ __forceinline__ void sglkv_copy_rows(const sglkv_copy_params &p) {
     }
     const bool clean = !__syncthreads_or(bad);
     // Per-layer quantisation scales ride along bit-exactly.
+    const uint32_t layer = blockIdx.y;
     if (blockIdx.x == 0 && tid < p.scale_count) {
-        reinterpret_cast<uint32_t *>(p.scale_dst)[tid] =
-            reinterpret_cast<const uint32_t *>(p.scale_src)[tid];
+        const uint32_t i = layer * p.scale_count + tid;
+        reinterpret_cast<uint32_t *>(p.scale_dst)[i] = reinterpret_cast<const uint32_t *>(p.scale_src)[i];
     }
 
     for (uint32_t j = threadIdx.x; j < p.vpr; j += blockDim.x) {
@@ -162,8 +163,10 @@ __device__ __forceinline__ void sglkv_copy_rows(const sglkv_copy_params &p) {
         const uint32_t jc = jt - h * p.vpc;
         // Select rather than index the kernel-argument arrays: a dynamic
         // index would copy the struct to scratch.
-        const uint64_t src_plane = t ? p.src.plane[1] : p.src.plane[0];
-        const uint64_t dst_plane = t ? p.dst.plane[1] : p.dst.plane[0];
+        const uint64_t src_plane =
+            (t ? p.src.plane[1] : p.src.plane[0]) + static_cast<uint64_t>(layer) * p.src.layer_stride;
+        const uint64_t dst_plane =
+            (t ? p.dst.plane[1] : p.dst.plane[0]) + static_cast<uint64_t>(layer) * p.dst.layer_stride;
         const uint64_t src_stride = t ? p.src.stride[1] : p.src.stride[0];
         const uint64_t dst_stride = t ? p.dst.stride[1] : p.dst.stride[0];
         sglkv_gsrc *sb = reinterpret_cast<sglkv_gsrc *>(src_plane +

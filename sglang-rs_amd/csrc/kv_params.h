@@ -20,6 +20,10 @@
  *        pages put each head's page_size chunks together (head_stride =
  *        page_size * chunk bytes, pos_mult = chunk bytes).
  *
+ * A launch covers one layer per gridDim.y: layer y's planes sit
+ * y * layer_stride bytes after layer 0's on each side (row offsets do not
+ * depend on the layer).
+ *
  * Vectors: the host picks the widest access width VB in {16, 8, 4, 2, 1}
  * that divides every base, stride and chunk size, so every access is
  * naturally aligned. Sizes below are in units of VB.
@@ -60,6 +64,7 @@ typedef struct sglkv_side {
     uint64_t pos_mult;      /* POOL: bytes between adjacent in-page positions */
     uint64_t head_stride;   /* bytes between head chunks of one row */
     uint64_t slot_count;    /* POOL: valid slots are [0, slot_count) */
+    uint64_t layer_stride;  /* bytes between consecutive layers' data (blockIdx.y = layer) */
     uint32_t page_size;     /* POOL: tokens per page */
     uint32_t reserved;
 } sglkv_side;
@@ -68,9 +73,9 @@ typedef struct sglkv_copy_params {
     sglkv_side src;
     sglkv_side dst;
     uint32_t *flag;         /* device error word (OR of SGLKV_FLAG_*) */
-    float *scale_src;       /* optional per-layer scales copied bit-exactly */
-    float *scale_dst;
-    uint32_t scale_count;   /* number of floats to copy (0: none) */
+    float *scale_src;       /* optional per-layer scales copied bit-exactly; layer y's */
+    float *scale_dst;       /* scale_count floats follow layer y - 1's */
+    uint32_t scale_count;   /* floats to copy per layer (0: none) */
     uint32_t rows;          /* rows in this launch */
     uint32_t vpr;           /* vectors per row, all tensors */
     uint32_t vpt;           /* vectors per tensor row */

@@ -25,36 +25,20 @@ constexpr int kWidths[5] = {16, 8, 4, 2, 1};
 constexpr int kPoolRows = 0, kRowsPool = 1, kPoolPool = 2;
 const char *const kKindNames[3] = {"pool_rows", "rows_pool", "pool_pool"};
 
-int32_t hip_fail(hipError_t err, const char *call) {
+}  // namespace
+
+int32_t sglkv::hip_fail(hipError_t err, const char *call) {
     return fail(SGL_KV_HIP, call, (uint64_t)err, 0, 0, "%s failed: %s (%d)", call,
                 hipGetErrorString(err), (int)err);
 }
+
+namespace {
 
 #define SGLKV_HIP(call)                                     \
     do {                                                    \
         hipError_t e_ = (call);                             \
         if (e_ != hipSuccess) return hip_fail(e_, #call);   \
     } while (0)
-
-// Makes the context's device current for one call and restores the
-// caller's device afterwards (the reference pushes and pops its CUDA
-// context around every call, crates/sglang-kernel/src/cuda.rs:559-586).
-class DeviceScope {
-  public:
-    explicit DeviceScope(int device) : prev_(-1), err_(hipSuccess) {
-        err_ = hipGetDevice(&prev_);
-        if (err_ == hipSuccess && prev_ != device) err_ = hipSetDevice(device);
-        device_ = device;
-    }
-    ~DeviceScope() {
-        if (prev_ >= 0 && prev_ != device_) (void)hipSetDevice(prev_);
-    }
-    hipError_t status() const { return err_; }
-
-  private:
-    int prev_, device_;
-    hipError_t err_;
-};
 
 int32_t out_of_bounds(const char *name, uint64_t offset, uint64_t len, uint64_t have) {
     return fail(SGL_KV_ALLOCATION_OUT_OF_BOUNDS, name, offset, len, have,
@@ -71,14 +55,6 @@ int32_t too_large(const char *name, uint64_t value, uint64_t maximum) {
 int32_t shape_overflow() {
     return fail(SGL_KV_SHAPE_OVERFLOW, nullptr, 0, 0, 0, "KV copy tensor shape overflowed");
 }
-
-// Geometry common to both sides of a copy.
-struct RowShape {
-    uint64_t row_bytes;
-    uint32_t tensors;
-    uint32_t heads;  // > 1 only when a side is head-major
-    bool split;      // some side is HND: copy head chunk by head chunk
-};
 
 // Validates one pool side and fills its kernel description.
 int32_t pool_side(const sgl_kv_pool_view *v, const sgl_kv_device_buffer *slots, uint64_t rows,
@@ -206,18 +182,6 @@ int vector_bytes(const sglkv_side &s, const sglkv_side &d, uint64_t chunk) {
 
 }  // namespace
 
-struct sgl_rocm_kv_ctx {
-    int device;
-    int cu_count;
-    hipModule_t module;
-    hipFunction_t copy[5][3];
-    hipFunction_t resolve;
-    hipFunction_t fill;
-    uint32_t *flag;
-    uint32_t rows_per_thread;  // from the code object
-    uint32_t max_tile_rows;
-};
-
 namespace {
 
 std::string default_code_object() {
@@ -231,29 +195,31 @@ std::string default_code_object() {
     return "sgl_rocm_kv_gfx950.co";
 }
 
-int32_t launch_copy(sgl_rocm_kv_ctx *ctx, int kind, sglkv_copy_params &p, const RowShape &shape,
-                    uint64_t rows, hipStream_t stream) {
-    if (rows > UINT32_MAX) return too_large("row_count", rows, UINT32_MAX);
+// Fills the launch geometry of a validated copy (vector width, tile) from
+// the context's code-object constants.
+int32_t finish_launch(const sgl_rocm_kv_ctx *ctx, Launch *l) {
+    sglkv_copy_params &p = l->params;
+    const RowShape &shape = l->shape;
+    if (l->rows > UINT32_MAX) return too_large("row_count", l->rows, UINT32_MAX);
     const uint64_t chunk = shape.split ? shape.row_bytes / shape.heads : shape.row_bytes;
     const int vb = vector_bytes(p.src, p.dst, chunk);
     uint64_t row_vectors = shape.row_bytes / vb * shape.tensors;
     if (row_vectors > (1ull << 31)) return too_large("row_bytes", shape.row_bytes, 1ull << 30);
     int wi = 0;
     while (kWidths[wi] != vb) ++wi;
+    l->width_index = wi;
     p.flag = ctx->flag;
-    p.rows = (uint32_t)rows;
+    p.rows = (uint32_t)l->rows;
     p.vpr = (uint32_t)row_vectors;
     p.vpt = (uint32_t)(shape.row_bytes / vb);
     p.vpc = (uint32_t)(chunk / vb);
-    const uint32_t bx = p.vpr < SGLKV_BLOCK_THREADS ? p.vpr : SGLKV_BLOCK_THREADS;
-    uint32_t by = SGLKV_BLOCK_THREADS / bx;
+    l->block_x = p.vpr < SGLKV_BLOCK_THREADS ? p.vpr : SGLKV_BLOCK_THREADS;
+    uint32_t by = SGLKV_BLOCK_THREADS / l->block_x;
     if (by > ctx->max_tile_rows / ctx->rows_per_thread) by = ctx->max_tile_rows / ctx->rows_per_thread;
+    l->block_y = by;
     p.tile_rows = by * ctx->rows_per_thread;
-    const uint64_t grid = (rows + p.tile_rows - 1) / p.tile_rows;
-    if (grid > INT32_MAX) return too_large("grid blocks", grid, INT32_MAX);
-    void *args[] = {&p};
-    SGLKV_HIP(hipModuleLaunchKernel(ctx->copy[wi][kind], (unsigned)grid, 1, 1, bx, by, 1, 0, stream,
-                                    args, nullptr));
+    l->grid = (l->rows + p.tile_rows - 1) / p.tile_rows;
+    if (l->grid > INT32_MAX) return too_large("grid blocks", l->grid, INT32_MAX);
     return SGL_KV_OK;
 }
 
@@ -265,7 +231,7 @@ void attach_scales(sglkv_copy_params &p, float *src, float *dst, uint32_t tensor
     }
 }
 
-int32_t check_ctx(sgl_rocm_kv_ctx *ctx) {
+int32_t check_ctx(const sgl_rocm_kv_ctx *ctx) {
     if (!ctx) return fail(SGL_KV_INVALID_ARGUMENT, "ctx", 0, 0, 0, "null context");
     return SGL_KV_OK;
 }
@@ -339,9 +305,12 @@ int32_t pair_copy(sgl_rocm_kv_ctx *ctx, const sgl_kv_pair_copy_plan *plan,
     if (plan->layout.page_size > UINT32_MAX)
         return too_large("page_size", plan->layout.page_size, UINT32_MAX);
 
-    RowShape shape{plan->layout.row_bytes, 2, 1, false};
-    sglkv_copy_params p;
-    memset(&p, 0, sizeof p);
+    Launch l;
+    memset(&l, 0, sizeof l);
+    l.shape = RowShape{plan->layout.row_bytes, 2, 1, false};
+    l.kind = scatter ? kRowsPool : kPoolRows;
+    l.rows = plan->row_count;
+    sglkv_copy_params &p = l.params;
     sglkv_side &ps = scatter ? p.dst : p.src;
     sglkv_side &rs = scatter ? p.src : p.dst;
     ps.plane[0] = pool + plan->layout.key_in_page_offset;
@@ -357,10 +326,10 @@ int32_t pair_copy(sgl_rocm_kv_ctx *ctx, const sgl_kv_pair_copy_plan *plan,
     rs.stride[0] = plan->key_row_stride_bytes;
     rs.stride[1] = plan->value_row_stride_bytes;
     rs.head_stride = plan->layout.row_bytes;
+    if ((rc = finish_launch(ctx, &l))) return rc;
 
     SGLKV_HIP(hipMemsetAsync(ctx->flag, 0, sizeof(uint32_t), stream));
-    rc = launch_copy(ctx, scatter ? kRowsPool : kPoolRows, p, shape, plan->row_count, stream);
-    if (rc) return rc;
+    if ((rc = submit_launch(ctx, l, stream))) return rc;
     SGLKV_HIP(hipStreamSynchronize(stream));
     uint32_t flag = 0;
     SGLKV_HIP(hipMemcpy(&flag, ctx->flag, sizeof flag, hipMemcpyDeviceToHost));
@@ -458,49 +427,178 @@ extern "C" int32_t sgl_rocm_kv_pair_gather(sgl_rocm_kv_ctx *ctx, const sgl_kv_pa
     return pair_copy(ctx, plan, buffers, static_cast<hipStream_t>(stream), false);
 }
 
-extern "C" int32_t sgl_rocm_kv_pack_layer(sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src,
-                                          const sgl_kv_device_buffer *slots, uint64_t row_count,
-                                          const sgl_kv_rows_view *dst, void *stream) {
+namespace sglkv {
+
+// Validates the last layer of a multi-layer launch (the first is validated
+// by the caller) and that the destination's layers do not overlap.
+int32_t check_layer_span(const sgl_kv_pool_view *pool, bool pool_is_dst,
+                         const sgl_kv_rows_view *rows, const LayerSpan &span, uint64_t row_count,
+                         const RowShape &shape, const sgl_kv_device_buffer *slots) {
+    if (span.count == 0 || span.count > 65535)
+        return fail(SGL_KV_INVALID_ARGUMENT, "layer_count", span.count, 65535, 0,
+                    "a launch covers 1 to 65535 layers, not %u", span.count);
+    if (span.count == 1) return SGL_KV_OK;
+    const uint64_t n = span.count - 1;
+    uint64_t pool_shift, rows_shift;
+    if (mul_ovf(n, span.pool_stride, &pool_shift) || mul_ovf(n, span.rows_stride, &rows_shift))
+        return shape_overflow();
+    // The last layer, as a view of its own.
+    sgl_kv_pool_view last_pool = *pool;
+    for (uint32_t t = 0; t < pool->tensor_count; ++t)
+        if (add_ovf(last_pool.tensor_offset[t], pool_shift, &last_pool.tensor_offset[t]))
+            return shape_overflow();
+    sgl_kv_rows_view last_rows = *rows;
+    const char *names[2] = {shape.tensors == 2 ? "keys" : "rows", "values"};
+    for (uint32_t t = 0; t < shape.tensors; ++t) {
+        if (rows->plane_bytes[t] < rows_shift)
+            return out_of_bounds(names[t], rows_shift, 0, rows->plane_bytes[t]);
+        last_rows.planes[t] = static_cast<char *>(rows->planes[t]) + rows_shift;
+        last_rows.plane_bytes[t] = rows->plane_bytes[t] - rows_shift;
+    }
+    sglkv_side scratch;
+    int32_t rc;
+    if ((rc = pool_side(&last_pool, slots, row_count, shape, &scratch)) ||
+        (rc = rows_side(&last_rows, row_count, shape, names, &scratch)))
+        return rc;
+    // Layers written by the launch must not overlap one another.
+    uint64_t lo = UINT64_MAX, hi = 0;
+    if (pool_is_dst) {
+        for (uint32_t t = 0; t < pool->tensor_count; ++t) {
+            lo = pool->tensor_offset[t] < lo ? pool->tensor_offset[t] : lo;
+            const uint64_t end = pool->tensor_offset[t] + pool->page_size * pool->row_bytes;
+            hi = end > hi ? end : hi;
+        }
+        if (span.pool_stride < hi - lo)
+            return fail(SGL_KV_INVALID_ARGUMENT, "pool_layer_stride", span.pool_stride, hi - lo, 0,
+                        "destination layers %llu bytes apart overlap their %llu-byte regions",
+                        (unsigned long long)span.pool_stride, (unsigned long long)(hi - lo));
+    } else {
+        for (uint32_t t = 0; t < shape.tensors; ++t) {
+            const uint64_t b = (uint64_t)(uintptr_t)rows->planes[t];
+            const uint64_t end = b + (row_count - 1) * rows->row_stride[t] + shape.row_bytes;
+            lo = b < lo ? b : lo;
+            hi = end > hi ? end : hi;
+        }
+        if (span.rows_stride < hi - lo)
+            return fail(SGL_KV_INVALID_ARGUMENT, "rows_layer_stride", span.rows_stride, hi - lo, 0,
+                        "destination layers %llu bytes apart overlap their %llu-byte rows",
+                        (unsigned long long)span.rows_stride, (unsigned long long)(hi - lo));
+    }
+    return SGL_KV_OK;
+}
+
+int32_t prepare_pack(const sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src,
+                     const sgl_kv_device_buffer *slots, uint64_t row_count,
+                     const sgl_kv_rows_view *dst, Launch *l, LayerSpan span) {
     int32_t rc = check_ctx(ctx);
     if (!rc) rc = check_pool_shape(src);
     if (rc) return rc;
     if (!dst) return fail(SGL_KV_INVALID_ARGUMENT, "rows", 0, 0, 0, "null rows view");
-    if (row_count == 0) return ok();
+    memset(l, 0, sizeof *l);
+    l->kind = kPoolRows;
+    l->rows = row_count;
+    l->layers = span.count;
+    if (row_count == 0) return SGL_KV_OK;
     const bool split = src->head_layout == SGL_KV_HND;
-    RowShape shape{src->row_bytes, src->tensor_count, split ? src->heads : 1u, split};
-    sglkv_copy_params p;
-    memset(&p, 0, sizeof p);
+    l->shape = RowShape{src->row_bytes, src->tensor_count, split ? src->heads : 1u, split};
     const char *names[2] = {src->tensor_count == 2 ? "keys" : "rows", "values"};
-    if ((rc = pool_side(src, slots, row_count, shape, &p.src)) ||
-        (rc = rows_side(dst, row_count, shape, names, &p.dst)))
+    if ((rc = pool_side(src, slots, row_count, l->shape, &l->params.src)) ||
+        (rc = rows_side(dst, row_count, l->shape, names, &l->params.dst)) ||
+        (rc = check_layer_span(src, false, dst, span, row_count, l->shape, slots)))
         return rc;
-    attach_scales(p, src->scale, dst->scale, src->tensor_count);
+    l->params.src.layer_stride = span.pool_stride;
+    l->params.dst.layer_stride = span.rows_stride;
+    attach_scales(l->params, src->scale, dst->scale, src->tensor_count);
+    return finish_launch(ctx, l);
+}
+
+int32_t prepare_unpack(const sgl_rocm_kv_ctx *ctx, const sgl_kv_rows_view *src, uint64_t row_count,
+                       const sgl_kv_pool_view *dst, const sgl_kv_device_buffer *slots, Launch *l,
+                       LayerSpan span) {
+    int32_t rc = check_ctx(ctx);
+    if (!rc) rc = check_pool_shape(dst);
+    if (rc) return rc;
+    if (!src) return fail(SGL_KV_INVALID_ARGUMENT, "rows", 0, 0, 0, "null rows view");
+    memset(l, 0, sizeof *l);
+    l->kind = kRowsPool;
+    l->rows = row_count;
+    l->layers = span.count;
+    if (row_count == 0) return SGL_KV_OK;
+    const bool split = dst->head_layout == SGL_KV_HND;
+    l->shape = RowShape{dst->row_bytes, dst->tensor_count, split ? dst->heads : 1u, split};
+    const char *names[2] = {dst->tensor_count == 2 ? "keys" : "rows", "values"};
+    if ((rc = rows_side(src, row_count, l->shape, names, &l->params.src)) ||
+        (rc = pool_side(dst, slots, row_count, l->shape, &l->params.dst)) ||
+        (rc = check_layer_span(dst, true, src, span, row_count, l->shape, slots)))
+        return rc;
+    l->params.src.layer_stride = span.rows_stride;
+    l->params.dst.layer_stride = span.pool_stride;
+    attach_scales(l->params, src->scale, dst->scale, dst->tensor_count);
+    return finish_launch(ctx, l);
+}
+
+int32_t submit_launch(sgl_rocm_kv_ctx *ctx, Launch &l, hipStream_t stream) {
+    if (l.rows == 0) return SGL_KV_OK;
+    void *args[] = {&l.params};
+    SGLKV_HIP(hipModuleLaunchKernel(ctx->copy[l.width_index][l.kind], (unsigned)l.grid,
+                                    l.layers ? l.layers : 1, 1, l.block_x, l.block_y, 1, 0, stream,
+                                    args, nullptr));
+    return SGL_KV_OK;
+}
+
+}  // namespace sglkv
+
+extern "C" int32_t sgl_rocm_kv_pack_layer(sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src,
+                                          const sgl_kv_device_buffer *slots, uint64_t row_count,
+                                          const sgl_kv_rows_view *dst, void *stream) {
+    Launch l;
+    int32_t rc = prepare_pack(ctx, src, slots, row_count, dst, &l);
+    if (rc) return rc;
     DeviceScope scope(ctx->device);
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
-    rc = launch_copy(ctx, kPoolRows, p, shape, row_count, static_cast<hipStream_t>(stream));
+    rc = submit_launch(ctx, l, static_cast<hipStream_t>(stream));
     return rc ? rc : ok();
 }
 
 extern "C" int32_t sgl_rocm_kv_unpack_layer(sgl_rocm_kv_ctx *ctx, const sgl_kv_rows_view *src,
                                             uint64_t row_count, const sgl_kv_pool_view *dst,
                                             const sgl_kv_device_buffer *slots, void *stream) {
-    int32_t rc = check_ctx(ctx);
-    if (!rc) rc = check_pool_shape(dst);
+    Launch l;
+    int32_t rc = prepare_unpack(ctx, src, row_count, dst, slots, &l);
     if (rc) return rc;
-    if (!src) return fail(SGL_KV_INVALID_ARGUMENT, "rows", 0, 0, 0, "null rows view");
-    if (row_count == 0) return ok();
-    const bool split = dst->head_layout == SGL_KV_HND;
-    RowShape shape{dst->row_bytes, dst->tensor_count, split ? dst->heads : 1u, split};
-    sglkv_copy_params p;
-    memset(&p, 0, sizeof p);
-    const char *names[2] = {dst->tensor_count == 2 ? "keys" : "rows", "values"};
-    if ((rc = rows_side(src, row_count, shape, names, &p.src)) ||
-        (rc = pool_side(dst, slots, row_count, shape, &p.dst)))
-        return rc;
-    attach_scales(p, src->scale, dst->scale, dst->tensor_count);
     DeviceScope scope(ctx->device);
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
-    rc = launch_copy(ctx, kRowsPool, p, shape, row_count, static_cast<hipStream_t>(stream));
+    rc = submit_launch(ctx, l, static_cast<hipStream_t>(stream));
+    return rc ? rc : ok();
+}
+
+extern "C" int32_t sgl_rocm_kv_pack_layers(sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src,
+                                           uint64_t pool_layer_stride, uint32_t layer_count,
+                                           const sgl_kv_device_buffer *slots, uint64_t row_count,
+                                           const sgl_kv_rows_view *dst, uint64_t rows_layer_stride,
+                                           void *stream) {
+    Launch l;
+    int32_t rc = prepare_pack(ctx, src, slots, row_count, dst, &l,
+                              LayerSpan{layer_count, pool_layer_stride, rows_layer_stride});
+    if (rc) return rc;
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    rc = submit_launch(ctx, l, static_cast<hipStream_t>(stream));
+    return rc ? rc : ok();
+}
+
+extern "C" int32_t sgl_rocm_kv_unpack_layers(sgl_rocm_kv_ctx *ctx, const sgl_kv_rows_view *src,
+                                             uint64_t rows_layer_stride, uint32_t layer_count,
+                                             uint64_t row_count, const sgl_kv_pool_view *dst,
+                                             uint64_t pool_layer_stride,
+                                             const sgl_kv_device_buffer *slots, void *stream) {
+    Launch l;
+    int32_t rc = prepare_unpack(ctx, src, row_count, dst, slots, &l,
+                                LayerSpan{layer_count, pool_layer_stride, rows_layer_stride});
+    if (rc) return rc;
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    rc = submit_launch(ctx, l, static_cast<hipStream_t>(stream));
     return rc ? rc : ok();
 }
 
@@ -526,16 +624,19 @@ extern "C" int32_t sgl_rocm_kv_transfer_layer(sgl_rocm_kv_ctx *ctx, const sgl_kv
                     "%u heads do not split a %llu-byte row evenly", src->heads,
                     (unsigned long long)src->row_bytes);
     if (row_count == 0) return ok();
-    RowShape shape{src->row_bytes, src->tensor_count, split ? src->heads : 1u, split};
-    sglkv_copy_params p;
-    memset(&p, 0, sizeof p);
-    if ((rc = pool_side(src, src_slots, row_count, shape, &p.src)) ||
-        (rc = pool_side(dst, dst_slots, row_count, shape, &p.dst)))
+    Launch l;
+    memset(&l, 0, sizeof l);
+    l.kind = kPoolPool;
+    l.rows = row_count;
+    l.shape = RowShape{src->row_bytes, src->tensor_count, split ? src->heads : 1u, split};
+    if ((rc = pool_side(src, src_slots, row_count, l.shape, &l.params.src)) ||
+        (rc = pool_side(dst, dst_slots, row_count, l.shape, &l.params.dst)))
         return rc;
-    attach_scales(p, src->scale, dst->scale, src->tensor_count);
+    attach_scales(l.params, src->scale, dst->scale, src->tensor_count);
+    if ((rc = finish_launch(ctx, &l))) return rc;
     DeviceScope scope(ctx->device);
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
-    rc = launch_copy(ctx, kPoolPool, p, shape, row_count, static_cast<hipStream_t>(stream));
+    rc = submit_launch(ctx, l, static_cast<hipStream_t>(stream));
     return rc ? rc : ok();
 }
 

@@ -149,6 +149,14 @@ class RowsView(ctypes.Structure):
                 ("row_stride", _u64 * 2), ("scale", ctypes.c_void_p)]
 
 
+class _PipelineDesc(ctypes.Structure):
+    _fields_ = [("layers", ctypes.c_uint32), ("staged", ctypes.c_uint32),
+                ("src_layers", ctypes.POINTER(PoolView)), ("dst_layers", ctypes.POINTER(PoolView)),
+                ("src_slots", _DeviceBuffer), ("dst_slots", _DeviceBuffer), ("row_count", _u64),
+                ("send", _DeviceBuffer * 2), ("recv", _DeviceBuffer * 2),
+                ("host", ctypes.c_void_p * 2), ("host_bytes", _u64)]
+
+
 SPAN_DTYPE = np.dtype([("row_start", "<u4"), ("token_offset", "<u4"), ("token_count", "<u4"),
                        ("page_table_start", "<u4")])
 
@@ -200,6 +208,13 @@ _EXPORTS = {
     "sgl_rocm_kv_unpack_layer": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(RowsView), _u64,
                                                   ctypes.POINTER(PoolView),
                                                   ctypes.POINTER(_DeviceBuffer), ctypes.c_void_p]),
+    "sgl_rocm_kv_pack_layers": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(PoolView), _u64,
+                                                 ctypes.c_uint32, ctypes.POINTER(_DeviceBuffer), _u64,
+                                                 ctypes.POINTER(RowsView), _u64, ctypes.c_void_p]),
+    "sgl_rocm_kv_unpack_layers": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(RowsView), _u64,
+                                                   ctypes.c_uint32, _u64, ctypes.POINTER(PoolView),
+                                                   _u64, ctypes.POINTER(_DeviceBuffer),
+                                                   ctypes.c_void_p]),
     "sgl_rocm_kv_transfer_layer": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(PoolView),
                                                     ctypes.POINTER(_DeviceBuffer), _u64,
                                                     ctypes.POINTER(PoolView),
@@ -211,6 +226,14 @@ _EXPORTS = {
                                                    ctypes.POINTER(_DeviceBuffer),
                                                    ctypes.c_void_p]),
     "sgl_rocm_kv_check_errors": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_void_p]),
+    "sgl_rocm_kv_pipeline_create": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_PipelineDesc),
+                                                     ctypes.POINTER(ctypes.c_void_p)]),
+    "sgl_rocm_kv_pipeline_run": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_void_p]),
+    "sgl_rocm_kv_pipeline_wait": (ctypes.c_int32, [ctypes.c_void_p]),
+    "sgl_rocm_kv_pipeline_layer_times": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_uint32,
+                                                          ctypes.POINTER(ctypes.c_float)]),
+    "sgl_rocm_kv_pipeline_elapsed": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_float)]),
+    "sgl_rocm_kv_pipeline_destroy": (ctypes.c_int32, [ctypes.c_void_p]),
     "sgl_rocm_kv_fill_synthetic": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_DeviceBuffer),
                                                     _u64, ctypes.c_uint32, ctypes.c_void_p]),
 }
@@ -534,6 +557,22 @@ class RocmKvPairCopyKernels:
         _call(lib().sgl_rocm_kv_unpack_layer, self._h, ctypes.byref(src), row_count,
               ctypes.byref(dst), ctypes.byref(slots), _stream(stream))
 
+    def pack_layers(self, src: PoolView, pool_layer_stride: int, layer_count: int,
+                    slots: _DeviceBuffer, row_count: int, dst: RowsView, rows_layer_stride: int,
+                    stream=None):
+        """Pack `layer_count` consecutive layers in one launch."""
+        _call(lib().sgl_rocm_kv_pack_layers, self._h, ctypes.byref(src), pool_layer_stride,
+              layer_count, ctypes.byref(slots), row_count, ctypes.byref(dst), rows_layer_stride,
+              _stream(stream))
+
+    def unpack_layers(self, src: RowsView, rows_layer_stride: int, layer_count: int,
+                      row_count: int, dst: PoolView, pool_layer_stride: int, slots: _DeviceBuffer,
+                      stream=None):
+        """Unpack `layer_count` consecutive layers in one launch."""
+        _call(lib().sgl_rocm_kv_unpack_layers, self._h, ctypes.byref(src), rows_layer_stride,
+              layer_count, row_count, ctypes.byref(dst), pool_layer_stride, ctypes.byref(slots),
+              _stream(stream))
+
     def transfer_layer(self, src: PoolView, src_slots: _DeviceBuffer, row_count: int,
                        dst: PoolView, dst_slots: _DeviceBuffer, stream=None):
         _call(lib().sgl_rocm_kv_transfer_layer, self._h, ctypes.byref(src),
@@ -553,6 +592,62 @@ class RocmKvPairCopyKernels:
     def fill_synthetic(self, buffer: _DeviceBuffer, seed: int, kind: int = FILL_BITS, stream=None):
         _call(lib().sgl_rocm_kv_fill_synthetic, self._h, ctypes.byref(buffer), seed, kind,
               _stream(stream))
+
+
+class LayerPipeline:
+    """sgl_rocm_kv_pipeline: a whole-request transfer, layer by layer, with
+    pack, the optional pinned-host hop (D2H then H2D) and unpack overlapped
+    across layers on four streams. ``send``/``recv`` are pairs of device
+    buffers and ``host`` a pair of pinned host buffers (objects with .ptr and
+    .nbytes), each holding one layer's rows."""
+
+    def __init__(self, kernels: "RocmKvPairCopyKernels", src_layers, dst_layers, src_slots,
+                 dst_slots, row_count: int, send, recv=None, host=None):
+        n = len(src_layers)
+        self._src = (PoolView * n)(*src_layers)
+        self._dst = (PoolView * n)(*dst_layers)
+        d = _PipelineDesc()
+        d.layers, d.staged = n, int(host is not None)
+        d.src_layers, d.dst_layers = self._src, self._dst
+        d.src_slots, d.dst_slots, d.row_count = src_slots, dst_slots, row_count
+        for i in range(2):
+            d.send[i] = _DeviceBuffer(send[i].ptr, send[i].nbytes)
+            if host is not None:
+                d.recv[i] = _DeviceBuffer(recv[i].ptr, recv[i].nbytes)
+                d.host[i] = host[i].ptr
+        d.host_bytes = min(h.nbytes for h in host) if host is not None else 0
+        self.layers = n
+        h = ctypes.c_void_p()
+        _call(lib().sgl_rocm_kv_pipeline_create, kernels._h, ctypes.byref(d), ctypes.byref(h))
+        self._h = h.value
+
+    def run(self, after=None):
+        _call(lib().sgl_rocm_kv_pipeline_run, self._h, getattr(after, "handle", after))
+
+    def wait(self):
+        _call(lib().sgl_rocm_kv_pipeline_wait, self._h)
+
+    def layer_times(self, layer: int):
+        """(pack, d2h, h2d, unpack, latency) in ms of `layer`'s last run."""
+        ms = (ctypes.c_float * 5)()
+        _call(lib().sgl_rocm_kv_pipeline_layer_times, self._h, layer, ms)
+        return tuple(ms)
+
+    def elapsed_ms(self) -> float:
+        ms = ctypes.c_float()
+        _call(lib().sgl_rocm_kv_pipeline_elapsed, self._h, ctypes.byref(ms))
+        return ms.value
+
+    def close(self):
+        if self._h:
+            _call(lib().sgl_rocm_kv_pipeline_destroy, self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def synthetic_words(seed: int, word_index) -> np.ndarray:

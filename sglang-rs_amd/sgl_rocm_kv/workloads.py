@@ -211,3 +211,33 @@ def scaled(t: Transfer, max_rows: int, seed: int = 0) -> Transfer:
     table, spans, dslots = _page_table_slots(rng, lengths, prefix, dst.page_size, dst.page_count)
     return Transfer(t.name + f" (first {rows} rows)", t.shape, src, dst, lengths, sslots, dslots,
                     table, spans, prefix)
+
+
+def waves(t: Transfer, max_rows: int, max_pages: int, seed: int = 0):
+    """Splits `t` into request waves whose rows fit a page_size-1 source pool
+    of `max_rows` slots and whose pages (cached prefix included) fit a
+    destination pool of `max_pages` pages; each wave gets fresh seeded slot
+    maps inside those two fixed pools (the pools are reused wave after wave)."""
+    rng = np.random.default_rng(seed)
+    prefix = t.prefix_tokens if t.prefix_tokens is not None else np.zeros(len(t.lengths), np.int64)
+    P = t.dst.page_size
+    out, start = [], 0
+    while start < len(t.lengths):
+        rows = pages = 0
+        end = start
+        while end < len(t.lengths):
+            r = int(t.lengths[end])
+            pg = -(-(int(prefix[end]) + r) // P)
+            if end > start and (rows + r > max_rows or pages + pg > max_pages):
+                break
+            rows, pages, end = rows + r, pages + pg, end + 1
+        if rows > max_rows or pages > max_pages:
+            raise ValueError(f"request {start} alone exceeds the wave pools")
+        lengths, pre = t.lengths[start:end], prefix[start:end]
+        src = PoolSpec(1, max_rows, t.src.head_layout)
+        dst = PoolSpec(P, max_pages, t.dst.head_layout)
+        table, spans, dslots = _page_table_slots(rng, lengths, pre, P, max_pages)
+        out.append(Transfer(f"{t.name} wave {len(out)}", t.shape, src, dst, lengths,
+                            _token_slots(rng, rows, max_rows), dslots, table, spans, pre))
+        start = end
+    return out

@@ -1,0 +1,139 @@
+// Host-only driver for the layout / plan mirror (kv_layout.cpp), built with
+// AddressSanitizer and UndefinedBehaviorSanitizer by tests/test_host_sanitizers.py.
+// It replays the reference goldens, then fuzzes every group-1 entry point
+// with small, boundary and overflowing values and checks what must hold for
+// any accepted input: every byte range lies inside the pool and the plan's
+// required sizes cover the last row and the last slot.
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <random>
+#include <vector>
+
+#include "sgl_rocm_kv.h"
+
+static int failures = 0;
+#define CHECK(cond)                                                        \
+    do {                                                                   \
+        if (!(cond)) {                                                     \
+            fprintf(stderr, "CHECK failed at line %d: %s\n", __LINE__, #cond); \
+            ++failures;                                                    \
+        }                                                                  \
+    } while (0)
+
+static uint64_t pick(std::mt19937_64 &rng) {
+    switch (rng() % 8) {
+    case 0: return 0;
+    case 1: return 1 + rng() % 4;
+    case 2: return 1 + rng() % 256;
+    case 3: return 1ull << (rng() % 64);
+    case 4: return UINT64_MAX - rng() % 4;
+    case 5: return rng();
+    case 6: return (1ull << 32) + rng() % 8;
+    default: return 2 * (1 + rng() % 64);
+    }
+}
+
+int main() {
+    // Goldens: crates/sglang-srt/tests/kv_cache.rs:51-217.
+    sgl_kv_runtime_layout rt;
+    memset(&rt, 0, sizeof rt);
+    rt.dtype = SGL_KV_DTYPE_BFLOAT16;
+    rt.page_size = 4;
+    rt.num_layers = 2;
+    rt.kv_heads = 2;
+    rt.head_dim = 8;
+    rt.kv_tensors_per_token = 2;
+    rt.bytes_per_token = 128;
+    rt.page_size_bytes = 512;
+    sgl_kv_paged_layout l;
+    CHECK(sgl_kv_paged_layout_new(&rt, 3, &l) == SGL_KV_OK);
+    uint64_t s = 0, e = 0;
+    CHECK(sgl_kv_paged_layout_tensor_token_byte_range(&l, 1, 1, 1, 3, &s, &e) == SGL_KV_OK);
+    CHECK(s == 992 && e == 1024);
+    CHECK(sgl_kv_paged_layout_tensor_slot_byte_range(&l, 1, 1, 12, &s, &e) ==
+          SGL_KV_LAYOUT_SLOT_OUT_OF_RANGE);
+    sgl_kv_pair_copy_layout pl = {4, 512, 256, 384, 32};
+    sgl_kv_pair_copy_plan plan;
+    CHECK(sgl_kv_pair_copy_plan_new(3, 12, &pl, 40, 48, &plan) == SGL_KV_OK);
+    CHECK(plan.key_rows_required_bytes == 112 && plan.pool_required_bytes == 1536);
+
+    std::mt19937_64 rng(20261201);
+    for (int it = 0; it < 200000; ++it) {
+        sgl_kv_runtime_layout r;
+        memset(&r, 0, sizeof r);
+        r.dtype = (int32_t)(rng() % 6);
+        r.page_size = pick(rng);
+        r.num_layers = pick(rng);
+        r.kv_heads = pick(rng);
+        r.head_dim = pick(rng);
+        r.kv_tensors_per_token = rng() % 2 ? 2 : pick(rng);
+        // Mostly self-consistent runtimes so that the range functions run.
+        if (rng() % 4) {
+            r.bytes_per_token = r.num_layers * r.kv_tensors_per_token * (1 + rng() % 64);
+            r.page_size_bytes = r.page_size * r.bytes_per_token;
+        } else {
+            r.bytes_per_token = pick(rng);
+            r.page_size_bytes = pick(rng);
+        }
+        const uint64_t pages = pick(rng);
+        sgl_kv_paged_layout lay;
+        int32_t rc;
+        if (rng() % 3)
+            rc = sgl_kv_paged_layout_new(&r, pages, &lay);
+        else
+            rc = sgl_kv_paged_layout_new_with_tensor_pair(&r, pages, pick(rng), pick(rng), &lay);
+        if (rc != SGL_KV_OK) continue;
+        for (int k = 0; k < 8; ++k) {
+            const uint64_t layer = rng() % 2 ? rng() % (r.num_layers + 1) : pick(rng);
+            const uint64_t tensor = rng() % 3;
+            const uint64_t slot = rng() % 2 ? rng() % (lay.slot_count + 2) : pick(rng);
+            if (sgl_kv_paged_layout_tensor_slot_byte_range(&lay, layer, tensor, slot, &s, &e) ==
+                SGL_KV_OK) {
+                CHECK(s < e);
+                CHECK(e <= lay.total_byte_len);
+                CHECK(slot < lay.slot_count && layer < r.num_layers);
+            }
+            sgl_kv_pair_copy_layout g;
+            if (sgl_kv_paged_layout_kv_pair_copy_geometry(&lay, layer, &g) == SGL_KV_OK) {
+                CHECK(g.key_in_page_offset + g.page_size * g.row_bytes <= g.page_stride_bytes);
+                CHECK(g.value_in_page_offset + g.page_size * g.row_bytes <= g.page_stride_bytes);
+            }
+        }
+    }
+
+    for (int it = 0; it < 200000; ++it) {
+        sgl_kv_pair_copy_layout g = {pick(rng), pick(rng), pick(rng), pick(rng), pick(rng)};
+        const uint64_t rows = pick(rng), slots = pick(rng), ks = pick(rng), vs = pick(rng);
+        sgl_kv_pair_copy_plan p;
+        if (sgl_kv_pair_copy_plan_new(rows, slots, &g, ks, vs, &p) != SGL_KV_OK) continue;
+        // Every accepted plan covers its last row and its last slot.
+        CHECK(p.key_rows_required_bytes >= g.row_bytes && p.value_rows_required_bytes >= g.row_bytes);
+        CHECK(p.slot_indices_required_bytes == rows * 8);
+        const uint64_t last = slots - 1;
+        const uint64_t key_end = (last / g.page_size) * g.page_stride_bytes + g.key_in_page_offset +
+                                 (last % g.page_size + 1) * g.row_bytes;
+        const uint64_t val_end = (last / g.page_size) * g.page_stride_bytes +
+                                 g.value_in_page_offset + (last % g.page_size + 1) * g.row_bytes;
+        CHECK(p.pool_required_bytes >= key_end && p.pool_required_bytes >= val_end);
+    }
+
+    for (int it = 0; it < 100000; ++it) {
+        const uint64_t page_size = rng() % 5;
+        std::vector<uint64_t> cache(rng() % 12);
+        uint64_t base = (rng() % 6) * (page_size ? page_size : 1);
+        for (size_t i = 0; i < cache.size(); ++i) cache[i] = rng() % 8 ? base + i : rng() % 64;
+        std::vector<uint64_t> out(cache.size() + 1);
+        uint64_t n = 0;
+        const int32_t rc = sgl_kv_transfer_page_indices(0, (rng() % 3) * 2, cache.data(), cache.size(),
+                                                        page_size, out.data(), &n);
+        if (rc == SGL_KV_OK) CHECK(n <= cache.size());
+    }
+    if (failures) {
+        fprintf(stderr, "%d checks failed\n", failures);
+        return 1;
+    }
+    printf("layout fuzz ok\n");
+    return 0;
+}

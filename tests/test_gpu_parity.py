@@ -452,3 +452,152 @@ def test_c2_full_size_three_layers(k):
                 want = kv.synthetic_words(seed, idx.reshape(-1))
                 np.testing.assert_array_equal(got[tns, lo:hi].reshape(-1), want)
         assert np.array_equal(rows.download(), again.download()), "unpack -> re-pack round trip differs"
+
+
+# --- layer pipeline (pack -> pinned-host hop -> unpack) ----------------------------------------
+
+def _pipeline_case(k, t, staged, seed):
+    sh = t.shape
+    rb, n, T, L = sh.row_bytes, t.rows, sh.tensors, sh.layers
+    rng = np.random.default_rng(seed)
+    src_h = rng.integers(0, 256, t.src.byte_len(sh), dtype=np.uint8)
+    dst_h = rng.integers(0, 256, t.dst.byte_len(sh), dtype=np.uint8)
+    src, dst = hip.DeviceBuffer.from_array(src_h), hip.DeviceBuffer.from_array(dst_h)
+    ss, ds = hip.DeviceBuffer.from_array(t.src_slots), hip.DeviceBuffer.from_array(t.dst_slots)
+    layer_bytes = T * n * rb
+    send = [hip.DeviceBuffer(layer_bytes) for _ in range(2)]
+    recv = [hip.DeviceBuffer(layer_bytes) for _ in range(2)] if staged else None
+    host = [hip.PinnedBuffer(layer_bytes) for _ in range(2)] if staged else None
+    pipe = kv.LayerPipeline(k, [_kpool(src, t.src, sh, l) for l in range(L)],
+                            [_kpool(dst, t.dst, sh, l) for l in range(L)], _db(ss), _db(ds), n,
+                            send, recv, host)
+    want = dst_h.copy()
+    rows = [np.zeros(n * rb, np.uint8) for _ in range(T)]
+    for l in range(L):
+        oracle.pack(_opool(t.src, sh, l), src_h, t.src_slots, rows[0], rows[1] if T == 2 else None,
+                    rb, rb, threads=4)
+        oracle.unpack(_opool(t.dst, sh, l), want, t.dst_slots, rows[0], rows[1] if T == 2 else None,
+                      rb, rb, threads=4)
+    for run in range(2):
+        if run:
+            dst.upload(dst_h)
+        pipe.run()
+        pipe.wait()
+        np.testing.assert_array_equal(dst.download(), want)
+        times = [pipe.layer_times(l) for l in range(L)]
+        assert all(tt[0] > 0 and tt[3] > 0 for tt in times)
+        assert all((tt[1] > 0 and tt[2] > 0) == staged for tt in times)
+        assert pipe.elapsed_ms() >= max(tt[4] for tt in times) * 0.999
+    pipe.close()
+
+
+def test_staged_pipeline_matches_oracle(k):
+    """C5 shape: cached prefixes, pack -> D2H -> pinned host -> H2D -> unpack
+    over all 32 layers, run twice (buffer reuse across runs)."""
+    t = wl.scaled(wl.c5(), 5000, seed=12)
+    _say(f"staged pipeline: {t.rows} rows x {t.shape.layers} layers")
+    _pipeline_case(k, t, staged=True, seed=31)
+
+
+def test_direct_pipeline_matches_oracle(k):
+    t = wl.scaled(wl.c3(), 9000, seed=13)
+    _say(f"direct pipeline (HND dst): {t.rows} rows x {t.shape.layers} layers")
+    _pipeline_case(k, t, staged=False, seed=32)
+
+
+def test_pipeline_rejects_short_staging_buffers(k):
+    t = wl.scaled(wl.c2(), 100, seed=14)
+    sh = t.shape
+    src, dst = hip.DeviceBuffer(t.src.byte_len(sh)), hip.DeviceBuffer(t.dst.byte_len(sh))
+    ss, ds = hip.DeviceBuffer.from_array(t.src_slots), hip.DeviceBuffer.from_array(t.dst_slots)
+    lb = 2 * t.rows * sh.row_bytes
+    send = [hip.DeviceBuffer(lb), hip.DeviceBuffer(lb)]
+    recv = [hip.DeviceBuffer(lb), hip.DeviceBuffer(lb - 16)]
+    host = [hip.PinnedBuffer(lb), hip.PinnedBuffer(lb)]
+    with pytest.raises(kv.KvError) as ei:
+        kv.LayerPipeline(k, [_kpool(src, t.src, sh, l) for l in range(2)],
+                         [_kpool(dst, t.dst, sh, l) for l in range(2)], _db(ss), _db(ds), t.rows,
+                         send, recv, host)
+    assert ei.value.variant == "AllocationOutOfBounds" and ei.value.name == "recv[1]"
+
+
+# --- multi-layer launches ----------------------------------------------------------------------------
+
+def _multi_layer_case(k, t, seed, fp8_scales=False):
+    sh = t.shape
+    rb, n, T, L = sh.row_bytes, t.rows, sh.tensors, sh.layers
+    rng = np.random.default_rng(seed)
+    src_h = rng.integers(0, 256, t.src.byte_len(sh), dtype=np.uint8)
+    dst_h = rng.integers(0, 256, t.dst.byte_len(sh), dtype=np.uint8)
+    src, dst = hip.DeviceBuffer.from_array(src_h), hip.DeviceBuffer.from_array(dst_h)
+    ss, ds = hip.DeviceBuffer.from_array(t.src_slots), hip.DeviceBuffer.from_array(t.dst_slots)
+    layer_bytes = T * n * rb
+    rows = hip.DeviceBuffer(L * layer_bytes)
+    scales_h = rng.standard_normal(L * T).astype(np.float32)
+    sc_src = hip.DeviceBuffer.from_array(scales_h)
+    sc_rows, sc_dst = hip.DeviceBuffer(L * T * 4), hip.DeviceBuffer(L * T * 4)
+    rv = kv.rows_view([rows.ptr + i * n * rb for i in range(T)],
+                      [L * layer_bytes - i * n * rb for i in range(T)], [rb] * T,
+                      sc_rows.ptr if fp8_scales else None)
+    sv = _kpool(src, t.src, sh, 0, sc_src.ptr if fp8_scales else None)
+    dv = _kpool(dst, t.dst, sh, 0, sc_dst.ptr if fp8_scales else None)
+    k.pack_layers(sv, t.src.page_size * T * rb, L, _db(ss), n, rv, layer_bytes)
+    k.unpack_layers(rv, layer_bytes, L, n, dv, t.dst.page_size * T * rb, _db(ds))
+    k.check_errors()
+    want_rows = np.zeros(L * layer_bytes, np.uint8)
+    want_dst = dst_h.copy()
+    for l in range(L):
+        part = want_rows[l * layer_bytes:(l + 1) * layer_bytes]
+        r0, r1 = part[: n * rb], (part[n * rb:] if T == 2 else None)
+        oracle.pack(_opool(t.src, sh, l), src_h, t.src_slots, r0, r1, rb, rb, threads=4)
+        oracle.unpack(_opool(t.dst, sh, l), want_dst, t.dst_slots, r0, r1, rb, rb, threads=4)
+    np.testing.assert_array_equal(rows.download(), want_rows)
+    np.testing.assert_array_equal(dst.download(), want_dst)
+    if fp8_scales:
+        np.testing.assert_array_equal(sc_rows.download(dtype=np.uint32), scales_h.view(np.uint32))
+        np.testing.assert_array_equal(sc_dst.download(dtype=np.uint32), scales_h.view(np.uint32))
+
+
+def test_multi_layer_c1_full_size(k):
+    """Every layer of C1 in one pack launch and one unpack launch."""
+    t = wl.c1()
+    _say(f"multi-layer C1: {t.rows} rows x {t.shape.layers} layers per launch")
+    _multi_layer_case(k, t, seed=41)
+
+
+@pytest.mark.parametrize("name,make,max_rows", [
+    ("C3-hnd", wl.c3, 3000), ("C4-fp8", lambda: wl.c4(fp8=True), 2000), ("C5", wl.c5, 3000)])
+def test_multi_layer_scaled_configs(k, name, make, max_rows):
+    t = wl.scaled(make(), max_rows, seed=len(name) + 50)
+    _say(f"multi-layer {name}: {t.rows} rows x {t.shape.layers} layers")
+    _multi_layer_case(k, t, seed=len(name), fp8_scales=name == "C4-fp8")
+
+
+def test_multi_layer_validation(k):
+    t = wl.scaled(wl.c2(), 100, seed=15)
+    sh = t.shape
+    rb, n = sh.row_bytes, t.rows
+    src, dst = hip.DeviceBuffer(t.src.byte_len(sh)), hip.DeviceBuffer(t.dst.byte_len(sh))
+    ss, ds = hip.DeviceBuffer.from_array(t.src_slots), hip.DeviceBuffer.from_array(t.dst_slots)
+    rows = hip.DeviceBuffer(34 * 2 * n * rb)
+    rv = kv.rows_view([rows.ptr, rows.ptr + n * rb], [34 * 2 * n * rb, 34 * 2 * n * rb - n * rb], [rb, rb])
+    sv, dv = _kpool(src, t.src, sh, 0), _kpool(dst, t.dst, sh, 0)
+    # 33 layers run past the pool's pages (the rows buffer holds 34)
+    with pytest.raises(kv.KvError) as ei:
+        k.pack_layers(sv, t.src.page_size * 2 * rb, 33, _db(ss), n, rv, 2 * n * rb)
+    assert ei.value.variant == "TensorPageRegionOutOfBounds"
+    # 35 layers also run past the rows buffer, which is checked first
+    with pytest.raises(kv.KvError) as ei:
+        k.pack_layers(sv, t.src.page_size * 2 * rb, 35, _db(ss), n, rv, 2 * n * rb)
+    assert ei.value.variant == "AllocationOutOfBounds" and ei.value.name == "values"
+    # destination rows of consecutive layers would overlap
+    with pytest.raises(kv.KvError) as ei:
+        k.pack_layers(sv, t.src.page_size * 2 * rb, 4, _db(ss), n, rv, n * rb)
+    assert ei.value.variant == "InvalidArgument" and ei.value.name == "rows_layer_stride"
+    # destination pool layers would overlap
+    with pytest.raises(kv.KvError) as ei:
+        k.unpack_layers(rv, 2 * n * rb, 4, n, dv, t.dst.page_size * rb, _db(ds))
+    assert ei.value.variant == "InvalidArgument" and ei.value.name == "pool_layer_stride"
+    with pytest.raises(kv.KvError) as ei:
+        k.unpack_layers(rv, 2 * n * rb, 0, n, dv, t.dst.page_size * 2 * rb, _db(ds))
+    assert ei.value.variant == "InvalidArgument" and ei.value.name == "layer_count"

@@ -1,0 +1,29 @@
+"""The host layout / plan code of libsgl_rocm_kv under AddressSanitizer and
+UndefinedBehaviorSanitizer: tests/native/layout_fuzz.cpp replays reference
+goldens and fuzzes every group-1 entry point (small, boundary and
+overflowing values); any out-of-bounds access, overflow UB or violated
+invariant fails the run. Host code only (g++, no device code)."""
+import os
+import shutil
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CSRC = os.path.join(ROOT, "sglang-rs_amd", "csrc")
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="g++ not available")
+def test_layout_fuzz_under_asan_ubsan(tmp_path):
+    exe = tmp_path / "layout_fuzz"
+    cmd = ["g++", "-std=c++17", "-O1", "-g", "-fno-omit-frame-pointer",
+           "-fsanitize=address,undefined", "-fno-sanitize-recover=all",
+           "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include", "-I" + os.path.join(ROOT, "include"),
+           "-I" + CSRC, os.path.join(ROOT, "tests", "native", "layout_fuzz.cpp"),
+           os.path.join(CSRC, "kv_layout.cpp"), "-o", str(exe)]
+    subprocess.run(cmd, check=True, capture_output=True, timeout=240)
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=0",
+               UBSAN_OPTIONS="print_stacktrace=1")
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=240, env=env)
+    assert r.returncode == 0, r.stderr[-4000:]
+    assert "layout fuzz ok" in r.stdout

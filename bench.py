@@ -172,7 +172,8 @@ def run_coresident(t, config, args):
                             [xfer.nbytes - i * n * rb for i in range(T)], [rb] * T, sc(1, 0))
     s_pack = hip.Stream()
     s_unpack = hip.Stream() if args.streams == 2 else s_pack
-    if args.launch == "auto":   # measured on MI355X: per-layer launches win on large layers
+    auto = args.launch == "auto"
+    if auto:   # measured on MI355X: per-layer launches win on large layers
         args.launch = "layers" if 2 * T * n * rb < (256 << 20) else "layer"
     multi = args.launch == "layers"
     units = 1 if multi else L   # launches of each kind per step
@@ -270,8 +271,8 @@ def run_coresident(t, config, args):
         "kernel_sum_gbs": round(kernel_gbs, 1),
         "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     # the committed counter summary covers per-layer launches
-                     "traffic": None if multi else _traffic_from_profiles(dom_name, config),
+                     # the committed counter summaries were taken with --launch auto
+                     "traffic": _traffic_from_profiles(dom_name, config) if auto else None,
                      "algorithmic_bytes_per_launch": launch_bytes * (L if multi else 1)},
     }
 

@@ -196,40 +196,37 @@ __device__ __forceinline__ void sglkv_copy_rows(const sglkv_copy_params &p) {
             }
             continue;
         }
-        // Ragged or faulty tile: offsets of this thread's rows first, then
-        // every load, then every store, each row predicated.
-        uint64_t soff[RU];
-        uint64_t doff[RU];
-#pragma unroll
+        // Ragged or faulty tile (the last tile, or a bad slot): row by row,
+        // kept rolled so that it does not inflate the register allocation of
+        // the clean path above.
+#pragma unroll 1
         for (uint32_t k = 0; k < RU; ++k) {
             const uint32_t i = threadIdx.y + k * blockDim.y;
             const uint32_t r = row0 + i;
-            uint64_t so = SGLKV_INVALID_OFFSET;
-            uint64_t dof = SGLKV_INVALID_OFFSET;
-            if (r < p.rows) {
-                so = SK == SGLKV_SIDE_POOL ? s_src[i] : static_cast<uint64_t>(r) * src_stride;
-                dof = DK == SGLKV_SIDE_POOL ? s_dst[i] : static_cast<uint64_t>(r) * dst_stride;
-                if (so == SGLKV_INVALID_OFFSET) dof = SGLKV_INVALID_OFFSET;
-            }
-            soff[k] = so;
-            doff[k] = dof;
-        }
-#pragma unroll
-        for (uint32_t k = 0; k < RU; ++k) {
-            if (doff[k] != SGLKV_INVALID_OFFSET)
-                buf[k] = sglkv_load<V, NT>(reinterpret_cast<gload_t *>(sb + soff[k]));
-        }
-#pragma unroll
-        for (uint32_t k = 0; k < RU; ++k) {
-            if (doff[k] != SGLKV_INVALID_OFFSET)
-                sglkv_store<V, NT>(reinterpret_cast<gstore_t *>(db + doff[k]), buf[k]);
+            if (r >= p.rows) break;
+            const uint64_t so = SK == SGLKV_SIDE_POOL ? s_src[i] : static_cast<uint64_t>(r) * src_stride;
+            const uint64_t dof = DK == SGLKV_SIDE_POOL ? s_dst[i] : static_cast<uint64_t>(r) * dst_stride;
+            if (so == SGLKV_INVALID_OFFSET || dof == SGLKV_INVALID_OFFSET) continue;
+            sglkv_store<V, NT>(reinterpret_cast<gstore_t *>(db + dof),
+                               sglkv_load<V, NT>(reinterpret_cast<gload_t *>(sb + so)));
         }
     }
 }
 
+// Occupancy hint: the waves per SIMD the register allocation must allow
+// (0 = the compiler's choice).
+#ifndef SGLKV_WAVES_PER_EU
+#define SGLKV_WAVES_PER_EU 0
+#endif
+#if SGLKV_WAVES_PER_EU
+#define SGLKV_OCCUPANCY __attribute__((amdgpu_waves_per_eu(SGLKV_WAVES_PER_EU)))
+#else
+#define SGLKV_OCCUPANCY
+#endif
+
 #define SGLKV_COPY_KERNEL(VB, SK, DK, NT, REMAP, NAME)                                 \
-    extern "C" __global__ __launch_bounds__(SGLKV_BLOCK_THREADS) void NAME(           \
-        const sglkv_copy_params p) {                                                   \
+    extern "C" __global__ __launch_bounds__(SGLKV_BLOCK_THREADS) SGLKV_OCCUPANCY void  \
+    NAME(const sglkv_copy_params p) {                                                  \
         sglkv_copy_rows<VB, SK, DK, NT, REMAP>(p);                                     \
     }
 

@@ -601,3 +601,65 @@ def test_multi_layer_validation(k):
     with pytest.raises(kv.KvError) as ei:
         k.unpack_layers(rv, 2 * n * rb, 0, n, dv, t.dst.page_size * 2 * rb, _db(ds))
     assert ei.value.variant == "InvalidArgument" and ei.value.name == "layer_count"
+
+
+# --- randomized shapes ------------------------------------------------------------------------------
+
+def _random_case(rng):
+    T = int(rng.integers(1, 3))
+    H = int(rng.choice([1, 2, 3, 4, 8]))
+    elt = int(rng.choice([1, 2, 4]))
+    D = int(rng.choice([1, 3, 8, 24, 64, 128, 160]))
+    L = int(rng.integers(1, 4))
+    rb = H * D * elt
+    src = wl.PoolSpec(int(rng.choice([1, 2, 16, 64])), 0, int(rng.integers(0, 2)))
+    dst = wl.PoolSpec(int(rng.choice([1, 4, 16, 64])), 0, int(rng.integers(0, 2)))
+    rows = int(rng.choice([1, 5, 64, 200, 777, 2048]))
+    src.page_count = -(-rows // src.page_size) + int(rng.integers(0, 4))
+    dst.page_count = -(-rows // dst.page_size) + int(rng.integers(0, 4))
+    shape = wl.Shape(L, H, D, elt, T)
+    ss = rng.permutation(src.page_count * src.page_size)[:rows].astype(np.uint64)
+    ds = rng.permutation(dst.page_count * dst.page_size)[:rows].astype(np.uint64)
+    extra = int(rng.choice([0, 0, 16, 1, 2, 4, 8, 48]))
+    return shape, src, dst, ss, ds, rows, rb + extra
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_shapes_pack_unpack_transfer(k, seed):
+    """Random T, heads, dim, element size, page sizes, NHD/HND on either
+    side, row strides and row counts: pack, unpack and pool-to-pool against
+    the oracle on the same bytes."""
+    rng = np.random.default_rng(1000 + seed)
+    sh, sspec, dspec, ss, ds, rows, stride = _random_case(rng)
+    rb, T = sh.row_bytes, sh.tensors
+    layer = int(rng.integers(0, sh.layers))
+    _say(f"random case {seed}: T={T} H={sh.heads} D={sh.head_dim} elt={sh.elt_bytes} rows={rows} "
+         f"P {sspec.page_size}{'H' if sspec.head_layout else 'N'}->{dspec.page_size}"
+         f"{'H' if dspec.head_layout else 'N'} stride={stride}")
+    src_h = rng.integers(0, 256, sspec.byte_len(sh), dtype=np.uint8)
+    dst_h = rng.integers(0, 256, dspec.byte_len(sh), dtype=np.uint8)
+    src, dst = hip.DeviceBuffer.from_array(src_h), hip.DeviceBuffer.from_array(dst_h)
+    sb, dbuf = hip.DeviceBuffer.from_array(ss), hip.DeviceBuffer.from_array(ds)
+    plane = (rows - 1) * stride + rb
+    rows_buf = hip.DeviceBuffer(T * plane)
+    rows_buf.fill(0x3C)
+    rv = kv.rows_view([rows_buf.ptr + t_ * plane for t_ in range(T)], [plane] * T, [stride] * T)
+    k.pack_layer(_kpool(src, sspec, sh, layer), _db(sb), rows, rv)
+    k.unpack_layer(rv, rows, _kpool(dst, dspec, sh, layer), _db(dbuf))
+    k.check_errors()
+    want_rows = np.full(T * plane, 0x3C, np.uint8)
+    r0, r1 = want_rows[:plane], (want_rows[plane:] if T == 2 else None)
+    oracle.pack(_opool(sspec, sh, layer), src_h, ss, r0, r1, stride, stride)
+    want_dst = dst_h.copy()
+    oracle.unpack(_opool(dspec, sh, layer), want_dst, ds, r0, r1, stride, stride)
+    np.testing.assert_array_equal(rows_buf.download(), want_rows)
+    np.testing.assert_array_equal(dst.download(), want_dst)
+    # pool -> pool of another layer, into a fresh destination
+    layer2 = int(rng.integers(0, sh.layers))
+    dst2_h = rng.integers(0, 256, dspec.byte_len(sh), dtype=np.uint8)
+    dst2 = hip.DeviceBuffer.from_array(dst2_h)
+    k.transfer_layer(_kpool(src, sspec, sh, layer2), _db(sb), rows, _kpool(dst2, dspec, sh, layer2),
+                     _db(dbuf))
+    k.check_errors()
+    oracle.transfer(_opool(sspec, sh, layer2), src_h, ss, _opool(dspec, sh, layer2), dst2_h, ds)
+    np.testing.assert_array_equal(dst2.download(), dst2_h)

@@ -58,6 +58,10 @@ DESCRIPTIONS = {
           "src and dst page_size-64 pools with independent random page tables",
     "c4fp8": "C4 fp8: MLA latent rows as 576-byte fp8-e4m3 rows with per-layer scales passed "
              "through, 61 layers, 32 requests x 8192, page_size-64 -> page_size-64",
+    "c2pages": "C2 shape as the reference transfers it today: page-for-page copies between "
+               "page_size-64 pools of equal layout (131072 tokens = 2048 pages of 8 MiB, random "
+               "source and destination pages), built with sgl_kv_build_page_requests and run "
+               "as one launch (no relayout); algorithmic bytes = 2 x payload",
     "c5": "C5: ragged radix-prefix GQA transfer (Llama-3-8B shape), 512 requests log-uniform "
           "[16,32768], page-aligned cached prefixes U[0,0.9]; request waves through the layer "
           "pipeline pack -> D2H -> pinned host -> H2D -> unpack on 4 streams",
@@ -368,6 +372,63 @@ def run_staged(t, args):
     }
 
 
+def run_pages(args):
+    """The reference's PD transfer (transfer.rs:1945-2090) on one GPU: whole
+    pages of equal-layout pools, one page request per page, executed by one
+    launch per step."""
+    import sgl_rocm_kv as kv
+    from sgl_rocm_kv import hip
+    from sgl_rocm_kv import workloads as wl
+    sh = wl.c2().shape
+    P, pages_moved, pool_pages = 64, 2048, 4096
+    spec = wl.PoolSpec(P, pool_pages)
+    pb = spec.page_stride(sh)
+    rng = np.random.default_rng(11)
+    src_pages = rng.permutation(pool_pages)[:pages_moved]
+    dst_pages = rng.permutation(pool_pages)[:pages_moved]
+    k = kv.RocmKvPairCopyKernels(0)
+    src, dst = hip.DeviceBuffer(spec.byte_len(sh)), hip.DeviceBuffer(spec.byte_len(sh))
+    k.fill_synthetic(kv.device_buffer(src.ptr, src.nbytes), 2024, kv.FILL_BF16_NORMAL)
+    # the decode side's dst_kv_ptrs = [pool base], dst_kv_indices = its pages
+    reqs = kv.build_remote_page_requests(src.ptr, pb, pages_moved * P, P, src_pages, [dst.ptr],
+                                         dst_pages.astype(np.int32), pb)
+    rq = hip.DeviceBuffer.from_array(reqs)
+    args_k = (kv.device_buffer(rq.ptr, rq.nbytes), len(reqs), pb, kv.device_buffer(src.ptr, src.nbytes),
+              kv.device_buffer(dst.ptr, dst.nbytes), True)
+    s = hip.Stream()
+    for _ in range(args.warmup):
+        k.execute_page_requests(*args_k, stream=s)
+    s.synchronize()
+    k.check_errors()
+    a, b = hip.Event(), hip.Event()
+    hip.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        k.execute_page_requests(*args_k, stream=s)
+    hip.synchronize()
+    wall = time.perf_counter() - t0
+    a.record(s)
+    k.execute_page_requests(*args_k, stream=s)
+    b.record(s)
+    s.synchronize()
+    k.check_errors()
+    launch_ms = a.elapsed_ms(b)
+    payload = pages_moved * pb
+    gbs = 2 * payload / (wall / args.steps) / 1e9
+    achieved = 2 * payload / (launch_ms / 1e3) / 1e9
+    log(f"page requests: {len(reqs)} x {pb >> 20} MiB, wall {gbs:.0f} GB/s, launch {launch_ms:.3f} ms")
+    k.close()
+    return {
+        "value": round(gbs, 1),
+        "ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "config_extra": {"pages": pages_moved, "page_bytes": pb, "payload_bytes": payload,
+                         "algorithmic_bytes_per_step": 2 * payload},
+        "roofline": {"bound": "hbm", "kernel": "sglkv_copy_requests", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "algorithmic_bytes_per_launch": 2 * payload},
+    }
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -398,10 +459,15 @@ def main():
 
     from sgl_rocm_kv import workloads as wl
     makers = {"c1": wl.c1, "c2": wl.c2, "c3": wl.c3, "c4": wl.c4,
-              "c4fp8": lambda: wl.c4(fp8=True), "c5": wl.c5}
+              "c4fp8": lambda: wl.c4(fp8=True), "c5": wl.c5, "c2pages": wl.c2}
     t = makers[args.config]()
     log(f"workload {t.name}: {t.rows} tokens moved, payload {t.payload_bytes / 2**30:.2f} GiB")
-    r = run_staged(t, args) if args.config == "c5" else run_coresident(t, args.config, args)
+    if args.config == "c5":
+        r = run_staged(t, args)
+    elif args.config == "c2pages":
+        r = run_pages(args)
+    else:
+        r = run_coresident(t, args.config, args)
     gbs = r.pop("value")
     extra = r.pop("config_extra")
     out = {

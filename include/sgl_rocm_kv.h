@@ -94,7 +94,19 @@ typedef enum sgl_kv_status {
     SGL_KV_PLAN_NON_CONTIGUOUS_CACHE_SLOTS = 45,/* a = request index, b = expected, c = actual */
 
     SGL_KV_DEVICE_PAGE_INDEX_OUT_OF_RANGE = 50, /* a page-table entry is negative, past the table or past the pool */
-    SGL_KV_DEVICE_SPAN_OUT_OF_RANGE = 51        /* a row is not covered by its span list */
+    SGL_KV_DEVICE_SPAN_OUT_OF_RANGE = 51,       /* a row is not covered by its span list */
+    SGL_KV_DEVICE_REQUEST_OUT_OF_RANGE = 52,    /* a page request outside its source or target region */
+
+    /* 60.. mirror MooncakeRequestBuildError (crates/sglang-srt/src/transfer.rs:2092-2112) */
+    SGL_KV_REQ_ZERO_PAGE_SIZE = 60,
+    SGL_KV_REQ_ZERO_REMOTE_ITEM_SIZE = 61,
+    SGL_KV_REQ_MISSING_REMOTE_POINTERS = 62,
+    SGL_KV_REQ_SPAN_PAGE_COUNT_MISMATCH = 63,   /* a = expected_page_count, b = source_page_index_count */
+    SGL_KV_REQ_REMOTE_INDEX_COUNT_MISMATCH = 64,/* a = source_page_count, b = dst_kv_index_count */
+    SGL_KV_REQ_REMOTE_ITEM_LAYOUT_MISMATCH = 65,/* a = page_size_bytes, b = split_page_size */
+    SGL_KV_REQ_NEGATIVE_REMOTE_INDEX = 66,      /* a = the index (as int64) */
+    SGL_KV_REQ_ADDRESS_OVERFLOW = 67,
+    SGL_KV_REQ_OFFSET_OVERFLOW = 68
 } sgl_kv_status;
 
 /* Detail of the calling thread's most recent failure. */
@@ -222,6 +234,37 @@ int32_t sgl_kv_pair_copy_plan_new(uint64_t row_count, uint64_t slot_count,
 int32_t sgl_kv_transfer_page_indices(uint64_t request_index, uint64_t token_offset,
                                      const uint64_t *cache_slots, uint64_t slot_len,
                                      uint64_t page_size, uint64_t *out_pages, uint64_t *out_len);
+
+/* One page write of a PD transfer (MooncakeTransferRequest without the
+ * transport fields, transfer.rs:1945-2090): `length` bytes from host-visible
+ * address `source` to `target_offset` in the target's registered memory. */
+typedef struct sgl_kv_page_request {
+    uint64_t source;
+    uint64_t target_offset;
+    uint64_t length;
+} sgl_kv_page_request;
+
+/* build_mooncake_kv_transfer_requests (transfer.rs:1945-1997): one request per
+ * source page of a span; target page = span page offset (token_offset /
+ * page_size) + i. `out` needs page_count entries. */
+int32_t sgl_kv_build_page_requests(uint64_t source_base_addr, uint64_t page_size_bytes,
+                                   uint64_t target_base_offset, uint64_t token_offset,
+                                   uint64_t token_count, uint64_t page_size,
+                                   const uint64_t *page_indices, uint64_t page_count,
+                                   sgl_kv_page_request *out, uint64_t out_capacity,
+                                   uint64_t *out_len);
+/* build_mooncake_remote_kv_transfer_requests (transfer.rs:1999-2090): the
+ * decode side advertises dst_kv_ptrs (one per split of a page) and one
+ * dst_kv_indices entry per page; each source page becomes ptr_count
+ * requests of dst_kv_item_len bytes. `out` needs page_count * ptr_count
+ * entries. */
+int32_t sgl_kv_build_remote_page_requests(uint64_t source_base_addr, uint64_t page_size_bytes,
+                                          uint64_t token_count, uint64_t page_size,
+                                          const uint64_t *page_indices, uint64_t page_count,
+                                          const uint64_t *dst_kv_ptrs, uint64_t ptr_count,
+                                          const int32_t *dst_kv_indices, uint64_t index_count,
+                                          uint64_t dst_kv_item_len, sgl_kv_page_request *out,
+                                          uint64_t out_capacity, uint64_t *out_len);
 
 /* ------------------------------------------------------------------------ */
 /* Group 2: kernels                                                         */
@@ -453,9 +496,27 @@ typedef enum sgl_kv_fill_kind {
 int32_t sgl_rocm_kv_fill_synthetic(sgl_rocm_kv_ctx *ctx, const sgl_kv_device_buffer *buffer,
                                    uint64_t seed, uint32_t kind, void *stream);
 
+/* Executes page requests (sgl_kv_build_page_requests /
+ * sgl_kv_build_remote_page_requests output, uploaded to the device) as
+ * device copies: the page-for-page PD transfer between co-resident pools of
+ * equal page size and layout, one launch for the whole list instead of one
+ * transport write per page (transfer.rs:3071-3137). Request i copies
+ * length_i bytes from `source` to target_base + target_offset_i, where
+ * target_base is target_region.ptr, or 0 when `offsets_are_addresses` (the
+ * remote form, whose offsets are dst_kv_ptrs-based addresses). Every request
+ * must lie inside source_region and target_region and be at most
+ * `max_length` bytes; others are skipped and raise the error word (REQUEST).
+ * Asynchronous. */
+int32_t sgl_rocm_kv_execute_page_requests(sgl_rocm_kv_ctx *ctx,
+                                          const sgl_kv_device_buffer *requests, uint64_t count,
+                                          uint64_t max_length,
+                                          const sgl_kv_device_buffer *source_region,
+                                          const sgl_kv_device_buffer *target_region,
+                                          uint32_t offsets_are_addresses, void *stream);
+
 /* Synchronises `stream`, reads and clears the error word, and maps it to
- * SGL_KV_DEVICE_SLOT_INDEX_OUT_OF_RANGE, _PAGE_INDEX_ or _SPAN_ (the first
- * raised, in that order). Replaces the flag readback of
+ * SGL_KV_DEVICE_SLOT_INDEX_OUT_OF_RANGE, _PAGE_INDEX_, _SPAN_ or _REQUEST_
+ * (the first raised, in that order). Replaces the flag readback of
  * cuda_kv_kernels.rs:613-621 for the asynchronous calls. */
 int32_t sgl_rocm_kv_check_errors(sgl_rocm_kv_ctx *ctx, void *stream);
 

@@ -71,6 +71,7 @@ struct sgl_rocm_kv_ctx {
     hipFunction_t copy[5][3];
     hipFunction_t resolve;
     hipFunction_t fill;
+    hipFunction_t requests;
     uint32_t *flag;
     uint32_t rows_per_thread;  // from the code object
     uint32_t max_tile_rows;

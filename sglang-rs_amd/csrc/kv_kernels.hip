@@ -336,3 +336,61 @@ extern "C" __global__ __launch_bounds__(SGLKV_BLOCK_THREADS) void sglkv_fill_syn
         out[i] = w;
     }
 }
+
+// Executes PD page requests (the descriptors of
+// build_mooncake_{,remote_}kv_transfer_requests,
+// crates/sglang-srt/src/transfer.rs:1945-2090) as device copies: the
+// page-for-page transfer between co-resident pools of equal page size and
+// layout, in one launch instead of one transport write per page. Workgroup b
+// copies chunk b % chunks (64 KiB) of request b / chunks. A request whose
+// source or target range leaves its region, or that is longer than the
+// launch's chunks cover, is skipped and raises SGLKV_FLAG_REQUEST.
+__device__ __forceinline__ bool sglkv_inside(uint64_t addr, uint64_t len, uint64_t lo, uint64_t hi) {
+    return lo <= hi && addr >= lo && len <= hi - lo && addr - lo <= (hi - lo) - len;
+}
+
+extern "C" __global__ __launch_bounds__(SGLKV_BLOCK_THREADS) void sglkv_copy_requests(
+    const sglkv_request_params p) {
+    const uint64_t b = blockIdx.x;
+    const uint64_t index = b / p.chunks;
+    const uint64_t chunk = b - index * p.chunks;
+    if (index >= p.count) return;
+    const sglkv_request r = p.requests[index];
+    const uint64_t begin = chunk * SGLKV_REQUEST_CHUNK;
+    const bool target_wraps = r.target_offset > ~0ull - p.target_base;
+    const uint64_t target = p.target_base + r.target_offset;
+    const bool ok = !target_wraps && r.length <= p.chunks * SGLKV_REQUEST_CHUNK &&
+                    sglkv_inside(r.source, r.length, p.source_lo, p.source_hi) &&
+                    sglkv_inside(target, r.length, p.target_lo, p.target_hi);
+    if (!ok) {
+        if (chunk == 0 && threadIdx.x == 0) atomicOr(p.flag, SGLKV_FLAG_REQUEST);
+        return;
+    }
+    if (begin >= r.length) return;
+    const uint64_t n = r.length - begin < SGLKV_REQUEST_CHUNK ? r.length - begin : SGLKV_REQUEST_CHUNK;
+    sglkv_gsrc *s = reinterpret_cast<sglkv_gsrc *>(r.source + begin);
+    sglkv_gdst *d = reinterpret_cast<sglkv_gdst *>(target + begin);
+    if (((r.source | target | n) & 15u) == 0) {
+        typedef __attribute__((address_space(1))) const sglkv_v4u gload_t;
+        typedef __attribute__((address_space(1))) sglkv_v4u gstore_t;
+        gload_t *sv = reinterpret_cast<gload_t *>(s);
+        gstore_t *dv = reinterpret_cast<gstore_t *>(d);
+        const uint32_t vecs = static_cast<uint32_t>(n / 16);
+        constexpr uint32_t U = 8;
+        for (uint32_t base = threadIdx.x; base < vecs; base += U * SGLKV_BLOCK_THREADS) {
+            sglkv_v4u buf[U];
+#pragma unroll
+            for (uint32_t k = 0; k < U; ++k) {
+                const uint32_t v = base + k * SGLKV_BLOCK_THREADS;
+                if (v < vecs) buf[k] = __builtin_nontemporal_load(sv + v);
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < U; ++k) {
+                const uint32_t v = base + k * SGLKV_BLOCK_THREADS;
+                if (v < vecs) __builtin_nontemporal_store(buf[k], dv + v);
+            }
+        }
+    } else {
+        for (uint64_t i = threadIdx.x; i < n; i += SGLKV_BLOCK_THREADS) d[i] = s[i];
+    }
+}

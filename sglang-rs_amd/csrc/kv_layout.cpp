@@ -82,6 +82,16 @@ extern "C" const char *sgl_kv_status_name(int32_t code) {
     case SGL_KV_PLAN_NON_CONTIGUOUS_CACHE_SLOTS: return "NonContiguousCacheSlots";
     case SGL_KV_DEVICE_PAGE_INDEX_OUT_OF_RANGE: return "DevicePageIndexOutOfRange";
     case SGL_KV_DEVICE_SPAN_OUT_OF_RANGE: return "DeviceSpanOutOfRange";
+    case SGL_KV_DEVICE_REQUEST_OUT_OF_RANGE: return "DeviceRequestOutOfRange";
+    case SGL_KV_REQ_ZERO_PAGE_SIZE: return "ZeroPageSize";
+    case SGL_KV_REQ_ZERO_REMOTE_ITEM_SIZE: return "ZeroRemoteKvItemSize";
+    case SGL_KV_REQ_MISSING_REMOTE_POINTERS: return "MissingRemoteKvPointers";
+    case SGL_KV_REQ_SPAN_PAGE_COUNT_MISMATCH: return "SpanPageCountMismatch";
+    case SGL_KV_REQ_REMOTE_INDEX_COUNT_MISMATCH: return "RemoteKvIndexCountMismatch";
+    case SGL_KV_REQ_REMOTE_ITEM_LAYOUT_MISMATCH: return "RemoteKvItemLayoutMismatch";
+    case SGL_KV_REQ_NEGATIVE_REMOTE_INDEX: return "NegativeRemoteKvIndex";
+    case SGL_KV_REQ_ADDRESS_OVERFLOW: return "AddressOverflow";
+    case SGL_KV_REQ_OFFSET_OVERFLOW: return "OffsetOverflow";
     default: return "Unknown";
     }
 }
@@ -547,5 +557,126 @@ extern "C" int32_t sgl_kv_pool_view_for_layer(const sgl_kv_paged_layout *layout,
     v.heads = (uint32_t)heads;
     v.head_layout = head_layout;
     *out = v;
+    return ok();
+}
+
+// --- PD page-request descriptors (crates/sglang-srt/src/transfer.rs:1945-2090) ---
+
+static int32_t span_pages_match(uint64_t token_count, uint64_t page_size, uint64_t page_count) {
+    // token_count.div_ceil(page_size) == page_indices.len()
+    const uint64_t expected = token_count / page_size + (token_count % page_size ? 1 : 0);
+    if (expected != page_count)
+        return fail(SGL_KV_REQ_SPAN_PAGE_COUNT_MISMATCH, nullptr, expected, page_count, 0,
+                    "KV transfer span requires %llu physical pages but has %llu source page "
+                    "indices",
+                    (unsigned long long)expected, (unsigned long long)page_count);
+    return SGL_KV_OK;
+}
+
+static int32_t address_overflow() {
+    return fail(SGL_KV_REQ_ADDRESS_OVERFLOW, nullptr, 0, 0, 0, "Mooncake source address overflowed");
+}
+
+static int32_t offset_overflow() {
+    return fail(SGL_KV_REQ_OFFSET_OVERFLOW, nullptr, 0, 0, 0, "Mooncake target offset overflowed");
+}
+
+extern "C" int32_t sgl_kv_build_page_requests(uint64_t source_base_addr, uint64_t page_size_bytes,
+                                              uint64_t target_base_offset, uint64_t token_offset,
+                                              uint64_t token_count, uint64_t page_size,
+                                              const uint64_t *page_indices, uint64_t page_count,
+                                              sgl_kv_page_request *out, uint64_t out_capacity,
+                                              uint64_t *out_len) {
+    if (!out_len) return fail(SGL_KV_INVALID_ARGUMENT, "out_len", 0, 0, 0, "null argument");
+    *out_len = 0;
+    if (page_size_bytes == 0)
+        return fail(SGL_KV_REQ_ZERO_PAGE_SIZE, nullptr, 0, 0, 0, "Mooncake KV page size must be non-zero");
+    if (page_size == 0)
+        return fail(SGL_KV_PLAN_ZERO_PAGE_SIZE, nullptr, 0, 0, 0, "KV transfer page size must be non-zero");
+    int32_t rc = span_pages_match(token_count, page_size, page_count);
+    if (rc) return rc;
+    if (page_count && (!page_indices || !out))
+        return fail(SGL_KV_INVALID_ARGUMENT, "page_indices/out", 0, 0, 0, "null argument");
+    if (out_capacity < page_count)
+        return fail(SGL_KV_INVALID_ARGUMENT, "out_capacity", out_capacity, page_count, 0,
+                    "%llu request slots for %llu pages", (unsigned long long)out_capacity,
+                    (unsigned long long)page_count);
+    const uint64_t page_offset = token_offset / page_size;  // KvCacheTransferSpan::page_offset
+    for (uint64_t i = 0; i < page_count; ++i) {
+        uint64_t src, tgt_page, tgt;
+        if (mul_ovf(page_indices[i], page_size_bytes, &src) || add_ovf(source_base_addr, src, &src))
+            return address_overflow();
+        if (add_ovf(page_offset, i, &tgt_page) || mul_ovf(tgt_page, page_size_bytes, &tgt) ||
+            add_ovf(target_base_offset, tgt, &tgt))
+            return offset_overflow();
+        out[i].source = src;
+        out[i].target_offset = tgt;
+        out[i].length = page_size_bytes;
+    }
+    *out_len = page_count;
+    return ok();
+}
+
+extern "C" int32_t sgl_kv_build_remote_page_requests(
+    uint64_t source_base_addr, uint64_t page_size_bytes, uint64_t token_count, uint64_t page_size,
+    const uint64_t *page_indices, uint64_t page_count, const uint64_t *dst_kv_ptrs,
+    uint64_t ptr_count, const int32_t *dst_kv_indices, uint64_t index_count,
+    uint64_t dst_kv_item_len, sgl_kv_page_request *out, uint64_t out_capacity, uint64_t *out_len) {
+    if (!out_len) return fail(SGL_KV_INVALID_ARGUMENT, "out_len", 0, 0, 0, "null argument");
+    *out_len = 0;
+    if (page_size_bytes == 0)
+        return fail(SGL_KV_REQ_ZERO_PAGE_SIZE, nullptr, 0, 0, 0, "Mooncake KV page size must be non-zero");
+    if (dst_kv_item_len == 0)
+        return fail(SGL_KV_REQ_ZERO_REMOTE_ITEM_SIZE, nullptr, 0, 0, 0,
+                    "Mooncake remote KV item size must be non-zero");
+    if (ptr_count == 0)
+        return fail(SGL_KV_REQ_MISSING_REMOTE_POINTERS, nullptr, 0, 0, 0,
+                    "Mooncake remote KV pointers must not be empty");
+    if (page_size == 0)
+        return fail(SGL_KV_PLAN_ZERO_PAGE_SIZE, nullptr, 0, 0, 0, "KV transfer page size must be non-zero");
+    int32_t rc = span_pages_match(token_count, page_size, page_count);
+    if (rc) return rc;
+    if (page_count != index_count)
+        return fail(SGL_KV_REQ_REMOTE_INDEX_COUNT_MISMATCH, nullptr, page_count, index_count, 0,
+                    "KV transfer span has %llu source pages but %llu remote KV indices",
+                    (unsigned long long)page_count, (unsigned long long)index_count);
+    uint64_t split;
+    if (mul_ovf(dst_kv_item_len, ptr_count, &split)) return address_overflow();
+    if (split != page_size_bytes)
+        return fail(SGL_KV_REQ_REMOTE_ITEM_LAYOUT_MISMATCH, nullptr, page_size_bytes, split, 0,
+                    "Mooncake remote KV item layout splits a %llu-byte page into %llu bytes",
+                    (unsigned long long)page_size_bytes, (unsigned long long)split);
+    if (page_count && (!page_indices || !dst_kv_indices || !dst_kv_ptrs || !out))
+        return fail(SGL_KV_INVALID_ARGUMENT, "page_indices/dst_kv_indices/dst_kv_ptrs/out", 0, 0, 0,
+                    "null argument");
+    uint64_t need;
+    if (mul_ovf(page_count, ptr_count, &need) || out_capacity < need)
+        return fail(SGL_KV_INVALID_ARGUMENT, "out_capacity", out_capacity, need, 0,
+                    "%llu request slots for %llu pages x %llu pointers",
+                    (unsigned long long)out_capacity, (unsigned long long)page_count,
+                    (unsigned long long)ptr_count);
+    uint64_t n = 0;
+    for (uint64_t i = 0; i < page_count; ++i) {
+        const int32_t index = dst_kv_indices[i];
+        if (index < 0)
+            return fail(SGL_KV_REQ_NEGATIVE_REMOTE_INDEX, nullptr, (uint64_t)(int64_t)index, 0, 0,
+                        "Mooncake remote KV index %d is negative", index);
+        uint64_t page_addr;
+        if (mul_ovf(page_indices[i], page_size_bytes, &page_addr) ||
+            add_ovf(source_base_addr, page_addr, &page_addr))
+            return address_overflow();
+        for (uint64_t j = 0; j < ptr_count; ++j) {
+            uint64_t src, tgt;
+            if (mul_ovf(j, dst_kv_item_len, &src) || add_ovf(page_addr, src, &src))
+                return address_overflow();
+            if (mul_ovf((uint64_t)index, dst_kv_item_len, &tgt) || add_ovf(dst_kv_ptrs[j], tgt, &tgt))
+                return offset_overflow();
+            out[n].source = src;
+            out[n].target_offset = tgt;
+            out[n].length = dst_kv_item_len;
+            ++n;
+        }
+    }
+    *out_len = n;
     return ok();
 }

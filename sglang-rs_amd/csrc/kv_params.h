@@ -53,6 +53,7 @@
 #define SGLKV_FLAG_SLOT 1u /* a slot map entry >= slot_count (reference flag value) */
 #define SGLKV_FLAG_PAGE 2u /* a page-table entry out of range while resolving spans */
 #define SGLKV_FLAG_SPAN 4u /* a row not covered by any span */
+#define SGLKV_FLAG_REQUEST 8u /* a page request outside its source or target region */
 
 /* A resolved row offset that must not be touched. */
 #define SGLKV_INVALID_OFFSET 0xFFFFFFFFFFFFFFFFull
@@ -107,5 +108,26 @@ typedef struct sglkv_resolve_params {
     uint32_t rows;
     uint32_t reserved;
 } sglkv_resolve_params;
+
+/* Page-request execution: request i copies length_i bytes from source_i to
+ * target_base + target_offset_i. Workgroup b handles chunk b % chunks of
+ * request b / chunks (chunk = SGLKV_REQUEST_CHUNK bytes). */
+#define SGLKV_REQUEST_CHUNK 65536u
+
+typedef struct sglkv_request {
+    uint64_t source;
+    uint64_t target_offset;
+    uint64_t length;
+} sglkv_request;
+
+typedef struct sglkv_request_params {
+    const sglkv_request *requests;
+    uint32_t *flag;
+    uint64_t count;
+    uint64_t chunks;        /* chunks per request (of the longest request) */
+    uint64_t target_base;   /* added to every target_offset (0: offsets are addresses) */
+    uint64_t source_lo, source_hi;   /* allowed source bytes [lo, hi) */
+    uint64_t target_lo, target_hi;   /* allowed target bytes [lo, hi) */
+} sglkv_request_params;
 
 #endif

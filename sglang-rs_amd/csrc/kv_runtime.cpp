@@ -377,6 +377,7 @@ extern "C" int32_t sgl_rocm_kv_init(int32_t device, const char *code_object_path
         }
     err = hipModuleGetFunction(&ctx->resolve, ctx->module, "sglkv_resolve_spans");
     if (err == hipSuccess) err = hipModuleGetFunction(&ctx->fill, ctx->module, "sglkv_fill_synthetic");
+    if (err == hipSuccess) err = hipModuleGetFunction(&ctx->requests, ctx->module, "sglkv_copy_requests");
     if (err == hipSuccess) err = hipDeviceGetAttribute(&ctx->cu_count, hipDeviceAttributeMultiprocessorCount, device);
     // The tile constants the kernels were compiled with.
     const char *const constants[2] = {"sglkv_rows_per_thread", "sglkv_max_tile_rows"};
@@ -703,6 +704,9 @@ extern "C" int32_t sgl_rocm_kv_check_errors(sgl_rocm_kv_ctx *ctx, void *stream) 
     if (flag & SGLKV_FLAG_SPAN)
         return fail(SGL_KV_DEVICE_SPAN_OUT_OF_RANGE, nullptr, 0, flag, 0,
                     "KV transfer row is not covered by any span");
+    if (flag & SGLKV_FLAG_REQUEST)
+        return fail(SGL_KV_DEVICE_REQUEST_OUT_OF_RANGE, nullptr, 0, flag, 0,
+                    "KV page request lies outside its source or target region");
     return ok();
 }
 
@@ -727,6 +731,48 @@ extern "C" int32_t sgl_rocm_kv_fill_synthetic(sgl_rocm_kv_ctx *ctx, const sgl_kv
     void *ptr = buffer->ptr;
     void *args[] = {&ptr, &words, &seed, &kind};
     SGLKV_HIP(hipModuleLaunchKernel(ctx->fill, (unsigned)blocks, 1, 1, SGLKV_BLOCK_THREADS, 1, 1, 0,
+                                    static_cast<hipStream_t>(stream), args, nullptr));
+    return ok();
+}
+
+extern "C" int32_t sgl_rocm_kv_execute_page_requests(sgl_rocm_kv_ctx *ctx,
+                                                     const sgl_kv_device_buffer *requests,
+                                                     uint64_t count, uint64_t max_length,
+                                                     const sgl_kv_device_buffer *source_region,
+                                                     const sgl_kv_device_buffer *target_region,
+                                                     uint32_t offsets_are_addresses, void *stream) {
+    int32_t rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (count == 0) return ok();
+    if (!requests || !requests->ptr || !source_region || !source_region->ptr || !target_region ||
+        !target_region->ptr)
+        return fail(SGL_KV_INVALID_ARGUMENT, "requests/source_region/target_region", 0, 0, 0,
+                    "null buffer");
+    static_assert(sizeof(sgl_kv_page_request) == sizeof(sglkv_request), "request layouts differ");
+    uint64_t need;
+    if (mul_ovf(count, sizeof(sglkv_request), &need)) return shape_overflow();
+    if (need > requests->byte_len) return out_of_bounds("requests", 0, need, requests->byte_len);
+    if (max_length == 0) return fail(SGL_KV_ZERO_DIMENSION, "max_length", 0, 0, 0,
+                                     "KV copy dimension max_length must be non-zero");
+    const uint64_t chunks = max_length / SGLKV_REQUEST_CHUNK + (max_length % SGLKV_REQUEST_CHUNK ? 1 : 0);
+    uint64_t grid;
+    if (mul_ovf(count, chunks, &grid) || grid > INT32_MAX) return too_large("grid blocks", grid, INT32_MAX);
+    sglkv_request_params p;
+    memset(&p, 0, sizeof p);
+    p.requests = static_cast<const sglkv_request *>(requests->ptr);
+    p.flag = ctx->flag;
+    p.count = count;
+    p.chunks = chunks;
+    p.source_lo = (uint64_t)(uintptr_t)source_region->ptr;
+    p.target_lo = (uint64_t)(uintptr_t)target_region->ptr;
+    if (add_ovf(p.source_lo, source_region->byte_len, &p.source_hi) ||
+        add_ovf(p.target_lo, target_region->byte_len, &p.target_hi))
+        return shape_overflow();
+    p.target_base = offsets_are_addresses ? 0 : p.target_lo;
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    void *args[] = {&p};
+    SGLKV_HIP(hipModuleLaunchKernel(ctx->requests, (unsigned)grid, 1, 1, SGLKV_BLOCK_THREADS, 1, 1, 0,
                                     static_cast<hipStream_t>(stream), args, nullptr));
     return ok();
 }

@@ -69,6 +69,7 @@ PLAN_UNALIGNED_CACHE_SLOT = 44
 PLAN_NON_CONTIGUOUS_CACHE_SLOTS = 45
 DEVICE_PAGE_INDEX_OUT_OF_RANGE = 50
 DEVICE_SPAN_OUT_OF_RANGE = 51
+DEVICE_REQUEST_OUT_OF_RANGE = 52
 
 DTYPES = {"auto": 0, "float32": 1, "bf16": 2, "bfloat16": 2, "fp8_e4m3": 3, "fp8_e5m2": 4,
           "fp4_e2m1": 5}
@@ -157,6 +158,9 @@ class _PipelineDesc(ctypes.Structure):
                 ("host", ctypes.c_void_p * 2), ("host_bytes", _u64)]
 
 
+PAGE_REQUEST_DTYPE = np.dtype([("source", "<u8"), ("target_offset", "<u8"), ("length", "<u8")])
+
+
 SPAN_DTYPE = np.dtype([("row_start", "<u4"), ("token_offset", "<u4"), ("token_count", "<u4"),
                        ("page_table_start", "<u4")])
 
@@ -191,6 +195,13 @@ _EXPORTS = {
     "sgl_kv_pool_view_for_layer": (
         ctypes.c_int32, [ctypes.POINTER(_PagedLayout), ctypes.c_void_p, _u64, ctypes.c_uint32,
                          _u64, _u64, _u64, _u64, ctypes.POINTER(PoolView)]),
+    "sgl_kv_build_page_requests": (
+        ctypes.c_int32, [_u64, _u64, _u64, _u64, _u64, _u64, ctypes.POINTER(_u64), _u64,
+                         ctypes.c_void_p, _u64, ctypes.POINTER(_u64)]),
+    "sgl_kv_build_remote_page_requests": (
+        ctypes.c_int32, [_u64, _u64, _u64, _u64, ctypes.POINTER(_u64), _u64, ctypes.POINTER(_u64),
+                         _u64, ctypes.POINTER(ctypes.c_int32), _u64, _u64, ctypes.c_void_p, _u64,
+                         ctypes.POINTER(_u64)]),
     "sgl_rocm_kv_init": (ctypes.c_int32, [ctypes.c_int32, ctypes.c_char_p,
                                           ctypes.POINTER(ctypes.c_void_p)]),
     "sgl_rocm_kv_destroy": (ctypes.c_int32, [ctypes.c_void_p]),
@@ -234,6 +245,11 @@ _EXPORTS = {
                                                           ctypes.POINTER(ctypes.c_float)]),
     "sgl_rocm_kv_pipeline_elapsed": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_float)]),
     "sgl_rocm_kv_pipeline_destroy": (ctypes.c_int32, [ctypes.c_void_p]),
+    "sgl_rocm_kv_execute_page_requests": (ctypes.c_int32, [ctypes.c_void_p,
+                                                           ctypes.POINTER(_DeviceBuffer), _u64, _u64,
+                                                           ctypes.POINTER(_DeviceBuffer),
+                                                           ctypes.POINTER(_DeviceBuffer),
+                                                           ctypes.c_uint32, ctypes.c_void_p]),
     "sgl_rocm_kv_fill_synthetic": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_DeviceBuffer),
                                                     _u64, ctypes.c_uint32, ctypes.c_void_p]),
 }
@@ -443,6 +459,35 @@ def transfer_page_indices(request_index: int, token_offset: int, cache_slots, pa
     return out[: n.value].tolist()
 
 
+def build_page_requests(source_base_addr: int, page_size_bytes: int, target_base_offset: int,
+                        token_offset: int, token_count: int, page_size: int, page_indices):
+    """build_mooncake_kv_transfer_requests (transfer.rs:1945-1997): one page
+    write per source page; returns a PAGE_REQUEST_DTYPE array."""
+    pages = _u64_array(page_indices)
+    out = np.zeros(max(1, len(pages)), dtype=PAGE_REQUEST_DTYPE)
+    n = _u64()
+    _call(lib().sgl_kv_build_page_requests, source_base_addr, page_size_bytes, target_base_offset,
+          token_offset, token_count, page_size, _pu64(pages), len(pages), out.ctypes.data, len(out),
+          ctypes.byref(n))
+    return out[: n.value]
+
+
+def build_remote_page_requests(source_base_addr: int, page_size_bytes: int, token_count: int,
+                               page_size: int, page_indices, dst_kv_ptrs, dst_kv_indices,
+                               dst_kv_item_len: int):
+    """build_mooncake_remote_kv_transfer_requests (transfer.rs:1999-2090): every
+    source page split into len(dst_kv_ptrs) writes of dst_kv_item_len bytes."""
+    pages, ptrs = _u64_array(page_indices), _u64_array(dst_kv_ptrs)
+    idx = np.ascontiguousarray(np.asarray(dst_kv_indices, dtype=np.int32))
+    out = np.zeros(max(1, len(pages) * max(1, len(ptrs))), dtype=PAGE_REQUEST_DTYPE)
+    n = _u64()
+    _call(lib().sgl_kv_build_remote_page_requests, source_base_addr, page_size_bytes, token_count,
+          page_size, _pu64(pages), len(pages), _pu64(ptrs), len(ptrs),
+          idx.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), len(idx), dst_kv_item_len,
+          out.ctypes.data, len(out), ctypes.byref(n))
+    return out[: n.value]
+
+
 # --- group 2: device calls -------------------------------------------------------------------
 
 def device_buffer(ptr: int, byte_len: int) -> _DeviceBuffer:
@@ -585,6 +630,14 @@ class RocmKvPairCopyKernels:
         _call(lib().sgl_rocm_kv_resolve_spans, self._h, page_size, page_count,
               ctypes.byref(spans), span_count, ctypes.byref(page_table), page_table_len,
               row_count, ctypes.byref(out_slots), _stream(stream))
+
+    def execute_page_requests(self, requests: _DeviceBuffer, count: int, max_length: int,
+                              source_region: _DeviceBuffer, target_region: _DeviceBuffer,
+                              offsets_are_addresses: bool = False, stream=None):
+        """Page requests (PAGE_REQUEST_DTYPE, on the device) as device copies."""
+        _call(lib().sgl_rocm_kv_execute_page_requests, self._h, ctypes.byref(requests), count,
+              max_length, ctypes.byref(source_region), ctypes.byref(target_region),
+              int(offsets_are_addresses), _stream(stream))
 
     def check_errors(self, stream=None):
         _call(lib().sgl_rocm_kv_check_errors, self._h, _stream(stream))

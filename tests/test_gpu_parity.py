@@ -663,3 +663,90 @@ def test_random_shapes_pack_unpack_transfer(k, seed):
     k.check_errors()
     oracle.transfer(_opool(sspec, sh, layer2), src_h, ss, _opool(dspec, sh, layer2), dst2_h, ds)
     np.testing.assert_array_equal(dst2.download(), dst2_h)
+
+
+# --- page-request execution (the reference's page-for-page PD transfer) ------------------------------
+
+@pytest.mark.parametrize("page_bytes,pages", [(3072, 40), (100, 17), (8 << 20, 6)])
+def test_execute_page_requests_local(k, page_bytes, pages):
+    """build_page_requests -> device copies: target page page_offset + i of the
+    destination segment receives source page page_indices[i]."""
+    rng = np.random.default_rng(page_bytes)
+    src_pages, page_size = pages * 3, 4
+    src_h = rng.integers(0, 256, src_pages * page_bytes, dtype=np.uint8)
+    src = hip.DeviceBuffer.from_array(src_h)
+    target_base_offset, token_offset = 2 * page_bytes, 8
+    dst_bytes = target_base_offset + (token_offset // page_size + pages) * page_bytes
+    dst_h = rng.integers(0, 256, dst_bytes, dtype=np.uint8)
+    dst = hip.DeviceBuffer.from_array(dst_h)
+    page_indices = rng.permutation(src_pages)[:pages]
+    reqs = kv.build_page_requests(src.ptr, page_bytes, target_base_offset, token_offset,
+                                  pages * page_size - 1, page_size, page_indices)
+    rq = hip.DeviceBuffer.from_array(reqs)
+    k.execute_page_requests(_db(rq), len(reqs), page_bytes, _db(src), _db(dst))
+    k.check_errors()
+    want = dst_h.copy()
+    for i, p in enumerate(page_indices):
+        t0 = target_base_offset + (token_offset // page_size + i) * page_bytes
+        want[t0:t0 + page_bytes] = src_h[p * page_bytes:(p + 1) * page_bytes]
+    np.testing.assert_array_equal(dst.download(), want)
+
+
+def test_execute_remote_page_requests_split_over_pointers(k):
+    """The decode side advertises 4 per-split regions (dst_kv_ptrs) of one
+    device buffer; each source page lands split by split at its index."""
+    rng = np.random.default_rng(7)
+    PB, J, pages, slots = 8192, 4, 33, 50
+    item = PB // J
+    src_h = rng.integers(0, 256, 80 * PB, dtype=np.uint8)
+    src = hip.DeviceBuffer.from_array(src_h)
+    dst = hip.DeviceBuffer(J * slots * item)
+    dst.fill(0)
+    ptrs = [dst.ptr + j * slots * item for j in range(J)]
+    page_indices = rng.permutation(80)[:pages]
+    dst_idx = rng.permutation(slots)[:pages].astype(np.int32)
+    reqs = kv.build_remote_page_requests(src.ptr, PB, pages, 1, page_indices, ptrs, dst_idx, item)
+    rq = hip.DeviceBuffer.from_array(reqs)
+    k.execute_page_requests(_db(rq), len(reqs), item, _db(src), _db(dst), offsets_are_addresses=True)
+    k.check_errors()
+    got = dst.download().reshape(J, slots, item)
+    for i, p in enumerate(page_indices):
+        np.testing.assert_array_equal(got[:, dst_idx[i], :], src_h[p * PB:(p + 1) * PB].reshape(J, item))
+
+
+def test_execute_page_requests_skips_and_reports_out_of_region(k):
+    rng = np.random.default_rng(9)
+    PB = 4096
+    src_h = rng.integers(0, 256, 8 * PB, dtype=np.uint8)
+    src = hip.DeviceBuffer.from_array(src_h)
+    dst = hip.DeviceBuffer(8 * PB)
+    dst.fill(0)
+    reqs = kv.build_page_requests(src.ptr, PB, 0, 0, 3, 1, [1, 7, 2])
+    reqs[1]["source"] = src.ptr + 8 * PB          # past the source region
+    bad_target = reqs.copy()
+    bad_target[0]["target_offset"] = 8 * PB - 16  # runs past the target region
+    rq = hip.DeviceBuffer.from_array(reqs)
+    k.execute_page_requests(_db(rq), 3, PB, _db(src), _db(dst))
+    with pytest.raises(kv.KvError) as ei:
+        k.check_errors()
+    assert ei.value.variant == "DeviceRequestOutOfRange"
+    got = dst.download()
+    np.testing.assert_array_equal(got[:PB], src_h[PB:2 * PB])
+    assert not got[PB:2 * PB].any()
+    np.testing.assert_array_equal(got[2 * PB:3 * PB], src_h[2 * PB:3 * PB])
+    rq.upload(bad_target)
+    k.execute_page_requests(_db(rq), 3, PB, _db(src), _db(dst))
+    with pytest.raises(kv.KvError):
+        k.check_errors()
+    # a request longer than the launch's max_length covers is skipped, not cut
+    big_h = rng.integers(0, 256, 1 << 17, dtype=np.uint8)
+    big, big_dst = hip.DeviceBuffer.from_array(big_h), hip.DeviceBuffer(1 << 17)
+    big_dst.fill(0)
+    one = hip.DeviceBuffer.from_array(kv.build_page_requests(big.ptr, 1 << 17, 0, 0, 1, 1, [0]))
+    k.execute_page_requests(_db(one), 1, 1 << 16, _db(big), _db(big_dst))
+    with pytest.raises(kv.KvError):
+        k.check_errors()
+    assert not big_dst.download().any()
+    k.execute_page_requests(_db(one), 1, 1 << 17, _db(big), _db(big_dst))
+    k.check_errors()
+    np.testing.assert_array_equal(big_dst.download(), big_h)

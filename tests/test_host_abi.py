@@ -241,3 +241,72 @@ def test_synthetic_words_is_splitmix64():
     got = kv.synthetic_words(0, np.arange(3))
     assert [hex(int(x)) for x in got] == ["0xe220a8397b1dcdaf", "0x6e789e6aa1b965f4",
                                           "0x6c45d188009454f"]
+
+
+# --- PD page-request descriptors (crates/sglang-srt/src/transfer.rs:1945-2090) ------------------
+
+def test_remote_page_requests_golden(goldens):
+    """crates/sglang-srt/tests/http_server.rs:2826-2833: a two-token prefill
+    (page size 1) to a decode side advertising dst_kv_ptrs [0x9000],
+    dst_kv_indices [4, 5], item length 128 -> target offsets 0x9000 + 4*128
+    and 0x9000 + 5*128."""
+    g = goldens["mooncake_remote_offsets"]
+    reqs = kv.build_remote_page_requests(0x2000, g["item_len"], 2, 1, [0, 1], [g["dst_base"]],
+                                         g["dst_kv_indices"], g["item_len"])
+    assert list(reqs["target_offset"]) == g["target_offsets"]
+    assert list(reqs["length"]) == [g["item_len"]] * 2
+    assert list(reqs["source"]) == [0x2000, 0x2000 + g["item_len"]]
+
+
+def test_page_requests_follow_the_span_page_offset():
+    # token_offset 8 with page size 4 -> the span starts at target page 2
+    reqs = kv.build_page_requests(0x1000, 256, 0x40000, 8, 6, 4, [7, 3])
+    assert list(reqs["source"]) == [0x1000 + 7 * 256, 0x1000 + 3 * 256]
+    assert list(reqs["target_offset"]) == [0x40000 + 2 * 256, 0x40000 + 3 * 256]
+
+
+def test_remote_page_requests_place_every_split_of_every_page():
+    """Execute the requests as byte copies on host buffers: split j of source
+    page i must land at index dst_kv_indices[i] of decode buffer j."""
+    rng = np.random.default_rng(2)
+    PB, J, pages = 384, 3, 9
+    item = PB // J
+    base = 0x10_0000
+    src = rng.integers(0, 256, 64 * PB, dtype=np.uint8)
+    page_indices = rng.permutation(64)[:pages]
+    dst_idx = rng.permutation(40)[:pages].astype(np.int32)
+    ptrs = [0x4000_0000 + j * 0x100_0000 for j in range(J)]
+    reqs = kv.build_remote_page_requests(base, PB, pages * 16 - 5, 16, page_indices, ptrs, dst_idx,
+                                         item)
+    assert len(reqs) == pages * J
+    targets = [np.zeros(40 * item, np.uint8) for _ in range(J)]
+    for r in reqs:
+        j = max(i for i, p in enumerate(ptrs) if p <= r["target_offset"])
+        off = int(r["target_offset"]) - ptrs[j]
+        s0 = int(r["source"]) - base
+        targets[j][off: off + int(r["length"])] = src[s0: s0 + int(r["length"])]
+    for i, p in enumerate(page_indices):
+        page = src[p * PB:(p + 1) * PB].reshape(J, item)
+        for j in range(J):
+            np.testing.assert_array_equal(targets[j][dst_idx[i] * item:(dst_idx[i] + 1) * item], page[j])
+
+
+@pytest.mark.parametrize("args,variant,fields", [
+    ((0x1000, 0, 2, 1, [0, 1], [0x9000], [4, 5], 128), "ZeroPageSize", None),
+    ((0x1000, 128, 2, 1, [0, 1], [0x9000], [4, 5], 0), "ZeroRemoteKvItemSize", None),
+    ((0x1000, 128, 2, 1, [0, 1], [], [4, 5], 128), "MissingRemoteKvPointers", None),
+    ((0x1000, 128, 3, 2, [0], [0x9000], [4], 128), "SpanPageCountMismatch", (2, 1)),
+    ((0x1000, 128, 2, 1, [0, 1], [0x9000], [4], 128), "RemoteKvIndexCountMismatch", (2, 1)),
+    ((0x1000, 128, 2, 1, [0, 1], [0x9000, 0xA000], [4, 5], 128), "RemoteKvItemLayoutMismatch", (128, 256)),
+    ((0x1000, 128, 2, 1, [0, 1], [0x9000], [4, -1], 128), "NegativeRemoteKvIndex", None),
+    ((0x1000, 128, 1, 1, [2**60], [0x9000], [4], 128), "AddressOverflow", None),
+    ((0x1000, 128, 1, 1, [0], [2**64 - 64], [4], 128), "OffsetOverflow", None),
+])
+def test_remote_page_request_errors(args, variant, fields):
+    with pytest.raises(kv.KvError) as ei:
+        kv.build_remote_page_requests(*args)
+    assert ei.value.variant == variant
+    if fields:
+        assert ei.value.fields[:2] == fields
+    if variant == "NegativeRemoteKvIndex":
+        assert ei.value.fields[0] == 2**64 - 1

@@ -106,7 +106,13 @@ typedef enum sgl_kv_status {
     SGL_KV_REQ_REMOTE_ITEM_LAYOUT_MISMATCH = 65,/* a = page_size_bytes, b = split_page_size */
     SGL_KV_REQ_NEGATIVE_REMOTE_INDEX = 66,      /* a = the index (as int64) */
     SGL_KV_REQ_ADDRESS_OVERFLOW = 67,
-    SGL_KV_REQ_OFFSET_OVERFLOW = 68
+    SGL_KV_REQ_OFFSET_OVERFLOW = 68,
+
+    /* 70.. mirror CacheAllocationError (crates/sglang-srt/src/cache.rs:63-74) */
+    SGL_KV_ALLOC_ZERO_PAGE_SIZE = 70,
+    SGL_KV_ALLOC_ZERO_SLOT_CAPACITY = 71,
+    SGL_KV_ALLOC_SLOT_CAPACITY_NOT_PAGE_ALIGNED = 72, /* a = slot_capacity, b = page_size */
+    SGL_KV_ALLOC_OUT_OF_SLOTS = 73                    /* a = requested, b = available */
 } sgl_kv_status;
 
 /* Detail of the calling thread's most recent failure. */
@@ -265,6 +271,45 @@ int32_t sgl_kv_build_remote_page_requests(uint64_t source_base_addr, uint64_t pa
                                           const int32_t *dst_kv_indices, uint64_t index_count,
                                           uint64_t dst_kv_item_len, sgl_kv_page_request *out,
                                           uint64_t out_capacity, uint64_t *out_len);
+
+/* KV page allocator (CachePageAllocator, crates/sglang-srt/src/cache.rs:
+ * 340-473): the producer of the slot indices every copy call takes. Pages
+ * are handed out from the front of a free list; released pages return to
+ * its front in release order. Not thread-safe (the reference takes &mut). */
+typedef struct sgl_kv_page_allocator sgl_kv_page_allocator;
+/* CachePageAllocator::with_page_size (cache.rs:353-376). */
+int32_t sgl_kv_page_allocator_new(uint64_t slot_capacity, uint64_t page_size,
+                                  sgl_kv_page_allocator **out);
+int32_t sgl_kv_page_allocator_destroy(sgl_kv_page_allocator *allocator);
+uint64_t sgl_kv_page_allocator_available_pages(const sgl_kv_page_allocator *allocator);
+uint64_t sgl_kv_page_allocator_available_slots(const sgl_kv_page_allocator *allocator);
+/* CachePageAllocator::allocate_for_sequence (cache.rs:397-447): writes
+ * slot_count slots to out_slots, first the free tail of the sequence's last
+ * page, then whole new pages. OutOfSlots leaves the allocator unchanged.
+ * sequence_len 0 is CachePageAllocator::allocate. */
+int32_t sgl_kv_page_allocator_allocate_for_sequence(sgl_kv_page_allocator *allocator,
+                                                    const uint64_t *sequence_slots,
+                                                    uint64_t sequence_len, uint64_t slot_count,
+                                                    uint64_t *out_slots);
+/* CachePageAllocator::release (cache.rs:449-466). */
+int32_t sgl_kv_page_allocator_release(sgl_kv_page_allocator *allocator, const uint64_t *cache_pages,
+                                      uint64_t count);
+/* CachePageAllocator::reset (cache.rs:468-471). */
+int32_t sgl_kv_page_allocator_reset(sgl_kv_page_allocator *allocator);
+
+/* KvCacheTransferSpan::descriptor_checksum (transfer.rs:548-570): lowercase
+ * hex SHA-256 of the span's identifying fields, as /poll_transfers reports
+ * it. Strings are (pointer, length) byte strings. */
+int32_t sgl_kv_transfer_span_checksum(const char *request_id, uint64_t request_id_len,
+                                      const char *bootstrap_host, uint64_t bootstrap_host_len,
+                                      uint16_t bootstrap_port, uint64_t bootstrap_room,
+                                      int32_t data_parallel_rank, uint64_t token_offset,
+                                      uint64_t token_count, uint64_t page_size,
+                                      const uint64_t *cache_pages, uint64_t cache_page_count,
+                                      const uint64_t *page_indices, uint64_t page_index_count,
+                                      char out_hex[65]);
+/* SHA-256 (FIPS 180-4) of `len` bytes as lowercase hex; the checksum's hash. */
+int32_t sgl_kv_sha256_hex(const void *data, uint64_t len, char out_hex[65]);
 
 /* ------------------------------------------------------------------------ */
 /* Group 2: kernels                                                         */

@@ -92,6 +92,10 @@ extern "C" const char *sgl_kv_status_name(int32_t code) {
     case SGL_KV_REQ_NEGATIVE_REMOTE_INDEX: return "NegativeRemoteKvIndex";
     case SGL_KV_REQ_ADDRESS_OVERFLOW: return "AddressOverflow";
     case SGL_KV_REQ_OFFSET_OVERFLOW: return "OffsetOverflow";
+    case SGL_KV_ALLOC_ZERO_PAGE_SIZE: return "ZeroPageSize";
+    case SGL_KV_ALLOC_ZERO_SLOT_CAPACITY: return "ZeroSlotCapacity";
+    case SGL_KV_ALLOC_SLOT_CAPACITY_NOT_PAGE_ALIGNED: return "SlotCapacityNotPageAligned";
+    case SGL_KV_ALLOC_OUT_OF_SLOTS: return "OutOfSlots";
     default: return "Unknown";
     }
 }

@@ -202,6 +202,19 @@ _EXPORTS = {
         ctypes.c_int32, [_u64, _u64, _u64, _u64, ctypes.POINTER(_u64), _u64, ctypes.POINTER(_u64),
                          _u64, ctypes.POINTER(ctypes.c_int32), _u64, _u64, ctypes.c_void_p, _u64,
                          ctypes.POINTER(_u64)]),
+    "sgl_kv_page_allocator_new": (ctypes.c_int32, [_u64, _u64, ctypes.POINTER(ctypes.c_void_p)]),
+    "sgl_kv_page_allocator_destroy": (ctypes.c_int32, [ctypes.c_void_p]),
+    "sgl_kv_page_allocator_available_pages": (_u64, [ctypes.c_void_p]),
+    "sgl_kv_page_allocator_available_slots": (_u64, [ctypes.c_void_p]),
+    "sgl_kv_page_allocator_allocate_for_sequence": (
+        ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_u64), _u64, _u64, ctypes.POINTER(_u64)]),
+    "sgl_kv_page_allocator_release": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_u64), _u64]),
+    "sgl_kv_page_allocator_reset": (ctypes.c_int32, [ctypes.c_void_p]),
+    "sgl_kv_transfer_span_checksum": (
+        ctypes.c_int32, [ctypes.c_char_p, _u64, ctypes.c_char_p, _u64, ctypes.c_uint16, _u64,
+                         ctypes.c_int32, _u64, _u64, _u64, ctypes.POINTER(_u64), _u64,
+                         ctypes.POINTER(_u64), _u64, ctypes.c_char_p]),
+    "sgl_kv_sha256_hex": (ctypes.c_int32, [ctypes.c_char_p, _u64, ctypes.c_char_p]),
     "sgl_rocm_kv_init": (ctypes.c_int32, [ctypes.c_int32, ctypes.c_char_p,
                                           ctypes.POINTER(ctypes.c_void_p)]),
     "sgl_rocm_kv_destroy": (ctypes.c_int32, [ctypes.c_void_p]),
@@ -486,6 +499,67 @@ def build_remote_page_requests(source_base_addr: int, page_size_bytes: int, toke
           idx.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), len(idx), dst_kv_item_len,
           out.ctypes.data, len(out), ctypes.byref(n))
     return out[: n.value]
+
+
+class CachePageAllocator:
+    """CachePageAllocator (crates/sglang-srt/src/cache.rs:340-473)."""
+
+    def __init__(self, slot_capacity: int, page_size: int = 1):
+        h = ctypes.c_void_p()
+        _call(lib().sgl_kv_page_allocator_new, slot_capacity, page_size, ctypes.byref(h))
+        self._h = h.value
+
+    with_page_size = classmethod(lambda cls, slot_capacity, page_size: cls(slot_capacity, page_size))
+
+    def available_pages(self) -> int:
+        return lib().sgl_kv_page_allocator_available_pages(self._h)
+
+    def available_slots(self) -> int:
+        return lib().sgl_kv_page_allocator_available_slots(self._h)
+
+    def allocate_for_sequence(self, sequence_slots, slot_count: int):
+        seq = _u64_array(sequence_slots)
+        out = np.zeros(max(1, slot_count), dtype=np.uint64)
+        _call(lib().sgl_kv_page_allocator_allocate_for_sequence, self._h, _pu64(seq), len(seq),
+              slot_count, _pu64(out))
+        return out[:slot_count].tolist()
+
+    def allocate(self, slot_count: int):
+        return self.allocate_for_sequence([], slot_count)
+
+    def release(self, cache_pages):
+        a = _u64_array(cache_pages)
+        _call(lib().sgl_kv_page_allocator_release, self._h, _pu64(a), len(a))
+
+    def reset(self):
+        _call(lib().sgl_kv_page_allocator_reset, self._h)
+
+    def __del__(self):
+        try:
+            if self._h:
+                lib().sgl_kv_page_allocator_destroy(self._h)
+                self._h = None
+        except Exception:
+            pass
+
+
+def transfer_span_checksum(request_id: str, bootstrap_host: str, bootstrap_port: int,
+                           bootstrap_room: int, data_parallel_rank: int, token_offset: int,
+                           token_count: int, page_size: int, cache_pages, page_indices) -> str:
+    """KvCacheTransferSpan::descriptor_checksum (transfer.rs:548-570)."""
+    rid, host = request_id.encode(), bootstrap_host.encode()
+    cp, pi = _u64_array(cache_pages), _u64_array(page_indices)
+    out = ctypes.create_string_buffer(65)
+    _call(lib().sgl_kv_transfer_span_checksum, rid, len(rid), host, len(host), bootstrap_port,
+          bootstrap_room, data_parallel_rank, token_offset, token_count, page_size, _pu64(cp),
+          len(cp), _pu64(pi), len(pi), out)
+    return out.value.decode()
+
+
+def sha256_hex(data: bytes) -> str:
+    out = ctypes.create_string_buffer(65)
+    _call(lib().sgl_kv_sha256_hex, data, len(data), out)
+    return out.value.decode()
 
 
 # --- group 2: device calls -------------------------------------------------------------------

@@ -130,6 +130,52 @@ int main() {
                                                         page_size, out.data(), &n);
         if (rc == SGL_KV_OK) CHECK(n <= cache.size());
     }
+    // Page allocator under random traffic: allocations never overlap live
+    // slots and stay in range; the allocator never leaks or double-frees.
+    for (int round = 0; round < 20; ++round) {
+        const uint64_t P = 1 + rng() % 16, pages = 1 + rng() % 64;
+        sgl_kv_page_allocator *a = nullptr;
+        CHECK(sgl_kv_page_allocator_new(P * pages, P, &a) == SGL_KV_OK);
+        std::vector<std::vector<uint64_t>> live;
+        std::vector<uint8_t> used(P * pages, 0);
+        for (int it = 0; it < 2000; ++it) {
+            if (!live.empty() && rng() % 3 == 0) {
+                const size_t v = rng() % live.size();
+                for (uint64_t slot : live[v]) used[slot] = 0;
+                CHECK(sgl_kv_page_allocator_release(a, live[v].data(), live[v].size()) == SGL_KV_OK);
+                live.erase(live.begin() + v);
+                continue;
+            }
+            const uint64_t n = 1 + rng() % (3 * P);
+            std::vector<uint64_t> out(n);
+            const int32_t rc = sgl_kv_page_allocator_allocate_for_sequence(a, nullptr, 0, n, out.data());
+            if (rc != SGL_KV_OK) {
+                CHECK(rc == SGL_KV_ALLOC_OUT_OF_SLOTS);
+                continue;
+            }
+            for (uint64_t slot : out) {
+                CHECK(slot < P * pages && !used[slot]);
+                used[slot] = 1;
+            }
+            live.push_back(out);
+        }
+        // release garbage, then everything
+        const uint64_t junk[4] = {UINT64_MAX, P * pages, 1, P * pages + P};
+        CHECK(sgl_kv_page_allocator_release(a, junk, 4) == SGL_KV_OK);
+        for (auto &v : live) sgl_kv_page_allocator_release(a, v.data(), v.size());
+        CHECK(sgl_kv_page_allocator_available_pages(a) <= pages);
+        sgl_kv_page_allocator_destroy(a);
+    }
+    char hex[65];
+    const uint64_t pages2[2] = {0, 1};
+    CHECK(sgl_kv_transfer_span_checksum("http-pd-poll", 12, "10.0.0.8", 8, 8200, 42, 0, 0, 2, 1, pages2, 2,
+                                        pages2, 2, hex) == SGL_KV_OK);
+    CHECK(strcmp(hex, "e37f348404de723244ca004c09d05fccfdcad793f9013bd1f882c332d1c50b5d") == 0);
+    std::vector<uint8_t> blob(5000);
+    for (auto &x : blob) x = (uint8_t)rng();
+    for (size_t n = 0; n < blob.size(); n += 1 + rng() % 97)
+        CHECK(sgl_kv_sha256_hex(blob.data(), n, hex) == SGL_KV_OK && strlen(hex) == 64);
+
     if (failures) {
         fprintf(stderr, "%d checks failed\n", failures);
         return 1;

@@ -310,3 +310,113 @@ def test_remote_page_request_errors(args, variant, fields):
         assert ei.value.fields[:2] == fields
     if variant == "NegativeRemoteKvIndex":
         assert ei.value.fields[0] == 2**64 - 1
+
+
+# --- page allocator (crates/sglang-srt/tests/cache_allocator.rs) ------------------------------
+
+def test_allocator_returns_contiguous_free_pages_in_page_order():
+    a = kv.CachePageAllocator(4)
+    assert a.allocate(3) == [0, 1, 2]
+    assert a.allocate(1) == [3]
+    assert a.available_pages() == 0
+
+
+def test_allocator_does_not_consume_pages_when_allocation_cannot_be_satisfied():
+    a = kv.CachePageAllocator(2)
+    with pytest.raises(kv.KvError) as ei:
+        a.allocate(3)
+    assert ei.value.variant == "OutOfSlots" and ei.value.fields[:2] == (3, 2)
+    assert a.available_pages() == 2
+    assert a.allocate(2) == [0, 1]
+
+
+def test_allocator_reuses_released_pages_before_never_allocated_pages():
+    a = kv.CachePageAllocator(5)
+    allocated = a.allocate(3)
+    a.release(allocated[1:])
+    assert a.allocate(3) == [1, 2, 3]
+
+
+def test_allocator_reset_restores_all_pages_in_page_order():
+    a = kv.CachePageAllocator(4)
+    a.allocate(3)
+    a.reset()
+    assert a.available_pages() == 4
+    assert a.allocate(4) == [0, 1, 2, 3]
+
+
+def test_page_aware_allocator_keeps_independent_requests_on_separate_pages():
+    a = kv.CachePageAllocator.with_page_size(8, 4)
+    assert a.allocate(3) == [0, 1, 2]
+    assert a.allocate(2) == [4, 5]
+    assert a.available_pages() == 0 and a.available_slots() == 0
+
+
+def test_page_aware_allocator_extends_a_sequence_tail_before_reserving_another_page():
+    a = kv.CachePageAllocator.with_page_size(8, 4)
+    sequence = a.allocate(3)
+    extension = a.allocate_for_sequence(sequence, 2)
+    assert extension == [3, 4]
+    sequence += extension
+    a.release(extension)
+    assert a.available_pages() == 1
+    assert a.allocate(1) == [4]
+    a.release(sequence[:3])
+    assert a.available_pages() == 1
+
+
+@pytest.mark.parametrize("cap,ps,variant,fields", [
+    (8, 0, "ZeroPageSize", None), (0, 4, "ZeroSlotCapacity", None),
+    (10, 4, "SlotCapacityNotPageAligned", (10, 4))])
+def test_page_aware_allocator_rejects_invalid_pool_geometry(cap, ps, variant, fields):
+    with pytest.raises(kv.KvError) as ei:
+        kv.CachePageAllocator.with_page_size(cap, ps)
+    assert ei.value.variant == variant
+    if fields:
+        assert ei.value.fields[:2] == fields
+
+
+def test_allocator_slots_are_a_valid_transfer_plan():
+    """Random allocate/release traffic: every allocation is distinct from
+    every live slot, in range, and transfer_page_indices accepts each
+    page-aligned allocation (slots contiguous within pages)."""
+    rng = np.random.default_rng(4)
+    P, cap = 16, 16 * 64
+    a = kv.CachePageAllocator.with_page_size(cap, P)
+    live = []
+    for _ in range(400):
+        if live and rng.random() < 0.4:
+            victim = live.pop(int(rng.integers(0, len(live))))
+            a.release(victim)
+            continue
+        n = int(rng.integers(1, 3 * P))
+        try:
+            slots = a.allocate(n)
+        except kv.KvError as e:
+            assert e.variant == "OutOfSlots"
+            continue
+        assert len(slots) == n and len(set(slots)) == n and max(slots) < cap
+        used = {s for x in live for s in x}
+        assert not used & set(slots)
+        assert kv.transfer_page_indices(0, 0, slots, P) == [s // P for s in slots[::P]]
+        live.append(slots)
+    assert a.available_slots() + sum(-(-len(x) // P) * P for x in live) == cap
+
+
+# --- span descriptor checksum (crates/sglang-srt/src/transfer.rs:548-570) ---------------------
+
+def test_span_descriptor_checksum_golden(goldens):
+    g = goldens["span_descriptor_checksum"]
+    got = kv.transfer_span_checksum(g["request_id"], g["bootstrap_host"], g["bootstrap_port"],
+                                    g["bootstrap_room"], g["data_parallel_rank"], g["token_offset"],
+                                    g["token_count"], g["page_size"], g["cache_pages"],
+                                    g["page_indices"])
+    assert got == g["checksum"]
+
+
+def test_sha256_matches_hashlib():
+    import hashlib
+    rng = np.random.default_rng(5)
+    for n in [0, 1, 55, 56, 63, 64, 65, 119, 120, 1000, 4096 + 3]:
+        data = rng.integers(0, 256, n, dtype=np.uint8).tobytes()
+        assert kv.sha256_hex(data) == hashlib.sha256(data).hexdigest(), n

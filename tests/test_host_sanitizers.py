@@ -1,7 +1,8 @@
 """The host layout / plan code of libsgl_rocm_kv under AddressSanitizer and
 UndefinedBehaviorSanitizer: tests/native/layout_fuzz.cpp replays reference
 goldens and fuzzes every group-1 entry point (small, boundary and
-overflowing values); any out-of-bounds access, overflow UB or violated
+overflowing values), the page allocator under random traffic and the
+checksum; any out-of-bounds access, overflow UB or violated
 invariant fails the run. Host code only (g++, no device code)."""
 import os
 import shutil
@@ -20,7 +21,7 @@ def test_layout_fuzz_under_asan_ubsan(tmp_path):
            "-fsanitize=address,undefined", "-fno-sanitize-recover=all",
            "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include", "-I" + os.path.join(ROOT, "include"),
            "-I" + CSRC, os.path.join(ROOT, "tests", "native", "layout_fuzz.cpp"),
-           os.path.join(CSRC, "kv_layout.cpp"), "-o", str(exe)]
+           os.path.join(CSRC, "kv_layout.cpp"), os.path.join(CSRC, "kv_plan.cpp"), "-o", str(exe)]
     subprocess.run(cmd, check=True, capture_output=True, timeout=240)
     env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=0",
                UBSAN_OPTIONS="print_stacktrace=1")

@@ -452,6 +452,14 @@ int32_t sgl_rocm_kv_transfer_layer(sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view 
                                    const sgl_kv_pool_view *dst,
                                    const sgl_kv_device_buffer *dst_slots, void *stream);
 
+/* Multi-layer pool -> pool: layer i of each side is its view with every
+ * tensor_offset advanced by i * that side's layer stride. */
+int32_t sgl_rocm_kv_transfer_layers(sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src,
+                                    uint64_t src_layer_stride, uint32_t layer_count,
+                                    const sgl_kv_device_buffer *src_slots, uint64_t row_count,
+                                    const sgl_kv_pool_view *dst, uint64_t dst_layer_stride,
+                                    const sgl_kv_device_buffer *dst_slots, void *stream);
+
 /* A request's run of transfer rows (KvCacheTransferSpan, transfer.rs:495-505):
  * rows [row_start, row_start + token_count) hold request tokens
  * [token_offset, token_offset + token_count); token k lives in page
@@ -558,6 +566,101 @@ int32_t sgl_rocm_kv_execute_page_requests(sgl_rocm_kv_ctx *ctx,
                                           const sgl_kv_device_buffer *source_region,
                                           const sgl_kv_device_buffer *target_region,
                                           uint32_t offsets_are_addresses, void *stream);
+
+/* ---- Transfer backend: KvTransferBackend (transfer.rs:1145-1151) ----
+ * register / submit / poll / cancel / shutdown for a prefill pool and a
+ * decode pool on this context's device. A span's rows are validated on the
+ * host at submit, then moved asynchronously:
+ *   DIRECT  one pool-to-pool launch over all layers (transfer_layers);
+ *   STAGED  the layer pipeline with the pinned-host hop (pack -> D2H ->
+ *           H2D -> unpack), spans in submission order over shared staging.
+ * poll reports each finished span once (poll_submitted_transfers,
+ * transfer.rs:2633-2674); cancel drops a room's spans without an event
+ * (cancel_submitted_transfers_for_room, transfer.rs:2605-2631). Calls on one
+ * backend must not overlap. */
+typedef struct sgl_rocm_kv_backend sgl_rocm_kv_backend;
+
+typedef enum sgl_kv_backend_mode {
+    SGL_KV_BACKEND_DIRECT = 0,
+    SGL_KV_BACKEND_STAGED = 1
+} sgl_kv_backend_mode;
+
+typedef struct sgl_kv_backend_config {
+    uint32_t mode;       /* sgl_kv_backend_mode */
+    uint32_t reserved;
+    uint64_t max_rows;   /* largest token_count a span may carry; sizes the staging */
+} sgl_kv_backend_config;
+
+/* One side's TransferableKvCacheMemory (defined in the un-vendored
+ * nexus-transfer crate, pinned at crates/sglang-srt/Cargo.toml:35; provided
+ * by kv_cache.rs's KvCacheMemoryProvider): the pool's layout and its device
+ * allocation. Every layer moves its first
+ * min(kv_tensors_per_token, 2) tensors. */
+typedef struct sgl_kv_backend_memory {
+    sgl_kv_paged_layout layout;
+    void *base;
+    uint64_t byte_len;
+    uint32_t head_layout;  /* sgl_kv_head_layout */
+    uint32_t reserved;
+    uint64_t heads;        /* head chunks per row; 0 = layout.runtime.kv_heads */
+} sgl_kv_backend_memory;
+
+/* One KvCacheTransferSpan (transfer.rs:495-505) as the decode side sees it:
+ * rows token_offset .. token_offset+token_count of the request move from
+ * prefill slots cache_slots[i] to decode slot
+ * dst_page_table[(token_offset+i) / decode_page_size] * decode_page_size +
+ * (token_offset+i) % decode_page_size. Host arrays, read during submit. */
+typedef struct sgl_kv_transfer_span_desc {
+    uint64_t bootstrap_room;
+    char descriptor_checksum[65];  /* NUL-terminated hex (sgl_kv_transfer_span_checksum) */
+    char reserved[7];
+    uint64_t token_offset;
+    uint64_t token_count;
+    const uint64_t *cache_slots;     /* token_count prefill slots */
+    const int32_t *dst_page_table;   /* decode pages of the request */
+    uint64_t dst_page_table_len;
+} sgl_kv_transfer_span_desc;
+
+/* KvTransferEventStatus (transfer.rs:1066-1071). */
+typedef enum sgl_kv_transfer_status {
+    SGL_KV_TRANSFER_COMPLETED = 0,
+    SGL_KV_TRANSFER_FAILED = 1,
+    SGL_KV_TRANSFER_CANCELED = 2
+} sgl_kv_transfer_status;
+
+/* KvTransferCompletionEvent (transfer.rs:1073-1078); a failed event carries
+ * the status code of the device error in error_code. */
+typedef struct sgl_kv_transfer_event {
+    uint64_t bootstrap_room;
+    char descriptor_checksum[65];
+    char reserved[3];
+    int32_t status;       /* sgl_kv_transfer_status */
+    int32_t error_code;   /* SGL_KV_OK unless FAILED */
+} sgl_kv_transfer_event;
+
+int32_t sgl_rocm_kv_backend_create(sgl_rocm_kv_ctx *ctx, const sgl_kv_backend_config *config,
+                                   sgl_rocm_kv_backend **out);
+/* Registers both pools; their layer count, tensors per token and token
+ * widths must agree. STAGED allocates its staging here (4 device and 2
+ * pinned host buffers of one layer's rows at max_rows). */
+int32_t sgl_rocm_kv_backend_register(sgl_rocm_kv_backend *backend,
+                                     const sgl_kv_backend_memory *prefill,
+                                     const sgl_kv_backend_memory *decode);
+/* Validates the span (prefill slots, decode page table entries) and
+ * enqueues its transfer; a span with token_count 0 completes at once. */
+int32_t sgl_rocm_kv_backend_submit(sgl_rocm_kv_backend *backend,
+                                   const sgl_kv_transfer_span_desc *span);
+/* Writes up to `capacity` events for finished spans; *pending = spans
+ * submitted, not canceled and not yet reported. Never blocks on transfers. */
+int32_t sgl_rocm_kv_backend_poll(sgl_rocm_kv_backend *backend, sgl_kv_transfer_event *events,
+                                 uint64_t capacity, uint64_t *event_count, uint64_t *pending);
+int32_t sgl_rocm_kv_backend_cancel(sgl_rocm_kv_backend *backend, uint64_t bootstrap_room);
+/* Blocks until every submitted span has finished on the device (no events
+ * are consumed). */
+int32_t sgl_rocm_kv_backend_wait(sgl_rocm_kv_backend *backend);
+/* Drains, releases every transfer and the staging, and forgets the pools. */
+int32_t sgl_rocm_kv_backend_shutdown(sgl_rocm_kv_backend *backend);
+int32_t sgl_rocm_kv_backend_destroy(sgl_rocm_kv_backend *backend);
 
 /* Synchronises `stream`, reads and clears the error word, and maps it to
  * SGL_KV_DEVICE_SLOT_INDEX_OUT_OF_RANGE, _PAGE_INDEX_, _SPAN_ or _REQUEST_

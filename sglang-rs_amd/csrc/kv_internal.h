@@ -55,8 +55,27 @@ int32_t prepare_pack(const sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src,
 int32_t prepare_unpack(const sgl_rocm_kv_ctx *ctx, const sgl_kv_rows_view *src, uint64_t row_count,
                        const sgl_kv_pool_view *dst, const sgl_kv_device_buffer *slots, Launch *l,
                        LayerSpan span = {1, 0, 0});
+int32_t prepare_transfer(const sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src,
+                         const sgl_kv_device_buffer *src_slots, uint64_t row_count,
+                         const sgl_kv_pool_view *dst, const sgl_kv_device_buffer *dst_slots,
+                         Launch *l, uint32_t layers, uint64_t src_layer_stride,
+                         uint64_t dst_layer_stride);
 int32_t submit_launch(sgl_rocm_kv_ctx *ctx, Launch &l, hipStream_t stream);
+hipStream_t pipeline_final_stream(sgl_rocm_kv_pipeline *pipe);
 int32_t hip_fail(hipError_t err, const char *call);
+int32_t flag_status(uint32_t flag);
+
+inline int32_t too_large_rows(uint64_t rows, uint64_t maximum) {
+    return fail(SGL_KV_DIMENSION_TOO_LARGE, "row_count", rows, maximum, 0,
+                "KV copy dimension row_count=%llu exceeds maximum %llu", (unsigned long long)rows,
+                (unsigned long long)maximum);
+}
+
+#define SGLKV_CHECK_HIP(call)                                              \
+    do {                                                                   \
+        hipError_t e_ = (call);                                            \
+        if (e_ != hipSuccess) return ::sglkv::hip_fail(e_, #call);         \
+    } while (0)
 
 inline bool mul_ovf(uint64_t a, uint64_t b, uint64_t *out) { return __builtin_mul_overflow(a, b, out); }
 inline bool add_ovf(uint64_t a, uint64_t b, uint64_t *out) { return __builtin_add_overflow(a, b, out); }

@@ -260,3 +260,7 @@ extern "C" int32_t sgl_rocm_kv_pipeline_destroy(sgl_rocm_kv_pipeline *p) {
     delete p;
     return ok();
 }
+
+// The stream of a pipeline's last stage (its unpacks): work recorded there
+// after a run completes after every layer of that run.
+hipStream_t sglkv::pipeline_final_stream(sgl_rocm_kv_pipeline *p) { return p->stream[kUnpack]; }

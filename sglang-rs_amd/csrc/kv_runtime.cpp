@@ -603,10 +603,15 @@ extern "C" int32_t sgl_rocm_kv_unpack_layers(sgl_rocm_kv_ctx *ctx, const sgl_kv_
     return rc ? rc : ok();
 }
 
-extern "C" int32_t sgl_rocm_kv_transfer_layer(sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src,
-                                              const sgl_kv_device_buffer *src_slots,
-                                              uint64_t row_count, const sgl_kv_pool_view *dst,
-                                              const sgl_kv_device_buffer *dst_slots, void *stream) {
+namespace sglkv {
+
+// Pool -> pool over `layers` consecutive layers (layer i of a side: its
+// view with every tensor offset advanced by i * stride).
+int32_t prepare_transfer(const sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src,
+                         const sgl_kv_device_buffer *src_slots, uint64_t row_count,
+                         const sgl_kv_pool_view *dst, const sgl_kv_device_buffer *dst_slots,
+                         Launch *l, uint32_t layers, uint64_t src_layer_stride,
+                         uint64_t dst_layer_stride) {
     int32_t rc = check_ctx(ctx);
     if (!rc) rc = check_pool_shape(src);
     if (!rc) rc = check_pool_shape(dst);
@@ -624,17 +629,68 @@ extern "C" int32_t sgl_rocm_kv_transfer_layer(sgl_rocm_kv_ctx *ctx, const sgl_kv
         return fail(SGL_KV_INVALID_ARGUMENT, "heads", src->heads, src->row_bytes, 0,
                     "%u heads do not split a %llu-byte row evenly", src->heads,
                     (unsigned long long)src->row_bytes);
-    if (row_count == 0) return ok();
-    Launch l;
-    memset(&l, 0, sizeof l);
-    l.kind = kPoolPool;
-    l.rows = row_count;
-    l.shape = RowShape{src->row_bytes, src->tensor_count, split ? src->heads : 1u, split};
-    if ((rc = pool_side(src, src_slots, row_count, l.shape, &l.params.src)) ||
-        (rc = pool_side(dst, dst_slots, row_count, l.shape, &l.params.dst)))
+    if (layers == 0 || layers > 65535)
+        return fail(SGL_KV_INVALID_ARGUMENT, "layer_count", layers, 65535, 0,
+                    "a launch covers 1 to 65535 layers, not %u", layers);
+    memset(l, 0, sizeof *l);
+    l->kind = kPoolPool;
+    l->rows = row_count;
+    l->layers = layers;
+    if (row_count == 0) return SGL_KV_OK;
+    l->shape = RowShape{src->row_bytes, src->tensor_count, split ? src->heads : 1u, split};
+    if ((rc = pool_side(src, src_slots, row_count, l->shape, &l->params.src)) ||
+        (rc = pool_side(dst, dst_slots, row_count, l->shape, &l->params.dst)))
         return rc;
-    attach_scales(l.params, src->scale, dst->scale, src->tensor_count);
-    if ((rc = finish_launch(ctx, &l))) return rc;
+    if (layers > 1) {
+        // The last layer of each side, as views of their own.
+        sgl_kv_pool_view last[2] = {*src, *dst};
+        const uint64_t strides[2] = {src_layer_stride, dst_layer_stride};
+        const sgl_kv_device_buffer *slots[2] = {src_slots, dst_slots};
+        sglkv_side scratch;
+        for (int side = 0; side < 2; ++side) {
+            uint64_t shift;
+            if (mul_ovf(layers - 1, strides[side], &shift)) return shape_overflow();
+            for (uint32_t t = 0; t < last[side].tensor_count; ++t)
+                if (add_ovf(last[side].tensor_offset[t], shift, &last[side].tensor_offset[t]))
+                    return shape_overflow();
+            if ((rc = pool_side(&last[side], slots[side], row_count, l->shape, &scratch))) return rc;
+        }
+        uint64_t lo = UINT64_MAX, hi = 0;
+        for (uint32_t t = 0; t < dst->tensor_count; ++t) {
+            lo = dst->tensor_offset[t] < lo ? dst->tensor_offset[t] : lo;
+            const uint64_t end = dst->tensor_offset[t] + dst->page_size * dst->row_bytes;
+            hi = end > hi ? end : hi;
+        }
+        if (dst_layer_stride < hi - lo)
+            return fail(SGL_KV_INVALID_ARGUMENT, "dst_layer_stride", dst_layer_stride, hi - lo, 0,
+                        "destination layers %llu bytes apart overlap their %llu-byte regions",
+                        (unsigned long long)dst_layer_stride, (unsigned long long)(hi - lo));
+    }
+    l->params.src.layer_stride = src_layer_stride;
+    l->params.dst.layer_stride = dst_layer_stride;
+    attach_scales(l->params, src->scale, dst->scale, src->tensor_count);
+    return finish_launch(ctx, l);
+}
+
+}  // namespace sglkv
+
+extern "C" int32_t sgl_rocm_kv_transfer_layer(sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src,
+                                              const sgl_kv_device_buffer *src_slots,
+                                              uint64_t row_count, const sgl_kv_pool_view *dst,
+                                              const sgl_kv_device_buffer *dst_slots, void *stream) {
+    return sgl_rocm_kv_transfer_layers(ctx, src, 0, 1, src_slots, row_count, dst, 0, dst_slots, stream);
+}
+
+extern "C" int32_t sgl_rocm_kv_transfer_layers(sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src,
+                                               uint64_t src_layer_stride, uint32_t layer_count,
+                                               const sgl_kv_device_buffer *src_slots,
+                                               uint64_t row_count, const sgl_kv_pool_view *dst,
+                                               uint64_t dst_layer_stride,
+                                               const sgl_kv_device_buffer *dst_slots, void *stream) {
+    Launch l;
+    int32_t rc = prepare_transfer(ctx, src, src_slots, row_count, dst, dst_slots, &l, layer_count,
+                                  src_layer_stride, dst_layer_stride);
+    if (rc) return rc;
     DeviceScope scope(ctx->device);
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
     rc = submit_launch(ctx, l, static_cast<hipStream_t>(stream));
@@ -685,16 +741,8 @@ extern "C" int32_t sgl_rocm_kv_resolve_spans(sgl_rocm_kv_ctx *ctx, uint64_t page
     return ok();
 }
 
-extern "C" int32_t sgl_rocm_kv_check_errors(sgl_rocm_kv_ctx *ctx, void *stream) {
-    int32_t rc = check_ctx(ctx);
-    if (rc) return rc;
-    DeviceScope scope(ctx->device);
-    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    SGLKV_HIP(hipStreamSynchronize(s));
-    uint32_t flag = 0;
-    SGLKV_HIP(hipMemcpy(&flag, ctx->flag, sizeof flag, hipMemcpyDeviceToHost));
-    if (flag) SGLKV_HIP(hipMemset(ctx->flag, 0, sizeof(uint32_t)));
+// Maps the device error word to the status (and detail record) it reports.
+int32_t sglkv::flag_status(uint32_t flag) {
     if (flag & SGLKV_FLAG_SLOT)
         return fail(SGL_KV_DEVICE_SLOT_INDEX_OUT_OF_RANGE, nullptr, 0, flag, 0,
                     "KV copy device slot map contains an index outside the pool's slots");
@@ -708,6 +756,19 @@ extern "C" int32_t sgl_rocm_kv_check_errors(sgl_rocm_kv_ctx *ctx, void *stream) 
         return fail(SGL_KV_DEVICE_REQUEST_OUT_OF_RANGE, nullptr, 0, flag, 0,
                     "KV page request lies outside its source or target region");
     return ok();
+}
+
+extern "C" int32_t sgl_rocm_kv_check_errors(sgl_rocm_kv_ctx *ctx, void *stream) {
+    int32_t rc = check_ctx(ctx);
+    if (rc) return rc;
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    SGLKV_HIP(hipStreamSynchronize(s));
+    uint32_t flag = 0;
+    SGLKV_HIP(hipMemcpy(&flag, ctx->flag, sizeof flag, hipMemcpyDeviceToHost));
+    if (flag) SGLKV_HIP(hipMemset(ctx->flag, 0, sizeof(uint32_t)));
+    return flag_status(flag);
 }
 
 extern "C" int32_t sgl_rocm_kv_fill_synthetic(sgl_rocm_kv_ctx *ctx, const sgl_kv_device_buffer *buffer,

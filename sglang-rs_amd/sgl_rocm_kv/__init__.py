@@ -158,6 +158,29 @@ class _PipelineDesc(ctypes.Structure):
                 ("host", ctypes.c_void_p * 2), ("host_bytes", _u64)]
 
 
+class _BackendConfig(ctypes.Structure):
+    _fields_ = [("mode", ctypes.c_uint32), ("reserved", ctypes.c_uint32), ("max_rows", _u64)]
+
+
+class _BackendMemory(ctypes.Structure):
+    _fields_ = [("layout", _PagedLayout), ("base", ctypes.c_void_p), ("byte_len", _u64),
+                ("head_layout", ctypes.c_uint32), ("reserved", ctypes.c_uint32), ("heads", _u64)]
+
+
+class _SpanDesc(ctypes.Structure):
+    _fields_ = [("bootstrap_room", _u64), ("descriptor_checksum", ctypes.c_char * 65),
+                ("reserved", ctypes.c_char * 7), ("token_offset", _u64), ("token_count", _u64),
+                ("cache_slots", ctypes.POINTER(_u64)),
+                ("dst_page_table", ctypes.POINTER(ctypes.c_int32)),
+                ("dst_page_table_len", _u64)]
+
+
+class _TransferEvent(ctypes.Structure):
+    _fields_ = [("bootstrap_room", _u64), ("descriptor_checksum", ctypes.c_char * 65),
+                ("reserved", ctypes.c_char * 3), ("status", ctypes.c_int32),
+                ("error_code", ctypes.c_int32)]
+
+
 PAGE_REQUEST_DTYPE = np.dtype([("source", "<u8"), ("target_offset", "<u8"), ("length", "<u8")])
 
 
@@ -239,6 +262,10 @@ _EXPORTS = {
                                                    ctypes.c_uint32, _u64, ctypes.POINTER(PoolView),
                                                    _u64, ctypes.POINTER(_DeviceBuffer),
                                                    ctypes.c_void_p]),
+    "sgl_rocm_kv_transfer_layers": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(PoolView), _u64,
+                                                     ctypes.c_uint32, ctypes.POINTER(_DeviceBuffer),
+                                                     _u64, ctypes.POINTER(PoolView), _u64,
+                                                     ctypes.POINTER(_DeviceBuffer), ctypes.c_void_p]),
     "sgl_rocm_kv_transfer_layer": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(PoolView),
                                                     ctypes.POINTER(_DeviceBuffer), _u64,
                                                     ctypes.POINTER(PoolView),
@@ -258,6 +285,18 @@ _EXPORTS = {
                                                           ctypes.POINTER(ctypes.c_float)]),
     "sgl_rocm_kv_pipeline_elapsed": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_float)]),
     "sgl_rocm_kv_pipeline_destroy": (ctypes.c_int32, [ctypes.c_void_p]),
+    "sgl_rocm_kv_backend_create": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_BackendConfig),
+                                                    ctypes.POINTER(ctypes.c_void_p)]),
+    "sgl_rocm_kv_backend_register": (ctypes.c_int32, [ctypes.c_void_p,
+                                                      ctypes.POINTER(_BackendMemory),
+                                                      ctypes.POINTER(_BackendMemory)]),
+    "sgl_rocm_kv_backend_submit": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_SpanDesc)]),
+    "sgl_rocm_kv_backend_poll": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_TransferEvent),
+                                                  _u64, ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
+    "sgl_rocm_kv_backend_cancel": (ctypes.c_int32, [ctypes.c_void_p, _u64]),
+    "sgl_rocm_kv_backend_wait": (ctypes.c_int32, [ctypes.c_void_p]),
+    "sgl_rocm_kv_backend_shutdown": (ctypes.c_int32, [ctypes.c_void_p]),
+    "sgl_rocm_kv_backend_destroy": (ctypes.c_int32, [ctypes.c_void_p]),
     "sgl_rocm_kv_execute_page_requests": (ctypes.c_int32, [ctypes.c_void_p,
                                                            ctypes.POINTER(_DeviceBuffer), _u64, _u64,
                                                            ctypes.POINTER(_DeviceBuffer),
@@ -698,6 +737,14 @@ class RocmKvPairCopyKernels:
               ctypes.byref(src_slots), row_count, ctypes.byref(dst), ctypes.byref(dst_slots),
               _stream(stream))
 
+    def transfer_layers(self, src: PoolView, src_layer_stride: int, layer_count: int,
+                        src_slots: _DeviceBuffer, row_count: int, dst: PoolView,
+                        dst_layer_stride: int, dst_slots: _DeviceBuffer, stream=None):
+        """Pool -> pool over `layer_count` consecutive layers in one launch."""
+        _call(lib().sgl_rocm_kv_transfer_layers, self._h, ctypes.byref(src), src_layer_stride,
+              layer_count, ctypes.byref(src_slots), row_count, ctypes.byref(dst), dst_layer_stride,
+              ctypes.byref(dst_slots), _stream(stream))
+
     def resolve_spans(self, page_size: int, page_count: int, spans: _DeviceBuffer,
                       span_count: int, page_table: _DeviceBuffer, page_table_len: int,
                       row_count: int, out_slots: _DeviceBuffer, stream=None):
@@ -768,6 +815,94 @@ class LayerPipeline:
     def close(self):
         if self._h:
             _call(lib().sgl_rocm_kv_pipeline_destroy, self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+BACKEND_DIRECT, BACKEND_STAGED = 0, 1
+TRANSFER_COMPLETED, TRANSFER_FAILED, TRANSFER_CANCELED = 0, 1, 2
+
+
+@dataclass(frozen=True)
+class KvTransferCompletionEvent:
+    """KvTransferCompletionEvent (transfer.rs:1073-1078); error_code is the
+    device error's status for a FAILED event."""
+    bootstrap_room: int
+    descriptor_checksum: str
+    status: int
+    error_code: int = 0
+
+
+class RocmKvTransferBackend:
+    """sgl_rocm_kv_backend: KvTransferBackend (transfer.rs:1145-1151) over a
+    prefill pool and a decode pool on one device. ``mode`` is BACKEND_DIRECT
+    (one pool-to-pool launch per span) or BACKEND_STAGED (the layer pipeline
+    through pinned host memory); ``max_rows`` bounds a span's token_count."""
+
+    def __init__(self, kernels: "RocmKvPairCopyKernels", mode: int = BACKEND_DIRECT,
+                 max_rows: int = 1 << 20):
+        self._kernels = kernels  # the context must outlive the backend
+        cfg = _BackendConfig(mode, 0, max_rows)
+        h = ctypes.c_void_p()
+        _call(lib().sgl_rocm_kv_backend_create, kernels._h, ctypes.byref(cfg), ctypes.byref(h))
+        self._h = h.value
+
+    @staticmethod
+    def _memory(layout: PagedKvCacheLayout, base: int, byte_len: int, head_layout: int,
+                heads: int) -> _BackendMemory:
+        return _BackendMemory(layout._c, base, byte_len, head_layout, 0, heads)
+
+    def register(self, prefill: PagedKvCacheLayout, prefill_base: int, prefill_len: int,
+                 decode: PagedKvCacheLayout, decode_base: int, decode_len: int, *,
+                 prefill_head_layout: int = NHD, prefill_heads: int = 0,
+                 decode_head_layout: int = NHD, decode_heads: int = 0):
+        """Registers both pools; heads 0 takes the layout's kv_heads."""
+        p = self._memory(prefill, prefill_base, prefill_len, prefill_head_layout, prefill_heads)
+        d = self._memory(decode, decode_base, decode_len, decode_head_layout, decode_heads)
+        _call(lib().sgl_rocm_kv_backend_register, self._h, ctypes.byref(p), ctypes.byref(d))
+
+    def submit(self, bootstrap_room: int, descriptor_checksum: str, token_offset: int,
+               cache_slots, dst_page_table):
+        """Submits one span: prefill `cache_slots` hold the request's tokens
+        token_offset.. ; the decode side holds them in `dst_page_table`."""
+        slots = _u64_array(cache_slots)
+        table = np.ascontiguousarray(np.asarray(dst_page_table, dtype=np.int32))
+        d = _SpanDesc()
+        d.bootstrap_room = bootstrap_room
+        d.descriptor_checksum = descriptor_checksum.encode()[:64]
+        d.token_offset, d.token_count = token_offset, len(slots)
+        d.cache_slots = slots.ctypes.data_as(ctypes.POINTER(_u64))
+        d.dst_page_table = table.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+        d.dst_page_table_len = len(table)
+        _call(lib().sgl_rocm_kv_backend_submit, self._h, ctypes.byref(d))
+
+    def poll(self, capacity: int = 256):
+        """(events, pending_transfers), as KvTransferPoll (transfer.rs:1122-1143)."""
+        events = (_TransferEvent * max(capacity, 1))()
+        n, pending = _u64(), _u64()
+        _call(lib().sgl_rocm_kv_backend_poll, self._h, events, capacity, ctypes.byref(n),
+              ctypes.byref(pending))
+        out = [KvTransferCompletionEvent(e.bootstrap_room, e.descriptor_checksum.decode(),
+                                         e.status, e.error_code) for e in events[:n.value]]
+        return out, pending.value
+
+    def cancel(self, bootstrap_room: int):
+        _call(lib().sgl_rocm_kv_backend_cancel, self._h, bootstrap_room)
+
+    def wait(self):
+        _call(lib().sgl_rocm_kv_backend_wait, self._h)
+
+    def shutdown(self):
+        _call(lib().sgl_rocm_kv_backend_shutdown, self._h)
+
+    def close(self):
+        if self._h:
+            _call(lib().sgl_rocm_kv_backend_destroy, self._h)
             self._h = None
 
     def __del__(self):

@@ -1,0 +1,292 @@
+"""GPU tests of the transfer backend (sgl_rocm_kv_backend_*), the device
+counterpart of KvTransferBackend (crates/sglang-srt/src/transfer.rs:
+1145-1151), and of the multi-layer pool-to-pool launch it uses.
+
+Every moved byte is checked against the CPU oracle (oracle/kv_oracle.c) on
+the same seeded pools, bit for bit: the prefill pool is page size 1 NHD, the
+decode pool page size 16 HND with its own page table, and spans carry cached
+prefixes (token_offset > 0, as in crates/sglang-srt/tests/pd_transfer_plan.rs:
+85-114). Event semantics follow the Mooncake executor's poll and cancel
+(transfer.rs:2605-2674): each finished span is reported once with its
+bootstrap room and descriptor checksum; a canceled room reports nothing.
+"""
+import numpy as np
+import pytest
+
+import oracle
+import sgl_rocm_kv as kv
+from sgl_rocm_kv import hip
+from sgl_rocm_kv import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+L, H, D = 4, 8, 128          # layers, KV heads, head dim (bf16): 2 KiB rows
+P_PREFILL, P_DECODE = 1, 16
+PREFILL_PAGES, DECODE_PAGES = 4096, 256
+
+
+def _say(msg):
+    print(f"[gpu] {msg}", flush=True)
+
+
+@pytest.fixture(scope="module")
+def k():
+    if hip.device_count() == 0:
+        pytest.fail("no GPU visible: the gpu tests need an MI355X")
+    ctx = kv.RocmKvPairCopyKernels(0)
+    yield ctx
+    ctx.close()
+
+
+def _layouts():
+    pre = kv.PagedKvCacheLayout.new(kv.KvCacheRuntimeLayout.for_model("bf16", P_PREFILL, L, H, D),
+                                    PREFILL_PAGES)
+    dec = kv.PagedKvCacheLayout.new(kv.KvCacheRuntimeLayout.for_model("bf16", P_DECODE, L, H, D),
+                                    DECODE_PAGES)
+    return pre, dec
+
+
+def _opool(view: kv.PoolView) -> oracle.Pool:
+    t = view.tensor_count
+    return oracle.Pool(view.page_size, view.page_stride_bytes, view.page_count,
+                       tuple(view.tensor_offset[:t]), view.row_bytes, t, view.heads,
+                       view.head_layout == kv.HND)
+
+
+class _Pools:
+    """Seeded prefill and decode pools on the device, with host copies of
+    what the decode pool must hold after the submitted spans."""
+
+    def __init__(self, seed):
+        self.pre, self.dec = _layouts()
+        rng = np.random.default_rng(seed)
+        self.src_h = rng.integers(0, 256, self.pre.total_byte_len, dtype=np.uint8)
+        self.dst_h = rng.integers(0, 256, self.dec.total_byte_len, dtype=np.uint8)
+        self.src = hip.DeviceBuffer.from_array(self.src_h)
+        self.dst = hip.DeviceBuffer.from_array(self.dst_h)
+        self.want = self.dst_h.copy()
+
+    def register(self, backend):
+        backend.register(self.pre, self.src.ptr, self.src.nbytes, self.dec, self.dst.ptr,
+                         self.dst.nbytes, decode_head_layout=kv.HND)
+
+    def expect(self, token_offset, cache_slots, page_table):
+        """Applies one span to the expected decode pool with the oracle."""
+        tokens = token_offset + np.arange(len(cache_slots), dtype=np.uint64)
+        table = np.asarray(page_table, dtype=np.uint64)
+        dst_slots = table[tokens // P_DECODE] * P_DECODE + tokens % P_DECODE
+        for layer in range(L):
+            sv = self.pre.pool_view(self.src.ptr, self.src.nbytes, layer, kv.NHD, H)
+            dv = self.dec.pool_view(self.dst.ptr, self.dst.nbytes, layer, kv.HND, H)
+            oracle.transfer(_opool(sv), self.src_h, cache_slots, _opool(dv), self.want, dst_slots,
+                            threads=4)
+
+    def check(self):
+        np.testing.assert_array_equal(self.dst.download(), self.want)
+
+
+def _span(rng, token_offset, count, pages):
+    """A request's prefill slots (distinct, shuffled pages of size 1) and a
+    decode page table covering tokens 0 .. token_offset+count."""
+    slots = rng.choice(PREFILL_PAGES, size=count, replace=False).astype(np.uint64)
+    need = -(-(token_offset + count) // P_DECODE)
+    table = rng.choice(pages, size=need, replace=False).astype(np.int32)
+    return slots, table
+
+
+def _checksum(room, token_offset, slots):
+    pages = [int(s) for s in slots]
+    return kv.transfer_span_checksum(f"req-{room}", "10.0.0.8", 8200, room, 0, token_offset,
+                                     len(slots), P_PREFILL, pages,
+                                     [p for p in pages])
+
+
+@pytest.mark.parametrize("mode", [kv.BACKEND_DIRECT, kv.BACKEND_STAGED])
+def test_backend_spans_match_oracle(k, mode):
+    """Spans with and without cached prefixes, a no-op span, and in-order
+    completion events carrying each span's room and checksum."""
+    name = "direct" if mode == kv.BACKEND_DIRECT else "staged"
+    _say(f"backend {name}: 4 spans over {L} layers")
+    rng = np.random.default_rng(100 + mode)
+    pools = _Pools(seed=7 + mode)
+    b = kv.RocmKvTransferBackend(k, mode, max_rows=512)
+    pools.register(b)
+    # Each request owns a disjoint group of decode pages.
+    groups = rng.permutation(DECODE_PAGES).reshape(8, -1)
+    cases = [(11, 0, 37), (12, 16, 50), (13, 5, 0), (14, 32, 300)]
+    sums = {}
+    for i, (room, off, n) in enumerate(cases):
+        slots, table = _span(rng, off, n, groups[i])
+        sums[room] = _checksum(room, off, slots)
+        b.submit(room, sums[room], off, slots, table)
+        if n:
+            pools.expect(off, slots, table)
+    b.wait()
+    events, pending = b.poll()
+    assert pending == 0
+    assert [e.bootstrap_room for e in events] == [c[0] for c in cases]
+    for e in events:
+        assert e.status == kv.TRANSFER_COMPLETED and e.error_code == 0
+        assert e.descriptor_checksum == sums[e.bootstrap_room]
+    assert b.poll() == ([], 0)  # each span is reported once
+    pools.check()
+    b.close()
+
+
+def test_backend_poll_capacity_and_cancel(k):
+    """poll returns at most `capacity` events and keeps the rest; a canceled
+    room never reports; pending counts spans not yet reported."""
+    rng = np.random.default_rng(5)
+    pools = _Pools(seed=8)
+    b = kv.RocmKvTransferBackend(k, kv.BACKEND_DIRECT, max_rows=256)
+    pools.register(b)
+    groups = rng.permutation(DECODE_PAGES).reshape(8, -1)
+    for i, room in enumerate((21, 22, 23, 24)):
+        slots, table = _span(rng, 0, 100, groups[i])
+        b.submit(room, f"{room:064x}", 0, slots, table)
+        pools.expect(0, slots, table)
+    b.cancel(23)
+    b.wait()
+    first, pending = b.poll(capacity=1)
+    assert [e.bootstrap_room for e in first] == [21] and pending == 2
+    rest, pending = b.poll()
+    assert [e.bootstrap_room for e in rest] == [22, 24] and pending == 0
+    assert rest[0].descriptor_checksum == f"{22:064x}"
+    # A canceled span's device work still ran to completion.
+    pools.check()
+    b.shutdown()
+    # After shutdown the backend can be registered again.
+    pools.register(b)
+    b.close()
+
+
+def test_backend_staged_spans_reuse_staging_in_order(k):
+    """Staged spans share one set of staging buffers: many back-to-back
+    submissions must each complete intact."""
+    rng = np.random.default_rng(9)
+    pools = _Pools(seed=10)
+    b = kv.RocmKvTransferBackend(k, kv.BACKEND_STAGED, max_rows=128)
+    pools.register(b)
+    groups = rng.permutation(DECODE_PAGES).reshape(16, -1)
+    rooms = list(range(31, 47))
+    for i, room in enumerate(rooms):
+        off = int(rng.integers(0, 32))
+        n = int(rng.integers(1, 129))
+        n = min(n, (len(groups[i]) * P_DECODE) - off)
+        slots, table = _span(rng, off, n, groups[i])
+        b.submit(room, "", off, slots, table)
+        pools.expect(off, slots, table)
+    seen = []
+    for _ in range(2 * len(rooms)):
+        if len(seen) == len(rooms):
+            break
+        events, pending = b.poll(capacity=3)
+        seen += [e.bootstrap_room for e in events]
+        assert pending == len(rooms) - len(seen)
+        if not events:
+            b.wait()
+    assert seen == rooms
+    pools.check()
+    b.close()
+
+
+def test_backend_submit_validation(k):
+    """Bad spans are refused on the host before anything is enqueued, with
+    the reference's layout error variants; nothing is written."""
+    rng = np.random.default_rng(3)
+    pools = _Pools(seed=11)
+    b = kv.RocmKvTransferBackend(k, kv.BACKEND_DIRECT, max_rows=64)
+    with pytest.raises(kv.KvError) as e:          # nothing registered yet
+        b.submit(1, "", 0, [0], [0])
+    assert e.value.code == 12
+    pools.register(b)
+    with pytest.raises(kv.KvError) as e:          # registered twice
+        pools.register(b)
+    assert e.value.code == 12
+    slots, table = _span(rng, 0, 40, np.arange(DECODE_PAGES))
+    bad = slots.copy()
+    bad[7] = PREFILL_PAGES                        # past the prefill pool
+    with pytest.raises(kv.KvError) as e:
+        b.submit(2, "", 0, bad, table)
+    assert e.value.variant == "BatchSlotOutOfRange" and e.value.fields[:3] == (7, PREFILL_PAGES,
+                                                                                PREFILL_PAGES)
+    with pytest.raises(kv.KvError) as e:          # page table too short
+        b.submit(3, "", 0, slots, table[:2])
+    assert e.value.code == 12 and e.value.name == "dst_page_table"
+    neg = table.copy()
+    neg[1] = -1
+    with pytest.raises(kv.KvError) as e:
+        b.submit(4, "", 0, slots, neg)
+    assert e.value.variant == "PageOutOfRange"
+    past = table.copy()
+    past[2] = DECODE_PAGES
+    with pytest.raises(kv.KvError) as e:
+        b.submit(5, "", 0, slots, past)
+    assert e.value.variant == "PageOutOfRange" and e.value.fields[:2] == (DECODE_PAGES,
+                                                                          DECODE_PAGES)
+    big, big_table = _span(rng, 0, 65, np.arange(DECODE_PAGES))
+    with pytest.raises(kv.KvError) as e:          # more rows than max_rows
+        b.submit(6, "", 0, big, big_table)
+    assert e.value.code == 3
+    assert b.poll() == ([], 0)
+    pools.check()                                 # untouched
+    b.close()
+
+
+def test_backend_register_rejects_mismatched_pools(k):
+    pre = kv.PagedKvCacheLayout.new(kv.KvCacheRuntimeLayout.for_model("bf16", 1, L, H, D), 64)
+    other = kv.PagedKvCacheLayout.new(kv.KvCacheRuntimeLayout.for_model("bf16", 16, L + 1, H, D), 4)
+    a, c = hip.DeviceBuffer(pre.total_byte_len), hip.DeviceBuffer(other.total_byte_len)
+    b = kv.RocmKvTransferBackend(k, kv.BACKEND_DIRECT, max_rows=16)
+    with pytest.raises(kv.KvError) as e:
+        b.register(pre, a.ptr, a.nbytes, other, c.ptr, c.nbytes)
+    assert e.value.code == 12
+    with pytest.raises(kv.KvError) as e:          # decode allocation too small
+        b.register(pre, a.ptr, a.nbytes, pre, c.ptr, pre.total_byte_len - 1)
+    assert e.value.code == 11 and e.value.name == "decode"
+    assert e.value.fields[1:] == (pre.total_byte_len, pre.total_byte_len - 1)
+    b.register(pre, a.ptr, a.nbytes, pre, c.ptr, pre.total_byte_len)  # exactly enough
+    b.close()
+
+
+def test_transfer_layers_matches_per_layer_oracle(k):
+    """One pool-to-pool launch over all layers (P=1 NHD -> P=64 HND) equals
+    the per-layer oracle; a layer span that runs past the destination is
+    refused on the host."""
+    t = wl.scaled(wl.c2(), 3000, seed=6)
+    t.dst = wl.PoolSpec(64, t.dst.page_count, kv.HND)
+    sh = t.shape
+    layers = 6
+    _say(f"transfer_layers {t.name}: {t.rows} rows x {layers} layers")
+    rng = np.random.default_rng(22)
+    src_h = rng.integers(0, 256, t.src.byte_len(sh), dtype=np.uint8)
+    dst_h = rng.integers(0, 256, t.dst.byte_len(sh), dtype=np.uint8)
+    src, dst = hip.DeviceBuffer.from_array(src_h), hip.DeviceBuffer.from_array(dst_h)
+    ss, ds = hip.DeviceBuffer.from_array(t.src_slots), hip.DeviceBuffer.from_array(t.dst_slots)
+
+    def view(buf, spec, layer):
+        return kv.pool_view(buf.ptr, buf.nbytes, page_size=spec.page_size,
+                            page_stride_bytes=spec.page_stride(sh), page_count=spec.page_count,
+                            tensor_offset=spec.tensor_offsets(sh, layer), row_bytes=sh.row_bytes,
+                            tensor_count=sh.tensors, heads=sh.heads, head_layout=spec.head_layout)
+
+    def opool(spec, layer):
+        return oracle.Pool(spec.page_size, spec.page_stride(sh), spec.page_count,
+                           spec.tensor_offsets(sh, layer), sh.row_bytes, sh.tensors, sh.heads,
+                           spec.head_layout == kv.HND)
+
+    first = 3
+    s_stride = t.src.tensor_offsets(sh, first + 1)[0] - t.src.tensor_offsets(sh, first)[0]
+    d_stride = t.dst.tensor_offsets(sh, first + 1)[0] - t.dst.tensor_offsets(sh, first)[0]
+    k.transfer_layers(view(src, t.src, first), s_stride, layers, kv.device_buffer(ss.ptr, ss.nbytes),
+                      t.rows, view(dst, t.dst, first), d_stride,
+                      kv.device_buffer(ds.ptr, ds.nbytes))
+    k.check_errors()
+    for layer in range(first, first + layers):
+        oracle.transfer(opool(t.src, layer), src_h, t.src_slots, opool(t.dst, layer), dst_h,
+                        t.dst_slots, threads=4)
+    np.testing.assert_array_equal(dst.download(), dst_h)
+    with pytest.raises(kv.KvError):
+        k.transfer_layers(view(src, t.src, first), s_stride, sh.layers,
+                          kv.device_buffer(ss.ptr, ss.nbytes), t.rows, view(dst, t.dst, first),
+                          d_stride, kv.device_buffer(ds.ptr, ds.nbytes))

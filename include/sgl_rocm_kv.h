@@ -445,6 +445,28 @@ int32_t sgl_rocm_kv_unpack_layers(sgl_rocm_kv_ctx *ctx, const sgl_kv_rows_view *
                                   uint64_t row_count, const sgl_kv_pool_view *dst,
                                   uint64_t pool_layer_stride, const sgl_kv_device_buffer *slots,
                                   void *stream);
+/* One tensor of one layer for `count` slots (u64, on the device), between a
+ * pool laid out by `layout` (NHD) and rows source_offset + i *
+ * source_row_stride: the batched form of
+ * CudaKvStorage::write_tensor_slot_from_device / read_tensor_slot_to_device
+ * (crates/sglang-srt/src/cuda_kv_cache.rs:258-294), which the MLA forward
+ * pass calls once per token and tensor (cuda_mla.rs:256-271). Works for
+ * tensor-pair layouts with unequal key/value widths (MLA 576/512), one
+ * call per tensor. Layer and tensor are checked on the host
+ * (LayerOutOfRange / TensorOutOfRange); a slot past the pool raises the
+ * error word (SLOT) and its row is skipped. Asynchronous. */
+int32_t sgl_rocm_kv_write_tensor_slots(sgl_rocm_kv_ctx *ctx, const sgl_kv_paged_layout *layout,
+                                       const sgl_kv_device_buffer *pool, uint64_t layer,
+                                       uint64_t tensor, const sgl_kv_device_buffer *slots,
+                                       uint64_t count, const sgl_kv_device_buffer *source,
+                                       uint64_t source_offset, uint64_t source_row_stride,
+                                       void *stream);
+int32_t sgl_rocm_kv_read_tensor_slots(sgl_rocm_kv_ctx *ctx, const sgl_kv_paged_layout *layout,
+                                      const sgl_kv_device_buffer *pool, uint64_t layer,
+                                      uint64_t tensor, const sgl_kv_device_buffer *slots,
+                                      uint64_t count, const sgl_kv_device_buffer *destination,
+                                      uint64_t destination_offset,
+                                      uint64_t destination_row_stride, void *stream);
 /* Pool -> pool in one pass for co-resident prefill and decode pools:
  * the composition unpack(pack(.)) without the transfer rows. */
 int32_t sgl_rocm_kv_transfer_layer(sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src,

@@ -603,6 +603,66 @@ extern "C" int32_t sgl_rocm_kv_unpack_layers(sgl_rocm_kv_ctx *ctx, const sgl_kv_
     return rc ? rc : ok();
 }
 
+namespace {
+
+// One tensor of one layer, `count` slots, between a pool described by its
+// PagedKvCacheLayout and strided rows: the batched form of
+// CudaKvStorage::write_tensor_slot_from_device / read_tensor_slot_to_device
+// (cuda_kv_cache.rs:258-294), which copy one slot per cuMemcpyDtoD (the MLA
+// forward pass calls them per token, cuda_mla.rs:256-271).
+int32_t tensor_slots(sgl_rocm_kv_ctx *ctx, const sgl_kv_paged_layout *layout,
+                     const sgl_kv_device_buffer *pool, uint64_t layer, uint64_t tensor,
+                     const sgl_kv_device_buffer *slots, uint64_t count,
+                     const sgl_kv_device_buffer *rows, uint64_t rows_offset, uint64_t rows_stride,
+                     bool write, void *stream) {
+    int32_t rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!layout || !pool || !rows)
+        return fail(SGL_KV_INVALID_ARGUMENT, "layout/pool/rows", 0, 0, 0, "null argument");
+    if (pool->byte_len < layout->total_byte_len)
+        return out_of_bounds("pool", 0, layout->total_byte_len, pool->byte_len);
+    sgl_kv_pool_view v;
+    if ((rc = sgl_kv_pool_view_for_layer(layout, pool->ptr, pool->byte_len, SGL_KV_NHD, 1, layer,
+                                         tensor, 1, &v)))
+        return rc;
+    if (rows_offset > rows->byte_len) return out_of_bounds(write ? "source" : "destination",
+                                                           rows_offset, 0, rows->byte_len);
+    sgl_kv_rows_view r;
+    memset(&r, 0, sizeof r);
+    r.planes[0] = rows->ptr ? static_cast<char *>(rows->ptr) + rows_offset : nullptr;
+    r.plane_bytes[0] = rows->byte_len - rows_offset;
+    r.row_stride[0] = rows_stride;
+    Launch l;
+    rc = write ? prepare_unpack(ctx, &r, count, &v, slots, &l) : prepare_pack(ctx, &v, slots, count, &r, &l);
+    if (rc) return rc;
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    rc = submit_launch(ctx, l, static_cast<hipStream_t>(stream));
+    return rc ? rc : ok();
+}
+
+}  // namespace
+
+extern "C" int32_t sgl_rocm_kv_write_tensor_slots(sgl_rocm_kv_ctx *ctx, const sgl_kv_paged_layout *layout,
+                                                  const sgl_kv_device_buffer *pool, uint64_t layer,
+                                                  uint64_t tensor, const sgl_kv_device_buffer *slots,
+                                                  uint64_t count, const sgl_kv_device_buffer *source,
+                                                  uint64_t source_offset, uint64_t source_row_stride,
+                                                  void *stream) {
+    return tensor_slots(ctx, layout, pool, layer, tensor, slots, count, source, source_offset,
+                        source_row_stride, true, stream);
+}
+
+extern "C" int32_t sgl_rocm_kv_read_tensor_slots(sgl_rocm_kv_ctx *ctx, const sgl_kv_paged_layout *layout,
+                                                 const sgl_kv_device_buffer *pool, uint64_t layer,
+                                                 uint64_t tensor, const sgl_kv_device_buffer *slots,
+                                                 uint64_t count, const sgl_kv_device_buffer *destination,
+                                                 uint64_t destination_offset,
+                                                 uint64_t destination_row_stride, void *stream) {
+    return tensor_slots(ctx, layout, pool, layer, tensor, slots, count, destination,
+                        destination_offset, destination_row_stride, false, stream);
+}
+
 namespace sglkv {
 
 // Pool -> pool over `layers` consecutive layers (layer i of a side: its

@@ -262,6 +262,16 @@ _EXPORTS = {
                                                    ctypes.c_uint32, _u64, ctypes.POINTER(PoolView),
                                                    _u64, ctypes.POINTER(_DeviceBuffer),
                                                    ctypes.c_void_p]),
+    "sgl_rocm_kv_write_tensor_slots": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_PagedLayout),
+                                                        ctypes.POINTER(_DeviceBuffer), _u64, _u64,
+                                                        ctypes.POINTER(_DeviceBuffer), _u64,
+                                                        ctypes.POINTER(_DeviceBuffer), _u64, _u64,
+                                                        ctypes.c_void_p]),
+    "sgl_rocm_kv_read_tensor_slots": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_PagedLayout),
+                                                       ctypes.POINTER(_DeviceBuffer), _u64, _u64,
+                                                       ctypes.POINTER(_DeviceBuffer), _u64,
+                                                       ctypes.POINTER(_DeviceBuffer), _u64, _u64,
+                                                       ctypes.c_void_p]),
     "sgl_rocm_kv_transfer_layers": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(PoolView), _u64,
                                                      ctypes.c_uint32, ctypes.POINTER(_DeviceBuffer),
                                                      _u64, ctypes.POINTER(PoolView), _u64,
@@ -412,6 +422,10 @@ class PagedKvCacheLayout:
     @property
     def bytes_per_token_per_tensor(self):
         return None if self._c.tensor_pair else self._c.token_bytes[0]
+
+    def tensor_token_bytes(self, tensor: int) -> int:
+        """Bytes of one token of `tensor` in one layer (per-tensor width of a pair layout)."""
+        return self._c.token_bytes[min(tensor, 1)]
 
     @property
     def bytes_per_tensor_page(self):
@@ -729,6 +743,31 @@ class RocmKvPairCopyKernels:
         """Unpack `layer_count` consecutive layers in one launch."""
         _call(lib().sgl_rocm_kv_unpack_layers, self._h, ctypes.byref(src), rows_layer_stride,
               layer_count, row_count, ctypes.byref(dst), pool_layer_stride, ctypes.byref(slots),
+              _stream(stream))
+
+    def write_tensor_slots(self, layout: "PagedKvCacheLayout", pool: _DeviceBuffer, layer: int,
+                           tensor: int, slots: _DeviceBuffer, count: int, source: _DeviceBuffer,
+                           source_offset: int = 0, source_row_stride: int | None = None,
+                           stream=None):
+        """Batched CudaKvStorage::write_tensor_slot_from_device: rows
+        source_offset + i * stride -> (layer, tensor, slots[i]) of the pool.
+        The stride defaults to the tensor's token width."""
+        if source_row_stride is None:
+            source_row_stride = layout.tensor_token_bytes(tensor)
+        _call(lib().sgl_rocm_kv_write_tensor_slots, self._h, ctypes.byref(layout._c),
+              ctypes.byref(pool), layer, tensor, ctypes.byref(slots), count, ctypes.byref(source),
+              source_offset, source_row_stride, _stream(stream))
+
+    def read_tensor_slots(self, layout: "PagedKvCacheLayout", pool: _DeviceBuffer, layer: int,
+                          tensor: int, slots: _DeviceBuffer, count: int, destination: _DeviceBuffer,
+                          destination_offset: int = 0, destination_row_stride: int | None = None,
+                          stream=None):
+        """Batched CudaKvStorage::read_tensor_slot_to_device."""
+        if destination_row_stride is None:
+            destination_row_stride = layout.tensor_token_bytes(tensor)
+        _call(lib().sgl_rocm_kv_read_tensor_slots, self._h, ctypes.byref(layout._c),
+              ctypes.byref(pool), layer, tensor, ctypes.byref(slots), count,
+              ctypes.byref(destination), destination_offset, destination_row_stride,
               _stream(stream))
 
     def transfer_layer(self, src: PoolView, src_slots: _DeviceBuffer, row_count: int,

@@ -112,14 +112,27 @@ typedef enum sgl_kv_status {
     SGL_KV_ALLOC_ZERO_PAGE_SIZE = 70,
     SGL_KV_ALLOC_ZERO_SLOT_CAPACITY = 71,
     SGL_KV_ALLOC_SLOT_CAPACITY_NOT_PAGE_ALIGNED = 72, /* a = slot_capacity, b = page_size */
-    SGL_KV_ALLOC_OUT_OF_SLOTS = 73                    /* a = requested, b = available */
+    SGL_KV_ALLOC_OUT_OF_SLOTS = 73,                   /* a = requested, b = available */
+
+    /* 80.. mirror CudaBf16PagedAttentionError (crates/sglang-kernel/src/cuda_attention.rs:518-564)
+     * and CudaPagedAttentionError's plan variants (crates/sglang-srt/src/cuda_attention.rs:15-75);
+     * ZeroDimension, ShapeOverflow, DimensionTooLarge, TensorPageRegionOutOfBounds and
+     * DeviceMismatch reuse codes 1, 2, 3, 5 and 7. */
+    SGL_KV_ATTN_INVALID_SCALE = 80,                   /* a = the scale's f32 bits */
+    SGL_KV_ATTN_QUERY_HEADS_NOT_DIVISIBLE = 81,       /* a = query_head_count, b = kv_head_count */
+    SGL_KV_ATTN_KEY_ROW_BYTES_MISMATCH = 82,          /* a = expected, b = actual */
+    SGL_KV_ATTN_VALUE_ROW_BYTES_MISMATCH = 83,        /* a = expected, b = actual */
+    SGL_KV_ATTN_TENSOR_PAGE_REGIONS_OVERLAP = 84,     /* a = key_offset, b = value_offset, c = key_page_bytes, d = value_page_bytes */
+    SGL_KV_ATTN_DEVICE_METADATA_INVALID = 85,         /* a = flags: request 0x1, sequence 0x2, slot 0x4 */
+    SGL_KV_ATTN_UNSUPPORTED_KV_DTYPE = 86,            /* a = actual dtype, b = required */
+    SGL_KV_ATTN_TENSOR_ROW_GEOMETRY_MISMATCH = 87     /* name = tensor, a = row_bytes, b = kv_head_count, c = element_bytes */
 } sgl_kv_status;
 
 /* Detail of the calling thread's most recent failure. */
 typedef struct sgl_kv_error_detail {
     int32_t code;          /* sgl_kv_status */
     int32_t reserved;
-    uint64_t a, b, c;      /* variant fields, in the order listed above */
+    uint64_t a, b, c, d;   /* variant fields, in the order listed above */
     char name[64];         /* dimension / tensor / field / allocation / call name */
     char message[320];     /* human-readable text, as the reference's Display impl */
 } sgl_kv_error_detail;
@@ -588,6 +601,87 @@ int32_t sgl_rocm_kv_execute_page_requests(sgl_rocm_kv_ctx *ctx,
                                           const sgl_kv_device_buffer *source_region,
                                           const sgl_kv_device_buffer *target_region,
                                           uint32_t offsets_are_addresses, void *stream);
+
+/* ---- Paged attention over bf16 K/V pages ----
+ * The reader of the pools the copies write: CudaBf16PagedAttentionKernels
+ * (crates/sglang-kernel/src/cuda_attention.rs:10-850) with the same plan,
+ * metadata and results, plus head-major (HND) pages, which the reference's
+ * kernel cannot read. Query q of request r attends the first
+ * query_sequence_lengths[q] slots of
+ * sequence_slots[request_slot_offsets[r] .. request_slot_offsets[r+1]);
+ * query head h reads KV head h / (query_head_count / kv_head_count). */
+typedef struct sgl_kv_attention_layout {   /* CudaBf16PagedAttentionLayout (:157-236) */
+    uint64_t page_size;
+    uint64_t page_stride_bytes;
+    uint64_t key_in_page_offset;
+    uint64_t value_in_page_offset;
+    uint64_t key_row_bytes;    /* kv_head_count * query_key_head_dim * 2 */
+    uint64_t value_row_bytes;  /* kv_head_count * value_head_dim * 2 */
+    uint32_t head_layout;      /* SGL_KV_NHD (the reference's) or SGL_KV_HND */
+    uint32_t reserved;
+} sgl_kv_attention_layout;
+
+typedef struct sgl_kv_attention_plan_config {  /* CudaBf16PagedAttentionPlanConfig (:263-275) */
+    uint64_t query_count;
+    uint64_t request_count;
+    uint64_t sequence_slot_count;
+    uint64_t slot_count;
+    uint64_t query_head_count;
+    uint64_t kv_head_count;
+    uint64_t query_key_head_dim;
+    uint64_t value_head_dim;
+    float scale;
+    uint32_t reserved;
+    sgl_kv_attention_layout layout;
+} sgl_kv_attention_plan_config;
+
+typedef struct sgl_kv_attention_plan {  /* CudaBf16PagedAttentionPlan (:239-261) */
+    sgl_kv_attention_plan_config config;
+    uint64_t query_required_bytes;
+    uint64_t query_request_indices_required_bytes;
+    uint64_t query_sequence_lengths_required_bytes;
+    uint64_t request_slot_offsets_required_bytes;
+    uint64_t sequence_slots_required_bytes;
+    uint64_t pool_required_bytes;
+    uint64_t output_required_bytes;
+} sgl_kv_attention_plan;
+
+/* CudaBf16PagedAttentionLaunch (:659-674): queries bf16 [query][head][dk];
+ * query_request_indices u32; query_sequence_lengths u64;
+ * request_slot_offsets u64 (request_count + 1); sequence_slots u64; output
+ * bf16 [query][head][dv]. */
+typedef struct sgl_kv_attention_buffers {
+    sgl_kv_device_buffer queries;                uint64_t queries_offset;
+    sgl_kv_device_buffer query_request_indices;  uint64_t query_request_indices_offset;
+    sgl_kv_device_buffer query_sequence_lengths; uint64_t query_sequence_lengths_offset;
+    sgl_kv_device_buffer request_slot_offsets;   uint64_t request_slot_offsets_offset;
+    sgl_kv_device_buffer sequence_slots;         uint64_t sequence_slots_offset;
+    sgl_kv_device_buffer pool;                   uint64_t pool_offset;
+    sgl_kv_device_buffer output;                 uint64_t output_offset;
+} sgl_kv_attention_buffers;
+
+/* CudaBf16PagedAttentionPlan::new (cuda_attention.rs:277-430): same checks,
+ * same order, same variants. HND pools must hold the last page's whole key
+ * and value regions. */
+int32_t sgl_kv_attention_plan_new(const sgl_kv_attention_plan_config *config,
+                                  sgl_kv_attention_plan *out);
+/* build_plan (crates/sglang-srt/src/cuda_attention.rs:505-572): the plan for
+ * layer `layer` of a bf16 pool (UnsupportedKvDtype otherwise). */
+int32_t sgl_kv_attention_plan_for_layer(const sgl_kv_paged_layout *layout, uint64_t layer,
+                                        uint64_t query_count, uint64_t request_count,
+                                        uint64_t sequence_slot_count, uint64_t query_head_count,
+                                        float scale, uint32_t head_layout,
+                                        sgl_kv_attention_plan *out);
+/* CudaBf16PagedAttentionKernels::forward (cuda_attention.rs:681-850):
+ * checks devices and ranges, clears the error word, runs, synchronises
+ * `stream` and reports bad metadata as SGL_KV_ATTN_DEVICE_METADATA_INVALID
+ * (the outputs of the affected queries are then unspecified).
+ * max_sequence_length (0 = unknown) bounds the query lengths and only
+ * steers how sequences are split across workgroups. Long sequences use a
+ * context-owned workspace, grown on demand. */
+int32_t sgl_rocm_kv_paged_attention(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *plan,
+                                    const sgl_kv_attention_buffers *buffers,
+                                    uint64_t max_sequence_length, void *stream);
 
 /* ---- Transfer backend: KvTransferBackend (transfer.rs:1145-1151) ----
  * register / submit / poll / cancel / shutdown for a prefill pool and a

@@ -4,8 +4,10 @@ TEST INFRASTRUCTURE: only tests/, ``__graft_entry__.smoke()`` and bench.py's
 ``cpu_baseline`` leg import this package, and only as the checker. The
 product library never loads it.
 
-The C sources (kv_oracle.c) restate the reference algorithm; the functions
-here only marshal numpy arrays. Build with ``make -C oracle``.
+The C sources (kv_oracle.c) restate the reference's byte-movement
+algorithm; the functions here marshal numpy arrays to them. The paged
+attention restatement (floating point) is numpy, in float64. Build with
+``make -C oracle``.
 """
 from __future__ import annotations
 
@@ -239,3 +241,74 @@ def f32_to_bf16(values: np.ndarray) -> np.ndarray:
     out = np.empty(v.shape, dtype=np.uint16)
     lib().ora_f32_to_bf16(_p(v, ctypes.c_float), _p(out, ctypes.c_uint16), v.size)
     return out
+
+
+# --- paged attention (float64 restatement, test infrastructure) -------------------------------
+
+FLAG_ATTN_REQUEST = 1
+FLAG_ATTN_SEQUENCE = 2
+FLAG_ATTN_SLOT = 4
+
+
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    """bf16 bit patterns -> float32 (exact)."""
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
+def paged_attention(pool: np.ndarray, queries: np.ndarray, query_request_indices,
+                    query_sequence_lengths, request_slot_offsets, sequence_slots, *,
+                    page_size: int, page_stride: int, key_offset: int, value_offset: int,
+                    kv_heads: int, dk: int, dv: int, scale: float, slot_count: int,
+                    hnd: bool = False):
+    """sglang_paged_attention_bf16 (crates/sglang-kernel/src/cuda_attention.rs:
+    14-155) in float64: for query q of request r, softmax(scale * q.k) . v over
+    the first len_q slots of r's slot list; query head h reads KV head
+    h // (query_heads // kv_heads). Keys of KV head g at slot s start at byte
+    (s // P) * page_stride + key_offset + (NHD) (s % P) * kv_heads*dk*2 + g*dk*2
+    or (HND) g*P*dk*2 + (s % P)*dk*2; values alike.
+
+    `pool` is the pool's bytes (uint8), `queries` bf16 bits [Q][QH][dk].
+    Returns (out float64 [Q][QH][dv] with NaN rows for rejected queries,
+    flags): the reference's metadata checks (:59-82) and slot check (:96-99)
+    set flag bits 1, 2, 4 and skip the query.
+    """
+    q_bits = np.asarray(queries, dtype=np.uint16)
+    nq, qh, _ = q_bits.shape
+    group = qh // kv_heads
+    pool16 = np.asarray(pool, dtype=np.uint8).view(np.uint16)
+    qri = np.asarray(query_request_indices, dtype=np.uint64)
+    qsl = np.asarray(query_sequence_lengths, dtype=np.uint64)
+    rso = np.asarray(request_slot_offsets, dtype=np.uint64)
+    slots_all = np.asarray(sequence_slots, dtype=np.uint64)
+    request_count = len(rso) - 1
+    out = np.full((nq, qh, dv), np.nan)
+    flags = 0
+    for q in range(nq):
+        r = int(qri[q])
+        if r >= request_count:
+            flags |= FLAG_ATTN_REQUEST
+            continue
+        s0, s1, n = int(rso[r]), int(rso[r + 1]), int(qsl[q])
+        if s0 > s1 or s1 > len(slots_all) or n == 0 or n > s1 - s0:
+            flags |= FLAG_ATTN_SEQUENCE
+            continue
+        sl = slots_all[s0:s0 + n].astype(np.int64)
+        if (sl >= slot_count).any():
+            flags |= FLAG_ATTN_SLOT
+            continue
+        page, pos = sl // page_size, sl % page_size
+        for g in range(kv_heads):
+            if hnd:
+                kbyte = page * page_stride + key_offset + g * page_size * dk * 2 + pos * dk * 2
+                vbyte = page * page_stride + value_offset + g * page_size * dv * 2 + pos * dv * 2
+            else:
+                kbyte = page * page_stride + key_offset + pos * kv_heads * dk * 2 + g * dk * 2
+                vbyte = page * page_stride + value_offset + pos * kv_heads * dv * 2 + g * dv * 2
+            k = bf16_to_f32(pool16[(kbyte // 2)[:, None] + np.arange(dk)]).astype(np.float64)
+            v = bf16_to_f32(pool16[(vbyte // 2)[:, None] + np.arange(dv)]).astype(np.float64)
+            qv = bf16_to_f32(q_bits[q, g * group:(g + 1) * group]).astype(np.float64)
+            s = (qv @ k.T) * scale
+            s -= s.max(axis=1, keepdims=True)
+            w = np.exp(s)
+            out[q, g * group:(g + 1) * group] = (w @ v) / w.sum(axis=1, keepdims=True)
+    return out, flags

@@ -1,0 +1,378 @@
+// kv_attention.cpp -- host side of the paged-attention reader: the plan
+// (CudaBf16PagedAttentionPlan::new, crates/sglang-kernel/src/
+// cuda_attention.rs:277-430, same validation order and error variants),
+// the plan derived from a pool layout (build_plan,
+// crates/sglang-srt/src/cuda_attention.rs:505-572) and the launch
+// (CudaBf16PagedAttentionKernels::forward, cuda_attention.rs:681-850:
+// device and range checks, clear the error word, launch, synchronise, read
+// the word).
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <string.h>
+
+#include "kv_internal.h"
+
+using namespace sglkv;
+
+namespace {
+
+int32_t attn_overflow() {
+    return fail(SGL_KV_SHAPE_OVERFLOW, nullptr, 0, 0, 0, "CUDA paged attention shape overflowed");
+}
+
+int32_t region_end(const char *tensor, uint64_t offset, uint64_t page_bytes, uint64_t stride,
+                   uint64_t *end) {
+    if (add_ovf(offset, page_bytes, end)) return attn_overflow();
+    if (*end > stride)
+        return fail(SGL_KV_TENSOR_PAGE_REGION_OUT_OF_BOUNDS, tensor, offset, page_bytes, stride,
+                    "CUDA paged attention %s page region [%llu, %llu) exceeds page stride %llu", tensor,
+                    (unsigned long long)offset, (unsigned long long)*end, (unsigned long long)stride);
+    return SGL_KV_OK;
+}
+
+}  // namespace
+
+extern "C" int32_t sgl_kv_attention_plan_new(const sgl_kv_attention_plan_config *c,
+                                             sgl_kv_attention_plan *out) {
+    if (!c || !out) return fail(SGL_KV_INVALID_ARGUMENT, "config/out", 0, 0, 0, "null argument");
+    const sgl_kv_attention_layout &lay = c->layout;
+    const struct {
+        const char *name;
+        uint64_t value;
+    } dims[] = {{"query_count", c->query_count},
+                {"request_count", c->request_count},
+                {"sequence_slot_count", c->sequence_slot_count},
+                {"slot_count", c->slot_count},
+                {"query_head_count", c->query_head_count},
+                {"kv_head_count", c->kv_head_count},
+                {"query_key_head_dim", c->query_key_head_dim},
+                {"value_head_dim", c->value_head_dim},
+                {"page_size", lay.page_size},
+                {"page_stride_bytes", lay.page_stride_bytes},
+                {"key_row_bytes", lay.key_row_bytes},
+                {"value_row_bytes", lay.value_row_bytes}};
+    for (const auto &d : dims)
+        if (d.value == 0)
+            return fail(SGL_KV_ZERO_DIMENSION, d.name, 0, 0, 0,
+                        "CUDA paged attention dimension %s must be non-zero", d.name);
+    if (!isfinite(c->scale) || c->scale <= 0.0f) {
+        uint32_t bits;
+        memcpy(&bits, &c->scale, sizeof bits);
+        return fail(SGL_KV_ATTN_INVALID_SCALE, nullptr, bits, 0, 0,
+                    "CUDA paged attention scale must be finite and positive, got %g", (double)c->scale);
+    }
+    if (c->query_head_count % c->kv_head_count)
+        return fail(SGL_KV_ATTN_QUERY_HEADS_NOT_DIVISIBLE, nullptr, c->query_head_count,
+                    c->kv_head_count, 0,
+                    "CUDA paged attention query head count %llu is not divisible by KV head count %llu",
+                    (unsigned long long)c->query_head_count, (unsigned long long)c->kv_head_count);
+    uint64_t want;
+    if (mul_ovf(c->kv_head_count, c->query_key_head_dim, &want) || mul_ovf(want, 2, &want))
+        return attn_overflow();
+    if (lay.key_row_bytes != want)
+        return fail(SGL_KV_ATTN_KEY_ROW_BYTES_MISMATCH, nullptr, want, lay.key_row_bytes, 0,
+                    "CUDA BF16 paged attention requires %llu bytes per KV row, layout has %llu",
+                    (unsigned long long)want, (unsigned long long)lay.key_row_bytes);
+    if (mul_ovf(c->kv_head_count, c->value_head_dim, &want) || mul_ovf(want, 2, &want))
+        return attn_overflow();
+    if (lay.value_row_bytes != want)
+        return fail(SGL_KV_ATTN_VALUE_ROW_BYTES_MISMATCH, nullptr, want, lay.value_row_bytes, 0,
+                    "CUDA BF16 paged attention requires %llu bytes per value row, layout has %llu",
+                    (unsigned long long)want, (unsigned long long)lay.value_row_bytes);
+    uint64_t key_page, value_page, key_end, value_end;
+    if (mul_ovf(lay.page_size, lay.key_row_bytes, &key_page) ||
+        mul_ovf(lay.page_size, lay.value_row_bytes, &value_page))
+        return attn_overflow();
+    int32_t rc;
+    if ((rc = region_end("key", lay.key_in_page_offset, key_page, lay.page_stride_bytes, &key_end)) ||
+        (rc = region_end("value", lay.value_in_page_offset, value_page, lay.page_stride_bytes, &value_end)))
+        return rc;
+    if (lay.key_in_page_offset < value_end && lay.value_in_page_offset < key_end) {
+        rc = fail(SGL_KV_ATTN_TENSOR_PAGE_REGIONS_OVERLAP, nullptr, lay.key_in_page_offset,
+                  lay.value_in_page_offset, key_page,
+                  "CUDA paged attention key/value page regions overlap: key offset %llu (%llu bytes), "
+                  "value offset %llu (%llu bytes)",
+                  (unsigned long long)lay.key_in_page_offset, (unsigned long long)key_page,
+                  (unsigned long long)lay.value_in_page_offset, (unsigned long long)value_page);
+        set_detail_d(value_page);
+        return rc;
+    }
+    if (lay.head_layout > SGL_KV_HND)
+        return fail(SGL_KV_INVALID_ARGUMENT, "head_layout", lay.head_layout, 0, 0,
+                    "unknown head layout %u", lay.head_layout);
+
+    sgl_kv_attention_plan p;
+    memset(&p, 0, sizeof p);
+    p.config = *c;
+    uint64_t v;
+    if (mul_ovf(c->query_count, c->query_head_count, &v) || mul_ovf(v, c->query_key_head_dim, &v) ||
+        mul_ovf(v, 2, &p.query_required_bytes))
+        return attn_overflow();
+    if (mul_ovf(c->query_count, 4, &p.query_request_indices_required_bytes) ||
+        mul_ovf(c->query_count, 8, &p.query_sequence_lengths_required_bytes) ||
+        add_ovf(c->request_count, 1, &v) || mul_ovf(v, 8, &p.request_slot_offsets_required_bytes) ||
+        mul_ovf(c->sequence_slot_count, 8, &p.sequence_slots_required_bytes))
+        return attn_overflow();
+    // The pool must reach the last slot's key and value rows (NHD, as the
+    // reference computes it) or, for head-major pages, the last page's
+    // whole key and value regions.
+    const uint64_t last_slot = c->slot_count - 1;
+    const uint64_t last_page = last_slot / lay.page_size, last_token = last_slot % lay.page_size;
+    uint64_t kend, vend;
+    if (lay.head_layout == SGL_KV_HND) {
+        kend = key_end;
+        vend = value_end;
+    } else if (mul_ovf(last_token, lay.key_row_bytes, &kend) ||
+               add_ovf(kend, lay.key_in_page_offset, &kend) || add_ovf(kend, lay.key_row_bytes, &kend) ||
+               mul_ovf(last_token, lay.value_row_bytes, &vend) ||
+               add_ovf(vend, lay.value_in_page_offset, &vend) ||
+               add_ovf(vend, lay.value_row_bytes, &vend)) {
+        return attn_overflow();
+    }
+    if (mul_ovf(last_page, lay.page_stride_bytes, &v) ||
+        add_ovf(v, kend > vend ? kend : vend, &p.pool_required_bytes))
+        return attn_overflow();
+    if (mul_ovf(c->query_count, c->query_head_count, &v) || mul_ovf(v, c->value_head_dim, &v) ||
+        mul_ovf(v, 2, &p.output_required_bytes))
+        return attn_overflow();
+    // The reference sizes its block's shared memory as (256 + dv) floats and
+    // launches one block per (query, head); keep its limits.
+    if (add_ovf(256, c->value_head_dim, &v) || mul_ovf(v, 4, &v) || v > UINT32_MAX) return attn_overflow();
+    if (c->query_count > UINT32_MAX)
+        return too_large_dim("query_count", c->query_count, UINT32_MAX);
+    if (c->query_head_count > UINT32_MAX)
+        return too_large_dim("query_head_count", c->query_head_count, UINT32_MAX);
+    *out = p;
+    return ok();
+}
+
+// build_plan (crates/sglang-srt/src/cuda_attention.rs:505-572): the
+// attention geometry of one layer of a bf16 pool.
+extern "C" int32_t sgl_kv_attention_plan_for_layer(const sgl_kv_paged_layout *layout, uint64_t layer,
+                                                   uint64_t query_count, uint64_t request_count,
+                                                   uint64_t sequence_slot_count,
+                                                   uint64_t query_head_count, float scale,
+                                                   uint32_t head_layout, sgl_kv_attention_plan *out) {
+    if (!layout || !out) return fail(SGL_KV_INVALID_ARGUMENT, "layout/out", 0, 0, 0, "null argument");
+    const sgl_kv_runtime_layout &rt = layout->runtime;
+    if (rt.dtype != SGL_KV_DTYPE_BFLOAT16) {
+        static const char *const names[] = {"Auto", "Float32", "Bfloat16", "Fp8E4M3", "Fp8E5M2", "Fp4E2M1"};
+        const char *name = rt.dtype >= 0 && rt.dtype <= 5 ? names[rt.dtype] : "unknown";
+        return fail(SGL_KV_ATTN_UNSUPPORTED_KV_DTYPE, nullptr, (uint64_t)(int64_t)rt.dtype,
+                    SGL_KV_DTYPE_BFLOAT16, 0,
+                    "CUDA paged attention requires KV cache dtype Bfloat16, found %s", name);
+    }
+    uint64_t start, end, key_row, value_row;
+    int32_t rc;
+    if ((rc = sgl_kv_paged_layout_tensor_token_byte_range(layout, 0, layer, 0, 0, &start, &end)))
+        return rc;
+    key_row = end - start;
+    const uint64_t key_offset = start;
+    if ((rc = sgl_kv_paged_layout_tensor_token_byte_range(layout, 0, layer, 1, 0, &start, &end)))
+        return rc;
+    value_row = end - start;
+    const uint64_t value_offset = start;
+    uint64_t denom;
+    if (mul_ovf(rt.kv_heads, 2, &denom) || key_row % denom)
+        return fail(SGL_KV_ATTN_TENSOR_ROW_GEOMETRY_MISMATCH, "key", key_row, rt.kv_heads, 2,
+                    "CUDA paged attention key row has %llu bytes, which cannot be divided across %llu "
+                    "heads of 2-byte elements",
+                    (unsigned long long)key_row, (unsigned long long)rt.kv_heads);
+    if (value_row % denom)
+        return fail(SGL_KV_ATTN_TENSOR_ROW_GEOMETRY_MISMATCH, "value", value_row, rt.kv_heads, 2,
+                    "CUDA paged attention value row has %llu bytes, which cannot be divided across %llu "
+                    "heads of 2-byte elements",
+                    (unsigned long long)value_row, (unsigned long long)rt.kv_heads);
+    sgl_kv_attention_plan_config c;
+    memset(&c, 0, sizeof c);
+    c.query_count = query_count;
+    c.request_count = request_count;
+    c.sequence_slot_count = sequence_slot_count;
+    c.slot_count = layout->slot_count;
+    c.query_head_count = query_head_count;
+    c.kv_head_count = rt.kv_heads;
+    c.query_key_head_dim = key_row / denom;
+    c.value_head_dim = value_row / denom;
+    c.scale = scale;
+    c.layout.page_size = rt.page_size;
+    c.layout.page_stride_bytes = rt.page_size_bytes;
+    c.layout.key_in_page_offset = key_offset;
+    c.layout.value_in_page_offset = value_offset;
+    c.layout.key_row_bytes = key_row;
+    c.layout.value_row_bytes = value_row;
+    c.layout.head_layout = head_layout;
+    return sgl_kv_attention_plan_new(&c, out);
+}
+
+namespace {
+
+int32_t attn_ptr(const char *name, const sgl_kv_device_buffer &b, uint64_t offset, uint64_t need,
+                 uint64_t *addr) {
+    if (!b.ptr) return fail(SGL_KV_INVALID_ARGUMENT, name, 0, 0, 0, "null buffer %s", name);
+    uint64_t end;
+    if (add_ovf(offset, need, &end) || end > b.byte_len)
+        return fail(SGL_KV_ALLOCATION_OUT_OF_BOUNDS, name, offset, need, b.byte_len,
+                    "allocation %s range [%llu, +%llu) exceeds its %llu bytes", name,
+                    (unsigned long long)offset, (unsigned long long)need,
+                    (unsigned long long)b.byte_len);
+    *addr = (uint64_t)(uintptr_t)b.ptr + offset;
+    return SGL_KV_OK;
+}
+
+uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
+
+}  // namespace
+
+extern "C" int32_t sgl_rocm_kv_paged_attention(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *plan,
+                                               const sgl_kv_attention_buffers *b,
+                                               uint64_t max_sequence_length, void *stream) {
+    if (!ctx || !plan || !b)
+        return fail(SGL_KV_INVALID_ARGUMENT, "ctx/plan/buffers", 0, 0, 0, "null argument");
+    const sgl_kv_attention_plan_config &c = plan->config;
+    const sgl_kv_attention_layout &lay = c.layout;
+    const struct {
+        const char *name;
+        const sgl_kv_device_buffer *buf;
+    } all[] = {{"queries", &b->queries},
+               {"query_request_indices", &b->query_request_indices},
+               {"query_sequence_lengths", &b->query_sequence_lengths},
+               {"request_slot_offsets", &b->request_slot_offsets},
+               {"sequence_slots", &b->sequence_slots},
+               {"pool", &b->pool},
+               {"output", &b->output}};
+    int32_t rc;
+    for (const auto &a : all)
+        if ((rc = check_device(ctx, a.name, *a.buf))) return rc;
+    uint64_t qp, rip, slp, rop, ssp, poolp, outp;
+    if ((rc = attn_ptr("queries", b->queries, b->queries_offset, plan->query_required_bytes, &qp)) ||
+        (rc = attn_ptr("query_request_indices", b->query_request_indices, b->query_request_indices_offset,
+                       plan->query_request_indices_required_bytes, &rip)) ||
+        (rc = attn_ptr("query_sequence_lengths", b->query_sequence_lengths,
+                       b->query_sequence_lengths_offset, plan->query_sequence_lengths_required_bytes,
+                       &slp)) ||
+        (rc = attn_ptr("request_slot_offsets", b->request_slot_offsets, b->request_slot_offsets_offset,
+                       plan->request_slot_offsets_required_bytes, &rop)) ||
+        (rc = attn_ptr("sequence_slots", b->sequence_slots, b->sequence_slots_offset,
+                       plan->sequence_slots_required_bytes, &ssp)) ||
+        (rc = attn_ptr("pool", b->pool, b->pool_offset, plan->pool_required_bytes, &poolp)) ||
+        (rc = attn_ptr("output", b->output, b->output_offset, plan->output_required_bytes, &outp)))
+        return rc;
+    if (c.query_key_head_dim > SGLKV_ATTN_MAX_DK)
+        return too_large_dim("query_key_head_dim", c.query_key_head_dim, SGLKV_ATTN_MAX_DK);
+    // Every element access is naturally aligned.
+    const bool aligned = qp % 2 == 0 && outp % 2 == 0 && rip % 4 == 0 && slp % 8 == 0 && rop % 8 == 0 &&
+                         ssp % 8 == 0 &&
+                         ((poolp | lay.key_in_page_offset | lay.value_in_page_offset |
+                           lay.page_stride_bytes | lay.key_row_bytes | lay.value_row_bytes) & 1) == 0;
+    if (!aligned)
+        return fail(SGL_KV_INVALID_ARGUMENT, "alignment", 0, 0, 0,
+                    "paged attention buffers must be aligned to their element sizes");
+
+    sglkv_attn_params p;
+    memset(&p, 0, sizeof p);
+    p.queries = reinterpret_cast<const uint16_t *>(qp);
+    p.query_request_indices = reinterpret_cast<const uint32_t *>(rip);
+    p.query_sequence_lengths = reinterpret_cast<const uint64_t *>(slp);
+    p.request_slot_offsets = reinterpret_cast<const uint64_t *>(rop);
+    p.sequence_slots = reinterpret_cast<const uint64_t *>(ssp);
+    p.pool = reinterpret_cast<const uint8_t *>(poolp);
+    p.output = reinterpret_cast<uint16_t *>(outp);
+    p.flag = ctx->flag;
+    p.query_count = c.query_count;
+    p.request_count = c.request_count;
+    p.sequence_slot_count = c.sequence_slot_count;
+    p.slot_count = c.slot_count;
+    p.page_size = lay.page_size;
+    p.page_stride = lay.page_stride_bytes;
+    p.key_offset = lay.key_in_page_offset;
+    p.value_offset = lay.value_in_page_offset;
+    const uint64_t kh = c.query_key_head_dim * 2, vh = c.value_head_dim * 2;
+    if (lay.head_layout == SGL_KV_HND) {
+        p.key_head_stride = lay.page_size * kh;
+        p.key_token_stride = kh;
+        p.value_head_stride = lay.page_size * vh;
+        p.value_token_stride = vh;
+    } else {
+        p.key_head_stride = kh;
+        p.key_token_stride = lay.key_row_bytes;
+        p.value_head_stride = vh;
+        p.value_token_stride = lay.value_row_bytes;
+    }
+    p.query_heads = (uint32_t)c.query_head_count;
+    p.kv_heads = (uint32_t)c.kv_head_count;
+    p.group = (uint32_t)(c.query_head_count / c.kv_head_count);
+    p.head_groups = (uint32_t)ceil_div(p.group, SGLKV_ATTN_HEADS);
+    p.dk = (uint32_t)c.query_key_head_dim;
+    p.dk_pad = (uint32_t)ceil_div(p.dk, 32) * 32;
+    p.dv = (uint32_t)c.value_head_dim;
+    p.dv_blocks = (uint32_t)ceil_div(p.dv, SGLKV_ATTN_DV);
+    p.scale_log2 = c.scale * 1.4426950408889634f;
+
+    // Workgroups before splitting; split each query's sequence so the
+    // launch holds about eight waves per CU.
+    uint64_t base = c.query_count;
+    if (mul_ovf(base, p.kv_heads, &base) || mul_ovf(base, p.head_groups, &base) ||
+        mul_ovf(base, p.dv_blocks, &base) || base > INT32_MAX)
+        return too_large_dim("workgroups", base, INT32_MAX);
+    uint64_t max_len = max_sequence_length ? max_sequence_length : c.sequence_slot_count;
+    if (max_len > c.sequence_slot_count) max_len = c.sequence_slot_count;
+    const uint64_t target = 8ull * (uint64_t)(ctx->cu_count > 0 ? ctx->cu_count : 256);
+    const uint64_t want = base >= target ? 1 : ceil_div(target, base);
+    uint64_t chunk = ceil_div(max_len, want);
+    chunk = ceil_div(chunk < 256 ? 256 : chunk, SGLKV_ATTN_TOKENS) * SGLKV_ATTN_TOKENS;
+    uint64_t splits = ceil_div(max_len, chunk);
+    if (splits > 65535) {  // grid y limit
+        chunk = ceil_div(ceil_div(max_len, 65535), SGLKV_ATTN_TOKENS) * SGLKV_ATTN_TOKENS;
+        splits = ceil_div(max_len, chunk);
+    }
+    p.chunk_tokens = chunk;
+    p.splits = (uint32_t)splits;
+
+    const bool vec = (p.dk % 8 == 0) && (p.dv % 8 == 0) &&
+                     ((poolp + lay.key_in_page_offset) % 16 == 0) &&
+                     ((poolp + lay.value_in_page_offset) % 16 == 0) &&
+                     ((lay.page_stride_bytes | p.key_head_stride | p.key_token_stride | p.value_head_stride |
+                       p.value_token_stride) % 16 == 0);
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    if (splits > 1) {
+        uint64_t bytes;
+        if (mul_ovf(c.query_count * c.query_head_count, splits, &bytes) ||
+            mul_ovf(bytes, (uint64_t)p.dv + 2, &bytes) || mul_ovf(bytes, 4, &bytes))
+            return attn_overflow();
+        if (bytes > ctx->attention_partial_bytes) {
+            if (ctx->attention_partial) {
+                SGLKV_CHECK_HIP(hipDeviceSynchronize());
+                SGLKV_CHECK_HIP(hipFree(ctx->attention_partial));
+                ctx->attention_partial = nullptr;
+                ctx->attention_partial_bytes = 0;
+            }
+            SGLKV_CHECK_HIP(hipMalloc(&ctx->attention_partial, bytes));
+            ctx->attention_partial_bytes = bytes;
+        }
+        p.partial = static_cast<float *>(ctx->attention_partial);
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    SGLKV_CHECK_HIP(hipMemsetAsync(ctx->flag, 0, sizeof(uint32_t), s));
+    const unsigned lds = (unsigned)((SGLKV_ATTN_HEADS * (p.dk_pad + 8) +
+                                     SGLKV_ATTN_DV * SGLKV_ATTN_VT_STRIDE) * sizeof(uint16_t));
+    void *args[] = {&p};
+    SGLKV_CHECK_HIP(hipModuleLaunchKernel(ctx->attention[vec ? 0 : 1], (unsigned)base, (unsigned)splits, 1,
+                                          64, 1, 1, lds, s, args, nullptr));
+    if (splits > 1)
+        SGLKV_CHECK_HIP(hipModuleLaunchKernel(ctx->attention_combine,
+                                              (unsigned)(c.query_count * c.query_head_count), 1, 1, 128,
+                                              1, 1, 0, s, args, nullptr));
+    SGLKV_CHECK_HIP(hipStreamSynchronize(s));
+    uint32_t flag = 0;
+    SGLKV_CHECK_HIP(hipMemcpy(&flag, ctx->flag, sizeof flag, hipMemcpyDeviceToHost));
+    const uint32_t bad = ((flag & SGLKV_FLAG_ATTN_REQUEST) ? 1u : 0u) |
+                         ((flag & SGLKV_FLAG_ATTN_SEQUENCE) ? 2u : 0u) |
+                         ((flag & SGLKV_FLAG_ATTN_SLOT) ? 4u : 0u);
+    if (bad)
+        return fail(SGL_KV_ATTN_DEVICE_METADATA_INVALID, nullptr, bad, 0, 0,
+                    "CUDA paged attention rejected device metadata with error flags 0x%x "
+                    "(request=0x1, sequence=0x2, slot=0x4)",
+                    bad);
+    return ok();
+}

@@ -20,6 +20,8 @@ int32_t fail(int32_t code, const char *name, uint64_t a, uint64_t b, uint64_t c,
              const char *fmt, ...) __attribute__((format(printf, 6, 7)));
 // Clears the detail record and returns SGL_KV_OK.
 int32_t ok();
+// Sets the fourth field of the detail record of the last failure.
+void set_detail_d(uint64_t d);
 
 // Geometry common to both sides of a copy.
 struct RowShape {
@@ -65,11 +67,19 @@ hipStream_t pipeline_final_stream(sgl_rocm_kv_pipeline *pipe);
 int32_t hip_fail(hipError_t err, const char *call);
 int32_t flag_status(uint32_t flag);
 
-inline int32_t too_large_rows(uint64_t rows, uint64_t maximum) {
-    return fail(SGL_KV_DIMENSION_TOO_LARGE, "row_count", rows, maximum, 0,
-                "KV copy dimension row_count=%llu exceeds maximum %llu", (unsigned long long)rows,
+inline int32_t too_large_dim(const char *name, uint64_t value, uint64_t maximum) {
+    return fail(SGL_KV_DIMENSION_TOO_LARGE, name, value, maximum, 0,
+                "KV dimension %s=%llu exceeds maximum %llu", name, (unsigned long long)value,
                 (unsigned long long)maximum);
 }
+
+inline int32_t too_large_rows(uint64_t rows, uint64_t maximum) {
+    return too_large_dim("row_count", rows, maximum);
+}
+
+// CudaKvPairCopyKernels::validate_device (cuda_kv_kernels.rs:625-642):
+// DeviceMismatch unless `b` lives on the context's device.
+int32_t check_device(const sgl_rocm_kv_ctx *ctx, const char *name, const sgl_kv_device_buffer &b);
 
 #define SGLKV_CHECK_HIP(call)                                              \
     do {                                                                   \
@@ -91,7 +101,11 @@ struct sgl_rocm_kv_ctx {
     hipFunction_t resolve;
     hipFunction_t fill;
     hipFunction_t requests;
+    hipFunction_t attention[2];     // 16-byte vector / element-wise loads
+    hipFunction_t attention_combine;
     uint32_t *flag;
+    void *attention_partial;        // split records, grown on demand
+    uint64_t attention_partial_bytes;
     uint32_t rows_per_thread;  // from the code object
     uint32_t max_tile_rows;
 };

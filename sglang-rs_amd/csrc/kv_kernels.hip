@@ -394,3 +394,6 @@ extern "C" __global__ __launch_bounds__(SGLKV_BLOCK_THREADS) void sglkv_copy_req
         for (uint64_t i = threadIdx.x; i < n; i += SGLKV_BLOCK_THREADS) d[i] = s[i];
     }
 }
+
+// The paged-attention reader of the same pools shares this code object.
+#include "kv_attention.hip"

@@ -34,6 +34,8 @@ int32_t ok() {
     return SGL_KV_OK;
 }
 
+void set_detail_d(uint64_t d) { t_last.d = d; }
+
 }  // namespace sglkv
 
 using namespace sglkv;
@@ -70,6 +72,14 @@ extern "C" const char *sgl_kv_status_name(int32_t code) {
     case SGL_KV_LAYOUT_SLOT_OUT_OF_RANGE: return "SlotOutOfRange";
     case SGL_KV_LAYOUT_EMPTY_SLOT_MAP: return "EmptySlotMap";
     case SGL_KV_LAYOUT_BATCH_SLOT_OUT_OF_RANGE: return "BatchSlotOutOfRange";
+    case SGL_KV_ATTN_INVALID_SCALE: return "InvalidScale";
+    case SGL_KV_ATTN_QUERY_HEADS_NOT_DIVISIBLE: return "QueryHeadsNotDivisibleByKvHeads";
+    case SGL_KV_ATTN_KEY_ROW_BYTES_MISMATCH: return "KvRowByteSizeMismatch";
+    case SGL_KV_ATTN_VALUE_ROW_BYTES_MISMATCH: return "ValueRowByteSizeMismatch";
+    case SGL_KV_ATTN_TENSOR_PAGE_REGIONS_OVERLAP: return "TensorPageRegionsOverlap";
+    case SGL_KV_ATTN_DEVICE_METADATA_INVALID: return "DeviceMetadataInvalid";
+    case SGL_KV_ATTN_UNSUPPORTED_KV_DTYPE: return "UnsupportedKvDtype";
+    case SGL_KV_ATTN_TENSOR_ROW_GEOMETRY_MISMATCH: return "TensorRowGeometryMismatch";
     case SGL_KV_LAYOUT_KV_PAIR_REQUIRES_TWO_TENSORS: return "KvPairRequiresTwoTensors";
     case SGL_KV_LAYOUT_TENSOR_PAIR_REQUIRES_TWO_TENSORS: return "TensorPairRequiresTwoTensors";
     case SGL_KV_LAYOUT_TENSOR_PAIR_SIZE_MISMATCH: return "TensorPairSizeMismatch";

@@ -54,6 +54,11 @@
 #define SGLKV_FLAG_PAGE 2u /* a page-table entry out of range while resolving spans */
 #define SGLKV_FLAG_SPAN 4u /* a row not covered by any span */
 #define SGLKV_FLAG_REQUEST 8u /* a page request outside its source or target region */
+/* Paged attention metadata errors (the reference kernel's flag values 1, 2
+ * and 4, cuda_attention.rs:64-98, shifted above the copy flags). */
+#define SGLKV_FLAG_ATTN_REQUEST 16u  /* query_request_indices entry >= request_count */
+#define SGLKV_FLAG_ATTN_SEQUENCE 32u /* request range or query length invalid */
+#define SGLKV_FLAG_ATTN_SLOT 64u     /* a sequence slot >= slot_count */
 
 /* A resolved row offset that must not be touched. */
 #define SGLKV_INVALID_OFFSET 0xFFFFFFFFFFFFFFFFull
@@ -129,5 +134,58 @@ typedef struct sglkv_request_params {
     uint64_t source_lo, source_hi;   /* allowed source bytes [lo, hi) */
     uint64_t target_lo, target_hi;   /* allowed target bytes [lo, hi) */
 } sglkv_request_params;
+
+/* Paged decode/prefill attention over bf16 K/V pages.
+ *
+ * Query q attends the first len_q = query_sequence_lengths[q] slots of its
+ * request's slot list (sequence_slots[request_slot_offsets[r] ..]). Key k of
+ * KV head h at slot s is at
+ *     pool + (s / page_size) * page_stride + key_offset
+ *          + h * key_head_stride + (s % page_size) * key_token_stride
+ * (NHD: head stride = Dk * 2, token stride = key row bytes; HND: head
+ * stride = page_size * Dk * 2, token stride = Dk * 2), values alike.
+ *
+ * A workgroup is one wave and owns (query, KV head, group of up to
+ * SGLKV_ATTN_HEADS query heads, block of SGLKV_ATTN_DV value dims) for the
+ * tokens [split * chunk_tokens, +chunk_tokens) of gridDim.y's split. With
+ * one split it writes the output; otherwise it writes a partial record
+ * (running max m in log2 units, sum l, unnormalised o[dv]) that the combine
+ * kernel merges. */
+#define SGLKV_ATTN_TOKENS 32u   /* tokens per wave iteration */
+#define SGLKV_ATTN_HEADS 16u    /* query heads per workgroup (MFMA N) */
+#define SGLKV_ATTN_DV 128u      /* value dims per workgroup */
+#define SGLKV_ATTN_VT_STRIDE 40u /* u16 per transposed-V row in LDS (32 tokens + pad) */
+#define SGLKV_ATTN_MAX_DK 1024u /* query/key head dim limit (LDS-resident queries) */
+
+typedef struct sglkv_attn_params {
+    const uint16_t *queries;              /* bf16 [query][query_head][dk] */
+    const uint32_t *query_request_indices;
+    const uint64_t *query_sequence_lengths;
+    const uint64_t *request_slot_offsets; /* request_count + 1 */
+    const uint64_t *sequence_slots;
+    const uint8_t *pool;
+    uint16_t *output;                     /* bf16 [query][query_head][dv] */
+    float *partial;                       /* split records, or null */
+    uint32_t *flag;
+    uint64_t query_count;
+    uint64_t request_count;
+    uint64_t sequence_slot_count;
+    uint64_t slot_count;
+    uint64_t page_size;
+    uint64_t page_stride;
+    uint64_t key_offset, value_offset;
+    uint64_t key_head_stride, key_token_stride;
+    uint64_t value_head_stride, value_token_stride;
+    uint64_t chunk_tokens;                /* tokens per split */
+    uint32_t query_heads, kv_heads;
+    uint32_t group;                       /* query heads per KV head */
+    uint32_t head_groups;                 /* ceil(group / SGLKV_ATTN_HEADS) */
+    uint32_t dk, dk_pad;                  /* dk_pad = dk rounded up to 32 */
+    uint32_t dv, dv_blocks;               /* dv_blocks = ceil(dv / SGLKV_ATTN_DV) */
+    uint32_t splits;
+    uint32_t reserved;
+    float scale_log2;                     /* scale * log2(e) */
+    float reserved_f;
+} sglkv_attn_params;
 
 #endif

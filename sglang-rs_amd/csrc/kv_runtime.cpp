@@ -260,6 +260,14 @@ int32_t validate_device(const sgl_rocm_kv_ctx *ctx, const char *name, const sgl_
     return SGL_KV_OK;
 }
 
+}  // namespace
+
+int32_t sglkv::check_device(const sgl_rocm_kv_ctx *ctx, const char *name, const sgl_kv_device_buffer &b) {
+    return validate_device(ctx, name, b);
+}
+
+namespace {
+
 // CudaDeviceAllocation::device_ptr_at (cuda.rs:895-916).
 int32_t ptr_at(const char *name, const sgl_kv_device_buffer &b, uint64_t offset, uint64_t len,
                uint64_t *out) {
@@ -378,6 +386,12 @@ extern "C" int32_t sgl_rocm_kv_init(int32_t device, const char *code_object_path
     err = hipModuleGetFunction(&ctx->resolve, ctx->module, "sglkv_resolve_spans");
     if (err == hipSuccess) err = hipModuleGetFunction(&ctx->fill, ctx->module, "sglkv_fill_synthetic");
     if (err == hipSuccess) err = hipModuleGetFunction(&ctx->requests, ctx->module, "sglkv_copy_requests");
+    if (err == hipSuccess)
+        err = hipModuleGetFunction(&ctx->attention[0], ctx->module, "sglkv_paged_attention_v16");
+    if (err == hipSuccess)
+        err = hipModuleGetFunction(&ctx->attention[1], ctx->module, "sglkv_paged_attention_v2");
+    if (err == hipSuccess)
+        err = hipModuleGetFunction(&ctx->attention_combine, ctx->module, "sglkv_paged_attention_combine");
     if (err == hipSuccess) err = hipDeviceGetAttribute(&ctx->cu_count, hipDeviceAttributeMultiprocessorCount, device);
     // The tile constants the kernels were compiled with.
     const char *const constants[2] = {"sglkv_rows_per_thread", "sglkv_max_tile_rows"};
@@ -406,6 +420,7 @@ extern "C" int32_t sgl_rocm_kv_init(int32_t device, const char *code_object_path
 extern "C" int32_t sgl_rocm_kv_destroy(sgl_rocm_kv_ctx *ctx) {
     if (!ctx) return ok();
     DeviceScope scope(ctx->device);
+    if (ctx->attention_partial) (void)hipFree(ctx->attention_partial);
     hipError_t e1 = hipFree(ctx->flag);
     hipError_t e2 = hipModuleUnload(ctx->module);
     delete ctx;

@@ -97,7 +97,8 @@ _u64 = ctypes.c_uint64
 
 class _ErrorDetail(ctypes.Structure):
     _fields_ = [("code", ctypes.c_int32), ("reserved", ctypes.c_int32), ("a", _u64), ("b", _u64),
-                ("c", _u64), ("name", ctypes.c_char * 64), ("message", ctypes.c_char * 320)]
+                ("c", _u64), ("d", _u64), ("name", ctypes.c_char * 64),
+                ("message", ctypes.c_char * 320)]
 
 
 class _RuntimeLayout(ctypes.Structure):
@@ -179,6 +180,37 @@ class _TransferEvent(ctypes.Structure):
     _fields_ = [("bootstrap_room", _u64), ("descriptor_checksum", ctypes.c_char * 65),
                 ("reserved", ctypes.c_char * 3), ("status", ctypes.c_int32),
                 ("error_code", ctypes.c_int32)]
+
+
+class _AttentionLayout(ctypes.Structure):
+    _fields_ = [(n, _u64) for n in ("page_size", "page_stride_bytes", "key_in_page_offset",
+                                    "value_in_page_offset", "key_row_bytes", "value_row_bytes")] + [
+        ("head_layout", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
+
+
+class _AttentionPlanConfig(ctypes.Structure):
+    _fields_ = [(n, _u64) for n in ("query_count", "request_count", "sequence_slot_count",
+                                    "slot_count", "query_head_count", "kv_head_count",
+                                    "query_key_head_dim", "value_head_dim")] + [
+        ("scale", ctypes.c_float), ("reserved", ctypes.c_uint32), ("layout", _AttentionLayout)]
+
+
+_ATTENTION_REQUIRED = ("query_required_bytes", "query_request_indices_required_bytes",
+                       "query_sequence_lengths_required_bytes",
+                       "request_slot_offsets_required_bytes", "sequence_slots_required_bytes",
+                       "pool_required_bytes", "output_required_bytes")
+
+
+class _AttentionPlan(ctypes.Structure):
+    _fields_ = [("config", _AttentionPlanConfig)] + [(n, _u64) for n in _ATTENTION_REQUIRED]
+
+
+_ATTENTION_BUFFERS = ("queries", "query_request_indices", "query_sequence_lengths",
+                      "request_slot_offsets", "sequence_slots", "pool", "output")
+
+
+class _AttentionBuffers(ctypes.Structure):
+    _fields_ = [f for n in _ATTENTION_BUFFERS for f in ((n, _DeviceBuffer), (n + "_offset", _u64))]
 
 
 PAGE_REQUEST_DTYPE = np.dtype([("source", "<u8"), ("target_offset", "<u8"), ("length", "<u8")])
@@ -307,6 +339,15 @@ _EXPORTS = {
     "sgl_rocm_kv_backend_wait": (ctypes.c_int32, [ctypes.c_void_p]),
     "sgl_rocm_kv_backend_shutdown": (ctypes.c_int32, [ctypes.c_void_p]),
     "sgl_rocm_kv_backend_destroy": (ctypes.c_int32, [ctypes.c_void_p]),
+    "sgl_kv_attention_plan_new": (ctypes.c_int32, [ctypes.POINTER(_AttentionPlanConfig),
+                                                   ctypes.POINTER(_AttentionPlan)]),
+    "sgl_kv_attention_plan_for_layer": (ctypes.c_int32, [ctypes.POINTER(_PagedLayout), _u64, _u64,
+                                                         _u64, _u64, _u64, ctypes.c_float,
+                                                         ctypes.c_uint32,
+                                                         ctypes.POINTER(_AttentionPlan)]),
+    "sgl_rocm_kv_paged_attention": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_AttentionPlan),
+                                                     ctypes.POINTER(_AttentionBuffers), _u64,
+                                                     ctypes.c_void_p]),
     "sgl_rocm_kv_execute_page_requests": (ctypes.c_int32, [ctypes.c_void_p,
                                                            ctypes.POINTER(_DeviceBuffer), _u64, _u64,
                                                            ctypes.POINTER(_DeviceBuffer),
@@ -335,6 +376,10 @@ def lib():
     return _lib
 
 
+# Status codes whose variant carries four fields (a, b, c, d).
+_FOUR_FIELD_CODES = frozenset({84})
+
+
 def exported_names():
     return list(_EXPORTS)
 
@@ -346,7 +391,8 @@ def status_name(code: int) -> str:
 def _raise(code: int):
     d = _ErrorDetail()
     lib().sgl_kv_last_error(ctypes.byref(d))
-    raise KvError(code, status_name(code), d.name.decode(), (d.a, d.b, d.c), d.message.decode())
+    fields = (d.a, d.b, d.c) + ((d.d,) if code in _FOUR_FIELD_CODES else ())
+    raise KvError(code, status_name(code), d.name.decode(), fields, d.message.decode())
 
 
 def _call(fn, *args):
@@ -799,6 +845,15 @@ class RocmKvPairCopyKernels:
               max_length, ctypes.byref(source_region), ctypes.byref(target_region),
               int(offsets_are_addresses), _stream(stream))
 
+    def paged_attention(self, plan: "PagedAttentionPlan", *, max_sequence_length: int = 0,
+                        stream=None, **buffers):
+        """CudaBf16PagedAttentionKernels::forward (cuda_attention.rs:681-850):
+        keyword buffers queries, query_request_indices, query_sequence_lengths,
+        request_slot_offsets, sequence_slots, pool and output (objects with
+        .ptr/.nbytes, or device_buffer(...)), each with an optional
+        <name>_offset. Synchronous; bad metadata raises DeviceMetadataInvalid."""
+        _paged_attention(self, plan, buffers, max_sequence_length, stream)
+
     def check_errors(self, stream=None):
         _call(lib().sgl_rocm_kv_check_errors, self._h, _stream(stream))
 
@@ -949,6 +1004,69 @@ class RocmKvTransferBackend:
             self.close()
         except Exception:
             pass
+
+
+class PagedAttentionPlan:
+    """CudaBf16PagedAttentionPlan (cuda_attention.rs:239-430), plus the
+    head layout of the pages (NHD as the reference, or HND)."""
+
+    def __init__(self, c: _AttentionPlan):
+        self._c = c
+
+    @classmethod
+    def new(cls, *, query_count: int, request_count: int, sequence_slot_count: int,
+            slot_count: int, query_head_count: int, kv_head_count: int, query_key_head_dim: int,
+            value_head_dim: int, scale: float, page_size: int, page_stride_bytes: int,
+            key_in_page_offset: int, value_in_page_offset: int, key_row_bytes: int,
+            value_row_bytes: int, head_layout: int = NHD) -> "PagedAttentionPlan":
+        cfg = _AttentionPlanConfig(query_count, request_count, sequence_slot_count, slot_count,
+                                   query_head_count, kv_head_count, query_key_head_dim,
+                                   value_head_dim, scale, 0,
+                                   _AttentionLayout(page_size, page_stride_bytes,
+                                                    key_in_page_offset, value_in_page_offset,
+                                                    key_row_bytes, value_row_bytes, head_layout, 0))
+        out = _AttentionPlan()
+        _call(lib().sgl_kv_attention_plan_new, ctypes.byref(cfg), ctypes.byref(out))
+        return cls(out)
+
+    @classmethod
+    def for_layer(cls, layout: PagedKvCacheLayout, layer: int, query_count: int,
+                  request_count: int, sequence_slot_count: int, query_head_count: int,
+                  scale: float, head_layout: int = NHD) -> "PagedAttentionPlan":
+        """CudaBf16PagedAttentionExecutor::plan / build_plan
+        (crates/sglang-srt/src/cuda_attention.rs:438-572)."""
+        out = _AttentionPlan()
+        _call(lib().sgl_kv_attention_plan_for_layer, ctypes.byref(layout._c), layer, query_count,
+              request_count, sequence_slot_count, query_head_count, scale, head_layout,
+              ctypes.byref(out))
+        return cls(out)
+
+    def __getattr__(self, name):
+        c = self.__dict__["_c"]
+        if name in _ATTENTION_REQUIRED:
+            return getattr(c, name)
+        if hasattr(c.config.layout, name) and name != "reserved":
+            return getattr(c.config.layout, name)
+        if hasattr(c.config, name) and name != "reserved":
+            return getattr(c.config, name)
+        raise AttributeError(name)
+
+    @property
+    def layout(self):
+        lay = self._c.config.layout
+        return (lay.page_size, lay.page_stride_bytes, lay.key_in_page_offset,
+                lay.value_in_page_offset, lay.key_row_bytes, lay.value_row_bytes)
+
+
+def _paged_attention(kernels, plan: PagedAttentionPlan, buffers: dict, max_sequence_length: int,
+                     stream):
+    b = _AttentionBuffers()
+    for n in _ATTENTION_BUFFERS:
+        buf = buffers[n]
+        setattr(b, n, _DeviceBuffer(buf.ptr, buf.nbytes) if hasattr(buf, "nbytes") else buf)
+        setattr(b, n + "_offset", buffers.get(n + "_offset", 0))
+    _call(lib().sgl_rocm_kv_paged_attention, kernels._h, ctypes.byref(plan._c), ctypes.byref(b),
+          max_sequence_length, _stream(stream))
 
 
 def synthetic_words(seed: int, word_index) -> np.ndarray:

@@ -1,0 +1,225 @@
+"""GPU tests of the paged-attention reader (sgl_rocm_kv_paged_attention)
+against the float64 oracle (oracle.paged_attention, itself pinned against
+torch's scaled_dot_product_attention in tests/test_host_attention.py).
+
+Tolerance: the kernel rounds the softmax weights to bf16 for the p.v matrix
+product and rounds the output to bf16; against the float64 oracle every
+output element must satisfy |got - want| <= 1e-2 + 1e-2 * |want| (values
+and queries are N(0, 1) bf16).
+
+Cases: the reference's own scheduler metadata (causal prefill of two
+requests, crates/sglang-srt/tests/cuda_attention.rs:70-97); Llama-3-8B
+decode shapes on NHD and HND pages; a GQA group wider than one workgroup;
+MLA widths (576/512, the DeepSeek pair); odd head dims (element-wise
+path); long sequences split across workgroups; metadata errors; and an
+HND decode pool written by the transfer kernels read back through
+attention.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+import sgl_rocm_kv as kv
+from sgl_rocm_kv import hip
+
+pytestmark = pytest.mark.gpu
+RTOL = ATOL = 1e-2
+
+
+def _say(msg):
+    print(f"[gpu] {msg}", flush=True)
+
+
+@pytest.fixture(scope="module")
+def k():
+    if hip.device_count() == 0:
+        pytest.fail("no GPU visible: the gpu tests need an MI355X")
+    ctx = kv.RocmKvPairCopyKernels(0)
+    yield ctx
+    ctx.close()
+
+
+def _bf16_normal(rng, n):
+    return oracle.f32_to_bf16(rng.standard_normal(n).astype(np.float32))
+
+
+class _Case:
+    """A pool layout (uniform K/V or an MLA pair), seeded bf16 contents,
+    queries and metadata; runs the kernel and the oracle."""
+
+    def __init__(self, rng, *, P, L, H, dk, dv, qh, pages, layer, hnd=False):
+        kb, vb = H * dk * 2, H * dv * 2
+        rt = kv.KvCacheRuntimeLayout("bf16", P, L, H, dk, 2, L * (kb + vb), L * (kb + vb) * P)
+        if kb == vb:
+            self.layout = kv.PagedKvCacheLayout.new(rt, pages)
+        else:
+            self.layout = kv.PagedKvCacheLayout.new_with_tensor_pair(rt, pages, kb, vb)
+        self.P, self.H, self.dk, self.dv, self.qh, self.layer, self.hnd = P, H, dk, dv, qh, layer, hnd
+        self.pool_h = _bf16_normal(rng, self.layout.total_byte_len // 2).view(np.uint8)
+        self.pool = hip.DeviceBuffer.from_array(self.pool_h)
+
+    def run(self, k, queries, qri, qsl, rso, slots, scale, max_len=0):
+        qri = np.asarray(qri, np.uint32)
+        qsl = np.asarray(qsl, np.uint64)
+        rso = np.asarray(rso, np.uint64)
+        slots = np.asarray(slots, np.uint64)
+        plan = kv.PagedAttentionPlan.for_layer(self.layout, self.layer, len(qri), len(rso) - 1,
+                                               len(slots), self.qh, scale,
+                                               kv.HND if self.hnd else kv.NHD)
+        out = hip.DeviceBuffer(plan.output_required_bytes)
+        out.upload(np.zeros(plan.output_required_bytes, np.uint8))
+        bufs = dict(queries=hip.DeviceBuffer.from_array(queries),
+                    query_request_indices=hip.DeviceBuffer.from_array(qri),
+                    query_sequence_lengths=hip.DeviceBuffer.from_array(qsl),
+                    request_slot_offsets=hip.DeviceBuffer.from_array(rso),
+                    sequence_slots=hip.DeviceBuffer.from_array(slots), pool=self.pool, output=out)
+        k.paged_attention(plan, max_sequence_length=max_len, **bufs)
+        got = oracle.bf16_to_f32(out.download().view(np.uint16)).reshape(len(qri), self.qh, self.dv)
+        want, flags = oracle.paged_attention(
+            self.pool_h, queries, qri, qsl, rso, slots, page_size=self.P,
+            page_stride=plan.page_stride_bytes, key_offset=plan.key_in_page_offset,
+            value_offset=plan.value_in_page_offset, kv_heads=self.H, dk=self.dk, dv=self.dv,
+            scale=scale, slot_count=self.layout.slot_count, hnd=self.hnd)
+        assert flags == 0
+        return got, want
+
+
+def _random_batch(rng, requests, max_len, slot_count, min_len=1):
+    lens = rng.integers(min_len, max_len + 1, size=requests)
+    rso = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint64)
+    slots = rng.choice(slot_count, size=int(rso[-1]), replace=False).astype(np.uint64)
+    return lens, rso, slots
+
+
+def test_reference_scheduler_metadata(k, goldens):
+    """The two-request causal prefill of the reference's attention test:
+    query_request_indices [0,0,0,1,1], lengths [1,2,3,1,2], slots 0..4 on a
+    P4 L2 H2 D8 pool, layer 1, 4 query heads, scale 1/sqrt(8)."""
+    f = goldens["paged_attention_plan"]["from_layout"]
+    rng = np.random.default_rng(1)
+    c = _Case(rng, P=4, L=2, H=2, dk=8, dv=8, qh=4, pages=2, layer=1)
+    m = f["metadata"]
+    q = _bf16_normal(rng, 5 * 4 * 8).reshape(5, 4, 8)
+    got, want = c.run(k, q, m["query_request_indices"], m["query_sequence_lengths"],
+                      m["request_slot_offsets"], m["sequence_slots"], 1.0 / math.sqrt(8.0))
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("hnd,P", [(False, 16), (True, 64), (False, 1)])
+def test_llama3_8b_decode(k, hnd, P):
+    """32 query heads over 8 KV heads of 128 dims; 16 requests of up to
+    1,500 tokens, one decode query each (length = the whole sequence)."""
+    rng = np.random.default_rng(10 + P)
+    pages = -(-16 * 1500 // P) + 4
+    c = _Case(rng, P=P, L=2, H=8, dk=128, dv=128, qh=32, pages=pages, layer=1, hnd=hnd)
+    lens, rso, slots = _random_batch(rng, 16, 1500, c.layout.slot_count)
+    q = _bf16_normal(rng, 16 * 32 * 128).reshape(16, 32, 128)
+    _say(f"llama3-8b decode P={P} hnd={hnd} tokens={int(rso[-1])}")
+    got, want = c.run(k, q, np.arange(16), lens, rso, slots, 1.0 / math.sqrt(128), max_len=1500)
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+
+
+def test_long_sequence_is_split_and_combined(k):
+    """One request of 20,000 tokens (many splits through the combine kernel)
+    and a short one in the same launch; the short query's sequence ends
+    inside the first split."""
+    rng = np.random.default_rng(2)
+    c = _Case(rng, P=16, L=1, H=8, dk=128, dv=128, qh=32, pages=1300, layer=0)
+    lens = np.array([20000, 40])
+    rso = np.array([0, 20000, 20040], np.uint64)
+    slots = rng.choice(c.layout.slot_count, size=20040, replace=False).astype(np.uint64)
+    q = _bf16_normal(rng, 3 * 32 * 128).reshape(3, 32, 128)
+    _say("split attention: 20,000 + 40 tokens")
+    got, want = c.run(k, q, [0, 1, 0], [20000, 40, 77], rso, slots, 1.0 / math.sqrt(128),
+                      max_len=20000)
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+    # The same launch without the length hint (the split comes from the
+    # total slot count) gives the same result.
+    got2, _ = c.run(k, q, [0, 1, 0], [20000, 40, 77], rso, slots, 1.0 / math.sqrt(128))
+    np.testing.assert_allclose(got2, want, rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("H,qh,dk,dv,hnd", [
+    (2, 64, 128, 128, False),    # group of 32: two head groups per KV head
+    (1, 16, 576, 512, False),    # MLA widths (DeepSeek pair): dv spans 4 blocks
+    (1, 20, 576, 512, True),     # MLA widths, head-major, group not a multiple of 16
+    (2, 6, 12, 4, False),        # odd widths: element-wise loads
+    (3, 9, 40, 24, True),        # dims not multiples of 32
+])
+def test_shapes(k, H, qh, dk, dv, hnd):
+    rng = np.random.default_rng(dk + dv + qh)
+    P = 16
+    c = _Case(rng, P=P, L=2, H=H, dk=dk, dv=dv, qh=qh, pages=200, layer=1, hnd=hnd)
+    lens, rso, slots = _random_batch(rng, 5, 600, c.layout.slot_count)
+    nq = 7
+    qri = rng.integers(0, 5, size=nq)
+    qsl = np.array([rng.integers(1, lens[r] + 1) for r in qri])
+    q = _bf16_normal(rng, nq * qh * dk).reshape(nq, qh, dk)
+    _say(f"attention shape H={H} qh={qh} dk={dk} dv={dv} hnd={hnd}")
+    got, want = c.run(k, q, qri, qsl, rso, slots, 1.0 / math.sqrt(dk), max_len=600)
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+
+
+def test_metadata_errors(k):
+    """Bad request index, empty or overlong length, and a slot past the pool
+    raise DeviceMetadataInvalid with the reference's flag values."""
+    rng = np.random.default_rng(4)
+    c = _Case(rng, P=16, L=1, H=2, dk=64, dv=64, qh=4, pages=4, layer=0)
+    q = _bf16_normal(rng, 2 * 4 * 64).reshape(2, 4, 64)
+    cases = [([0, 1], [3, 3], [0, 3], [0, 1, 2], 0x1),
+             ([0, 0], [3, 0], [0, 3], [0, 1, 2], 0x2),
+             ([0, 0], [3, 4], [0, 3], [0, 1, 2], 0x2),
+             ([0, 0], [3, 2], [0, 3], [0, 64, 2], 0x4)]
+    for qri, qsl, rso, slots, want in cases:
+        plan = kv.PagedAttentionPlan.for_layer(c.layout, 0, 2, len(rso) - 1, len(slots), 4, 0.125)
+        out = hip.DeviceBuffer(plan.output_required_bytes)
+        with pytest.raises(kv.KvError) as ei:
+            k.paged_attention(plan, queries=hip.DeviceBuffer.from_array(q),
+                              query_request_indices=hip.DeviceBuffer.from_array(np.array(qri, np.uint32)),
+                              query_sequence_lengths=hip.DeviceBuffer.from_array(np.array(qsl, np.uint64)),
+                              request_slot_offsets=hip.DeviceBuffer.from_array(np.array(rso, np.uint64)),
+                              sequence_slots=hip.DeviceBuffer.from_array(np.array(slots, np.uint64)),
+                              pool=c.pool, output=out)
+        assert ei.value.variant == "DeviceMetadataInvalid" and ei.value.fields[0] == want
+
+
+def test_host_range_checks(k):
+    rng = np.random.default_rng(5)
+    c = _Case(rng, P=16, L=1, H=2, dk=64, dv=64, qh=4, pages=4, layer=0)
+    plan = kv.PagedAttentionPlan.for_layer(c.layout, 0, 1, 1, 3, 4, 0.125)
+    q = hip.DeviceBuffer(plan.query_required_bytes - 2)
+    ok = dict(query_request_indices=hip.DeviceBuffer(4), query_sequence_lengths=hip.DeviceBuffer(8),
+              request_slot_offsets=hip.DeviceBuffer(16), sequence_slots=hip.DeviceBuffer(24),
+              pool=c.pool, output=hip.DeviceBuffer(plan.output_required_bytes))
+    with pytest.raises(kv.KvError) as ei:
+        k.paged_attention(plan, queries=q, **ok)
+    assert ei.value.code == 11 and ei.value.name == "queries"
+
+
+def test_reads_an_hnd_pool_written_by_the_transfer_kernels(k):
+    """Prefill pool (P=1 NHD) -> decode pool (P=64 HND) with transfer_layers,
+    then attention over the decode pool's HND pages equals attention over
+    the prefill pool's NHD pages for the same tokens."""
+    rng = np.random.default_rng(6)
+    L, H, D, qh, n = 2, 8, 128, 32, 3000
+    src = _Case(rng, P=1, L=L, H=H, dk=D, dv=D, qh=qh, pages=4096, layer=1)
+    dst = _Case(rng, P=64, L=L, H=H, dk=D, dv=D, qh=qh, pages=64, layer=1, hnd=True)
+    src_slots = rng.choice(src.layout.slot_count, size=n, replace=False).astype(np.uint64)
+    table = rng.permutation(dst.layout.page_count)[: -(-n // 64)]
+    dst_slots = (table[np.arange(n) // 64] * 64 + np.arange(n) % 64).astype(np.uint64)
+    ss, ds = hip.DeviceBuffer.from_array(src_slots), hip.DeviceBuffer.from_array(dst_slots)
+    sv = src.layout.pool_view(src.pool.ptr, src.pool.nbytes, 0, kv.NHD, H)
+    dv = dst.layout.pool_view(dst.pool.ptr, dst.pool.nbytes, 0, kv.HND, H)
+    k.transfer_layers(sv, src.layout.bytes_per_layer_page, L, kv.device_buffer(ss.ptr, ss.nbytes), n,
+                      dv, dst.layout.bytes_per_layer_page, kv.device_buffer(ds.ptr, ds.nbytes))
+    k.check_errors()
+    dst.pool_h = dst.pool.download()
+    q = _bf16_normal(rng, 4 * qh * D).reshape(4, qh, D)
+    qsl = [n, 1, 1777, 64]
+    got_src, want = src.run(k, q, [0] * 4, qsl, [0, n], src_slots, 1.0 / math.sqrt(D), max_len=n)
+    got_dst, want_dst = dst.run(k, q, [0] * 4, qsl, [0, n], dst_slots, 1.0 / math.sqrt(D), max_len=n)
+    np.testing.assert_allclose(want_dst, want, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(got_dst, want, rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(got_src, want, rtol=RTOL, atol=ATOL)

@@ -676,8 +676,10 @@ int32_t sgl_kv_attention_plan_for_layer(const sgl_kv_paged_layout *layout, uint6
  * checks devices and ranges, clears the error word, runs, synchronises
  * `stream` and reports bad metadata as SGL_KV_ATTN_DEVICE_METADATA_INVALID
  * (the outputs of the affected queries are then unspecified).
- * max_sequence_length (0 = unknown) bounds the query lengths and only
- * steers how sequences are split across workgroups. Long sequences use a
+ * max_sequence_length (0 = unknown, then sequence_slot_count) bounds the
+ * query lengths and steers how sequences are split across workgroups; a
+ * query longer than it is reported as a sequence error (flag 0x2), not
+ * truncated. Long sequences use a
  * context-owned workspace, grown on demand. */
 int32_t sgl_rocm_kv_paged_attention(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *plan,
                                     const sgl_kv_attention_buffers *buffers,

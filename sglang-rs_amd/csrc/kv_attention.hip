@@ -70,7 +70,11 @@ __device__ __forceinline__ bool attn_metadata(const sglkv_attn_params &p, uint64
     }
     const uint64_t s = p.request_slot_offsets[req], e = p.request_slot_offsets[req + 1];
     const uint64_t n = p.query_sequence_lengths[q];
-    if (s > e || e > p.sequence_slot_count || n == 0 || n > e - s) {
+    // The launch covers splits * chunk_tokens tokens per query (sized from
+    // the caller's maximum length); a longer query is rejected rather than
+    // truncated, and the combine pass never reads past its split records.
+    if (s > e || e > p.sequence_slot_count || n == 0 || n > e - s ||
+        n > p.chunk_tokens * static_cast<uint64_t>(p.splits)) {
         if (report) atomicOr(p.flag, SGLKV_FLAG_ATTN_SEQUENCE);
         return false;
     }

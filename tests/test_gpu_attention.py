@@ -185,6 +185,25 @@ def test_metadata_errors(k):
         assert ei.value.variant == "DeviceMetadataInvalid" and ei.value.fields[0] == want
 
 
+def test_length_above_the_stated_maximum_is_rejected(k):
+    """A query longer than max_sequence_length (here 600 tokens against a
+    stated 300, which the launch covers with 2 splits of 256) is reported as
+    a sequence error, not truncated or combined from missing splits."""
+    rng = np.random.default_rng(7)
+    c = _Case(rng, P=16, L=1, H=2, dk=64, dv=64, qh=4, pages=64, layer=0)
+    slots = rng.choice(c.layout.slot_count, size=600, replace=False).astype(np.uint64)
+    q = _bf16_normal(rng, 2 * 4 * 64).reshape(2, 4, 64)
+    plan = kv.PagedAttentionPlan.for_layer(c.layout, 0, 2, 1, 600, 4, 0.125)
+    with pytest.raises(kv.KvError) as ei:
+        k.paged_attention(plan, max_sequence_length=300, queries=hip.DeviceBuffer.from_array(q),
+                          query_request_indices=hip.DeviceBuffer.from_array(np.zeros(2, np.uint32)),
+                          query_sequence_lengths=hip.DeviceBuffer.from_array(np.array([100, 600], np.uint64)),
+                          request_slot_offsets=hip.DeviceBuffer.from_array(np.array([0, 600], np.uint64)),
+                          sequence_slots=hip.DeviceBuffer.from_array(slots), pool=c.pool,
+                          output=hip.DeviceBuffer(plan.output_required_bytes))
+    assert ei.value.variant == "DeviceMetadataInvalid" and ei.value.fields[0] == 0x2
+
+
 def test_host_range_checks(k):
     rng = np.random.default_rng(5)
     c = _Case(rng, P=16, L=1, H=2, dk=64, dv=64, qh=4, pages=4, layer=0)

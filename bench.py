@@ -21,6 +21,11 @@ way; --config c5 runs the ragged radix-prefix transfer in request waves
 through the layer pipeline with its pinned-host hop (D2H then H2D), which
 bounds it by the host link rather than HBM.
 
+--config attn|attn_hnd measures the reader of the unpacked pages instead:
+paged-attention decode over the C2 decode pool (NHD or head-major pages),
+64 queries x 32 heads over 64 x 2,048 tokens, one launch per layer; its
+line carries its own metric (GB/s of K/V read).
+
 Prints one JSON line (the driver's contract), with a `roofline` object for
 the dominant kernel and a `cpu_baseline` object: the CPU oracle
 (oracle/kv_oracle.c, one thread) timed on a bounded sample of the same
@@ -44,6 +49,7 @@ import numpy as np  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "KV pack+unpack GB/s and % of HBM peak, Llama-3-8B shape; per-layer p50 µs"
+ATTN_METRIC = "paged-attention decode GB/s of K/V read and % of HBM peak, Llama-3-8B shape"
 
 DESCRIPTIONS = {
     "c1": "C1: Qwen2-0.5B-like GQA KV transfer, 24 layers x 2 KV heads x 64, bf16, 8 requests "
@@ -62,6 +68,10 @@ DESCRIPTIONS = {
                "page_size-64 pools of equal layout (131072 tokens = 2048 pages of 8 MiB, random "
                "source and destination pages), built with sgl_kv_build_page_requests and run "
                "as one launch (no relayout); algorithmic bytes = 2 x payload",
+    "attn": "paged-attention decode over the C2 decode pool (the reader of the unpacked pages): "
+            "Llama-3-8B shape, 32 layers x 8 KV heads x 128, bf16, page_size-64 NHD pool with a "
+            "random page table, 64 requests x 2048 tokens, one decode query each with 32 query heads",
+    "attn_hnd": "paged-attention decode as attn, over head-major (HND) pages",
     "c5": "C5: ragged radix-prefix GQA transfer (Llama-3-8B shape), 512 requests log-uniform "
           "[16,32768], page-aligned cached prefixes U[0,0.9]; request waves through the layer "
           "pipeline pack -> D2H -> pinned host -> H2D -> unpack on 4 streams",
@@ -429,6 +439,126 @@ def run_pages(args):
     }
 
 
+def attention_cpu_baseline(seconds: float, hnd: bool):
+    """The float64 attention oracle (numpy) on a sample of the attention
+    workload: 2 of its decode queries over their 2,048-token sequences, one
+    layer, on a host pool holding just those pages."""
+    import oracle
+    import sgl_rocm_kv as kv
+    L, H, D, P, qh, n, nq = 32, 8, 128, 64, 32, 2048, 2
+    rb = H * D * 2
+    rt = kv.KvCacheRuntimeLayout("bf16", P, L, H, D, 2, L * 2 * rb, L * 2 * rb * P)
+    layout = kv.PagedKvCacheLayout.new(rt, nq * n // P)
+    rng = np.random.default_rng(3)
+    pool = rng.integers(0, 1 << 16, layout.total_byte_len // 2, dtype=np.uint16)
+    pool &= np.uint16(0xBFFF)   # finite bf16 values of magnitude < 2
+    slots = rng.permutation(layout.slot_count).astype(np.uint64)[: nq * n]
+    q = oracle.f32_to_bf16(rng.standard_normal(nq * qh * D).astype(np.float32)).reshape(nq, qh, D)
+    plan = kv.PagedAttentionPlan.for_layer(layout, 0, nq, nq, nq * n, qh, 1.0 / np.sqrt(D),
+                                           kv.HND if hnd else kv.NHD)
+    def one():
+        oracle.paged_attention(pool.view(np.uint8), q, np.arange(nq), [n] * nq,
+                               np.arange(nq + 1) * n, slots, page_size=P,
+                               page_stride=plan.page_stride_bytes,
+                               key_offset=plan.key_in_page_offset,
+                               value_offset=plan.value_in_page_offset, kv_heads=H, dk=D, dv=D,
+                               scale=1.0 / np.sqrt(D), slot_count=layout.slot_count, hnd=hnd)
+    one()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        one()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or reps >= 1000:
+            break
+    kv_bytes = nq * n * 2 * rb
+    return {"value": round(kv_bytes * reps / el / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{nq} decode queries x {n} tokens x {qh} heads, one layer "
+                      f"({kv_bytes >> 20} MiB of K/V), x {reps} in {el:.1f} s, float64 numpy "
+                      f"oracle (oracle.paged_attention), single thread"}
+
+
+def run_attention(args, hnd: bool):
+    """Decode attention over every layer of the C2 decode pool: one async
+    launch per layer on one stream. Algorithmic bytes per launch = the K and
+    V rows the queries attend (64 x 2048 tokens x 2 x 2,048 B) + queries +
+    outputs; the 8 B/token slot list is excluded, as the copies' slot maps
+    are."""
+    import sgl_rocm_kv as kv
+    from sgl_rocm_kv import hip
+    from sgl_rocm_kv import workloads as wl
+    t = wl.c2()
+    sh, spec = t.shape, t.dst
+    L, H, D, P, qh = sh.layers, sh.heads, sh.head_dim, spec.page_size, 32
+    rb = sh.row_bytes
+    nreq, n = len(t.lengths), int(t.lengths[0])
+    rt = kv.KvCacheRuntimeLayout("bf16", P, L, H, D, 2, sh.token_bytes, spec.page_stride(sh))
+    layout = kv.PagedKvCacheLayout.new(rt, spec.page_count)
+    k = kv.RocmKvPairCopyKernels(0)
+    pool = hip.DeviceBuffer(layout.total_byte_len)
+    k.fill_synthetic(kv.device_buffer(pool.ptr, pool.nbytes), 2025, kv.FILL_BF16_NORMAL)
+    rng = np.random.default_rng(9)
+    import oracle
+    q = oracle.f32_to_bf16(rng.standard_normal(nreq * qh * D).astype(np.float32))
+    bufs = dict(queries=hip.DeviceBuffer.from_array(q),
+                query_request_indices=hip.DeviceBuffer.from_array(np.arange(nreq, dtype=np.uint32)),
+                query_sequence_lengths=hip.DeviceBuffer.from_array(t.lengths.astype(np.uint64)),
+                request_slot_offsets=hip.DeviceBuffer.from_array(
+                    np.concatenate([[0], np.cumsum(t.lengths)]).astype(np.uint64)),
+                sequence_slots=hip.DeviceBuffer.from_array(t.dst_slots), pool=pool)
+    outs = [hip.DeviceBuffer(nreq * qh * D * 2) for _ in range(L)]
+    plans = [kv.PagedAttentionPlan.for_layer(layout, l, nreq, nreq, len(t.dst_slots), qh,
+                                             1.0 / np.sqrt(D), kv.HND if hnd else kv.NHD)
+             for l in range(L)]
+    s = hip.Stream()
+    hip.synchronize()
+    log(f"pool resident: {pool.nbytes / 2**30:.1f} GiB, {'HND' if hnd else 'NHD'} pages")
+
+    def step(ev):
+        for l in range(L):
+            if ev:
+                ev[l][0].record(s)
+            k.paged_attention_async(plans[l], max_sequence_length=n, stream=s, output=outs[l], **bufs)
+            if ev:
+                ev[l][1].record(s)
+
+    for _ in range(args.warmup):
+        step(None)
+    k.check_errors(s)
+    hip.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(None)
+    hip.synchronize()
+    wall = time.perf_counter() - t0
+    k.check_errors(s)
+    ev = [[[hip.Event(), hip.Event()] for _ in range(L)] for _ in range(args.steps)]
+    for i in range(args.steps):
+        step(ev[i])
+    hip.synchronize()
+    k.check_errors(s)
+    launch_ms = [e[0].elapsed_ms(e[1]) for es in ev for e in es]
+    launch_bytes = nreq * n * 2 * rb + 2 * nreq * qh * D * 2
+    avg = float(np.mean(launch_ms))
+    achieved = launch_bytes / (avg / 1e3) / 1e9
+    gbs = launch_bytes * L / (wall / args.steps) / 1e9
+    log(f"attention avg {avg * 1e3:.1f} us per layer ({achieved:.0f} GB/s), wall {gbs:.0f} GB/s")
+    k.close()
+    return {
+        "value": round(gbs, 1),
+        "ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "config_extra": {"requests": nreq, "tokens_per_request": n, "layers": L, "kv_heads": H,
+                         "query_heads": qh, "head_dim": D, "page_size": P,
+                         "head_layout": "HND" if hnd else "NHD",
+                         "algorithmic_bytes_per_step": launch_bytes * L},
+        "per_layer_p50_us": round(float(np.percentile(launch_ms, 50)) * 1e3, 2),
+        "roofline": {"bound": "hbm", "kernel": "sglkv_paged_attention_v16",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": launch_bytes},
+    }
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -459,19 +589,23 @@ def main():
 
     from sgl_rocm_kv import workloads as wl
     makers = {"c1": wl.c1, "c2": wl.c2, "c3": wl.c3, "c4": wl.c4,
-              "c4fp8": lambda: wl.c4(fp8=True), "c5": wl.c5, "c2pages": wl.c2}
+              "c4fp8": lambda: wl.c4(fp8=True), "c5": wl.c5, "c2pages": wl.c2, "attn": wl.c2,
+              "attn_hnd": wl.c2}
+    attention = args.config in ("attn", "attn_hnd")
     t = makers[args.config]()
     log(f"workload {t.name}: {t.rows} tokens moved, payload {t.payload_bytes / 2**30:.2f} GiB")
     if args.config == "c5":
         r = run_staged(t, args)
     elif args.config == "c2pages":
         r = run_pages(args)
+    elif args.config in ("attn", "attn_hnd"):
+        r = run_attention(args, args.config == "attn_hnd")
     else:
         r = run_coresident(t, args.config, args)
     gbs = r.pop("value")
     extra = r.pop("config_extra")
     out = {
-        "metric": METRIC,
+        "metric": ATTN_METRIC if attention else METRIC,
         "value": gbs,
         "unit": "GB/s",
         "n_gpus": 1,
@@ -481,7 +615,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u8",
+        "dtype": "bf16" if attention else "u8",
         "data": "synthetic (values generated on the device; seeded slot permutations and page tables)",
         "config": dict({"workload": DESCRIPTIONS[args.config], "parallelism": "single GPU"}, **extra),
         "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
@@ -490,7 +624,8 @@ def main():
     out["cpu_baseline"] = None
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle, 1 thread)")
-        out["cpu_baseline"] = cpu_baseline(makers[args.config], args.cpu_seconds)
+        out["cpu_baseline"] = (attention_cpu_baseline(args.cpu_seconds, args.config == "attn_hnd")
+                               if attention else cpu_baseline(makers[args.config], args.cpu_seconds))
     print(json.dumps(out), flush=True)
 
 

@@ -684,6 +684,17 @@ int32_t sgl_kv_attention_plan_for_layer(const sgl_kv_paged_layout *layout, uint6
 int32_t sgl_rocm_kv_paged_attention(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *plan,
                                     const sgl_kv_attention_buffers *buffers,
                                     uint64_t max_sequence_length, void *stream);
+/* The same launch without the wait: nothing synchronises, and bad metadata
+ * surfaces at the next sgl_rocm_kv_check_errors on `stream` (as
+ * SGL_KV_ATTN_DEVICE_METADATA_INVALID). The error word is not cleared
+ * first, so an earlier unchecked error stays visible. The split workspace
+ * is shared by all calls on the context: issue calls that split on one
+ * stream (growing it waits for the whole device). No counterpart in the
+ * reference, whose forward always synchronises (cuda_attention.rs:821-829);
+ * it is for decode loops that check errors once per step. */
+int32_t sgl_rocm_kv_paged_attention_async(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *plan,
+                                          const sgl_kv_attention_buffers *buffers,
+                                          uint64_t max_sequence_length, void *stream);
 
 /* ---- Transfer backend: KvTransferBackend (transfer.rs:1145-1151) ----
  * register / submit / poll / cancel / shutdown for a prefill pool and a

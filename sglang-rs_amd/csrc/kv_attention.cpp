@@ -32,6 +32,21 @@ int32_t region_end(const char *tensor, uint64_t offset, uint64_t page_bytes, uin
 
 }  // namespace
 
+// Device error word bits of the attention kernels ->
+// DeviceMetadataInvalid with the reference's bit values (request 0x1,
+// sequence 0x2, slot 0x4; cuda_attention.rs:59-99).
+int32_t sglkv::attention_flag_status(uint32_t flag) {
+    const uint32_t bad = ((flag & SGLKV_FLAG_ATTN_REQUEST) ? 1u : 0u) |
+                         ((flag & SGLKV_FLAG_ATTN_SEQUENCE) ? 2u : 0u) |
+                         ((flag & SGLKV_FLAG_ATTN_SLOT) ? 4u : 0u);
+    if (bad)
+        return fail(SGL_KV_ATTN_DEVICE_METADATA_INVALID, nullptr, bad, 0, 0,
+                    "CUDA paged attention rejected device metadata with error flags 0x%x "
+                    "(request=0x1, sequence=0x2, slot=0x4)",
+                    bad);
+    return ok();
+}
+
 extern "C" int32_t sgl_kv_attention_plan_new(const sgl_kv_attention_plan_config *c,
                                              sgl_kv_attention_plan *out) {
     if (!c || !out) return fail(SGL_KV_INVALID_ARGUMENT, "config/out", 0, 0, 0, "null argument");
@@ -221,11 +236,11 @@ int32_t attn_ptr(const char *name, const sgl_kv_device_buffer &b, uint64_t offse
 
 uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
 
-}  // namespace
-
-extern "C" int32_t sgl_rocm_kv_paged_attention(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *plan,
-                                               const sgl_kv_attention_buffers *b,
-                                               uint64_t max_sequence_length, void *stream) {
+// Validates, sizes the split and launches the attention (and, with
+// several splits, the combine pass) on `stream`; nothing waits.
+int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *plan,
+                          const sgl_kv_attention_buffers *b, uint64_t max_sequence_length,
+                          hipStream_t s, bool clear_flag) {
     if (!ctx || !plan || !b)
         return fail(SGL_KV_INVALID_ARGUMENT, "ctx/plan/buffers", 0, 0, 0, "null argument");
     const sgl_kv_attention_plan_config &c = plan->config;
@@ -352,10 +367,9 @@ extern "C" int32_t sgl_rocm_kv_paged_attention(sgl_rocm_kv_ctx *ctx, const sgl_k
         }
         p.partial = static_cast<float *>(ctx->attention_partial);
     }
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    SGLKV_CHECK_HIP(hipMemsetAsync(ctx->flag, 0, sizeof(uint32_t), s));
     const unsigned lds = (unsigned)((SGLKV_ATTN_HEADS * (p.dk_pad + 8) +
                                      SGLKV_ATTN_DV * SGLKV_ATTN_VT_STRIDE) * sizeof(uint16_t));
+    if (clear_flag) SGLKV_CHECK_HIP(hipMemsetAsync(ctx->flag, 0, sizeof(uint32_t), s));
     void *args[] = {&p};
     SGLKV_CHECK_HIP(hipModuleLaunchKernel(ctx->attention[vec ? 0 : 1], (unsigned)base, (unsigned)splits, 1,
                                           64, 1, 1, lds, s, args, nullptr));
@@ -363,16 +377,34 @@ extern "C" int32_t sgl_rocm_kv_paged_attention(sgl_rocm_kv_ctx *ctx, const sgl_k
         SGLKV_CHECK_HIP(hipModuleLaunchKernel(ctx->attention_combine,
                                               (unsigned)(c.query_count * c.query_head_count), 1, 1, 128,
                                               1, 1, 0, s, args, nullptr));
+    return SGL_KV_OK;
+}
+
+}  // namespace
+
+extern "C" int32_t sgl_rocm_kv_paged_attention(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *plan,
+                                               const sgl_kv_attention_buffers *b,
+                                               uint64_t max_sequence_length, void *stream) {
+    if (!ctx) return fail(SGL_KV_INVALID_ARGUMENT, "ctx", 0, 0, 0, "null argument");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int32_t rc = attention_enqueue(ctx, plan, b, max_sequence_length, s, true);
+    if (rc) return rc;
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
     SGLKV_CHECK_HIP(hipStreamSynchronize(s));
     uint32_t flag = 0;
     SGLKV_CHECK_HIP(hipMemcpy(&flag, ctx->flag, sizeof flag, hipMemcpyDeviceToHost));
-    const uint32_t bad = ((flag & SGLKV_FLAG_ATTN_REQUEST) ? 1u : 0u) |
-                         ((flag & SGLKV_FLAG_ATTN_SEQUENCE) ? 2u : 0u) |
-                         ((flag & SGLKV_FLAG_ATTN_SLOT) ? 4u : 0u);
-    if (bad)
-        return fail(SGL_KV_ATTN_DEVICE_METADATA_INVALID, nullptr, bad, 0, 0,
-                    "CUDA paged attention rejected device metadata with error flags 0x%x "
-                    "(request=0x1, sequence=0x2, slot=0x4)",
-                    bad);
-    return ok();
+    // A reported error is consumed, as sgl_rocm_kv_check_errors does.
+    if (flag) SGLKV_CHECK_HIP(hipMemset(ctx->flag, 0, sizeof(uint32_t)));
+    return attention_flag_status(flag);
+}
+
+extern "C" int32_t sgl_rocm_kv_paged_attention_async(sgl_rocm_kv_ctx *ctx,
+                                                     const sgl_kv_attention_plan *plan,
+                                                     const sgl_kv_attention_buffers *b,
+                                                     uint64_t max_sequence_length, void *stream) {
+    if (!ctx) return fail(SGL_KV_INVALID_ARGUMENT, "ctx", 0, 0, 0, "null argument");
+    const int32_t rc =
+        attention_enqueue(ctx, plan, b, max_sequence_length, static_cast<hipStream_t>(stream), false);
+    return rc ? rc : ok();
 }

@@ -66,6 +66,7 @@ int32_t submit_launch(sgl_rocm_kv_ctx *ctx, Launch &l, hipStream_t stream);
 hipStream_t pipeline_final_stream(sgl_rocm_kv_pipeline *pipe);
 int32_t hip_fail(hipError_t err, const char *call);
 int32_t flag_status(uint32_t flag);
+int32_t attention_flag_status(uint32_t flag);
 
 inline int32_t too_large_dim(const char *name, uint64_t value, uint64_t maximum) {
     return fail(SGL_KV_DIMENSION_TOO_LARGE, name, value, maximum, 0,

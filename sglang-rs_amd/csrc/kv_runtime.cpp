@@ -341,6 +341,9 @@ int32_t pair_copy(sgl_rocm_kv_ctx *ctx, const sgl_kv_pair_copy_plan *plan,
     SGLKV_HIP(hipStreamSynchronize(stream));
     uint32_t flag = 0;
     SGLKV_HIP(hipMemcpy(&flag, ctx->flag, sizeof flag, hipMemcpyDeviceToHost));
+    // A reported error is consumed, so that a later asynchronous call's
+    // check_errors does not report it again.
+    if (flag) SGLKV_HIP(hipMemset(ctx->flag, 0, sizeof(uint32_t)));
     if (flag)
         return fail(SGL_KV_DEVICE_SLOT_INDEX_OUT_OF_RANGE, nullptr, plan->slot_count, 0, 0,
                     "KV copy device slot map contains an index outside %llu slots",
@@ -830,7 +833,7 @@ int32_t sglkv::flag_status(uint32_t flag) {
     if (flag & SGLKV_FLAG_REQUEST)
         return fail(SGL_KV_DEVICE_REQUEST_OUT_OF_RANGE, nullptr, 0, flag, 0,
                     "KV page request lies outside its source or target region");
-    return ok();
+    return attention_flag_status(flag);
 }
 
 extern "C" int32_t sgl_rocm_kv_check_errors(sgl_rocm_kv_ctx *ctx, void *stream) {

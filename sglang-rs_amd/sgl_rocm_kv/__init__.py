@@ -348,6 +348,10 @@ _EXPORTS = {
     "sgl_rocm_kv_paged_attention": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_AttentionPlan),
                                                      ctypes.POINTER(_AttentionBuffers), _u64,
                                                      ctypes.c_void_p]),
+    "sgl_rocm_kv_paged_attention_async": (ctypes.c_int32, [ctypes.c_void_p,
+                                                           ctypes.POINTER(_AttentionPlan),
+                                                           ctypes.POINTER(_AttentionBuffers), _u64,
+                                                           ctypes.c_void_p]),
     "sgl_rocm_kv_execute_page_requests": (ctypes.c_int32, [ctypes.c_void_p,
                                                            ctypes.POINTER(_DeviceBuffer), _u64, _u64,
                                                            ctypes.POINTER(_DeviceBuffer),
@@ -852,7 +856,15 @@ class RocmKvPairCopyKernels:
         request_slot_offsets, sequence_slots, pool and output (objects with
         .ptr/.nbytes, or device_buffer(...)), each with an optional
         <name>_offset. Synchronous; bad metadata raises DeviceMetadataInvalid."""
-        _paged_attention(self, plan, buffers, max_sequence_length, stream)
+        _paged_attention(lib().sgl_rocm_kv_paged_attention, self, plan, buffers,
+                         max_sequence_length, stream)
+
+    def paged_attention_async(self, plan: "PagedAttentionPlan", *, max_sequence_length: int = 0,
+                              stream=None, **buffers):
+        """paged_attention without the wait: bad metadata surfaces at the next
+        check_errors. Buffers as for paged_attention."""
+        _paged_attention(lib().sgl_rocm_kv_paged_attention_async, self, plan, buffers,
+                         max_sequence_length, stream)
 
     def check_errors(self, stream=None):
         _call(lib().sgl_rocm_kv_check_errors, self._h, _stream(stream))
@@ -1058,15 +1070,15 @@ class PagedAttentionPlan:
                 lay.value_in_page_offset, lay.key_row_bytes, lay.value_row_bytes)
 
 
-def _paged_attention(kernels, plan: PagedAttentionPlan, buffers: dict, max_sequence_length: int,
+def _paged_attention(fn, kernels, plan: PagedAttentionPlan, buffers: dict, max_sequence_length: int,
                      stream):
     b = _AttentionBuffers()
     for n in _ATTENTION_BUFFERS:
         buf = buffers[n]
         setattr(b, n, _DeviceBuffer(buf.ptr, buf.nbytes) if hasattr(buf, "nbytes") else buf)
         setattr(b, n + "_offset", buffers.get(n + "_offset", 0))
-    _call(lib().sgl_rocm_kv_paged_attention, kernels._h, ctypes.byref(plan._c), ctypes.byref(b),
-          max_sequence_length, _stream(stream))
+    _call(fn, kernels._h, ctypes.byref(plan._c), ctypes.byref(b), max_sequence_length,
+          _stream(stream))
 
 
 def synthetic_words(seed: int, word_index) -> np.ndarray:

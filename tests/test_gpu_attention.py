@@ -60,7 +60,7 @@ class _Case:
         self.pool_h = _bf16_normal(rng, self.layout.total_byte_len // 2).view(np.uint8)
         self.pool = hip.DeviceBuffer.from_array(self.pool_h)
 
-    def run(self, k, queries, qri, qsl, rso, slots, scale, max_len=0):
+    def run(self, k, queries, qri, qsl, rso, slots, scale, max_len=0, use_async=False):
         qri = np.asarray(qri, np.uint32)
         qsl = np.asarray(qsl, np.uint64)
         rso = np.asarray(rso, np.uint64)
@@ -75,7 +75,11 @@ class _Case:
                     query_sequence_lengths=hip.DeviceBuffer.from_array(qsl),
                     request_slot_offsets=hip.DeviceBuffer.from_array(rso),
                     sequence_slots=hip.DeviceBuffer.from_array(slots), pool=self.pool, output=out)
-        k.paged_attention(plan, max_sequence_length=max_len, **bufs)
+        if use_async:
+            k.paged_attention_async(plan, max_sequence_length=max_len, **bufs)
+            k.check_errors()
+        else:
+            k.paged_attention(plan, max_sequence_length=max_len, **bufs)
         got = oracle.bf16_to_f32(out.download().view(np.uint16)).reshape(len(qri), self.qh, self.dv)
         want, flags = oracle.paged_attention(
             self.pool_h, queries, qri, qsl, rso, slots, page_size=self.P,
@@ -202,6 +206,31 @@ def test_length_above_the_stated_maximum_is_rejected(k):
                           sequence_slots=hip.DeviceBuffer.from_array(slots), pool=c.pool,
                           output=hip.DeviceBuffer(plan.output_required_bytes))
     assert ei.value.variant == "DeviceMetadataInvalid" and ei.value.fields[0] == 0x2
+
+
+@pytest.mark.parametrize("max_len", [0, 1500])
+def test_async_launch_matches_and_reports_at_check_errors(k, max_len):
+    """paged_attention_async gives the synchronous call's results (split and
+    unsplit launches) and its metadata errors surface at check_errors."""
+    rng = np.random.default_rng(8)
+    c = _Case(rng, P=64, L=1, H=8, dk=128, dv=128, qh=32, pages=400, layer=0, hnd=True)
+    lens, rso, slots = _random_batch(rng, 12, 1500, c.layout.slot_count)
+    q = _bf16_normal(rng, 12 * 32 * 128).reshape(12, 32, 128)
+    got, want = c.run(k, q, np.arange(12), lens, rso, slots, 1.0 / math.sqrt(128), max_len=max_len,
+                      use_async=True)
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+    plan = kv.PagedAttentionPlan.for_layer(c.layout, 0, 2, 1, 4, 32, 0.1, kv.HND)
+    bad = dict(queries=hip.DeviceBuffer.from_array(q[:2]),
+               query_request_indices=hip.DeviceBuffer.from_array(np.array([0, 3], np.uint32)),
+               query_sequence_lengths=hip.DeviceBuffer.from_array(np.array([2, 2], np.uint64)),
+               request_slot_offsets=hip.DeviceBuffer.from_array(np.array([0, 4], np.uint64)),
+               sequence_slots=hip.DeviceBuffer.from_array(slots[:4]), pool=c.pool,
+               output=hip.DeviceBuffer(plan.output_required_bytes))
+    k.paged_attention_async(plan, max_sequence_length=max_len, **bad)
+    with pytest.raises(kv.KvError) as ei:
+        k.check_errors()
+    assert ei.value.variant == "DeviceMetadataInvalid" and ei.value.fields[0] == 0x1
+    k.check_errors()   # the word was cleared
 
 
 def test_host_range_checks(k):

@@ -131,6 +131,9 @@ def test_pair_gather_out_of_range_slot_is_flagged_and_skipped(k):
     np.testing.assert_array_equal(kh[:8], pool_h[8:16])
     np.testing.assert_array_equal(vh[:8], pool_h[24:32])
     assert (kh[8:] == 0xEE).all() and (vh[8:] == 0xEE).all()
+    # the reported error was consumed: check_errors (which asynchronous
+    # calls report through) does not see it again
+    k.check_errors()
     # the flag was cleared: a valid call afterwards succeeds
     sl.upload(np.array([1, 7], np.uint64))
     k.gather(plan, pool=pool, slot_indices=sl, keys=keys, values=values)

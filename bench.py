@@ -82,10 +82,11 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def _traffic_from_profiles(kernel: str, config: str):
+def _traffic_from_profiles(kernel: str, summary: str):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 counter
-    summary (FETCH_SIZE + WRITE_SIZE, calibrated), or None."""
-    path = os.path.join(ROOT, "profiles", f"kv_copy_{config}_counters.txt")
+    summary profiles/<summary>_counters.txt (FETCH_SIZE + WRITE_SIZE,
+    calibrated), or None."""
+    path = os.path.join(ROOT, "profiles", f"{summary}_counters.txt")
     if not os.path.exists(path):
         return None
     for line in open(path):
@@ -286,7 +287,7 @@ def run_coresident(t, config, args):
         "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      # the committed counter summaries were taken with --launch auto
-                     "traffic": _traffic_from_profiles(dom_name, config) if auto else None,
+                     "traffic": _traffic_from_profiles(dom_name, f"kv_copy_{config}") if auto else None,
                      "algorithmic_bytes_per_launch": launch_bytes * (L if multi else 1)},
     }
 
@@ -538,6 +539,12 @@ def run_attention(args, hnd: bool):
     hip.synchronize()
     k.check_errors(s)
     launch_ms = [e[0].elapsed_ms(e[1]) for es in ev for e in es]
+    if args.calibration_copy:   # a plain copy of known size for the counter runs
+        span = 1 << 30
+        for _ in range(3):
+            hip.memcpy_async(pool.ptr + span, pool.ptr, span, "d2d", s)
+        s.synchronize()
+        log(f"calibration copies done (3 x {span} B device-to-device)")
     launch_bytes = nreq * n * 2 * rb + 2 * nreq * qh * D * 2
     avg = float(np.mean(launch_ms))
     achieved = launch_bytes / (avg / 1e3) / 1e9
@@ -552,9 +559,14 @@ def run_attention(args, hnd: bool):
                          "head_layout": "HND" if hnd else "NHD",
                          "algorithmic_bytes_per_step": launch_bytes * L},
         "per_layer_p50_us": round(float(np.percentile(launch_ms, 50)) * 1e3, 2),
-        "roofline": {"bound": "hbm", "kernel": "sglkv_paged_attention_v16",
+        # One launch = the attention kernel and its combine pass: the events
+        # bracket both (one C-ABI call), so the pair is the measured unit.
+        "roofline": {"bound": "hbm", "kernel": "sglkv_paged_attention_pipe128+sglkv_paged_attention_combine",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": _traffic_from_profiles(
+                         "sglkv_paged_attention_pipe128+sglkv_paged_attention_combine",
+                         "paged_attention_decode_hnd" if hnd else "paged_attention_decode_nhd"),
                      "algorithmic_bytes_per_launch": launch_bytes},
     }
 

@@ -322,17 +322,51 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
     p.dv = (uint32_t)c.value_head_dim;
     p.dv_blocks = (uint32_t)ceil_div(p.dv, SGLKV_ATTN_DV);
     p.scale_log2 = c.scale * 1.4426950408889634f;
+    p.page_shift = 32;
+    if ((lay.page_size & (lay.page_size - 1)) == 0) {
+        p.page_shift = 0;
+        while ((1ull << p.page_shift) < lay.page_size) ++p.page_shift;
+    }
 
-    // Workgroups before splitting; split each query's sequence so the
-    // launch holds about eight waves per CU.
+    const bool vec = (p.dk % 8 == 0) && (p.dv % 8 == 0) &&
+                     ((poolp + lay.key_in_page_offset) % 16 == 0) &&
+                     ((poolp + lay.value_in_page_offset) % 16 == 0) &&
+                     ((lay.page_stride_bytes | p.key_head_stride | p.key_token_stride | p.value_head_stride |
+                       p.value_token_stride) % 16 == 0);
+    // Head dims up to 128 on 16-byte rows, power-of-two pages and strides
+    // that fit 32 bits take the software-pipelined body.
+    const bool pipe = vec && p.dk_pad <= 128 && p.dv <= SGLKV_ATTN_DV && p.page_shift < 32 &&
+                      c.slot_count < (1ull << 32) && lay.page_stride_bytes <= UINT32_MAX &&
+                      p.key_token_stride <= UINT32_MAX && p.value_token_stride <= UINT32_MAX;
+    const int which = !vec ? 1 : !pipe ? 0 : (p.dk == 128 && p.dv == 128) ? 2 : 3;
+    p.zero_row = ctx->zero_row;
+    p.page_stride32 = (uint32_t)lay.page_stride_bytes;
+    p.key_token_stride32 = (uint32_t)p.key_token_stride;
+    p.value_token_stride32 = (uint32_t)p.value_token_stride;
+    const unsigned lds = (unsigned)((SGLKV_ATTN_HEADS * (p.dk_pad + 8) +
+                                     SGLKV_ATTN_DV * SGLKV_ATTN_VT_STRIDE) * sizeof(uint16_t));
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+
+    // Workgroups before splitting; split each query's sequence so that the
+    // launch fills every CU with as many workgroups as stay resident at
+    // once (the kernel's occupancy at this LDS size), in one round.
     uint64_t base = c.query_count;
     if (mul_ovf(base, p.kv_heads, &base) || mul_ovf(base, p.head_groups, &base) ||
         mul_ovf(base, p.dv_blocks, &base) || base > INT32_MAX)
         return too_large_dim("workgroups", base, INT32_MAX);
+    if (ctx->attention_occupancy_lds[which] != lds) {
+        int per_cu = 0;
+        SGLKV_CHECK_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ctx->attention[which],
+                                                                           64, lds));
+        ctx->attention_occupancy[which] = per_cu > 0 ? (uint32_t)per_cu : 1;
+        ctx->attention_occupancy_lds[which] = lds;
+    }
     uint64_t max_len = max_sequence_length ? max_sequence_length : c.sequence_slot_count;
     if (max_len > c.sequence_slot_count) max_len = c.sequence_slot_count;
-    const uint64_t target = 8ull * (uint64_t)(ctx->cu_count > 0 ? ctx->cu_count : 256);
-    const uint64_t want = base >= target ? 1 : ceil_div(target, base);
+    const uint64_t target =
+        (uint64_t)ctx->attention_occupancy[which] * (uint64_t)(ctx->cu_count > 0 ? ctx->cu_count : 256);
+    const uint64_t want = base >= target ? 1 : target / base;
     uint64_t chunk = ceil_div(max_len, want);
     chunk = ceil_div(chunk < 256 ? 256 : chunk, SGLKV_ATTN_TOKENS) * SGLKV_ATTN_TOKENS;
     uint64_t splits = ceil_div(max_len, chunk);
@@ -343,13 +377,6 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
     p.chunk_tokens = chunk;
     p.splits = (uint32_t)splits;
 
-    const bool vec = (p.dk % 8 == 0) && (p.dv % 8 == 0) &&
-                     ((poolp + lay.key_in_page_offset) % 16 == 0) &&
-                     ((poolp + lay.value_in_page_offset) % 16 == 0) &&
-                     ((lay.page_stride_bytes | p.key_head_stride | p.key_token_stride | p.value_head_stride |
-                       p.value_token_stride) % 16 == 0);
-    DeviceScope scope(ctx->device);
-    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
     if (splits > 1) {
         uint64_t bytes;
         if (mul_ovf(c.query_count * c.query_head_count, splits, &bytes) ||
@@ -367,12 +394,10 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
         }
         p.partial = static_cast<float *>(ctx->attention_partial);
     }
-    const unsigned lds = (unsigned)((SGLKV_ATTN_HEADS * (p.dk_pad + 8) +
-                                     SGLKV_ATTN_DV * SGLKV_ATTN_VT_STRIDE) * sizeof(uint16_t));
     if (clear_flag) SGLKV_CHECK_HIP(hipMemsetAsync(ctx->flag, 0, sizeof(uint32_t), s));
     void *args[] = {&p};
-    SGLKV_CHECK_HIP(hipModuleLaunchKernel(ctx->attention[vec ? 0 : 1], (unsigned)base, (unsigned)splits, 1,
-                                          64, 1, 1, lds, s, args, nullptr));
+    SGLKV_CHECK_HIP(hipModuleLaunchKernel(ctx->attention[which], (unsigned)base, (unsigned)splits, 1, 64, 1,
+                                          1, lds, s, args, nullptr));
     if (splits > 1)
         SGLKV_CHECK_HIP(hipModuleLaunchKernel(ctx->attention_combine,
                                               (unsigned)(c.query_count * c.query_head_count), 1, 1, 128,

@@ -102,9 +102,12 @@ struct sgl_rocm_kv_ctx {
     hipFunction_t resolve;
     hipFunction_t fill;
     hipFunction_t requests;
-    hipFunction_t attention[2];     // 16-byte vector / element-wise loads
+    hipFunction_t attention[4];     // 16-byte vector / element-wise / pipelined dims 128 / pipelined dims <= 128
     hipFunction_t attention_combine;
-    uint32_t *flag;
+    uint32_t attention_occupancy[4];      // resident workgroups per CU of attention[i] ...
+    uint32_t attention_occupancy_lds[4];  // ... at this LDS size (0 = not yet queried)
+    uint32_t *flag;                 // device error word, at the start of a small zeroed block
+    const uint8_t *zero_row;        // SGLKV_ZERO_ROW_BYTES of zeros inside that block
     void *attention_partial;        // split records, grown on demand
     uint64_t attention_partial_bytes;
     uint32_t rows_per_thread;  // from the code object

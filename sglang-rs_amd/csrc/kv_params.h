@@ -183,9 +183,18 @@ typedef struct sglkv_attn_params {
     uint32_t dk, dk_pad;                  /* dk_pad = dk rounded up to 32 */
     uint32_t dv, dv_blocks;               /* dv_blocks = ceil(dv / SGLKV_ATTN_DV) */
     uint32_t splits;
-    uint32_t reserved;
+    uint32_t page_shift;                  /* log2(page_size) if a power of two, else 32 */
     float scale_log2;                     /* scale * log2(e) */
     float reserved_f;
+    /* Pipelined body only (page size a power of two, strides < 2^32): */
+    const uint8_t *zero_row;              /* SGLKV_ZERO_ROW_BYTES of zeros (context-owned) */
+    uint32_t page_stride32;
+    uint32_t key_token_stride32, value_token_stride32;
+    uint32_t reserved2;
 } sglkv_attn_params;
+
+/* Bytes of zeros the context keeps for reads that must contribute nothing
+ * (>= the widest row piece a pipelined attention lane reads, 256 B). */
+#define SGLKV_ZERO_ROW_BYTES 1024u
 
 #endif

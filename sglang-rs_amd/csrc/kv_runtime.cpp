@@ -394,6 +394,10 @@ extern "C" int32_t sgl_rocm_kv_init(int32_t device, const char *code_object_path
     if (err == hipSuccess)
         err = hipModuleGetFunction(&ctx->attention[1], ctx->module, "sglkv_paged_attention_v2");
     if (err == hipSuccess)
+        err = hipModuleGetFunction(&ctx->attention[2], ctx->module, "sglkv_paged_attention_pipe128");
+    if (err == hipSuccess)
+        err = hipModuleGetFunction(&ctx->attention[3], ctx->module, "sglkv_paged_attention_pipe");
+    if (err == hipSuccess)
         err = hipModuleGetFunction(&ctx->attention_combine, ctx->module, "sglkv_paged_attention_combine");
     if (err == hipSuccess) err = hipDeviceGetAttribute(&ctx->cu_count, hipDeviceAttributeMultiprocessorCount, device);
     // The tile constants the kernels were compiled with.
@@ -408,8 +412,11 @@ extern "C" int32_t sgl_rocm_kv_init(int32_t device, const char *code_object_path
     }
     if (err == hipSuccess && (ctx->rows_per_thread == 0 || ctx->rows_per_thread > ctx->max_tile_rows))
         err = hipErrorInvalidImage;
-    if (err == hipSuccess) err = hipMalloc(reinterpret_cast<void **>(&ctx->flag), sizeof(uint32_t));
-    if (err == hipSuccess) err = hipMemset(ctx->flag, 0, sizeof(uint32_t));
+    // One small block: the error word at offset 0, the zero row at 256.
+    constexpr size_t kFlagBlock = 256 + SGLKV_ZERO_ROW_BYTES;
+    if (err == hipSuccess) err = hipMalloc(reinterpret_cast<void **>(&ctx->flag), kFlagBlock);
+    if (err == hipSuccess) err = hipMemset(ctx->flag, 0, kFlagBlock);
+    if (err == hipSuccess) ctx->zero_row = reinterpret_cast<const uint8_t *>(ctx->flag) + 256;
     if (err != hipSuccess) {
         if (ctx->flag) (void)hipFree(ctx->flag);
         (void)hipModuleUnload(ctx->module);

@@ -166,6 +166,39 @@ def test_shapes(k, H, qh, dk, dv, hnd):
     np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("dk,dv,P", [(128, 128, 64), (64, 64, 16), (576, 512, 16)])
+def test_slots_outside_the_sequences_hold_nan(k, dk, dv, P):
+    """Every pool byte the queries do not attend is a NaN pattern: padded
+    tokens of the last block (lengths not a multiple of 32) and split ends
+    must contribute exact zeros, never garbage, on the pipelined body
+    (dims 128 and 64) and the generic one (MLA widths)."""
+    rng = np.random.default_rng(dk + P)
+    c = _Case(rng, P=P, L=1, H=1, dk=dk, dv=dv, qh=8, pages=120, layer=0)
+    lens = np.array([1, 31, 33, 700, 1001])
+    rso = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint64)
+    slots = rng.choice(c.layout.slot_count, size=int(rso[-1]), replace=False).astype(np.uint64)
+    pool16 = c.pool_h.view(np.uint16)
+    keep = np.zeros(c.layout.slot_count, bool)
+    keep[slots.astype(np.int64)] = True
+    plan = kv.PagedAttentionPlan.for_layer(c.layout, 0, 5, 5, len(slots), 8, 0.1)
+    per_slot = np.arange(c.layout.total_byte_len // 2)
+    page_elems = plan.page_stride_bytes // 2
+    tok = (per_slot % page_elems)
+    key_e, val_e = plan.key_in_page_offset // 2, plan.value_in_page_offset // 2
+    in_key = (tok >= key_e) & (tok < key_e + P * dk)
+    in_val = (tok >= val_e) & (tok < val_e + P * dv)
+    slot_of = np.where(in_key, (per_slot // page_elems) * P + (tok - key_e) // dk,
+                       (per_slot // page_elems) * P + (tok - val_e) // max(dv, 1))
+    nan_mask = ~((in_key | in_val) & keep[np.clip(slot_of, 0, c.layout.slot_count - 1)])
+    pool16[nan_mask] = 0x7FC1
+    c.pool.upload(c.pool_h)
+    q = _bf16_normal(rng, 5 * 8 * dk).reshape(5, 8, dk)
+    _say(f"nan-filled pool dk={dk} dv={dv} P={P}")
+    got, want = c.run(k, q, np.arange(5), lens, rso, slots, 1.0 / math.sqrt(dk), max_len=1001)
+    assert np.isfinite(want).all() and np.isfinite(got).all()
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+
+
 def test_metadata_errors(k):
     """Bad request index, empty or overlong length, and a slot past the pool
     raise DeviceMetadataInvalid with the reference's flag values."""

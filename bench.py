@@ -21,6 +21,10 @@ way; --config c5 runs the ragged radix-prefix transfer in request waves
 through the layer pipeline with its pinned-host hop (D2H then H2D), which
 bounds it by the host link rather than HBM.
 
+--config ceilings prints what plain contiguous streams reach on the device
+(copy, read, write, hipMemcpyDtoD): the practical ceilings against which the
+copy kernels' fractions of the nominal 8 TB/s should be read.
+
 --config attn|attn_hnd measures the reader of the unpacked pages instead:
 paged-attention decode over the C2 decode pool (NHD or head-major pages),
 64 queries x 32 heads over 64 x 2,048 tokens, one launch per layer; its
@@ -72,6 +76,8 @@ DESCRIPTIONS = {
             "Llama-3-8B shape, 32 layers x 8 KV heads x 128, bf16, page_size-64 NHD pool with a "
             "random page table, 64 requests x 2048 tokens, one decode query each with 32 query heads",
     "attn_hnd": "paged-attention decode as attn, over head-major (HND) pages",
+    "ceilings": "the device's streaming ceilings: contiguous copy, read and write of 1 GiB in "
+                "16-byte non-temporal vectors (sgl_rocm_kv_stream), and hipMemcpyDtoD",
     "c5": "C5: ragged radix-prefix GQA transfer (Llama-3-8B shape), 512 requests log-uniform "
           "[16,32768], page-aligned cached prefixes U[0,0.9]; request waves through the layer "
           "pipeline pack -> D2H -> pinned host -> H2D -> unpack on 4 streams",
@@ -571,6 +577,53 @@ def run_attention(args, hnd: bool):
     }
 
 
+def run_ceilings(args):
+    """What plain contiguous streams reach on this device: the practical
+    ceilings the copy kernels' roofline fractions should be read against
+    (HBM moves reads faster than writes, so a copy tops out well below the
+    nominal peak)."""
+    import sgl_rocm_kv as kv
+    from sgl_rocm_kv import hip
+    n = 1 << 30
+    k = kv.RocmKvPairCopyKernels(0)
+    a, b = hip.DeviceBuffer(n), hip.DeviceBuffer(n)
+    k.fill_synthetic(kv.device_buffer(a.ptr, a.nbytes), 1, kv.FILL_BITS)
+    k.fill_synthetic(kv.device_buffer(b.ptr, b.nbytes), 2, kv.FILL_BITS)
+    ab, bb = kv.device_buffer(a.ptr, a.nbytes), kv.device_buffer(b.ptr, b.nbytes)
+    s = hip.Stream()
+    out = {}
+    for name, launch, moved in (
+            ("copy", lambda: k.stream_ceiling(kv.STREAM_COPY, ab, bb, n, s), 2 * n),
+            ("read", lambda: k.stream_ceiling(kv.STREAM_READ, ab, bb, n, s), n),
+            ("write", lambda: k.stream_ceiling(kv.STREAM_WRITE, None, bb, n, s), n),
+            ("memcpy_dtod", lambda: hip.memcpy_async(b.ptr, a.ptr, n, "d2d", s), 2 * n)):
+        for _ in range(args.warmup):
+            launch()
+        e0, e1 = hip.Event(), hip.Event()
+        e0.record(s)
+        for _ in range(args.steps):
+            launch()
+        e1.record(s)
+        e1.synchronize()
+        ms = e0.elapsed_ms(e1) / args.steps
+        out[name] = (moved / (ms / 1e3) / 1e9, ms)
+        log(f"{name}: {ms * 1e3:.1f} us per GiB pass, {out[name][0]:.0f} GB/s")
+    k.check_errors(s)
+    k.close()
+    gbs = out["copy"][0]
+    return {
+        "value": round(gbs, 1),
+        "ms_per_step": round(out["copy"][1], 4),
+        "config_extra": {"bytes_per_pass": n, "algorithmic_bytes_per_step": 2 * n},
+        "read_gbs": round(out["read"][0], 1),
+        "write_gbs": round(out["write"][0], 1),
+        "memcpy_dtod_gbs": round(out["memcpy_dtod"][0], 1),
+        "roofline": {"bound": "hbm", "kernel": "sglkv_stream_copy", "achieved": round(gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None, "algorithmic_bytes_per_launch": 2 * n},
+    }
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -602,7 +655,7 @@ def main():
     from sgl_rocm_kv import workloads as wl
     makers = {"c1": wl.c1, "c2": wl.c2, "c3": wl.c3, "c4": wl.c4,
               "c4fp8": lambda: wl.c4(fp8=True), "c5": wl.c5, "c2pages": wl.c2, "attn": wl.c2,
-              "attn_hnd": wl.c2}
+              "attn_hnd": wl.c2, "ceilings": wl.c2}
     attention = args.config in ("attn", "attn_hnd")
     t = makers[args.config]()
     log(f"workload {t.name}: {t.rows} tokens moved, payload {t.payload_bytes / 2**30:.2f} GiB")
@@ -612,6 +665,8 @@ def main():
         r = run_pages(args)
     elif args.config in ("attn", "attn_hnd"):
         r = run_attention(args, args.config == "attn_hnd")
+    elif args.config == "ceilings":
+        r = run_ceilings(args)
     else:
         r = run_coresident(t, args.config, args)
     gbs = r.pop("value")
@@ -634,7 +689,9 @@ def main():
     }
     out.update(r)
     out["cpu_baseline"] = None
-    if not args.no_cpu_baseline:
+    if args.config == "ceilings":
+        out["metric"] = "device streaming ceilings: contiguous copy GB/s (read, write alongside)"
+    elif not args.no_cpu_baseline:
         log("cpu baseline (oracle, 1 thread)")
         out["cpu_baseline"] = (attention_cpu_baseline(args.cpu_seconds, args.config == "attn_hnd")
                                if attention else cpu_baseline(makers[args.config], args.cpu_seconds))

@@ -584,6 +584,19 @@ typedef enum sgl_kv_fill_kind {
 int32_t sgl_rocm_kv_fill_synthetic(sgl_rocm_kv_ctx *ctx, const sgl_kv_device_buffer *buffer,
                                    uint64_t seed, uint32_t kind, void *stream);
 
+/* Streaming ceilings of the device, for the benchmark's roofline context;
+ * no counterpart in the reference. kind COPY moves `bytes` from src to
+ * dst, READ reads `bytes` of src (dst receives at most 16 bytes), WRITE
+ * writes `bytes` of dst; contiguous, 16-byte non-temporal vectors.
+ * `bytes` is a multiple of 16. Asynchronous. */
+typedef enum sgl_kv_stream_kind {
+    SGL_KV_STREAM_COPY = 0,
+    SGL_KV_STREAM_READ = 1,
+    SGL_KV_STREAM_WRITE = 2
+} sgl_kv_stream_kind;
+int32_t sgl_rocm_kv_stream(sgl_rocm_kv_ctx *ctx, uint32_t kind, const sgl_kv_device_buffer *src,
+                           const sgl_kv_device_buffer *dst, uint64_t bytes, void *stream);
+
 /* Executes page requests (sgl_kv_build_page_requests /
  * sgl_kv_build_remote_page_requests output, uploaded to the device) as
  * device copies: the page-for-page PD transfer between co-resident pools of

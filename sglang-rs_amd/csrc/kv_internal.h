@@ -102,6 +102,7 @@ struct sgl_rocm_kv_ctx {
     hipFunction_t resolve;
     hipFunction_t fill;
     hipFunction_t requests;
+    hipFunction_t stream_fn[3];     // streaming ceilings: copy, read, write
     hipFunction_t attention[4];     // 16-byte vector / element-wise / pipelined dims 128 / pipelined dims <= 128
     hipFunction_t attention_combine;
     uint32_t attention_occupancy[4];      // resident workgroups per CU of attention[i] ...

@@ -395,5 +395,58 @@ extern "C" __global__ __launch_bounds__(SGLKV_BLOCK_THREADS) void sglkv_copy_req
     }
 }
 
+// Streaming ceilings of the device, for the benchmark's roofline context:
+// a plain contiguous copy, read and write of 16-byte vectors, grid-stride,
+// non-temporal, U vectors in flight per thread (the fastest settings of a
+// sweep on MI355X). Not used by the transfer path itself.
+template <int MODE, int U>
+__device__ __forceinline__ void sglkv_stream_body(const sglkv_v4u *src, sglkv_v4u *dst, uint64_t vecs) {
+    typedef __attribute__((address_space(1))) const sglkv_v4u gload_t;
+    typedef __attribute__((address_space(1))) sglkv_v4u gstore_t;
+    const uint64_t step = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    sglkv_v4u acc = {0, 0, 0, 0};
+    for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * blockDim.x * U + threadIdx.x; base < vecs;
+         base += step * U) {
+        sglkv_v4u b[U];
+        if (MODE != 2) {
+#pragma unroll
+            for (int k = 0; k < U; ++k) {
+                const uint64_t i = base + static_cast<uint64_t>(k) * blockDim.x;
+                b[k] = __builtin_nontemporal_load(
+                    reinterpret_cast<gload_t *>(reinterpret_cast<uint64_t>(src + (i < vecs ? i : 0))));
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < U; ++k) {
+            const uint64_t i = base + static_cast<uint64_t>(k) * blockDim.x;
+            if (MODE == 1) {
+                acc ^= b[k];
+            } else if (i < vecs) {
+                const sglkv_v4u v = MODE == 0 ? b[k] : sglkv_v4u{static_cast<uint32_t>(i), 1u, 2u, 3u};
+                __builtin_nontemporal_store(v, reinterpret_cast<gstore_t *>(reinterpret_cast<uint64_t>(dst + i)));
+            }
+        }
+    }
+    // The read keeps its loads alive with a store no input can trigger in
+    // practice (an XOR of every word equal to this constant).
+    if (MODE == 1 && (acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x5D1E5EEDu) dst[0] = acc;
+}
+
+extern "C" __global__ __launch_bounds__(SGLKV_BLOCK_THREADS) void sglkv_stream_copy(const sglkv_v4u *src,
+                                                                                   sglkv_v4u *dst,
+                                                                                   uint64_t vecs) {
+    sglkv_stream_body<0, 4>(src, dst, vecs);
+}
+extern "C" __global__ __launch_bounds__(SGLKV_BLOCK_THREADS) void sglkv_stream_read(const sglkv_v4u *src,
+                                                                                   sglkv_v4u *dst,
+                                                                                   uint64_t vecs) {
+    sglkv_stream_body<1, 8>(src, dst, vecs);
+}
+extern "C" __global__ __launch_bounds__(SGLKV_BLOCK_THREADS) void sglkv_stream_write(const sglkv_v4u *src,
+                                                                                    sglkv_v4u *dst,
+                                                                                    uint64_t vecs) {
+    sglkv_stream_body<2, 8>(src, dst, vecs);
+}
+
 // The paged-attention reader of the same pools shares this code object.
 #include "kv_attention.hip"

@@ -75,6 +75,7 @@ DTYPES = {"auto": 0, "float32": 1, "bf16": 2, "bfloat16": 2, "fp8_e4m3": 3, "fp8
           "fp4_e2m1": 5}
 NHD, HND = 0, 1
 FILL_BITS, FILL_BF16_NORMAL, FILL_BF16_UNIFORM = 0, 1, 2
+STREAM_COPY, STREAM_READ, STREAM_WRITE = 0, 1, 2
 
 
 class ExtensionMissing(RuntimeError):
@@ -359,6 +360,8 @@ _EXPORTS = {
                                                            ctypes.c_uint32, ctypes.c_void_p]),
     "sgl_rocm_kv_fill_synthetic": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_DeviceBuffer),
                                                     _u64, ctypes.c_uint32, ctypes.c_void_p]),
+    "sgl_rocm_kv_stream": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_uint32, ctypes.POINTER(_DeviceBuffer),
+                                            ctypes.POINTER(_DeviceBuffer), _u64, ctypes.c_void_p]),
 }
 
 _lib = None
@@ -871,6 +874,14 @@ class RocmKvPairCopyKernels:
 
     def fill_synthetic(self, buffer: _DeviceBuffer, seed: int, kind: int = FILL_BITS, stream=None):
         _call(lib().sgl_rocm_kv_fill_synthetic, self._h, ctypes.byref(buffer), seed, kind,
+              _stream(stream))
+
+    def stream_ceiling(self, kind: int, src, dst, nbytes: int, stream=None):
+        """The device's streaming ceilings (STREAM_COPY / READ / WRITE of
+        `nbytes` contiguous bytes); src or dst may be None where unused."""
+        s = src if src is not None else _DeviceBuffer(None, 0)
+        d = dst if dst is not None else _DeviceBuffer(None, 0)
+        _call(lib().sgl_rocm_kv_stream, self._h, kind, ctypes.byref(s), ctypes.byref(d), nbytes,
               _stream(stream))
 
 

@@ -125,7 +125,21 @@ typedef enum sgl_kv_status {
     SGL_KV_ATTN_TENSOR_PAGE_REGIONS_OVERLAP = 84,     /* a = key_offset, b = value_offset, c = key_page_bytes, d = value_page_bytes */
     SGL_KV_ATTN_DEVICE_METADATA_INVALID = 85,         /* a = flags: request 0x1, sequence 0x2, slot 0x4 */
     SGL_KV_ATTN_UNSUPPORTED_KV_DTYPE = 86,            /* a = actual dtype, b = required */
-    SGL_KV_ATTN_TENSOR_ROW_GEOMETRY_MISMATCH = 87     /* name = tensor, a = row_bytes, b = kv_head_count, c = element_bytes */
+    SGL_KV_ATTN_TENSOR_ROW_GEOMETRY_MISMATCH = 87,    /* name = tensor, a = row_bytes, b = kv_head_count, c = element_bytes */
+
+    /* 90.. mirror MooncakeBootstrapFrameError (crates/sglang-srt/src/pd_bootstrap.rs:576-600),
+     * MooncakeRemoteKvLayoutError (:504-510) and MooncakeDecodeBootstrapError::MissingAuxIndex
+     * (:920); 99 is the decode-layout extension of this build. */
+    SGL_KV_BOOT_MISSING_FIELD = 90,             /* name = frame, a = expected, b = actual */
+    SGL_KV_BOOT_UTF8_FIELD = 91,                /* name = field */
+    SGL_KV_BOOT_INTEGER_FIELD = 92,             /* name = field; the value is quoted in the message */
+    SGL_KV_BOOT_BINARY_LENGTH = 93,             /* name = field, a = width, b = actual */
+    SGL_KV_BOOT_PACKED_LIST_HEADER = 94,        /* name = field */
+    SGL_KV_BOOT_PACKED_LIST_LENGTH = 95,        /* name = field */
+    SGL_KV_BOOT_MISSING_TRANSFER_ROOM = 96,     /* a = room */
+    SGL_KV_BOOT_MISSING_KV_ARGS = 97,           /* a = room; the session id is quoted in the message */
+    SGL_KV_BOOT_MISSING_AUX_INDEX = 98,         /* the session id is quoted in the message */
+    SGL_KV_BOOT_DECODE_LAYOUT = 99              /* name = what is wrong, a, b = values */
 } sgl_kv_status;
 
 /* Detail of the calling thread's most recent failure. */
@@ -708,6 +722,150 @@ int32_t sgl_rocm_kv_paged_attention(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention
 int32_t sgl_rocm_kv_paged_attention_async(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *plan,
                                           const sgl_kv_attention_buffers *buffers,
                                           uint64_t max_sequence_length, void *stream);
+
+/* ---- Bootstrap wire format: the decode side's page table and layout ----
+ * The multipart frames a decode worker sends a prefill worker's bootstrap
+ * listener (Mooncake protocol, crates/sglang-srt/src/pd_bootstrap.rs):
+ *  - KVArgs registration, part 0 "None": endpoint, port, session id, then
+ *    dst_kv_ptrs (u64 LE), dst_aux_ptrs, dst_state_data_ptrs (packed u64
+ *    lists), tp rank, attn tp size, dst_kv_item_len, optional packed u32
+ *    lists (:416-449, encoder :685-706);
+ *  - transfer metadata, part 0 the room: endpoint, port, session id,
+ *    dst_kv_indices (i32 LE), aux index, dst_state_indices (packed i32
+ *    lists), required_dst_info_num, optional decode_prefix_len (:451-494,
+ *    encoder :720-749).
+ * Integers in text parts are ASCII decimal; a packed list is a u32 LE
+ * count, the u32 LE byte length of each buffer, then the buffers
+ * (:1255-1270, decoder :1605-1636).
+ *
+ * Decode-layout extension (no counterpart in the reference): a KVArgs frame
+ * may carry one more part, after the 14 the reference's encoder writes, that
+ * describes the decode pool's page geometry, so a prefill side can relayout
+ * (page size, NHD/HND) instead of copying page for page. A reference prefill
+ * reads only parts 0..11 and ignores it. Layout of the part, little endian:
+ *   u32 magic 0x4C564B53 ("SKVL"), u32 version 1,
+ *   i32 dtype, u32 head_layout,
+ *   u64 page_size, num_layers, kv_heads, head_dim, kv_tensors_per_token,
+ *       bytes_per_token, page_size_bytes, page_count,
+ *   u64 tensor_pair (0/1), key_token_bytes, value_token_bytes, heads
+ * (112 bytes). */
+#define SGL_KV_DECODE_LAYOUT_MAGIC 0x4C564B53u
+#define SGL_KV_DECODE_LAYOUT_BYTES 112u
+#define SGL_KV_BOOTSTRAP_MAX_PARTS 16u
+
+typedef struct sgl_kv_frame_part {
+    const uint8_t *data;
+    uint64_t len;
+} sgl_kv_frame_part;
+
+/* The decode pool as the extension advertises it: the geometry, its head
+ * layout and head chunks per row (what sgl_kv_backend_memory needs besides
+ * the base pointer, which travels as dst_kv_ptrs[0]). */
+typedef struct sgl_kv_decode_layout {
+    sgl_kv_paged_layout layout;
+    uint32_t head_layout;  /* sgl_kv_head_layout */
+    uint32_t reserved;
+    uint64_t heads;        /* 0 = layout.runtime.kv_heads */
+} sgl_kv_decode_layout;
+
+/* A flattened list of lists: list i is values[offsets[i] .. offsets[i+1]),
+ * offsets has count + 1 entries. */
+typedef struct sgl_kv_u64_lists { const uint64_t *values; const uint64_t *offsets; uint64_t count; } sgl_kv_u64_lists;
+typedef struct sgl_kv_u32_lists { const uint32_t *values; const uint64_t *offsets; uint64_t count; } sgl_kv_u32_lists;
+typedef struct sgl_kv_i32_lists { const int32_t *values; const uint64_t *offsets; uint64_t count; } sgl_kv_i32_lists;
+
+/* MooncakeKvArgsRegisterInfo (pd_bootstrap.rs:416-429) / the encoder's
+ * MooncakeDecodeKvArgsRegistration (:671-683). Strings are NUL-terminated.
+ * As a view returned by sgl_kv_bootstrap_get_kv_args, every pointer stays valid
+ * until the next ingest into, or the destruction of, the state. */
+typedef struct sgl_kv_bootstrap_kv_args {
+    const char *endpoint;
+    const char *mooncake_session_id;
+    uint32_t dst_port;
+    int32_t dst_tp_rank;
+    uint64_t dst_attn_tp_size;
+    uint64_t dst_kv_item_len;
+    const uint64_t *dst_kv_ptrs;  uint64_t dst_kv_ptr_count;
+    const uint64_t *dst_aux_ptrs; uint64_t dst_aux_ptr_count;
+    sgl_kv_u64_lists dst_state_data_ptrs;
+    sgl_kv_u32_lists dst_state_item_lens;
+    sgl_kv_u32_lists dst_state_dim_per_tensor;
+    const sgl_kv_decode_layout *decode_layout;  /* NULL: none advertised */
+} sgl_kv_bootstrap_kv_args;
+
+/* MooncakeTransferInfo (pd_bootstrap.rs:451-462) / the encoder's
+ * MooncakeDecodeTransferMetadata (:708-718). */
+typedef struct sgl_kv_bootstrap_transfer {
+    uint64_t room;
+    const char *endpoint;
+    const char *mooncake_session_id;
+    uint32_t dst_port;
+    uint32_t is_dummy;
+    const int32_t *dst_kv_indices; uint64_t dst_kv_index_count;
+    uint32_t has_dst_aux_index;
+    int32_t dst_aux_index;
+    sgl_kv_i32_lists dst_state_indices;
+    uint64_t required_dst_info_num;
+    uint32_t has_decode_prefix_len;
+    uint32_t reserved;
+    uint64_t decode_prefix_len;
+} sgl_kv_bootstrap_transfer;
+
+/* MooncakeRemoteKvLayout (crates/sglang-srt/src/transfer.rs:1651-1656) of
+ * one decode session, plus the advertised decode layout if any. */
+typedef struct sgl_kv_remote_kv_layout {
+    const char *mooncake_session_id;
+    const uint64_t *dst_kv_ptrs;    uint64_t dst_kv_ptr_count;
+    const int32_t *dst_kv_indices;  uint64_t dst_kv_index_count;
+    uint64_t dst_kv_item_len;
+    const sgl_kv_decode_layout *decode_layout;  /* NULL: none advertised */
+} sgl_kv_remote_kv_layout;
+
+/* The Mooncake tables of PrefillBootstrapState (pd_bootstrap.rs:150-235). */
+typedef struct sgl_kv_bootstrap sgl_kv_bootstrap;
+int32_t sgl_kv_bootstrap_create(sgl_kv_bootstrap **out);
+int32_t sgl_kv_bootstrap_destroy(sgl_kv_bootstrap *state);
+/* ingest_mooncake_bootstrap_frame (:180-217): "WATERMARK" and
+ * "STAGING_RSP" frames are accepted and ignored, "None" registers KVArgs
+ * (replacing the session's previous registration), anything else is
+ * transfer metadata for a room, which turns WaitingForInput once
+ * required_dst_info_num sessions have reported. Errors leave the state
+ * unchanged. */
+int32_t sgl_kv_bootstrap_ingest(sgl_kv_bootstrap *state, const sgl_kv_frame_part *parts, uint32_t part_count);
+/* KVArgs registrations ingested so far (decode_kv_args_registration_count). */
+int32_t sgl_kv_bootstrap_registration_count(const sgl_kv_bootstrap *state, uint64_t *count);
+/* decode_kv_args (:221-223); SGL_KV_BOOT_MISSING_KV_ARGS (room 0) when the
+ * session has not registered. */
+int32_t sgl_kv_bootstrap_get_kv_args(const sgl_kv_bootstrap *state, const char *mooncake_session_id,
+                                 sgl_kv_bootstrap_kv_args *out);
+/* transfer_status (:233-235): *status = KvPoll (Failed 0, Bootstrapping 1,
+ * WaitingForInput 2, Transferring 3, Success 4; transfer.rs:355-361), or -1
+ * for an unknown room. */
+int32_t sgl_kv_bootstrap_transfer_status(const sgl_kv_bootstrap *state, uint64_t room, int32_t *status);
+/* MooncakeTransferRoom (:497-502): the room's required_dst_info_num,
+ * decode_prefix_len (has = 0: none) and the sessions reported so far. */
+int32_t sgl_kv_bootstrap_room(const sgl_kv_bootstrap *state, uint64_t room, uint64_t *required_dst_info_num,
+                              uint32_t *has_decode_prefix_len, uint64_t *decode_prefix_len,
+                              uint64_t *session_count);
+/* One session's transfer metadata in a room. */
+int32_t sgl_kv_bootstrap_get_transfer(const sgl_kv_bootstrap *state, uint64_t room, const char *mooncake_session_id,
+                                  sgl_kv_bootstrap_transfer *out);
+/* remote_kv_layouts_for_room (:237-270): one entry per non-dummy session,
+ * in session-id order; writes up to `capacity`, *count = the total. */
+int32_t sgl_kv_bootstrap_remote_layouts(const sgl_kv_bootstrap *state, uint64_t room,
+                                        sgl_kv_remote_kv_layout *out, uint64_t capacity, uint64_t *count);
+/* The encoders (:685-706 and :720-749): write the frame's parts into `buf`
+ * and describe them in parts[SGL_KV_BOOTSTRAP_MAX_PARTS]. With buf NULL,
+ * only *bytes_needed is computed; a non-NULL buf shorter than that is
+ * AllocationOutOfBounds. The KVArgs frame has 14 parts as the reference
+ * writes it, 15 with a decode layout. A non-dummy transfer without an aux
+ * index is SGL_KV_BOOT_MISSING_AUX_INDEX. */
+int32_t sgl_kv_bootstrap_encode_kv_args(const sgl_kv_bootstrap_kv_args *args, uint8_t *buf, uint64_t capacity,
+                                        sgl_kv_frame_part *parts, uint32_t *part_count,
+                                        uint64_t *bytes_needed);
+int32_t sgl_kv_bootstrap_encode_transfer(const sgl_kv_bootstrap_transfer *transfer, uint8_t *buf,
+                                         uint64_t capacity, sgl_kv_frame_part *parts, uint32_t *part_count,
+                                         uint64_t *bytes_needed);
 
 /* ---- Transfer backend: KvTransferBackend (transfer.rs:1145-1151) ----
  * register / submit / poll / cancel / shutdown for a prefill pool and a

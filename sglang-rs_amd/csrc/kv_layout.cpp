@@ -80,6 +80,16 @@ extern "C" const char *sgl_kv_status_name(int32_t code) {
     case SGL_KV_ATTN_DEVICE_METADATA_INVALID: return "DeviceMetadataInvalid";
     case SGL_KV_ATTN_UNSUPPORTED_KV_DTYPE: return "UnsupportedKvDtype";
     case SGL_KV_ATTN_TENSOR_ROW_GEOMETRY_MISMATCH: return "TensorRowGeometryMismatch";
+    case SGL_KV_BOOT_MISSING_FIELD: return "MissingField";
+    case SGL_KV_BOOT_UTF8_FIELD: return "Utf8Field";
+    case SGL_KV_BOOT_INTEGER_FIELD: return "IntegerField";
+    case SGL_KV_BOOT_BINARY_LENGTH: return "BinaryLength";
+    case SGL_KV_BOOT_PACKED_LIST_HEADER: return "PackedListHeader";
+    case SGL_KV_BOOT_PACKED_LIST_LENGTH: return "PackedListLength";
+    case SGL_KV_BOOT_MISSING_TRANSFER_ROOM: return "MissingTransferRoom";
+    case SGL_KV_BOOT_MISSING_KV_ARGS: return "MissingKvArgsRegistration";
+    case SGL_KV_BOOT_MISSING_AUX_INDEX: return "MissingAuxIndex";
+    case SGL_KV_BOOT_DECODE_LAYOUT: return "DecodeLayout";
     case SGL_KV_LAYOUT_KV_PAIR_REQUIRES_TWO_TENSORS: return "KvPairRequiresTwoTensors";
     case SGL_KV_LAYOUT_TENSOR_PAIR_REQUIRES_TWO_TENSORS: return "TensorPairRequiresTwoTensors";
     case SGL_KV_LAYOUT_TENSOR_PAIR_SIZE_MISMATCH: return "TensorPairSizeMismatch";

@@ -131,6 +131,51 @@ class _DeviceBuffer(ctypes.Structure):
     _fields_ = [("ptr", ctypes.c_void_p), ("byte_len", _u64)]
 
 
+class _FramePart(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("len", _u64)]
+
+
+class _DecodeLayout(ctypes.Structure):
+    _fields_ = [("layout", _PagedLayout), ("head_layout", ctypes.c_uint32), ("reserved", ctypes.c_uint32),
+                ("heads", _u64)]
+
+
+def _lists_struct(ct):
+    class L(ctypes.Structure):
+        _fields_ = [("values", ctypes.POINTER(ct)), ("offsets", ctypes.POINTER(_u64)), ("count", _u64)]
+    return L
+
+
+_U64Lists, _U32Lists, _I32Lists = _lists_struct(_u64), _lists_struct(ctypes.c_uint32), _lists_struct(ctypes.c_int32)
+
+
+class _BootKvArgs(ctypes.Structure):
+    _fields_ = [("endpoint", ctypes.c_char_p), ("mooncake_session_id", ctypes.c_char_p),
+                ("dst_port", ctypes.c_uint32), ("dst_tp_rank", ctypes.c_int32),
+                ("dst_attn_tp_size", _u64), ("dst_kv_item_len", _u64),
+                ("dst_kv_ptrs", ctypes.POINTER(_u64)), ("dst_kv_ptr_count", _u64),
+                ("dst_aux_ptrs", ctypes.POINTER(_u64)), ("dst_aux_ptr_count", _u64),
+                ("dst_state_data_ptrs", _U64Lists), ("dst_state_item_lens", _U32Lists),
+                ("dst_state_dim_per_tensor", _U32Lists), ("decode_layout", ctypes.POINTER(_DecodeLayout))]
+
+
+class _BootTransfer(ctypes.Structure):
+    _fields_ = [("room", _u64), ("endpoint", ctypes.c_char_p), ("mooncake_session_id", ctypes.c_char_p),
+                ("dst_port", ctypes.c_uint32), ("is_dummy", ctypes.c_uint32),
+                ("dst_kv_indices", ctypes.POINTER(ctypes.c_int32)), ("dst_kv_index_count", _u64),
+                ("has_dst_aux_index", ctypes.c_uint32), ("dst_aux_index", ctypes.c_int32),
+                ("dst_state_indices", _I32Lists), ("required_dst_info_num", _u64),
+                ("has_decode_prefix_len", ctypes.c_uint32), ("reserved", ctypes.c_uint32),
+                ("decode_prefix_len", _u64)]
+
+
+class _RemoteKvLayout(ctypes.Structure):
+    _fields_ = [("mooncake_session_id", ctypes.c_char_p),
+                ("dst_kv_ptrs", ctypes.POINTER(_u64)), ("dst_kv_ptr_count", _u64),
+                ("dst_kv_indices", ctypes.POINTER(ctypes.c_int32)), ("dst_kv_index_count", _u64),
+                ("dst_kv_item_len", _u64), ("decode_layout", ctypes.POINTER(_DecodeLayout))]
+
+
 class _PairCopyBuffers(ctypes.Structure):
     _fields_ = [("keys", _DeviceBuffer), ("keys_offset", _u64), ("values", _DeviceBuffer),
                 ("values_offset", _u64), ("slot_indices", _DeviceBuffer),
@@ -362,6 +407,26 @@ _EXPORTS = {
                                                     _u64, ctypes.c_uint32, ctypes.c_void_p]),
     "sgl_rocm_kv_stream": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_uint32, ctypes.POINTER(_DeviceBuffer),
                                             ctypes.POINTER(_DeviceBuffer), _u64, ctypes.c_void_p]),
+    "sgl_kv_bootstrap_create": (ctypes.c_int32, [ctypes.POINTER(ctypes.c_void_p)]),
+    "sgl_kv_bootstrap_destroy": (ctypes.c_int32, [ctypes.c_void_p]),
+    "sgl_kv_bootstrap_ingest": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_FramePart), ctypes.c_uint32]),
+    "sgl_kv_bootstrap_registration_count": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_u64)]),
+    "sgl_kv_bootstrap_get_kv_args": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_char_p,
+                                                      ctypes.POINTER(_BootKvArgs)]),
+    "sgl_kv_bootstrap_transfer_status": (ctypes.c_int32, [ctypes.c_void_p, _u64, ctypes.POINTER(ctypes.c_int32)]),
+    "sgl_kv_bootstrap_room": (ctypes.c_int32, [ctypes.c_void_p, _u64, ctypes.POINTER(_u64),
+                                               ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(_u64),
+                                               ctypes.POINTER(_u64)]),
+    "sgl_kv_bootstrap_get_transfer": (ctypes.c_int32, [ctypes.c_void_p, _u64, ctypes.c_char_p,
+                                                       ctypes.POINTER(_BootTransfer)]),
+    "sgl_kv_bootstrap_remote_layouts": (ctypes.c_int32, [ctypes.c_void_p, _u64, ctypes.POINTER(_RemoteKvLayout),
+                                                         _u64, ctypes.POINTER(_u64)]),
+    "sgl_kv_bootstrap_encode_kv_args": (ctypes.c_int32, [ctypes.POINTER(_BootKvArgs), ctypes.c_void_p, _u64,
+                                                         ctypes.POINTER(_FramePart),
+                                                         ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(_u64)]),
+    "sgl_kv_bootstrap_encode_transfer": (ctypes.c_int32, [ctypes.POINTER(_BootTransfer), ctypes.c_void_p, _u64,
+                                                          ctypes.POINTER(_FramePart),
+                                                          ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(_u64)]),
 }
 
 _lib = None
@@ -1101,3 +1166,181 @@ def synthetic_words(seed: int, word_index) -> np.ndarray:
         z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
         z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
         return z ^ (z >> np.uint64(31))
+
+
+# --- bootstrap wire format (pd_bootstrap.rs) --------------------------------------------------
+
+BOOTSTRAP_MAX_PARTS = 16
+KV_POLL = {0: "Failed", 1: "Bootstrapping", 2: "WaitingForInput", 3: "Transferring", 4: "Success"}
+
+
+def _ptr_list(ptr, n):
+    return [ptr[i] for i in range(n)]
+
+
+def _lists_out(l):
+    return [[l.values[j] for j in range(l.offsets[i], l.offsets[i + 1])] for i in range(l.count)]
+
+
+def _lists_in(lists, ctype, struct):
+    """(struct, keep-alive arrays) for a list of lists."""
+    values = [v for one in lists for v in one]
+    offsets = [0]
+    for one in lists:
+        offsets.append(offsets[-1] + len(one))
+    va = (ctype * max(1, len(values)))(*values)
+    oa = (_u64 * len(offsets))(*offsets)
+    return struct(ctypes.cast(va, ctypes.POINTER(ctype)), ctypes.cast(oa, ctypes.POINTER(_u64)), len(lists)), (va, oa)
+
+
+class DecodeLayout:
+    """A decode pool's geometry as the layout extension advertises it: a
+    PagedKvCacheLayout, its head layout (NHD/HND) and head chunks per row."""
+
+    def __init__(self, layout: "PagedKvCacheLayout", head_layout: int = NHD, heads: int = 0):
+        self.layout, self.head_layout, self.heads = layout, head_layout, heads
+
+    def _c(self) -> _DecodeLayout:
+        return _DecodeLayout(self.layout._c, self.head_layout, 0, self.heads)
+
+    @classmethod
+    def _from_c(cls, p):
+        if not p:
+            return None
+        d = p.contents
+        c = _PagedLayout()
+        ctypes.pointer(c)[0] = d.layout
+        return cls(PagedKvCacheLayout(c), d.head_layout, d.heads)
+
+
+def _frame_parts(frame):
+    """(parts array, keep-alive buffers) for a list of bytes-like parts."""
+    bufs = [ctypes.create_string_buffer(bytes(p), max(1, len(p))) for p in frame]
+    parts = (_FramePart * max(1, len(frame)))(
+        *[_FramePart(ctypes.cast(b, ctypes.c_void_p), len(p)) for b, p in zip(bufs, frame)])
+    return parts, bufs
+
+
+def _emit(fn, struct):
+    needed, count = _u64(), ctypes.c_uint32()
+    _call(fn, ctypes.byref(struct), None, 0, None, ctypes.byref(count), ctypes.byref(needed))
+    buf = ctypes.create_string_buffer(max(1, needed.value))
+    parts = (_FramePart * BOOTSTRAP_MAX_PARTS)()
+    _call(fn, ctypes.byref(struct), ctypes.cast(buf, ctypes.c_void_p), needed.value, parts,
+          ctypes.byref(count), ctypes.byref(needed))
+    base = ctypes.addressof(buf)
+    raw = buf.raw
+    return [raw[parts[i].data - base: parts[i].data - base + parts[i].len] if parts[i].len else b""
+            for i in range(count.value)]
+
+
+def encode_kv_args_frame(*, endpoint: str, dst_port: int, mooncake_session_id: str, dst_kv_ptrs,
+                         dst_aux_ptrs=(), dst_state_data_ptrs=(), dst_tp_rank: int = 0,
+                         dst_attn_tp_size: int = 1, dst_kv_item_len: int = 0, dst_state_item_lens=(),
+                         dst_state_dim_per_tensor=(), decode_layout: DecodeLayout | None = None):
+    """MooncakeDecodeKvArgsRegistration::to_frame (pd_bootstrap.rs:685-706),
+    plus the decode-layout part when `decode_layout` is given."""
+    kp = (_u64 * max(1, len(dst_kv_ptrs)))(*dst_kv_ptrs)
+    ap = (_u64 * max(1, len(dst_aux_ptrs)))(*dst_aux_ptrs)
+    sd, k1 = _lists_in(dst_state_data_ptrs, _u64, _U64Lists)
+    il, k2 = _lists_in(dst_state_item_lens, ctypes.c_uint32, _U32Lists)
+    dp, k3 = _lists_in(dst_state_dim_per_tensor, ctypes.c_uint32, _U32Lists)
+    dl = decode_layout._c() if decode_layout is not None else None
+    a = _BootKvArgs(endpoint.encode(), mooncake_session_id.encode(), dst_port, dst_tp_rank, dst_attn_tp_size,
+                    dst_kv_item_len, ctypes.cast(kp, ctypes.POINTER(_u64)), len(dst_kv_ptrs),
+                    ctypes.cast(ap, ctypes.POINTER(_u64)), len(dst_aux_ptrs), sd, il, dp,
+                    ctypes.pointer(dl) if dl is not None else None)
+    return _emit(lib().sgl_kv_bootstrap_encode_kv_args, a)
+
+
+def encode_transfer_frame(*, room: int, endpoint: str, dst_port: int, mooncake_session_id: str,
+                          dst_kv_indices=(), dst_aux_index: int | None = 0, dst_state_indices=(),
+                          required_dst_info_num: int = 1, decode_prefix_len: int | None = None,
+                          is_dummy: bool = False):
+    """MooncakeDecodeTransferMetadata::to_frame (pd_bootstrap.rs:720-749)."""
+    ki = (ctypes.c_int32 * max(1, len(dst_kv_indices)))(*dst_kv_indices)
+    si, keep = _lists_in(dst_state_indices, ctypes.c_int32, _I32Lists)
+    t = _BootTransfer(room, endpoint.encode(), mooncake_session_id.encode(), dst_port, int(is_dummy),
+                      ctypes.cast(ki, ctypes.POINTER(ctypes.c_int32)), len(dst_kv_indices),
+                      0 if dst_aux_index is None else 1, dst_aux_index or 0, si, required_dst_info_num,
+                      0 if decode_prefix_len is None else 1, 0, decode_prefix_len or 0)
+    return _emit(lib().sgl_kv_bootstrap_encode_transfer, t)
+
+
+class PrefillBootstrapState:
+    """The Mooncake tables of PrefillBootstrapState (pd_bootstrap.rs:150-270)."""
+
+    def __init__(self):
+        h = ctypes.c_void_p()
+        _call(lib().sgl_kv_bootstrap_create, ctypes.byref(h))
+        self._h = h.value
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().sgl_kv_bootstrap_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def ingest_mooncake_bootstrap_frame(self, frame):
+        parts, keep = _frame_parts(frame)
+        _call(lib().sgl_kv_bootstrap_ingest, self._h, parts, len(frame))
+
+    def decode_kv_args_registration_count(self) -> int:
+        n = _u64()
+        _call(lib().sgl_kv_bootstrap_registration_count, self._h, ctypes.byref(n))
+        return n.value
+
+    def decode_kv_args(self, session: str) -> dict:
+        a = _BootKvArgs()
+        _call(lib().sgl_kv_bootstrap_get_kv_args, self._h, session.encode(), ctypes.byref(a))
+        return {"endpoint": a.endpoint.decode(), "dst_port": a.dst_port,
+                "mooncake_session_id": a.mooncake_session_id.decode(),
+                "dst_kv_ptrs": _ptr_list(a.dst_kv_ptrs, a.dst_kv_ptr_count),
+                "dst_aux_ptrs": _ptr_list(a.dst_aux_ptrs, a.dst_aux_ptr_count),
+                "dst_state_data_ptrs": _lists_out(a.dst_state_data_ptrs),
+                "dst_tp_rank": a.dst_tp_rank, "dst_attn_tp_size": a.dst_attn_tp_size,
+                "dst_kv_item_len": a.dst_kv_item_len,
+                "dst_state_item_lens": _lists_out(a.dst_state_item_lens),
+                "dst_state_dim_per_tensor": _lists_out(a.dst_state_dim_per_tensor),
+                "decode_layout": DecodeLayout._from_c(a.decode_layout)}
+
+    def transfer_status(self, room: int):
+        st = ctypes.c_int32()
+        _call(lib().sgl_kv_bootstrap_transfer_status, self._h, room, ctypes.byref(st))
+        return None if st.value < 0 else KV_POLL[st.value]
+
+    def transfer_room(self, room: int) -> dict:
+        req, has, pre, n = _u64(), ctypes.c_uint32(), _u64(), _u64()
+        _call(lib().sgl_kv_bootstrap_room, self._h, room, ctypes.byref(req), ctypes.byref(has),
+              ctypes.byref(pre), ctypes.byref(n))
+        return {"required_dst_info_num": req.value, "decode_prefix_len": pre.value if has.value else None,
+                "transfer_count": n.value}
+
+    def transfer(self, room: int, session: str) -> dict:
+        t = _BootTransfer()
+        _call(lib().sgl_kv_bootstrap_get_transfer, self._h, room, session.encode(), ctypes.byref(t))
+        return {"room": t.room, "endpoint": t.endpoint.decode(), "dst_port": t.dst_port,
+                "mooncake_session_id": t.mooncake_session_id.decode(), "is_dummy": bool(t.is_dummy),
+                "dst_kv_indices": _ptr_list(t.dst_kv_indices, t.dst_kv_index_count),
+                "dst_aux_index": t.dst_aux_index if t.has_dst_aux_index else None,
+                "dst_state_indices": _lists_out(t.dst_state_indices),
+                "required_dst_info_num": t.required_dst_info_num,
+                "decode_prefix_len": t.decode_prefix_len if t.has_decode_prefix_len else None}
+
+    def remote_kv_layouts_for_room(self, room: int):
+        """[(session, {dst_kv_ptrs, dst_kv_indices, dst_kv_item_len, decode_layout})]."""
+        n = _u64()
+        _call(lib().sgl_kv_bootstrap_remote_layouts, self._h, room, None, 0, ctypes.byref(n))
+        out = (_RemoteKvLayout * max(1, n.value))()
+        _call(lib().sgl_kv_bootstrap_remote_layouts, self._h, room, out, n.value, ctypes.byref(n))
+        return [(l.mooncake_session_id.decode(),
+                 {"dst_kv_ptrs": _ptr_list(l.dst_kv_ptrs, l.dst_kv_ptr_count),
+                  "dst_kv_indices": _ptr_list(l.dst_kv_indices, l.dst_kv_index_count),
+                  "dst_kv_item_len": l.dst_kv_item_len,
+                  "decode_layout": DecodeLayout._from_c(l.decode_layout)})
+                for l in out[: n.value]]

@@ -290,3 +290,55 @@ def test_transfer_layers_matches_per_layer_oracle(k):
         k.transfer_layers(view(src, t.src, first), s_stride, sh.layers,
                           kv.device_buffer(ss.ptr, ss.nbytes), t.rows, view(dst, t.dst, first),
                           d_stride, kv.device_buffer(ds.ptr, ds.nbytes))
+
+
+@pytest.mark.parametrize("mode", [kv.BACKEND_DIRECT, kv.BACKEND_STAGED])
+def test_bootstrap_frames_drive_the_backend(k, mode):
+    """The decode side advertises its pool in bootstrap frames: KVArgs with
+    dst_kv_ptrs = [pool base] and the decode-layout extension (page size 16,
+    head-major), then one transfer frame per request carrying its page
+    table as dst_kv_indices and decode_prefix_len. The prefill side
+    ingests the frames, rebuilds the decode registration from the
+    advertised layout and base pointer, and moves each request's uncached
+    tokens through the backend; every byte matches the oracle."""
+    rng = np.random.default_rng(300 + mode)
+    pools = _Pools(seed=30 + mode)
+    decode_layout = kv.DecodeLayout(pools.dec, kv.HND, H)
+    frames = [kv.encode_kv_args_frame(endpoint="10.0.0.9", dst_port=41001, mooncake_session_id="decode-0",
+                                      dst_kv_ptrs=[pools.dst.ptr],
+                                      dst_kv_item_len=pools.dec._c.runtime.page_size_bytes,
+                                      decode_layout=decode_layout)]
+    groups = rng.permutation(DECODE_PAGES).reshape(8, -1)
+    requests = {}
+    for i, (room, cached, n) in enumerate([(51, 0, 90), (52, 32, 140), (53, 16, 1)]):
+        slots, table = _span(rng, cached, n, groups[i])
+        requests[room] = (cached, slots)
+        frames.append(kv.encode_transfer_frame(room=room, endpoint="10.0.0.9", dst_port=41001,
+                                               mooncake_session_id="decode-0", dst_kv_indices=table,
+                                               dst_aux_index=0, decode_prefix_len=cached + n))
+    state = kv.PrefillBootstrapState()
+    for f in frames:
+        state.ingest_mooncake_bootstrap_frame(f)
+    b = kv.RocmKvTransferBackend(k, mode, max_rows=256)
+    registered = False
+    for room, (cached, slots) in requests.items():
+        assert state.transfer_status(room) == "WaitingForInput"
+        [(session, remote)] = state.remote_kv_layouts_for_room(room)
+        adv = remote["decode_layout"]
+        assert session == "decode-0" and adv is not None and adv.head_layout == kv.HND
+        if not registered:
+            base = remote["dst_kv_ptrs"][0]
+            b.register(pools.pre, pools.src.ptr, pools.src.nbytes, adv.layout, base,
+                       adv.layout.total_byte_len, decode_head_layout=adv.head_layout,
+                       decode_heads=adv.heads)
+            registered = True
+        table = remote["dst_kv_indices"]
+        b.submit(room, "", cached, slots, table)
+        pools.expect(cached, slots, table)
+    b.wait()
+    events, pending = b.poll()
+    assert pending == 0 and sorted(e.bootstrap_room for e in events) == sorted(requests)
+    assert all(e.status == kv.TRANSFER_COMPLETED for e in events)
+    pools.check()
+    b.close()
+    state.close()

@@ -102,9 +102,10 @@ def _traffic_from_profiles(kernel: str, summary: str):
     return None
 
 
-def cpu_baseline(make, seconds: float = 10.0, rows: int = 8192):
-    """The CPU oracle's pack + unpack (1 thread) on the first `rows` tokens
-    of the workload, repeated for about `seconds`."""
+def cpu_baseline(make, seconds: float = 10.0, rows: int = 8192, threads: int = 1):
+    """The CPU oracle's pack + unpack on `threads` host threads (rows split
+    evenly) on the first `rows` tokens of the workload, repeated for about
+    `seconds`."""
     import oracle
     from sgl_rocm_kv import workloads as wl
     t = wl.scaled(make(), rows, seed=1)
@@ -124,9 +125,9 @@ def cpu_baseline(make, seconds: float = 10.0, rows: int = 8192):
         pools.append((opool(t.src), opool(t.dst), part[: n * rb], part[n * rb:] if T == 2 else None))
     def one_pass():
         for sp, dp, r0, r1 in pools:
-            oracle.pack(sp, src, t.src_slots, r0, r1, rb, rb, threads=1)
+            oracle.pack(sp, src, t.src_slots, r0, r1, rb, rb, threads=threads)
         for sp, dp, r0, r1 in pools:
-            oracle.unpack(dp, dst, t.dst_slots, r0, r1, rb, rb, threads=1)
+            oracle.unpack(dp, dst, t.dst_slots, r0, r1, rb, rb, threads=threads)
 
     one_pass()   # untimed: faults every page of the lazily mapped buffers in
     reps, t0 = 0, time.perf_counter()
@@ -137,10 +138,10 @@ def cpu_baseline(make, seconds: float = 10.0, rows: int = 8192):
         if el >= seconds or reps >= 1000:
             break
     gbs = 4 * t.payload_bytes * reps / el / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"{t.name.split(' (')[0]} shape, first {n} tokens ({sh.layers} layers, "
                       f"{t.payload_bytes >> 20} MiB payload), pack+unpack x {reps} in {el:.1f} s, "
-                      f"oracle/kv_oracle.c single thread"}
+                      f"oracle/kv_oracle.c, {threads} thread{'s' if threads > 1 else ''}"}
 
 
 def _views(kv, buf, spec, sh, layer, scale=None):
@@ -637,7 +638,10 @@ def main():
                     help="layer: one pack and one unpack launch per layer; layers: one launch of "
                          "each covering every layer; auto (default): layers when one layer moves "
                          "less than 256 MiB (launch-bound sizes), else layer")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=6.0,
+                    help="seconds of CPU work per CPU-baseline figure")
+    ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1),
+                    help="threads of the all-core CPU baseline (default: the box's share, at most 16)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="after timing, run 3 hipMemcpyDtoD copies of exactly 1 GiB: a plain copy "
@@ -695,6 +699,12 @@ def main():
         log("cpu baseline (oracle, 1 thread)")
         out["cpu_baseline"] = (attention_cpu_baseline(args.cpu_seconds, args.config == "attn_hnd")
                                if attention else cpu_baseline(makers[args.config], args.cpu_seconds))
+        if not attention and args.cpu_threads > 1:
+            # The same sample on the box's host share of cores, beside the
+            # single-thread figure.
+            log(f"cpu baseline (oracle, {args.cpu_threads} threads)")
+            out["cpu_baseline_all_cores"] = cpu_baseline(makers[args.config], args.cpu_seconds,
+                                                         threads=args.cpu_threads)
     print(json.dumps(out), flush=True)
 
 

@@ -266,6 +266,25 @@ def run_coresident(t, config, args):
         s_pack.synchronize()
         log(f"calibration copies done (3 x {span} B device-to-device)")
 
+    # The device's contiguous-copy ceiling, measured in the same process on
+    # the transfer buffer (1 GiB each way; skipped for buffers too small to
+    # stream past the caches).
+    ceiling = None
+    span = min(1 << 30, xfer.nbytes // 2)
+    if span >= 256 << 20:
+        a_buf = kv.device_buffer(xfer.ptr, span)
+        b_buf = kv.device_buffer(xfer.ptr + span, span)
+        for _ in range(3):
+            k.stream_ceiling(kv.STREAM_COPY, a_buf, b_buf, span, s_pack)
+        c0, c1 = hip.Event(), hip.Event()
+        c0.record(s_pack)
+        for _ in range(10):
+            k.stream_ceiling(kv.STREAM_COPY, a_buf, b_buf, span, s_pack)
+        c1.record(s_pack)
+        c1.synchronize()
+        ceiling = 2 * span * 10 / (c0.elapsed_ms(c1) / 1e3) / 1e9
+        log(f"contiguous copy ceiling on this device: {ceiling:.0f} GB/s")
+
     step_bytes = t.algorithmic_bytes
     gbs = step_bytes / (wall / args.steps) / 1e9
     launch_bytes = T * n * rb * 2     # one layer; pack_ms / unpack_ms are per layer
@@ -288,6 +307,10 @@ def run_coresident(t, config, args):
                          "payload_bytes": t.payload_bytes, "algorithmic_bytes_per_step": step_bytes,
                          "streams": args.streams, "launch": args.launch},
         "per_layer_p50_us": round(float(np.percentile(layer_us, 50)), 2),
+        "copy_ceiling": None if ceiling is None else {
+            "gbs": round(ceiling, 1), "value_frac_of_ceiling": round(gbs / ceiling, 4),
+            "note": "sgl_rocm_kv_stream contiguous copy of 1 GiB, same process: the most any "
+                    "read+write stream reaches on this device"},
         "pack_us_avg": round(avg_pack * 1e3, 2),
         "unpack_us_avg": round(avg_unpack * 1e3, 2),
         "kernel_sum_gbs": round(kernel_gbs, 1),

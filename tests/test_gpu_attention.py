@@ -199,6 +199,43 @@ def test_slots_outside_the_sequences_hold_nan(k, dk, dv, P):
     np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
 
 
+def _random_shape(rng):
+    """One random attention problem: head dims, GQA group, page size (powers
+    of two take the pipelined body, others the generic one), head layout,
+    request lengths (tails not a multiple of 32), queries per request."""
+    H = int(rng.choice([1, 2, 4, 8]))
+    group = int(rng.choice([1, 2, 4, 5, 8, 16, 24]))
+    dk = int(rng.choice([8, 16, 40, 64, 96, 128, 192]))
+    dv = dk if rng.random() < 0.7 else int(rng.choice([8, 64, 128, 136]))
+    P = int(rng.choice([1, 3, 8, 16, 64]))
+    hnd = bool(rng.random() < 0.5)
+    requests = int(rng.integers(1, 6))
+    lens = rng.integers(1, 700, size=requests)
+    return dict(H=H, qh=H * group, dk=dk, dv=dv, P=P, hnd=hnd, lens=lens)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_shapes(k, seed):
+    rng = np.random.default_rng(1000 + seed)
+    sh = _random_shape(rng)
+    lens = sh["lens"]
+    total = int(lens.sum())
+    pages = -(-total // sh["P"]) + 8
+    c = _Case(rng, P=sh["P"], L=2, H=sh["H"], dk=sh["dk"], dv=sh["dv"], qh=sh["qh"], pages=pages, layer=1,
+              hnd=sh["hnd"])
+    rso = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint64)
+    slots = rng.choice(c.layout.slot_count, size=total, replace=False).astype(np.uint64)
+    nq = int(rng.integers(1, 9))
+    qri = rng.integers(0, len(lens), size=nq)
+    qsl = np.array([rng.integers(1, lens[r] + 1) for r in qri])
+    q = _bf16_normal(rng, nq * sh["qh"] * sh["dk"]).reshape(nq, sh["qh"], sh["dk"])
+    _say(f"random attention seed={seed} {dict((k_, v) for k_, v in sh.items() if k_ != 'lens')} "
+         f"lens={list(lens)} queries={nq}")
+    got, want = c.run(k, q, qri, qsl, rso, slots, 1.0 / math.sqrt(sh["dk"]), max_len=int(lens.max()),
+                      use_async=bool(seed % 2))
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+
+
 def test_metadata_errors(k):
     """Bad request index, empty or overlong length, and a slot past the pool
     raise DeviceMetadataInvalid with the reference's flag values."""

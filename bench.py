@@ -77,7 +77,8 @@ DESCRIPTIONS = {
             "random page table, 64 requests x 2048 tokens, one decode query each with 32 query heads",
     "attn_hnd": "paged-attention decode as attn, over head-major (HND) pages",
     "ceilings": "the device's streaming ceilings: contiguous copy, read and write of 1 GiB in "
-                "16-byte non-temporal vectors (sgl_rocm_kv_stream), and hipMemcpyDtoD",
+                "16-byte non-temporal vectors (sgl_rocm_kv_stream), hipMemcpyDtoD, and the host "
+                "link (1 GiB DMA copies to and from pinned host memory, one direction at a time)",
     "c5": "C5: ragged radix-prefix GQA transfer (Llama-3-8B shape), 512 requests log-uniform "
           "[16,32768], page-aligned cached prefixes U[0,0.9]; request waves through the layer "
           "pipeline pack -> D2H -> pinned host -> H2D -> unpack on 4 streams",
@@ -632,6 +633,22 @@ def run_ceilings(args):
         ms = e0.elapsed_ms(e1) / args.steps
         out[name] = (moved / (ms / 1e3) / 1e9, ms)
         log(f"{name}: {ms * 1e3:.1f} us per GiB pass, {out[name][0]:.0f} GB/s")
+    # The host link (what bounds C5): one direction at a time, runtime DMA
+    # copies of 1 GiB between HBM and pinned host memory.
+    host = hip.PinnedBuffer(n)
+    for name, launch in (("link_d2h", lambda: hip.memcpy_async(host.ptr, a.ptr, n, "d2h", s)),
+                         ("link_h2d", lambda: hip.memcpy_async(a.ptr, host.ptr, n, "h2d", s))):
+        launch()
+        e0, e1 = hip.Event(), hip.Event()
+        e0.record(s)
+        for _ in range(3):
+            launch()
+        e1.record(s)
+        e1.synchronize()
+        ms = e0.elapsed_ms(e1) / 3
+        out[name] = (n / (ms / 1e3) / 1e9, ms)
+        log(f"{name}: {ms:.1f} ms per GiB, {out[name][0]:.1f} GB/s")
+    host.free()
     k.check_errors(s)
     k.close()
     gbs = out["copy"][0]
@@ -642,6 +659,8 @@ def run_ceilings(args):
         "read_gbs": round(out["read"][0], 1),
         "write_gbs": round(out["write"][0], 1),
         "memcpy_dtod_gbs": round(out["memcpy_dtod"][0], 1),
+        "link_d2h_gbs": round(out["link_d2h"][0], 1),
+        "link_h2d_gbs": round(out["link_h2d"][0], 1),
         "roofline": {"bound": "hbm", "kernel": "sglkv_stream_copy", "achieved": round(gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": None, "algorithmic_bytes_per_launch": 2 * n},

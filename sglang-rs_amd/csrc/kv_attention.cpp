@@ -333,32 +333,53 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
                      ((poolp + lay.value_in_page_offset) % 16 == 0) &&
                      ((lay.page_stride_bytes | p.key_head_stride | p.key_token_stride | p.value_head_stride |
                        p.value_token_stride) % 16 == 0);
-    // Head dims up to 128 on 16-byte rows, power-of-two pages and strides
-    // that fit 32 bits take the software-pipelined body.
-    const bool pipe = vec && p.dk_pad <= 128 && p.dv <= SGLKV_ATTN_DV && p.page_shift < 32 &&
-                      c.slot_count < (1ull << 32) && lay.page_stride_bytes <= UINT32_MAX &&
-                      p.key_token_stride <= UINT32_MAX && p.value_token_stride <= UINT32_MAX;
-    const int which = !vec ? 1 : !pipe ? 0 : (p.dk == 128 && p.dv == 128) ? 2 : 3;
+    // 16-byte rows, power-of-two pages and strides that fit 32 bits admit
+    // the pipelined and wide bodies (32-bit slots, shift-and-mask pages);
+    // head dims up to 128 take the software-pipelined body.
+    const bool fast = vec && p.page_shift < 32 && c.slot_count < (1ull << 32) &&
+                      lay.page_stride_bytes <= UINT32_MAX && p.key_token_stride <= UINT32_MAX &&
+                      p.value_token_stride <= UINT32_MAX;
+    const bool pipe = fast && p.dk_pad <= 128 && p.dv <= SGLKV_ATTN_DV;
+    int which = !vec ? 1 : !pipe ? 0 : (p.dk == 128 && p.dv == 128) ? 2 : 3;
+    // Many query heads per KV head (more than one 16-head group) or wide
+    // values: the wide bodies share each K/V block among 4 head groups
+    // instead of every group and value block reading it again.
+    unsigned threads = 64;
+    unsigned lds = (unsigned)((SGLKV_ATTN_HEADS * (p.dk_pad + 8) + SGLKV_ATTN_DV * SGLKV_ATTN_VT_STRIDE) *
+                              sizeof(uint16_t));
+    if (fast && (p.head_groups > 1 || p.dv > SGLKV_ATTN_DV)) {
+        const unsigned narrow = SGLKV_ATTN_WIDE_LDS_BYTES(4u, 8u), wide = SGLKV_ATTN_WIDE_LDS_BYTES(18u, 32u);
+        if (p.dk_pad <= 128 && p.dv <= 128 && narrow <= (unsigned)ctx->max_lds_per_block) {
+            which = 5;
+            lds = narrow;
+            threads = 64 * SGLKV_ATTN_WIDE_WAVES;
+        } else if (p.dk_pad <= 576 && p.dv <= 512 && wide <= (unsigned)ctx->max_lds_per_block) {
+            which = 4;
+            lds = wide;
+            threads = 64 * SGLKV_ATTN_WIDE_WAVES;
+        }
+    }
     p.zero_row = ctx->zero_row;
     p.page_stride32 = (uint32_t)lay.page_stride_bytes;
     p.key_token_stride32 = (uint32_t)p.key_token_stride;
     p.value_token_stride32 = (uint32_t)p.value_token_stride;
-    const unsigned lds = (unsigned)((SGLKV_ATTN_HEADS * (p.dk_pad + 8) +
-                                     SGLKV_ATTN_DV * SGLKV_ATTN_VT_STRIDE) * sizeof(uint16_t));
     DeviceScope scope(ctx->device);
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
 
     // Workgroups before splitting; split each query's sequence so that the
     // launch fills every CU with as many workgroups as stay resident at
     // once (the kernel's occupancy at this LDS size), in one round.
+    const bool wide = which >= 4;
+    const uint64_t hblocks = (p.head_groups + SGLKV_ATTN_WIDE_GROUPS - 1) / SGLKV_ATTN_WIDE_GROUPS;
     uint64_t base = c.query_count;
-    if (mul_ovf(base, p.kv_heads, &base) || mul_ovf(base, p.head_groups, &base) ||
-        mul_ovf(base, p.dv_blocks, &base) || base > INT32_MAX)
+    if (mul_ovf(base, p.kv_heads, &base) || (wide && mul_ovf(base, hblocks, &base)) ||
+        (!wide && (mul_ovf(base, p.head_groups, &base) || mul_ovf(base, p.dv_blocks, &base))) ||
+        base > INT32_MAX)
         return too_large_dim("workgroups", base, INT32_MAX);
     if (ctx->attention_occupancy_lds[which] != lds) {
         int per_cu = 0;
         SGLKV_CHECK_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ctx->attention[which],
-                                                                           64, lds));
+                                                                           (int)threads, lds));
         ctx->attention_occupancy[which] = per_cu > 0 ? (uint32_t)per_cu : 1;
         ctx->attention_occupancy_lds[which] = lds;
     }
@@ -396,8 +417,8 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
     }
     if (clear_flag) SGLKV_CHECK_HIP(hipMemsetAsync(ctx->flag, 0, sizeof(uint32_t), s));
     void *args[] = {&p};
-    SGLKV_CHECK_HIP(hipModuleLaunchKernel(ctx->attention[which], (unsigned)base, (unsigned)splits, 1, 64, 1,
-                                          1, lds, s, args, nullptr));
+    SGLKV_CHECK_HIP(hipModuleLaunchKernel(ctx->attention[which], (unsigned)base, (unsigned)splits, 1, threads,
+                                          1, 1, lds, s, args, nullptr));
     if (splits > 1)
         SGLKV_CHECK_HIP(hipModuleLaunchKernel(ctx->attention_combine,
                                               (unsigned)(c.query_count * c.query_head_count), 1, 1, 128,

@@ -147,27 +147,32 @@ __device__ __forceinline__ void attn_stage_queries(const sglkv_attn_params &p, c
 }
 
 // Online-softmax state of one wave: lane (g, r) tracks head r.
-struct attn_state {
+// NJ = blocks of 16 value dims the wave accumulates.
+template <int NJ>
+struct attn_state_n {
     float m_run;   // running max (log2 units) of head r
     float l_part;  // this lane's share of head r's sum
-    sglkv_f32x4 o[SGLKV_ATTN_DV / 16];
+    sglkv_f32x4 o[NJ];
 };
+typedef attn_state_n<SGLKV_ATTN_DV / 16> attn_state;
 
-__device__ __forceinline__ void attn_state_init(attn_state &st) {
+template <int NJ>
+__device__ __forceinline__ void attn_state_init(attn_state_n<NJ> &st) {
     st.m_run = -3.402823466e+38f;
     st.l_part = 0.0f;
 #pragma unroll
-    for (uint32_t j = 0; j < SGLKV_ATTN_DV / 16; ++j) st.o[j] = sglkv_f32x4{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t j = 0; j < NJ; ++j) st.o[j] = sglkv_f32x4{0.f, 0.f, 0.f, 0.f};
 }
 
 // One 32-token block after q.k: sc[b][e] is head r's score of row 4g+e of
 // score block b (token 8g + 4b + e of the block), vb0/vb1 the validity
 // ballots of the rows, and vt the block's values transposed in LDS
 // (vt[dim][token]). Updates the softmax state and o += p.v.
-template <bool FULL_DV = false>
+// vt rows are VTS elements apart.
+template <bool FULL_DV = false, int NJ = SGLKV_ATTN_DV / 16, int VTS = SGLKV_ATTN_VT_STRIDE>
 __device__ __forceinline__ void attn_softmax_pv(const sglkv_attn_params &p, uint32_t g, uint32_t d0,
                                                 const sglkv_f32x4 (&sc)[2], uint64_t vb0, uint64_t vb1,
-                                                const uint16_t *vt, uint32_t r, attn_state &st) {
+                                                const uint16_t *vt, uint32_t r, attn_state_n<NJ> &st) {
     float x[8];
     float mx = -INFINITY;
 #pragma unroll
@@ -199,17 +204,16 @@ __device__ __forceinline__ void attn_softmax_pv(const sglkv_attn_params &p, uint
 #pragma unroll
     for (uint32_t e = 0; e < 4; ++e) arow[e] = __shfl(alpha, 4 * g + e);
 #pragma unroll
-    for (uint32_t j = 0; j < SGLKV_ATTN_DV / 16; ++j)
+    for (uint32_t j = 0; j < NJ; ++j)
 #pragma unroll
         for (uint32_t e = 0; e < 4; ++e) st.o[j][e] *= arow[e];
 
     __builtin_amdgcn_wave_barrier();
     // o[head 4g+e][dim 16j + r] += sum_t p[head][t] * v[t][dim].
 #pragma unroll
-    for (uint32_t j = 0; j < SGLKV_ATTN_DV / 16; ++j) {
+    for (uint32_t j = 0; j < NJ; ++j) {
         if (!FULL_DV && d0 + 16 * j >= p.dv) break;
-        const sglkv_u16x8 vv =
-            *reinterpret_cast<const sglkv_u16x8 *>(vt + (16 * j + r) * SGLKV_ATTN_VT_STRIDE + 8 * g);
+        const sglkv_u16x8 vv = *reinterpret_cast<const sglkv_u16x8 *>(vt + (16 * j + r) * VTS + 8 * g);
         st.o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(pbits), attn_as_bf16(vv), st.o[j], 0,
                                                           0, 0);
     }
@@ -217,8 +221,9 @@ __device__ __forceinline__ void attn_softmax_pv(const sglkv_attn_params &p, uint
 }
 
 // Output (one split) or the split record [m, l, o[0..dv)].
+template <int NJ>
 __device__ __forceinline__ void attn_finish(const sglkv_attn_params &p, const attn_work &w, uint32_t g,
-                                            uint32_t r, const attn_state &st) {
+                                            uint32_t r, const attn_state_n<NJ> &st) {
     float l_tot = st.l_part + __shfl_xor(st.l_part, 16);
     l_tot += __shfl_xor(l_tot, 32);
     if (p.splits == 1) {
@@ -226,7 +231,7 @@ __device__ __forceinline__ void attn_finish(const sglkv_attn_params &p, const at
 #pragma unroll
         for (uint32_t e = 0; e < 4; ++e) linv[e] = 1.0f / __shfl(l_tot, 4 * g + e);
 #pragma unroll
-        for (uint32_t j = 0; j < SGLKV_ATTN_DV / 16; ++j) {
+        for (uint32_t j = 0; j < NJ; ++j) {
             const uint32_t dim = w.d0 + 16 * j + r;
             if (dim >= p.dv) continue;
 #pragma unroll
@@ -244,7 +249,7 @@ __device__ __forceinline__ void attn_finish(const sglkv_attn_params &p, const at
             pr[1] = l_tot;
         }
 #pragma unroll
-        for (uint32_t j = 0; j < SGLKV_ATTN_DV / 16; ++j) {
+        for (uint32_t j = 0; j < NJ; ++j) {
             const uint32_t dim = w.d0 + 16 * j + r;
             if (dim >= p.dv) continue;
 #pragma unroll
@@ -540,6 +545,231 @@ __device__ __forceinline__ void attn_pipe_body(const sglkv_attn_params &p) {
     attn_finish(p, w, g, r, st);
 }
 
+// ---- Wide body: many query heads per KV head (MLA), dims up to 576/512 ----
+//
+// The reference's MLA decode calls this attention with every query head of
+// the model over one latent KV head (crates/sglang-srt/src/cuda_mla.rs:
+// 273-294): 128 heads, K rows of 576 and V rows of 512 for DeepSeek-V3.
+// Per-wave bodies would read each K row once per 16-head group and per
+// 128-dim value block (32 times for that shape). Here a workgroup of 8
+// waves owns (query, KV head, up to 4 groups of 16 query heads) and stages
+// each 32-token block once in LDS: K rows as they are (row-major), V rows
+// transposed (vt[dim][token], four tokens per 8-byte store). Wave w serves
+// head group w % 4 and half the value dims (w / 4), so a wave accumulates
+// at most 256 dims; the two waves of a group compute the same scores. The
+// queries sit in LDS. The next block's rows load into registers while the
+// current block computes; the slots of the block after that load one step
+// earlier still, into a two-entry ring in LDS. Rows past the end or with a
+// slot outside the pool read the context's zero row.
+
+template <int DKC, int NJ>  // K dims padded to 32*DKC, V dims to 16*NJ (NJ even, <= 32)
+struct attn_wide_geom {
+    static constexpr uint32_t B = SGLKV_ATTN_TOKENS;
+    static constexpr uint32_t THREADS = 64 * SGLKV_ATTN_WIDE_WAVES;
+    static constexpr uint32_t NJH = NJ / 2;                // value blocks per wave
+    static constexpr uint32_t KS = 32 * DKC + 8;          // LDS K and query row stride (u16)
+    static constexpr uint32_t VS = B + 8;                 // LDS vt row stride (u16)
+    static constexpr uint32_t KCOLS = 4 * DKC;            // 16-byte pieces per K row
+    static constexpr uint32_t KPIECES = B * KCOLS;
+    static constexpr uint32_t KPT = (KPIECES + THREADS - 1) / THREADS;
+    static constexpr uint32_t VGROUPS = 2 * NJ;           // 8-dim groups of V
+    static constexpr uint32_t KS_ELEMS = B * KS;
+    static constexpr uint32_t VT_ELEMS = 16 * NJ * VS;
+    static constexpr uint32_t QS_ELEMS = SGLKV_ATTN_WIDE_GROUPS * SGLKV_ATTN_HEADS * KS;
+    static constexpr uint32_t LDS_BYTES = 2 * (KS_ELEMS + VT_ELEMS + QS_ELEMS) + 2 * B * 4;
+    static_assert(NJ % 2 == 0 && NJ <= 32, "V staging covers 64 groups of 8 dims");
+    static_assert(LDS_BYTES == SGLKV_ATTN_WIDE_LDS_BYTES(DKC, NJ), "the host sizes the same LDS");
+    static_assert(SGLKV_ATTN_WIDE_WAVES == 2 * SGLKV_ATTN_WIDE_GROUPS, "two waves per head group");
+};
+
+constexpr uint32_t kAttnInvalidSlot = 0xFFFFFFFFu;  // the host keeps slot_count below 2^32
+
+// A slot value of token `tok` checked against the chunk end and the pool.
+__device__ __forceinline__ uint32_t attn_wide_slot(const sglkv_attn_params &p, uint64_t raw, uint64_t tok,
+                                                   uint64_t t1) {
+    if (tok >= t1) return kAttnInvalidSlot;
+    if (raw >= p.slot_count) {
+        atomicOr(p.flag, SGLKV_FLAG_ATTN_SLOT);
+        return kAttnInvalidSlot;
+    }
+    return static_cast<uint32_t>(raw);
+}
+
+// One thread's share of a block: K pieces tid + k*THREADS (token =
+// piece / KCOLS), and V dims 8*(tid/8) .. +7 of tokens 4*(tid%8) .. +3.
+template <int DKC, int NJ>
+struct attn_wide_stage {
+    sglkv_u16x8 k[attn_wide_geom<DKC, NJ>::KPT];
+    sglkv_u16x8 v[4];
+};
+
+template <int DKC, int NJ>
+__device__ __forceinline__ void attn_wide_load(const sglkv_attn_params &p, uint64_t kbase, uint64_t vbase,
+                                               const uint32_t *ring, uint32_t tid,
+                                               attn_wide_stage<DKC, NJ> &st) {
+    typedef attn_wide_geom<DKC, NJ> G;
+    const uint64_t zero = reinterpret_cast<uint64_t>(p.zero_row);
+    const uint32_t mask = (1u << p.page_shift) - 1;
+#pragma unroll
+    for (uint32_t k = 0; k < G::KPT; ++k) {
+        const uint32_t piece = tid + k * G::THREADS;
+        const uint32_t tok = piece / G::KCOLS, col = piece % G::KCOLS;
+        const uint32_t s32 = piece < G::KPIECES ? ring[tok] : kAttnInvalidSlot;
+        const bool ok = s32 != kAttnInvalidSlot && 8 * col < p.dk;
+        const uint64_t row = kbase + static_cast<uint64_t>(s32 >> p.page_shift) * p.page_stride32 +
+                             static_cast<uint64_t>(s32 & mask) * p.key_token_stride32 + 16ull * col;
+        st.k[k] = *reinterpret_cast<__attribute__((address_space(1))) const sglkv_u16x8 *>(ok ? row : zero);
+    }
+    const uint32_t tg = tid & 7, dg = tid >> 3;
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+        const uint32_t s32 = dg < G::VGROUPS ? ring[4 * tg + i] : kAttnInvalidSlot;
+        const uint32_t dim = 8 * dg;
+        const bool ok = s32 != kAttnInvalidSlot && dim < p.dv;
+        const uint64_t row = vbase + static_cast<uint64_t>(s32 >> p.page_shift) * p.page_stride32 +
+                             static_cast<uint64_t>(s32 & mask) * p.value_token_stride32 + 2ull * dim;
+        st.v[i] = *reinterpret_cast<__attribute__((address_space(1))) const sglkv_u16x8 *>(ok ? row : zero);
+    }
+}
+
+template <int DKC, int NJ>
+__device__ __forceinline__ void attn_wide_store(uint16_t *ks, uint16_t *vt, uint32_t tid,
+                                                const attn_wide_stage<DKC, NJ> &st) {
+    typedef attn_wide_geom<DKC, NJ> G;
+#pragma unroll
+    for (uint32_t k = 0; k < G::KPT; ++k) {
+        const uint32_t piece = tid + k * G::THREADS;
+        if (piece < G::KPIECES)
+            *reinterpret_cast<sglkv_u16x8 *>(ks + (piece / G::KCOLS) * G::KS + 8 * (piece % G::KCOLS)) = st.k[k];
+    }
+    const uint32_t tg = tid & 7, dg = tid >> 3;
+    if (dg < G::VGROUPS) {
+#pragma unroll
+        for (uint32_t e = 0; e < 8; ++e) {
+            sglkv_u16x4 t4;
+#pragma unroll
+            for (uint32_t i = 0; i < 4; ++i) t4[i] = st.v[i][e];
+            *reinterpret_cast<sglkv_u16x4 *>(vt + (8 * dg + e) * G::VS + 4 * tg) = t4;
+        }
+    }
+}
+
+template <int DKC, int NJ>
+__device__ __forceinline__ void attn_wide_body(const sglkv_attn_params &p) {
+    typedef attn_wide_geom<DKC, NJ> G;
+    constexpr uint32_t B = G::B;
+    extern __shared__ __attribute__((aligned(16))) uint16_t attn_lds[];
+    uint16_t *ks = attn_lds;
+    uint16_t *vt = attn_lds + G::KS_ELEMS;
+    uint16_t *qs = attn_lds + G::KS_ELEMS + G::VT_ELEMS;               // [group][head][KS]
+    uint32_t *ring = reinterpret_cast<uint32_t *>(qs + G::QS_ELEMS);  // [2][B]
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const uint32_t g = lane >> 4, r = lane & 15;
+    const uint32_t grp = wv % SGLKV_ATTN_WIDE_GROUPS, half = wv / SGLKV_ATTN_WIDE_GROUPS;
+
+    // Workgroup -> (query, KV head, block of up to 4 head groups); the head
+    // block varies slowest, so the workgroups of one query that read the
+    // same rows run on one XCD when query_count * kv_heads is a multiple
+    // of 8.
+    const uint32_t hblocks = (p.head_groups + SGLKV_ATTN_WIDE_GROUPS - 1) / SGLKV_ATTN_WIDE_GROUPS;
+    uint64_t bx = blockIdx.x;
+    const uint64_t q = bx % p.query_count;
+    bx /= p.query_count;
+    const uint32_t kvh = static_cast<uint32_t>(bx % p.kv_heads);
+    const uint32_t hb = static_cast<uint32_t>(bx / p.kv_heads);
+    const uint32_t split = blockIdx.y;
+    uint64_t start = 0, len = 0;
+    if (!attn_metadata(p, q, tid == 0 && split == 0 && hb == 0 && kvh == 0, &start, &len)) return;
+    const uint64_t t0 = static_cast<uint64_t>(split) * p.chunk_tokens;
+    if (t0 >= len || hb >= hblocks) return;
+    const uint64_t t1 = len < t0 + p.chunk_tokens ? len : t0 + p.chunk_tokens;
+    const uint32_t hg = hb * SGLKV_ATTN_WIDE_GROUPS + grp;
+    const bool active = hg < p.head_groups;
+    const uint32_t d0 = half * 16 * G::NJH;
+    attn_work w;
+    w.q = q;
+    w.start = start;
+    w.t0 = t0;
+    w.t1 = t1;
+    w.kvh = kvh;
+    w.h0 = kvh * p.group + hg * SGLKV_ATTN_HEADS;
+    w.nh = !active ? 0
+                   : (p.group - hg * SGLKV_ATTN_HEADS < SGLKV_ATTN_HEADS ? p.group - hg * SGLKV_ATTN_HEADS
+                                                                         : SGLKV_ATTN_HEADS);
+    w.d0 = d0;
+    w.split = split;
+    w.dblk = half;  // only the first half writes a split record's (m, l)
+
+    // The group's queries (the B operand of q.k) go to LDS rows 16*grp ..,
+    // zero past the group or past dk, written by the group's first wave;
+    // the barrier after the prologue publishes them.
+    uint16_t *qw = qs + SGLKV_ATTN_HEADS * grp * G::KS;
+    if (half == 0) {
+        for (uint32_t i = lane; i < SGLKV_ATTN_HEADS * 32 * DKC; i += 64) {
+            const uint32_t h = i / (32 * DKC), d = i % (32 * DKC);
+            uint16_t v = 0;
+            if (h < w.nh && d < p.dk) v = p.queries[(q * p.query_heads + w.h0 + h) * p.dk + d];
+            qw[h * G::KS + d] = v;
+        }
+    }
+
+    const uint64_t pool = reinterpret_cast<uint64_t>(p.pool);
+    const uint64_t kbase = pool + p.key_offset + kvh * p.key_head_stride;
+    const uint64_t vbase = pool + p.value_offset + kvh * p.value_head_stride;
+
+    // Prologue: the slots of blocks 0 and 1, the rows of block 0.
+    uint64_t sraw = 0;
+    if (tid < B) {
+        const uint64_t tok = t0 + tid;
+        ring[tid] = attn_wide_slot(p, p.sequence_slots[start + (tok < t1 ? tok : t1 - 1)], tok, t1);
+        const uint64_t tok1 = t0 + B + tid;
+        sraw = p.sequence_slots[start + (tok1 < t1 ? tok1 : t1 - 1)];
+    }
+    __syncthreads();
+    attn_wide_stage<DKC, NJ> stage;
+    attn_wide_load<DKC, NJ>(p, kbase, vbase, ring, tid, stage);
+    attn_wide_store<DKC, NJ>(ks, vt, tid, stage);
+    if (tid < B) ring[B + tid] = attn_wide_slot(p, sraw, t0 + B + tid, t1);
+    __syncthreads();
+
+    attn_state_n<G::NJH> st;
+    attn_state_init(st);
+    uint32_t parity = 0;  // ring entry of the block in LDS
+    for (uint64_t tb = t0; tb < t1; tb += B, parity ^= 1) {
+        const bool more = tb + B < t1;
+        const bool further = tb + 2 * B < t1;
+        if (more) attn_wide_load<DKC, NJ>(p, kbase, vbase, ring + (parity ^ 1) * B, tid, stage);
+        if (tid < B && further) {
+            const uint64_t tok = tb + 2 * B + tid;
+            sraw = p.sequence_slots[start + (tok < t1 ? tok : t1 - 1)];
+        }
+        if (active) {
+            // q.k: row r of score block b is token 8*(r/4) + 4b + r%4.
+            sglkv_f32x4 sc[2] = {sglkv_f32x4{0.f, 0.f, 0.f, 0.f}, sglkv_f32x4{0.f, 0.f, 0.f, 0.f}};
+            const uint32_t row0 = 8 * (r >> 2) + (r & 3);
+            for (uint32_t c = 0; c < DKC; ++c) {
+                const sglkv_u16x8 qv = *reinterpret_cast<const sglkv_u16x8 *>(qw + r * G::KS + 32 * c + 8 * g);
+#pragma unroll
+                for (uint32_t b = 0; b < 2; ++b) {
+                    const sglkv_u16x8 kv =
+                        *reinterpret_cast<const sglkv_u16x8 *>(ks + (row0 + 4 * b) * G::KS + 32 * c + 8 * g);
+                    sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(kv), attn_as_bf16(qv), sc[b], 0,
+                                                                    0, 0);
+                }
+            }
+            const uint32_t *cur = ring + parity * B;
+            const uint64_t vb0 = __ballot(cur[row0] != kAttnInvalidSlot);
+            const uint64_t vb1 = __ballot(cur[row0 + 4] != kAttnInvalidSlot);
+            attn_softmax_pv<false, G::NJH, G::VS>(p, g, d0, sc, vb0, vb1, vt + d0 * G::VS, r, st);
+        }
+        __syncthreads();  // every wave is done with this block's K, V and slots
+        if (more) attn_wide_store<DKC, NJ>(ks, vt, tid, stage);
+        if (tid < B && further) ring[parity * B + tid] = attn_wide_slot(p, sraw, tb + 2 * B + tid, t1);
+        __syncthreads();
+    }
+    if (active) attn_finish<G::NJH>(p, w, g, r, st);
+}
+
 }  // namespace
 
 extern "C" __global__ __launch_bounds__(64) void sglkv_paged_attention_v16(sglkv_attn_params p) {
@@ -548,6 +778,15 @@ extern "C" __global__ __launch_bounds__(64) void sglkv_paged_attention_v16(sglkv
 
 extern "C" __global__ __launch_bounds__(64) void sglkv_paged_attention_v2(sglkv_attn_params p) {
     attn_body<false>(p);
+}
+
+// Many heads per KV head: MLA widths (K <= 576, V <= 512) / dims <= 128.
+extern "C" __global__ __launch_bounds__(512) void sglkv_paged_attention_wide576(sglkv_attn_params p) {
+    attn_wide_body<18, 32>(p);
+}
+
+extern "C" __global__ __launch_bounds__(512) void sglkv_paged_attention_wide128(sglkv_attn_params p) {
+    attn_wide_body<4, 8>(p);
 }
 
 // Head dims exactly 128 (no per-dim masks) / up to 128.

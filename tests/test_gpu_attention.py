@@ -199,6 +199,22 @@ def test_slots_outside_the_sequences_hold_nan(k, dk, dv, P):
     np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("qh,hnd", [(128, False), (64, True), (48, False)])
+def test_mla_many_heads(k, qh, hnd):
+    """DeepSeek-V3's MLA decode as the reference calls it (cuda_mla.rs:273-294):
+    every query head over one latent KV head, K 576 and V 512 wide (the
+    reference's pair layout), sequences long enough to split, partial head
+    blocks (48 heads) and head-major pages."""
+    rng = np.random.default_rng(qh + 5)
+    c = _Case(rng, P=64, L=2, H=1, dk=576, dv=512, qh=qh, pages=200, layer=1, hnd=hnd)
+    lens, rso, slots = _random_batch(rng, 6, 2000, c.layout.slot_count)
+    q = _bf16_normal(rng, 6 * qh * 576).reshape(6, qh, 576)
+    _say(f"mla decode qh={qh} hnd={hnd} tokens={int(rso[-1])}")
+    got, want = c.run(k, q, np.arange(6), lens, rso, slots, 1.0 / math.sqrt(576), max_len=2000,
+                      use_async=hnd)
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+
+
 def _random_shape(rng):
     """One random attention problem: head dims, GQA group, page size (powers
     of two take the pipelined body, others the generic one), head layout,

@@ -28,7 +28,9 @@ copy kernels' fractions of the nominal 8 TB/s should be read.
 --config attn|attn_hnd measures the reader of the unpacked pages instead:
 paged-attention decode over the C2 decode pool (NHD or head-major pages),
 64 queries x 32 heads over 64 x 2,048 tokens, one launch per layer; its
-line carries its own metric (GB/s of K/V read).
+line carries its own metric (GB/s of K/V read). --config attn_mla does the
+same over the C4 pool in DeepSeek-V3's MLA form (K 576 / V 512 pair rows,
+128 query heads on one KV head).
 
 Prints one JSON line (the driver's contract), with a `roofline` object for
 the dominant kernel and a `cpu_baseline` object: the CPU oracle
@@ -54,6 +56,7 @@ import numpy as np  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 METRIC = "KV pack+unpack GB/s and % of HBM peak, Llama-3-8B shape; per-layer p50 µs"
 ATTN_METRIC = "paged-attention decode GB/s of K/V read and % of HBM peak, Llama-3-8B shape"
+MLA_METRIC = "paged-attention decode GB/s of K/V read and % of HBM peak, DeepSeek-V3 MLA shape"
 
 DESCRIPTIONS = {
     "c1": "C1: Qwen2-0.5B-like GQA KV transfer, 24 layers x 2 KV heads x 64, bf16, 8 requests "
@@ -76,6 +79,10 @@ DESCRIPTIONS = {
             "Llama-3-8B shape, 32 layers x 8 KV heads x 128, bf16, page_size-64 NHD pool with a "
             "random page table, 64 requests x 2048 tokens, one decode query each with 32 query heads",
     "attn_hnd": "paged-attention decode as attn, over head-major (HND) pages",
+    "attn_mla": "paged-attention decode over the C4 decode pool as DeepSeek-V3's MLA decode reads "
+                "it: 61 layers of the reference's tensor-pair layout (576-wide latent+rope key, "
+                "512-wide latent value, bf16, one KV head), page_size 64 with a random page "
+                "table, 32 requests x 8192 tokens, one decode query each with 128 query heads",
     "ceilings": "the device's streaming ceilings: contiguous copy, read and write of 1 GiB in "
                 "16-byte non-temporal vectors (sgl_rocm_kv_stream), hipMemcpyDtoD, and the host "
                 "link (1 GiB DMA copies to and from pinned host memory, one direction at a time)",
@@ -471,30 +478,51 @@ def run_pages(args):
     }
 
 
-def attention_cpu_baseline(seconds: float, hnd: bool):
+def _attention_geometry(config: str):
+    """(layers, kv_heads, dk, dv, page_size, query_heads, scale) of an
+    attention bench configuration: the C2 decode pool read by Llama-3-8B's
+    32 query heads, or the C4 pool in the reference's MLA tensor-pair form
+    (key 576 = kv_lora_rank 512 + rope 64, value 512; `models/deepseek.rs:
+    360-369`) read by DeepSeek-V3's 128 heads at its qk head dim (192)."""
+    if config == "attn_mla":
+        return 61, 1, 576, 512, 64, 128, 1.0 / np.sqrt(192)
+    return 32, 8, 128, 128, 64, 32, 1.0 / np.sqrt(128)
+
+
+def _attention_layout(kv, config: str, pages: int):
+    L, H, dk, dv, P, _, _ = _attention_geometry(config)
+    kb, vb = H * dk * 2, H * dv * 2
+    rt = kv.KvCacheRuntimeLayout("bf16", P, L, H, dk, 2, L * (kb + vb), L * (kb + vb) * P)
+    if dk == dv:
+        return kv.PagedKvCacheLayout.new(rt, pages)
+    return kv.PagedKvCacheLayout.new_with_tensor_pair(rt, pages, kb, vb)
+
+
+def attention_cpu_baseline(seconds: float, config: str):
     """The float64 attention oracle (numpy) on a sample of the attention
-    workload: 2 of its decode queries over their 2,048-token sequences, one
-    layer, on a host pool holding just those pages."""
+    workload: 2 of its decode queries over 2,048-token sequences, one layer,
+    on a host pool holding just those pages."""
     import oracle
     import sgl_rocm_kv as kv
-    L, H, D, P, qh, n, nq = 32, 8, 128, 64, 32, 2048, 2
-    rb = H * D * 2
-    rt = kv.KvCacheRuntimeLayout("bf16", P, L, H, D, 2, L * 2 * rb, L * 2 * rb * P)
-    layout = kv.PagedKvCacheLayout.new(rt, nq * n // P)
+    hnd = config == "attn_hnd"
+    L, H, dk, dv, P, qh, scale = _attention_geometry(config)
+    n, nq = 2048, 2
+    D = dk
+    layout = _attention_layout(kv, config, nq * n // P)
     rng = np.random.default_rng(3)
     pool = rng.integers(0, 1 << 16, layout.total_byte_len // 2, dtype=np.uint16)
     pool &= np.uint16(0xBFFF)   # finite bf16 values of magnitude < 2
     slots = rng.permutation(layout.slot_count).astype(np.uint64)[: nq * n]
     q = oracle.f32_to_bf16(rng.standard_normal(nq * qh * D).astype(np.float32)).reshape(nq, qh, D)
-    plan = kv.PagedAttentionPlan.for_layer(layout, 0, nq, nq, nq * n, qh, 1.0 / np.sqrt(D),
+    plan = kv.PagedAttentionPlan.for_layer(layout, 0, nq, nq, nq * n, qh, scale,
                                            kv.HND if hnd else kv.NHD)
     def one():
         oracle.paged_attention(pool.view(np.uint8), q, np.arange(nq), [n] * nq,
                                np.arange(nq + 1) * n, slots, page_size=P,
                                page_stride=plan.page_stride_bytes,
                                key_offset=plan.key_in_page_offset,
-                               value_offset=plan.value_in_page_offset, kv_heads=H, dk=D, dv=D,
-                               scale=1.0 / np.sqrt(D), slot_count=layout.slot_count, hnd=hnd)
+                               value_offset=plan.value_in_page_offset, kv_heads=H, dk=dk, dv=dv,
+                               scale=scale, slot_count=layout.slot_count, hnd=hnd)
     one()
     reps, t0 = 0, time.perf_counter()
     while True:
@@ -503,44 +531,46 @@ def attention_cpu_baseline(seconds: float, hnd: bool):
         el = time.perf_counter() - t0
         if el >= seconds or reps >= 1000:
             break
-    kv_bytes = nq * n * 2 * rb
+    kv_bytes = nq * n * H * (dk + dv) * 2
     return {"value": round(kv_bytes * reps / el / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"{nq} decode queries x {n} tokens x {qh} heads, one layer "
                       f"({kv_bytes >> 20} MiB of K/V), x {reps} in {el:.1f} s, float64 numpy "
                       f"oracle (oracle.paged_attention), single thread"}
 
 
-def run_attention(args, hnd: bool):
-    """Decode attention over every layer of the C2 decode pool: one async
-    launch per layer on one stream. Algorithmic bytes per launch = the K and
-    V rows the queries attend (64 x 2048 tokens x 2 x 2,048 B) + queries +
+def run_attention(args, config: str):
+    """Decode attention over every layer of a decode pool: one async launch
+    per layer on one stream. attn/attn_hnd read the C2 pool (Llama-3-8B GQA),
+    attn_mla the C4 pool in MLA tensor-pair form. Algorithmic bytes per
+    launch = the K and V rows the queries attend (C2: 64 x 2048 tokens x
+    2 x 2,048 B; MLA: 32 x 8192 tokens x (1,152 + 1,024) B) + queries +
     outputs; the 8 B/token slot list is excluded, as the copies' slot maps
     are."""
     import sgl_rocm_kv as kv
     from sgl_rocm_kv import hip
     from sgl_rocm_kv import workloads as wl
-    t = wl.c2()
-    sh, spec = t.shape, t.dst
-    L, H, D, P, qh = sh.layers, sh.heads, sh.head_dim, spec.page_size, 32
-    rb = sh.row_bytes
+    hnd, mla = config == "attn_hnd", config == "attn_mla"
+    t = wl.c4() if mla else wl.c2()
+    L, H, dk, dv, P, qh, scale = _attention_geometry(config)
+    D = dk
+    assert t.dst.page_size == P and t.shape.layers == L
     nreq, n = len(t.lengths), int(t.lengths[0])
-    rt = kv.KvCacheRuntimeLayout("bf16", P, L, H, D, 2, sh.token_bytes, spec.page_stride(sh))
-    layout = kv.PagedKvCacheLayout.new(rt, spec.page_count)
+    layout = _attention_layout(kv, config, t.dst.page_count)
     k = kv.RocmKvPairCopyKernels(0)
     pool = hip.DeviceBuffer(layout.total_byte_len)
     k.fill_synthetic(kv.device_buffer(pool.ptr, pool.nbytes), 2025, kv.FILL_BF16_NORMAL)
     rng = np.random.default_rng(9)
     import oracle
-    q = oracle.f32_to_bf16(rng.standard_normal(nreq * qh * D).astype(np.float32))
+    q = oracle.f32_to_bf16(rng.standard_normal(nreq * qh * dk).astype(np.float32))
     bufs = dict(queries=hip.DeviceBuffer.from_array(q),
                 query_request_indices=hip.DeviceBuffer.from_array(np.arange(nreq, dtype=np.uint32)),
                 query_sequence_lengths=hip.DeviceBuffer.from_array(t.lengths.astype(np.uint64)),
                 request_slot_offsets=hip.DeviceBuffer.from_array(
                     np.concatenate([[0], np.cumsum(t.lengths)]).astype(np.uint64)),
                 sequence_slots=hip.DeviceBuffer.from_array(t.dst_slots), pool=pool)
-    outs = [hip.DeviceBuffer(nreq * qh * D * 2) for _ in range(L)]
+    outs = [hip.DeviceBuffer(nreq * qh * dv * 2) for _ in range(L)]
     plans = [kv.PagedAttentionPlan.for_layer(layout, l, nreq, nreq, len(t.dst_slots), qh,
-                                             1.0 / np.sqrt(D), kv.HND if hnd else kv.NHD)
+                                             scale, kv.HND if hnd else kv.NHD)
              for l in range(L)]
     s = hip.Stream()
     hip.synchronize()
@@ -576,28 +606,34 @@ def run_attention(args, hnd: bool):
             hip.memcpy_async(pool.ptr + span, pool.ptr, span, "d2d", s)
         s.synchronize()
         log(f"calibration copies done (3 x {span} B device-to-device)")
-    launch_bytes = nreq * n * 2 * rb + 2 * nreq * qh * D * 2
+    launch_bytes = nreq * n * H * (dk + dv) * 2 + nreq * qh * (dk + dv) * 2
+    launch_flops = 2 * nreq * n * qh * (dk + dv)
     avg = float(np.mean(launch_ms))
     achieved = launch_bytes / (avg / 1e3) / 1e9
     gbs = launch_bytes * L / (wall / args.steps) / 1e9
-    log(f"attention avg {avg * 1e3:.1f} us per layer ({achieved:.0f} GB/s), wall {gbs:.0f} GB/s")
+    log(f"attention avg {avg * 1e3:.1f} us per layer ({achieved:.0f} GB/s, "
+        f"{launch_flops / avg / 1e9:.1f} TFLOP/s), wall {gbs:.0f} GB/s")
     k.close()
+    kernel = ("sglkv_paged_attention_wide576" if mla else "sglkv_paged_attention_pipe128") + \
+        "+sglkv_paged_attention_combine"
+    summary = "paged_attention_decode_" + ("mla" if mla else "hnd" if hnd else "nhd")
+    extra = {"requests": nreq, "tokens_per_request": n, "layers": L, "kv_heads": H,
+             "query_heads": qh, "key_dim": dk, "value_dim": dv, "page_size": P,
+             "head_layout": "HND" if hnd else "NHD",
+             "algorithmic_bytes_per_step": launch_bytes * L}
     return {
         "value": round(gbs, 1),
         "ms_per_step": round(wall * 1e3 / args.steps, 4),
-        "config_extra": {"requests": nreq, "tokens_per_request": n, "layers": L, "kv_heads": H,
-                         "query_heads": qh, "head_dim": D, "page_size": P,
-                         "head_layout": "HND" if hnd else "NHD",
-                         "algorithmic_bytes_per_step": launch_bytes * L},
+        "config_extra": extra,
         "per_layer_p50_us": round(float(np.percentile(launch_ms, 50)) * 1e3, 2),
+        # q.k and p.v at bf16: 2 * (dk + dv) flops per token per query head.
+        "mfma_tflops": round(launch_flops / (avg / 1e3) / 1e12, 1),
         # One launch = the attention kernel and its combine pass: the events
         # bracket both (one C-ABI call), so the pair is the measured unit.
-        "roofline": {"bound": "hbm", "kernel": "sglkv_paged_attention_pipe128+sglkv_paged_attention_combine",
+        "roofline": {"bound": "hbm", "kernel": kernel,
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": _traffic_from_profiles(
-                         "sglkv_paged_attention_pipe128+sglkv_paged_attention_combine",
-                         "paged_attention_decode_hnd" if hnd else "paged_attention_decode_nhd"),
+                     "traffic": _traffic_from_profiles(kernel, summary),
                      "algorithmic_bytes_per_launch": launch_bytes},
     }
 
@@ -701,16 +737,16 @@ def main():
     from sgl_rocm_kv import workloads as wl
     makers = {"c1": wl.c1, "c2": wl.c2, "c3": wl.c3, "c4": wl.c4,
               "c4fp8": lambda: wl.c4(fp8=True), "c5": wl.c5, "c2pages": wl.c2, "attn": wl.c2,
-              "attn_hnd": wl.c2, "ceilings": wl.c2}
-    attention = args.config in ("attn", "attn_hnd")
+              "attn_hnd": wl.c2, "attn_mla": wl.c4, "ceilings": wl.c2}
+    attention = args.config in ("attn", "attn_hnd", "attn_mla")
     t = makers[args.config]()
     log(f"workload {t.name}: {t.rows} tokens moved, payload {t.payload_bytes / 2**30:.2f} GiB")
     if args.config == "c5":
         r = run_staged(t, args)
     elif args.config == "c2pages":
         r = run_pages(args)
-    elif args.config in ("attn", "attn_hnd"):
-        r = run_attention(args, args.config == "attn_hnd")
+    elif attention:
+        r = run_attention(args, args.config)
     elif args.config == "ceilings":
         r = run_ceilings(args)
     else:
@@ -718,7 +754,7 @@ def main():
     gbs = r.pop("value")
     extra = r.pop("config_extra")
     out = {
-        "metric": ATTN_METRIC if attention else METRIC,
+        "metric": (MLA_METRIC if args.config == "attn_mla" else ATTN_METRIC) if attention else METRIC,
         "value": gbs,
         "unit": "GB/s",
         "n_gpus": 1,
@@ -739,7 +775,7 @@ def main():
         out["metric"] = "device streaming ceilings: contiguous copy GB/s (read, write alongside)"
     elif not args.no_cpu_baseline:
         log("cpu baseline (oracle, 1 thread)")
-        out["cpu_baseline"] = (attention_cpu_baseline(args.cpu_seconds, args.config == "attn_hnd")
+        out["cpu_baseline"] = (attention_cpu_baseline(args.cpu_seconds, args.config)
                                if attention else cpu_baseline(makers[args.config], args.cpu_seconds))
         if not attention and args.cpu_threads > 1:
             # The same sample on the box's host share of cores, beside the

@@ -343,20 +343,29 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
     int which = !vec ? 1 : !pipe ? 0 : (p.dk == 128 && p.dv == 128) ? 2 : 3;
     // Many query heads per KV head (more than one 16-head group) or wide
     // values: the wide bodies share each K/V block among 4 head groups
-    // instead of every group and value block reading it again.
+    // instead of every group and value block reading it again. They hold
+    // the queries in registers as 16-byte vectors.
     unsigned threads = 64;
     unsigned lds = (unsigned)((SGLKV_ATTN_HEADS * (p.dk_pad + 8) + SGLKV_ATTN_DV * SGLKV_ATTN_VT_STRIDE) *
                               sizeof(uint16_t));
-    if (fast && (p.head_groups > 1 || p.dv > SGLKV_ATTN_DV)) {
-        const unsigned narrow = SGLKV_ATTN_WIDE_LDS_BYTES(4u, 8u), wide = SGLKV_ATTN_WIDE_LDS_BYTES(18u, 32u);
+    uint64_t max_len = max_sequence_length ? max_sequence_length : c.sequence_slot_count;
+    if (max_len > c.sequence_slot_count) max_len = c.sequence_slot_count;
+    uint64_t value_dims_per_group = 0;  // wide bodies: value dims per workgroup
+    // (Their chunks fit the slot table, so the grid's 65535 splits bound
+    // the length they take.)
+    if (fast && qp % 16 == 0 && (p.head_groups > 1 || p.dv > SGLKV_ATTN_DV) &&
+        max_len <= 65535ull * SGLKV_ATTN_WIDE_SLOTS) {
+        const unsigned narrow = SGLKV_ATTN_WIDE_LDS_BYTES(4u, 8u), wide = SGLKV_ATTN_WIDE_LDS_BYTES(18u, 16u);
         if (p.dk_pad <= 128 && p.dv <= 128 && narrow <= (unsigned)ctx->max_lds_per_block) {
             which = 5;
             lds = narrow;
             threads = 64 * SGLKV_ATTN_WIDE_WAVES;
-        } else if (p.dk_pad <= 576 && p.dv <= 512 && wide <= (unsigned)ctx->max_lds_per_block) {
+            value_dims_per_group = 128;
+        } else if (p.dk_pad <= 576 && wide <= (unsigned)ctx->max_lds_per_block) {
             which = 4;
             lds = wide;
             threads = 64 * SGLKV_ATTN_WIDE_WAVES;
+            value_dims_per_group = 256;
         }
     }
     p.zero_row = ctx->zero_row;
@@ -370,9 +379,10 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
     // launch fills every CU with as many workgroups as stay resident at
     // once (the kernel's occupancy at this LDS size), in one round.
     const bool wide = which >= 4;
-    const uint64_t hblocks = (p.head_groups + SGLKV_ATTN_WIDE_GROUPS - 1) / SGLKV_ATTN_WIDE_GROUPS;
+    const uint64_t hblocks = (p.head_groups + SGLKV_ATTN_WIDE_WAVES - 1) / SGLKV_ATTN_WIDE_WAVES;
+    const uint64_t vblocks = wide ? ceil_div(p.dv, value_dims_per_group) : 1;
     uint64_t base = c.query_count;
-    if (mul_ovf(base, p.kv_heads, &base) || (wide && mul_ovf(base, hblocks, &base)) ||
+    if (mul_ovf(base, p.kv_heads, &base) || (wide && (mul_ovf(base, hblocks, &base) || mul_ovf(base, vblocks, &base))) ||
         (!wide && (mul_ovf(base, p.head_groups, &base) || mul_ovf(base, p.dv_blocks, &base))) ||
         base > INT32_MAX)
         return too_large_dim("workgroups", base, INT32_MAX);
@@ -383,14 +393,16 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
         ctx->attention_occupancy[which] = per_cu > 0 ? (uint32_t)per_cu : 1;
         ctx->attention_occupancy_lds[which] = lds;
     }
-    uint64_t max_len = max_sequence_length ? max_sequence_length : c.sequence_slot_count;
-    if (max_len > c.sequence_slot_count) max_len = c.sequence_slot_count;
     const uint64_t target =
         (uint64_t)ctx->attention_occupancy[which] * (uint64_t)(ctx->cu_count > 0 ? ctx->cu_count : 256);
     const uint64_t want = base >= target ? 1 : target / base;
     uint64_t chunk = ceil_div(max_len, want);
     chunk = ceil_div(chunk < 256 ? 256 : chunk, SGLKV_ATTN_TOKENS) * SGLKV_ATTN_TOKENS;
     uint64_t splits = ceil_div(max_len, chunk);
+    if (wide && chunk > SGLKV_ATTN_WIDE_SLOTS) {  // the wide bodies' slot table
+        chunk = SGLKV_ATTN_WIDE_SLOTS;
+        splits = ceil_div(max_len, chunk);
+    }
     if (splits > 65535) {  // grid y limit
         chunk = ceil_div(ceil_div(max_len, 65535), SGLKV_ATTN_TOKENS) * SGLKV_ATTN_TOKENS;
         splits = ceil_div(max_len, chunk);

@@ -165,9 +165,9 @@ __device__ __forceinline__ void attn_state_init(attn_state_n<NJ> &st) {
 }
 
 // One 32-token block after q.k: sc[b][e] is head r's score of row 4g+e of
-// score block b (token 8g + 4b + e of the block), vb0/vb1 the validity
-// ballots of the rows, and vt the block's values transposed in LDS
-// (vt[dim][token]). Updates the softmax state and o += p.v.
+// score block b, the token that vt holds at position 8g + 4b + e; vb0/vb1
+// the validity ballots of the rows, and vt the block's values transposed
+// in LDS (vt[dim][position]). Updates the softmax state and o += p.v.
 // vt rows are VTS elements apart.
 template <bool FULL_DV = false, int NJ = SGLKV_ATTN_DV / 16, int VTS = SGLKV_ATTN_VT_STRIDE>
 __device__ __forceinline__ void attn_softmax_pv(const sglkv_attn_params &p, uint32_t g, uint32_t d0,
@@ -551,35 +551,66 @@ __device__ __forceinline__ void attn_pipe_body(const sglkv_attn_params &p) {
 // the model over one latent KV head (crates/sglang-srt/src/cuda_mla.rs:
 // 273-294): 128 heads, K rows of 576 and V rows of 512 for DeepSeek-V3.
 // Per-wave bodies would read each K row once per 16-head group and per
-// 128-dim value block (32 times for that shape). Here a workgroup of 8
-// waves owns (query, KV head, up to 4 groups of 16 query heads) and stages
-// each 32-token block once in LDS: K rows as they are (row-major), V rows
-// transposed (vt[dim][token], four tokens per 8-byte store). Wave w serves
-// head group w % 4 and half the value dims (w / 4), so a wave accumulates
-// at most 256 dims; the two waves of a group compute the same scores. The
-// queries sit in LDS. The next block's rows load into registers while the
-// current block computes; the slots of the block after that load one step
-// earlier still, into a two-entry ring in LDS. Rows past the end or with a
-// slot outside the pool read the context's zero row.
+// 128-dim value block (32 times for that shape). Here a workgroup of four
+// waves, one per SIMD, owns (query, KV head, block of 16*NJ value dims, up
+// to 4 groups of 16 query heads) and stages each 32-token block once in
+// LDS, row-major as the pool holds it: the K rows and its value dims of the
+// V rows. Wave w serves head group w: its queries stay in registers (the B
+// operand of q.k), its output (16 heads x 16*NJ dims) in accumulators. The
+// workgroups of the other value block recompute q.k, and read K again from
+// L2 (they run on the same XCD), which keeps a wave's accumulators small
+// enough for two register stages of rows.
+//
+// Two blocks are in flight from HBM at any time: block k+2 loads into one
+// register stage while block k+1, loaded one iteration earlier, is written
+// to the LDS stage that block k-1 used; block k computes from the other
+// stage, so each iteration ends in one barrier. The chunk's slots are read,
+// checked and kept in an LDS table at the start.
+//
+// q.k: score block b covers tokens 16b .. 16b+15, so lane (g, r) holds head
+// r's scores of tokens 16b + 4g + e. p.v takes those as k index 8g + 4b + e;
+// its B operand (V[token][dim]) comes from two transposing LDS reads
+// (ds_read_b64_tr_b16: within 16 lanes, lane j's element i is element j%4
+// of the 8 bytes addressed by lane 4i + j/4), lane r of group g pointing at
+// row 4g + r/4 (then 16 + 4g + r/4), dims 4(r%4) of the 16-dim block.
+//
+// Softmax reference: the first valid block of a split fixes head h's
+// reference maximum m, and every later block adds p = 2^(x - m) without
+// rescaling, so nothing but MFMAs touches the accumulators in the loop. The
+// split record carries (m, l, o) relative to that reference, which is what
+// the combine pass needs of it. That is exact arithmetic as long as p stays
+// representable: a block whose maximum exceeds m by more than
+// SGLKV_ATTN_FIXED_MAX_LOG2 flags the workgroup, which then recomputes its
+// split with the usual per-block rescaling. With the bound at 64 and chunks
+// of at most SGLKV_ATTN_WIDE_SLOTS tokens, l < 2^76 and o stays finite for
+// |v| < 4e15.
 
-template <int DKC, int NJ>  // K dims padded to 32*DKC, V dims to 16*NJ (NJ even, <= 32)
+#define SGLKV_ATTN_FIXED_MAX_LOG2 64.0f
+
+template <int DKC, int NJ>  // K dims padded to 32*DKC, 16*NJ value dims per workgroup
 struct attn_wide_geom {
     static constexpr uint32_t B = SGLKV_ATTN_TOKENS;
     static constexpr uint32_t THREADS = 64 * SGLKV_ATTN_WIDE_WAVES;
-    static constexpr uint32_t NJH = NJ / 2;                // value blocks per wave
-    static constexpr uint32_t KS = 32 * DKC + 8;          // LDS K and query row stride (u16)
-    static constexpr uint32_t VS = B + 8;                 // LDS vt row stride (u16)
-    static constexpr uint32_t KCOLS = 4 * DKC;            // 16-byte pieces per K row
-    static constexpr uint32_t KPIECES = B * KCOLS;
-    static constexpr uint32_t KPT = (KPIECES + THREADS - 1) / THREADS;
-    static constexpr uint32_t VGROUPS = 2 * NJ;           // 8-dim groups of V
-    static constexpr uint32_t KS_ELEMS = B * KS;
-    static constexpr uint32_t VT_ELEMS = 16 * NJ * VS;
-    static constexpr uint32_t QS_ELEMS = SGLKV_ATTN_WIDE_GROUPS * SGLKV_ATTN_HEADS * KS;
-    static constexpr uint32_t LDS_BYTES = 2 * (KS_ELEMS + VT_ELEMS + QS_ELEMS) + 2 * B * 4;
-    static_assert(NJ % 2 == 0 && NJ <= 32, "V staging covers 64 groups of 8 dims");
+    static constexpr uint32_t KS = 32 * DKC + 8;   // LDS K row stride (u16)
+    static constexpr uint32_t VS = 16 * NJ + 16;   // LDS V row stride (u16)
+    static constexpr uint32_t KCOLS = 4 * DKC;     // 16-byte pieces per K row
+    static constexpr uint32_t VCOLS = 2 * NJ;      // 16-byte pieces per V row
+    // Thread t moves column t % COLS of tokens (t / COLS) * PT + i, i < PT:
+    // K columns [0, KM) and every V column that way; the KR columns past KM
+    // (576-wide keys: 8) are one more piece, token t / KR. A thread's tokens
+    // are consecutive, so their slots come in one or two vector reads.
+    static constexpr uint32_t KM = KCOLS < 64 ? KCOLS : 64;
+    static constexpr uint32_t KR = KCOLS - KM;
+    static constexpr uint32_t KPT = B * KM / THREADS;
+    static constexpr uint32_t VPT = B * VCOLS / THREADS;
+    static constexpr uint32_t RPT = KR ? 1 : 0;
+    static constexpr uint32_t STAGE_ELEMS = B * KS + B * VS;
+    static constexpr uint32_t LDS_BYTES = 2 * 2 * STAGE_ELEMS + 4 * SGLKV_ATTN_WIDE_SLOTS + 16;
+    static_assert(NJ <= 32 && DKC <= 18, "accumulators and queries of one wave");
+    static_assert(THREADS % KM == 0 && THREADS % VCOLS == 0 && KPT >= 1 && VPT >= 1, "whole rows per pass");
+    static_assert(KR == 0 || B * KR == THREADS, "one remainder piece per thread");
     static_assert(LDS_BYTES == SGLKV_ATTN_WIDE_LDS_BYTES(DKC, NJ), "the host sizes the same LDS");
-    static_assert(SGLKV_ATTN_WIDE_WAVES == 2 * SGLKV_ATTN_WIDE_GROUPS, "two waves per head group");
+    static_assert(SGLKV_ATTN_WIDE_SLOTS % B == 0, "whole blocks in the slot table");
 };
 
 constexpr uint32_t kAttnInvalidSlot = 0xFFFFFFFFu;  // the host keeps slot_count below 2^32
@@ -595,63 +626,225 @@ __device__ __forceinline__ uint32_t attn_wide_slot(const sglkv_attn_params &p, u
     return static_cast<uint32_t>(raw);
 }
 
-// One thread's share of a block: K pieces tid + k*THREADS (token =
-// piece / KCOLS), and V dims 8*(tid/8) .. +7 of tokens 4*(tid%8) .. +3.
+// One thread's share of a block (the pieces named in attn_wide_geom).
 template <int DKC, int NJ>
 struct attn_wide_stage {
     sglkv_u16x8 k[attn_wide_geom<DKC, NJ>::KPT];
-    sglkv_u16x8 v[4];
+    sglkv_u16x8 v[attn_wide_geom<DKC, NJ>::VPT];
+    sglkv_u16x8 kr[attn_wide_geom<DKC, NJ>::RPT ? 1 : 1];
 };
 
+// 16 bytes at base + (row of slot s32) + off, or at the zero row when !ok:
+// the row offset is masked and the base selected, so the address is pure
+// arithmetic (no branch around the load).
+__device__ __forceinline__ sglkv_u16x8 attn_wide_get(const sglkv_attn_params &p, uint64_t base, uint32_t s32,
+                                                     uint32_t stride, uint32_t off, bool ok) {
+    const uint64_t row = static_cast<uint64_t>(s32 >> p.page_shift) * p.page_stride32 +
+                         static_cast<uint64_t>(s32 & ((1u << p.page_shift) - 1)) * stride + off;
+    const uint64_t at = (ok ? base : reinterpret_cast<uint64_t>(p.zero_row)) + (row & (ok ? ~0ull : 0ull));
+    return *reinterpret_cast<__attribute__((address_space(1))) const sglkv_u16x8 *>(at);
+}
+
+// N consecutive slots from the LDS table (16-byte aligned when N % 4 == 0).
+template <uint32_t N>
+__device__ __forceinline__ void attn_wide_slots(const uint32_t *at, uint32_t (&s)[N]) {
+    if constexpr (N % 4 == 0) {
+#pragma unroll
+        for (uint32_t i = 0; i < N; i += 4) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(at + i);
+            s[i] = v.x, s[i + 1] = v.y, s[i + 2] = v.z, s[i + 3] = v.w;
+        }
+    } else if constexpr (N % 2 == 0) {
+#pragma unroll
+        for (uint32_t i = 0; i < N; i += 2) {
+            const uint2 v = *reinterpret_cast<const uint2 *>(at + i);
+            s[i] = v.x, s[i + 1] = v.y;
+        }
+    } else {
+#pragma unroll
+        for (uint32_t i = 0; i < N; ++i) s[i] = at[i];
+    }
+}
+
+// Issues the loads of the block whose slots start at `slots`; a piece of
+// an invalid token or past dk / dv reads the zero row.
+// vbase points at the workgroup's first value dim, dvl dims remain.
 template <int DKC, int NJ>
 __device__ __forceinline__ void attn_wide_load(const sglkv_attn_params &p, uint64_t kbase, uint64_t vbase,
-                                               const uint32_t *ring, uint32_t tid,
+                                               uint32_t dvl, const uint32_t *slots, uint32_t tid,
                                                attn_wide_stage<DKC, NJ> &st) {
     typedef attn_wide_geom<DKC, NJ> G;
-    const uint64_t zero = reinterpret_cast<uint64_t>(p.zero_row);
-    const uint32_t mask = (1u << p.page_shift) - 1;
+    uint32_t sk[G::KPT], sv[G::VPT];
+    attn_wide_slots(slots + (tid / G::KM) * G::KPT, sk);
+    attn_wide_slots(slots + (tid / G::VCOLS) * G::VPT, sv);
+    const uint32_t rcol = G::KM + tid % (G::KR ? G::KR : 1);
+    const uint32_t sr = G::RPT ? slots[tid / (G::KR ? G::KR : 1)] : kAttnInvalidSlot;
+    {
+        const uint32_t col = tid % G::KM;
+        const bool in = 8 * col < p.dk;
 #pragma unroll
-    for (uint32_t k = 0; k < G::KPT; ++k) {
-        const uint32_t piece = tid + k * G::THREADS;
-        const uint32_t tok = piece / G::KCOLS, col = piece % G::KCOLS;
-        const uint32_t s32 = piece < G::KPIECES ? ring[tok] : kAttnInvalidSlot;
-        const bool ok = s32 != kAttnInvalidSlot && 8 * col < p.dk;
-        const uint64_t row = kbase + static_cast<uint64_t>(s32 >> p.page_shift) * p.page_stride32 +
-                             static_cast<uint64_t>(s32 & mask) * p.key_token_stride32 + 16ull * col;
-        st.k[k] = *reinterpret_cast<__attribute__((address_space(1))) const sglkv_u16x8 *>(ok ? row : zero);
+        for (uint32_t i = 0; i < G::KPT; ++i) {
+            st.k[i] = attn_wide_get(p, kbase, sk[i], p.key_token_stride32, 16 * col, in && sk[i] != kAttnInvalidSlot);
+        }
     }
-    const uint32_t tg = tid & 7, dg = tid >> 3;
+    {
+        const uint32_t col = tid % G::VCOLS;
+        const bool in = 8 * col < dvl;
 #pragma unroll
-    for (uint32_t i = 0; i < 4; ++i) {
-        const uint32_t s32 = dg < G::VGROUPS ? ring[4 * tg + i] : kAttnInvalidSlot;
-        const uint32_t dim = 8 * dg;
-        const bool ok = s32 != kAttnInvalidSlot && dim < p.dv;
-        const uint64_t row = vbase + static_cast<uint64_t>(s32 >> p.page_shift) * p.page_stride32 +
-                             static_cast<uint64_t>(s32 & mask) * p.value_token_stride32 + 2ull * dim;
-        st.v[i] = *reinterpret_cast<__attribute__((address_space(1))) const sglkv_u16x8 *>(ok ? row : zero);
+        for (uint32_t i = 0; i < G::VPT; ++i) {
+            st.v[i] = attn_wide_get(p, vbase, sv[i], p.value_token_stride32, 16 * col, in && sv[i] != kAttnInvalidSlot);
+        }
+    }
+    if (G::RPT) {
+        st.kr[0] = attn_wide_get(p, kbase, sr, p.key_token_stride32, 16 * rcol, 8 * rcol < p.dk && sr != kAttnInvalidSlot);
     }
 }
 
 template <int DKC, int NJ>
-__device__ __forceinline__ void attn_wide_store(uint16_t *ks, uint16_t *vt, uint32_t tid,
-                                                const attn_wide_stage<DKC, NJ> &st) {
+__device__ __forceinline__ void attn_wide_store(uint16_t *stage, uint32_t tid, const attn_wide_stage<DKC, NJ> &st) {
     typedef attn_wide_geom<DKC, NJ> G;
+    {
+        uint16_t *at = stage + (tid / G::KM) * G::KPT * G::KS + 8 * (tid % G::KM);
 #pragma unroll
-    for (uint32_t k = 0; k < G::KPT; ++k) {
-        const uint32_t piece = tid + k * G::THREADS;
-        if (piece < G::KPIECES)
-            *reinterpret_cast<sglkv_u16x8 *>(ks + (piece / G::KCOLS) * G::KS + 8 * (piece % G::KCOLS)) = st.k[k];
+        for (uint32_t i = 0; i < G::KPT; ++i) *reinterpret_cast<sglkv_u16x8 *>(at + i * G::KS) = st.k[i];
     }
-    const uint32_t tg = tid & 7, dg = tid >> 3;
-    if (dg < G::VGROUPS) {
+    {
+        uint16_t *at = stage + G::B * G::KS + (tid / G::VCOLS) * G::VPT * G::VS + 8 * (tid % G::VCOLS);
 #pragma unroll
-        for (uint32_t e = 0; e < 8; ++e) {
-            sglkv_u16x4 t4;
+        for (uint32_t i = 0; i < G::VPT; ++i) *reinterpret_cast<sglkv_u16x8 *>(at + i * G::VS) = st.v[i];
+    }
+    if (G::RPT) {
+        const uint32_t col = G::KM + tid % (G::KR ? G::KR : 1), tok = tid / (G::KR ? G::KR : 1);
+        *reinterpret_cast<sglkv_u16x8 *>(stage + tok * G::KS + 8 * col) = st.kr[0];
+    }
+}
+
+typedef short attn_i16x4 __attribute__((ext_vector_type(4)));
+
+// Four u16 of V for the p.v B operand (see the layout note above).
+__device__ __forceinline__ attn_i16x4 attn_wide_vtr(const uint16_t *at) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) attn_i16x4 *)(reinterpret_cast<uintptr_t>(at)));
+}
+
+// q.k, softmax and p.v of one block staged at `stage`; `cur` its slots.
+// Scheduling masks of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedMfma = 0x008, kSchedDsRead = 0x100;
+constexpr uint32_t kWideAhead = 4;  // k-steps / value blocks of LDS reads issued ahead
+
+// q.k, softmax and p.v of one block staged at `stage`; `cur` its slots.
+// The LDS reads run kWideAhead steps ahead of the MFMAs that use them (the
+// group barriers pin that order; with one wave per SIMD nothing else hides
+// their latency), and q.k keeps four accumulators, so no MFMA waits on the
+// one before it. EXACT: the running maximum and per-block rescaling;
+// otherwise the fixed reference, with *over set when a block exceeds it.
+template <bool EXACT, int DKC, int NJ>
+__device__ __forceinline__ void attn_wide_block(const sglkv_attn_params &p, const uint16_t *stage,
+                                                const uint32_t *cur, const sglkv_u16x8 (&qf)[DKC], uint32_t g,
+                                                uint32_t r, attn_state_n<NJ> &st, bool *over) {
+    typedef attn_wide_geom<DKC, NJ> G;
+    static_assert(DKC >= kWideAhead && NJ >= kWideAhead, "read-ahead depth");
+    const uint16_t *ks = stage, *vs = stage + G::B * G::KS;
+    const uint16_t *k0 = ks + r * G::KS + 8 * g, *k1 = ks + (16 + r) * G::KS + 8 * g;
+    sglkv_u16x8 kf[DKC][2];
 #pragma unroll
-            for (uint32_t i = 0; i < 4; ++i) t4[i] = st.v[i][e];
-            *reinterpret_cast<sglkv_u16x4 *>(vt + (8 * dg + e) * G::VS + 4 * tg) = t4;
+    for (uint32_t c = 0; c < DKC; ++c) {
+        kf[c][0] = *reinterpret_cast<const sglkv_u16x8 *>(k0 + 32 * c);
+        kf[c][1] = *reinterpret_cast<const sglkv_u16x8 *>(k1 + 32 * c);
+    }
+    sglkv_f32x4 acc[2][2];
+#pragma unroll
+    for (uint32_t b = 0; b < 2; ++b) acc[b][0] = acc[b][1] = sglkv_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (uint32_t c = 0; c < DKC; ++c)
+#pragma unroll
+        for (uint32_t b = 0; b < 2; ++b)
+            acc[b][c & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(kf[c][b]), attn_as_bf16(qf[c]),
+                                                                    acc[b][c & 1], 0, 0, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * kWideAhead, 0);
+#pragma unroll
+    for (uint32_t c = 0; c < DKC - kWideAhead; ++c) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2 * kWideAhead, 0);
+    sglkv_f32x4 sc[2];
+#pragma unroll
+    for (uint32_t b = 0; b < 2; ++b) sc[b] = acc[b][0] + acc[b][1];
+
+    // Bit 4g+e of ballot b: token 16b + 4g + e is valid.
+    const uint64_t vb0 = __ballot(cur[r] != kAttnInvalidSlot);
+    const uint64_t vb1 = __ballot(cur[16 + r] != kAttnInvalidSlot);
+    float x[8];
+    float mx = -INFINITY;
+#pragma unroll
+    for (uint32_t b = 0; b < 2; ++b)
+#pragma unroll
+        for (uint32_t e = 0; e < 4; ++e) {
+            const bool ok = (((b ? vb1 : vb0) >> (4 * g + e)) & 1) != 0;
+            const float v = ok ? sc[b][e] * p.scale_log2 : -INFINITY;
+            x[4 * b + e] = v;
+            mx = fmaxf(mx, v);
         }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    sglkv_u16x8 pbits;
+    float psum = 0.0f;
+    if (EXACT) {
+        const float m_new = fmaxf(st.m_run, mx);
+        const float alpha = exp2f(st.m_run - m_new);
+#pragma unroll
+        for (uint32_t i = 0; i < 8; ++i) {
+            const float pi = exp2f(x[i] - m_new);
+            psum += pi;
+            pbits[i] = attn_to_bf16(pi);
+        }
+        st.l_part = st.l_part * alpha + psum;
+        st.m_run = m_new;
+        float arow[4];
+#pragma unroll
+        for (uint32_t e = 0; e < 4; ++e) arow[e] = __shfl(alpha, 4 * g + e);
+#pragma unroll
+        for (uint32_t j = 0; j < NJ; ++j)
+#pragma unroll
+            for (uint32_t e = 0; e < 4; ++e) st.o[j][e] *= arow[e];
+    } else {
+        // m_run is -inf until a valid token arrives (l and o are zero until
+        // then, so fixing the reference needs no rescale).
+        if (st.m_run == -INFINITY) st.m_run = mx;
+        const float m_ref = st.m_run == -INFINITY ? 0.0f : st.m_run;
+        *over = *over || mx > m_ref + SGLKV_ATTN_FIXED_MAX_LOG2;
+#pragma unroll
+        for (uint32_t i = 0; i < 8; ++i) {
+            const float pi = exp2f(fminf(x[i] - m_ref, SGLKV_ATTN_FIXED_MAX_LOG2));
+            psum += pi;
+            pbits[i] = attn_to_bf16(pi);
+        }
+        st.l_part += psum;
     }
+    // o[head 4g+e][dim 16j + r] += sum over the block of p * v. Every value
+    // block is computed: staged dims past dv are zero, and the finish
+    // writes none of them.
+    const uint16_t *v0 = vs + (4 * g + (r >> 2)) * G::VS + 4 * (r & 3);
+    attn_i16x4 vlo[NJ], vhi[NJ];
+#pragma unroll
+    for (uint32_t j = 0; j < NJ; ++j) {
+        vlo[j] = attn_wide_vtr(v0 + 16 * j);
+        vhi[j] = attn_wide_vtr(v0 + 16 * G::VS + 16 * j);
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < NJ; ++j) {
+        const sglkv_u16x8 vv = {(uint16_t)vlo[j][0], (uint16_t)vlo[j][1], (uint16_t)vlo[j][2], (uint16_t)vlo[j][3],
+                                (uint16_t)vhi[j][0], (uint16_t)vhi[j][1], (uint16_t)vhi[j][2], (uint16_t)vhi[j][3]};
+        st.o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(pbits), attn_as_bf16(vv), st.o[j], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * kWideAhead, 1);
+#pragma unroll
+    for (uint32_t j = 0; j < NJ - kWideAhead; ++j) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 1);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 1);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, kWideAhead, 1);
 }
 
 template <int DKC, int NJ>
@@ -659,33 +852,34 @@ __device__ __forceinline__ void attn_wide_body(const sglkv_attn_params &p) {
     typedef attn_wide_geom<DKC, NJ> G;
     constexpr uint32_t B = G::B;
     extern __shared__ __attribute__((aligned(16))) uint16_t attn_lds[];
-    uint16_t *ks = attn_lds;
-    uint16_t *vt = attn_lds + G::KS_ELEMS;
-    uint16_t *qs = attn_lds + G::KS_ELEMS + G::VT_ELEMS;               // [group][head][KS]
-    uint32_t *ring = reinterpret_cast<uint32_t *>(qs + G::QS_ELEMS);  // [2][B]
+    uint16_t *stage0 = attn_lds, *stage1 = attn_lds + G::STAGE_ELEMS;
+    uint32_t *slots = reinterpret_cast<uint32_t *>(attn_lds + 2 * G::STAGE_ELEMS);
+    uint32_t *redo = slots + SGLKV_ATTN_WIDE_SLOTS;  // set: recompute the split exactly
     const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const uint32_t g = lane >> 4, r = lane & 15;
-    const uint32_t grp = wv % SGLKV_ATTN_WIDE_GROUPS, half = wv / SGLKV_ATTN_WIDE_GROUPS;
 
-    // Workgroup -> (query, KV head, block of up to 4 head groups); the head
-    // block varies slowest, so the workgroups of one query that read the
-    // same rows run on one XCD when query_count * kv_heads is a multiple
-    // of 8.
-    const uint32_t hblocks = (p.head_groups + SGLKV_ATTN_WIDE_GROUPS - 1) / SGLKV_ATTN_WIDE_GROUPS;
+    // Workgroup -> (query, KV head, value block, block of up to 4 head
+    // groups); value and head blocks vary slowest, so the workgroups of one
+    // query that read the same rows run on one XCD when query_count *
+    // kv_heads is a multiple of 8.
+    const uint32_t hblocks = (p.head_groups + SGLKV_ATTN_WIDE_WAVES - 1) / SGLKV_ATTN_WIDE_WAVES;
+    const uint32_t vblocks = (p.dv + 16 * NJ - 1) / (16 * NJ);
     uint64_t bx = blockIdx.x;
     const uint64_t q = bx % p.query_count;
     bx /= p.query_count;
     const uint32_t kvh = static_cast<uint32_t>(bx % p.kv_heads);
-    const uint32_t hb = static_cast<uint32_t>(bx / p.kv_heads);
+    bx /= p.kv_heads;
+    const uint32_t vb = static_cast<uint32_t>(bx % vblocks);
+    const uint32_t hb = static_cast<uint32_t>(bx / vblocks);
     const uint32_t split = blockIdx.y;
     uint64_t start = 0, len = 0;
     if (!attn_metadata(p, q, tid == 0 && split == 0 && hb == 0 && kvh == 0, &start, &len)) return;
     const uint64_t t0 = static_cast<uint64_t>(split) * p.chunk_tokens;
     if (t0 >= len || hb >= hblocks) return;
     const uint64_t t1 = len < t0 + p.chunk_tokens ? len : t0 + p.chunk_tokens;
-    const uint32_t hg = hb * SGLKV_ATTN_WIDE_GROUPS + grp;
+    const uint32_t nb = static_cast<uint32_t>((t1 - t0 + B - 1) / B);  // <= SLOTS / B (host bound)
+    const uint32_t hg = hb * SGLKV_ATTN_WIDE_WAVES + wv;
     const bool active = hg < p.head_groups;
-    const uint32_t d0 = half * 16 * G::NJH;
     attn_work w;
     w.q = q;
     w.start = start;
@@ -696,78 +890,74 @@ __device__ __forceinline__ void attn_wide_body(const sglkv_attn_params &p) {
     w.nh = !active ? 0
                    : (p.group - hg * SGLKV_ATTN_HEADS < SGLKV_ATTN_HEADS ? p.group - hg * SGLKV_ATTN_HEADS
                                                                          : SGLKV_ATTN_HEADS);
-    w.d0 = d0;
+    w.d0 = vb * 16 * NJ;
     w.split = split;
-    w.dblk = half;  // only the first half writes a split record's (m, l)
+    w.dblk = vb;  // only the first value block writes a split record's (m, l)
+    const uint32_t dvl = p.dv - w.d0;
 
-    // The group's queries (the B operand of q.k) go to LDS rows 16*grp ..,
-    // zero past the group or past dk, written by the group's first wave;
-    // the barrier after the prologue publishes them.
-    uint16_t *qw = qs + SGLKV_ATTN_HEADS * grp * G::KS;
-    if (half == 0) {
-        for (uint32_t i = lane; i < SGLKV_ATTN_HEADS * 32 * DKC; i += 64) {
-            const uint32_t h = i / (32 * DKC), d = i % (32 * DKC);
-            uint16_t v = 0;
-            if (h < w.nh && d < p.dk) v = p.queries[(q * p.query_heads + w.h0 + h) * p.dk + d];
-            qw[h * G::KS + d] = v;
-        }
+    // Queries: lane (g, r) holds head r, dims 32c + 8g .. +7 (zero past the
+    // group or past dk); the host requires 16-byte aligned queries.
+    sglkv_u16x8 qf[DKC];
+#pragma unroll
+    for (uint32_t c = 0; c < DKC; ++c) {
+        qf[c] = sglkv_u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        if (r < w.nh && 32 * c + 8 * g < p.dk)
+            qf[c] = *reinterpret_cast<const sglkv_u16x8 *>(p.queries + (q * p.query_heads + w.h0 + r) * p.dk +
+                                                           32 * c + 8 * g);
     }
+
+    // The chunk's slots, checked once; tokens past t1 are invalid.
+    if (tid == 0) *redo = 0;
+    for (uint32_t i = tid; i < nb * B; i += G::THREADS) {
+        const uint64_t tok = t0 + i;
+        slots[i] = attn_wide_slot(p, tok < t1 ? p.sequence_slots[start + tok] : 0, tok, t1);
+    }
+    __syncthreads();
 
     const uint64_t pool = reinterpret_cast<uint64_t>(p.pool);
     const uint64_t kbase = pool + p.key_offset + kvh * p.key_head_stride;
-    const uint64_t vbase = pool + p.value_offset + kvh * p.value_head_stride;
-
-    // Prologue: the slots of blocks 0 and 1, the rows of block 0.
-    uint64_t sraw = 0;
-    if (tid < B) {
-        const uint64_t tok = t0 + tid;
-        ring[tid] = attn_wide_slot(p, p.sequence_slots[start + (tok < t1 ? tok : t1 - 1)], tok, t1);
-        const uint64_t tok1 = t0 + B + tid;
-        sraw = p.sequence_slots[start + (tok1 < t1 ? tok1 : t1 - 1)];
-    }
-    __syncthreads();
-    attn_wide_stage<DKC, NJ> stage;
-    attn_wide_load<DKC, NJ>(p, kbase, vbase, ring, tid, stage);
-    attn_wide_store<DKC, NJ>(ks, vt, tid, stage);
-    if (tid < B) ring[B + tid] = attn_wide_slot(p, sraw, t0 + B + tid, t1);
+    const uint64_t vbase = pool + p.value_offset + kvh * p.value_head_stride + 2ull * w.d0;
+    attn_wide_stage<DKC, NJ> ra, rb;
+    attn_wide_load<DKC, NJ>(p, kbase, vbase, dvl, slots, tid, ra);
+    if (nb > 1) attn_wide_load<DKC, NJ>(p, kbase, vbase, dvl, slots + B, tid, rb);
+    attn_wide_store<DKC, NJ>(stage0, tid, ra);
     __syncthreads();
 
-    attn_state_n<G::NJH> st;
+    attn_state_n<NJ> st;
     attn_state_init(st);
-    uint32_t parity = 0;  // ring entry of the block in LDS
-    for (uint64_t tb = t0; tb < t1; tb += B, parity ^= 1) {
-        const bool more = tb + B < t1;
-        const bool further = tb + 2 * B < t1;
-        if (more) attn_wide_load<DKC, NJ>(p, kbase, vbase, ring + (parity ^ 1) * B, tid, stage);
-        if (tid < B && further) {
-            const uint64_t tok = tb + 2 * B + tid;
-            sraw = p.sequence_slots[start + (tok < t1 ? tok : t1 - 1)];
-        }
-        if (active) {
-            // q.k: row r of score block b is token 8*(r/4) + 4b + r%4.
-            sglkv_f32x4 sc[2] = {sglkv_f32x4{0.f, 0.f, 0.f, 0.f}, sglkv_f32x4{0.f, 0.f, 0.f, 0.f}};
-            const uint32_t row0 = 8 * (r >> 2) + (r & 3);
-            for (uint32_t c = 0; c < DKC; ++c) {
-                const sglkv_u16x8 qv = *reinterpret_cast<const sglkv_u16x8 *>(qw + r * G::KS + 32 * c + 8 * g);
-#pragma unroll
-                for (uint32_t b = 0; b < 2; ++b) {
-                    const sglkv_u16x8 kv =
-                        *reinterpret_cast<const sglkv_u16x8 *>(ks + (row0 + 4 * b) * G::KS + 32 * c + 8 * g);
-                    sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(kv), attn_as_bf16(qv), sc[b], 0,
-                                                                    0, 0);
-                }
-            }
-            const uint32_t *cur = ring + parity * B;
-            const uint64_t vb0 = __ballot(cur[row0] != kAttnInvalidSlot);
-            const uint64_t vb1 = __ballot(cur[row0 + 4] != kAttnInvalidSlot);
-            attn_softmax_pv<false, G::NJH, G::VS>(p, g, d0, sc, vb0, vb1, vt + d0 * G::VS, r, st);
-        }
-        __syncthreads();  // every wave is done with this block's K, V and slots
-        if (more) attn_wide_store<DKC, NJ>(ks, vt, tid, stage);
-        if (tid < B && further) ring[parity * B + tid] = attn_wide_slot(p, sraw, tb + 2 * B + tid, t1);
+    st.m_run = -INFINITY;  // reference not fixed yet
+    bool over = false;
+    // Block k computes from stage k%2; its iteration loads block k+2 into
+    // the register stage block k left and stores block k+1 (the other
+    // register stage) into the LDS stage block k-1 left.
+    for (uint32_t k = 0; k < nb; k += 2) {
+        if (k + 2 < nb) attn_wide_load<DKC, NJ>(p, kbase, vbase, dvl, slots + (k + 2) * B, tid, ra);
+        if (active) attn_wide_block<false, DKC, NJ>(p, stage0, slots + k * B, qf, g, r, st, &over);
+        if (k + 1 < nb) attn_wide_store<DKC, NJ>(stage1, tid, rb);
+        __syncthreads();
+        if (k + 1 >= nb) break;
+        if (k + 3 < nb) attn_wide_load<DKC, NJ>(p, kbase, vbase, dvl, slots + (k + 3) * B, tid, rb);
+        if (active) attn_wide_block<false, DKC, NJ>(p, stage1, slots + (k + 1) * B, qf, g, r, st, &over);
+        if (k + 2 < nb) attn_wide_store<DKC, NJ>(stage0, tid, ra);
         __syncthreads();
     }
-    if (active) attn_finish<G::NJH>(p, w, g, r, st);
+    if (active && __any(over) && lane == 0) *redo = 1;
+    __syncthreads();
+    if (*redo) {
+        // A block outran the fixed reference by more than the bound: the
+        // split again, one block at a time, with the running maximum.
+        attn_state_init(st);
+        for (uint32_t k = 0; k < nb; ++k) {
+            attn_wide_load<DKC, NJ>(p, kbase, vbase, dvl, slots + k * B, tid, ra);
+            attn_wide_store<DKC, NJ>(stage0, tid, ra);
+            __syncthreads();
+            if (active) attn_wide_block<true, DKC, NJ>(p, stage0, slots + k * B, qf, g, r, st, &over);
+            __syncthreads();
+        }
+    } else if (st.m_run == -INFINITY) {
+        st.m_run = -3.402823466e+38f;  // no valid token: the record's m as the exact path leaves it
+    }
+    if (active) attn_finish<NJ>(p, w, g, r, st);
 }
 
 }  // namespace
@@ -780,12 +970,12 @@ extern "C" __global__ __launch_bounds__(64) void sglkv_paged_attention_v2(sglkv_
     attn_body<false>(p);
 }
 
-// Many heads per KV head: MLA widths (K <= 576, V <= 512) / dims <= 128.
-extern "C" __global__ __launch_bounds__(512) void sglkv_paged_attention_wide576(sglkv_attn_params p) {
-    attn_wide_body<18, 32>(p);
+// Many heads per KV head: MLA widths (K <= 576, V in blocks of 256) / dims <= 128.
+extern "C" __global__ __launch_bounds__(256) void sglkv_paged_attention_wide576(sglkv_attn_params p) {
+    attn_wide_body<18, 16>(p);
 }
 
-extern "C" __global__ __launch_bounds__(512) void sglkv_paged_attention_wide128(sglkv_attn_params p) {
+extern "C" __global__ __launch_bounds__(256) void sglkv_paged_attention_wide128(sglkv_attn_params p) {
     attn_wide_body<4, 8>(p);
 }
 

@@ -215,6 +215,23 @@ def test_mla_many_heads(k, qh, hnd):
     np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("dk,dv,qh,hnd", [(576, 512, 32, False), (128, 128, 48, True)])
+def test_wide_reference_outrun(k, dk, dv, qh, hnd):
+    """Queries 100 times larger spread the scores over hundreds of log2
+    units, so later blocks of a split exceed its first block's maximum by
+    far more than the wide bodies' fixed reference allows: the workgroup
+    must notice and recompute the split with per-block rescaling (a clamped
+    fast path would give visibly wrong weights)."""
+    rng = np.random.default_rng(dk + qh)
+    c = _Case(rng, P=64, L=2, H=1, dk=dk, dv=dv, qh=qh, pages=120, layer=0, hnd=hnd)
+    lens, rso, slots = _random_batch(rng, 5, 1500, c.layout.slot_count, min_len=600)
+    q = oracle.f32_to_bf16(100.0 * rng.standard_normal(5 * qh * dk).astype(np.float32)).reshape(5, qh, dk)
+    _say(f"wide reference outrun dk={dk} dv={dv} qh={qh} hnd={hnd}")
+    got, want = c.run(k, q, np.arange(5), lens, rso, slots, 1.0 / math.sqrt(dk), max_len=1500)
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+
+
 def _random_shape(rng):
     """One random attention problem: head dims, GQA group, page size (powers
     of two take the pipelined body, others the generic one), head layout,

@@ -350,22 +350,19 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
                               sizeof(uint16_t));
     uint64_t max_len = max_sequence_length ? max_sequence_length : c.sequence_slot_count;
     if (max_len > c.sequence_slot_count) max_len = c.sequence_slot_count;
-    uint64_t value_dims_per_group = 0;  // wide bodies: value dims per workgroup
     // (Their chunks fit the slot table, so the grid's 65535 splits bound
     // the length they take.)
     if (fast && qp % 16 == 0 && (p.head_groups > 1 || p.dv > SGLKV_ATTN_DV) &&
         max_len <= 65535ull * SGLKV_ATTN_WIDE_SLOTS) {
-        const unsigned narrow = SGLKV_ATTN_WIDE_LDS_BYTES(4u, 8u), wide = SGLKV_ATTN_WIDE_LDS_BYTES(18u, 16u);
+        const unsigned narrow = SGLKV_ATTN_WIDE_LDS_BYTES(4u, 8u), wide = SGLKV_ATTN_WIDE_LDS_BYTES(18u, 32u);
         if (p.dk_pad <= 128 && p.dv <= 128 && narrow <= (unsigned)ctx->max_lds_per_block) {
             which = 5;
             lds = narrow;
             threads = 64 * SGLKV_ATTN_WIDE_WAVES;
-            value_dims_per_group = 128;
-        } else if (p.dk_pad <= 576 && wide <= (unsigned)ctx->max_lds_per_block) {
+        } else if (p.dk_pad <= 576 && p.dv <= 512 && wide <= (unsigned)ctx->max_lds_per_block) {
             which = 4;
             lds = wide;
             threads = 64 * SGLKV_ATTN_WIDE_WAVES;
-            value_dims_per_group = 256;
         }
     }
     p.zero_row = ctx->zero_row;
@@ -379,10 +376,9 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
     // launch fills every CU with as many workgroups as stay resident at
     // once (the kernel's occupancy at this LDS size), in one round.
     const bool wide = which >= 4;
-    const uint64_t hblocks = (p.head_groups + SGLKV_ATTN_WIDE_WAVES - 1) / SGLKV_ATTN_WIDE_WAVES;
-    const uint64_t vblocks = wide ? ceil_div(p.dv, value_dims_per_group) : 1;
+    const uint64_t hblocks = (p.head_groups + SGLKV_ATTN_WIDE_GROUPS - 1) / SGLKV_ATTN_WIDE_GROUPS;
     uint64_t base = c.query_count;
-    if (mul_ovf(base, p.kv_heads, &base) || (wide && (mul_ovf(base, hblocks, &base) || mul_ovf(base, vblocks, &base))) ||
+    if (mul_ovf(base, p.kv_heads, &base) || (wide && mul_ovf(base, hblocks, &base)) ||
         (!wide && (mul_ovf(base, p.head_groups, &base) || mul_ovf(base, p.dv_blocks, &base))) ||
         base > INT32_MAX)
         return too_large_dim("workgroups", base, INT32_MAX);

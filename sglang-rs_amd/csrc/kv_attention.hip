@@ -551,20 +551,23 @@ __device__ __forceinline__ void attn_pipe_body(const sglkv_attn_params &p) {
 // the model over one latent KV head (crates/sglang-srt/src/cuda_mla.rs:
 // 273-294): 128 heads, K rows of 576 and V rows of 512 for DeepSeek-V3.
 // Per-wave bodies would read each K row once per 16-head group and per
-// 128-dim value block (32 times for that shape). Here a workgroup of four
-// waves, one per SIMD, owns (query, KV head, block of 16*NJ value dims, up
-// to 4 groups of 16 query heads) and stages each 32-token block once in
-// LDS, row-major as the pool holds it: the K rows and its value dims of the
-// V rows. Wave w serves head group w: its queries stay in registers (the B
-// operand of q.k), its output (16 heads x 16*NJ dims) in accumulators. The
-// workgroups of the other value block recompute q.k, and read K again from
-// L2 (they run on the same XCD), which keeps a wave's accumulators small
-// enough for two register stages of rows.
+// 128-dim value block (32 times for that shape). Here a workgroup of eight
+// waves owns (query, KV head, up to 4 groups of 16 query heads) and stages
+// each 32-token block once in LDS, row-major as the pool holds it. The two
+// waves of a head group share one SIMD and split the work in halves: wave
+// (group, half) computes q.k over key dims [half, half + 1) * dk/2 with that
+// half of the queries in registers, the two partial score tiles meet
+// through LDS (each wave adds the other's to its own, so both hold the
+// same scores), and each accumulates p.v for its half of the value dims.
+// Nothing is computed twice, and a wave holds 16 heads x dv/2 outputs.
 //
-// Two blocks are in flight from HBM at any time: block k+2 loads into one
-// register stage while block k+1, loaded one iteration earlier, is written
-// to the LDS stage that block k-1 used; block k computes from the other
-// stage, so each iteration ends in one barrier. The chunk's slots are read,
+// Rows stay in flight from HBM across the loop: while block k computes,
+// block k+2's K rows load into one register stage and block k+1's K rows
+// (loaded one iteration earlier) wait in the other, next to block k+1's V
+// rows (loaded at the start of this iteration). Block k+1's K rows are
+// written to LDS once every wave is past q.k of block k (the first
+// barrier), its V rows once every wave is past p.v (the second), so one LDS
+// stage serves. The chunk's slots are read,
 // checked and kept in an LDS table at the start.
 //
 // q.k: score block b covers tokens 16b .. 16b+15, so lane (g, r) holds head
@@ -587,28 +590,37 @@ __device__ __forceinline__ void attn_pipe_body(const sglkv_attn_params &p) {
 
 #define SGLKV_ATTN_FIXED_MAX_LOG2 64.0f
 
-template <int DKC, int NJ>  // K dims padded to 32*DKC, 16*NJ value dims per workgroup
+template <int DKC, int NJ>  // K dims padded to 32*DKC, V dims to 16*NJ (both even)
 struct attn_wide_geom {
     static constexpr uint32_t B = SGLKV_ATTN_TOKENS;
-    static constexpr uint32_t THREADS = 64 * SGLKV_ATTN_WIDE_WAVES;
+    static constexpr uint32_t WAVES = SGLKV_ATTN_WIDE_WAVES;
+    static constexpr uint32_t GROUPS = SGLKV_ATTN_WIDE_GROUPS;
+    static constexpr uint32_t THREADS = 64 * WAVES;
+    static constexpr uint32_t KH = DKC / 2;        // q.k k-steps of one wave
+    static constexpr uint32_t NJH = NJ / 2;        // value blocks of one wave
     static constexpr uint32_t KS = 32 * DKC + 8;   // LDS K row stride (u16)
     static constexpr uint32_t VS = 16 * NJ + 16;   // LDS V row stride (u16)
     static constexpr uint32_t KCOLS = 4 * DKC;     // 16-byte pieces per K row
     static constexpr uint32_t VCOLS = 2 * NJ;      // 16-byte pieces per V row
     // Thread t moves column t % COLS of tokens (t / COLS) * PT + i, i < PT:
     // K columns [0, KM) and every V column that way; the KR columns past KM
-    // (576-wide keys: 8) are one more piece, token t / KR. A thread's tokens
-    // are consecutive, so their slots come in one or two vector reads.
+    // (576-wide keys: 8) are one piece of threads t < B * KR, token t / KR.
+    // A thread's tokens are consecutive, so their slots come in one read.
     static constexpr uint32_t KM = KCOLS < 64 ? KCOLS : 64;
     static constexpr uint32_t KR = KCOLS - KM;
     static constexpr uint32_t KPT = B * KM / THREADS;
     static constexpr uint32_t VPT = B * VCOLS / THREADS;
-    static constexpr uint32_t RPT = KR ? 1 : 0;
-    static constexpr uint32_t STAGE_ELEMS = B * KS + B * VS;
-    static constexpr uint32_t LDS_BYTES = 2 * 2 * STAGE_ELEMS + 4 * SGLKV_ATTN_WIDE_SLOTS + 16;
-    static_assert(NJ <= 32 && DKC <= 18, "accumulators and queries of one wave");
+    static constexpr uint32_t RTHREADS = B * KR;
+    static constexpr uint32_t KS_ELEMS = B * KS;
+    static constexpr uint32_t VS_ELEMS = B * VS;
+    static constexpr uint32_t SX_BYTES = WAVES * 2 * 64 * 16;  // partial score tiles
+    static constexpr uint32_t LDS_BYTES = 2 * (KS_ELEMS + VS_ELEMS) + SX_BYTES + 4 * SGLKV_ATTN_WIDE_SLOTS + 16;
+    static constexpr uint32_t QK_AHEAD = KH < 2 ? KH : 2;    // LDS reads issued ahead of their MFMAs
+    static constexpr uint32_t PV_AHEAD = NJH < 2 ? NJH : 2;
+    static_assert(DKC % 2 == 0 && NJ % 2 == 0 && DKC <= 18 && NJ <= 32, "halves of one head group");
+    static_assert(WAVES == 2 * GROUPS, "two waves per head group");
     static_assert(THREADS % KM == 0 && THREADS % VCOLS == 0 && KPT >= 1 && VPT >= 1, "whole rows per pass");
-    static_assert(KR == 0 || B * KR == THREADS, "one remainder piece per thread");
+    static_assert(RTHREADS <= THREADS, "one remainder piece per thread at most");
     static_assert(LDS_BYTES == SGLKV_ATTN_WIDE_LDS_BYTES(DKC, NJ), "the host sizes the same LDS");
     static_assert(SGLKV_ATTN_WIDE_SLOTS % B == 0, "whole blocks in the slot table");
 };
@@ -626,12 +638,13 @@ __device__ __forceinline__ uint32_t attn_wide_slot(const sglkv_attn_params &p, u
     return static_cast<uint32_t>(raw);
 }
 
-// One thread's share of a block (the pieces named in attn_wide_geom).
+// One thread's share of a block (the pieces named in attn_wide_geom); the
+// main loop keeps two of these for K rows and uses one's v for V rows.
 template <int DKC, int NJ>
 struct attn_wide_stage {
     sglkv_u16x8 k[attn_wide_geom<DKC, NJ>::KPT];
     sglkv_u16x8 v[attn_wide_geom<DKC, NJ>::VPT];
-    sglkv_u16x8 kr[attn_wide_geom<DKC, NJ>::RPT ? 1 : 1];
+    sglkv_u16x8 kr;
 };
 
 // 16 bytes at base + (row of slot s32) + off, or at the zero row when !ok:
@@ -666,57 +679,59 @@ __device__ __forceinline__ void attn_wide_slots(const uint32_t *at, uint32_t (&s
     }
 }
 
-// Issues the loads of the block whose slots start at `slots`; a piece of
+// Issues the loads of the K rows (attn_wide_load_k) or V rows
+// (attn_wide_load_v) of the block whose slots start at `slots`; a piece of
 // an invalid token or past dk / dv reads the zero row.
-// vbase points at the workgroup's first value dim, dvl dims remain.
 template <int DKC, int NJ>
-__device__ __forceinline__ void attn_wide_load(const sglkv_attn_params &p, uint64_t kbase, uint64_t vbase,
-                                               uint32_t dvl, const uint32_t *slots, uint32_t tid,
-                                               attn_wide_stage<DKC, NJ> &st) {
+__device__ __forceinline__ void attn_wide_load_k(const sglkv_attn_params &p, uint64_t kbase, const uint32_t *slots,
+                                                 uint32_t tid, attn_wide_stage<DKC, NJ> &st) {
     typedef attn_wide_geom<DKC, NJ> G;
-    uint32_t sk[G::KPT], sv[G::VPT];
+    uint32_t sk[G::KPT];
     attn_wide_slots(slots + (tid / G::KM) * G::KPT, sk);
-    attn_wide_slots(slots + (tid / G::VCOLS) * G::VPT, sv);
+    const bool rem = G::RTHREADS != 0 && tid < G::RTHREADS;
     const uint32_t rcol = G::KM + tid % (G::KR ? G::KR : 1);
-    const uint32_t sr = G::RPT ? slots[tid / (G::KR ? G::KR : 1)] : kAttnInvalidSlot;
-    {
-        const uint32_t col = tid % G::KM;
-        const bool in = 8 * col < p.dk;
+    const uint32_t sr = rem ? slots[tid / (G::KR ? G::KR : 1)] : kAttnInvalidSlot;
+    const uint32_t col = tid % G::KM;
+    const bool in = 8 * col < p.dk;
 #pragma unroll
-        for (uint32_t i = 0; i < G::KPT; ++i) {
-            st.k[i] = attn_wide_get(p, kbase, sk[i], p.key_token_stride32, 16 * col, in && sk[i] != kAttnInvalidSlot);
-        }
-    }
-    {
-        const uint32_t col = tid % G::VCOLS;
-        const bool in = 8 * col < dvl;
+    for (uint32_t i = 0; i < G::KPT; ++i)
+        st.k[i] = attn_wide_get(p, kbase, sk[i], p.key_token_stride32, 16 * col, in && sk[i] != kAttnInvalidSlot);
+    if (G::RTHREADS != 0)
+        st.kr = attn_wide_get(p, kbase, sr, p.key_token_stride32, 16 * rcol,
+                              rem && 8 * rcol < p.dk && sr != kAttnInvalidSlot);
+}
+
+template <int DKC, int NJ>
+__device__ __forceinline__ void attn_wide_load_v(const sglkv_attn_params &p, uint64_t vbase, const uint32_t *slots,
+                                                 uint32_t tid, attn_wide_stage<DKC, NJ> &st) {
+    typedef attn_wide_geom<DKC, NJ> G;
+    uint32_t sv[G::VPT];
+    attn_wide_slots(slots + (tid / G::VCOLS) * G::VPT, sv);
+    const uint32_t col = tid % G::VCOLS;
+    const bool in = 8 * col < p.dv;
 #pragma unroll
-        for (uint32_t i = 0; i < G::VPT; ++i) {
-            st.v[i] = attn_wide_get(p, vbase, sv[i], p.value_token_stride32, 16 * col, in && sv[i] != kAttnInvalidSlot);
-        }
-    }
-    if (G::RPT) {
-        st.kr[0] = attn_wide_get(p, kbase, sr, p.key_token_stride32, 16 * rcol, 8 * rcol < p.dk && sr != kAttnInvalidSlot);
+    for (uint32_t i = 0; i < G::VPT; ++i)
+        st.v[i] = attn_wide_get(p, vbase, sv[i], p.value_token_stride32, 16 * col, in && sv[i] != kAttnInvalidSlot);
+}
+
+template <int DKC, int NJ>
+__device__ __forceinline__ void attn_wide_store_k(uint16_t *ks, uint32_t tid, const attn_wide_stage<DKC, NJ> &st) {
+    typedef attn_wide_geom<DKC, NJ> G;
+    uint16_t *at = ks + (tid / G::KM) * G::KPT * G::KS + 8 * (tid % G::KM);
+#pragma unroll
+    for (uint32_t i = 0; i < G::KPT; ++i) *reinterpret_cast<sglkv_u16x8 *>(at + i * G::KS) = st.k[i];
+    if (G::RTHREADS != 0 && tid < G::RTHREADS) {
+        const uint32_t kr = G::KR ? G::KR : 1;
+        *reinterpret_cast<sglkv_u16x8 *>(ks + (tid / kr) * G::KS + 8 * (G::KM + tid % kr)) = st.kr;
     }
 }
 
 template <int DKC, int NJ>
-__device__ __forceinline__ void attn_wide_store(uint16_t *stage, uint32_t tid, const attn_wide_stage<DKC, NJ> &st) {
+__device__ __forceinline__ void attn_wide_store_v(uint16_t *vs, uint32_t tid, const attn_wide_stage<DKC, NJ> &st) {
     typedef attn_wide_geom<DKC, NJ> G;
-    {
-        uint16_t *at = stage + (tid / G::KM) * G::KPT * G::KS + 8 * (tid % G::KM);
+    uint16_t *at = vs + (tid / G::VCOLS) * G::VPT * G::VS + 8 * (tid % G::VCOLS);
 #pragma unroll
-        for (uint32_t i = 0; i < G::KPT; ++i) *reinterpret_cast<sglkv_u16x8 *>(at + i * G::KS) = st.k[i];
-    }
-    {
-        uint16_t *at = stage + G::B * G::KS + (tid / G::VCOLS) * G::VPT * G::VS + 8 * (tid % G::VCOLS);
-#pragma unroll
-        for (uint32_t i = 0; i < G::VPT; ++i) *reinterpret_cast<sglkv_u16x8 *>(at + i * G::VS) = st.v[i];
-    }
-    if (G::RPT) {
-        const uint32_t col = G::KM + tid % (G::KR ? G::KR : 1), tok = tid / (G::KR ? G::KR : 1);
-        *reinterpret_cast<sglkv_u16x8 *>(stage + tok * G::KS + 8 * col) = st.kr[0];
-    }
+    for (uint32_t i = 0; i < G::VPT; ++i) *reinterpret_cast<sglkv_u16x8 *>(at + i * G::VS) = st.v[i];
 }
 
 typedef short attn_i16x4 __attribute__((ext_vector_type(4)));
@@ -727,51 +742,53 @@ __device__ __forceinline__ attn_i16x4 attn_wide_vtr(const uint16_t *at) {
         (__attribute__((address_space(3))) attn_i16x4 *)(reinterpret_cast<uintptr_t>(at)));
 }
 
-// q.k, softmax and p.v of one block staged at `stage`; `cur` its slots.
 // Scheduling masks of __builtin_amdgcn_sched_group_barrier.
 constexpr int kSchedMfma = 0x008, kSchedDsRead = 0x100;
-constexpr uint32_t kWideAhead = 4;  // k-steps / value blocks of LDS reads issued ahead
 
-// q.k, softmax and p.v of one block staged at `stage`; `cur` its slots.
-// The LDS reads run kWideAhead steps ahead of the MFMAs that use them (the
-// group barriers pin that order; with one wave per SIMD nothing else hides
-// their latency), and q.k keeps four accumulators, so no MFMA waits on the
-// one before it. EXACT: the running maximum and per-block rescaling;
-// otherwise the fixed reference, with *over set when a block exceeds it.
-template <bool EXACT, int DKC, int NJ>
-__device__ __forceinline__ void attn_wide_block(const sglkv_attn_params &p, const uint16_t *stage,
-                                                const uint32_t *cur, const sglkv_u16x8 (&qf)[DKC], uint32_t g,
-                                                uint32_t r, attn_state_n<NJ> &st, bool *over) {
+// This wave's partial q.k of the staged block over its KH k-steps (queries
+// qf), left in sc and written to its score tile (sxw[b * 64 + lane]). The
+// LDS reads run QK_AHEAD k-steps ahead of the MFMAs that use them (the
+// group barriers pin that order).
+template <int DKC, int NJ>
+__device__ __forceinline__ void attn_wide_qk(const uint16_t *ks, const sglkv_u16x8 (&qf)[DKC / 2], uint32_t kc0,
+                                             uint32_t g, uint32_t r, uint32_t lane, sglkv_f32x4 (&sc)[2],
+                                             sglkv_f32x4 *sxw) {
     typedef attn_wide_geom<DKC, NJ> G;
-    static_assert(DKC >= kWideAhead && NJ >= kWideAhead, "read-ahead depth");
-    const uint16_t *ks = stage, *vs = stage + G::B * G::KS;
-    const uint16_t *k0 = ks + r * G::KS + 8 * g, *k1 = ks + (16 + r) * G::KS + 8 * g;
-    sglkv_u16x8 kf[DKC][2];
+    const uint16_t *k0 = ks + r * G::KS + 32 * kc0 + 8 * g, *k1 = k0 + 16 * G::KS;
+    sglkv_u16x8 kf[G::KH][2];
 #pragma unroll
-    for (uint32_t c = 0; c < DKC; ++c) {
+    for (uint32_t c = 0; c < G::KH; ++c) {
         kf[c][0] = *reinterpret_cast<const sglkv_u16x8 *>(k0 + 32 * c);
         kf[c][1] = *reinterpret_cast<const sglkv_u16x8 *>(k1 + 32 * c);
     }
-    sglkv_f32x4 acc[2][2];
+    sc[0] = sc[1] = sglkv_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (uint32_t b = 0; b < 2; ++b) acc[b][0] = acc[b][1] = sglkv_f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (uint32_t c = 0; c < DKC; ++c)
+    for (uint32_t c = 0; c < G::KH; ++c)
 #pragma unroll
         for (uint32_t b = 0; b < 2; ++b)
-            acc[b][c & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(kf[c][b]), attn_as_bf16(qf[c]),
-                                                                    acc[b][c & 1], 0, 0, 0);
-    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * kWideAhead, 0);
+            sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(kf[c][b]), attn_as_bf16(qf[c]), sc[b], 0, 0, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * G::QK_AHEAD, 0);
 #pragma unroll
-    for (uint32_t c = 0; c < DKC - kWideAhead; ++c) {
+    for (uint32_t c = 0; c < G::KH - G::QK_AHEAD; ++c) {
         __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
         __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2 * kWideAhead, 0);
-    sglkv_f32x4 sc[2];
-#pragma unroll
-    for (uint32_t b = 0; b < 2; ++b) sc[b] = acc[b][0] + acc[b][1];
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2 * G::QK_AHEAD, 0);
+    sxw[lane] = sc[0];
+    sxw[64 + lane] = sc[1];
+}
 
+// Adds the other half's partial scores (sxo) to sc, then softmax and p.v
+// over this wave's value blocks (from dim 16 * j0). EXACT: the running
+// maximum and per-block rescaling; otherwise the fixed reference, with
+// *over set when a block exceeds it.
+template <bool EXACT, int DKC, int NJ>
+__device__ __forceinline__ void attn_wide_pv(const sglkv_attn_params &p, const uint16_t *vs, sglkv_f32x4 (&sc)[2],
+                                             const sglkv_f32x4 *sxo, const uint32_t *cur, uint32_t j0, uint32_t g,
+                                             uint32_t r, uint32_t lane, attn_state_n<NJ / 2> &st, bool *over) {
+    typedef attn_wide_geom<DKC, NJ> G;
+    sc[0] += sxo[lane];
+    sc[1] += sxo[64 + lane];
     // Bit 4g+e of ballot b: token 16b + 4g + e is valid.
     const uint64_t vb0 = __ballot(cur[r] != kAttnInvalidSlot);
     const uint64_t vb1 = __ballot(cur[16 + r] != kAttnInvalidSlot);
@@ -805,7 +822,7 @@ __device__ __forceinline__ void attn_wide_block(const sglkv_attn_params &p, cons
 #pragma unroll
         for (uint32_t e = 0; e < 4; ++e) arow[e] = __shfl(alpha, 4 * g + e);
 #pragma unroll
-        for (uint32_t j = 0; j < NJ; ++j)
+        for (uint32_t j = 0; j < G::NJH; ++j)
 #pragma unroll
             for (uint32_t e = 0; e < 4; ++e) st.o[j][e] *= arow[e];
     } else {
@@ -822,29 +839,29 @@ __device__ __forceinline__ void attn_wide_block(const sglkv_attn_params &p, cons
         }
         st.l_part += psum;
     }
-    // o[head 4g+e][dim 16j + r] += sum over the block of p * v. Every value
-    // block is computed: staged dims past dv are zero, and the finish
+    // o[head 4g+e][dim 16(j0 + j) + r] += sum over the block of p * v. Every
+    // value block is computed: staged dims past dv are zero, and the finish
     // writes none of them.
-    const uint16_t *v0 = vs + (4 * g + (r >> 2)) * G::VS + 4 * (r & 3);
-    attn_i16x4 vlo[NJ], vhi[NJ];
+    const uint16_t *v0 = vs + (4 * g + (r >> 2)) * G::VS + 4 * (r & 3) + 16 * j0;
+    attn_i16x4 vlo[G::NJH], vhi[G::NJH];
 #pragma unroll
-    for (uint32_t j = 0; j < NJ; ++j) {
+    for (uint32_t j = 0; j < G::NJH; ++j) {
         vlo[j] = attn_wide_vtr(v0 + 16 * j);
         vhi[j] = attn_wide_vtr(v0 + 16 * G::VS + 16 * j);
     }
 #pragma unroll
-    for (uint32_t j = 0; j < NJ; ++j) {
+    for (uint32_t j = 0; j < G::NJH; ++j) {
         const sglkv_u16x8 vv = {(uint16_t)vlo[j][0], (uint16_t)vlo[j][1], (uint16_t)vlo[j][2], (uint16_t)vlo[j][3],
                                 (uint16_t)vhi[j][0], (uint16_t)vhi[j][1], (uint16_t)vhi[j][2], (uint16_t)vhi[j][3]};
         st.o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(pbits), attn_as_bf16(vv), st.o[j], 0, 0, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * kWideAhead, 1);
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * G::PV_AHEAD, 1);
 #pragma unroll
-    for (uint32_t j = 0; j < NJ - kWideAhead; ++j) {
+    for (uint32_t j = 0; j < G::NJH - G::PV_AHEAD; ++j) {
         __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 1);
         __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 1);
     }
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, kWideAhead, 1);
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, G::PV_AHEAD, 1);
 }
 
 template <int DKC, int NJ>
@@ -852,25 +869,25 @@ __device__ __forceinline__ void attn_wide_body(const sglkv_attn_params &p) {
     typedef attn_wide_geom<DKC, NJ> G;
     constexpr uint32_t B = G::B;
     extern __shared__ __attribute__((aligned(16))) uint16_t attn_lds[];
-    uint16_t *stage0 = attn_lds, *stage1 = attn_lds + G::STAGE_ELEMS;
-    uint32_t *slots = reinterpret_cast<uint32_t *>(attn_lds + 2 * G::STAGE_ELEMS);
+    uint16_t *ks = attn_lds, *vs = attn_lds + G::KS_ELEMS;
+    sglkv_f32x4 *sx = reinterpret_cast<sglkv_f32x4 *>(vs + G::VS_ELEMS);           // [wave][b][lane]
+    uint32_t *slots = reinterpret_cast<uint32_t *>(vs + G::VS_ELEMS + G::SX_BYTES / 2);
     uint32_t *redo = slots + SGLKV_ATTN_WIDE_SLOTS;  // set: recompute the split exactly
     const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const uint32_t g = lane >> 4, r = lane & 15;
+    const uint32_t grp = wv % G::GROUPS, half = wv / G::GROUPS;
+    sglkv_f32x4 *sxw = sx + wv * 128, *sxo = sx + (wv ^ G::GROUPS) * 128;
 
-    // Workgroup -> (query, KV head, value block, block of up to 4 head
-    // groups); value and head blocks vary slowest, so the workgroups of one
-    // query that read the same rows run on one XCD when query_count *
-    // kv_heads is a multiple of 8.
-    const uint32_t hblocks = (p.head_groups + SGLKV_ATTN_WIDE_WAVES - 1) / SGLKV_ATTN_WIDE_WAVES;
-    const uint32_t vblocks = (p.dv + 16 * NJ - 1) / (16 * NJ);
+    // Workgroup -> (query, KV head, block of up to 4 head groups); the head
+    // block varies slowest, so the workgroups of one query that read the
+    // same rows run on one XCD when query_count * kv_heads is a multiple
+    // of 8.
+    const uint32_t hblocks = (p.head_groups + G::GROUPS - 1) / G::GROUPS;
     uint64_t bx = blockIdx.x;
     const uint64_t q = bx % p.query_count;
     bx /= p.query_count;
     const uint32_t kvh = static_cast<uint32_t>(bx % p.kv_heads);
-    bx /= p.kv_heads;
-    const uint32_t vb = static_cast<uint32_t>(bx % vblocks);
-    const uint32_t hb = static_cast<uint32_t>(bx / vblocks);
+    const uint32_t hb = static_cast<uint32_t>(bx / p.kv_heads);
     const uint32_t split = blockIdx.y;
     uint64_t start = 0, len = 0;
     if (!attn_metadata(p, q, tid == 0 && split == 0 && hb == 0 && kvh == 0, &start, &len)) return;
@@ -878,8 +895,8 @@ __device__ __forceinline__ void attn_wide_body(const sglkv_attn_params &p) {
     if (t0 >= len || hb >= hblocks) return;
     const uint64_t t1 = len < t0 + p.chunk_tokens ? len : t0 + p.chunk_tokens;
     const uint32_t nb = static_cast<uint32_t>((t1 - t0 + B - 1) / B);  // <= SLOTS / B (host bound)
-    const uint32_t hg = hb * SGLKV_ATTN_WIDE_WAVES + wv;
-    const bool active = hg < p.head_groups;
+    const uint32_t hg = hb * G::GROUPS + grp;
+    const bool active = hg < p.head_groups;  // the same for both waves of a group
     attn_work w;
     w.q = q;
     w.start = start;
@@ -890,20 +907,21 @@ __device__ __forceinline__ void attn_wide_body(const sglkv_attn_params &p) {
     w.nh = !active ? 0
                    : (p.group - hg * SGLKV_ATTN_HEADS < SGLKV_ATTN_HEADS ? p.group - hg * SGLKV_ATTN_HEADS
                                                                          : SGLKV_ATTN_HEADS);
-    w.d0 = vb * 16 * NJ;
+    w.d0 = half * 16 * G::NJH;
     w.split = split;
-    w.dblk = vb;  // only the first value block writes a split record's (m, l)
-    const uint32_t dvl = p.dv - w.d0;
+    w.dblk = half;  // only the first half writes a split record's (m, l)
+    const uint32_t kc0 = half * G::KH, j0 = half * G::NJH;
 
-    // Queries: lane (g, r) holds head r, dims 32c + 8g .. +7 (zero past the
-    // group or past dk); the host requires 16-byte aligned queries.
-    sglkv_u16x8 qf[DKC];
+    // This half's queries: lane (g, r) holds head r, dims 32(kc0 + c) + 8g
+    // .. +7 (zero past the group or past dk); the host requires 16-byte
+    // aligned queries.
+    sglkv_u16x8 qf[G::KH];
 #pragma unroll
-    for (uint32_t c = 0; c < DKC; ++c) {
+    for (uint32_t c = 0; c < G::KH; ++c) {
+        const uint32_t d = 32 * (kc0 + c) + 8 * g;
         qf[c] = sglkv_u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-        if (r < w.nh && 32 * c + 8 * g < p.dk)
-            qf[c] = *reinterpret_cast<const sglkv_u16x8 *>(p.queries + (q * p.query_heads + w.h0 + r) * p.dk +
-                                                           32 * c + 8 * g);
+        if (r < w.nh && d < p.dk)
+            qf[c] = *reinterpret_cast<const sglkv_u16x8 *>(p.queries + (q * p.query_heads + w.h0 + r) * p.dk + d);
     }
 
     // The chunk's slots, checked once; tokens past t1 are invalid.
@@ -916,30 +934,38 @@ __device__ __forceinline__ void attn_wide_body(const sglkv_attn_params &p) {
 
     const uint64_t pool = reinterpret_cast<uint64_t>(p.pool);
     const uint64_t kbase = pool + p.key_offset + kvh * p.key_head_stride;
-    const uint64_t vbase = pool + p.value_offset + kvh * p.value_head_stride + 2ull * w.d0;
-    attn_wide_stage<DKC, NJ> ra, rb;
-    attn_wide_load<DKC, NJ>(p, kbase, vbase, dvl, slots, tid, ra);
-    if (nb > 1) attn_wide_load<DKC, NJ>(p, kbase, vbase, dvl, slots + B, tid, rb);
-    attn_wide_store<DKC, NJ>(stage0, tid, ra);
+    const uint64_t vbase = pool + p.value_offset + kvh * p.value_head_stride;
+    attn_wide_stage<DKC, NJ> ra, rb;  // K rows: two stages; V rows: ra.v
+    attn_wide_load_k<DKC, NJ>(p, kbase, slots, tid, ra);
+    attn_wide_load_v<DKC, NJ>(p, vbase, slots, tid, ra);
+    if (nb > 1) attn_wide_load_k<DKC, NJ>(p, kbase, slots + B, tid, rb);
+    attn_wide_store_k<DKC, NJ>(ks, tid, ra);
+    attn_wide_store_v<DKC, NJ>(vs, tid, ra);
     __syncthreads();
 
-    attn_state_n<NJ> st;
+    attn_state_n<G::NJH> st;
     attn_state_init(st);
     st.m_run = -INFINITY;  // reference not fixed yet
     bool over = false;
-    // Block k computes from stage k%2; its iteration loads block k+2 into
-    // the register stage block k left and stores block k+1 (the other
-    // register stage) into the LDS stage block k-1 left.
+    // Block k is in LDS and block k+1's K rows in register stage `next`:
+    // load block k+1's V rows and block k+2's K rows (into `fr`, the stage
+    // block k left), q.k, barrier, store k+1's K rows, p.v, barrier, store
+    // its V rows.
+    auto step = [&](uint32_t k, attn_wide_stage<DKC, NJ> &fr, attn_wide_stage<DKC, NJ> &next) {
+        if (k + 1 < nb) attn_wide_load_v<DKC, NJ>(p, vbase, slots + (k + 1) * B, tid, ra);
+        if (k + 2 < nb) attn_wide_load_k<DKC, NJ>(p, kbase, slots + (k + 2) * B, tid, fr);
+        sglkv_f32x4 sc[2];
+        if (active) attn_wide_qk<DKC, NJ>(ks, qf, kc0, g, r, lane, sc, sxw);
+        __syncthreads();
+        if (k + 1 < nb) attn_wide_store_k<DKC, NJ>(ks, tid, next);
+        if (active) attn_wide_pv<false, DKC, NJ>(p, vs, sc, sxo, slots + k * B, j0, g, r, lane, st, &over);
+        __syncthreads();
+        if (k + 1 < nb) attn_wide_store_v<DKC, NJ>(vs, tid, ra);
+    };
     for (uint32_t k = 0; k < nb; k += 2) {
-        if (k + 2 < nb) attn_wide_load<DKC, NJ>(p, kbase, vbase, dvl, slots + (k + 2) * B, tid, ra);
-        if (active) attn_wide_block<false, DKC, NJ>(p, stage0, slots + k * B, qf, g, r, st, &over);
-        if (k + 1 < nb) attn_wide_store<DKC, NJ>(stage1, tid, rb);
-        __syncthreads();
+        step(k, ra, rb);
         if (k + 1 >= nb) break;
-        if (k + 3 < nb) attn_wide_load<DKC, NJ>(p, kbase, vbase, dvl, slots + (k + 3) * B, tid, rb);
-        if (active) attn_wide_block<false, DKC, NJ>(p, stage1, slots + (k + 1) * B, qf, g, r, st, &over);
-        if (k + 2 < nb) attn_wide_store<DKC, NJ>(stage0, tid, ra);
-        __syncthreads();
+        step(k + 1, rb, ra);
     }
     if (active && __any(over) && lane == 0) *redo = 1;
     __syncthreads();
@@ -948,16 +974,21 @@ __device__ __forceinline__ void attn_wide_body(const sglkv_attn_params &p) {
         // split again, one block at a time, with the running maximum.
         attn_state_init(st);
         for (uint32_t k = 0; k < nb; ++k) {
-            attn_wide_load<DKC, NJ>(p, kbase, vbase, dvl, slots + k * B, tid, ra);
-            attn_wide_store<DKC, NJ>(stage0, tid, ra);
+            attn_wide_load_k<DKC, NJ>(p, kbase, slots + k * B, tid, ra);
+            attn_wide_load_v<DKC, NJ>(p, vbase, slots + k * B, tid, ra);
+            attn_wide_store_k<DKC, NJ>(ks, tid, ra);
+            attn_wide_store_v<DKC, NJ>(vs, tid, ra);
             __syncthreads();
-            if (active) attn_wide_block<true, DKC, NJ>(p, stage0, slots + k * B, qf, g, r, st, &over);
+            sglkv_f32x4 sc[2];
+            if (active) attn_wide_qk<DKC, NJ>(ks, qf, kc0, g, r, lane, sc, sxw);
+            __syncthreads();
+            if (active) attn_wide_pv<true, DKC, NJ>(p, vs, sc, sxo, slots + k * B, j0, g, r, lane, st, &over);
             __syncthreads();
         }
     } else if (st.m_run == -INFINITY) {
         st.m_run = -3.402823466e+38f;  // no valid token: the record's m as the exact path leaves it
     }
-    if (active) attn_finish<NJ>(p, w, g, r, st);
+    if (active) attn_finish<G::NJH>(p, w, g, r, st);
 }
 
 }  // namespace
@@ -970,12 +1001,12 @@ extern "C" __global__ __launch_bounds__(64) void sglkv_paged_attention_v2(sglkv_
     attn_body<false>(p);
 }
 
-// Many heads per KV head: MLA widths (K <= 576, V in blocks of 256) / dims <= 128.
-extern "C" __global__ __launch_bounds__(256) void sglkv_paged_attention_wide576(sglkv_attn_params p) {
-    attn_wide_body<18, 16>(p);
+// Many heads per KV head: MLA widths (K <= 576, V <= 512) / dims <= 128.
+extern "C" __global__ __launch_bounds__(512) void sglkv_paged_attention_wide576(sglkv_attn_params p) {
+    attn_wide_body<18, 32>(p);
 }
 
-extern "C" __global__ __launch_bounds__(256) void sglkv_paged_attention_wide128(sglkv_attn_params p) {
+extern "C" __global__ __launch_bounds__(512) void sglkv_paged_attention_wide128(sglkv_attn_params p) {
     attn_wide_body<4, 8>(p);
 }
 

@@ -157,16 +157,18 @@ typedef struct sglkv_request_params {
 #define SGLKV_ATTN_VT_STRIDE 40u /* u16 per transposed-V row in LDS (32 tokens + pad) */
 #define SGLKV_ATTN_MAX_DK 1024u /* query/key head dim limit (LDS-resident queries) */
 /* The wide bodies (many query heads per KV head, e.g. MLA): a workgroup of
- * SGLKV_ATTN_WIDE_WAVES waves (one per SIMD) serves SGLKV_ATTN_WIDE_WAVES
- * groups of SGLKV_ATTN_HEADS heads and one block of 16*NJ value dims; K dims
- * padded to 32*DKC. Its LDS: two stages of a 32-token block (K rows of
- * 32*DKC+8 and V rows of 16*NJ+16 u16), the chunk's slot table (u32, at
- * most SGLKV_ATTN_WIDE_SLOTS tokens, which bounds the chunk) and a flag. */
-#define SGLKV_ATTN_WIDE_WAVES 4u
+ * SGLKV_ATTN_WIDE_WAVES waves serves SGLKV_ATTN_WIDE_GROUPS groups of
+ * SGLKV_ATTN_HEADS heads, two waves per group; K dims padded to 32*DKC, V
+ * dims to 16*NJ. Its LDS: one 32-token block (K rows of 32*DKC+8 and V rows
+ * of 16*NJ+16 u16), a 2 KiB partial score tile per wave, the chunk's slot
+ * table (u32, at most SGLKV_ATTN_WIDE_SLOTS tokens, which bounds the chunk)
+ * and a flag. */
+#define SGLKV_ATTN_WIDE_GROUPS 4u
+#define SGLKV_ATTN_WIDE_WAVES 8u
 #define SGLKV_ATTN_WIDE_SLOTS 4096u
 #define SGLKV_ATTN_WIDE_LDS_BYTES(DKC, NJ)                                                     \
-    (2u * 2u * SGLKV_ATTN_TOKENS * ((32u * (DKC) + 8u) + (16u * (NJ) + 16u)) +                 \
-     4u * SGLKV_ATTN_WIDE_SLOTS + 16u)
+    (2u * SGLKV_ATTN_TOKENS * ((32u * (DKC) + 8u) + (16u * (NJ) + 16u)) +                      \
+     SGLKV_ATTN_WIDE_WAVES * 2u * 64u * 16u + 4u * SGLKV_ATTN_WIDE_SLOTS + 16u)
 
 typedef struct sglkv_attn_params {
     const uint16_t *queries;              /* bf16 [query][query_head][dk] */

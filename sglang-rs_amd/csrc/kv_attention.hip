@@ -561,13 +561,14 @@ __device__ __forceinline__ void attn_pipe_body(const sglkv_attn_params &p) {
 // same scores), and each accumulates p.v for its half of the value dims.
 // Nothing is computed twice, and a wave holds 16 heads x dv/2 outputs.
 //
-// Rows stay in flight from HBM across the loop: while block k computes,
-// block k+2's K rows load into one register stage and block k+1's K rows
-// (loaded one iteration earlier) wait in the other, next to block k+1's V
-// rows (loaded at the start of this iteration). Block k+1's K rows are
-// written to LDS once every wave is past q.k of block k (the first
-// barrier), its V rows once every wave is past p.v (the second), so one LDS
-// stage serves. The chunk's slots are read,
+// Rows stay in flight from HBM across the loop, in registers. Iteration k
+// (block k's K rows in LDS): issue block k+2's K rows into one register
+// stage between the q.k MFMAs of block k, write block k's V rows (loaded
+// during the previous iteration) to LDS and issue block k+1's V rows,
+// barrier; write block k+1's K rows (the other stage, loaded an iteration
+// earlier) between the p.v MFMAs of block k, barrier. One LDS stage serves:
+// K rows are only read by q.k and V rows only by p.v, and the two barriers
+// keep each area's writers and readers apart. The chunk's slots are read,
 // checked and kept in an LDS table at the start.
 //
 // q.k: score block b covers tokens 16b .. 16b+15, so lane (g, r) holds head
@@ -743,13 +744,13 @@ __device__ __forceinline__ attn_i16x4 attn_wide_vtr(const uint16_t *at) {
 }
 
 // Scheduling masks of __builtin_amdgcn_sched_group_barrier.
-constexpr int kSchedMfma = 0x008, kSchedDsRead = 0x100;
+constexpr int kSchedMfma = 0x008, kSchedVmemRead = 0x020, kSchedDsRead = 0x100;
 
 // This wave's partial q.k of the staged block over its KH k-steps (queries
-// qf), left in sc and written to its score tile (sxw[b * 64 + lane]). The
-// LDS reads run QK_AHEAD k-steps ahead of the MFMAs that use them (the
-// group barriers pin that order).
-template <int DKC, int NJ>
+// qf), left in sc and written to its score tile (sxw[b * 64 + lane]). PIN:
+// the group barriers make the LDS reads run QK_AHEAD k-steps ahead of the
+// MFMAs that use them (otherwise the caller pins the whole region).
+template <int DKC, int NJ, bool PIN = true>
 __device__ __forceinline__ void attn_wide_qk(const uint16_t *ks, const sglkv_u16x8 (&qf)[DKC / 2], uint32_t kc0,
                                              uint32_t g, uint32_t r, uint32_t lane, sglkv_f32x4 (&sc)[2],
                                              sglkv_f32x4 *sxw) {
@@ -767,13 +768,15 @@ __device__ __forceinline__ void attn_wide_qk(const uint16_t *ks, const sglkv_u16
 #pragma unroll
         for (uint32_t b = 0; b < 2; ++b)
             sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(kf[c][b]), attn_as_bf16(qf[c]), sc[b], 0, 0, 0);
-    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * G::QK_AHEAD, 0);
+    if (PIN) {
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * G::QK_AHEAD, 0);
 #pragma unroll
-    for (uint32_t c = 0; c < G::KH - G::QK_AHEAD; ++c) {
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+        for (uint32_t c = 0; c < G::KH - G::QK_AHEAD; ++c) {
+            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2 * G::QK_AHEAD, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2 * G::QK_AHEAD, 0);
     sxw[lane] = sc[0];
     sxw[64 + lane] = sc[1];
 }
@@ -781,8 +784,8 @@ __device__ __forceinline__ void attn_wide_qk(const uint16_t *ks, const sglkv_u16
 // Adds the other half's partial scores (sxo) to sc, then softmax and p.v
 // over this wave's value blocks (from dim 16 * j0). EXACT: the running
 // maximum and per-block rescaling; otherwise the fixed reference, with
-// *over set when a block exceeds it.
-template <bool EXACT, int DKC, int NJ>
+// *over set when a block exceeds it. PIN as for attn_wide_qk.
+template <bool EXACT, int DKC, int NJ, bool PIN = true>
 __device__ __forceinline__ void attn_wide_pv(const sglkv_attn_params &p, const uint16_t *vs, sglkv_f32x4 (&sc)[2],
                                              const sglkv_f32x4 *sxo, const uint32_t *cur, uint32_t j0, uint32_t g,
                                              uint32_t r, uint32_t lane, attn_state_n<NJ / 2> &st, bool *over) {
@@ -855,13 +858,15 @@ __device__ __forceinline__ void attn_wide_pv(const sglkv_attn_params &p, const u
                                 (uint16_t)vhi[j][0], (uint16_t)vhi[j][1], (uint16_t)vhi[j][2], (uint16_t)vhi[j][3]};
         st.o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(pbits), attn_as_bf16(vv), st.o[j], 0, 0, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * G::PV_AHEAD, 1);
+    if (PIN) {
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * G::PV_AHEAD, 1);
 #pragma unroll
-    for (uint32_t j = 0; j < G::NJH - G::PV_AHEAD; ++j) {
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 1);
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 1);
+        for (uint32_t j = 0; j < G::NJH - G::PV_AHEAD; ++j) {
+            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 1);
+            __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 1);
+        }
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, G::PV_AHEAD, 1);
     }
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, G::PV_AHEAD, 1);
 }
 
 template <int DKC, int NJ>
@@ -938,29 +943,43 @@ __device__ __forceinline__ void attn_wide_body(const sglkv_attn_params &p) {
     attn_wide_stage<DKC, NJ> ra, rb;  // K rows: two stages; V rows: ra.v
     attn_wide_load_k<DKC, NJ>(p, kbase, slots, tid, ra);
     attn_wide_load_v<DKC, NJ>(p, vbase, slots, tid, ra);
-    if (nb > 1) attn_wide_load_k<DKC, NJ>(p, kbase, slots + B, tid, rb);
+    attn_wide_load_k<DKC, NJ>(p, kbase, slots + (nb > 1 ? B : 0), tid, rb);
     attn_wide_store_k<DKC, NJ>(ks, tid, ra);
-    attn_wide_store_v<DKC, NJ>(vs, tid, ra);
     __syncthreads();
 
     attn_state_n<G::NJH> st;
     attn_state_init(st);
     st.m_run = -INFINITY;  // reference not fixed yet
     bool over = false;
-    // Block k is in LDS and block k+1's K rows in register stage `next`:
-    // load block k+1's V rows and block k+2's K rows (into `fr`, the stage
-    // block k left), q.k, barrier, store k+1's K rows, p.v, barrier, store
-    // its V rows.
+    // One iteration (block k; `fr` is the K stage block k left, `next`
+    // holds block k+1's K rows). Loads and stores run whether or not their
+    // block exists (block indices clamp to the last block; K rows stored
+    // after the last block are never read), and inactive waves (head
+    // groups past the query's) run q.k on zero queries, so the region up
+    // to the first barrier is one straight-line block and the group
+    // barriers at its end can interleave the K-row loads with the q.k
+    // MFMAs. p.v stays behind `active`: the accumulators of a wave that
+    // skips it are never written.
     auto step = [&](uint32_t k, attn_wide_stage<DKC, NJ> &fr, attn_wide_stage<DKC, NJ> &next) {
-        if (k + 1 < nb) attn_wide_load_v<DKC, NJ>(p, vbase, slots + (k + 1) * B, tid, ra);
-        if (k + 2 < nb) attn_wide_load_k<DKC, NJ>(p, kbase, slots + (k + 2) * B, tid, fr);
+        const uint32_t k1 = k + 1 < nb ? k + 1 : nb - 1, k2 = k + 2 < nb ? k + 2 : nb - 1;
+        attn_wide_load_k<DKC, NJ>(p, kbase, slots + k2 * B, tid, fr);
         sglkv_f32x4 sc[2];
-        if (active) attn_wide_qk<DKC, NJ>(ks, qf, kc0, g, r, lane, sc, sxw);
+        attn_wide_qk<DKC, NJ, false>(ks, qf, kc0, g, r, lane, sc, sxw);
+        attn_wide_store_v<DKC, NJ>(vs, tid, ra);
+        attn_wide_load_v<DKC, NJ>(p, vbase, slots + k1 * B, tid, ra);
+        // Slot reads, then K-row loads between the q.k MFMAs, LDS reads of
+        // K running QK_AHEAD k-steps ahead.
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 + 2 * G::QK_AHEAD, 0);
+#pragma unroll
+        for (uint32_t c = 0; c < G::KH; ++c) {
+            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
+            if (c < G::KPT + (G::RTHREADS ? 1 : 0)) __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
+            if (c + G::QK_AHEAD < G::KH) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+        }
         __syncthreads();
-        if (k + 1 < nb) attn_wide_store_k<DKC, NJ>(ks, tid, next);
-        if (active) attn_wide_pv<false, DKC, NJ>(p, vs, sc, sxo, slots + k * B, j0, g, r, lane, st, &over);
+        attn_wide_store_k<DKC, NJ>(ks, tid, next);
+        if (active) attn_wide_pv<false, DKC, NJ, false>(p, vs, sc, sxo, slots + k * B, j0, g, r, lane, st, &over);
         __syncthreads();
-        if (k + 1 < nb) attn_wide_store_v<DKC, NJ>(vs, tid, ra);
     };
     for (uint32_t k = 0; k < nb; k += 2) {
         step(k, ra, rb);

@@ -21,12 +21,13 @@
 //  - long sequences are split over gridDim.y (flash-decoding): each split
 //    writes (max, sum, unnormalised output) and a combine kernel merges
 //    them, so a small batch still fills 256 CUs.
-// Two bodies share this math. The pipelined one (head dims up to 128,
+// Three bodies share this math. The pipelined one (head dims up to 128,
 // 16-byte rows, power-of-two pages: every Llama/Qwen-style decode) loads
 // the slots of block i+2 and the K/V rows of block i+1 while it computes
 // block i, so a wave never waits on the dependent slot -> row loads; the
-// generic one serves every other shape (MLA widths, odd dims) one block at
-// a time.
+// wide one (many query heads per KV head, MLA widths) stages each block
+// once in LDS for up to 64 heads; the generic one serves every other shape
+// (odd dims, unaligned rows) one block at a time.
 // Metadata errors set the device error word (SGLKV_FLAG_ATTN_*) and skip
 // the query, as the reference's kernel does.
 

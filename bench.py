@@ -84,8 +84,9 @@ DESCRIPTIONS = {
                 "512-wide latent value, bf16, one KV head), page_size 64 with a random page "
                 "table, 32 requests x 8192 tokens, one decode query each with 128 query heads",
     "ceilings": "the device's streaming ceilings: contiguous copy, read and write of 1 GiB in "
-                "16-byte non-temporal vectors (sgl_rocm_kv_stream), hipMemcpyDtoD, and the host "
-                "link (1 GiB DMA copies to and from pinned host memory, one direction at a time)",
+                "16-byte non-temporal vectors (sgl_rocm_kv_stream), hipMemcpyDtoD, the same copy "
+                "over 16 GiB, and the host link (1 GiB DMA copies to and from pinned host memory, "
+                "one direction at a time)",
     "c5": "C5: ragged radix-prefix GQA transfer (Llama-3-8B shape), 512 requests log-uniform "
           "[16,32768], page-aligned cached prefixes U[0,0.9]; request waves through the layer "
           "pipeline pack -> D2H -> pinned host -> H2D -> unpack on 4 streams",
@@ -466,12 +467,28 @@ def run_pages(args):
     gbs = 2 * payload / (wall / args.steps) / 1e9
     achieved = 2 * payload / (launch_ms / 1e3) / 1e9
     log(f"page requests: {len(reqs)} x {pb >> 20} MiB, wall {gbs:.0f} GB/s, launch {launch_ms:.3f} ms")
+    # The ceiling at this footprint: one contiguous copy of the same payload
+    # between the same two pools (HBM streams more slowly over 16 GiB than
+    # over 1 GiB).
+    sb, db = kv.device_buffer(src.ptr, payload), kv.device_buffer(dst.ptr, payload)
+    k.stream_ceiling(kv.STREAM_COPY, sb, db, payload, s)
+    a.record(s)
+    for _ in range(3):
+        k.stream_ceiling(kv.STREAM_COPY, sb, db, payload, s)
+    b.record(s)
+    s.synchronize()
+    k.check_errors()
+    ceiling = 2 * payload * 3 / (a.elapsed_ms(b) / 1e3) / 1e9
+    log(f"contiguous copy of the same {payload >> 30} GiB: {ceiling:.0f} GB/s")
     k.close()
     return {
         "value": round(gbs, 1),
         "ms_per_step": round(wall * 1e3 / args.steps, 4),
         "config_extra": {"pages": pages_moved, "page_bytes": pb, "payload_bytes": payload,
                          "algorithmic_bytes_per_step": 2 * payload},
+        "copy_ceiling": {"gbs": round(ceiling, 1), "value_frac_of_ceiling": round(gbs / ceiling, 4),
+                         "note": "sgl_rocm_kv_stream contiguous copy of the same payload between "
+                                 "the same pools, same process"},
         "roofline": {"bound": "hbm", "kernel": "sglkv_copy_requests", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": None, "algorithmic_bytes_per_launch": 2 * payload},
@@ -685,6 +702,26 @@ def run_ceilings(args):
         out[name] = (n / (ms / 1e3) / 1e9, ms)
         log(f"{name}: {ms:.1f} ms per GiB, {out[name][0]:.1f} GB/s")
     host.free()
+    # The same copy over 16 GiB: HBM reaches a lower rate once the footprint
+    # is far larger than the last-level cache, which is the regime of
+    # transfers that move the whole pool in one launch (c2pages).
+    a.free()
+    b.free()
+    big = 16 << 30
+    a, b = hip.DeviceBuffer(big), hip.DeviceBuffer(big)
+    abig, bbig = kv.device_buffer(a.ptr, big), kv.device_buffer(b.ptr, big)
+    k.stream_ceiling(kv.STREAM_COPY, abig, bbig, big, s)
+    e0, e1 = hip.Event(), hip.Event()
+    e0.record(s)
+    for _ in range(3):
+        k.stream_ceiling(kv.STREAM_COPY, abig, bbig, big, s)
+    e1.record(s)
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1) / 3
+    out["copy_16gib"] = (2 * big / (ms / 1e3) / 1e9, ms)
+    log(f"copy 16 GiB: {ms:.2f} ms per pass, {out['copy_16gib'][0]:.0f} GB/s")
+    a.free()
+    b.free()
     k.check_errors(s)
     k.close()
     gbs = out["copy"][0]
@@ -695,6 +732,7 @@ def run_ceilings(args):
         "read_gbs": round(out["read"][0], 1),
         "write_gbs": round(out["write"][0], 1),
         "memcpy_dtod_gbs": round(out["memcpy_dtod"][0], 1),
+        "copy_16gib_gbs": round(out["copy_16gib"][0], 1),
         "link_d2h_gbs": round(out["link_d2h"][0], 1),
         "link_h2d_gbs": round(out["link_h2d"][0], 1),
         "roofline": {"bound": "hbm", "kernel": "sglkv_stream_copy", "achieved": round(gbs, 1),

@@ -199,7 +199,7 @@ def test_slots_outside_the_sequences_hold_nan(k, dk, dv, P):
     np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
 
 
-@pytest.mark.parametrize("qh,hnd", [(128, False), (64, True), (48, False)])
+@pytest.mark.parametrize("qh,hnd", [(128, False), (64, True), (48, False), (16, False), (8, True)])
 def test_mla_many_heads(k, qh, hnd):
     """DeepSeek-V3's MLA decode as the reference calls it (cuda_mla.rs:273-294):
     every query head over one latent KV head, K 576 and V 512 wide (the
@@ -230,6 +230,66 @@ def test_wide_reference_outrun(k, dk, dv, qh, hnd):
     got, want = c.run(k, q, np.arange(5), lens, rso, slots, 1.0 / math.sqrt(dk), max_len=1500)
     assert np.isfinite(got).all()
     np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+
+
+def test_wide_unaligned_queries(k):
+    """A query buffer that is only 2-byte aligned: the wide bodies hold
+    queries as 16-byte vectors, so the launch must take the generic body,
+    with the same results."""
+    rng = np.random.default_rng(41)
+    c = _Case(rng, P=64, L=2, H=1, dk=576, dv=512, qh=32, pages=60, layer=1)
+    lens, rso, slots = _random_batch(rng, 3, 900, c.layout.slot_count)
+    q = _bf16_normal(rng, 3 * 32 * 576).reshape(3, 32, 576)
+    plan = kv.PagedAttentionPlan.for_layer(c.layout, 1, 3, 3, len(slots), 32, 1.0 / math.sqrt(576))
+    qbuf = hip.DeviceBuffer(q.nbytes + 2)
+    qbuf.upload(np.concatenate([np.zeros(1, np.uint16), q.reshape(-1)]).view(np.uint8))
+    out = hip.DeviceBuffer(plan.output_required_bytes)
+    _say("wide body, queries at a 2-byte offset")
+    k.paged_attention(plan, max_sequence_length=900, queries=qbuf, queries_offset=2,
+                      query_request_indices=hip.DeviceBuffer.from_array(np.arange(3, dtype=np.uint32)),
+                      query_sequence_lengths=hip.DeviceBuffer.from_array(lens.astype(np.uint64)),
+                      request_slot_offsets=hip.DeviceBuffer.from_array(rso),
+                      sequence_slots=hip.DeviceBuffer.from_array(slots), pool=c.pool, output=out)
+    got = oracle.bf16_to_f32(out.download().view(np.uint16)).reshape(3, 32, 512)
+    want, flags = oracle.paged_attention(
+        c.pool_h, q, np.arange(3), lens, rso, slots, page_size=64, page_stride=plan.page_stride_bytes,
+        key_offset=plan.key_in_page_offset, value_offset=plan.value_in_page_offset, kv_heads=1, dk=576,
+        dv=512, scale=1.0 / math.sqrt(576), slot_count=c.layout.slot_count)
+    assert flags == 0
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("dk,dv,qh,max_len", [(576, 512, 16, 4300), (128, 128, 32, 20000)])
+def test_wide_chunk_capped_by_slot_table(k, dk, dv, qh, max_len):
+    """Enough queries to fill the GPU without splitting (256 workgroups)
+    and sequences longer than the wide bodies' 4,096-token slot table: the
+    host must cap the chunk, so a query takes several splits, and the
+    shorter ones use fewer of them than the launch has. Sequences reuse the
+    rows of a small pool (slots drawn with replacement, as a slot list may
+    repeat them). A sample of the queries is checked."""
+    rng = np.random.default_rng(43 + dk)
+    nq = 256
+    c = _Case(rng, P=64, L=1, H=1, dk=dk, dv=dv, qh=qh, pages=48, layer=0)
+    lens = rng.integers(max_len - 300, max_len + 1, size=nq)
+    rso = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint64)
+    slots = rng.integers(0, c.layout.slot_count, size=int(rso[-1])).astype(np.uint64)
+    q = _bf16_normal(rng, nq * qh * dk).reshape(nq, qh, dk)
+    plan = kv.PagedAttentionPlan.for_layer(c.layout, 0, nq, nq, len(slots), qh, 1.0 / math.sqrt(dk))
+    out = hip.DeviceBuffer(plan.output_required_bytes)
+    _say(f"wide body, chunk capped: {nq} queries x up to {lens.max()} tokens, dk {dk}")
+    k.paged_attention(plan, max_sequence_length=int(lens.max()), queries=hip.DeviceBuffer.from_array(q),
+                      query_request_indices=hip.DeviceBuffer.from_array(np.arange(nq, dtype=np.uint32)),
+                      query_sequence_lengths=hip.DeviceBuffer.from_array(lens.astype(np.uint64)),
+                      request_slot_offsets=hip.DeviceBuffer.from_array(rso),
+                      sequence_slots=hip.DeviceBuffer.from_array(slots), pool=c.pool, output=out)
+    got = oracle.bf16_to_f32(out.download().view(np.uint16)).reshape(nq, qh, dv)
+    pick = np.array([0, int(np.argmax(lens)), int(np.argmin(lens)), 101, nq - 1])
+    want, flags = oracle.paged_attention(
+        c.pool_h, q[pick], pick, lens[pick], rso, slots, page_size=64, page_stride=plan.page_stride_bytes,
+        key_offset=plan.key_in_page_offset, value_offset=plan.value_in_page_offset, kv_heads=1, dk=dk,
+        dv=dv, scale=1.0 / math.sqrt(dk), slot_count=c.layout.slot_count)
+    assert flags == 0
+    np.testing.assert_allclose(got[pick], want, rtol=RTOL, atol=ATOL)
 
 
 def _random_shape(rng):

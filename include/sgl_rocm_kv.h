@@ -488,6 +488,21 @@ int32_t sgl_rocm_kv_write_tensor_slots(sgl_rocm_kv_ctx *ctx, const sgl_kv_paged_
                                        uint64_t count, const sgl_kv_device_buffer *source,
                                        uint64_t source_offset, uint64_t source_row_stride,
                                        void *stream);
+/* Both tensors of one layer (key rows keys_offset + i * keys_row_stride,
+ * value rows values_offset + i * values_row_stride; widths from the
+ * layout, unequal for MLA's 576/512 pair) to `count` slots in one launch:
+ * the forward-pass write the reference's MLA decode makes per token with
+ * two write_tensor_slot_from_device calls (cuda_mla.rs:256-271 through
+ * cuda_kv_cache.rs:258-294). Layer checked on the host (LayerOutOfRange;
+ * TensorOutOfRange for a one-tensor layout); a slot past the pool raises
+ * the error word (SLOT) and its row is skipped. Asynchronous. */
+int32_t sgl_rocm_kv_write_tensor_pair_slots(sgl_rocm_kv_ctx *ctx, const sgl_kv_paged_layout *layout,
+                                            const sgl_kv_device_buffer *pool, uint64_t layer,
+                                            const sgl_kv_device_buffer *slots, uint64_t count,
+                                            const sgl_kv_device_buffer *keys, uint64_t keys_offset,
+                                            uint64_t keys_row_stride, const sgl_kv_device_buffer *values,
+                                            uint64_t values_offset, uint64_t values_row_stride,
+                                            void *stream);
 int32_t sgl_rocm_kv_read_tensor_slots(sgl_rocm_kv_ctx *ctx, const sgl_kv_paged_layout *layout,
                                       const sgl_kv_device_buffer *pool, uint64_t layer,
                                       uint64_t tensor, const sgl_kv_device_buffer *slots,

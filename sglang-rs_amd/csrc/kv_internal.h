@@ -102,6 +102,7 @@ struct sgl_rocm_kv_ctx {
     hipFunction_t resolve;
     hipFunction_t fill;
     hipFunction_t requests;
+    hipFunction_t pair_slots[2];    // key+value slot writes: 16-byte, 1-byte pieces
     hipFunction_t stream_fn[3];     // streaming ceilings: copy, read, write
     // 16-byte vector / element-wise / pipelined dims 128 / pipelined dims <= 128 /
     // wide (K <= 576, V <= 512) / wide dims <= 128

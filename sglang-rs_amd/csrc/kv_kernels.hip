@@ -395,6 +395,44 @@ extern "C" __global__ __launch_bounds__(SGLKV_BLOCK_THREADS) void sglkv_copy_req
     }
 }
 
+// Forward-pass write of a layer's key and value rows (unequal widths) to
+// their slots: one launch for both tensors of a layer, where the reference
+// copies one (token, tensor) per cuMemcpyDtoD (cuda_mla.rs:256-271 through
+// cuda_kv_cache.rs:258-294). A slot >= slot_count raises SGLKV_FLAG_SLOT
+// and its row is skipped.
+template <int W>
+__device__ __forceinline__ void sglkv_pair_slots_body(const sglkv_pair_slots_params &p) {
+    const uint64_t per_row = p.pieces[0] + p.pieces[1];
+    const uint64_t t = static_cast<uint64_t>(blockIdx.x) * SGLKV_BLOCK_THREADS + threadIdx.x;
+    const uint64_t row = t / per_row;
+    if (row >= p.count) return;
+    const uint64_t piece = t - row * per_row;
+    const uint64_t slot = p.slots[row];
+    if (slot >= p.slot_count) {
+        if (piece == 0) atomicOr(p.flag, SGLKV_FLAG_SLOT);
+        return;
+    }
+    const uint32_t k = piece < p.pieces[0] ? 0 : 1;
+    const uint64_t pc = k ? piece - p.pieces[0] : piece;
+    const uint64_t page = slot / p.page_size, pos = slot - page * p.page_size;
+    uint8_t *dst = p.pool + page * p.page_stride + p.offset[k] + pos * p.row_bytes[k] + pc * W;
+    const uint8_t *src = p.rows[k] + row * p.row_stride[k] + pc * W;
+    if (W == 16)
+        *reinterpret_cast<sglkv_v4u *>(dst) = *reinterpret_cast<const sglkv_v4u *>(src);
+    else
+        *dst = *src;
+}
+
+extern "C" __global__ __launch_bounds__(SGLKV_BLOCK_THREADS) void sglkv_write_pair_slots_v16(
+    const sglkv_pair_slots_params p) {
+    sglkv_pair_slots_body<16>(p);
+}
+
+extern "C" __global__ __launch_bounds__(SGLKV_BLOCK_THREADS) void sglkv_write_pair_slots_v1(
+    const sglkv_pair_slots_params p) {
+    sglkv_pair_slots_body<1>(p);
+}
+
 // Streaming ceilings of the device, for the benchmark's roofline context:
 // a plain contiguous copy, read and write of 16-byte vectors, grid-stride,
 // non-temporal, U vectors in flight per thread (the fastest settings of a

@@ -206,6 +206,26 @@ typedef struct sglkv_attn_params {
     uint32_t reserved2;
 } sglkv_attn_params;
 
+/* Both tensors of one layer for `count` slots in one launch (key and value
+ * rows of unequal width, as MLA writes them): thread t moves piece
+ * t % (pieces[0] + pieces[1]) of row t / (pieces[0] + pieces[1]), the key
+ * row's pieces first. A piece is W bytes (kernel variant: 16 or 1). */
+typedef struct sglkv_pair_slots_params {
+    const uint64_t *slots;
+    uint64_t count;
+    uint64_t slot_count;
+    uint8_t *pool;
+    uint64_t page_size;
+    uint64_t page_stride;
+    uint64_t offset[2];      /* in-page offset of the layer's key / value region */
+    uint64_t row_bytes[2];
+    const uint8_t *rows[2];  /* source rows of each tensor */
+    uint64_t row_stride[2];
+    uint64_t pieces[2];      /* row_bytes / W */
+    uint32_t *flag;          /* device error word (SGLKV_FLAG_SLOT) */
+    uint32_t reserved;
+} sglkv_pair_slots_params;
+
 /* Bytes of zeros the context keeps for reads that must contribute nothing
  * (>= the widest row piece a pipelined attention lane reads, 256 B). */
 #define SGLKV_ZERO_ROW_BYTES 1024u

@@ -393,6 +393,10 @@ extern "C" int32_t sgl_rocm_kv_init(int32_t device, const char *code_object_path
         err = hipModuleGetFunction(&ctx->stream_fn[i], ctx->module, stream_names[i]);
     if (err == hipSuccess) err = hipModuleGetFunction(&ctx->requests, ctx->module, "sglkv_copy_requests");
     if (err == hipSuccess)
+        err = hipModuleGetFunction(&ctx->pair_slots[0], ctx->module, "sglkv_write_pair_slots_v16");
+    if (err == hipSuccess)
+        err = hipModuleGetFunction(&ctx->pair_slots[1], ctx->module, "sglkv_write_pair_slots_v1");
+    if (err == hipSuccess)
         err = hipModuleGetFunction(&ctx->attention[0], ctx->module, "sglkv_paged_attention_v16");
     if (err == hipSuccess)
         err = hipModuleGetFunction(&ctx->attention[1], ctx->module, "sglkv_paged_attention_v2");
@@ -685,6 +689,72 @@ extern "C" int32_t sgl_rocm_kv_write_tensor_slots(sgl_rocm_kv_ctx *ctx, const sg
                                                   void *stream) {
     return tensor_slots(ctx, layout, pool, layer, tensor, slots, count, source, source_offset,
                         source_row_stride, true, stream);
+}
+
+extern "C" int32_t sgl_rocm_kv_write_tensor_pair_slots(
+    sgl_rocm_kv_ctx *ctx, const sgl_kv_paged_layout *layout, const sgl_kv_device_buffer *pool, uint64_t layer,
+    const sgl_kv_device_buffer *slots, uint64_t count, const sgl_kv_device_buffer *keys, uint64_t keys_offset,
+    uint64_t keys_row_stride, const sgl_kv_device_buffer *values, uint64_t values_offset,
+    uint64_t values_row_stride, void *stream) {
+    int32_t rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!layout || !pool || !slots || !keys || !values)
+        return fail(SGL_KV_INVALID_ARGUMENT, "layout/pool/slot_indices/keys/values", 0, 0, 0, "null argument");
+    if (pool->byte_len < layout->total_byte_len)
+        return out_of_bounds("pool", 0, layout->total_byte_len, pool->byte_len);
+    sgl_kv_pool_view v[2];
+    for (uint32_t t = 0; t < 2; ++t)
+        if ((rc = sgl_kv_pool_view_for_layer(layout, pool->ptr, pool->byte_len, SGL_KV_NHD, 1, layer, t, 1,
+                                             &v[t])))
+            return rc;
+    if (count == 0) return ok();
+    if (!pool->ptr) return fail(SGL_KV_INVALID_ARGUMENT, "pool", 0, 0, 0, "null pool");
+    if (!slots->ptr) return fail(SGL_KV_INVALID_ARGUMENT, "slot_indices", 0, 0, 0, "null slot map");
+    uint64_t need;
+    if (mul_ovf(count, sizeof(uint64_t), &need)) return shape_overflow();
+    if (need > slots->byte_len) return out_of_bounds("slot_indices", 0, need, slots->byte_len);
+    const sgl_kv_device_buffer *rows[2] = {keys, values};
+    const uint64_t offs[2] = {keys_offset, values_offset}, strides[2] = {keys_row_stride, values_row_stride};
+    const char *const names[2] = {"keys", "values"};
+    sglkv_pair_slots_params p;
+    memset(&p, 0, sizeof p);
+    uint64_t bits = (uint64_t)(uintptr_t)pool->ptr | v[0].page_stride_bytes;
+    for (uint32_t t = 0; t < 2; ++t) {
+        if (!rows[t]->ptr) return fail(SGL_KV_INVALID_ARGUMENT, names[t], 0, 0, 0, "null rows");
+        if (strides[t] < v[t].row_bytes)
+            return fail(SGL_KV_ROW_STRIDE_TOO_SMALL, names[t], v[t].row_bytes, strides[t], 0,
+                        "KV copy %s row stride %llu bytes is smaller than row width %llu bytes", names[t],
+                        (unsigned long long)strides[t], (unsigned long long)v[t].row_bytes);
+        if (mul_ovf(count - 1, strides[t], &need) || add_ovf(need, v[t].row_bytes, &need) ||
+            add_ovf(need, offs[t], &need))
+            return shape_overflow();
+        if (need > rows[t]->byte_len) return out_of_bounds(names[t], offs[t], need - offs[t], rows[t]->byte_len);
+        p.offset[t] = v[t].tensor_offset[0];
+        p.row_bytes[t] = v[t].row_bytes;
+        p.rows[t] = static_cast<const uint8_t *>(rows[t]->ptr) + offs[t];
+        p.row_stride[t] = strides[t];
+        bits |= p.offset[t] | p.row_bytes[t] | (uint64_t)(uintptr_t)p.rows[t] | p.row_stride[t];
+    }
+    const uint32_t w = (bits & 15u) == 0 ? 16u : 1u;
+    p.slots = static_cast<const uint64_t *>(slots->ptr);
+    p.count = count;
+    p.pool = static_cast<uint8_t *>(pool->ptr);
+    p.page_size = v[0].page_size;
+    p.page_stride = v[0].page_stride_bytes;
+    if (mul_ovf(v[0].page_size, v[0].page_count, &p.slot_count)) return shape_overflow();
+    p.pieces[0] = p.row_bytes[0] / w;
+    p.pieces[1] = p.row_bytes[1] / w;
+    p.flag = ctx->flag;
+    uint64_t threads;
+    if (mul_ovf(count, p.pieces[0] + p.pieces[1], &threads)) return shape_overflow();
+    const uint64_t grid = threads / SGLKV_BLOCK_THREADS + (threads % SGLKV_BLOCK_THREADS ? 1 : 0);
+    if (grid > INT32_MAX) return too_large("grid blocks", grid, INT32_MAX);
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    void *args[] = {&p};
+    SGLKV_HIP(hipModuleLaunchKernel(ctx->pair_slots[w == 16 ? 0 : 1], (unsigned)grid, 1, 1, SGLKV_BLOCK_THREADS,
+                                    1, 1, 0, static_cast<hipStream_t>(stream), args, nullptr));
+    return ok();
 }
 
 extern "C" int32_t sgl_rocm_kv_read_tensor_slots(sgl_rocm_kv_ctx *ctx, const sgl_kv_paged_layout *layout,

@@ -345,6 +345,12 @@ _EXPORTS = {
                                                         ctypes.POINTER(_DeviceBuffer), _u64,
                                                         ctypes.POINTER(_DeviceBuffer), _u64, _u64,
                                                         ctypes.c_void_p]),
+    "sgl_rocm_kv_write_tensor_pair_slots": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_PagedLayout),
+                                                             ctypes.POINTER(_DeviceBuffer), _u64,
+                                                             ctypes.POINTER(_DeviceBuffer), _u64,
+                                                             ctypes.POINTER(_DeviceBuffer), _u64, _u64,
+                                                             ctypes.POINTER(_DeviceBuffer), _u64, _u64,
+                                                             ctypes.c_void_p]),
     "sgl_rocm_kv_read_tensor_slots": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_PagedLayout),
                                                        ctypes.POINTER(_DeviceBuffer), _u64, _u64,
                                                        ctypes.POINTER(_DeviceBuffer), _u64,
@@ -875,6 +881,21 @@ class RocmKvPairCopyKernels:
         _call(lib().sgl_rocm_kv_write_tensor_slots, self._h, ctypes.byref(layout._c),
               ctypes.byref(pool), layer, tensor, ctypes.byref(slots), count, ctypes.byref(source),
               source_offset, source_row_stride, _stream(stream))
+
+    def write_tensor_pair_slots(self, layout: "PagedKvCacheLayout", pool: _DeviceBuffer, layer: int,
+                                slots: _DeviceBuffer, count: int, keys: _DeviceBuffer, values: _DeviceBuffer,
+                                keys_offset: int = 0, keys_row_stride: int | None = None,
+                                values_offset: int = 0, values_row_stride: int | None = None, stream=None):
+        """Both tensors of `layer` for `count` slots in one launch: key rows
+        keys_offset + i * stride and value rows values_offset + i * stride
+        (strides default to each tensor's token width)."""
+        if keys_row_stride is None:
+            keys_row_stride = layout.tensor_token_bytes(0)
+        if values_row_stride is None:
+            values_row_stride = layout.tensor_token_bytes(1)
+        _call(lib().sgl_rocm_kv_write_tensor_pair_slots, self._h, ctypes.byref(layout._c),
+              ctypes.byref(pool), layer, ctypes.byref(slots), count, ctypes.byref(keys), keys_offset,
+              keys_row_stride, ctypes.byref(values), values_offset, values_row_stride, _stream(stream))
 
     def read_tensor_slots(self, layout: "PagedKvCacheLayout", pool: _DeviceBuffer, layer: int,
                           tensor: int, slots: _DeviceBuffer, count: int, destination: _DeviceBuffer,

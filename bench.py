@@ -480,6 +480,12 @@ def run_pages(args):
     k.check_errors()
     ceiling = 2 * payload * 3 / (a.elapsed_ms(b) / 1e3) / 1e9
     log(f"contiguous copy of the same {payload >> 30} GiB: {ceiling:.0f} GB/s")
+    if args.calibration_copy:   # a plain copy of known size for the counter runs
+        span = 1 << 30
+        for _ in range(3):
+            hip.memcpy_async(dst.ptr, src.ptr, span, "d2d", s)
+        s.synchronize()
+        log(f"calibration copies done (3 x {span} B device-to-device)")
     k.close()
     return {
         "value": round(gbs, 1),
@@ -491,7 +497,8 @@ def run_pages(args):
                                  "the same pools, same process"},
         "roofline": {"bound": "hbm", "kernel": "sglkv_copy_requests", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "algorithmic_bytes_per_launch": 2 * payload},
+                     "traffic": _traffic_from_profiles("sglkv_copy_requests", "kv_copy_c2pages"),
+                     "algorithmic_bytes_per_launch": 2 * payload},
     }
 
 

@@ -141,6 +141,49 @@ def test_oracle_attention_matches_torch_sdpa(hnd):
     np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
 
 
+def test_oracle_attention_pair_layout_matches_torch_sdpa():
+    """Unequal key and value widths in a tensor-pair layout, the MLA form
+    (576/512 for DeepSeek-V3, 24/16 here): rows gathered through the
+    layout's tensor_slot_byte_range (pinned by the reference's layout
+    goldens), attention by torch's scaled_dot_product_attention in float64
+    with every query head on the one KV head."""
+    torch = pytest.importorskip("torch")
+    P, L, dk, dv, pages, qh, layer = 4, 2, 24, 16, 6, 8, 1
+    kb, vb = dk * 2, dv * 2
+    rt = kv.KvCacheRuntimeLayout("bf16", P, L, 1, dk, 2, L * (kb + vb), L * (kb + vb) * P)
+    lay = kv.PagedKvCacheLayout.new_with_tensor_pair(rt, pages, kb, vb)
+    rng = np.random.default_rng(17)
+    pool = oracle.f32_to_bf16(rng.standard_normal(lay.total_byte_len // 2).astype(np.float32)).view(np.uint8)
+    lens = [7, 1, 11]
+    rso = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint64)
+    slots = rng.permutation(lay.slot_count)[:int(rso[-1])].astype(np.uint64)
+    qri, qsl = np.array([0, 1, 2, 2], np.uint32), np.array([7, 1, 11, 4], np.uint64)
+    queries = oracle.f32_to_bf16(rng.standard_normal((4, qh, dk)).astype(np.float32))
+    scale = 0.3
+    plan = kv.PagedAttentionPlan.for_layer(lay, layer, 4, 3, len(slots), qh, scale)
+    got, flags = oracle.paged_attention(pool, queries, qri, qsl, rso, slots, page_size=P,
+                                        page_stride=plan.page_stride_bytes, key_offset=plan.key_in_page_offset,
+                                        value_offset=plan.value_in_page_offset, kv_heads=1, dk=dk, dv=dv,
+                                        scale=scale, slot_count=lay.slot_count)
+    assert flags == 0
+
+    def rows(sl, tensor):
+        out = []
+        for s_ in sl:
+            a, b = lay.tensor_slot_byte_range(layer, tensor, int(s_))
+            out.append(oracle.bf16_to_f32(pool[a:b].view(np.uint16)))
+        return np.stack(out).astype(np.float64)
+
+    qf = oracle.bf16_to_f32(queries).astype(np.float64)
+    for q in range(4):
+        sl = slots[rso[qri[q]]:rso[qri[q]] + qsl[q]]
+        kt = torch.from_numpy(rows(sl, 0))[None].expand(qh, -1, -1)
+        vt = torch.from_numpy(rows(sl, 1))[None].expand(qh, -1, -1)
+        o = torch.nn.functional.scaled_dot_product_attention(torch.from_numpy(qf[q])[:, None, :], kt, vt,
+                                                             scale=scale)
+        np.testing.assert_allclose(got[q], o[:, 0, :].numpy(), rtol=1e-12, atol=1e-12)
+
+
 def test_oracle_attention_closed_forms_and_flags():
     """One attended token returns its value row exactly; equal keys return
     the mean of the values; bad metadata sets the reference's flag bits."""

@@ -57,6 +57,7 @@ HBM_PEAK_GBS = 8000.0
 METRIC = "KV pack+unpack GB/s and % of HBM peak, Llama-3-8B shape; per-layer p50 µs"
 ATTN_METRIC = "paged-attention decode GB/s of K/V read and % of HBM peak, Llama-3-8B shape"
 MLA_METRIC = "paged-attention decode GB/s of K/V read and % of HBM peak, DeepSeek-V3 MLA shape"
+DIRECT_METRIC = "KV pool-to-pool transfer GB/s (bytes read + written) and % of HBM peak, Llama-3-8B shape"
 
 DESCRIPTIONS = {
     "c1": "C1: Qwen2-0.5B-like GQA KV transfer, 24 layers x 2 KV heads x 64, bf16, 8 requests "
@@ -87,6 +88,8 @@ DESCRIPTIONS = {
                 "16-byte non-temporal vectors (sgl_rocm_kv_stream), hipMemcpyDtoD, the same copy "
                 "over 16 GiB, and the host link (1 GiB DMA copies to and from pinned host memory, "
                 "one direction at a time)",
+    "c2direct": "C2 moved pool -> pool (sgl_rocm_kv_transfer_layer per layer, no transfer rows): "
+                "the co-resident form of the C2 transfer; algorithmic bytes = 2 x payload",
     "c5": "C5: ragged radix-prefix GQA transfer (Llama-3-8B shape), 512 requests log-uniform "
           "[16,32768], page-aligned cached prefixes U[0,0.9]; request waves through the layer "
           "pipeline pack -> D2H -> pinned host -> H2D -> unpack on 4 streams",
@@ -111,10 +114,11 @@ def _traffic_from_profiles(kernel: str, summary: str):
     return None
 
 
-def cpu_baseline(make, seconds: float = 10.0, rows: int = 8192, threads: int = 1):
-    """The CPU oracle's pack + unpack on `threads` host threads (rows split
-    evenly) on the first `rows` tokens of the workload, repeated for about
-    `seconds`."""
+def cpu_baseline(make, seconds: float = 10.0, rows: int = 8192, threads: int = 1,
+                 direct: bool = False):
+    """The CPU oracle's pack + unpack (direct: its pool -> pool transfer) on
+    `threads` host threads (rows split evenly) on the first `rows` tokens of
+    the workload, repeated for about `seconds`."""
     import oracle
     from sgl_rocm_kv import workloads as wl
     t = wl.scaled(make(), rows, seed=1)
@@ -133,6 +137,10 @@ def cpu_baseline(make, seconds: float = 10.0, rows: int = 8192, threads: int = 1
         part = buf[layer * T * n * rb:(layer + 1) * T * n * rb]
         pools.append((opool(t.src), opool(t.dst), part[: n * rb], part[n * rb:] if T == 2 else None))
     def one_pass():
+        if direct:
+            for sp, dp, _, _ in pools:
+                oracle.transfer(sp, src, t.src_slots, dp, dst, t.dst_slots, threads=threads)
+            return
         for sp, dp, r0, r1 in pools:
             oracle.pack(sp, src, t.src_slots, r0, r1, rb, rb, threads=threads)
         for sp, dp, r0, r1 in pools:
@@ -146,10 +154,11 @@ def cpu_baseline(make, seconds: float = 10.0, rows: int = 8192, threads: int = 1
         el = time.perf_counter() - t0
         if el >= seconds or reps >= 1000:
             break
-    gbs = 4 * t.payload_bytes * reps / el / 1e9
+    gbs = (2 if direct else 4) * t.payload_bytes * reps / el / 1e9
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"{t.name.split(' (')[0]} shape, first {n} tokens ({sh.layers} layers, "
-                      f"{t.payload_bytes >> 20} MiB payload), pack+unpack x {reps} in {el:.1f} s, "
+                      f"{t.payload_bytes >> 20} MiB payload), "
+                      f"{'pool -> pool transfer' if direct else 'pack+unpack'} x {reps} in {el:.1f} s, "
                       f"oracle/kv_oracle.c, {threads} thread{'s' if threads > 1 else ''}"}
 
 
@@ -502,6 +511,143 @@ def run_pages(args):
     }
 
 
+def run_direct(t, args):
+    """C2 moved pool -> pool (sgl_rocm_kv_transfer_layer per layer): what
+    co-resident pools need, with no transfer rows between the two copies.
+    Algorithmic bytes = 2 x payload (each K/V row read once, written once)."""
+    import sgl_rocm_kv as kv
+    from sgl_rocm_kv import hip
+    sh = t.shape
+    rb, n, L, T = sh.row_bytes, t.rows, sh.layers, sh.tensors
+    k = kv.RocmKvPairCopyKernels(0)
+    src, dst = hip.DeviceBuffer(t.src.byte_len(sh)), hip.DeviceBuffer(t.dst.byte_len(sh))
+    k.fill_synthetic(kv.device_buffer(src.ptr, src.nbytes), 2024, kv.FILL_BF16_NORMAL)
+    ss, ds = hip.DeviceBuffer.from_array(t.src_slots), hip.DeviceBuffer.from_array(t.dst_slots)
+    ssb, dsb = kv.device_buffer(ss.ptr, ss.nbytes), kv.device_buffer(ds.ptr, ds.nbytes)
+    sviews = [_views(kv, src, t.src, sh, l) for l in range(L)]
+    dviews = [_views(kv, dst, t.dst, sh, l) for l in range(L)]
+    s = hip.Stream()
+
+    def step(ev):
+        for l in range(L):
+            if ev:
+                ev[l][0].record(s)
+            k.transfer_layer(sviews[l], ssb, n, dviews[l], dsb, s)
+            if ev:
+                ev[l][1].record(s)
+
+    for _ in range(args.warmup):
+        step(None)
+    hip.synchronize()
+    k.check_errors()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(None)
+    hip.synchronize()
+    wall = time.perf_counter() - t0
+    ev = [[[hip.Event(), hip.Event()] for _ in range(L)] for _ in range(args.steps)]
+    for i in range(args.steps):
+        step(ev[i])
+    hip.synchronize()
+    k.check_errors()
+    layer_ms = [e[0].elapsed_ms(e[1]) for es in ev for e in es]
+    payload = L * T * n * rb
+    launch_bytes = 2 * T * n * rb
+    gbs = 2 * payload / (wall / args.steps) / 1e9
+    achieved = launch_bytes / (float(np.mean(layer_ms)) / 1e3) / 1e9
+    log(f"pool -> pool: {float(np.mean(layer_ms)) * 1e3:.1f} us per layer ({achieved:.0f} GB/s), wall {gbs:.0f} GB/s")
+    if args.calibration_copy:   # a plain copy of known size for the counter runs
+        span = 1 << 30
+        for _ in range(3):
+            hip.memcpy_async(dst.ptr, src.ptr, span, "d2d", s)
+        s.synchronize()
+        log(f"calibration copies done (3 x {span} B device-to-device)")
+    traffic = _traffic_from_profiles("sglkv_copy_pool_pool_v16", "kv_copy_c2direct")
+    k.close()
+    return {
+        "value": round(gbs, 1),
+        "ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "config_extra": {"tokens": n, "layers": L, "payload_bytes": payload,
+                         "algorithmic_bytes_per_step": 2 * payload},
+        "per_layer_p50_us": round(float(np.percentile(layer_ms, 50)) * 1e3, 2),
+        "roofline": {"bound": "hbm", "kernel": "sglkv_copy_pool_pool_v16", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic, "algorithmic_bytes_per_launch": launch_bytes},
+    }
+
+
+def run_chunked(t, config, args):
+    """Pack + unpack of every layer in args.chunks pieces through one reused
+    transfer region of n / chunks rows: each piece's rows are unpacked right
+    after they are packed, while the 256 MiB Infinity Cache still holds
+    them. A schedule for co-resident pools, not what a transfer between
+    devices sees (there the rows travel through HBM to the link)."""
+    import sgl_rocm_kv as kv
+    from sgl_rocm_kv import hip
+    sh = t.shape
+    rb, n, L, T = sh.row_bytes, t.rows, sh.layers, sh.tensors
+    chunks = args.chunks
+    if n % chunks:
+        raise SystemExit(f"--chunks {chunks} does not divide {n} rows")
+    m = n // chunks
+    k = kv.RocmKvPairCopyKernels(0)
+    src, dst = hip.DeviceBuffer(t.src.byte_len(sh)), hip.DeviceBuffer(t.dst.byte_len(sh))
+    xfer = hip.DeviceBuffer(T * m * rb)
+    k.fill_synthetic(kv.device_buffer(src.ptr, src.nbytes), 2024, kv.FILL_BF16_NORMAL)
+    ss, ds = hip.DeviceBuffer.from_array(t.src_slots), hip.DeviceBuffer.from_array(t.dst_slots)
+    sviews = [_views(kv, src, t.src, sh, l) for l in range(L)]
+    dviews = [_views(kv, dst, t.dst, sh, l) for l in range(L)]
+    rows = kv.rows_view([xfer.ptr + i * m * rb for i in range(T)], [m * rb] * T, [rb] * T, None)
+    sb = [kv.device_buffer(ss.ptr + c * m * 8, m * 8) for c in range(chunks)]
+    db = [kv.device_buffer(ds.ptr + c * m * 8, m * 8) for c in range(chunks)]
+    s = hip.Stream()
+
+    def step(ev):
+        for l in range(L):
+            if ev:
+                ev[l][0].record(s)
+            for c in range(chunks):
+                k.pack_layer(sviews[l], sb[c], m, rows, s)
+                k.unpack_layer(rows, m, dviews[l], db[c], s)
+            if ev:
+                ev[l][1].record(s)
+
+    for _ in range(args.warmup):
+        step(None)
+    hip.synchronize()
+    k.check_errors()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(None)
+    hip.synchronize()
+    wall = time.perf_counter() - t0
+    ev = [[[hip.Event(), hip.Event()] for _ in range(L)] for _ in range(args.steps)]
+    for i in range(args.steps):
+        step(ev[i])
+    hip.synchronize()
+    k.check_errors()
+    layer_ms = [e[0].elapsed_ms(e[1]) for es in ev for e in es]
+    step_bytes = t.algorithmic_bytes
+    gbs = step_bytes / (wall / args.steps) / 1e9
+    layer_bytes = step_bytes // L
+    achieved = layer_bytes / (float(np.mean(layer_ms)) / 1e3) / 1e9
+    log(f"{chunks} pieces per layer ({T * m * rb >> 20} MiB of rows each): wall {gbs:.0f} GB/s")
+    k.close()
+    return {
+        "value": round(gbs, 1),
+        "ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "config_extra": {"tokens": n, "layers": L, "chunks_per_layer": chunks,
+                         "transfer_region_bytes": T * m * rb, "algorithmic_bytes_per_step": step_bytes},
+        "per_layer_p50_us": round(float(np.percentile(layer_ms, 50)) * 1e3, 2),
+        "roofline": {"bound": "hbm", "kernel": "sglkv_copy_pool_rows_v16+sglkv_copy_rows_pool_v16",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": layer_bytes,
+                     "note": "one layer = its chunks' pack and unpack launches; rows are re-read "
+                             "from the Infinity Cache"},
+    }
+
+
 def _attention_geometry(config: str):
     """(layers, kv_heads, dk, dv, page_size, query_heads, scale) of an
     attention bench configuration: the C2 decode pool read by Llama-3-8B's
@@ -761,6 +907,10 @@ def main():
                     help="layer: one pack and one unpack launch per layer; layers: one launch of "
                          "each covering every layer; auto (default): layers when one layer moves "
                          "less than 256 MiB (launch-bound sizes), else layer")
+    ap.add_argument("--chunks", type=int, default=1,
+                    help="c2/c3/c4: pack and unpack each layer in this many pieces through one reused "
+                         "transfer region (co-resident schedule; rows re-read from the Infinity Cache). "
+                         "Default 1: whole layers, every layer's rows in its own region")
     ap.add_argument("--cpu-seconds", type=float, default=6.0,
                     help="seconds of CPU work per CPU-baseline figure")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1),
@@ -782,7 +932,7 @@ def main():
     from sgl_rocm_kv import workloads as wl
     makers = {"c1": wl.c1, "c2": wl.c2, "c3": wl.c3, "c4": wl.c4,
               "c4fp8": lambda: wl.c4(fp8=True), "c5": wl.c5, "c2pages": wl.c2, "attn": wl.c2,
-              "attn_hnd": wl.c2, "attn_mla": wl.c4, "ceilings": wl.c2}
+              "attn_hnd": wl.c2, "attn_mla": wl.c4, "ceilings": wl.c2, "c2direct": wl.c2}
     attention = args.config in ("attn", "attn_hnd", "attn_mla")
     t = makers[args.config]()
     log(f"workload {t.name}: {t.rows} tokens moved, payload {t.payload_bytes / 2**30:.2f} GiB")
@@ -794,12 +944,19 @@ def main():
         r = run_attention(args, args.config)
     elif args.config == "ceilings":
         r = run_ceilings(args)
+    elif args.config == "c2direct":
+        r = run_direct(t, args)
+    elif args.chunks > 1:
+        if args.config not in ("c2", "c3", "c4"):
+            raise SystemExit("--chunks applies to c2, c3 and c4")
+        r = run_chunked(t, args.config, args)
     else:
         r = run_coresident(t, args.config, args)
     gbs = r.pop("value")
     extra = r.pop("config_extra")
     out = {
-        "metric": (MLA_METRIC if args.config == "attn_mla" else ATTN_METRIC) if attention else METRIC,
+        "metric": ((MLA_METRIC if args.config == "attn_mla" else ATTN_METRIC) if attention
+                   else DIRECT_METRIC if args.config == "c2direct" else METRIC),
         "value": gbs,
         "unit": "GB/s",
         "n_gpus": 1,
@@ -820,14 +977,16 @@ def main():
         out["metric"] = "device streaming ceilings: contiguous copy GB/s (read, write alongside)"
     elif not args.no_cpu_baseline:
         log("cpu baseline (oracle, 1 thread)")
+        direct = args.config == "c2direct"
         out["cpu_baseline"] = (attention_cpu_baseline(args.cpu_seconds, args.config)
-                               if attention else cpu_baseline(makers[args.config], args.cpu_seconds))
+                               if attention else cpu_baseline(makers[args.config], args.cpu_seconds,
+                                                              direct=direct))
         if not attention and args.cpu_threads > 1:
             # The same sample on the box's host share of cores, beside the
             # single-thread figure.
             log(f"cpu baseline (oracle, {args.cpu_threads} threads)")
             out["cpu_baseline_all_cores"] = cpu_baseline(makers[args.config], args.cpu_seconds,
-                                                         threads=args.cpu_threads)
+                                                         threads=args.cpu_threads, direct=direct)
     print(json.dumps(out), flush=True)
 
 

@@ -359,6 +359,13 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
             which = 5;
             lds = narrow;
             threads = 64 * SGLKV_ATTN_WIDE_WAVES;
+        } else if (p.dk > 512 && p.dk <= 576 && p.dv == 512 &&
+                   SGLKV_ATTN_LATENT_LDS_BYTES <= (unsigned)ctx->max_lds_per_block) {
+            // MLA's latent rows (K 576 = 512 + 64 rope dims, V 512): 32 heads
+            // per wave, rows loaded straight into LDS.
+            which = 6;
+            lds = SGLKV_ATTN_LATENT_LDS_BYTES;
+            threads = 64 * SGLKV_ATTN_LATENT_WAVES;
         } else if (p.dk_pad <= 576 && p.dv <= 512 && wide <= (unsigned)ctx->max_lds_per_block) {
             which = 4;
             lds = wide;
@@ -376,7 +383,8 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
     // launch fills every CU with as many workgroups as stay resident at
     // once (the kernel's occupancy at this LDS size), in one round.
     const bool wide = which >= 4;
-    const uint64_t hblocks = (p.head_groups + SGLKV_ATTN_WIDE_GROUPS - 1) / SGLKV_ATTN_WIDE_GROUPS;
+    const uint64_t hblocks = which == 6 ? ceil_div(p.group, SGLKV_ATTN_LATENT_HEADS)
+                                        : (p.head_groups + SGLKV_ATTN_WIDE_GROUPS - 1) / SGLKV_ATTN_WIDE_GROUPS;
     uint64_t base = c.query_count;
     if (mul_ovf(base, p.kv_heads, &base) || (wide && mul_ovf(base, hblocks, &base)) ||
         (!wide && (mul_ovf(base, p.head_groups, &base) || mul_ovf(base, p.dv_blocks, &base))) ||
@@ -409,7 +417,7 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
     if (splits > 1) {
         uint64_t bytes;
         if (mul_ovf(c.query_count * c.query_head_count, splits, &bytes) ||
-            mul_ovf(bytes, (uint64_t)p.dv + 2, &bytes) || mul_ovf(bytes, 4, &bytes))
+            mul_ovf(bytes, (uint64_t)SGLKV_ATTN_REC(p.dv), &bytes) || mul_ovf(bytes, 4, &bytes))
             return attn_overflow();
         if (bytes > ctx->attention_partial_bytes) {
             if (ctx->attention_partial) {

@@ -21,13 +21,15 @@
 //  - long sequences are split over gridDim.y (flash-decoding): each split
 //    writes (max, sum, unnormalised output) and a combine kernel merges
 //    them, so a small batch still fills 256 CUs.
-// Three bodies share this math. The pipelined one (head dims up to 128,
+// Four bodies share this math. The pipelined one (head dims up to 128,
 // 16-byte rows, power-of-two pages: every Llama/Qwen-style decode) loads
 // the slots of block i+2 and the K/V rows of block i+1 while it computes
 // block i, so a wave never waits on the dependent slot -> row loads; the
-// wide one (many query heads per KV head, MLA widths) stages each block
-// once in LDS for up to 64 heads; the generic one serves every other shape
-// (odd dims, unaligned rows) one block at a time.
+// latent one (MLA: K rows up to 576 dims, V rows of 512) loads each block
+// straight into LDS once for up to 128 heads; the wide one (other shapes
+// with many query heads per KV head) stages each block once in LDS for up
+// to 64 heads; the generic one serves every other shape (odd dims,
+// unaligned rows) one block at a time.
 // Metadata errors set the device error word (SGLKV_FLAG_ATTN_*) and skip
 // the query, as the reference's kernel does.
 
@@ -243,7 +245,7 @@ __device__ __forceinline__ void attn_finish(const sglkv_attn_params &p, const at
             }
         }
     } else {
-        const uint64_t rec = p.dv + 2;
+        const uint64_t rec = SGLKV_ATTN_REC(p.dv);
         if (w.dblk == 0 && g == 0 && r < w.nh) {
             float *pr = p.partial + ((w.q * p.query_heads + w.h0 + r) * p.splits + w.split) * rec;
             pr[0] = st.m_run;
@@ -257,7 +259,7 @@ __device__ __forceinline__ void attn_finish(const sglkv_attn_params &p, const at
             for (uint32_t e = 0; e < 4; ++e) {
                 const uint32_t h = 4 * g + e;
                 if (h < w.nh)
-                    p.partial[((w.q * p.query_heads + w.h0 + h) * p.splits + w.split) * rec + 2 + dim] =
+                    p.partial[((w.q * p.query_heads + w.h0 + h) * p.splits + w.split) * rec + 4 + dim] =
                         st.o[j][e];
             }
         }
@@ -1011,6 +1013,464 @@ __device__ __forceinline__ void attn_wide_body(const sglkv_attn_params &p) {
     if (active) attn_finish<G::NJH>(p, w, g, r, st);
 }
 
+// ---- Latent body: MLA decode, 32 query heads per wave ----
+//
+// For MLA's shape (K rows of 576 dims, V rows of 512, 128 query heads over
+// one KV head) the wide body's two waves per 16-head group read every staged
+// K and V byte once per 16 heads, and its staging registers leave room for
+// little LDS read-ahead. Here a workgroup of four waves (one per SIMD) owns
+// (query, KV head, up to 128 query heads, split) and wave w serves heads
+// 32w .. 32w+31 with v_mfma_f32_32x32x16_bf16, so LDS is read once per 32
+// heads:
+//  - q.k: S[token][head] = K (A operand: lane l holds token l%32, dims
+//    8(l/32) .. +7 of each 16-dim step, read from LDS) x Q^T (B operand: the
+//    lane's head, 36 steps of 8 dims held in 144 VGPRs). S comes out with
+//    lane l holding head l%32 and tokens 8(r/4) + 4(l/32) + r%4, r < 16.
+//  - p.v: O[head][dim] += P (A operand) x V (B operand). P's k index
+//    8(l/32) + i of step s is token 16s + 4(l/32) + i (i < 4) or
+//    16s + 8 + 4(l/32) + i - 4, exactly the tokens S left in the lane, so P
+//    needs no lane movement. V's B operand comes from two transposing LDS
+//    reads (ds_read_b64_tr_b16) per tile, lane (16c + L) of each half-wave
+//    addressing token 4(l/32) + L/4 (+8), dims 16c + 4(L%4) of the 32-dim
+//    tile. O is 16 tiles of 16 floats: 256 accumulator registers.
+//  - K and V rows go from HBM straight into LDS (global_load_lds_dwordx4:
+//    lane i's 16 bytes land at M0 + 16 i), so no staging register holds
+//    them. A K row's dims [0, 512) are one such load into a row of 1,040
+//    bytes (rows 4 banks apart: the q.k reads of 16 tokens hit 64 distinct
+//    banks); dims [512, 576) of 8 rows are one load into rows of 128 bytes,
+//    piece i of row t stored at (i ^ (t/2 % 8)) so that the q.k reads are
+//    conflict-free there too. A V row is one load into a row of 1,088
+//    bytes (16 banks apart: the transposing reads of a half-wave cover 64
+//    distinct banks). Each wave loads 8 of a block's 32 rows.
+//  - Pipeline: two K stages and two V stages. Iteration k waits for K(k)
+//    (barrier A), issues V(k+1) into the other V stage, runs q.k, waits for
+//    V(k) (barrier B), issues K(k+2) into the K stage q.k has just read, and
+//    runs softmax and p.v. The barriers wait for the wave's older loads only
+//    (s_waitcnt vmcnt(17): the newest K and V issues stay in flight), so up
+//    to three blocks' rows are in flight; every issue is the same 9 (K) or
+//    8 (V) loads, blocks past the chunk reading the zero row, so the counts
+//    hold.
+//  - Softmax with the wide body's fixed reference: the first valid block
+//    fixes each head's reference maximum and p = 2^(x - m) after it, so the
+//    loop never touches O outside the MFMAs. If a block outruns the
+//    reference by more than SGLKV_ATTN_FIXED_MAX_LOG2, the workgroup runs
+//    the split again twice: once for each head's true maximum (q.k only),
+//    then in full with that maximum as the reference.
+
+typedef float sglkv_f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr uint32_t kLatB = SGLKV_ATTN_TOKENS;
+constexpr uint32_t kLatThreads = 64 * SGLKV_ATTN_LATENT_WAVES;
+constexpr uint32_t kLatKSteps = 36;                             // 16-dim q.k steps over 576 dims
+constexpr uint32_t kLatNT = 16;                                 // 32-dim p.v tiles over 512 dims
+constexpr uint32_t kLatKP = 1040, kLatTP = 128, kLatVP = 1088;  // LDS row pitches (bytes)
+constexpr uint32_t kLatKMain = kLatB * kLatKP;
+constexpr uint32_t kLatK = SGLKV_ATTN_LATENT_KSTAGE, kLatV = SGLKV_ATTN_LATENT_VSTAGE;
+constexpr uint32_t kLatLoadsK = 9, kLatLoadsV = 8;  // loads one wave issues per block
+constexpr uint32_t kLatAhead = 4;                   // MFMA steps the LDS reads run ahead
+static_assert(kLatKMain + kLatB * kLatTP == kLatK && kLatB * kLatVP == kLatV, "stage layout");
+static_assert(kLatB == 8 * SGLKV_ATTN_LATENT_WAVES && SGLKV_ATTN_LATENT_HEADS == 32 * SGLKV_ATTN_LATENT_WAVES,
+              "8 rows and 32 heads per wave");
+static_assert(SGLKV_ATTN_LATENT_LDS_BYTES == 2 * (kLatK + kLatV) + 4 * SGLKV_ATTN_WIDE_SLOTS + 16,
+              "the host sizes the same LDS");
+
+__device__ __forceinline__ sglkv_f32x16 attn_mfma32(sglkv_u16x8 a, sglkv_u16x8 b, sglkv_f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(attn_as_bf16(a), attn_as_bf16(b), c, 0, 0, 0);
+}
+
+// Row loads into LDS: global_load_lds_dwordx4 takes the LDS address from
+// M0 and puts lane i's 16 bytes at M0 + 16 i. They are written out rather
+// than through the compiler's builtin, which makes every later LDS read that
+// it cannot prove disjoint wait for all such loads in flight (vmcnt(0)); the
+// barriers of the latent body do the waiting instead.
+__device__ __forceinline__ uint32_t attn_lat_lds_at(const uint8_t *dst) {
+    // dst is uniform (wave-indexed); readfirstlane tells the compiler so.
+    return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(
+        reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) uint8_t *)dst)));
+}
+
+// 16 bytes at src (per lane) into LDS at dst + 16 * lane.
+__device__ __forceinline__ void attn_lat_load(uint64_t src, const uint8_t *dst) {
+    uint32_t save;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+        : "=&s"(save)
+        : "v"(src), "s"(attn_lat_lds_at(dst)));
+}
+
+// Eight rows: row i's 1 KiB from a[i] (the same in every lane; lane l's 16
+// bytes at a[i] + 16 l) into LDS at at + i * PITCH. The leading s_nop 4
+// covers a VALU (readlane) write of a[i] just before; each M0 write is one
+// wait state ahead of the load that reads it.
+template <uint32_t PITCH>
+__device__ __forceinline__ void attn_lat_load8(const uint64_t (&a)[8], uint32_t at) {
+    uint32_t save;
+    asm volatile(
+        "s_nop 4\n\ts_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %3\n\t"
+        "s_add_u32 m0, %2, %11\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %4\n\t"
+        "s_add_u32 m0, %2, %12\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %5\n\t"
+        "s_add_u32 m0, %2, %13\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %6\n\t"
+        "s_add_u32 m0, %2, %14\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %7\n\t"
+        "s_add_u32 m0, %2, %15\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %8\n\t"
+        "s_add_u32 m0, %2, %16\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %9\n\t"
+        "s_add_u32 m0, %2, %17\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %10\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(save)
+        : "v"(16 * (threadIdx.x & 63)), "s"(at), "s"(a[0]), "s"(a[1]), "s"(a[2]), "s"(a[3]), "s"(a[4]), "s"(a[5]),
+          "s"(a[6]), "s"(a[7]), "n"(PITCH), "n"(2 * PITCH), "n"(3 * PITCH), "n"(4 * PITCH), "n"(5 * PITCH),
+          "n"(6 * PITCH), "n"(7 * PITCH)
+        : "scc");
+}
+
+__device__ __forceinline__ uint64_t attn_lat_row(const sglkv_attn_params &p, uint64_t base, uint32_t s,
+                                                 uint32_t stride) {
+    return base + static_cast<uint64_t>(s >> p.page_shift) * p.page_stride32 +
+           static_cast<uint64_t>(s & ((1u << p.page_shift) - 1)) * stride;
+}
+
+// Row address of the token whose slot is s (the zero row for an invalid
+// slot or a block past the chunk).
+__device__ __forceinline__ uint64_t attn_lat_row_or_zero(const sglkv_attn_params &p, uint64_t base, uint32_t s,
+                                                         uint32_t stride, bool live) {
+    return live && s != kAttnInvalidSlot ? attn_lat_row(p, base, s, stride) : reinterpret_cast<uint64_t>(p.zero_row);
+}
+
+// Lane i's 64-bit value for i < 8, in SGPRs. (readlane returns int: each
+// half goes through uint32_t so that the low half is not sign-extended.)
+__device__ __forceinline__ void attn_lat_lanes8(uint64_t v, uint64_t (&a)[8]) {
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) {
+        const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), i));
+        const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v >> 32), i));
+        a[i] = static_cast<uint64_t>(lo) | static_cast<uint64_t>(hi) << 32;
+    }
+}
+
+// Waits until at most N of this wave's vector-memory loads are in flight
+// and its LDS reads are done, then joins the workgroup barrier.
+template <int N>
+__device__ __forceinline__ void attn_lat_barrier() {
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// Wave w's 9 loads of a block's K rows (slots sl; live false: a block past
+// the chunk, every lane reads the zero row): rows 8w + i, dims [0, 512) at
+// kst + row * 1040 (the host requires dk > 512, so every lane is inside the
+// row), and the tail dims of rows 8w .. 8w+7 at kst + 32 * 1040 + 1024 w
+// (lane i: row 8w + i/8, piece (i%8) ^ (row/2 % 8)), zeros at or past dk.
+// Lanes 0..7 work out the eight row addresses at once.
+__device__ __forceinline__ void attn_lat_issue_k(const sglkv_attn_params &p, uint64_t kbase, const uint32_t *sl,
+                                                 bool live, uint32_t w, uint32_t lane, uint8_t *kst) {
+    uint64_t a[8];
+    attn_lat_lanes8(attn_lat_row_or_zero(p, kbase, sl[8 * w + (lane & 7)], p.key_token_stride32, live), a);
+    attn_lat_load8<kLatKP>(a, attn_lat_lds_at(kst + 8 * w * kLatKP));
+    const uint32_t t = 8 * w + (lane >> 3), piece = (lane & 7) ^ ((t >> 1) & 7);
+    const uint32_t st = sl[t];
+    const bool ok = live && st != kAttnInvalidSlot && 512 + 8 * piece < p.dk;
+    const uint64_t src = ok ? attn_lat_row(p, kbase, st, p.key_token_stride32) + 1024 + 16 * piece
+                            : reinterpret_cast<uint64_t>(p.zero_row) + 16 * (lane & 7);
+    attn_lat_load(src, kst + kLatKMain + 1024 * w);
+}
+
+// Wave w's 8 loads of a block's V rows: row 8w + i at vst + row * 1088
+// (the host requires dv = 512: every lane is inside the row).
+__device__ __forceinline__ void attn_lat_issue_v(const sglkv_attn_params &p, uint64_t vbase, const uint32_t *sl,
+                                                 bool live, uint32_t w, uint32_t lane, uint8_t *vst) {
+    uint64_t a[8];
+    attn_lat_lanes8(attn_lat_row_or_zero(p, vbase, sl[8 * w + (lane & 7)], p.value_token_stride32, live), a);
+    attn_lat_load8<kLatVP>(a, attn_lat_lds_at(vst + 8 * w * kLatVP));
+}
+
+// q.k MFMAs with the scores in VGPRs. The compiler gives every MFMA it
+// emits an accumulator in the same register file, and the 256 AGPRs are
+// exactly o's, so these are written out: c = a x b (+ c). The compiler's
+// hazard checks do not look inside them: the chain's first starts with 3
+// wait states (a VALU write of a or b just before needs 2; between the
+// chain's MFMAs there are only LDS reads), and its last adds 20 (an 8-pass
+// 32x32 MFMA needs 18 before another instruction reads c). The chain reads
+// its own previous result as the accumulator, which the hardware forwards.
+__device__ __forceinline__ void attn_lat_mfma_first(sglkv_f32x16 &c, sglkv_u16x8 a, sglkv_u16x8 b) {
+    asm("s_nop 2\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(c) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void attn_lat_mfma_next(sglkv_f32x16 &c, sglkv_u16x8 a, sglkv_u16x8 b) {
+    asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void attn_lat_mfma_last(sglkv_f32x16 &c, sglkv_u16x8 a, sglkv_u16x8 b) {
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7\n\ts_nop 3"
+                 : "+v"(c)
+                 : "v"(a), "v"(b));
+}
+
+// q.k of the staged block: lane l gets head l%32's scores of tokens
+// 8(r/4) + 4(l/32) + r%4 in s[r].
+__device__ __forceinline__ sglkv_f32x16 attn_lat_qk(const uint8_t *kst, const sglkv_u16x8 (&qf)[kLatKSteps],
+                                                    uint32_t lane) {
+    const uint32_t t = lane & 31, h = lane >> 5, sw = (t >> 1) & 7;
+    const uint8_t *ka = kst + t * kLatKP + 16 * h;
+    const uint8_t *ta = kst + kLatKMain + t * kLatTP;
+    auto kread = [&](uint32_t c) {
+        return *reinterpret_cast<const sglkv_u16x8 *>(c < 32 ? ka + 32 * c : ta + 16 * ((2 * (c - 32) + h) ^ sw));
+    };
+    // The reads run kLatAhead steps ahead of the MFMAs that use them.
+    sglkv_u16x8 kf[kLatAhead];
+#pragma unroll
+    for (uint32_t c = 0; c < kLatAhead; ++c) kf[c] = kread(c);
+    sglkv_f32x16 s;
+#pragma unroll
+    for (uint32_t c = 0; c < kLatKSteps; ++c) {
+        // sched_barrier(0): the scheduler keeps this order (it would sink
+        // each read next to its MFMA otherwise).
+        __builtin_amdgcn_sched_barrier(0);
+        const sglkv_u16x8 a = kf[c % kLatAhead];
+        if (c + kLatAhead < kLatKSteps) kf[c % kLatAhead] = kread(c + kLatAhead);
+        if (c == 0)
+            attn_lat_mfma_first(s, a, qf[c]);
+        else if (c + 1 < kLatKSteps)
+            attn_lat_mfma_next(s, a, qf[c]);
+        else
+            attn_lat_mfma_last(s, a, qf[c]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    return s;
+}
+
+__device__ __forceinline__ attn_i16x4 attn_lat_vtr(const uint8_t *at) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) attn_i16x4 *)(reinterpret_cast<uintptr_t>(at)));
+}
+
+// o += P x V over the staged block (pa: the probabilities, bf16, as the A
+// operand of the two 16-token steps). MFMA j is tile j/2, step j%2; its B
+// operand's two transposing reads run kLatAhead MFMAs ahead.
+__device__ __forceinline__ void attn_lat_pv(const uint8_t *vst, const sglkv_u16x8 (&pa)[2],
+                                            sglkv_f32x16 (&o)[kLatNT], uint32_t lane) {
+    const uint32_t L = lane & 15, c = (lane >> 4) & 1, h = lane >> 5;
+    const uint8_t *va = vst + (4 * h + (L >> 2)) * kLatVP + 32 * c + 8 * (L & 3);
+    auto vread = [&](uint32_t j) {
+        const uint8_t *at = va + 16 * (j & 1) * kLatVP + 64 * (j >> 1);
+        const attn_i16x4 lo = attn_lat_vtr(at), hi = attn_lat_vtr(at + 8 * kLatVP);
+        return sglkv_u16x8{(uint16_t)lo[0], (uint16_t)lo[1], (uint16_t)lo[2], (uint16_t)lo[3],
+                           (uint16_t)hi[0], (uint16_t)hi[1], (uint16_t)hi[2], (uint16_t)hi[3]};
+    };
+    sglkv_u16x8 vf[kLatAhead];
+#pragma unroll
+    for (uint32_t j = 0; j < kLatAhead; ++j) vf[j] = vread(j);
+#pragma unroll
+    for (uint32_t j = 0; j < 2 * kLatNT; ++j) {
+        __builtin_amdgcn_sched_barrier(0);
+        const sglkv_u16x8 b = vf[j % kLatAhead];
+        if (j + kLatAhead < 2 * kLatNT) vf[j % kLatAhead] = vread(j + kLatAhead);
+        o[j >> 1] = attn_mfma32(pa[j & 1], b, o[j >> 1]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// Scores of the lane's 16 tokens in log2 units (-inf where the token is
+// invalid: bit t of vm clear) and their maximum over the head's 32 tokens.
+__device__ __forceinline__ float attn_lat_scores(const sglkv_attn_params &p, const sglkv_f32x16 &s, uint64_t vm,
+                                                 uint32_t lane, float (&x)[16]) {
+    const uint32_t h = lane >> 5;
+    float mx = -INFINITY;
+    if (static_cast<uint32_t>(vm) == 0xFFFFFFFFu) {  // every token valid (the same in every lane)
+#pragma unroll
+        for (uint32_t r = 0; r < 16; ++r) {
+            x[r] = s[r] * p.scale_log2;
+            mx = fmaxf(mx, x[r]);
+        }
+    } else {
+#pragma unroll
+        for (uint32_t r = 0; r < 16; ++r) {
+            const uint32_t tok = 8 * (r >> 2) + 4 * h + (r & 3);
+            x[r] = ((vm >> tok) & 1) ? s[r] * p.scale_log2 : -INFINITY;
+            mx = fmaxf(mx, x[r]);
+        }
+    }
+    return fmaxf(mx, __shfl_xor(mx, 32));
+}
+
+// Validity of the block's 32 tokens (bit t), from its slots.
+__device__ __forceinline__ uint64_t attn_lat_valid(const uint32_t *sl, uint32_t lane) {
+    return __ballot(sl[lane & 31] != kAttnInvalidSlot);
+}
+
+// Softmax of one block against the fixed reference m_run (set by the first
+// valid block), l_part += the lane's p, pa = p in bf16; *over when the
+// block's maximum passes the reference by more than the bound.
+__device__ __forceinline__ void attn_lat_softmax(const sglkv_attn_params &p, const sglkv_f32x16 &s, uint64_t vm,
+                                                 uint32_t lane, float &m_run, float &l_part,
+                                                 sglkv_u16x8 (&pa)[2], bool &over) {
+    float x[16];
+    const float mx = attn_lat_scores(p, s, vm, lane, x);
+    if (m_run == -INFINITY) m_run = mx;
+    const float m_ref = m_run == -INFINITY ? 0.0f : m_run;
+    over = over || mx > m_ref + SGLKV_ATTN_FIXED_MAX_LOG2;
+    float psum = 0.0f;
+#pragma unroll
+    for (uint32_t r = 0; r < 16; ++r) {
+        // v_exp_f32: 2^y, 0 below the normal range (x = -inf for an invalid
+        // token gives exactly 0).
+        const float pr = __builtin_amdgcn_exp2f(fminf(x[r] - m_ref, SGLKV_ATTN_FIXED_MAX_LOG2));
+        psum += pr;
+        pa[r >> 3][r & 7] = attn_to_bf16(pr);
+    }
+    l_part += psum;
+}
+
+__device__ __forceinline__ void attn_latent_body(const sglkv_attn_params &p) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t attn_lat_lds[];
+    uint8_t *const k0 = attn_lat_lds, *const k1 = attn_lat_lds + kLatK;
+    uint8_t *const v0 = attn_lat_lds + 2 * kLatK, *const v1 = v0 + kLatV;
+    uint32_t *slots = reinterpret_cast<uint32_t *>(attn_lat_lds + 2 * (kLatK + kLatV));
+    uint32_t *redo = slots + SGLKV_ATTN_WIDE_SLOTS;
+    // w through readfirstlane: the compiler then keeps what derives from it
+    // (head range, LDS row addresses) in SGPRs rather than in every lane.
+    const uint32_t tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    // Workgroup -> (query, KV head, block of 128 query heads), split.
+    const uint32_t hblocks = (p.group + SGLKV_ATTN_LATENT_HEADS - 1) / SGLKV_ATTN_LATENT_HEADS;
+    uint64_t bx = blockIdx.x;
+    const uint64_t q = bx % p.query_count;
+    bx /= p.query_count;
+    const uint32_t kvh = static_cast<uint32_t>(bx % p.kv_heads);
+    const uint32_t hb = static_cast<uint32_t>(bx / p.kv_heads);
+    const uint32_t split = blockIdx.y;
+    uint64_t start = 0, len = 0;
+    if (!attn_metadata(p, q, tid == 0 && split == 0 && hb == 0 && kvh == 0, &start, &len)) return;
+    const uint64_t t0 = static_cast<uint64_t>(split) * p.chunk_tokens;
+    if (t0 >= len || hb >= hblocks) return;
+    const uint64_t t1 = len < t0 + p.chunk_tokens ? len : t0 + p.chunk_tokens;
+    const uint32_t nb = static_cast<uint32_t>((t1 - t0 + kLatB - 1) / kLatB);  // <= SLOTS / B (host bound)
+    const uint32_t hw = hb * SGLKV_ATTN_LATENT_HEADS + 32 * w;  // the wave's first head in the KV group
+    const uint32_t nh = hw >= p.group ? 0 : (p.group - hw < 32 ? p.group - hw : 32);
+    const bool active = nh > 0;
+    const uint64_t h0 = static_cast<uint64_t>(kvh) * p.group + hw;
+
+    // Queries: lane l holds head l%32, dims 16c + 8(l/32) .. +7 of step c.
+    sglkv_u16x8 qf[kLatKSteps];
+#pragma unroll
+    for (uint32_t c = 0; c < kLatKSteps; ++c) {
+        const uint32_t d = 16 * c + 8 * (lane >> 5);
+        qf[c] = sglkv_u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        if ((lane & 31) < nh && d < p.dk)
+            qf[c] = *reinterpret_cast<const sglkv_u16x8 *>(p.queries + (q * p.query_heads + h0 + (lane & 31)) * p.dk + d);
+    }
+    if (tid == 0) *redo = 0;
+    for (uint32_t i = tid; i < nb * kLatB; i += kLatThreads) {
+        const uint64_t tok = t0 + i;
+        slots[i] = attn_wide_slot(p, tok < t1 ? p.sequence_slots[start + tok] : 0, tok, t1);
+    }
+    __syncthreads();
+
+    // The query loads are complete before the row loads start: the loop's
+    // waits count the row loads alone (s_waitcnt vmcnt(0), lgkmcnt and
+    // expcnt left at their maxima).
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+
+    const uint64_t pool = reinterpret_cast<uint64_t>(p.pool);
+    const uint64_t kbase = pool + p.key_offset + kvh * p.key_head_stride;
+    const uint64_t vbase = pool + p.value_offset + kvh * p.value_head_stride;
+    auto blk = [&](uint32_t b) { return slots + (b < nb ? b : nb - 1) * kLatB; };
+
+    sglkv_f32x16 o[kLatNT];
+#pragma unroll
+    for (uint32_t n = 0; n < kLatNT; ++n) o[n] = sglkv_f32x16{};
+    float m_run = -INFINITY, l_part = 0.0f;
+    bool over = false;
+
+    attn_lat_issue_k(p, kbase, blk(0), true, w, lane, k0);
+    attn_lat_issue_v(p, vbase, blk(0), true, w, lane, v0);
+    attn_lat_issue_k(p, kbase, blk(1), 1 < nb, w, lane, k1);
+    // Iteration k with stages (kc, vc) holding block k; (vn) takes block
+    // k+1's V rows, kc block k+2's K rows.
+    // Iteration k: stages kc and vc hold block k; vn takes block k+1's V
+    // rows, kc (once q.k has read it) block k+2's K rows. A wave without
+    // heads runs the loop on zero queries and writes nothing, so the loop
+    // has no branch around the accumulators.
+    for (uint32_t k = 0; k < nb; ++k) {
+        uint8_t *const kc = (k & 1) ? k1 : k0;
+        uint8_t *const vc = (k & 1) ? v1 : v0;
+        uint8_t *const vn = (k & 1) ? v0 : v1;
+        attn_lat_barrier<kLatLoadsK + kLatLoadsV>();  // K(k) in LDS; p.v(k-1) done
+        attn_lat_issue_v(p, vbase, blk(k + 1), k + 1 < nb, w, lane, vn);
+        const sglkv_f32x16 s = attn_lat_qk(kc, qf, lane);
+        attn_lat_barrier<kLatLoadsV + kLatLoadsK>();  // V(k) in LDS; q.k(k) done
+        attn_lat_issue_k(p, kbase, blk(k + 2), k + 2 < nb, w, lane, kc);
+        sglkv_u16x8 pa[2];
+        attn_lat_softmax(p, s, attn_lat_valid(blk(k), lane), lane, m_run, l_part, pa, over);
+        attn_lat_pv(vc, pa, o, lane);
+    }
+    // Every row load (the zero rows issued past the chunk too) has landed:
+    // __syncthreads would not wait for them (its fence orders LDS and
+    // stores, and the compiler does not see these loads).
+    attn_lat_barrier<0>();
+    if (active && __any(over) && lane == 0) *redo = 1;
+    __syncthreads();
+    if (*redo) {
+        // A block outran the fixed reference: each head's true maximum over
+        // the split (q.k only), then the split again with that maximum as
+        // the reference, which no block can outrun.
+        float m_true = -INFINITY;
+        for (uint32_t k = 0; k < nb; ++k) {
+            attn_lat_issue_k(p, kbase, blk(k), true, w, lane, k0);
+            attn_lat_barrier<0>();
+            float x[16];
+            m_true = fmaxf(m_true,
+                           attn_lat_scores(p, attn_lat_qk(k0, qf, lane), attn_lat_valid(blk(k), lane), lane, x));
+            __syncthreads();
+        }
+#pragma unroll
+        for (uint32_t n = 0; n < kLatNT; ++n) o[n] = sglkv_f32x16{};
+        m_run = m_true;
+        l_part = 0.0f;
+        for (uint32_t k = 0; k < nb; ++k) {
+            attn_lat_issue_k(p, kbase, blk(k), true, w, lane, k0);
+            attn_lat_issue_v(p, vbase, blk(k), true, w, lane, v0);
+            attn_lat_barrier<0>();
+            sglkv_u16x8 pa[2];
+            attn_lat_softmax(p, attn_lat_qk(k0, qf, lane), attn_lat_valid(blk(k), lane), lane, m_run, l_part, pa,
+                             over);
+            attn_lat_pv(v0, pa, o, lane);
+            __syncthreads();
+        }
+    }
+    if (!active) return;
+    if (m_run == -INFINITY) m_run = -3.402823466e+38f;  // no valid token: the record's m as the other bodies leave it
+
+    // Output (one split) or the split record [m, l, o[0..dv)]: o[n][r] is
+    // head 8(r/4) + 4(l/32) + r%4, dim 32n + l%32; m and l of head l%32.
+    const float l_tot = l_part + __shfl_xor(l_part, 32);
+    const uint32_t hl = lane & 31, hh = lane >> 5;
+    if (p.splits == 1) {
+#pragma unroll
+        for (uint32_t r = 0; r < 16; ++r) {
+            const uint32_t head = 8 * (r >> 2) + 4 * hh + (r & 3);
+            const float linv = 1.0f / __shfl(l_tot, head);
+            if (head >= nh) continue;
+            uint16_t *out = p.output + (q * p.query_heads + h0 + head) * p.dv;
+#pragma unroll
+            for (uint32_t n = 0; n < kLatNT; ++n)
+                if (32 * n + hl < p.dv) out[32 * n + hl] = attn_to_bf16(o[n][r] * linv);
+        }
+    } else {
+        const uint64_t rec = SGLKV_ATTN_REC(p.dv);
+        if (hh == 0 && hl < nh) {
+            float *pr = p.partial + ((q * p.query_heads + h0 + hl) * p.splits + split) * rec;
+            pr[0] = m_run;
+            pr[1] = l_tot;
+        }
+#pragma unroll
+        for (uint32_t r = 0; r < 16; ++r) {
+            const uint32_t head = 8 * (r >> 2) + 4 * hh + (r & 3);
+            if (head >= nh) continue;
+            float *pr = p.partial + ((q * p.query_heads + h0 + head) * p.splits + split) * rec + 4;
+#pragma unroll
+            for (uint32_t n = 0; n < kLatNT; ++n)
+                if (32 * n + hl < p.dv) pr[32 * n + hl] = o[n][r];
+        }
+    }
+}
+
 }  // namespace
 
 extern "C" __global__ __launch_bounds__(64) void sglkv_paged_attention_v16(sglkv_attn_params p) {
@@ -1030,6 +1490,15 @@ extern "C" __global__ __launch_bounds__(512) void sglkv_paged_attention_wide128(
     attn_wide_body<4, 8>(p);
 }
 
+// MLA latent rows (K <= 576, V <= 512 dims), up to 128 query heads per
+// workgroup.
+extern "C" __global__ __launch_bounds__(256) void sglkv_paged_attention_latent(sglkv_attn_params p) {
+    // Naming an accumulator register keeps the compiler's MFMA accumulators
+    // in AGPRs (the 256 of o), leaving the VGPRs to the queries and scores.
+    asm volatile("" ::: "a0");
+    attn_latent_body(p);
+}
+
 // Head dims exactly 128 (no per-dim masks) / up to 128.
 extern "C" __global__ __launch_bounds__(64) void sglkv_paged_attention_pipe128(sglkv_attn_params p) {
     attn_pipe_body<true>(p);
@@ -1040,23 +1509,38 @@ extern "C" __global__ __launch_bounds__(64) void sglkv_paged_attention_pipe(sglk
 }
 
 // Merges the split records of one (query, head): m* = max m_s,
-// out = sum_s 2^(m_s - m*) o_s / sum_s 2^(m_s - m*) l_s.
+// out = sum_s 2^(m_s - m*) o_s / sum_s 2^(m_s - m*) l_s. Thread t handles
+// dims 4t .. 4t+3 (+512 ...), one 16-byte read per split record (records
+// keep o 16-byte aligned; dims past dv read the record's padding and are not
+// written).
 extern "C" __global__ __launch_bounds__(128) void sglkv_paged_attention_combine(sglkv_attn_params p) {
     const uint64_t q = blockIdx.x / p.query_heads;
     const uint32_t head = static_cast<uint32_t>(blockIdx.x % p.query_heads);
     uint64_t start = 0, len = 0;
     if (!attn_metadata(p, q, false, &start, &len)) return;
-    const uint64_t used = (len + p.chunk_tokens - 1) / p.chunk_tokens;
-    const uint64_t rec = p.dv + 2;
+    const uint32_t used = static_cast<uint32_t>((len + p.chunk_tokens - 1) / p.chunk_tokens);
+    const uint64_t rec = SGLKV_ATTN_REC(p.dv);
     const float *base = p.partial + (q * p.query_heads + head) * p.splits * rec;
     float m = -3.402823466e+38f;
-    for (uint64_t s = 0; s < used; ++s) m = fmaxf(m, base[s * rec]);
+    for (uint32_t s = 0; s < used; ++s) m = fmaxf(m, base[s * rec]);
     float l = 0.0f;
-    for (uint64_t s = 0; s < used; ++s) l += exp2f(base[s * rec] - m) * base[s * rec + 1];
+    for (uint32_t s = 0; s < used; ++s) l += exp2f(base[s * rec] - m) * base[s * rec + 1];
     const float linv = 1.0f / l;
-    for (uint32_t d = threadIdx.x; d < p.dv; d += 128) {
-        float acc = 0.0f;
-        for (uint64_t s = 0; s < used; ++s) acc += exp2f(base[s * rec] - m) * base[s * rec + 2 + d];
-        p.output[(q * p.query_heads + head) * p.dv + d] = attn_to_bf16(acc * linv);
+    uint16_t *out = p.output + (q * p.query_heads + head) * p.dv;
+    for (uint32_t d = 4 * threadIdx.x; d < p.dv; d += 512) {
+        float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 8
+        for (uint32_t s = 0; s < used; ++s) {
+            const float ws = exp2f(base[s * rec] - m);
+            const float4 v = *reinterpret_cast<const float4 *>(base + s * rec + 4 + d);
+            acc.x += ws * v.x;
+            acc.y += ws * v.y;
+            acc.z += ws * v.z;
+            acc.w += ws * v.w;
+        }
+        const float o4[4] = {acc.x, acc.y, acc.z, acc.w};
+#pragma unroll
+        for (uint32_t e = 0; e < 4; ++e)
+            if (d + e < p.dv) out[d + e] = attn_to_bf16(o4[e] * linv);
     }
 }

@@ -149,13 +149,16 @@ typedef struct sglkv_request_params {
  * SGLKV_ATTN_HEADS query heads, block of SGLKV_ATTN_DV value dims) for the
  * tokens [split * chunk_tokens, +chunk_tokens) of gridDim.y's split. With
  * one split it writes the output; otherwise it writes a partial record
- * (running max m in log2 units, sum l, unnormalised o[dv]) that the combine
- * kernel merges. */
+ * (running max m in log2 units, sum l, unnormalised o[dv]; the layout of
+ * SGLKV_ATTN_REC) that the combine kernel merges. */
 #define SGLKV_ATTN_TOKENS 32u   /* tokens per wave iteration */
 #define SGLKV_ATTN_HEADS 16u    /* query heads per workgroup (MFMA N) */
 #define SGLKV_ATTN_DV 128u      /* value dims per workgroup */
 #define SGLKV_ATTN_VT_STRIDE 40u /* u16 per transposed-V row in LDS (32 tokens + pad) */
 #define SGLKV_ATTN_MAX_DK 1024u /* query/key head dim limit (LDS-resident queries) */
+/* Floats per split record: m, l, two unused floats, then o[dv] padded to a
+ * multiple of 4, so that every record's o starts 16-byte aligned. */
+#define SGLKV_ATTN_REC(dv) (4u + (((dv) + 3u) & ~3u))
 /* The wide bodies (many query heads per KV head, e.g. MLA): a workgroup of
  * SGLKV_ATTN_WIDE_WAVES waves serves SGLKV_ATTN_WIDE_GROUPS groups of
  * SGLKV_ATTN_HEADS heads, two waves per group; K dims padded to 32*DKC, V
@@ -169,6 +172,18 @@ typedef struct sglkv_request_params {
 #define SGLKV_ATTN_WIDE_LDS_BYTES(DKC, NJ)                                                     \
     (2u * SGLKV_ATTN_TOKENS * ((32u * (DKC) + 8u) + (16u * (NJ) + 16u)) +                      \
      SGLKV_ATTN_WIDE_WAVES * 2u * 64u * 16u + 4u * SGLKV_ATTN_WIDE_SLOTS + 16u)
+/* The latent body (MLA decode: K rows up to 576 dims, V rows up to 512): a
+ * workgroup of SGLKV_ATTN_LATENT_WAVES waves serves up to
+ * SGLKV_ATTN_LATENT_HEADS query heads of one KV head, 32 per wave. Its LDS:
+ * two stages of a 32-token block's K rows (dims [0, 512) at a pitch of 1,040
+ * bytes, dims [512, 576) as 128-byte rows) and two of its V rows (pitch
+ * 1,088 bytes), the chunk's slot table and a flag. */
+#define SGLKV_ATTN_LATENT_WAVES 4u
+#define SGLKV_ATTN_LATENT_HEADS 128u
+#define SGLKV_ATTN_LATENT_KSTAGE (SGLKV_ATTN_TOKENS * (1040u + 128u))
+#define SGLKV_ATTN_LATENT_VSTAGE (SGLKV_ATTN_TOKENS * 1088u)
+#define SGLKV_ATTN_LATENT_LDS_BYTES                                                            \
+    (2u * (SGLKV_ATTN_LATENT_KSTAGE + SGLKV_ATTN_LATENT_VSTAGE) + 4u * SGLKV_ATTN_WIDE_SLOTS + 16u)
 
 typedef struct sglkv_attn_params {
     const uint16_t *queries;              /* bf16 [query][query_head][dk] */

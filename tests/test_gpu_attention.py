@@ -215,6 +215,25 @@ def test_mla_many_heads(k, qh, hnd):
     np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("H,qh,dk,hnd", [
+    (2, 256, 576, False),   # two KV heads, a full 128-head block each
+    (1, 160, 576, True),    # two head blocks, the second holding 32 heads
+    (1, 100, 544, False),   # the last wave with 4 heads; K rows with 32 of 64 tail dims
+])
+def test_latent_shapes(k, H, qh, dk, hnd):
+    """The latent body (V rows of 512, K rows of 520..576 dims) beyond
+    DeepSeek's exact shape: several KV heads, more than 128 query heads per
+    KV head, waves with fewer than 32 heads, and K rows whose last 64 dims
+    are only partly there (the rest must read as zeros)."""
+    rng = np.random.default_rng(qh + dk)
+    c = _Case(rng, P=64, L=2, H=H, dk=dk, dv=512, qh=qh, pages=80, layer=1, hnd=hnd)
+    lens, rso, slots = _random_batch(rng, 3, 1200, c.layout.slot_count)
+    q = _bf16_normal(rng, 3 * qh * dk).reshape(3, qh, dk)
+    _say(f"latent shape H={H} qh={qh} dk={dk} hnd={hnd} tokens={int(rso[-1])}")
+    got, want = c.run(k, q, np.arange(3), lens, rso, slots, 1.0 / math.sqrt(dk), max_len=1200)
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+
+
 @pytest.mark.parametrize("dk,dv,qh,hnd", [(576, 512, 32, False), (128, 128, 48, True)])
 def test_wide_reference_outrun(k, dk, dv, qh, hnd):
     """Queries 100 times larger spread the scores over hundreds of log2

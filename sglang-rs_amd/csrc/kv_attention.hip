@@ -1362,11 +1362,6 @@ __device__ __forceinline__ void attn_latent_body(const sglkv_attn_params &p) {
     }
     __syncthreads();
 
-    // The query loads are complete before the row loads start: the loop's
-    // waits count the row loads alone (s_waitcnt vmcnt(0), lgkmcnt and
-    // expcnt left at their maxima).
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-
     const uint64_t pool = reinterpret_cast<uint64_t>(p.pool);
     const uint64_t kbase = pool + p.key_offset + kvh * p.key_head_stride;
     const uint64_t vbase = pool + p.value_offset + kvh * p.value_head_stride;
@@ -1381,6 +1376,11 @@ __device__ __forceinline__ void attn_latent_body(const sglkv_attn_params &p) {
     attn_lat_issue_k(p, kbase, blk(0), true, w, lane, k0);
     attn_lat_issue_v(p, vbase, blk(0), true, w, lane, v0);
     attn_lat_issue_k(p, kbase, blk(1), 1 < nb, w, lane, k1);
+    // Every load so far (the queries, which the compiler tracks, and the
+    // first rows, which it does not) is complete before the loop, whose
+    // waits then count the row loads alone (s_waitcnt vmcnt(0), lgkmcnt and
+    // expcnt left at their maxima).
+    __builtin_amdgcn_s_waitcnt(0x0F70);
     // Iteration k with stages (kc, vc) holding block k; (vn) takes block
     // k+1's V rows, kc block k+2's K rows.
     // Iteration k: stages kc and vc hold block k; vn takes block k+1's V

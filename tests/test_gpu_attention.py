@@ -234,6 +234,20 @@ def test_latent_shapes(k, H, qh, dk, hnd):
     np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("qh,hnd", [(128, False), (72, True)])
+def test_latent_one_split(k, qh, hnd):
+    """MLA decode with sequences of at most 256 tokens: one split, so the
+    latent body writes the bf16 output itself (no split records, no
+    combine pass), with blocks past each sequence's end masked."""
+    rng = np.random.default_rng(qh + 7)
+    c = _Case(rng, P=64, L=2, H=1, dk=576, dv=512, qh=qh, pages=40, layer=0, hnd=hnd)
+    lens, rso, slots = _random_batch(rng, 9, 250, c.layout.slot_count)
+    q = _bf16_normal(rng, 9 * qh * 576).reshape(9, qh, 576)
+    _say(f"latent one split qh={qh} hnd={hnd} lens={lens.tolist()}")
+    got, want = c.run(k, q, np.arange(9), lens, rso, slots, 1.0 / math.sqrt(576), max_len=250)
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+
+
 @pytest.mark.parametrize("dk,dv,qh,hnd", [(576, 512, 32, False), (128, 128, 48, True)])
 def test_wide_reference_outrun(k, dk, dv, qh, hnd):
     """Queries 100 times larger spread the scores over hundreds of log2

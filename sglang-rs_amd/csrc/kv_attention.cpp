@@ -417,7 +417,7 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
     if (splits > 1) {
         uint64_t bytes;
         if (mul_ovf(c.query_count * c.query_head_count, splits, &bytes) ||
-            mul_ovf(bytes, (uint64_t)SGLKV_ATTN_REC(p.dv), &bytes) || mul_ovf(bytes, 4, &bytes))
+            mul_ovf(bytes, (uint64_t)SGLKV_ATTN_OPAD(p.dv) + 2, &bytes) || mul_ovf(bytes, 4, &bytes))
             return attn_overflow();
         if (bytes > ctx->attention_partial_bytes) {
             if (ctx->attention_partial) {

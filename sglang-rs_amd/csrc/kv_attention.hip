@@ -223,7 +223,16 @@ __device__ __forceinline__ void attn_softmax_pv(const sglkv_attn_params &p, uint
     __builtin_amdgcn_wave_barrier();
 }
 
-// Output (one split) or the split record [m, l, o[0..dv)].
+// Split record i = (q * query_heads + head) * splits + split: its o row
+// (SGLKV_ATTN_OPAD floats, 128-byte aligned) and its m, l pair.
+__device__ __forceinline__ float *attn_rec_o(const sglkv_attn_params &p, uint64_t i) {
+    return p.partial + i * SGLKV_ATTN_OPAD(p.dv);
+}
+__device__ __forceinline__ float *attn_rec_ml(const sglkv_attn_params &p, uint64_t i) {
+    return p.partial + p.query_count * p.query_heads * p.splits * SGLKV_ATTN_OPAD(p.dv) + 2 * i;
+}
+
+// Output (one split) or the split record (m, l, o[0..dv)).
 template <int NJ>
 __device__ __forceinline__ void attn_finish(const sglkv_attn_params &p, const attn_work &w, uint32_t g,
                                             uint32_t r, const attn_state_n<NJ> &st) {
@@ -245,9 +254,8 @@ __device__ __forceinline__ void attn_finish(const sglkv_attn_params &p, const at
             }
         }
     } else {
-        const uint64_t rec = SGLKV_ATTN_REC(p.dv);
         if (w.dblk == 0 && g == 0 && r < w.nh) {
-            float *pr = p.partial + ((w.q * p.query_heads + w.h0 + r) * p.splits + w.split) * rec;
+            float *pr = attn_rec_ml(p, (w.q * p.query_heads + w.h0 + r) * p.splits + w.split);
             pr[0] = st.m_run;
             pr[1] = l_tot;
         }
@@ -259,7 +267,7 @@ __device__ __forceinline__ void attn_finish(const sglkv_attn_params &p, const at
             for (uint32_t e = 0; e < 4; ++e) {
                 const uint32_t h = 4 * g + e;
                 if (h < w.nh)
-                    p.partial[((w.q * p.query_heads + w.h0 + h) * p.splits + w.split) * rec + 4 + dim] =
+                    attn_rec_o(p, (w.q * p.query_heads + w.h0 + h) * p.splits + w.split)[dim] =
                         st.o[j][e];
             }
         }
@@ -1453,9 +1461,8 @@ __device__ __forceinline__ void attn_latent_body(const sglkv_attn_params &p) {
                 if (32 * n + hl < p.dv) out[32 * n + hl] = attn_to_bf16(o[n][r] * linv);
         }
     } else {
-        const uint64_t rec = SGLKV_ATTN_REC(p.dv);
         if (hh == 0 && hl < nh) {
-            float *pr = p.partial + ((q * p.query_heads + h0 + hl) * p.splits + split) * rec;
+            float *pr = attn_rec_ml(p, (q * p.query_heads + h0 + hl) * p.splits + split);
             pr[0] = m_run;
             pr[1] = l_tot;
         }
@@ -1463,7 +1470,7 @@ __device__ __forceinline__ void attn_latent_body(const sglkv_attn_params &p) {
         for (uint32_t r = 0; r < 16; ++r) {
             const uint32_t head = 8 * (r >> 2) + 4 * hh + (r & 3);
             if (head >= nh) continue;
-            float *pr = p.partial + ((q * p.query_heads + h0 + head) * p.splits + split) * rec + 4;
+            float *pr = attn_rec_o(p, (q * p.query_heads + h0 + head) * p.splits + split);
 #pragma unroll
             for (uint32_t n = 0; n < kLatNT; ++n)
                 if (32 * n + hl < p.dv) pr[32 * n + hl] = o[n][r];
@@ -1510,8 +1517,8 @@ extern "C" __global__ __launch_bounds__(64) void sglkv_paged_attention_pipe(sglk
 
 // Merges the split records of one (query, head): m* = max m_s,
 // out = sum_s 2^(m_s - m*) o_s / sum_s 2^(m_s - m*) l_s. Thread t handles
-// dims 4t .. 4t+3 (+512 ...), one 16-byte read per split record (records
-// keep o 16-byte aligned; dims past dv read the record's padding and are not
+// dims 4t .. 4t+3 (+512 ...), one 16-byte read per split's o row (rows are
+// 128-byte aligned; dims past dv read the row's padding and are not
 // written).
 extern "C" __global__ __launch_bounds__(128) void sglkv_paged_attention_combine(sglkv_attn_params p) {
     const uint64_t q = blockIdx.x / p.query_heads;
@@ -1519,20 +1526,22 @@ extern "C" __global__ __launch_bounds__(128) void sglkv_paged_attention_combine(
     uint64_t start = 0, len = 0;
     if (!attn_metadata(p, q, false, &start, &len)) return;
     const uint32_t used = static_cast<uint32_t>((len + p.chunk_tokens - 1) / p.chunk_tokens);
-    const uint64_t rec = SGLKV_ATTN_REC(p.dv);
-    const float *base = p.partial + (q * p.query_heads + head) * p.splits * rec;
+    const uint64_t i0 = (q * p.query_heads + head) * p.splits;
+    const float *ml = attn_rec_ml(p, i0);
+    const float *o = attn_rec_o(p, i0);
+    const uint32_t opad = SGLKV_ATTN_OPAD(p.dv);
     float m = -3.402823466e+38f;
-    for (uint32_t s = 0; s < used; ++s) m = fmaxf(m, base[s * rec]);
+    for (uint32_t s = 0; s < used; ++s) m = fmaxf(m, ml[2 * s]);
     float l = 0.0f;
-    for (uint32_t s = 0; s < used; ++s) l += exp2f(base[s * rec] - m) * base[s * rec + 1];
+    for (uint32_t s = 0; s < used; ++s) l += exp2f(ml[2 * s] - m) * ml[2 * s + 1];
     const float linv = 1.0f / l;
     uint16_t *out = p.output + (q * p.query_heads + head) * p.dv;
     for (uint32_t d = 4 * threadIdx.x; d < p.dv; d += 512) {
         float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll 8
         for (uint32_t s = 0; s < used; ++s) {
-            const float ws = exp2f(base[s * rec] - m);
-            const float4 v = *reinterpret_cast<const float4 *>(base + s * rec + 4 + d);
+            const float ws = exp2f(ml[2 * s] - m);
+            const float4 v = *reinterpret_cast<const float4 *>(o + s * opad + d);
             acc.x += ws * v.x;
             acc.y += ws * v.y;
             acc.z += ws * v.z;

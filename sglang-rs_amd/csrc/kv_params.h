@@ -150,15 +150,17 @@ typedef struct sglkv_request_params {
  * tokens [split * chunk_tokens, +chunk_tokens) of gridDim.y's split. With
  * one split it writes the output; otherwise it writes a partial record
  * (running max m in log2 units, sum l, unnormalised o[dv]; the layout of
- * SGLKV_ATTN_REC) that the combine kernel merges. */
+ * SGLKV_ATTN_OPAD) that the combine kernel merges. */
 #define SGLKV_ATTN_TOKENS 32u   /* tokens per wave iteration */
 #define SGLKV_ATTN_HEADS 16u    /* query heads per workgroup (MFMA N) */
 #define SGLKV_ATTN_DV 128u      /* value dims per workgroup */
 #define SGLKV_ATTN_VT_STRIDE 40u /* u16 per transposed-V row in LDS (32 tokens + pad) */
 #define SGLKV_ATTN_MAX_DK 1024u /* query/key head dim limit (LDS-resident queries) */
-/* Floats per split record: m, l, two unused floats, then o[dv] padded to a
- * multiple of 4, so that every record's o starts 16-byte aligned. */
-#define SGLKV_ATTN_REC(dv) (4u + (((dv) + 3u) & ~3u))
+/* Split records: record i = (query * query_heads + head) * splits + split
+ * keeps its unnormalised o[dv] at partial + i * SGLKV_ATTN_OPAD(dv) floats
+ * (rows padded to whole 128-byte lines, so that the writes fill every line
+ * they touch) and its m, l at partial + records * SGLKV_ATTN_OPAD(dv) + 2 i. */
+#define SGLKV_ATTN_OPAD(dv) (((dv) + 31u) & ~31u)
 /* The wide bodies (many query heads per KV head, e.g. MLA): a workgroup of
  * SGLKV_ATTN_WIDE_WAVES waves serves SGLKV_ATTN_WIDE_GROUPS groups of
  * SGLKV_ATTN_HEADS heads, two waves per group; K dims padded to 32*DKC, V

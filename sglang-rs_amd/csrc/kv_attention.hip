@@ -224,7 +224,11 @@ __device__ __forceinline__ void attn_softmax_pv(const sglkv_attn_params &p, uint
 }
 
 // Split record i = (q * query_heads + head) * splits + split: its o row
-// (SGLKV_ATTN_OPAD floats, 128-byte aligned) and its m, l pair.
+// (SGLKV_ATTN_OPAD floats, 128-byte aligned) and its m, l pair. Records
+// are written with non-temporal stores: every workgroup writes its records
+// at its end, and streamed out so they do not pile up in L2 (measured on
+// the MLA decode: 12.5 us less per launch of the latent body, 1.4 us more
+// in the combine that reads them).
 __device__ __forceinline__ float *attn_rec_o(const sglkv_attn_params &p, uint64_t i) {
     return p.partial + i * SGLKV_ATTN_OPAD(p.dv);
 }
@@ -256,8 +260,8 @@ __device__ __forceinline__ void attn_finish(const sglkv_attn_params &p, const at
     } else {
         if (w.dblk == 0 && g == 0 && r < w.nh) {
             float *pr = attn_rec_ml(p, (w.q * p.query_heads + w.h0 + r) * p.splits + w.split);
-            pr[0] = st.m_run;
-            pr[1] = l_tot;
+            __builtin_nontemporal_store(st.m_run, pr);
+            __builtin_nontemporal_store(l_tot, pr + 1);
         }
 #pragma unroll
         for (uint32_t j = 0; j < NJ; ++j) {
@@ -267,8 +271,8 @@ __device__ __forceinline__ void attn_finish(const sglkv_attn_params &p, const at
             for (uint32_t e = 0; e < 4; ++e) {
                 const uint32_t h = 4 * g + e;
                 if (h < w.nh)
-                    attn_rec_o(p, (w.q * p.query_heads + w.h0 + h) * p.splits + w.split)[dim] =
-                        st.o[j][e];
+                    __builtin_nontemporal_store(
+                        st.o[j][e], attn_rec_o(p, (w.q * p.query_heads + w.h0 + h) * p.splits + w.split) + dim);
             }
         }
     }
@@ -1463,8 +1467,8 @@ __device__ __forceinline__ void attn_latent_body(const sglkv_attn_params &p) {
     } else {
         if (hh == 0 && hl < nh) {
             float *pr = attn_rec_ml(p, (q * p.query_heads + h0 + hl) * p.splits + split);
-            pr[0] = m_run;
-            pr[1] = l_tot;
+            __builtin_nontemporal_store(m_run, pr);
+            __builtin_nontemporal_store(l_tot, pr + 1);
         }
 #pragma unroll
         for (uint32_t r = 0; r < 16; ++r) {
@@ -1473,7 +1477,7 @@ __device__ __forceinline__ void attn_latent_body(const sglkv_attn_params &p) {
             float *pr = attn_rec_o(p, (q * p.query_heads + h0 + head) * p.splits + split);
 #pragma unroll
             for (uint32_t n = 0; n < kLatNT; ++n)
-                if (32 * n + hl < p.dv) pr[32 * n + hl] = o[n][r];
+                if (32 * n + hl < p.dv) __builtin_nontemporal_store(o[n][r], pr + 32 * n + hl);
         }
     }
 }

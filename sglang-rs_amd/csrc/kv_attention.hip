@@ -1094,7 +1094,9 @@ __device__ __forceinline__ sglkv_f32x16 attn_mfma32(sglkv_u16x8 a, sglkv_u16x8 b
 // M0 and puts lane i's 16 bytes at M0 + 16 i. They are written out rather
 // than through the compiler's builtin, which makes every later LDS read that
 // it cannot prove disjoint wait for all such loads in flight (vmcnt(0)); the
-// barriers of the latent body do the waiting instead.
+// barriers of the latent body do the waiting instead. Each row is read once
+// per workgroup, so the loads are non-temporal (nt): measured on the MLA
+// decode, 132 -> 114 us per launch.
 __device__ __forceinline__ uint32_t attn_lat_lds_at(const uint8_t *dst) {
     // dst is uniform (wave-indexed); readfirstlane tells the compiler so.
     return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(
@@ -1105,7 +1107,7 @@ __device__ __forceinline__ uint32_t attn_lat_lds_at(const uint8_t *dst) {
 __device__ __forceinline__ void attn_lat_load(uint64_t src, const uint8_t *dst) {
     uint32_t save;
     asm volatile(
-        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off nt\n\ts_mov_b32 m0, %0"
         : "=&s"(save)
         : "v"(src), "s"(attn_lat_lds_at(dst)));
 }
@@ -1119,14 +1121,14 @@ __device__ __forceinline__ void attn_lat_load8(const uint64_t (&a)[8], uint32_t 
     uint32_t save;
     asm volatile(
         "s_nop 4\n\ts_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %3\n\t"
-        "s_add_u32 m0, %2, %11\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %4\n\t"
-        "s_add_u32 m0, %2, %12\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %5\n\t"
-        "s_add_u32 m0, %2, %13\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %6\n\t"
-        "s_add_u32 m0, %2, %14\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %7\n\t"
-        "s_add_u32 m0, %2, %15\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %8\n\t"
-        "s_add_u32 m0, %2, %16\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %9\n\t"
-        "s_add_u32 m0, %2, %17\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %10\n\t"
+        "s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %3 nt\n\t"
+        "s_add_u32 m0, %2, %11\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %4 nt\n\t"
+        "s_add_u32 m0, %2, %12\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %5 nt\n\t"
+        "s_add_u32 m0, %2, %13\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %6 nt\n\t"
+        "s_add_u32 m0, %2, %14\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %7 nt\n\t"
+        "s_add_u32 m0, %2, %15\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %8 nt\n\t"
+        "s_add_u32 m0, %2, %16\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %9 nt\n\t"
+        "s_add_u32 m0, %2, %17\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %10 nt\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(save)
         : "v"(16 * (threadIdx.x & 63)), "s"(at), "s"(a[0]), "s"(a[1]), "s"(a[2]), "s"(a[3]), "s"(a[4]), "s"(a[5]),

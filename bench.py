@@ -784,7 +784,7 @@ def run_attention(args, config: str):
     log(f"attention avg {avg * 1e3:.1f} us per layer ({achieved:.0f} GB/s, "
         f"{launch_flops / avg / 1e9:.1f} TFLOP/s), wall {gbs:.0f} GB/s")
     k.close()
-    kernel = ("sglkv_paged_attention_latent" if mla else "sglkv_paged_attention_pipe128") + \
+    kernel = ("sglkv_paged_attention_latent" if mla else "sglkv_paged_attention_staged128") + \
         "+sglkv_paged_attention_combine"
     summary = "paged_attention_decode_" + ("mla" if mla else "hnd" if hnd else "nhd")
     extra = {"requests": nreq, "tokens_per_request": n, "layers": L, "kv_heads": H,

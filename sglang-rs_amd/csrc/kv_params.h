@@ -192,7 +192,7 @@ typedef struct sglkv_request_params {
  * the chunk's slot table (at most SGLKV_ATTN_STAGED_SLOTS tokens, which
  * bounds the chunk). */
 #define SGLKV_ATTN_STAGED_STAGES 2u
-#define SGLKV_ATTN_STAGED_SLOTS 512u
+#define SGLKV_ATTN_STAGED_SLOTS 1024u
 #define SGLKV_ATTN_STAGED_LDS_BYTES (SGLKV_ATTN_STAGED_STAGES * 16384u + 4u * SGLKV_ATTN_STAGED_SLOTS)
 
 typedef struct sglkv_attn_params {

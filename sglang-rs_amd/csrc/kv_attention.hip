@@ -21,11 +21,13 @@
 //  - long sequences are split over gridDim.y (flash-decoding): each split
 //    writes (max, sum, unnormalised output) and a combine kernel merges
 //    them, so a small batch still fills 256 CUs.
-// Four bodies share this math. The pipelined one (head dims up to 128,
-// 16-byte rows, power-of-two pages: every Llama/Qwen-style decode) loads
-// the slots of block i+2 and the K/V rows of block i+1 while it computes
-// block i, so a wave never waits on the dependent slot -> row loads; the
-// latent one (MLA: K rows up to 576 dims, V rows of 512) loads each block
+// Five bodies share this math. The staged one (head dims 128, up to 16
+// query heads per KV head, 16-byte rows, power-of-two pages: every
+// Llama/Qwen-style decode) loads each block's rows straight into LDS two
+// blocks deep; the pipelined one (the other head dims up to 128 on such
+// rows) loads the slots of block i+2 and the K/V rows of block i+1 into
+// registers while it computes block i, so a wave never waits on the
+// dependent slot -> row loads; the latent one (MLA: K rows up to 576 dims, V rows of 512) loads each block
 // straight into LDS once for up to 128 heads; the wide one (other shapes
 // with many query heads per KV head) stages each block once in LDS for up
 // to 64 heads; the generic one serves every other shape (odd dims,

@@ -265,29 +265,31 @@ def test_wide_reference_outrun(k, dk, dv, qh, hnd):
     np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
 
 
-def test_wide_unaligned_queries(k):
-    """A query buffer that is only 2-byte aligned: the wide bodies hold
-    queries as 16-byte vectors, so the launch must take the generic body,
-    with the same results."""
-    rng = np.random.default_rng(41)
-    c = _Case(rng, P=64, L=2, H=1, dk=576, dv=512, qh=32, pages=60, layer=1)
+@pytest.mark.parametrize("H,dk,dv", [(1, 576, 512), (8, 128, 128)])
+def test_wide_unaligned_queries(k, H, dk, dv):
+    """A query buffer that is only 2-byte aligned: the latent, wide and
+    staged bodies hold queries as 16-byte vectors, so the launch must take
+    the generic body (MLA widths) or the pipelined one (dims 128), with the
+    same results."""
+    rng = np.random.default_rng(41 + dk)
+    c = _Case(rng, P=64, L=2, H=H, dk=dk, dv=dv, qh=32, pages=60 * H, layer=1)
     lens, rso, slots = _random_batch(rng, 3, 900, c.layout.slot_count)
-    q = _bf16_normal(rng, 3 * 32 * 576).reshape(3, 32, 576)
-    plan = kv.PagedAttentionPlan.for_layer(c.layout, 1, 3, 3, len(slots), 32, 1.0 / math.sqrt(576))
+    q = _bf16_normal(rng, 3 * 32 * dk).reshape(3, 32, dk)
+    plan = kv.PagedAttentionPlan.for_layer(c.layout, 1, 3, 3, len(slots), 32, 1.0 / math.sqrt(dk))
     qbuf = hip.DeviceBuffer(q.nbytes + 2)
     qbuf.upload(np.concatenate([np.zeros(1, np.uint16), q.reshape(-1)]).view(np.uint8))
     out = hip.DeviceBuffer(plan.output_required_bytes)
-    _say("wide body, queries at a 2-byte offset")
+    _say(f"queries at a 2-byte offset, H={H} dk={dk} dv={dv}")
     k.paged_attention(plan, max_sequence_length=900, queries=qbuf, queries_offset=2,
                       query_request_indices=hip.DeviceBuffer.from_array(np.arange(3, dtype=np.uint32)),
                       query_sequence_lengths=hip.DeviceBuffer.from_array(lens.astype(np.uint64)),
                       request_slot_offsets=hip.DeviceBuffer.from_array(rso),
                       sequence_slots=hip.DeviceBuffer.from_array(slots), pool=c.pool, output=out)
-    got = oracle.bf16_to_f32(out.download().view(np.uint16)).reshape(3, 32, 512)
+    got = oracle.bf16_to_f32(out.download().view(np.uint16)).reshape(3, 32, dv)
     want, flags = oracle.paged_attention(
         c.pool_h, q, np.arange(3), lens, rso, slots, page_size=64, page_stride=plan.page_stride_bytes,
-        key_offset=plan.key_in_page_offset, value_offset=plan.value_in_page_offset, kv_heads=1, dk=576,
-        dv=512, scale=1.0 / math.sqrt(576), slot_count=c.layout.slot_count)
+        key_offset=plan.key_in_page_offset, value_offset=plan.value_in_page_offset, kv_heads=H, dk=dk,
+        dv=dv, scale=1.0 / math.sqrt(dk), slot_count=c.layout.slot_count)
     assert flags == 0
     np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
 

@@ -372,12 +372,14 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
             threads = 64 * SGLKV_ATTN_WIDE_WAVES;
         }
     }
-    // Dims 128 with one head group per KV head (every Llama/Qwen GQA decode):
-    // the staged body, rows loaded straight into LDS.
-    if (which == 2 && qp % 16 == 0 && p.head_groups == 1 && max_len <= 65535ull * SGLKV_ATTN_STAGED_SLOTS &&
-        SGLKV_ATTN_STAGED_LDS_BYTES <= (unsigned)ctx->max_lds_per_block) {
-        which = 7;
-        lds = SGLKV_ATTN_STAGED_LDS_BYTES;
+    // Dims 128 or 64 with one head group per KV head (the Llama/Qwen GQA
+    // decodes): the staged bodies, rows loaded straight into LDS.
+    const bool d64 = which == 3 && p.dk == 64 && p.dv == 64;
+    if ((which == 2 || d64) && qp % 16 == 0 && p.head_groups == 1 &&
+        max_len <= 65535ull * SGLKV_ATTN_STAGED_SLOTS &&
+        SGLKV_ATTN_STAGED_LDS_BYTES(p.dk) <= (unsigned)ctx->max_lds_per_block) {
+        which = d64 ? 8 : 7;
+        lds = SGLKV_ATTN_STAGED_LDS_BYTES(p.dk);
     }
     p.zero_row = ctx->zero_row;
     p.page_stride32 = (uint32_t)lay.page_stride_bytes;
@@ -389,7 +391,7 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
     // Workgroups before splitting; split each query's sequence so that the
     // launch fills every CU with as many workgroups as stay resident at
     // once (the kernel's occupancy at this LDS size), in one round.
-    const bool wide = which >= 4 && which <= 6;  // the wide and latent bodies (7: staged)
+    const bool wide = which >= 4 && which <= 6;  // the wide and latent bodies (7, 8: staged)
     const uint64_t hblocks = which == 6 ? ceil_div(p.group, SGLKV_ATTN_LATENT_HEADS)
                                         : (p.head_groups + SGLKV_ATTN_WIDE_GROUPS - 1) / SGLKV_ATTN_WIDE_GROUPS;
     uint64_t base = c.query_count;
@@ -410,7 +412,7 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
     uint64_t chunk = ceil_div(max_len, want);
     chunk = ceil_div(chunk < 256 ? 256 : chunk, SGLKV_ATTN_TOKENS) * SGLKV_ATTN_TOKENS;
     uint64_t splits = ceil_div(max_len, chunk);
-    const uint64_t table = wide ? SGLKV_ATTN_WIDE_SLOTS : which == 7 ? SGLKV_ATTN_STAGED_SLOTS : 0;
+    const uint64_t table = wide ? SGLKV_ATTN_WIDE_SLOTS : which >= 7 ? SGLKV_ATTN_STAGED_SLOTS : 0;
     if (table && chunk > table) {  // the slot table of the wide, latent and staged bodies
         chunk = table;
         splits = ceil_div(max_len, chunk);

@@ -21,8 +21,8 @@
 //  - long sequences are split over gridDim.y (flash-decoding): each split
 //    writes (max, sum, unnormalised output) and a combine kernel merges
 //    them, so a small batch still fills 256 CUs.
-// Five bodies share this math. The staged one (head dims 128, up to 16
-// query heads per KV head, 16-byte rows, power-of-two pages: every
+// Five bodies share this math. The staged one (head dims 128 or 64, up to
+// 16 query heads per KV head, 16-byte rows, power-of-two pages: every
 // Llama/Qwen-style decode) loads each block's rows straight into LDS two
 // blocks deep; the pipelined one (the other head dims up to 128 on such
 // rows) loads the slots of block i+2 and the K/V rows of block i+1 into
@@ -1486,17 +1486,17 @@ __device__ __forceinline__ void attn_latent_body(const sglkv_attn_params &p) {
     }
 }
 
-// ---- Staged body: GQA decode with K and V head dims 128 ----
+// ---- Staged bodies: GQA decode with K and V head dims D = 128 or 64 ----
 //
 // The pipelined body's loads put each 16-byte piece of a row into a
 // register, and its V transpose goes through LDS store by store. Here one
 // wave (a workgroup) owns (query, KV head, up to 16 query heads, split), as
 // there, but its K and V rows go from HBM straight into LDS with
-// non-temporal global_load_lds_dwordx4: one load moves the 256-byte head
-// slices of 4 tokens, 16 loads a 32-token block, with no register staging.
-// Three stages: while block k is computed, blocks k+1 and k+2 are loading.
-// One wave needs no barrier: s_waitcnt vmcnt(32) leaves the two newer
-// blocks' 32 loads in flight.
+// non-temporal global_load_lds_dwordx4: one load moves the 2D-byte head
+// slices of 512/D tokens (4 at D = 128, 8 at D = 64), D/2 loads a 32-token
+// block, with no register staging. Two stages: while block k is computed,
+// block k+1 is loading. One wave needs no barrier: s_waitcnt vmcnt(D/4)
+// leaves the newer block's loads in flight.
 //  - q.k is the pipelined body's (K as the A operand, lane (g, r) reading
 //    token 8(r/4) + 4b + r%4, dims 32c + 8g), from LDS; the queries are
 //    the B operand in registers.
@@ -1504,33 +1504,50 @@ __device__ __forceinline__ void attn_latent_body(const sglkv_attn_params &p) {
 //    16-lane group g addresses token 8g + r/4 (then 8g + 4 + r/4), dims
 //    16j + 4(r%4), which yields V[8g .. 8g+7][16j + r], the order the
 //    probabilities leave q.k in.
-//  - Piece (16 bytes) pc of token t's K row sits at position
-//    pc ^ ((t & 3) | ((t >> 3) << 2)) of its 256-byte LDS row: the 16 tokens
-//    one q.k read covers land in 16 distinct bank groups. V pieces sit at
-//    pc ^ (2(t & 3) | 8((t >> 3) & 1)): the 4 tokens x 4 dims of a
+//  - Piece (16 bytes) pc of token t's K row sits at position pc ^ mask(t)
+//    of its LDS row, the mask chosen so that the 16 tokens one q.k read
+//    covers land in 16 distinct 16-byte bank groups: at D = 128 (256-byte
+//    rows) mask = (t & 3) | 4(t >> 3); at D = 64 (128-byte rows, two per
+//    bank period, t & 1 already apart) mask = (t >> 1 & 1) | 2(t >> 3).
+//    V pieces: at D = 128 pc ^ (2(t & 3) | 8((t >> 3) & 1)), at D = 64
+//    pc ^ (2((t >> 1) & 1) | 4((t >> 3) & 1)): the 4 tokens x 4 dims of a
 //    16-lane transposing read, and the two 16-lane groups read together,
 //    land in distinct banks. Each load's lane fetches the global piece its
 //    LDS position holds.
-//  - The slot table keeps token t of a block at entry 8(t & 3) + t/4, so
-//    the 8 tokens 4j + c (j < 8) that lanes 16c .. 16c+15 load come in two
-//    16-byte reads.
+//  - The slot table keeps token t of a block at entry (D/16)(t % T) + t/T
+//    (T = 512/D tokens per load), so the D/16 tokens Tj + c that lanes
+//    with c = lane / (D/8) load come in 16-byte reads.
 //  - Online softmax with per-block rescaling, as the pipelined body (o is
-//    32 registers).
+//    D/4 registers).
 
-constexpr uint32_t kStgStage = 16384, kStgV = 8192;
-
-__device__ __forceinline__ uint32_t attn_stg_kpos(uint32_t t, uint32_t pc) {
-    return pc ^ ((t & 3) | ((t >> 1) & 12));
-}
-__device__ __forceinline__ uint32_t attn_stg_vpos(uint32_t t, uint32_t pc) {
-    return pc ^ (((t & 3) << 1) | (((t >> 3) & 1) << 3));
-}
-__device__ __forceinline__ uint32_t attn_stg_entry(uint32_t t) { return 8 * (t & 3) + (t >> 2); }
+template <uint32_t D>
+struct attn_stg {
+    static constexpr uint32_t ROW = 2 * D;                   // bytes of one token's head slice
+    static constexpr uint32_t PIECES = D / 8;                // 16-byte pieces per row
+    static constexpr uint32_t TPL = 1024 / ROW;              // tokens per load
+    static constexpr uint32_t LOADS = kLatB / TPL;           // loads per block, K (and as many V)
+    static constexpr uint32_t V = kLatB * ROW;               // V rows' offset in a stage
+    static constexpr uint32_t STAGE = 2 * V;                 // bytes of a stage
+    static constexpr uint32_t KC = D / 32;                   // q.k steps
+    static constexpr uint32_t NJ = D / 16;                   // p.v tiles
+    static_assert((D == 64 || D == 128) && STAGE * SGLKV_ATTN_STAGED_STAGES + 4 * SGLKV_ATTN_STAGED_SLOTS ==
+                                                SGLKV_ATTN_STAGED_LDS_BYTES(D),
+                  "stage layout");
+    static_assert(2 * LOADS % 8 == 0, "whole groups of eight loads");
+    static __device__ __forceinline__ uint32_t kpos(uint32_t t, uint32_t pc) {
+        return D == 128 ? pc ^ ((t & 3) | ((t >> 1) & 12)) : pc ^ (((t >> 1) & 1) | ((t >> 2) & 6));
+    }
+    static __device__ __forceinline__ uint32_t vpos(uint32_t t, uint32_t pc) {
+        return D == 128 ? pc ^ (((t & 3) << 1) | (((t >> 3) & 1) << 3))
+                        : pc ^ ((((t >> 1) & 1) << 1) | (((t >> 3) & 1) << 2));
+    }
+    static __device__ __forceinline__ uint32_t entry(uint32_t t) { return LOADS * (t % TPL) + t / TPL; }
+};
 
 // Eight loads: lane l's 16 bytes of load i from a[i] to LDS at
 // at + i * PITCH + 16 l (non-temporal).
 template <uint32_t PITCH>
-__device__ __forceinline__ void attn_lat_load8v(const uint64_t (&a)[8], uint32_t at) {
+__device__ __forceinline__ void attn_lat_load8v(const uint64_t *a, uint32_t at) {
     uint32_t save;
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
@@ -1550,37 +1567,47 @@ __device__ __forceinline__ void attn_lat_load8v(const uint64_t (&a)[8], uint32_t
         : "scc");
 }
 
-// The 16 loads of a block (its 32 slot entries at tb; live false: past the
-// chunk, every lane reads the zero row) into a stage: K rows, then V rows.
+// The 2 LOADS loads of a block (its 32 slot entries at tb; live false: past
+// the chunk, every lane reads the zero row) into a stage: K rows, then V
+// rows, 1 KiB each at consecutive LDS offsets.
+template <uint32_t D>
 __device__ __forceinline__ void attn_stg_issue(const sglkv_attn_params &p, uint64_t kbase, uint64_t vbase,
                                                const uint32_t *tb, bool live, uint32_t lane, const uint8_t *stage) {
-    const uint32_t c = lane >> 4, pc = lane & 15;
-    const uint4 s0 = *reinterpret_cast<const uint4 *>(tb + 8 * c);
-    const uint4 s1 = *reinterpret_cast<const uint4 *>(tb + 8 * c + 4);
-    const uint32_t s[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    typedef attn_stg<D> S;
+    const uint32_t c = lane / S::PIECES, pc = lane % S::PIECES;
+    uint32_t s[S::LOADS];
+#pragma unroll
+    for (uint32_t h = 0; h < S::LOADS / 4; ++h) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(tb + S::LOADS * c + 4 * h);
+        s[4 * h] = v.x;
+        s[4 * h + 1] = v.y;
+        s[4 * h + 2] = v.z;
+        s[4 * h + 3] = v.w;
+    }
     const uint64_t zero = reinterpret_cast<uint64_t>(p.zero_row) + 16 * pc;
     const uint32_t mask = (1u << p.page_shift) - 1;
-    uint64_t ka[8], va[8];
+    uint64_t a[2 * S::LOADS];
 #pragma unroll
-    for (uint32_t j = 0; j < 8; ++j) {
-        const uint32_t t = 4 * j + c;
+    for (uint32_t j = 0; j < S::LOADS; ++j) {
+        const uint32_t t = S::TPL * j + c;
         const bool ok = live && s[j] != kAttnInvalidSlot;
         const uint64_t page = static_cast<uint64_t>(s[j] >> p.page_shift) * p.page_stride32;
         const uint32_t pos = s[j] & mask;
-        ka[j] = ok ? kbase + page + static_cast<uint64_t>(pos) * p.key_token_stride32 + 16 * attn_stg_kpos(t, pc)
-                   : zero;
-        va[j] = ok ? vbase + page + static_cast<uint64_t>(pos) * p.value_token_stride32 + 16 * attn_stg_vpos(t, pc)
-                   : zero;
+        a[j] = ok ? kbase + page + static_cast<uint64_t>(pos) * p.key_token_stride32 + 16 * S::kpos(t, pc) : zero;
+        a[S::LOADS + j] =
+            ok ? vbase + page + static_cast<uint64_t>(pos) * p.value_token_stride32 + 16 * S::vpos(t, pc) : zero;
     }
-    attn_lat_load8v<1024>(ka, attn_lat_lds_at(stage));
-    attn_lat_load8v<1024>(va, attn_lat_lds_at(stage + kStgV));
+#pragma unroll
+    for (uint32_t h = 0; h < 2 * S::LOADS / 8; ++h) attn_lat_load8v<1024>(a + 8 * h, attn_lat_lds_at(stage + 8192 * h));
 }
 
 // Softmax of one block against the running maximum (rescaling o and l),
 // then o += p.v with V from the stage by transposing reads.
+template <uint32_t D>
 __device__ __forceinline__ void attn_stg_softmax_pv(const sglkv_attn_params &p, uint32_t g, uint32_t r,
                                                     const sglkv_f32x4 (&sc)[2], uint64_t vb0, uint64_t vb1,
-                                                    const uint8_t *vst, attn_state &st) {
+                                                    const uint8_t *vst, attn_state_n<attn_stg<D>::NJ> &st) {
+    typedef attn_stg<D> S;
     float x[8];
     float mx = -INFINITY;
 #pragma unroll
@@ -1610,25 +1637,27 @@ __device__ __forceinline__ void attn_stg_softmax_pv(const sglkv_attn_params &p, 
 #pragma unroll
     for (uint32_t e = 0; e < 4; ++e) arow[e] = __shfl(alpha, 4 * g + e);
 #pragma unroll
-    for (uint32_t j = 0; j < 8; ++j)
+    for (uint32_t j = 0; j < S::NJ; ++j)
 #pragma unroll
         for (uint32_t e = 0; e < 4; ++e) st.o[j][e] *= arow[e];
     // B operand of tile j: V[8g .. 8g+7][16j + r].
     const uint32_t t0 = 8 * g + (r >> 2), t1 = t0 + 4, d4 = r & 3;
 #pragma unroll
-    for (uint32_t j = 0; j < 8; ++j) {
+    for (uint32_t j = 0; j < S::NJ; ++j) {
         const uint32_t pc = 2 * j + (d4 >> 1), half = 8 * (d4 & 1);
-        const attn_i16x4 lo = attn_lat_vtr(vst + 256 * t0 + 16 * attn_stg_vpos(t0, pc) + half);
-        const attn_i16x4 hi = attn_lat_vtr(vst + 256 * t1 + 16 * attn_stg_vpos(t1, pc) + half);
+        const attn_i16x4 lo = attn_lat_vtr(vst + S::ROW * t0 + 16 * S::vpos(t0, pc) + half);
+        const attn_i16x4 hi = attn_lat_vtr(vst + S::ROW * t1 + 16 * S::vpos(t1, pc) + half);
         const sglkv_u16x8 vv = {(uint16_t)lo[0], (uint16_t)lo[1], (uint16_t)lo[2], (uint16_t)lo[3],
                                 (uint16_t)hi[0], (uint16_t)hi[1], (uint16_t)hi[2], (uint16_t)hi[3]};
         st.o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(pbits), attn_as_bf16(vv), st.o[j], 0, 0, 0);
     }
 }
 
+template <uint32_t D>
 __device__ __forceinline__ void attn_staged_body(const sglkv_attn_params &p) {
+    typedef attn_stg<D> S;
     extern __shared__ __attribute__((aligned(16))) uint8_t attn_stg_lds[];
-    uint32_t *table = reinterpret_cast<uint32_t *>(attn_stg_lds + SGLKV_ATTN_STAGED_STAGES * kStgStage);
+    uint32_t *table = reinterpret_cast<uint32_t *>(attn_stg_lds + SGLKV_ATTN_STAGED_STAGES * S::STAGE);
     const uint32_t lane = threadIdx.x;
     const uint32_t g = lane >> 4, r = lane & 15;
     attn_work w;
@@ -1636,19 +1665,19 @@ __device__ __forceinline__ void attn_staged_body(const sglkv_attn_params &p) {
     const uint32_t nb = static_cast<uint32_t>((w.t1 - w.t0 + kLatB - 1) / kLatB);  // <= SLOTS / 32 (host bound)
 
     // Queries (B operand of q.k): head r, dims 32c + 8g.
-    sglkv_u16x8 qf[4];
+    sglkv_u16x8 qf[S::KC];
 #pragma unroll
-    for (uint32_t c = 0; c < 4; ++c) {
+    for (uint32_t c = 0; c < S::KC; ++c) {
         qf[c] = sglkv_u16x8{0, 0, 0, 0, 0, 0, 0, 0};
         if (r < w.nh)
-            qf[c] = *reinterpret_cast<const sglkv_u16x8 *>(p.queries + (w.q * p.query_heads + w.h0 + r) * 128 +
+            qf[c] = *reinterpret_cast<const sglkv_u16x8 *>(p.queries + (w.q * p.query_heads + w.h0 + r) * D +
                                                             32 * c + 8 * g);
     }
     // The chunk's slots, checked once; token t of block b at entry
-    // 32 b + 8 (t & 3) + t / 4.
+    // 32 b + entry(t).
     for (uint32_t i = lane; i < nb * kLatB; i += 64) {
         const uint64_t tok = w.t0 + i;
-        table[(i & ~31u) + attn_stg_entry(i & 31)] =
+        table[(i & ~31u) + S::entry(i & 31)] =
             attn_wide_slot(p, tok < w.t1 ? p.sequence_slots[w.start + tok] : 0, tok, w.t1);
     }
     __syncthreads();
@@ -1657,41 +1686,41 @@ __device__ __forceinline__ void attn_staged_body(const sglkv_attn_params &p) {
     const uint64_t kbase = pool + p.key_offset + w.kvh * p.key_head_stride;
     const uint64_t vbase = pool + p.value_offset + w.kvh * p.value_head_stride;
     auto blk = [&](uint32_t b) { return table + (b < nb ? b : nb - 1) * kLatB; };
-    auto stage = [&](uint32_t b) { return attn_stg_lds + (b % SGLKV_ATTN_STAGED_STAGES) * kStgStage; };
+    auto stage = [&](uint32_t b) { return attn_stg_lds + (b % SGLKV_ATTN_STAGED_STAGES) * S::STAGE; };
 #pragma unroll
     for (uint32_t b = 0; b + 1 < SGLKV_ATTN_STAGED_STAGES; ++b)
-        attn_stg_issue(p, kbase, vbase, blk(b), b < nb, lane, stage(b));
+        attn_stg_issue<D>(p, kbase, vbase, blk(b), b < nb, lane, stage(b));
     // The query and slot loads (which the compiler tracks) are complete
     // before the loop; the loop's waits count the row loads alone.
     __builtin_amdgcn_s_waitcnt(0x0F70);
 
-    attn_state st;
+    attn_state_n<S::NJ> st;
     attn_state_init(st);
     for (uint32_t k = 0; k < nb; ++k) {
-        // Block k-1's LDS reads are done before block k+2's rows overwrite
-        // its stage; then block k's 16 loads (older than the 32 of blocks
-        // k+1 and k+2) have landed.
+        // Block k-1's LDS reads are done before block k+STAGES-1's rows
+        // overwrite its stage; then block k's loads (older than the newer
+        // blocks') have landed.
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        attn_stg_issue(p, kbase, vbase, blk(k + SGLKV_ATTN_STAGED_STAGES - 1), k + SGLKV_ATTN_STAGED_STAGES - 1 < nb,
-                       lane, stage(k + SGLKV_ATTN_STAGED_STAGES - 1));
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(16 * (SGLKV_ATTN_STAGED_STAGES - 1)) : "memory");
+        attn_stg_issue<D>(p, kbase, vbase, blk(k + SGLKV_ATTN_STAGED_STAGES - 1),
+                          k + SGLKV_ATTN_STAGED_STAGES - 1 < nb, lane, stage(k + SGLKV_ATTN_STAGED_STAGES - 1));
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * S::LOADS * (SGLKV_ATTN_STAGED_STAGES - 1)) : "memory");
         const uint8_t *kst = stage(k);
         sglkv_f32x4 sc[2] = {sglkv_f32x4{0.f, 0.f, 0.f, 0.f}, sglkv_f32x4{0.f, 0.f, 0.f, 0.f}};
         uint32_t valid = 0;
 #pragma unroll
         for (uint32_t b = 0; b < 2; ++b) {
             const uint32_t t = 8 * (r >> 2) + 4 * b + (r & 3);
-            valid |= (blk(k)[attn_stg_entry(t)] != kAttnInvalidSlot ? 1u : 0u) << b;
+            valid |= (blk(k)[S::entry(t)] != kAttnInvalidSlot ? 1u : 0u) << b;
 #pragma unroll
-            for (uint32_t c = 0; c < 4; ++c) {
+            for (uint32_t c = 0; c < S::KC; ++c) {
                 const sglkv_u16x8 kf =
-                    *reinterpret_cast<const sglkv_u16x8 *>(kst + 256 * t + 16 * attn_stg_kpos(t, 4 * c + g));
+                    *reinterpret_cast<const sglkv_u16x8 *>(kst + S::ROW * t + 16 * S::kpos(t, 4 * c + g));
                 sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(kf), attn_as_bf16(qf[c]), sc[b], 0, 0,
                                                                 0);
             }
         }
         const uint64_t vb0 = __ballot(valid & 1), vb1 = __ballot((valid >> 1) & 1);
-        attn_stg_softmax_pv(p, g, r, sc, vb0, vb1, kst + kStgV, st);
+        attn_stg_softmax_pv<D>(p, g, r, sc, vb0, vb1, kst + S::V, st);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the zero-row loads issued past the chunk
     attn_finish(p, w, g, r, st);
@@ -1716,10 +1745,14 @@ extern "C" __global__ __launch_bounds__(512) void sglkv_paged_attention_wide128(
     attn_wide_body<4, 8>(p);
 }
 
-// K and V head dims 128, up to 16 query heads per KV head, rows staged in
-// LDS.
+// K and V head dims 128 / 64, up to 16 query heads per KV head, rows
+// staged in LDS.
 extern "C" __global__ __launch_bounds__(64) void sglkv_paged_attention_staged128(sglkv_attn_params p) {
-    attn_staged_body(p);
+    attn_staged_body<128>(p);
+}
+
+extern "C" __global__ __launch_bounds__(64) void sglkv_paged_attention_staged64(sglkv_attn_params p) {
+    attn_staged_body<64>(p);
 }
 
 // MLA latent rows (K <= 576, V <= 512 dims), up to 128 query heads per

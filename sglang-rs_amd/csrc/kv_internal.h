@@ -106,11 +106,11 @@ struct sgl_rocm_kv_ctx {
     hipFunction_t stream_fn[3];     // streaming ceilings: copy, read, write
     // 16-byte vector / element-wise / pipelined dims 128 / pipelined dims <= 128 /
     // wide (K <= 576, V <= 512) / wide dims <= 128 / latent (MLA: K <= 576, V <= 512) /
-    // staged (dims 128, rows in LDS)
-    hipFunction_t attention[8];
+    // staged (dims 128, rows in LDS) / staged (dims 64)
+    hipFunction_t attention[9];
     hipFunction_t attention_combine;
-    uint32_t attention_occupancy[8];      // resident workgroups per CU of attention[i] ...
-    uint32_t attention_occupancy_lds[8];  // ... at this LDS size (0 = not yet queried)
+    uint32_t attention_occupancy[9];      // resident workgroups per CU of attention[i] ...
+    uint32_t attention_occupancy_lds[9];  // ... at this LDS size (0 = not yet queried)
     int max_lds_per_block;                // device limit on a workgroup's LDS bytes
     uint32_t *flag;                 // device error word, at the start of a small zeroed block
     const uint8_t *zero_row;        // SGLKV_ZERO_ROW_BYTES of zeros inside that block

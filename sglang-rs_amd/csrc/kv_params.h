@@ -186,14 +186,14 @@ typedef struct sglkv_request_params {
 #define SGLKV_ATTN_LATENT_VSTAGE (SGLKV_ATTN_TOKENS * 1088u)
 #define SGLKV_ATTN_LATENT_LDS_BYTES                                                            \
     (2u * (SGLKV_ATTN_LATENT_KSTAGE + SGLKV_ATTN_LATENT_VSTAGE) + 4u * SGLKV_ATTN_WIDE_SLOTS + 16u)
-/* The staged body (K and V head dims 128, at most SGLKV_ATTN_HEADS query
- * heads per KV head): one wave per workgroup, SGLKV_ATTN_STAGED_STAGES LDS
- * stages of a 32-token block (8 KiB of K rows, then 8 KiB of V rows) and
- * the chunk's slot table (at most SGLKV_ATTN_STAGED_SLOTS tokens, which
- * bounds the chunk). */
+/* The staged bodies (K and V head dims d = 64 or 128, at most
+ * SGLKV_ATTN_HEADS query heads per KV head): one wave per workgroup,
+ * SGLKV_ATTN_STAGED_STAGES LDS stages of a 32-token block (64 d bytes of K
+ * rows, then as many of V rows) and the chunk's slot table (at most
+ * SGLKV_ATTN_STAGED_SLOTS tokens, which bounds the chunk). */
 #define SGLKV_ATTN_STAGED_STAGES 2u
 #define SGLKV_ATTN_STAGED_SLOTS 1024u
-#define SGLKV_ATTN_STAGED_LDS_BYTES (SGLKV_ATTN_STAGED_STAGES * 16384u + 4u * SGLKV_ATTN_STAGED_SLOTS)
+#define SGLKV_ATTN_STAGED_LDS_BYTES(d) (SGLKV_ATTN_STAGED_STAGES * 128u * (d) + 4u * SGLKV_ATTN_STAGED_SLOTS)
 
 typedef struct sglkv_attn_params {
     const uint16_t *queries;              /* bf16 [query][query_head][dk] */

@@ -125,6 +125,24 @@ def test_llama3_8b_decode(k, hnd, P):
     np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("H,qh,P,hnd,nreq,max_len", [
+    (8, 32, 16, False, 16, 1500),   # Llama-3.2-1B: 32 query heads over 8 KV heads
+    (2, 14, 64, True, 8, 3000),     # Qwen2-0.5B: groups of 7 heads, head-major pages
+    (8, 32, 1, False, 4, 300),      # one-token pages
+    (1, 16, 16, False, 2, 9000),    # long sequences: many splits of the slot table's size
+])
+def test_dims64_decode(k, H, qh, P, hnd, nreq, max_len):
+    """Decode with K and V head dims 64 (the dims-64 staged body)."""
+    rng = np.random.default_rng(64 + P + qh)
+    pages = -(-nreq * max_len // P) + 4
+    c = _Case(rng, P=P, L=2, H=H, dk=64, dv=64, qh=qh, pages=pages, layer=1, hnd=hnd)
+    lens, rso, slots = _random_batch(rng, nreq, max_len, c.layout.slot_count)
+    q = _bf16_normal(rng, nreq * qh * 64).reshape(nreq, qh, 64)
+    _say(f"dims-64 decode H={H} qh={qh} P={P} hnd={hnd} tokens={int(rso[-1])}")
+    got, want = c.run(k, q, np.arange(nreq), lens, rso, slots, 1.0 / math.sqrt(64), max_len=max_len)
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+
+
 def test_long_sequence_is_split_and_combined(k):
     """One request of 20,000 tokens (many splits through the combine kernel)
     and a short one in the same launch; the short query's sequence ends

@@ -9,7 +9,8 @@ and queries are N(0, 1) bf16).
 
 Cases: the reference's own scheduler metadata (causal prefill of two
 requests, crates/sglang-srt/tests/cuda_attention.rs:70-97); Llama-3-8B
-decode shapes on NHD and HND pages; a GQA group wider than one workgroup;
+decode shapes on NHD and HND pages; dims-64 decode shapes (Llama-3.2-1B,
+Qwen2-0.5B); a GQA group wider than one workgroup;
 MLA widths (576/512, the DeepSeek pair); odd head dims (element-wise
 path); long sequences split across workgroups; metadata errors; and an
 HND decode pool written by the transfer kernels read back through
@@ -312,11 +313,16 @@ def test_wide_unaligned_queries(k, H, dk, dv):
     np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
 
 
-@pytest.mark.parametrize("dk,dv,qh,max_len", [(576, 512, 16, 4300), (128, 128, 32, 20000)])
+@pytest.mark.parametrize("dk,dv,qh,max_len", [
+    (576, 512, 16, 4300),    # latent body, 4,096-token table
+    (128, 128, 32, 20000),   # wide body, 4,096-token table
+    (128, 128, 16, 9000),    # staged body, 1,024-token table
+    (64, 64, 16, 9000),      # dims-64 staged body, 1,024-token table
+])
 def test_wide_chunk_capped_by_slot_table(k, dk, dv, qh, max_len):
-    """Enough queries to fill the GPU without splitting (256 workgroups)
-    and sequences longer than the wide bodies' 4,096-token slot table: the
-    host must cap the chunk, so a query takes several splits, and the
+    """Enough queries to fill the GPU with few splits (256 workgroups) and
+    sequences longer than the body's slot table allows per split: the host
+    must cap the chunk, so a query takes several splits, and the
     shorter ones use fewer of them than the launch has. Sequences reuse the
     rows of a small pool (slots drawn with replacement, as a slot list may
     repeat them). A sample of the queries is checked."""
@@ -329,7 +335,7 @@ def test_wide_chunk_capped_by_slot_table(k, dk, dv, qh, max_len):
     q = _bf16_normal(rng, nq * qh * dk).reshape(nq, qh, dk)
     plan = kv.PagedAttentionPlan.for_layer(c.layout, 0, nq, nq, len(slots), qh, 1.0 / math.sqrt(dk))
     out = hip.DeviceBuffer(plan.output_required_bytes)
-    _say(f"wide body, chunk capped: {nq} queries x up to {lens.max()} tokens, dk {dk}")
+    _say(f"chunk capped by the slot table: {nq} queries x up to {lens.max()} tokens, dk {dk} qh {qh}")
     k.paged_attention(plan, max_sequence_length=int(lens.max()), queries=hip.DeviceBuffer.from_array(q),
                       query_request_indices=hip.DeviceBuffer.from_array(np.arange(nq, dtype=np.uint32)),
                       query_sequence_lengths=hip.DeviceBuffer.from_array(lens.astype(np.uint64)),

@@ -1774,10 +1774,13 @@ extern "C" __global__ __launch_bounds__(64) void sglkv_paged_attention_pipe(sglk
 }
 
 // Merges the split records of one (query, head): m* = max m_s,
-// out = sum_s 2^(m_s - m*) o_s / sum_s 2^(m_s - m*) l_s. Thread t handles
-// dims 4t .. 4t+3 (+512 ...), one 16-byte read per split's o row (rows are
-// 128-byte aligned; dims past dv read the row's padding and are not
-// written).
+// out = sum_s 2^(m_s - m*) o_s / sum_s 2^(m_s - m*) l_s, with a running
+// maximum so that each group of eight splits' (m, l) pairs and o pieces is
+// loaded at once (one memory latency per group, not one for the maxima and
+// one for the rows). Thread t handles dims 4t .. 4t+3 (+512 ...), one
+// 16-byte read per split's o row (rows are 128-byte aligned; dims past dv
+// read the row's padding and are not written). Lanes of a group past the
+// used splits reload the last used split and weigh it 0.
 extern "C" __global__ __launch_bounds__(128) void sglkv_paged_attention_combine(sglkv_attn_params p) {
     const uint64_t q = blockIdx.x / p.query_heads;
     const uint32_t head = static_cast<uint32_t>(blockIdx.x % p.query_heads);
@@ -1785,26 +1788,37 @@ extern "C" __global__ __launch_bounds__(128) void sglkv_paged_attention_combine(
     if (!attn_metadata(p, q, false, &start, &len)) return;
     const uint32_t used = static_cast<uint32_t>((len + p.chunk_tokens - 1) / p.chunk_tokens);
     const uint64_t i0 = (q * p.query_heads + head) * p.splits;
-    const float *ml = attn_rec_ml(p, i0);
+    const float2 *ml = reinterpret_cast<const float2 *>(attn_rec_ml(p, i0));
     const float *o = attn_rec_o(p, i0);
     const uint32_t opad = SGLKV_ATTN_OPAD(p.dv);
-    float m = -3.402823466e+38f;
-    for (uint32_t s = 0; s < used; ++s) m = fmaxf(m, ml[2 * s]);
-    float l = 0.0f;
-    for (uint32_t s = 0; s < used; ++s) l += exp2f(ml[2 * s] - m) * ml[2 * s + 1];
-    const float linv = 1.0f / l;
     uint16_t *out = p.output + (q * p.query_heads + head) * p.dv;
     for (uint32_t d = 4 * threadIdx.x; d < p.dv; d += 512) {
+        float m = -3.402823466e+38f, l = 0.0f;
         float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 8
-        for (uint32_t s = 0; s < used; ++s) {
-            const float ws = exp2f(ml[2 * s] - m);
-            const float4 v = *reinterpret_cast<const float4 *>(o + s * opad + d);
-            acc.x += ws * v.x;
-            acc.y += ws * v.y;
-            acc.z += ws * v.z;
-            acc.w += ws * v.w;
+        for (uint32_t s0 = 0; s0 < used; s0 += 8) {
+            float2 r[8];
+            float4 v[8];
+#pragma unroll
+            for (uint32_t j = 0; j < 8; ++j) {
+                const uint32_t s = s0 + j < used ? s0 + j : used - 1;
+                r[j] = ml[s];
+                v[j] = *reinterpret_cast<const float4 *>(o + s * opad + d);
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < 8; ++j) {
+                const bool ok = s0 + j < used;
+                const float m_new = ok ? fmaxf(m, r[j].x) : m;
+                const float a = exp2f(m - m_new);
+                const float w = ok ? exp2f(r[j].x - m_new) : 0.0f;
+                l = l * a + w * r[j].y;
+                acc.x = acc.x * a + w * v[j].x;
+                acc.y = acc.y * a + w * v[j].y;
+                acc.z = acc.z * a + w * v[j].z;
+                acc.w = acc.w * a + w * v[j].w;
+                m = m_new;
+            }
         }
+        const float linv = 1.0f / l;
         const float o4[4] = {acc.x, acc.y, acc.z, acc.w};
 #pragma unroll
         for (uint32_t e = 0; e < 4; ++e)

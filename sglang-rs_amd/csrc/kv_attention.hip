@@ -1493,9 +1493,9 @@ __device__ __forceinline__ void attn_latent_body(const sglkv_attn_params &p) {
 // wave (a workgroup) owns (query, KV head, up to 16 query heads, split), as
 // there, but its K and V rows go from HBM straight into LDS with
 // non-temporal global_load_lds_dwordx4: one load moves the 2D-byte head
-// slices of 512/D tokens (4 at D = 128, 8 at D = 64), D/2 loads a 32-token
+// slices of 512/D tokens (4 at D = 128, 8 at D = 64), D/8 loads a 32-token
 // block, with no register staging. Two stages: while block k is computed,
-// block k+1 is loading. One wave needs no barrier: s_waitcnt vmcnt(D/4)
+// block k+1 is loading. One wave needs no barrier: s_waitcnt vmcnt(D/8)
 // leaves the newer block's loads in flight.
 //  - q.k is the pipelined body's (K as the A operand, lane (g, r) reading
 //    token 8(r/4) + 4b + r%4, dims 32c + 8g), from LDS; the queries are

@@ -74,6 +74,14 @@ DESCRIPTIONS = {
           "src and dst page_size-64 pools with independent random page tables",
     "c4fp8": "C4 fp8: MLA latent rows as 576-byte fp8-e4m3 rows with per-layer scales passed "
              "through, 61 layers, 32 requests x 8192, page_size-64 -> page_size-64",
+    "c4pair": "C4 over the pool the DeepSeek-V3 adapter allocates (models/deepseek.rs:360-369): "
+              "61 layers of a tensor pair, 576-wide bf16 key (latent + rope, 1152 B) and 512-wide "
+              "bf16 value (1024 B) per token, one launch per layer for both tensors; 32 requests x "
+              "8192, page_size-64 -> page_size-64 with independent random page tables",
+    "c4packed": "C4 over packed-MLA rows (packed_mla(61, 512, 64) = 649 bytes per token per "
+                "layer, kv_cache.rs:201-224, models/deepseek.rs:1035-1037), byte-realigning "
+                "kernels; 32 requests x 8192, page_size-64 -> page_size-64 with independent "
+                "random page tables",
     "c2pages": "C2 shape as the reference transfers it today: page-for-page copies between "
                "page_size-64 pools of equal layout (131072 tokens = 2048 pages of 8 MiB, random "
                "source and destination pages), built with sgl_kv_build_page_requests and run "
@@ -120,37 +128,43 @@ def _traffic_from_profiles(kernel: str, summary: str):
     return None
 
 
-def cpu_baseline(make, seconds: float = 10.0, rows: int = 8192, threads: int = 1,
+def cpu_baseline(make, seconds: float = 10.0, rows: int | None = 8192, threads: int = 1,
                  direct: bool = False):
     """The CPU oracle's pack + unpack (direct: its pool -> pool transfer) on
     `threads` host threads (rows split evenly) on the first `rows` tokens of
-    the workload, repeated for about `seconds`."""
+    the workload (None: the whole workload), repeated for about `seconds`
+    (at least once)."""
     import oracle
     from sgl_rocm_kv import workloads as wl
-    t = wl.scaled(make(), rows, seed=1)
+    t = make() if rows is None else wl.scaled(make(), rows, seed=1)
     sh = t.shape
-    rb, n, T = sh.row_bytes, t.rows, sh.tensors
+    n, T = t.rows, sh.tensors
+    rb = [sh.tensor_row_bytes(i) for i in range(T)] + [0]
+    lrb = sh.layer_row_bytes
     rng = np.random.default_rng(0)
-    src = rng.integers(0, 256, t.src.byte_len(sh), dtype=np.uint8)
+    # (the whole workload's pools: zeros, faulted in by the untimed pass;
+    # byte values do not change a copy's speed)
+    src = (np.zeros(t.src.byte_len(sh), np.uint8) if rows is None
+           else rng.integers(0, 256, t.src.byte_len(sh), dtype=np.uint8))
     dst = np.zeros(t.dst.byte_len(sh), np.uint8)
-    buf = np.zeros(sh.layers * T * n * rb, np.uint8)
+    buf = np.zeros(sh.layers * n * lrb, np.uint8)
     pools = []
     for layer in range(sh.layers):
         def opool(spec):
             return oracle.Pool(spec.page_size, spec.page_stride(sh), spec.page_count,
-                               spec.tensor_offsets(sh, layer), rb, T, sh.heads,
-                               spec.head_layout == 1)
-        part = buf[layer * T * n * rb:(layer + 1) * T * n * rb]
-        pools.append((opool(t.src), opool(t.dst), part[: n * rb], part[n * rb:] if T == 2 else None))
+                               spec.tensor_offsets(sh, layer), rb[0], T, sh.heads,
+                               spec.head_layout == 1, rb[1] if T == 2 and rb[1] != rb[0] else 0)
+        part = buf[layer * n * lrb:(layer + 1) * n * lrb]
+        pools.append((opool(t.src), opool(t.dst), part[: n * rb[0]], part[n * rb[0]:] if T == 2 else None))
     def one_pass():
         if direct:
             for sp, dp, _, _ in pools:
                 oracle.transfer(sp, src, t.src_slots, dp, dst, t.dst_slots, threads=threads)
             return
         for sp, dp, r0, r1 in pools:
-            oracle.pack(sp, src, t.src_slots, r0, r1, rb, rb, threads=threads)
+            oracle.pack(sp, src, t.src_slots, r0, r1, rb[0], rb[1], threads=threads)
         for sp, dp, r0, r1 in pools:
-            oracle.unpack(dp, dst, t.dst_slots, r0, r1, rb, rb, threads=threads)
+            oracle.unpack(dp, dst, t.dst_slots, r0, r1, rb[0], rb[1], threads=threads)
 
     one_pass()   # untimed: faults every page of the lazily mapped buffers in
     reps, t0 = 0, time.perf_counter()
@@ -161,11 +175,39 @@ def cpu_baseline(make, seconds: float = 10.0, rows: int = 8192, threads: int = 1
         if el >= seconds or reps >= 1000:
             break
     gbs = (2 if direct else 4) * t.payload_bytes * reps / el / 1e9
+    which = "all" if rows is None else "first"
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{t.name.split(' (')[0]} shape, first {n} tokens ({sh.layers} layers, "
+            "cpu_model": _cpu_model(),
+            "sample": f"{t.name.split(' (')[0]} shape, {which} {n} tokens ({sh.layers} layers, "
                       f"{t.payload_bytes >> 20} MiB payload), "
                       f"{'pool -> pool transfer' if direct else 'pack+unpack'} x {reps} in {el:.1f} s, "
                       f"oracle/kv_oracle.c, {threads} thread{'s' if threads > 1 else ''}"}
+
+
+def _cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo)."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _usable_cores() -> int:
+    """Cores this process may run on (its affinity mask; the box's share)."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
+
+
+def _host_ram_bytes() -> int:
+    try:
+        return os.sysconf("SC_PAGE_SIZE") * os.sysconf("SC_PHYS_PAGES")
+    except (ValueError, OSError):
+        return 0
 
 
 def _views(kv, buf, spec, sh, layer, scale=None):
@@ -173,7 +215,62 @@ def _views(kv, buf, spec, sh, layer, scale=None):
                         page_stride_bytes=spec.page_stride(sh), page_count=spec.page_count,
                         tensor_offset=spec.tensor_offsets(sh, layer), row_bytes=sh.row_bytes,
                         tensor_count=sh.tensors, heads=sh.heads, head_layout=spec.head_layout,
-                        scale=scale)
+                        scale=scale,
+                        value_row_bytes=sh.tensor_row_bytes(1) if sh.tensors == 2 and
+                        sh.tensor_row_bytes(1) != sh.row_bytes else 0)
+
+
+def _kernel_family(sh):
+    """The copy kernels a shape's rows take: the 16-byte-vector kernels when
+    every row width is a whole number of 16-byte vectors (every address and
+    stride of these workloads is then 16-byte aligned), the byte-realigning
+    kernels otherwise (the 649-byte packed-MLA rows)."""
+    if all(sh.tensor_row_bytes(t) % 16 == 0 for t in range(sh.tensors)):
+        return "sglkv_copy_pool_rows_v16", "sglkv_copy_rows_pool_v16"
+    return "sglkv_realign_pool_rows", "sglkv_realign_rows_pool"
+
+
+def _pool_row_ranges(spec, sh, layer, slot):
+    """(offset, length) pieces of (slot, layer)'s rows in a pool, tensor by
+    tensor and head chunk by head chunk (the page-major layout of
+    kv_cache.rs:653-700; HND pages keep each head's chunks together)."""
+    page, pos = divmod(int(slot), spec.page_size)
+    out = []
+    for t, off in enumerate(spec.tensor_offsets(sh, layer)):
+        rb = sh.tensor_row_bytes(t)
+        region = page * spec.page_stride(sh) + off
+        if spec.head_layout == 1:
+            c = rb // sh.heads
+            out += [(region + (h * spec.page_size + pos) * c, c) for h in range(sh.heads)]
+        else:
+            out.append((region + pos * rb, rb))
+    return out
+
+
+def verify_sample(t, src, xfer, dst, row_planes, rows_per_layer=64, seed=5):
+    """After the timed steps: for a sample of rows on the first, middle and
+    last layers, the source pool's bytes at the row's source slot, the
+    packed transfer row and the destination pool's bytes at its destination
+    slot must agree byte for byte (a check of the measured run itself; the
+    parity tests compare with the CPU oracle). Returns rows checked."""
+    sh = t.shape
+    L = sh.layers
+    rng = np.random.default_rng(seed)
+    checked = 0
+    for layer in sorted({0, L // 2, L - 1}):
+        for r in rng.choice(t.rows, size=min(rows_per_layer, t.rows), replace=False):
+            r = int(r)
+            want = b"".join(bytes(src.download(n, o)) for o, n in
+                            _pool_row_ranges(t.src, sh, layer, t.src_slots[r]))
+            got_dst = b"".join(bytes(dst.download(n, o)) for o, n in
+                               _pool_row_ranges(t.dst, sh, layer, t.dst_slots[r]))
+            packed = b"".join(bytes(xfer.download(sh.tensor_row_bytes(tt), row_planes(layer, tt, r)))
+                              for tt in range(sh.tensors))
+            if not (want == packed == got_dst):
+                raise SystemExit(f"verification failed: layer {layer} row {r} "
+                                 f"(src slot {t.src_slots[r]}, dst slot {t.dst_slots[r]})")
+            checked += 1
+    return checked
 
 
 def run_coresident(t, config, args):
@@ -181,13 +278,15 @@ def run_coresident(t, config, args):
     import sgl_rocm_kv as kv
     from sgl_rocm_kv import hip
     sh = t.shape
-    rb, n, L, T = sh.row_bytes, t.rows, sh.layers, sh.tensors
+    n, L, T = t.rows, sh.layers, sh.tensors
+    rb = [sh.tensor_row_bytes(i) for i in range(T)]
+    lrb = sh.layer_row_bytes           # one token's bytes in one layer, all tensors
     fp8 = config == "c4fp8"
     k = kv.RocmKvPairCopyKernels(0)
     src = hip.DeviceBuffer(t.src.byte_len(sh))
     dst = hip.DeviceBuffer(t.dst.byte_len(sh))
-    xfer = hip.DeviceBuffer(L * T * n * rb)
-    kind = kv.FILL_BITS if fp8 else kv.FILL_BF16_NORMAL
+    xfer = hip.DeviceBuffer(L * n * lrb)
+    kind = kv.FILL_BITS if sh.elt_bytes == 1 else kv.FILL_BF16_NORMAL
     k.fill_synthetic(kv.device_buffer(src.ptr, src.nbytes), 2024, kind)
     k.fill_synthetic(kv.device_buffer(dst.ptr, dst.nbytes), 2025, kind)
     ss = hip.DeviceBuffer.from_array(t.src_slots)
@@ -204,31 +303,37 @@ def run_coresident(t, config, args):
     def sc(i, layer):
         return scales[i].ptr + 4 * layer if scales else None
 
+    # The transfer buffer is [layer][tensor][token][row bytes of the tensor].
+    plane_off = [0] + [n * rb[0]] * (T - 1)
+
+    def row_planes(layer, tt, r):
+        return layer * n * lrb + plane_off[tt] + r * rb[tt]
+
     sviews = [_views(kv, src, t.src, sh, l, sc(0, l)) for l in range(L)]
     dviews = [_views(kv, dst, t.dst, sh, l, sc(2, l)) for l in range(L)]
     rviews = []
     for layer in range(L):
-        base = xfer.ptr + layer * T * n * rb
-        rviews.append(kv.rows_view([base + i * n * rb for i in range(T)], [n * rb] * T, [rb] * T,
-                                   sc(1, layer)))
+        base = xfer.ptr + layer * n * lrb
+        rviews.append(kv.rows_view([base + plane_off[i] for i in range(T)], [n * rb[i] for i in range(T)],
+                                   rb, sc(1, layer)))
 
     # All layers' rows as one view (multi-layer launches): plane t spans the
     # rest of the transfer buffer.
-    all_rows = kv.rows_view([xfer.ptr + i * n * rb for i in range(T)],
-                            [xfer.nbytes - i * n * rb for i in range(T)], [rb] * T, sc(1, 0))
+    all_rows = kv.rows_view([xfer.ptr + plane_off[i] for i in range(T)],
+                            [xfer.nbytes - plane_off[i] for i in range(T)], rb, sc(1, 0))
     s_pack = hip.Stream()
     s_unpack = hip.Stream() if args.streams == 2 else s_pack
     auto = args.launch == "auto"
     if auto:   # measured on MI355X: per-layer launches win on large layers
-        args.launch = "layers" if 2 * T * n * rb < (256 << 20) else "layer"
+        args.launch = "layers" if 2 * n * lrb < (256 << 20) else "layer"
     multi = args.launch == "layers"
     units = 1 if multi else L   # launches of each kind per step
     # Events for every launch of every instrumented step, read after the last
     # step, so that the device never idles between steps.
     ev = [[[hip.Event() for _ in range(4)] for _ in range(units)] for _ in range(args.steps)]
     gate = [hip.Event() for _ in range(units)]
-    pool_stride_s = t.src.page_size * T * rb
-    pool_stride_d = t.dst.page_size * T * rb
+    pool_stride_s = t.src.page_size * lrb
+    pool_stride_d = t.dst.page_size * lrb
 
     def step(e_step):
         for u in range(units):
@@ -236,7 +341,7 @@ def run_coresident(t, config, args):
             if e:
                 e[0].record(s_pack)
             if multi:
-                k.pack_layers(sviews[0], pool_stride_s, L, ssb, n, all_rows, T * n * rb, s_pack)
+                k.pack_layers(sviews[0], pool_stride_s, L, ssb, n, all_rows, n * lrb, s_pack)
             else:
                 k.pack_layer(sviews[u], ssb, n, rviews[u], s_pack)
             (e[1] if e else gate[u]).record(s_pack)
@@ -245,7 +350,7 @@ def run_coresident(t, config, args):
             if e:
                 e[2].record(s_unpack)
             if multi:
-                k.unpack_layers(all_rows, T * n * rb, L, n, dviews[0], pool_stride_d, dsb, s_unpack)
+                k.unpack_layers(all_rows, n * lrb, L, n, dviews[0], pool_stride_d, dsb, s_unpack)
             else:
                 k.unpack_layer(rviews[u], n, dviews[u], dsb, s_unpack)
             if e:
@@ -282,6 +387,8 @@ def run_coresident(t, config, args):
             pack_ms.append(p_ms / (L if multi else 1))
             unpack_ms.append(u_ms / (L if multi else 1))
             layer_us.append((p_ms + u_ms) * 1e3 / (L if multi else 1))
+    checked = verify_sample(t, src, xfer, dst, row_planes)
+    log(f"verified {checked} sampled rows of the measured run (source = transfer row = destination)")
 
     if args.calibration_copy:
         span = min(1 << 30, xfer.nbytes // 2)
@@ -311,25 +418,26 @@ def run_coresident(t, config, args):
 
     step_bytes = t.algorithmic_bytes
     gbs = step_bytes / (wall / args.steps) / 1e9
-    launch_bytes = T * n * rb * 2     # one layer; pack_ms / unpack_ms are per layer
+    launch_bytes = n * lrb * 2        # one layer; pack_ms / unpack_ms are per layer
     avg_pack, avg_unpack = float(np.mean(pack_ms)), float(np.mean(unpack_ms))
     kernel_gbs = step_bytes / (kernel_ms / args.steps / 1e3) / 1e9
-    vb = "v16"
-    dom_name, dom_ms = ((f"sglkv_copy_pool_rows_{vb}", avg_pack) if avg_pack >= avg_unpack
-                        else (f"sglkv_copy_rows_pool_{vb}", avg_unpack))
+    pack_name, unpack_name = _kernel_family(sh)
+    dom_name, dom_ms = ((pack_name, avg_pack) if avg_pack >= avg_unpack else (unpack_name, avg_unpack))
     achieved = launch_bytes / (dom_ms / 1e3) / 1e9
     log(f"pack avg {avg_pack * 1e3:.1f} us ({launch_bytes / avg_pack / 1e6:.0f} GB/s), "
         f"unpack avg {avg_unpack * 1e3:.1f} us ({launch_bytes / avg_unpack / 1e6:.0f} GB/s), "
         f"kernel-sum {kernel_gbs:.0f} GB/s, wall {gbs:.0f} GB/s")
     del src, dst, xfer
     k.close()
+    payload_dtype = "fp8_e4m3" if fp8 else "packed_mla_bytes" if config == "c4packed" else "bf16"
+    extra = {"tokens": n, "layers": L, "kv_heads": sh.heads, "head_dim": sh.head_dim,
+             "row_bytes": rb, "payload_dtype": payload_dtype,
+             "payload_bytes": t.payload_bytes, "algorithmic_bytes_per_step": step_bytes,
+             "streams": args.streams, "launch": args.launch}
     return {
         "value": round(gbs, 1),
         "ms_per_step": round(wall * 1e3 / args.steps, 4),
-        "config_extra": {"tokens": n, "layers": L, "kv_heads": sh.heads, "head_dim": sh.head_dim,
-                         "payload_dtype": "fp8_e4m3" if fp8 else "bf16",
-                         "payload_bytes": t.payload_bytes, "algorithmic_bytes_per_step": step_bytes,
-                         "streams": args.streams, "launch": args.launch},
+        "config_extra": extra,
         "per_layer_p50_us": round(float(np.percentile(layer_us, 50)), 2),
         "copy_ceiling": None if ceiling is None else {
             "gbs": round(ceiling, 1), "value_frac_of_ceiling": round(gbs / ceiling, 4),
@@ -338,6 +446,7 @@ def run_coresident(t, config, args):
         "pack_us_avg": round(avg_pack * 1e3, 2),
         "unpack_us_avg": round(avg_unpack * 1e3, 2),
         "kernel_sum_gbs": round(kernel_gbs, 1),
+        "verified_rows": checked,
         "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      # the committed counter summaries were taken with --launch auto
@@ -922,8 +1031,12 @@ def main():
                          "Default 1: whole layers, every layer's rows in its own region")
     ap.add_argument("--cpu-seconds", type=float, default=6.0,
                     help="seconds of CPU work per CPU-baseline figure")
-    ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1),
-                    help="threads of the all-core CPU baseline (default: the box's share, at most 16)")
+    ap.add_argument("--cpu-threads", type=int, default=_usable_cores(),
+                    help="threads of the all-core CPU baseline (default: every core this process "
+                         "may use)")
+    ap.add_argument("--cpu-full", action="store_true",
+                    help="time the all-core CPU baseline on the whole workload (when host RAM "
+                         "holds both pools and the rows) instead of its first 8192 tokens")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="after timing, run 3 hipMemcpyDtoD copies of exactly 1 GiB: a plain copy "
@@ -940,7 +1053,8 @@ def main():
 
     from sgl_rocm_kv import workloads as wl
     makers = {"c1": wl.c1, "c2": wl.c2, "c3": wl.c3, "c4": wl.c4,
-              "c4fp8": lambda: wl.c4(fp8=True), "c5": wl.c5, "c2pages": wl.c2, "attn": wl.c2,
+              "c4fp8": lambda: wl.c4(fp8=True), "c4pair": wl.c4pair, "c4packed": wl.c4packed,
+              "c5": wl.c5, "c2pages": wl.c2, "attn": wl.c2,
               "attn_hnd": wl.c2, "attn_mla": wl.c4, "attn64": wl.c2, "ceilings": wl.c2, "c2direct": wl.c2}
     attention = args.config in ("attn", "attn_hnd", "attn_mla", "attn64")
     t = makers[args.config]()
@@ -992,11 +1106,20 @@ def main():
                                if attention else cpu_baseline(makers[args.config], args.cpu_seconds,
                                                               direct=direct))
         if not attention and args.cpu_threads > 1:
-            # The same sample on the box's host share of cores, beside the
-            # single-thread figure.
-            log(f"cpu baseline (oracle, {args.cpu_threads} threads)")
+            # Every usable host core, beside the single-thread figure: on the
+            # whole workload with --cpu-full when host RAM holds it, else on
+            # the same sample.
+            full = False
+            if args.cpu_full:
+                need = t.src.byte_len(t.shape) + t.dst.byte_len(t.shape) + t.payload_bytes
+                full = need < _host_ram_bytes() // 2
+                if not full:
+                    log(f"--cpu-full: {need >> 30} GiB would not fit half of host RAM; sampling")
+            log(f"cpu baseline (oracle, {args.cpu_threads} threads, {'full' if full else 'sample'})")
             out["cpu_baseline_all_cores"] = cpu_baseline(makers[args.config], args.cpu_seconds,
+                                                         rows=None if full else 8192,
                                                          threads=args.cpu_threads, direct=direct)
+        out["cpu_baseline"]["host_cores"] = _usable_cores()
     print(json.dumps(out), flush=True)
 
 

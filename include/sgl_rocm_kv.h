@@ -139,7 +139,15 @@ typedef enum sgl_kv_status {
     SGL_KV_BOOT_MISSING_TRANSFER_ROOM = 96,     /* a = room */
     SGL_KV_BOOT_MISSING_KV_ARGS = 97,           /* a = room; the session id is quoted in the message */
     SGL_KV_BOOT_MISSING_AUX_INDEX = 98,         /* the session id is quoted in the message */
-    SGL_KV_BOOT_DECODE_LAYOUT = 99              /* name = what is wrong, a, b = values */
+    SGL_KV_BOOT_DECODE_LAYOUT = 99,             /* name = what is wrong, a, b = values */
+
+    /* 100.. mirror KvCacheLayoutError (crates/sglang-srt/src/kv_cache.rs:227-251) and the
+     * MissingCapabilities of validate_cache_config (crates/sglang-srt/src/backend_model.rs:457-475) */
+    SGL_KV_MODEL_DTYPE_REQUIRES_MODEL_METADATA = 100, /* a = dtype */
+    SGL_KV_MODEL_INVALID_PACKED_MLA_NOPE_HEAD_DIM = 101, /* a = qk_nope_head_dim */
+    SGL_KV_MODEL_ZERO_TENSOR_WIDTH = 102,
+    SGL_KV_MODEL_SIZE_OVERFLOW = 103,
+    SGL_KV_MODEL_MISSING_CAPABILITY = 104       /* the message names the capability; a, b = values */
 } sgl_kv_status;
 
 /* Detail of the calling thread's most recent failure. */
@@ -185,6 +193,57 @@ typedef struct sgl_kv_runtime_layout {
     uint64_t page_size_bytes;
 } sgl_kv_runtime_layout;
 
+/* KvCacheModelLayout (kv_cache.rs:68-225): a model's KV geometry before the
+ * dtype and page size are chosen. Built by the constructors below. */
+typedef enum sgl_kv_tensor_geometry {
+    SGL_KV_GEOMETRY_UNIFORM = 0,      /* multi_tensor: every tensor kv_heads * head_dim elements */
+    SGL_KV_GEOMETRY_PAIR = 1,         /* tensor_pair: key and value widths of their own */
+    SGL_KV_GEOMETRY_PACKED_BYTES = 2  /* packed_bytes_per_layer / packed_mla: a byte row */
+} sgl_kv_tensor_geometry;
+
+typedef struct sgl_kv_model_layout {
+    uint64_t num_layers;
+    uint64_t kv_heads;
+    uint64_t head_dim;
+    uint64_t kv_tensors_per_token;
+    uint64_t bytes_per_token_per_layer; /* PACKED_BYTES: the packed row (Some); 0 = None */
+    uint32_t geometry;                  /* sgl_kv_tensor_geometry */
+    uint32_t reserved;
+    uint64_t key_elements;              /* PAIR only */
+    uint64_t value_elements;            /* PAIR only */
+} sgl_kv_model_layout;
+
+/* KvCacheModelLayout::multi_tensor (kv_cache.rs:89-103); infallible. */
+int32_t sgl_kv_model_layout_multi_tensor(uint64_t num_layers, uint64_t kv_heads, uint64_t head_dim,
+                                         uint64_t kv_tensors_per_token, sgl_kv_model_layout *out);
+/* KvCacheModelLayout::tensor_pair (kv_cache.rs:105-132): SizeOverflow,
+ * ZeroTensorWidth. DeepSeek-V3 builds tensor_pair(L, 1, kv_lora_rank +
+ * qk_rope_head_dim, 1, kv_lora_rank) (models/deepseek.rs:360-369). */
+int32_t sgl_kv_model_layout_tensor_pair(uint64_t num_layers, uint64_t key_heads, uint64_t key_head_dim,
+                                        uint64_t value_heads, uint64_t value_head_dim,
+                                        sgl_kv_model_layout *out);
+/* KvCacheModelLayout::packed_bytes_per_layer (kv_cache.rs:134-143); infallible. */
+int32_t sgl_kv_model_layout_packed_bytes_per_layer(uint64_t num_layers, uint64_t bytes_per_token_per_layer,
+                                                   sgl_kv_model_layout *out);
+/* KvCacheModelLayout::packed_mla (kv_cache.rs:201-224): nope + 2 rope +
+ * nope / 64 + 1 bytes per token per layer (649 for DeepSeek's 512/64,
+ * models/deepseek.rs:1035-1037). InvalidPackedMlaNopeHeadDim unless nope %
+ * 64 == 0; SizeOverflow. */
+int32_t sgl_kv_model_layout_packed_mla(uint64_t num_layers, uint64_t qk_nope_head_dim,
+                                       uint64_t qk_rope_head_dim, sgl_kv_model_layout *out);
+/* elements_per_token (kv_cache.rs:146-158): *has = 0 (None) for packed
+ * layouts and on overflow. */
+int32_t sgl_kv_model_layout_elements_per_token(const sgl_kv_model_layout *layout, uint64_t *out,
+                                               uint32_t *has);
+/* token_size_bytes (kv_cache.rs:160-176): DtypeRequiresModelMetadata (fp4
+ * of a non-packed layout), SizeOverflow. */
+int32_t sgl_kv_model_layout_token_size_bytes(const sgl_kv_model_layout *layout, int32_t dtype,
+                                             uint64_t *out);
+/* tensor_pair_size_bytes (kv_cache.rs:178-199): *is_pair = 0 (None) unless a
+ * tensor pair; then out[0], out[1] = key and value bytes per token per layer. */
+int32_t sgl_kv_model_layout_tensor_pair_size_bytes(const sgl_kv_model_layout *layout, int32_t dtype,
+                                                   uint64_t out[2], uint32_t *is_pair);
+
 /* PagedKvCacheLayout (kv_cache.rs:437-445): page -> layer -> tensor -> token. */
 typedef struct sgl_kv_paged_layout {
     sgl_kv_runtime_layout runtime;
@@ -206,6 +265,14 @@ int32_t sgl_kv_paged_layout_new_with_tensor_pair(const sgl_kv_runtime_layout *ru
                                                  uint64_t page_count, uint64_t key_token_bytes,
                                                  uint64_t value_token_bytes,
                                                  sgl_kv_paged_layout *out);
+/* paged_kv_cache_layout_for_model (crates/sglang-srt/src/backend_model.rs:348-382):
+ * the runtime layout and pool a model gets for `dtype` at `page_size` with
+ * `slot_capacity` slots (slot_capacity / page_size pages): validate_cache_config
+ * (MissingCapability: zero capacity, zero page size, capacity not a multiple
+ * of the page size), token_size_bytes, then new_with_tensor_pair for a pair
+ * geometry and new otherwise. */
+int32_t sgl_kv_paged_layout_for_model(const sgl_kv_model_layout *model, int32_t dtype, uint64_t page_size,
+                                      uint64_t slot_capacity, sgl_kv_paged_layout *out);
 /* PagedKvCacheLayout::page_byte_range (kv_cache.rs:639-651); [start, end). */
 int32_t sgl_kv_paged_layout_page_byte_range(const sgl_kv_paged_layout *layout, uint64_t page_index,
                                             uint64_t *start, uint64_t *end);
@@ -409,19 +476,25 @@ typedef struct sgl_kv_pool_view {
     uint64_t page_stride_bytes; /* page_size_bytes */
     uint64_t page_count;
     uint64_t tensor_offset[2];  /* in-page offset of this layer's tensor regions */
-    uint64_t row_bytes;         /* bytes per (token, tensor): heads * head_dim * element bytes */
+    uint64_t row_bytes;         /* bytes per (token, tensor 0): heads * head_dim * element bytes */
     uint32_t tensor_count;      /* 2 = K/V pair, 1 = single tensor (MLA latent row) */
     uint32_t heads;             /* KV heads; HND splits a row into `heads` chunks */
     uint32_t head_layout;       /* sgl_kv_head_layout */
     uint32_t reserved;
     float *scale;               /* optional device pointer to this layer's tensor_count
                                    quantisation scales (fp8), or NULL */
+    uint64_t value_row_bytes;   /* bytes per (token, tensor 1) when they differ from
+                                   row_bytes (the tensor-pair layout of MLA: keys 576 and
+                                   values 512 wide, kv_cache.rs:480-529); 0 = row_bytes */
 } sgl_kv_pool_view;
 
 /* Builds the view of `layer` for tensors [first_tensor, first_tensor +
  * tensor_count). Errors: layer/tensor out of range (LayerOutOfRange,
- * TensorOutOfRange, kv_cache.rs:672-685); UnevenKvPairCopy when a
- * two-tensor view spans unequal widths (kv_cache.rs:758-763). */
+ * TensorOutOfRange, kv_cache.rs:672-685). A two-tensor view of a tensor-pair
+ * layout carries each tensor's width (value_row_bytes), so one launch moves
+ * a layer of keys and values of unequal widths; the reference's pair copy
+ * rejects such layouts (UnevenKvPairCopy, kv_cache.rs:758-763), and so does
+ * sgl_kv_paged_layout_kv_pair_copy_geometry, its drop-in. */
 int32_t sgl_kv_pool_view_for_layer(const sgl_kv_paged_layout *layout, void *base,
                                    uint64_t byte_len, uint32_t head_layout, uint64_t heads,
                                    uint64_t layer_index, uint64_t first_tensor,
@@ -561,7 +634,8 @@ int32_t sgl_rocm_kv_resolve_spans(sgl_rocm_kv_ctx *ctx, uint64_t page_size, uint
  * layer l crosses the hop and layer l - 1 unpacks. The staged hop stands in
  * for the inter-node link on one GPU. Buffers are double-buffered; events
  * order every reuse. Each send/recv/host buffer holds one layer's rows as
- * [tensor][row][row_bytes] (tensor_count * row_count * row_bytes bytes).
+ * [tensor][row][row bytes of the tensor] (row_count * (row_bytes +
+ * value_row_bytes) bytes for a pair, row_count * row_bytes for one tensor).
  * All buffers are the caller's; host buffers must be pinned (hipHostMalloc)
  * for the copies to be asynchronous. */
 typedef struct sgl_kv_pipeline_desc {
@@ -909,8 +983,9 @@ typedef struct sgl_kv_backend_config {
 /* One side's TransferableKvCacheMemory (defined in the un-vendored
  * nexus-transfer crate, pinned at crates/sglang-srt/Cargo.toml:35; provided
  * by kv_cache.rs's KvCacheMemoryProvider): the pool's layout and its device
- * allocation. Every layer moves its first
- * min(kv_tensors_per_token, 2) tensors. */
+ * allocation. Layouts of one or two tensors per token are moved whole (a
+ * tensor pair of unequal widths in one launch per layer); register rejects
+ * layouts of more tensors. */
 typedef struct sgl_kv_backend_memory {
     sgl_kv_paged_layout layout;
     void *base;
@@ -962,9 +1037,23 @@ int32_t sgl_rocm_kv_backend_register(sgl_rocm_kv_backend *backend,
                                      const sgl_kv_backend_memory *prefill,
                                      const sgl_kv_backend_memory *decode);
 /* Validates the span (prefill slots, decode page table entries) and
- * enqueues its transfer; a span with token_count 0 completes at once. */
+ * enqueues its transfer; a span with token_count 0 completes at once. At
+ * most 1,024 spans may be in flight (DimensionTooLarge beyond): each owns
+ * one of the backend's error words until poll reports it. */
 int32_t sgl_rocm_kv_backend_submit(sgl_rocm_kv_backend *backend,
                                    const sgl_kv_transfer_span_desc *span);
+/* The same with dst_page_table a device pointer (dst_page_table_len int32
+ * entries on the backend's device, valid until the span is reported), as a
+ * decode page table received into device memory: the prefill slots are
+ * validated on the host, the decode slots are resolved on the device
+ * (sgl_rocm_kv_resolve_spans). A row whose page entry is negative, past the
+ * table or past the decode pool is skipped and fails the span: poll reports
+ * it FAILED with SGL_KV_DEVICE_PAGE_INDEX_OUT_OF_RANGE, and the span's other
+ * rows and every other span are moved normally. No counterpart in the
+ * reference, whose Mooncake executor reads the indices on the host
+ * (transfer.rs:2298-2329 reports the failure). */
+int32_t sgl_rocm_kv_backend_submit_device_table(sgl_rocm_kv_backend *backend,
+                                                const sgl_kv_transfer_span_desc *span);
 /* Writes up to `capacity` events for finished spans; *pending = spans
  * submitted, not canceled and not yet reported. Never blocks on transfers. */
 int32_t sgl_rocm_kv_backend_poll(sgl_rocm_kv_backend *backend, sgl_kv_transfer_event *events,
@@ -977,9 +1066,14 @@ int32_t sgl_rocm_kv_backend_wait(sgl_rocm_kv_backend *backend);
 int32_t sgl_rocm_kv_backend_shutdown(sgl_rocm_kv_backend *backend);
 int32_t sgl_rocm_kv_backend_destroy(sgl_rocm_kv_backend *backend);
 
-/* Synchronises `stream`, reads and clears the error word, and maps it to
- * SGL_KV_DEVICE_SLOT_INDEX_OUT_OF_RANGE, _PAGE_INDEX_, _SPAN_ or _REQUEST_
- * (the first raised, in that order). Replaces the flag readback of
+/* After the work queued on `stream`, reads and clears (atomically, on the
+ * device) the error words of the asynchronous calls: the copies' word and
+ * the asynchronous attention's. Maps them to
+ * SGL_KV_DEVICE_PAGE_INDEX_OUT_OF_RANGE, _SPAN_, _SLOT_INDEX_ or _REQUEST_
+ * (the first raised, in that order: a row span resolution could not place
+ * also reaches the copies as a bad slot), then
+ * SGL_KV_ATTN_DEVICE_METADATA_INVALID. The synchronous pair scatter/gather
+ * and paged attention keep words of their own. Replaces the flag readback of
  * cuda_kv_kernels.rs:613-621 for the asynchronous calls. */
 int32_t sgl_rocm_kv_check_errors(sgl_rocm_kv_ctx *ctx, void *stream);
 

@@ -43,6 +43,7 @@ class OraPool(ctypes.Structure):
         ("page_count", ctypes.c_uint64), ("tensor_offset", ctypes.c_uint64 * 2),
         ("row_bytes", ctypes.c_uint64), ("tensors", ctypes.c_uint32),
         ("heads", ctypes.c_uint32), ("hnd", ctypes.c_uint32), ("reserved", ctypes.c_uint32),
+        ("value_row_bytes", ctypes.c_uint64),
     ]
 
 
@@ -166,11 +167,15 @@ class Pool:
     tensors: int
     heads: int
     hnd: bool
+    value_row_bytes: int = 0   # tensor 1's width when it differs (tensor-pair layouts)
+
+    def tensor_row_bytes(self, tensor: int) -> int:
+        return self.value_row_bytes if tensor == 1 and self.value_row_bytes else self.row_bytes
 
     def c(self) -> OraPool:
         off = (ctypes.c_uint64 * 2)(*(list(self.tensor_offset) + [0, 0])[:2])
         return OraPool(self.page_size, self.page_stride, self.page_count, off, self.row_bytes,
-                       self.tensors, self.heads, int(self.hnd), 0)
+                       self.tensors, self.heads, int(self.hnd), 0, self.value_row_bytes)
 
 
 def resolve_slots(pool: Pool, row_count: int, slots=None, page_table=None, spans=None):

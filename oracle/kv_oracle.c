@@ -15,8 +15,11 @@
  *    +11/+19, bytes (seed + 37 r + 13 b) % 251) and numpy fancy indexing.
  *  - ora_pack / ora_unpack / ora_transfer / ora_resolve_slots: numpy
  *    reshape views ([page][layer][tensor][pos][row] for NHD,
- *    [page][layer][tensor][head][pos][chunk] for HND), agreement with the
- *    literal byte-per-thread restatement on NHD pairs, and round trips.
+ *    [page][layer][tensor][head][pos][chunk] for HND; for a tensor pair of
+ *    unequal widths, [page][layer] split at page_size * key bytes into a
+ *    [pos][key] and a [pos][value] view), agreement with the literal
+ *    byte-per-thread restatement on NHD pairs, the asymmetric tensor-pair
+ *    goldens of crates/sglang-srt/tests/kv_cache.rs:180-217, and round trips.
  *  - ora_transfer_page_indices: transfer.rs:679-720 error cases and
  *    crates/sglang-srt/tests/pd_transfer_plan.rs:85-114.
  *  - ora_f32_to_bf16: torch's round-to-nearest-even float32 -> bfloat16.
@@ -30,7 +33,8 @@
 /* Layout (kv_cache.rs:448-777)                                            */
 /* ---------------------------------------------------------------------- */
 
-static int ora_layout_check(const ora_layout *l, uint64_t *per_layer, uint64_t *token_bytes) {
+/* The runtime checks both geometries share (kv_cache.rs:531-586). */
+static int ora_runtime_check(const ora_layout *l, uint64_t *per_layer) {
     if (l->page_count == 0) return ORA_LAYOUT_ZERO_PAGE_COUNT;
     if (l->page_size == 0 || l->num_layers == 0 || l->kv_tensors_per_token == 0 ||
         l->bytes_per_token == 0 || l->page_size_bytes == 0)
@@ -39,6 +43,13 @@ static int ora_layout_check(const ora_layout *l, uint64_t *per_layer, uint64_t *
         return ORA_LAYOUT_RUNTIME_PAGE_SIZE_MISMATCH;
     if (l->bytes_per_token % l->num_layers) return ORA_LAYOUT_UNEVEN_LAYER;
     *per_layer = l->bytes_per_token / l->num_layers;
+    return ORA_OK;
+}
+
+/* Uniform geometry: every tensor takes an equal share (kv_cache.rs:448-478). */
+static int ora_layout_check(const ora_layout *l, uint64_t *per_layer, uint64_t *token_bytes) {
+    int rc = ora_runtime_check(l, per_layer);
+    if (rc) return rc;
     if (*per_layer % l->kv_tensors_per_token) return ORA_LAYOUT_UNEVEN_TENSOR;
     *token_bytes = *per_layer / l->kv_tensors_per_token;
     return ORA_OK;
@@ -78,9 +89,12 @@ int ora_pair_tensor_token_byte_range(const ora_layout *l, uint64_t key_token_byt
                                      uint64_t value_token_bytes, uint64_t page, uint64_t layer,
                                      uint64_t tensor, uint64_t token, uint64_t *start,
                                      uint64_t *end) {
-    uint64_t per_layer, tb;
-    int rc = ora_layout_check(l, &per_layer, &tb);
+    uint64_t per_layer;
+    int rc = ora_runtime_check(l, &per_layer);
     if (rc) return rc;
+    /* the pair's widths need not be equal, but must fill the layer
+     * (TensorPairSizeMismatch, kv_cache.rs:499-508) */
+    if (key_token_bytes + value_token_bytes != per_layer) return ORA_LAYOUT_UNEVEN_TENSOR;
     if (page >= l->page_count) return ORA_LAYOUT_PAGE_OUT_OF_RANGE;
     if (layer >= l->num_layers) return ORA_LAYOUT_LAYER_OUT_OF_RANGE;
     if (tensor >= 2) return ORA_LAYOUT_TENSOR_OUT_OF_RANGE;
@@ -205,13 +219,18 @@ uint32_t ora_resolve_slots(const ora_pool *pool, const uint64_t *slots, const in
     return flag;
 }
 
+uint64_t ora_pool_row_bytes(const ora_pool *pool, uint32_t t) {
+    return t == 1 && pool->value_row_bytes ? pool->value_row_bytes : pool->row_bytes;
+}
+
 uint64_t ora_pool_chunk_offset(const ora_pool *pool, uint64_t slot, uint32_t t, uint32_t h) {
     const uint64_t page = slot / pool->page_size;
     const uint64_t pos = slot % pool->page_size;
-    const uint64_t chunk = pool->row_bytes / pool->heads;
+    const uint64_t rb = ora_pool_row_bytes(pool, t);
+    const uint64_t chunk = rb / pool->heads;
     const uint64_t region = page * pool->page_stride + pool->tensor_offset[t];
     if (pool->hnd) return region + ((uint64_t)h * pool->page_size + pos) * chunk;
-    return region + pos * pool->row_bytes + (uint64_t)h * chunk;
+    return region + pos * rb + (uint64_t)h * chunk;
 }
 
 typedef struct ora_job {
@@ -236,11 +255,11 @@ static void *ora_run(void *arg) {
             if (slot == UINT64_MAX) continue;
             for (uint32_t t = 0; t < tensors; ++t) {
                 uint8_t *out = j->rows_out[t] + r * j->stride[t];
+                const uint64_t rb = ora_pool_row_bytes(pool, t);
                 if (!pool->hnd) {
-                    memcpy(out, j->src_bytes + ora_pool_chunk_offset(pool, slot, t, 0),
-                           pool->row_bytes);
+                    memcpy(out, j->src_bytes + ora_pool_chunk_offset(pool, slot, t, 0), rb);
                 } else {
-                    const uint64_t chunk = pool->row_bytes / pool->heads;
+                    const uint64_t chunk = rb / pool->heads;
                     for (uint32_t h = 0; h < pool->heads; ++h)
                         memcpy(out + h * chunk,
                                j->src_bytes + ora_pool_chunk_offset(pool, slot, t, h), chunk);
@@ -251,11 +270,11 @@ static void *ora_run(void *arg) {
             if (slot == UINT64_MAX) continue;
             for (uint32_t t = 0; t < tensors; ++t) {
                 const uint8_t *in = j->rows_in[t] + r * j->stride[t];
+                const uint64_t rb = ora_pool_row_bytes(pool, t);
                 if (!pool->hnd) {
-                    memcpy(j->dst_bytes + ora_pool_chunk_offset(pool, slot, t, 0), in,
-                           pool->row_bytes);
+                    memcpy(j->dst_bytes + ora_pool_chunk_offset(pool, slot, t, 0), in, rb);
                 } else {
-                    const uint64_t chunk = pool->row_bytes / pool->heads;
+                    const uint64_t chunk = rb / pool->heads;
                     for (uint32_t h = 0; h < pool->heads; ++h)
                         memcpy(j->dst_bytes + ora_pool_chunk_offset(pool, slot, t, h),
                                in + h * chunk, chunk);
@@ -266,11 +285,12 @@ static void *ora_run(void *arg) {
             if (s == UINT64_MAX || d == UINT64_MAX) continue;
             /* Heads are the common unit of both layouts. */
             const uint32_t heads = j->src->heads;
-            const uint64_t chunk = j->src->row_bytes / heads;
-            for (uint32_t t = 0; t < tensors; ++t)
+            for (uint32_t t = 0; t < tensors; ++t) {
+                const uint64_t chunk = ora_pool_row_bytes(j->src, t) / heads;
                 for (uint32_t h = 0; h < heads; ++h)
                     memcpy(j->dst_bytes + ora_pool_chunk_offset(j->dst, d, t, h),
                            j->src_bytes + ora_pool_chunk_offset(j->src, s, t, h), chunk);
+            }
         }
     }
     return NULL;

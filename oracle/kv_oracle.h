@@ -89,14 +89,19 @@ uint32_t ora_ref_scatter_kv_pair_bytes(const uint8_t *keys, const uint8_t *value
 
 /* One layer of a pool. A (page, layer, tensor t) region starts at
  * page * page_stride + tensor_offset[t] and holds page_size rows of
- * row_bytes. NHD: token-major rows. HND: the region is [heads][page_size]
- * [row_bytes / heads]. */
+ * rb_t bytes, rb_0 = row_bytes and rb_1 = value_row_bytes (0: row_bytes;
+ * the tensor-pair layout of kv_cache.rs:480-529 has unequal widths).
+ * NHD: token-major rows. HND: the region is [heads][page_size][rb_t / heads]. */
 typedef struct ora_pool {
     uint64_t page_size, page_stride, page_count;
     uint64_t tensor_offset[2];
     uint64_t row_bytes;
     uint32_t tensors, heads, hnd, reserved;
+    uint64_t value_row_bytes;
 } ora_pool;
+
+/* Bytes per (token, tensor t) of a pool. */
+uint64_t ora_pool_row_bytes(const ora_pool *pool, uint32_t t);
 
 typedef struct ora_span {
     uint32_t row_start, token_offset, token_count, page_table_start;
@@ -113,8 +118,8 @@ uint32_t ora_resolve_slots(const ora_pool *pool, const uint64_t *slots, const in
 /* Byte offset of head chunk h of (slot, tensor t) in the pool. */
 uint64_t ora_pool_chunk_offset(const ora_pool *pool, uint64_t slot, uint32_t t, uint32_t h);
 
-/* Pack: rows[t] + r * stride[t] <- pool row (slot[r], t). Rows whose slot
- * is UINT64_MAX are left untouched. */
+/* Pack: rows[t] + r * stride[t] <- pool row (slot[r], t), rb_t bytes. Rows
+ * whose slot is UINT64_MAX are left untouched. */
 void ora_pack(const ora_pool *pool, const uint8_t *pool_bytes, const uint64_t *row_slots,
               uint64_t row_count, uint8_t *rows0, uint8_t *rows1, uint64_t stride0,
               uint64_t stride1, int threads);

@@ -292,7 +292,7 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
     p.sequence_slots = reinterpret_cast<const uint64_t *>(ssp);
     p.pool = reinterpret_cast<const uint8_t *>(poolp);
     p.output = reinterpret_cast<uint16_t *>(outp);
-    p.flag = ctx->flag;
+    p.flag = ctx->attn_flag;
     p.query_count = c.query_count;
     p.request_count = c.request_count;
     p.sequence_slot_count = c.sequence_slot_count;
@@ -441,7 +441,7 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
         }
         p.partial = static_cast<float *>(ctx->attention_partial);
     }
-    if (clear_flag) SGLKV_CHECK_HIP(hipMemsetAsync(ctx->flag, 0, sizeof(uint32_t), s));
+    if (clear_flag) SGLKV_CHECK_HIP(hipMemsetAsync(ctx->attn_flag, 0, sizeof(uint32_t), s));
     void *args[] = {&p};
     SGLKV_CHECK_HIP(hipModuleLaunchKernel(ctx->attention[which], (unsigned)base, (unsigned)splits, 1, threads,
                                           1, 1, lds, s, args, nullptr));
@@ -465,9 +465,11 @@ extern "C" int32_t sgl_rocm_kv_paged_attention(sgl_rocm_kv_ctx *ctx, const sgl_k
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
     SGLKV_CHECK_HIP(hipStreamSynchronize(s));
     uint32_t flag = 0;
-    SGLKV_CHECK_HIP(hipMemcpy(&flag, ctx->flag, sizeof flag, hipMemcpyDeviceToHost));
-    // A reported error is consumed, as sgl_rocm_kv_check_errors does.
-    if (flag) SGLKV_CHECK_HIP(hipMemset(ctx->flag, 0, sizeof(uint32_t)));
+    SGLKV_CHECK_HIP(hipMemcpy(&flag, ctx->attn_flag, sizeof flag, hipMemcpyDeviceToHost));
+    // A reported error is consumed, as sgl_rocm_kv_check_errors does. The
+    // attention word is its own (the copies raise another), so this read
+    // and clear takes no copy error away from check_errors.
+    if (flag) SGLKV_CHECK_HIP(hipMemset(ctx->attn_flag, 0, sizeof(uint32_t)));
     return attention_flag_status(flag);
 }
 

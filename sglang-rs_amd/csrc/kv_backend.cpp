@@ -38,7 +38,12 @@ struct Transfer {
     hipEvent_t done;
     SlotBuffer slots;
     sgl_rocm_kv_pipeline *pipeline;    // staged mode
+    int32_t word;                      // index of the span's error word (-1: none)
 };
+
+// Error words, one per span in flight: a span's kernels raise only its own
+// word, so poll charges a device error to the span that hit it.
+constexpr uint32_t kSpanWords = 1024;
 
 }  // namespace
 
@@ -51,7 +56,9 @@ struct sgl_rocm_kv_backend {
     uint64_t layer_stride[2] = {0, 0};
     hipStream_t stream = nullptr;      // direct launches
     hipStream_t side = nullptr;        // non-blocking: slot uploads, error-word reads
-    uint32_t *flag_host = nullptr;     // pinned copy of the error word
+    uint32_t *flag_host = nullptr;     // pinned copy of an error word
+    uint32_t *span_words = nullptr;    // device: kSpanWords error words
+    std::vector<int32_t> free_words;
     void *staging_device = nullptr;    // staged: send[2] + recv[2]
     void *staging_host = nullptr;      // staged: host[2] (pinned)
     uint64_t layer_bytes = 0;
@@ -69,9 +76,11 @@ void release_transfer(sgl_rocm_kv_backend *b, Transfer &t) {
     if (t.slots.ptr) b->free_slots.push_back(t.slots);
     if (t.done) (void)hipEventDestroy(t.done);
     if (b->last_done == t.done) b->last_done = nullptr;
+    if (t.word >= 0) b->free_words.push_back(t.word);
     t.pipeline = nullptr;
     t.slots = SlotBuffer{nullptr, 0};
     t.done = nullptr;
+    t.word = -1;
 }
 
 // A free slot buffer of at least `bytes` (the smallest that fits), or a new one.
@@ -98,20 +107,17 @@ void release_staging(sgl_rocm_kv_backend *b) {
     b->staging_device = b->staging_host = nullptr;
 }
 
-// Reads (and clears) the context's device error word without waiting for
-// work queued on other streams. Every span whose completion is reported
-// has finished, so its kernels' bits are in the word; a bit set by a span
-// still running is reported with the next span to complete.
-int32_t read_device_errors(sgl_rocm_kv_backend *b, uint32_t *flag) {
-    uint32_t *word = b->ctx->flag;
-    SGLKV_CHECK_HIP(hipMemcpyAsync(b->flag_host, word, sizeof(uint32_t), hipMemcpyDeviceToHost,
-                                   b->side));
+// Reads a finished span's error word without waiting for work queued on
+// other streams. Only that span's kernels raise the word and they have all
+// finished (its completion event fired), so the read is final; the word is
+// cleared again when a later span takes it.
+int32_t read_span_errors(sgl_rocm_kv_backend *b, const Transfer &t, uint32_t *flag) {
+    *flag = 0;
+    if (t.word < 0) return SGL_KV_OK;
+    SGLKV_CHECK_HIP(hipMemcpyAsync(b->flag_host, b->span_words + t.word, sizeof(uint32_t),
+                                   hipMemcpyDeviceToHost, b->side));
     SGLKV_CHECK_HIP(hipStreamSynchronize(b->side));
     *flag = *b->flag_host;
-    if (*flag) {
-        SGLKV_CHECK_HIP(hipMemsetAsync(word, 0, sizeof(uint32_t), b->side));
-        SGLKV_CHECK_HIP(hipStreamSynchronize(b->side));
-    }
     return SGL_KV_OK;
 }
 
@@ -141,12 +147,17 @@ extern "C" int32_t sgl_rocm_kv_backend_create(sgl_rocm_kv_ctx *ctx, const sgl_kv
     if (err == hipSuccess) err = hipStreamCreate(&b->stream);
     if (err == hipSuccess) err = hipStreamCreateWithFlags(&b->side, hipStreamNonBlocking);
     if (err == hipSuccess) err = hipHostMalloc((void **)&b->flag_host, sizeof(uint32_t), 0);
+    if (err == hipSuccess) err = hipMalloc((void **)&b->span_words, kSpanWords * sizeof(uint32_t));
+    if (err == hipSuccess) err = hipMemset(b->span_words, 0, kSpanWords * sizeof(uint32_t));
     if (err != hipSuccess) {
         if (b->stream) (void)hipStreamDestroy(b->stream);
         if (b->side) (void)hipStreamDestroy(b->side);
+        if (b->flag_host) (void)hipHostFree(b->flag_host);
+        if (b->span_words) (void)hipFree(b->span_words);
         delete b;
         return hip_fail(err, "sgl_rocm_kv_backend_create");
     }
+    for (uint32_t w = kSpanWords; w-- > 0;) b->free_words.push_back((int32_t)w);
     *out = b;
     return ok();
 }
@@ -181,7 +192,13 @@ extern "C" int32_t sgl_rocm_kv_backend_register(sgl_rocm_kv_backend *b,
                         side_names[side], (unsigned long long)m[side]->byte_len,
                         (unsigned long long)m[side]->layout.total_byte_len);
     }
-    const uint64_t tensors = r0.kv_tensors_per_token < 2 ? r0.kv_tensors_per_token : 2;
+    // One view per layer carries both tensors (of unequal widths for the
+    // MLA tensor pair); layouts of more tensors are not moved partially.
+    if (r0.kv_tensors_per_token > 2)
+        return fail(SGL_KV_INVALID_ARGUMENT, "kv_tensors_per_token", r0.kv_tensors_per_token, 2, 0,
+                    "the transfer backend moves layouts of one or two tensors per token, not %llu",
+                    (unsigned long long)r0.kv_tensors_per_token);
+    const uint64_t tensors = r0.kv_tensors_per_token;
     std::vector<sgl_kv_pool_view> views[2];
     for (int side = 0; side < 2; ++side) {
         const uint64_t heads = m[side]->heads ? m[side]->heads : m[side]->layout.runtime.kv_heads;
@@ -192,7 +209,9 @@ extern "C" int32_t sgl_rocm_kv_backend_register(sgl_rocm_kv_backend *b,
                                                  &views[side][l])))
                 return rc;
     }
-    b->layer_bytes = tensors * b->config.max_rows * views[0][0].row_bytes;
+    uint64_t row_bytes = views[0][0].row_bytes + (tensors == 2 ? view_row_bytes(views[0][0], 1) : 0);
+    if (mul_ovf(b->config.max_rows, row_bytes, &b->layer_bytes))
+        return fail(SGL_KV_SHAPE_OVERFLOW, nullptr, 0, 0, 0, "KV copy tensor shape overflowed");
     if (b->config.mode == SGL_KV_BACKEND_STAGED) {
         DeviceScope scope(b->ctx->device);
         hipError_t err = scope.status();
@@ -212,16 +231,25 @@ extern "C" int32_t sgl_rocm_kv_backend_register(sgl_rocm_kv_backend *b,
     return ok();
 }
 
-// KvTransferBackend::submit.
-extern "C" int32_t sgl_rocm_kv_backend_submit(sgl_rocm_kv_backend *b, const sgl_kv_transfer_span_desc *span) {
+namespace {
+
+// KvTransferBackend::submit. With `device_table`, span->dst_page_table is a
+// device pointer and the decode slots are resolved on the device into the
+// span's slot buffer; otherwise the table is a host array, checked entry by
+// entry here.
+int32_t submit_span(sgl_rocm_kv_backend *b, const sgl_kv_transfer_span_desc *span, bool device_table) {
     int32_t rc = check_backend(b);
     if (rc) return rc;
     if (!span) return fail(SGL_KV_INVALID_ARGUMENT, "span", 0, 0, 0, "null span");
     if (!b->registered) return fail(SGL_KV_INVALID_ARGUMENT, "register", 0, 0, 0, "no memory is registered");
     const uint64_t n = span->token_count;
     if (n > b->config.max_rows) return too_large_rows(n, b->config.max_rows);
+    if (b->free_words.empty())
+        return fail(SGL_KV_DIMENSION_TOO_LARGE, "spans in flight", kSpanWords + 1, kSpanWords, 0,
+                    "more than %u spans in flight: poll before submitting more", kSpanWords);
     Transfer t;
     memset(&t, 0, sizeof t);
+    t.word = -1;
     t.room = span->bootstrap_room;
     memcpy(t.checksum, span->descriptor_checksum, 64);
     t.checksum[64] = '\0';
@@ -235,6 +263,13 @@ extern "C" int32_t sgl_rocm_kv_backend_submit(sgl_rocm_kv_backend *b, const sgl_
     }
     if (!span->cache_slots || !span->dst_page_table)
         return fail(SGL_KV_INVALID_ARGUMENT, "cache_slots/dst_page_table", 0, 0, 0, "null argument");
+    if (device_table) {
+        uint64_t table_bytes;
+        if (mul_ovf(span->dst_page_table_len, sizeof(int32_t), &table_bytes))
+            return fail(SGL_KV_SHAPE_OVERFLOW, nullptr, 0, 0, 0, "KV copy tensor shape overflowed");
+        const sgl_kv_device_buffer table{const_cast<int32_t *>(span->dst_page_table), table_bytes};
+        if ((rc = check_device(b->ctx, "dst_page_table", table))) return rc;
+    }
     // Prefill slots: PagedKvCacheLayout::validate_slot_indices (kv_cache.rs:722-736).
     if ((rc = sgl_kv_paged_layout_validate_slot_indices(&b->memory[0].layout, span->cache_slots, n)))
         return rc;
@@ -242,42 +277,92 @@ extern "C" int32_t sgl_rocm_kv_backend_submit(sgl_rocm_kv_backend *b, const sgl_
     // page dst_page_table[k / page_size] at position k % page_size.
     const sgl_kv_paged_layout &dl = b->memory[1].layout;
     const uint64_t P = dl.runtime.page_size;
-    std::vector<uint64_t> slots(2 * n);
-    memcpy(slots.data(), span->cache_slots, n * sizeof(uint64_t));
-    for (uint64_t i = 0; i < n; ++i) {
-        const uint64_t token = span->token_offset + i;
-        const uint64_t index = token / P;
-        if (index >= span->dst_page_table_len)
-            return fail(SGL_KV_INVALID_ARGUMENT, "dst_page_table", index, span->dst_page_table_len, 0,
-                        "token %llu needs page-table entry %llu of %llu", (unsigned long long)token,
-                        (unsigned long long)index, (unsigned long long)span->dst_page_table_len);
-        const int32_t page = span->dst_page_table[index];
-        if (page < 0 || (uint64_t)page >= dl.page_count)
-            return fail(SGL_KV_LAYOUT_PAGE_OUT_OF_RANGE, nullptr, (uint64_t)(int64_t)page, dl.page_count, 0,
-                        "KV cache page index %d is outside %llu pages", page,
-                        (unsigned long long)dl.page_count);
-        slots[n + i] = (uint64_t)page * P + token % P;
+    if (device_table && (P > UINT32_MAX || span->token_offset + n > UINT32_MAX))
+        return too_large_dim("token_offset + token_count", span->token_offset + n, UINT32_MAX);
+    // The upload holds the prefill slots, then (host table) the decode
+    // slots, or (device table) the one span the resolve kernel reads.
+    std::vector<uint64_t> upload(2 * n + (device_table ? 2 : 0));
+    memcpy(upload.data(), span->cache_slots, n * sizeof(uint64_t));
+    if (device_table) {
+        const sgl_kv_span one{0, (uint32_t)span->token_offset, (uint32_t)n, 0};
+        memcpy(&upload[2 * n], &one, sizeof one);
+    } else {
+        for (uint64_t i = 0; i < n; ++i) {
+            const uint64_t token = span->token_offset + i;
+            const uint64_t index = token / P;
+            if (index >= span->dst_page_table_len)
+                return fail(SGL_KV_INVALID_ARGUMENT, "dst_page_table", index, span->dst_page_table_len, 0,
+                            "token %llu needs page-table entry %llu of %llu", (unsigned long long)token,
+                            (unsigned long long)index, (unsigned long long)span->dst_page_table_len);
+            const int32_t page = span->dst_page_table[index];
+            if (page < 0 || (uint64_t)page >= dl.page_count)
+                return fail(SGL_KV_LAYOUT_PAGE_OUT_OF_RANGE, nullptr, (uint64_t)(int64_t)page, dl.page_count, 0,
+                            "KV cache page index %d is outside %llu pages", page,
+                            (unsigned long long)dl.page_count);
+            upload[n + i] = (uint64_t)page * P + token % P;
+        }
     }
-    // The upload goes through the side stream, so that it does not wait
-    // for earlier spans still running on the transfer streams; the buffer
-    // is free, so no running span reads it.
-    if ((rc = take_slot_buffer(b, 2 * n * sizeof(uint64_t), &t.slots))) return rc;
-    hipError_t err = hipMemcpyAsync(t.slots.ptr, slots.data(), 2 * n * sizeof(uint64_t),
-                                    hipMemcpyHostToDevice, b->side);
+    // The upload and the clear of the span's error word go through the side
+    // stream, so that they do not wait for earlier spans still running on
+    // the transfer streams; the buffer and the word are free, so no running
+    // span reads them.
+    const uint64_t bytes = upload.size() * sizeof(uint64_t);
+    if ((rc = take_slot_buffer(b, bytes, &t.slots))) return rc;
+    t.word = b->free_words.back();
+    b->free_words.pop_back();
+    uint32_t *word = b->span_words + t.word;
+    hipError_t err = hipMemcpyAsync(t.slots.ptr, upload.data(), bytes, hipMemcpyHostToDevice, b->side);
+    if (err == hipSuccess) err = hipMemsetAsync(word, 0, sizeof(uint32_t), b->side);
     if (err == hipSuccess) err = hipStreamSynchronize(b->side);
     if (err == hipSuccess) err = hipEventCreateWithFlags(&t.done, hipEventDisableTiming);
     if (err != hipSuccess) {
         release_transfer(b, t);
         return hip_fail(err, "sgl_rocm_kv_backend_submit");
     }
-    sgl_kv_device_buffer src_slots{t.slots.ptr, n * sizeof(uint64_t)};
-    sgl_kv_device_buffer dst_slots{static_cast<uint64_t *>(t.slots.ptr) + n, n * sizeof(uint64_t)};
+    uint64_t *slot_words = static_cast<uint64_t *>(t.slots.ptr);
+    sgl_kv_device_buffer src_slots{slot_words, n * sizeof(uint64_t)};
+    sgl_kv_device_buffer dst_slots{slot_words + n, n * sizeof(uint64_t)};
     const uint32_t layers = (uint32_t)b->views[0].size();
+    hipEvent_t resolved = nullptr;  // staged: the device-side resolve precedes the pipeline
+    if (device_table) {
+        // Staged spans share the staging set, so even the resolve waits for
+        // the previous span; direct spans are ordered by b->stream itself.
+        if (b->config.mode == SGL_KV_BACKEND_STAGED && b->last_done)
+            err = hipStreamWaitEvent(b->stream, b->last_done, 0);
+        sglkv_resolve_params rp;
+        memset(&rp, 0, sizeof rp);
+        rp.spans = reinterpret_cast<const sglkv_span *>(slot_words + 2 * n);
+        rp.page_table = span->dst_page_table;
+        rp.out_slots = slot_words + n;
+        rp.flag = word;
+        rp.page_table_len = span->dst_page_table_len;
+        rp.page_count = dl.page_count;
+        rp.span_count = 1;
+        rp.page_size = (uint32_t)P;
+        rp.rows = (uint32_t)n;
+        void *args[] = {&rp};
+        if (err == hipSuccess)
+            err = hipModuleLaunchKernel(b->ctx->resolve, (unsigned)((n + SGLKV_BLOCK_THREADS - 1) / SGLKV_BLOCK_THREADS),
+                                        1, 1, SGLKV_BLOCK_THREADS, 1, 1, 0, b->stream, args, nullptr);
+        if (err == hipSuccess && b->config.mode == SGL_KV_BACKEND_STAGED) {
+            err = hipEventCreateWithFlags(&resolved, hipEventDisableTiming);
+            if (err == hipSuccess) err = hipEventRecord(resolved, b->stream);
+        }
+        if (err != hipSuccess) {
+            if (resolved) (void)hipEventDestroy(resolved);
+            (void)hipStreamSynchronize(b->stream);
+            release_transfer(b, t);
+            return hip_fail(err, "sgl_rocm_kv_backend_submit_device_table");
+        }
+    }
     if (b->config.mode == SGL_KV_BACKEND_DIRECT) {
         Launch l;
         rc = prepare_transfer(b->ctx, &b->views[0][0], &src_slots, n, &b->views[1][0], &dst_slots, &l,
                               layers, b->layer_stride[0], b->layer_stride[1]);
-        if (!rc) rc = submit_launch(b->ctx, l, b->stream);
+        if (!rc) {
+            set_launch_flag(l, word);
+            rc = submit_launch(b->ctx, l, b->stream);
+        }
         if (!rc && (err = hipEventRecord(t.done, b->stream)) != hipSuccess) rc = hip_fail(err, "hipEventRecord");
     } else {
         sgl_kv_pipeline_desc d;
@@ -298,12 +383,15 @@ extern "C" int32_t sgl_rocm_kv_backend_submit(sgl_rocm_kv_backend *b, const sgl_
         }
         d.host_bytes = b->layer_bytes;
         rc = sgl_rocm_kv_pipeline_create(b->ctx, &d, &t.pipeline);
-        // Spans share the staging buffers: each starts after the previous one.
-        if (!rc) rc = sgl_rocm_kv_pipeline_run(t.pipeline, b->last_done);
+        if (!rc) pipeline_set_error_word(t.pipeline, word);
+        // Spans share the staging buffers: each starts after the previous
+        // one (or after its own resolve, which waited for it).
+        if (!rc) rc = sgl_rocm_kv_pipeline_run(t.pipeline, resolved ? resolved : b->last_done);
         if (!rc && (err = hipEventRecord(t.done, pipeline_final_stream(t.pipeline))) != hipSuccess)
             rc = hip_fail(err, "hipEventRecord");
         if (!rc) b->last_done = t.done;
     }
+    if (resolved) (void)hipEventDestroy(resolved);
     if (rc) {
         // Nothing was enqueued after a failed preparation; a failed enqueue
         // leaves work that must drain before the buffers are reused.
@@ -314,6 +402,17 @@ extern "C" int32_t sgl_rocm_kv_backend_submit(sgl_rocm_kv_backend *b, const sgl_
     }
     b->inflight.push_back(t);
     return ok();
+}
+
+}  // namespace
+
+extern "C" int32_t sgl_rocm_kv_backend_submit(sgl_rocm_kv_backend *b, const sgl_kv_transfer_span_desc *span) {
+    return submit_span(b, span, false);
+}
+
+extern "C" int32_t sgl_rocm_kv_backend_submit_device_table(sgl_rocm_kv_backend *b,
+                                                           const sgl_kv_transfer_span_desc *span) {
+    return submit_span(b, span, true);
 }
 
 // KvTransferBackend::poll: each finished span once, in submission order
@@ -347,10 +446,11 @@ extern "C" int32_t sgl_rocm_kv_backend_poll(sgl_rocm_kv_backend *b, sgl_kv_trans
             return hip_fail(q, "hipEventQuery");
         }
         if (!t.canceled) {
-            // A device-side error (none is expected after host validation)
-            // fails the span that observed it.
+            // A device-side error fails the span that raised it (a decode
+            // page-table entry the device-side resolve found out of range;
+            // host-validated spans raise none).
             uint32_t flag = 0;
-            if ((rc = read_device_errors(b, &flag))) {
+            if ((rc = read_span_errors(b, t, &flag))) {
                 still.insert(still.end(), b->inflight.begin() + i, b->inflight.end());
                 b->inflight.swap(still);
                 return rc;
@@ -420,6 +520,7 @@ extern "C" int32_t sgl_rocm_kv_backend_destroy(sgl_rocm_kv_backend *b) {
         if (b->stream) (void)hipStreamDestroy(b->stream);
         if (b->side) (void)hipStreamDestroy(b->side);
         if (b->flag_host) (void)hipHostFree(b->flag_host);
+        if (b->span_words) (void)hipFree(b->span_words);
     }
     delete b;
     return ok();

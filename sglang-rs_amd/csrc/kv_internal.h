@@ -25,23 +25,40 @@ void set_detail_d(uint64_t d);
 
 // Geometry common to both sides of a copy.
 struct RowShape {
-    uint64_t row_bytes;
+    uint64_t row_bytes[2];  // per tensor (equal unless a pair of unequal widths)
     uint32_t tensors;
     uint32_t heads;  // > 1 only when a side is head-major
     bool split;      // some side is HND: copy head chunk by head chunk
+    uint64_t chunk(uint32_t t) const { return split ? row_bytes[t] / heads : row_bytes[t]; }
 };
+
+// Bytes per (token, tensor t) of a pool view: value_row_bytes 0 means both
+// tensors are row_bytes wide.
+inline uint64_t view_row_bytes(const sgl_kv_pool_view &v, uint32_t t) {
+    return t == 1 && v.value_row_bytes ? v.value_row_bytes : v.row_bytes;
+}
 
 // A validated copy launch: kernel parameters plus launch geometry.
 struct Launch {
     sglkv_copy_params params;
+    sglkv_realign_params realign;  // used when `realigned`
     RowShape shape;
     int kind;         // 0 pool->rows, 1 rows->pool, 2 pool->pool
     int width_index;  // vector width 16, 8, 4, 2, 1
+    bool realigned;   // the byte-realigning kernel (16-byte accesses at any alignment)
+    uint32_t lds_bytes;  // dynamic LDS of the realigning kernel
     uint64_t rows;
     uint64_t grid;
     uint32_t layers;  // grid y: one layer per row of workgroups
     uint32_t block_x, block_y;
 };
+
+// Replaces the device error word a validated launch raises (default: the
+// context's copy word).
+inline void set_launch_flag(Launch &l, uint32_t *flag) {
+    l.params.flag = flag;
+    l.realign.flag = flag;
+}
 
 // Layer span of a multi-layer launch: `count` layers, each side's data
 // `pool_stride` / `rows_stride` bytes after the previous layer's.
@@ -64,6 +81,7 @@ int32_t prepare_transfer(const sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src
                          uint64_t dst_layer_stride);
 int32_t submit_launch(sgl_rocm_kv_ctx *ctx, Launch &l, hipStream_t stream);
 hipStream_t pipeline_final_stream(sgl_rocm_kv_pipeline *pipe);
+void pipeline_set_error_word(sgl_rocm_kv_pipeline *pipe, uint32_t *flag);
 int32_t hip_fail(hipError_t err, const char *call);
 int32_t flag_status(uint32_t flag);
 int32_t attention_flag_status(uint32_t flag);
@@ -99,7 +117,9 @@ struct sgl_rocm_kv_ctx {
     int cu_count;
     hipModule_t module;
     hipFunction_t copy[5][3];
+    hipFunction_t realign[3];       // byte-realigning copies: pool->rows, rows->pool, pool->pool
     hipFunction_t resolve;
+    hipFunction_t take_flags;       // atomic read-and-clear of error words
     hipFunction_t fill;
     hipFunction_t requests;
     hipFunction_t pair_slots[2];    // key+value slot writes: 16-byte, 1-byte pieces
@@ -112,7 +132,13 @@ struct sgl_rocm_kv_ctx {
     uint32_t attention_occupancy[9];      // resident workgroups per CU of attention[i] ...
     uint32_t attention_occupancy_lds[9];  // ... at this LDS size (0 = not yet queried)
     int max_lds_per_block;                // device limit on a workgroup's LDS bytes
-    uint32_t *flag;                 // device error word, at the start of a small zeroed block
+    // Device error words, at the start of a small zeroed block: one per
+    // consumer, as the reference keeps one flag per kernels object
+    // (cuda_kv_kernels.rs:421, 460-461; cuda_attention.rs:667, 706-707), so that one
+    // consumer's read-and-clear never takes another's bits.
+    uint32_t *flag;                 // asynchronous copies, span resolution, page requests
+    uint32_t *attn_flag;            // paged attention
+    uint32_t *pair_flag;            // the synchronous pair scatter/gather drop-ins
     const uint8_t *zero_row;        // SGLKV_ZERO_ROW_BYTES of zeros inside that block
     void *attention_partial;        // split records, grown on demand
     uint64_t attention_partial_bytes;

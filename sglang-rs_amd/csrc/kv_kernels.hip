@@ -99,82 +99,104 @@ template <> struct sglkv_vec<4> { typedef uint32_t type; };
 template <> struct sglkv_vec<2> { typedef uint16_t type; };
 template <> struct sglkv_vec<1> { typedef uint8_t type; };
 
-// Byte offset (relative to plane[t]) of `row`'s data in a POOL side, or
-// SGLKV_INVALID_OFFSET after flagging a slot outside the pool. The host
-// guarantees slot_count < 2^32, so the page split runs in 32 bits.
-__device__ __forceinline__ uint64_t sglkv_pool_row_offset(const sglkv_side &s, uint32_t row,
-                                                         uint32_t *flag) {
+// Byte offsets (relative to plane[0] and plane[1]) of `row`'s tensor rows
+// in a POOL side: page * page stride + pos * pos_mult[t], or
+// SGLKV_INVALID_OFFSET for both after flagging a slot outside the pool. The
+// host guarantees slot_count < 2^32, so the page split runs in 32 bits.
+__device__ __forceinline__ void sglkv_pool_row(const sglkv_side &s, uint32_t row, uint32_t *flag,
+                                               uint64_t *off0, uint64_t *off1) {
     const uint64_t slot = s.slots[row];
     if (slot >= s.slot_count) {
         atomicOr(flag, SGLKV_FLAG_SLOT);
-        return SGLKV_INVALID_OFFSET;
+        *off0 = *off1 = SGLKV_INVALID_OFFSET;
+        return;
     }
     const uint32_t sl = static_cast<uint32_t>(slot);
     const uint32_t page = sl / s.page_size;
     const uint32_t pos = sl - page * s.page_size;
-    return static_cast<uint64_t>(page) * s.stride[0] + static_cast<uint64_t>(pos) * s.pos_mult;
+    const uint64_t base = static_cast<uint64_t>(page) * s.stride[0];
+    *off0 = base + static_cast<uint64_t>(pos) * s.pos_mult[0];
+    *off1 = base + static_cast<uint64_t>(pos) * s.pos_mult[1];
+}
+
+// Stages the tile's pool-row offsets in LDS (s_src[t][i], s_dst[t][i]:
+// tensor t's row of tile row i) and returns whether the tile is "clean":
+// every one of its rows exists and resolved to a valid slot.
+template <uint32_t SK, uint32_t DK>
+__device__ __forceinline__ bool sglkv_stage_tile(const sglkv_side &src, const sglkv_side &dst, uint32_t *flag,
+                                                 uint64_t row0, uint32_t tile, uint32_t rows, uint64_t *s_src0,
+                                                 uint64_t *s_src1, uint64_t *s_dst0, uint64_t *s_dst1) {
+    const uint32_t nthreads = blockDim.x * blockDim.y;
+    const uint32_t tid = threadIdx.y * blockDim.x + threadIdx.x;
+    // 64-bit: the last tile may reach past 2^32 rows.
+    int bad = row0 + tile > rows;
+    if (SK == SGLKV_SIDE_POOL || DK == SGLKV_SIDE_POOL) {
+        for (uint32_t i = tid; i < tile; i += nthreads) {
+            const uint64_t r = row0 + i;
+            if (r < rows) {
+                if (SK == SGLKV_SIDE_POOL) {
+                    sglkv_pool_row(src, static_cast<uint32_t>(r), flag, &s_src0[i], &s_src1[i]);
+                    bad |= s_src0[i] == SGLKV_INVALID_OFFSET;
+                }
+                if (DK == SGLKV_SIDE_POOL) {
+                    sglkv_pool_row(dst, static_cast<uint32_t>(r), flag, &s_dst0[i], &s_dst1[i]);
+                    bad |= s_dst0[i] == SGLKV_INVALID_OFFSET;
+                }
+            }
+        }
+    }
+    return !__syncthreads_or(bad);
+}
+
+// Per-layer quantisation scales ride along bit-exactly (workgroup 0 of each layer).
+__device__ __forceinline__ void sglkv_copy_scales(const float *src, float *dst, uint32_t count) {
+    const uint32_t tid = threadIdx.y * blockDim.x + threadIdx.x;
+    if (blockIdx.x == 0 && tid < count) {
+        const uint32_t i = blockIdx.y * count + tid;
+        reinterpret_cast<uint32_t *>(dst)[i] = reinterpret_cast<const uint32_t *>(src)[i];
+    }
 }
 
 template <int VB, uint32_t SK, uint32_t DK, int NT, int REMAP>
 __device__ __forceinline__ void sglkv_copy_rows(const sglkv_copy_params &p) {
     typedef typename sglkv_vec<VB>::type V;
     constexpr uint32_t RU = SGLKV_ROWS_PER_THREAD;
-    __shared__ uint64_t s_src[SGLKV_MAX_TILE_ROWS];
-    __shared__ uint64_t s_dst[SGLKV_MAX_TILE_ROWS];
+    __shared__ uint64_t s_src[2][SGLKV_MAX_TILE_ROWS];
+    __shared__ uint64_t s_dst[2][SGLKV_MAX_TILE_ROWS];
 
     const uint32_t tile = p.tile_rows;
-    const uint32_t row0 = sglkv_tile_index<REMAP>() * tile;
-    const uint32_t nthreads = blockDim.x * blockDim.y;
-    const uint32_t tid = threadIdx.y * blockDim.x + threadIdx.x;
+    const uint64_t row0 = static_cast<uint64_t>(sglkv_tile_index<REMAP>()) * tile;
 
-    // A tile is "clean" when every one of its rows exists and resolved to a
-    // valid offset; clean tiles (all but the last tile, unless a slot is bad)
-    // copy without per-row predicates, so the compiler can pipeline the
-    // stores behind the loads instead of draining the memory counter at
-    // every branch.
-    int bad = row0 + tile > p.rows;
-    if (SK == SGLKV_SIDE_POOL || DK == SGLKV_SIDE_POOL) {
-        for (uint32_t i = tid; i < tile; i += nthreads) {
-            const uint32_t r = row0 + i;
-            if (r < p.rows) {
-                if (SK == SGLKV_SIDE_POOL) {
-                    s_src[i] = sglkv_pool_row_offset(p.src, r, p.flag);
-                    bad |= s_src[i] == SGLKV_INVALID_OFFSET;
-                }
-                if (DK == SGLKV_SIDE_POOL) {
-                    s_dst[i] = sglkv_pool_row_offset(p.dst, r, p.flag);
-                    bad |= s_dst[i] == SGLKV_INVALID_OFFSET;
-                }
-            }
-        }
-    }
-    const bool clean = !__syncthreads_or(bad);
-    // Per-layer quantisation scales ride along bit-exactly.
+    // Clean tiles (all but the last tile, unless a slot is bad) copy without
+    // per-row predicates, so the compiler can pipeline the stores behind the
+    // loads instead of draining the memory counter at every branch.
+    const bool clean = sglkv_stage_tile<SK, DK>(p.src, p.dst, p.flag, row0, tile, p.rows, s_src[0], s_src[1],
+                                                s_dst[0], s_dst[1]);
+    sglkv_copy_scales(p.scale_src, p.scale_dst, p.scale_count);
     const uint32_t layer = blockIdx.y;
-    if (blockIdx.x == 0 && tid < p.scale_count) {
-        const uint32_t i = layer * p.scale_count + tid;
-        reinterpret_cast<uint32_t *>(p.scale_dst)[i] = reinterpret_cast<const uint32_t *>(p.scale_src)[i];
-    }
 
     for (uint32_t j = threadIdx.x; j < p.vpr; j += blockDim.x) {
-        const uint32_t t = j / p.vpt;
-        const uint32_t jt = j - t * p.vpt;
-        const uint32_t h = jt / p.vpc;
-        const uint32_t jc = jt - h * p.vpc;
         // Select rather than index the kernel-argument arrays: a dynamic
         // index would copy the struct to scratch.
+        const uint32_t t = j >= p.vpt;
+        const uint32_t jt = t ? j - p.vpt : j;
+        const uint32_t vpc = t ? p.vpc[1] : p.vpc[0];
+        const uint32_t h = jt / vpc;
+        const uint32_t jc = jt - h * vpc;
         const uint64_t src_plane =
             (t ? p.src.plane[1] : p.src.plane[0]) + static_cast<uint64_t>(layer) * p.src.layer_stride;
         const uint64_t dst_plane =
             (t ? p.dst.plane[1] : p.dst.plane[0]) + static_cast<uint64_t>(layer) * p.dst.layer_stride;
         const uint64_t src_stride = t ? p.src.stride[1] : p.src.stride[0];
         const uint64_t dst_stride = t ? p.dst.stride[1] : p.dst.stride[0];
-        sglkv_gsrc *sb = reinterpret_cast<sglkv_gsrc *>(src_plane +
-                                                       static_cast<uint64_t>(h) * p.src.head_stride +
-                                                       static_cast<uint64_t>(jc) * VB);
-        sglkv_gdst *db = reinterpret_cast<sglkv_gdst *>(dst_plane +
-                                                       static_cast<uint64_t>(h) * p.dst.head_stride +
-                                                       static_cast<uint64_t>(jc) * VB);
+        const uint64_t *so_t = s_src[t];
+        const uint64_t *do_t = s_dst[t];
+        sglkv_gsrc *sb = reinterpret_cast<sglkv_gsrc *>(
+            src_plane + static_cast<uint64_t>(h) * (t ? p.src.head_stride[1] : p.src.head_stride[0]) +
+            static_cast<uint64_t>(jc) * VB);
+        sglkv_gdst *db = reinterpret_cast<sglkv_gdst *>(
+            dst_plane + static_cast<uint64_t>(h) * (t ? p.dst.head_stride[1] : p.dst.head_stride[0]) +
+            static_cast<uint64_t>(jc) * VB);
 
         typedef __attribute__((address_space(1))) const V gload_t;
         typedef __attribute__((address_space(1))) V gstore_t;
@@ -183,15 +205,13 @@ __device__ __forceinline__ void sglkv_copy_rows(const sglkv_copy_params &p) {
 #pragma unroll
             for (uint32_t k = 0; k < RU; ++k) {
                 const uint32_t i = threadIdx.y + k * blockDim.y;
-                const uint64_t so =
-                    SK == SGLKV_SIDE_POOL ? s_src[i] : static_cast<uint64_t>(row0 + i) * src_stride;
+                const uint64_t so = SK == SGLKV_SIDE_POOL ? so_t[i] : (row0 + i) * src_stride;
                 buf[k] = sglkv_load<V, NT>(reinterpret_cast<gload_t *>(sb + so));
             }
 #pragma unroll
             for (uint32_t k = 0; k < RU; ++k) {
                 const uint32_t i = threadIdx.y + k * blockDim.y;
-                const uint64_t dof =
-                    DK == SGLKV_SIDE_POOL ? s_dst[i] : static_cast<uint64_t>(row0 + i) * dst_stride;
+                const uint64_t dof = DK == SGLKV_SIDE_POOL ? do_t[i] : (row0 + i) * dst_stride;
                 sglkv_store<V, NT>(reinterpret_cast<gstore_t *>(db + dof), buf[k]);
             }
             continue;
@@ -202,13 +222,159 @@ __device__ __forceinline__ void sglkv_copy_rows(const sglkv_copy_params &p) {
 #pragma unroll 1
         for (uint32_t k = 0; k < RU; ++k) {
             const uint32_t i = threadIdx.y + k * blockDim.y;
-            const uint32_t r = row0 + i;
+            const uint64_t r = row0 + i;
             if (r >= p.rows) break;
-            const uint64_t so = SK == SGLKV_SIDE_POOL ? s_src[i] : static_cast<uint64_t>(r) * src_stride;
-            const uint64_t dof = DK == SGLKV_SIDE_POOL ? s_dst[i] : static_cast<uint64_t>(r) * dst_stride;
+            const uint64_t so = SK == SGLKV_SIDE_POOL ? so_t[i] : r * src_stride;
+            const uint64_t dof = DK == SGLKV_SIDE_POOL ? do_t[i] : r * dst_stride;
             if (so == SGLKV_INVALID_OFFSET || dof == SGLKV_INVALID_OFFSET) continue;
             sglkv_store<V, NT>(reinterpret_cast<gstore_t *>(db + dof),
                                sglkv_load<V, NT>(reinterpret_cast<gload_t *>(sb + so)));
+        }
+    }
+}
+
+// Dword `i` (0..3) of a 16-byte vector held in four registers, by selects
+// (a dynamically indexed register array would live in scratch).
+__device__ __forceinline__ uint32_t sglkv_dword(uint32_t i, uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
+    return i == 0 ? w0 : i == 1 ? w1 : i == 2 ? w2 : w3;
+}
+
+// Writes bytes [lo, hi) of the 16-byte vector (w0..w3) whose aligned
+// destination is `d`, as naturally aligned 8, 4, 2 and 1-byte stores.
+template <int NT>
+__device__ __forceinline__ void sglkv_store_partial(uint64_t d, uint32_t lo, uint32_t hi, uint32_t w0,
+                                                    uint32_t w1, uint32_t w2, uint32_t w3) {
+    uint32_t pos = lo;
+#pragma unroll 1
+    while (pos < hi) {
+        const uint32_t rem = hi - pos;
+        const uint32_t a = sglkv_dword(pos >> 2, w0, w1, w2, w3);
+        const uint32_t sh = 8u * (pos & 3u);
+        if ((pos & 7u) == 0 && rem >= 8) {
+            const sglkv_v2u v = {a, sglkv_dword((pos >> 2) + 1, w0, w1, w2, w3)};
+            sglkv_store<sglkv_v2u, NT>(reinterpret_cast<__attribute__((address_space(1))) sglkv_v2u *>(d + pos), v);
+            pos += 8;
+        } else if ((pos & 3u) == 0 && rem >= 4) {
+            sglkv_store<uint32_t, NT>(reinterpret_cast<__attribute__((address_space(1))) uint32_t *>(d + pos), a);
+            pos += 4;
+        } else if ((pos & 1u) == 0 && rem >= 2) {
+            sglkv_store<uint16_t, NT>(reinterpret_cast<__attribute__((address_space(1))) uint16_t *>(d + pos),
+                                      static_cast<uint16_t>(a >> sh));
+            pos += 2;
+        } else {
+            sglkv_store<uint8_t, NT>(reinterpret_cast<__attribute__((address_space(1))) uint8_t *>(d + pos),
+                                     static_cast<uint8_t>(a >> sh));
+            pos += 1;
+        }
+    }
+}
+
+// The byte-realigning copy (sglkv_realign_params): every global access an
+// aligned 16-byte vector, whatever the row width and stride. Thread x owns
+// LDS vector x of each row (blockDim.x == vrow), thread y a row of each
+// group of blockDim.y rows.
+template <uint32_t SK, uint32_t DK, int NT, int REMAP>
+__device__ __forceinline__ void sglkv_realign_rows(const sglkv_realign_params &p) {
+    constexpr uint32_t RU = SGLKV_REALIGN_ROWS_PER_THREAD;
+    extern __shared__ __attribute__((aligned(16))) uint8_t sglkv_realign_lds[];
+    const uint32_t tile = p.tile_rows;
+    uint64_t *s_src0 = reinterpret_cast<uint64_t *>(sglkv_realign_lds);
+    uint64_t *s_src1 = s_src0 + tile;
+    uint64_t *s_dst0 = s_src1 + tile;
+    uint64_t *s_dst1 = s_dst0 + tile;
+    // The tile's rows, after a 16-byte pad (16-byte aligned).
+    uint8_t *data = reinterpret_cast<uint8_t *>(s_dst1 + tile) + 16;
+
+    const uint64_t row0 = static_cast<uint64_t>(sglkv_tile_index<REMAP>()) * tile;
+    sglkv_stage_tile<SK, DK>(p.src, p.dst, p.flag, row0, tile, p.rows, s_src0, s_src1, s_dst0, s_dst1);
+    sglkv_copy_scales(p.scale_src, p.scale_dst, p.scale_count);
+    const uint32_t layer = blockIdx.y;
+
+    const uint32_t j = threadIdx.x;
+    const uint32_t t = j >= p.vt0;
+    const uint32_t jt = t ? j - p.vt0 : j;
+    const uint32_t seg = t ? p.seg[1] : p.seg[0];
+    const uint32_t h = jt / seg;
+    const uint32_t m = jt - h * seg;
+    const uint32_t c = t ? p.chunk[1] : p.chunk[0];
+    const uint64_t src_base = (t ? p.src.plane[1] : p.src.plane[0]) +
+                              static_cast<uint64_t>(layer) * p.src.layer_stride +
+                              static_cast<uint64_t>(h) * (t ? p.src.head_stride[1] : p.src.head_stride[0]);
+    const uint64_t dst_base = (t ? p.dst.plane[1] : p.dst.plane[0]) +
+                              static_cast<uint64_t>(layer) * p.dst.layer_stride +
+                              static_cast<uint64_t>(h) * (t ? p.dst.head_stride[1] : p.dst.head_stride[0]);
+    const uint64_t src_stride = t ? p.src.stride[1] : p.src.stride[0];
+    const uint64_t dst_stride = t ? p.dst.stride[1] : p.dst.stride[0];
+    const uint64_t *so_t = t ? s_src1 : s_src0;
+    const uint64_t *do_t = t ? s_dst1 : s_dst0;
+    // This thread's LDS vector within a row's area: segment start + m.
+    uint8_t *lds_vec = data + 16u * j;
+    const uint32_t seg_lds = (j - m) * 16u;
+    const uint32_t row_lds = p.vrow * 16u;
+
+    typedef __attribute__((address_space(1))) const sglkv_v4u gload_t;
+    typedef __attribute__((address_space(1))) sglkv_v4u gstore_t;
+
+    // Phase 1: the aligned source vectors covering each segment -> LDS.
+    // Every lane loads (lanes with nothing to load read the context's zero
+    // row), so no branch separates the loads and all RU stay in flight.
+    sglkv_v4u buf[RU];
+    uint32_t live = 0;
+    const uint64_t zero = reinterpret_cast<uint64_t>(p.zero);
+#pragma unroll
+    for (uint32_t k = 0; k < RU; ++k) {
+        const uint32_t i = threadIdx.y + k * blockDim.y;
+        const uint64_t r = row0 + i;
+        const uint64_t so = SK == SGLKV_SIDE_POOL ? so_t[i] : r * src_stride;
+        const uint64_t dof = DK == SGLKV_SIDE_POOL ? do_t[i] : 0;
+        const uint64_t s = src_base + so;
+        const uint32_t sa = static_cast<uint32_t>(s & 15u);
+        const bool ok = r < p.rows && so != SGLKV_INVALID_OFFSET && dof != SGLKV_INVALID_OFFSET &&
+                        m < ((sa + c + 15u) >> 4);
+        buf[k] = sglkv_load<sglkv_v4u, NT>(reinterpret_cast<gload_t *>(ok ? s - sa + 16u * m : zero));
+        live |= static_cast<uint32_t>(ok) << k;
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < RU; ++k) {
+        const uint32_t i = threadIdx.y + k * blockDim.y;
+        if (live & (1u << k)) *reinterpret_cast<sglkv_v4u *>(lds_vec + i * row_lds) = buf[k];
+    }
+    __syncthreads();
+
+    // Phase 2: each aligned destination vector of each segment, shifted out
+    // of LDS by the source/destination misalignment.
+#pragma unroll 1
+    for (uint32_t k = 0; k < RU; ++k) {
+        const uint32_t i = threadIdx.y + k * blockDim.y;
+        const uint64_t r = row0 + i;
+        if (r >= p.rows) break;
+        const uint64_t so = SK == SGLKV_SIDE_POOL ? so_t[i] : r * src_stride;
+        const uint64_t dof = DK == SGLKV_SIDE_POOL ? do_t[i] : r * dst_stride;
+        if (so == SGLKV_INVALID_OFFSET || dof == SGLKV_INVALID_OFFSET) continue;
+        const uint32_t sa = static_cast<uint32_t>((src_base + so) & 15u);
+        const uint64_t d = dst_base + dof;
+        const uint32_t da = static_cast<uint32_t>(d & 15u);
+        if (m >= ((da + c + 15u) >> 4)) continue;
+        // Segment byte b sits at LDS offset seg + sa + b; destination vector
+        // m starts at segment byte 16 m - da. The offset is at least
+        // seg - 15, inside the front pad for the first segment.
+        const int32_t o = static_cast<int32_t>(i * row_lds + seg_lds + sa + 16u * m) - static_cast<int32_t>(da);
+        const uint32_t *wp = reinterpret_cast<const uint32_t *>(data + (o & ~3));
+        const uint32_t sh = static_cast<uint32_t>(o) & 3u;
+        const uint32_t x0 = wp[0], x1 = wp[1], x2 = wp[2], x3 = wp[3], x4 = wp[4];
+        const uint32_t w0 = __builtin_amdgcn_alignbyte(x1, x0, sh);
+        const uint32_t w1 = __builtin_amdgcn_alignbyte(x2, x1, sh);
+        const uint32_t w2 = __builtin_amdgcn_alignbyte(x3, x2, sh);
+        const uint32_t w3 = __builtin_amdgcn_alignbyte(x4, x3, sh);
+        const uint64_t dv = d - da + 16u * m;
+        const uint32_t lo = m == 0 ? da : 0u;
+        const uint32_t end = da + c - 16u * m;
+        const uint32_t hi = end < 16u ? end : 16u;
+        if (lo == 0 && hi == 16u) {
+            const sglkv_v4u v = {w0, w1, w2, w3};
+            sglkv_store<sglkv_v4u, NT>(reinterpret_cast<gstore_t *>(dv), v);
+        } else {
+            sglkv_store_partial<NT>(dv, lo, hi, w0, w1, w2, w3);
         }
     }
 }
@@ -243,6 +409,19 @@ SGLKV_COPY_KERNELS(8)
 SGLKV_COPY_KERNELS(4)
 SGLKV_COPY_KERNELS(2)
 SGLKV_COPY_KERNELS(1)
+
+#define SGLKV_REALIGN_KERNEL(SK, DK, NT, REMAP, NAME)                                  \
+    extern "C" __global__ __launch_bounds__(SGLKV_BLOCK_THREADS) void NAME(            \
+        const sglkv_realign_params p) {                                                \
+        sglkv_realign_rows<SK, DK, NT, REMAP>(p);                                      \
+    }
+
+SGLKV_REALIGN_KERNEL(SGLKV_SIDE_POOL, SGLKV_SIDE_ROWS, SGLKV_PACK_NT, SGLKV_PACK_REMAP,
+                     sglkv_realign_pool_rows)
+SGLKV_REALIGN_KERNEL(SGLKV_SIDE_ROWS, SGLKV_SIDE_POOL, SGLKV_UNPACK_NT, SGLKV_UNPACK_REMAP,
+                     sglkv_realign_rows_pool)
+SGLKV_REALIGN_KERNEL(SGLKV_SIDE_POOL, SGLKV_SIDE_POOL, SGLKV_TRANSFER_NT, SGLKV_TRANSFER_REMAP,
+                     sglkv_realign_pool_pool)
 
 // Spans + page table -> one physical slot per row (the decode side's
 // dst_kv_indices, crates/sglang-srt/src/pd_bootstrap.rs:416-494, expanded to
@@ -283,6 +462,14 @@ extern "C" __global__ __launch_bounds__(SGLKV_BLOCK_THREADS) void sglkv_resolve_
         }
     }
     p.out_slots[r] = out;
+}
+
+// Reads and clears error words in one atomic step each: out[i] <-
+// *words[i], *words[i] <- 0. A bit raised by work still running elsewhere
+// lands either in this read or in the word afterwards, never in neither.
+extern "C" __global__ void sglkv_take_flags(uint32_t *word0, uint32_t *word1, uint32_t *out) {
+    if (threadIdx.x == 0) out[0] = atomicExch(word0, 0u);
+    if (threadIdx.x == 1) out[1] = atomicExch(word1, 0u);
 }
 
 // Synthetic-input generator for benchmarks and tests (no reference

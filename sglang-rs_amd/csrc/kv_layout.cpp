@@ -90,6 +90,11 @@ extern "C" const char *sgl_kv_status_name(int32_t code) {
     case SGL_KV_BOOT_MISSING_KV_ARGS: return "MissingKvArgsRegistration";
     case SGL_KV_BOOT_MISSING_AUX_INDEX: return "MissingAuxIndex";
     case SGL_KV_BOOT_DECODE_LAYOUT: return "DecodeLayout";
+    case SGL_KV_MODEL_DTYPE_REQUIRES_MODEL_METADATA: return "DtypeRequiresModelMetadata";
+    case SGL_KV_MODEL_INVALID_PACKED_MLA_NOPE_HEAD_DIM: return "InvalidPackedMlaNopeHeadDim";
+    case SGL_KV_MODEL_ZERO_TENSOR_WIDTH: return "ZeroTensorWidth";
+    case SGL_KV_MODEL_SIZE_OVERFLOW: return "SizeOverflow";
+    case SGL_KV_MODEL_MISSING_CAPABILITY: return "MissingCapabilities";
     case SGL_KV_LAYOUT_KV_PAIR_REQUIRES_TWO_TENSORS: return "KvPairRequiresTwoTensors";
     case SGL_KV_LAYOUT_TENSOR_PAIR_REQUIRES_TWO_TENSORS: return "TensorPairRequiresTwoTensors";
     case SGL_KV_LAYOUT_TENSOR_PAIR_SIZE_MISMATCH: return "TensorPairSizeMismatch";
@@ -130,6 +135,150 @@ extern "C" size_t sgl_kv_dtype_bytes_per_element(int32_t dtype) {
     case SGL_KV_DTYPE_FP8_E5M2: return 1;
     default: return 0;
     }
+}
+
+// --- KvCacheModelLayout (crates/sglang-srt/src/kv_cache.rs:68-225) ---
+
+static const char *dtype_name(int32_t dtype) {
+    // KvCacheDtype::as_str (kv_cache.rs:28-37)
+    switch (dtype) {
+    case SGL_KV_DTYPE_AUTO: return "auto";
+    case SGL_KV_DTYPE_FLOAT32: return "float32";
+    case SGL_KV_DTYPE_BFLOAT16: return "bfloat16";
+    case SGL_KV_DTYPE_FP8_E4M3: return "fp8_e4m3";
+    case SGL_KV_DTYPE_FP8_E5M2: return "fp8_e5m2";
+    case SGL_KV_DTYPE_FP4_E2M1: return "fp4_e2m1";
+    default: return "unknown";
+    }
+}
+
+static int32_t model_overflow() {
+    return fail(SGL_KV_MODEL_SIZE_OVERFLOW, nullptr, 0, 0, 0, "KV cache layout byte size overflowed");
+}
+
+static int32_t model_dtype_width(int32_t dtype, uint64_t *width) {
+    *width = sgl_kv_dtype_bytes_per_element(dtype);
+    if (*width == 0)
+        return fail(SGL_KV_MODEL_DTYPE_REQUIRES_MODEL_METADATA, nullptr, (uint64_t)(int64_t)dtype, 0, 0,
+                    "KV cache dtype %s requires model metadata for byte width", dtype_name(dtype));
+    return SGL_KV_OK;
+}
+
+extern "C" int32_t sgl_kv_model_layout_multi_tensor(uint64_t num_layers, uint64_t kv_heads, uint64_t head_dim,
+                                                    uint64_t kv_tensors_per_token, sgl_kv_model_layout *out) {
+    if (!out) return fail(SGL_KV_INVALID_ARGUMENT, "out", 0, 0, 0, "null argument");
+    memset(out, 0, sizeof *out);
+    out->num_layers = num_layers;
+    out->kv_heads = kv_heads;
+    out->head_dim = head_dim;
+    out->kv_tensors_per_token = kv_tensors_per_token;
+    out->geometry = SGL_KV_GEOMETRY_UNIFORM;
+    return ok();
+}
+
+extern "C" int32_t sgl_kv_model_layout_tensor_pair(uint64_t num_layers, uint64_t key_heads, uint64_t key_head_dim,
+                                                   uint64_t value_heads, uint64_t value_head_dim,
+                                                   sgl_kv_model_layout *out) {
+    if (!out) return fail(SGL_KV_INVALID_ARGUMENT, "out", 0, 0, 0, "null argument");
+    uint64_t key_elements, value_elements;
+    if (mul_ovf(key_heads, key_head_dim, &key_elements) || mul_ovf(value_heads, value_head_dim, &value_elements))
+        return model_overflow();
+    if (key_elements == 0 || value_elements == 0)
+        return fail(SGL_KV_MODEL_ZERO_TENSOR_WIDTH, nullptr, 0, 0, 0, "KV cache tensor width must be non-zero");
+    memset(out, 0, sizeof *out);
+    out->num_layers = num_layers;
+    out->kv_heads = key_heads;
+    out->head_dim = key_head_dim;
+    out->kv_tensors_per_token = 2;
+    out->geometry = SGL_KV_GEOMETRY_PAIR;
+    out->key_elements = key_elements;
+    out->value_elements = value_elements;
+    return ok();
+}
+
+extern "C" int32_t sgl_kv_model_layout_packed_bytes_per_layer(uint64_t num_layers, uint64_t bytes_per_token_per_layer,
+                                                              sgl_kv_model_layout *out) {
+    if (!out) return fail(SGL_KV_INVALID_ARGUMENT, "out", 0, 0, 0, "null argument");
+    memset(out, 0, sizeof *out);
+    out->num_layers = num_layers;
+    out->kv_heads = 1;
+    out->head_dim = bytes_per_token_per_layer;
+    out->kv_tensors_per_token = 1;
+    out->bytes_per_token_per_layer = bytes_per_token_per_layer;
+    out->geometry = SGL_KV_GEOMETRY_PACKED_BYTES;
+    return ok();
+}
+
+extern "C" int32_t sgl_kv_model_layout_packed_mla(uint64_t num_layers, uint64_t qk_nope_head_dim,
+                                                  uint64_t qk_rope_head_dim, sgl_kv_model_layout *out) {
+    if (!out) return fail(SGL_KV_INVALID_ARGUMENT, "out", 0, 0, 0, "null argument");
+    if (qk_nope_head_dim % 64)
+        return fail(SGL_KV_MODEL_INVALID_PACKED_MLA_NOPE_HEAD_DIM, nullptr, qk_nope_head_dim, 0, 0,
+                    "qk_nope_head_dim must be divisible by 64 for packed MLA KV layout: %llu",
+                    (unsigned long long)qk_nope_head_dim);
+    // nope + 2 * rope + nope / 64 + 1 bytes, checked as the reference adds them
+    uint64_t bytes;
+    if (mul_ovf(qk_rope_head_dim, 2, &bytes) || add_ovf(qk_nope_head_dim, bytes, &bytes) ||
+        add_ovf(bytes, qk_nope_head_dim / 64, &bytes) || add_ovf(bytes, 1, &bytes))
+        return model_overflow();
+    return sgl_kv_model_layout_packed_bytes_per_layer(num_layers, bytes, out);
+}
+
+extern "C" int32_t sgl_kv_model_layout_elements_per_token(const sgl_kv_model_layout *l, uint64_t *out,
+                                                          uint32_t *has) {
+    if (!l || !out || !has) return fail(SGL_KV_INVALID_ARGUMENT, "layout/out/has", 0, 0, 0, "null argument");
+    *out = 0;
+    *has = 0;
+    uint64_t per_layer;
+    if (l->geometry == SGL_KV_GEOMETRY_UNIFORM) {
+        if (mul_ovf(l->kv_tensors_per_token, l->kv_heads, &per_layer) || mul_ovf(per_layer, l->head_dim, &per_layer))
+            return ok();
+    } else if (l->geometry == SGL_KV_GEOMETRY_PAIR) {
+        if (add_ovf(l->key_elements, l->value_elements, &per_layer)) return ok();
+    } else {
+        return ok();
+    }
+    if (mul_ovf(l->num_layers, per_layer, out)) {
+        *out = 0;
+        return ok();
+    }
+    *has = 1;
+    return ok();
+}
+
+extern "C" int32_t sgl_kv_model_layout_token_size_bytes(const sgl_kv_model_layout *l, int32_t dtype, uint64_t *out) {
+    if (!l || !out) return fail(SGL_KV_INVALID_ARGUMENT, "layout/out", 0, 0, 0, "null argument");
+    *out = 0;
+    if (l->geometry == SGL_KV_GEOMETRY_PACKED_BYTES || l->bytes_per_token_per_layer) {
+        if (mul_ovf(l->num_layers, l->bytes_per_token_per_layer, out)) return model_overflow();
+        return ok();
+    }
+    uint64_t elements;
+    uint32_t has;
+    sgl_kv_model_layout_elements_per_token(l, &elements, &has);
+    if (!has) return model_overflow();
+    uint64_t width;
+    int32_t rc = model_dtype_width(dtype, &width);
+    if (rc) return rc;
+    if (mul_ovf(elements, width, out)) return model_overflow();
+    return ok();
+}
+
+extern "C" int32_t sgl_kv_model_layout_tensor_pair_size_bytes(const sgl_kv_model_layout *l, int32_t dtype,
+                                                              uint64_t out[2], uint32_t *is_pair) {
+    if (!l || !out || !is_pair) return fail(SGL_KV_INVALID_ARGUMENT, "layout/out/is_pair", 0, 0, 0, "null argument");
+    out[0] = out[1] = 0;
+    *is_pair = 0;
+    if (l->geometry != SGL_KV_GEOMETRY_PAIR) return ok();
+    uint64_t width;
+    int32_t rc = model_dtype_width(dtype, &width);
+    if (rc) return rc;
+    if (mul_ovf(l->key_elements, width, &out[0]) || mul_ovf(l->value_elements, width, &out[1])) {
+        out[0] = out[1] = 0;
+        return model_overflow();
+    }
+    *is_pair = 1;
+    return ok();
 }
 
 static int32_t layout_overflow() {
@@ -530,6 +679,43 @@ extern "C" int32_t sgl_kv_transfer_page_indices(uint64_t request_index, uint64_t
     return ok();
 }
 
+// paged_kv_cache_layout_for_model (crates/sglang-srt/src/backend_model.rs:348-382).
+extern "C" int32_t sgl_kv_paged_layout_for_model(const sgl_kv_model_layout *model, int32_t dtype,
+                                                 uint64_t page_size, uint64_t slot_capacity,
+                                                 sgl_kv_paged_layout *out) {
+    if (!model || !out) return fail(SGL_KV_INVALID_ARGUMENT, "model/out", 0, 0, 0, "null argument");
+    // validate_cache_config (backend_model.rs:457-475)
+    if (slot_capacity == 0)
+        return fail(SGL_KV_MODEL_MISSING_CAPABILITY, "slot_capacity", 0, 0, 0,
+                    "missing capabilities: non-zero KV cache slot capacity");
+    if (page_size == 0)
+        return fail(SGL_KV_MODEL_MISSING_CAPABILITY, "page_size", 0, 0, 0,
+                    "missing capabilities: non-zero KV cache page size");
+    if (slot_capacity % page_size)
+        return fail(SGL_KV_MODEL_MISSING_CAPABILITY, "slot_capacity", slot_capacity, page_size, 0,
+                    "missing capabilities: KV cache slot capacity %llu divisible by page size %llu",
+                    (unsigned long long)slot_capacity, (unsigned long long)page_size);
+    uint64_t bytes_per_token, pair[2];
+    uint32_t is_pair;
+    int32_t rc = sgl_kv_model_layout_token_size_bytes(model, dtype, &bytes_per_token);
+    if (rc) return rc;
+    if ((rc = sgl_kv_model_layout_tensor_pair_size_bytes(model, dtype, pair, &is_pair))) return rc;
+    sgl_kv_runtime_layout rt;
+    memset(&rt, 0, sizeof rt);
+    if (mul_ovf(page_size, bytes_per_token, &rt.page_size_bytes))
+        return fail(SGL_KV_MODEL_SIZE_OVERFLOW, nullptr, 0, 0, 0, "KV page size overflowed");
+    rt.dtype = dtype;
+    rt.page_size = page_size;
+    rt.num_layers = model->num_layers;
+    rt.kv_heads = model->kv_heads;
+    rt.head_dim = model->head_dim;
+    rt.kv_tensors_per_token = model->kv_tensors_per_token;
+    rt.bytes_per_token = bytes_per_token;
+    const uint64_t page_count = slot_capacity / page_size;
+    if (is_pair) return sgl_kv_paged_layout_new_with_tensor_pair(&rt, page_count, pair[0], pair[1], out);
+    return sgl_kv_paged_layout_new(&rt, page_count, out);
+}
+
 // View of one layer of a paged pool for the per-layer copies.
 extern "C" int32_t sgl_kv_pool_view_for_layer(const sgl_kv_paged_layout *layout, void *base,
                                               uint64_t byte_len, uint32_t head_layout,
@@ -558,15 +744,11 @@ extern "C" int32_t sgl_kv_pool_view_for_layer(const sgl_kv_paged_layout *layout,
         if (rc) return rc;
         if (add_ovf(to[t], layer_off, &to[t])) return layout_overflow();
     }
-    if (tensor_count == 2 && tb[0] != tb[1])
-        return fail(SGL_KV_LAYOUT_UNEVEN_KV_PAIR_COPY, nullptr, tb[0], tb[1], 0,
-                    "the selected KV copy/attention kernel requires equal key and value widths, "
-                    "but the layout has %llu key bytes and %llu value bytes per token",
-                    (unsigned long long)tb[0], (unsigned long long)tb[1]);
-    if (heads == 0 || heads > UINT32_MAX || tb[0] % heads)
-        return fail(SGL_KV_INVALID_ARGUMENT, "heads", heads, tb[0], 0,
-                    "%llu heads do not split a %llu-byte row evenly", (unsigned long long)heads,
-                    (unsigned long long)tb[0]);
+    for (uint64_t t = 0; t < tensor_count; ++t)
+        if (heads == 0 || heads > UINT32_MAX || tb[t] % heads)
+            return fail(SGL_KV_INVALID_ARGUMENT, "heads", heads, tb[t], 0,
+                        "%llu heads do not split a %llu-byte row evenly", (unsigned long long)heads,
+                        (unsigned long long)tb[t]);
     sgl_kv_pool_view v;
     memset(&v, 0, sizeof v);
     v.base = base;
@@ -577,6 +759,7 @@ extern "C" int32_t sgl_kv_pool_view_for_layer(const sgl_kv_paged_layout *layout,
     v.tensor_offset[0] = to[0];
     v.tensor_offset[1] = to[1];
     v.row_bytes = tb[0];
+    v.value_row_bytes = tensor_count == 2 && tb[1] != tb[0] ? tb[1] : 0;
     v.tensor_count = (uint32_t)tensor_count;
     v.heads = (uint32_t)heads;
     v.head_layout = head_layout;

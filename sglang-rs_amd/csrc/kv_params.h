@@ -67,14 +67,18 @@ typedef struct sglkv_side {
     uint64_t plane[2];      /* byte address of tensor t's data (see above) */
     uint64_t stride[2];     /* ROWS: row stride of tensor t; POOL: page stride (both) */
     const uint64_t *slots;  /* POOL: physical slot of each row */
-    uint64_t pos_mult;      /* POOL: bytes between adjacent in-page positions */
-    uint64_t head_stride;   /* bytes between head chunks of one row */
+    uint64_t pos_mult[2];   /* POOL: bytes between adjacent in-page positions of tensor t */
+    uint64_t head_stride[2];/* bytes between head chunks of one row of tensor t */
     uint64_t slot_count;    /* POOL: valid slots are [0, slot_count) */
     uint64_t layer_stride;  /* bytes between consecutive layers' data (blockIdx.y = layer) */
     uint32_t page_size;     /* POOL: tokens per page */
     uint32_t reserved;
 } sglkv_side;
 
+/* The two tensors of a row may differ in width (MLA's 576/512-dim pair):
+ * tensor 0 owns the row's first vpt vectors, tensor 1 the remaining
+ * vpr - vpt, and each tensor's row is cut into head chunks of vpc[t]
+ * vectors. */
 typedef struct sglkv_copy_params {
     sglkv_side src;
     sglkv_side dst;
@@ -84,10 +88,54 @@ typedef struct sglkv_copy_params {
     uint32_t scale_count;   /* floats to copy per layer (0: none) */
     uint32_t rows;          /* rows in this launch */
     uint32_t vpr;           /* vectors per row, all tensors */
-    uint32_t vpt;           /* vectors per tensor row */
-    uint32_t vpc;           /* vectors per head chunk */
+    uint32_t vpt;           /* vectors of tensor 0's row */
+    uint32_t vpc[2];        /* vectors per head chunk of tensor t */
     uint32_t tile_rows;     /* rows per workgroup = blockDim.y * rows per thread */
+    uint32_t reserved;
 } sglkv_copy_params;
+
+/* Byte-realigning copy: for rows whose chunks are not whole 16-byte vectors
+ * at 16-byte aligned addresses (packed-MLA rows of 649 bytes, odd row
+ * strides), every memory access is still an aligned 16-byte vector.
+ * Segment (t, h) of a row is head chunk h of tensor t: chunk[t] bytes from
+ * source address S to destination address D. The workgroup loads the
+ * aligned 16-byte vectors covering [S, S + chunk) into LDS (seg[t] vectors
+ * reserved per segment, enough for any alignment), then builds each
+ * aligned destination vector of [D, D + chunk) from LDS shifted by
+ * (S - D) mod 16 and stores it; the partial first and last vectors are
+ * written as aligned 8/4/2/1-byte pieces. A row occupies vrow LDS vectors:
+ * tensor 0's heads[0] segments (vt0 vectors), then tensor 1's. */
+typedef struct sglkv_realign_params {
+    sglkv_side src;
+    sglkv_side dst;
+    uint32_t *flag;
+    float *scale_src;
+    float *scale_dst;
+    uint32_t scale_count;
+    uint32_t rows;
+    uint32_t chunk[2];      /* bytes per segment of tensor t */
+    uint32_t seg[2];        /* LDS vectors per segment of tensor t: (chunk + 30) / 16 */
+    uint32_t vt0;           /* LDS vectors of tensor 0's segments */
+    uint32_t vrow;          /* LDS vectors per row */
+    uint32_t tile_rows;     /* rows per workgroup = blockDim.y * rows per thread */
+    uint32_t rows_per_thread;
+    const uint8_t *zero;    /* 16 readable bytes (the context's zero row): the load of lanes
+                               with nothing to load */
+} sglkv_realign_params;
+
+/* Realigning kernel limits: rows a thread keeps in flight, and the LDS bytes
+ * a workgroup's tile of rows may take (the launcher shrinks the tile to
+ * fit; rows wider than SGLKV_REALIGN_MAX_ROW_VECTORS vectors use the plain
+ * kernels with narrower accesses). The LDS buffer carries 16 bytes of
+ * padding before the first row and SGLKV_REALIGN_TAIL_PAD after the last,
+ * so that the shifted reads of the first and last vectors stay inside it. */
+#define SGLKV_REALIGN_ROWS_PER_THREAD 8u
+#define SGLKV_REALIGN_MAX_ROW_VECTORS 256u
+#define SGLKV_REALIGN_TAIL_PAD 32u
+/* Dynamic LDS of a realigning workgroup: the tile's staged row offsets
+ * (one per tensor and side), the front pad, the rows and the tail pad. */
+#define SGLKV_REALIGN_LDS_BYTES(tile_rows, vrow)                                                   \
+    (32u * (tile_rows) + 16u + 16u * (tile_rows) * (vrow) + SGLKV_REALIGN_TAIL_PAD)
 
 /* One request's run of rows (KvCacheTransferSpan,
  * crates/sglang-srt/src/transfer.rs:495-505): rows [row_start, row_start +

@@ -30,7 +30,7 @@ struct sgl_rocm_kv_pipeline {
     sgl_rocm_kv_ctx *ctx = nullptr;
     uint32_t layers = 0;
     bool staged = false;
-    uint64_t layer_bytes = 0;  // one layer's rows: tensors * row_count * row_bytes
+    uint64_t layer_bytes = 0;  // one layer's rows: row_count * (key + value row bytes)
     std::vector<Launch> pack, unpack;
     void *send[2] = {nullptr, nullptr};
     void *recv[2] = {nullptr, nullptr};
@@ -62,16 +62,18 @@ struct sgl_rocm_kv_pipeline {
 
 namespace {
 
-// Rows view of one layer inside a [tensor][row][row_bytes] buffer.
+// Rows view of one layer inside a [tensor][row][row bytes of the tensor]
+// buffer (tensor 1's plane follows tensor 0's rows).
 sgl_kv_rows_view layer_rows(void *base, uint64_t byte_len, uint32_t tensors, uint64_t rows,
-                            uint64_t row_bytes) {
+                            const uint64_t row_bytes[2]) {
     sgl_kv_rows_view v;
     memset(&v, 0, sizeof v);
-    const uint64_t plane = rows * row_bytes;
+    uint64_t at = 0;
     for (uint32_t t = 0; t < tensors; ++t) {
-        v.planes[t] = static_cast<char *>(base) + t * plane;
-        v.plane_bytes[t] = byte_len > t * plane ? byte_len - t * plane : 0;
-        v.row_stride[t] = row_bytes;
+        v.planes[t] = static_cast<char *>(base) + at;
+        v.plane_bytes[t] = byte_len > at ? byte_len - at : 0;
+        v.row_stride[t] = row_bytes[t];
+        at += rows * row_bytes[t];
     }
     return v;
 }
@@ -97,10 +99,13 @@ extern "C" int32_t sgl_rocm_kv_pipeline_create(sgl_rocm_kv_ctx *ctx, const sgl_k
                     "a pipeline needs at least one layer and both layer view arrays");
     const sgl_kv_pool_view &first = d->src_layers[0];
     const uint32_t tensors = first.tensor_count;
-    const uint64_t row_bytes = first.row_bytes;
-    uint64_t layer_bytes;
-    if (mul_ovf(d->row_count, row_bytes, &layer_bytes) || mul_ovf(layer_bytes, tensors, &layer_bytes))
-        return fail(SGL_KV_SHAPE_OVERFLOW, nullptr, 0, 0, 0, "KV copy tensor shape overflowed");
+    const uint64_t row_bytes[2] = {first.row_bytes, view_row_bytes(first, 1)};
+    uint64_t layer_bytes = 0;
+    for (uint32_t t = 0; t < tensors && t < 2; ++t) {
+        uint64_t plane;
+        if (mul_ovf(d->row_count, row_bytes[t], &plane) || add_ovf(layer_bytes, plane, &layer_bytes))
+            return fail(SGL_KV_SHAPE_OVERFLOW, nullptr, 0, 0, 0, "KV copy tensor shape overflowed");
+    }
     int32_t rc;
     for (int b = 0; b < 2; ++b) {
         static const char *const send_names[2] = {"send[0]", "send[1]"};
@@ -129,8 +134,9 @@ extern "C" int32_t sgl_rocm_kv_pipeline_create(sgl_rocm_kv_ctx *ctx, const sgl_k
     for (uint32_t l = 0; l < d->layers; ++l) {
         const sgl_kv_pool_view &sv = d->src_layers[l];
         const sgl_kv_pool_view &dv = d->dst_layers[l];
-        if (sv.tensor_count != tensors || sv.row_bytes != row_bytes || dv.tensor_count != tensors ||
-            dv.row_bytes != row_bytes) {
+        if (sv.tensor_count != tensors || sv.row_bytes != row_bytes[0] ||
+            view_row_bytes(sv, 1) != row_bytes[1] || dv.tensor_count != tensors ||
+            dv.row_bytes != row_bytes[0] || view_row_bytes(dv, 1) != row_bytes[1]) {
             delete p;
             return fail(SGL_KV_INVALID_ARGUMENT, "layers", l, 0, 0,
                         "layer %u's views differ in row shape from layer 0", l);
@@ -264,3 +270,10 @@ extern "C" int32_t sgl_rocm_kv_pipeline_destroy(sgl_rocm_kv_pipeline *p) {
 // The stream of a pipeline's last stage (its unpacks): work recorded there
 // after a run completes after every layer of that run.
 hipStream_t sglkv::pipeline_final_stream(sgl_rocm_kv_pipeline *p) { return p->stream[kUnpack]; }
+
+// Points every launch of the pipeline at `flag` (a transfer backend gives
+// each span its own error word).
+void sglkv::pipeline_set_error_word(sgl_rocm_kv_pipeline *p, uint32_t *flag) {
+    for (Launch &l : p->pack) set_launch_flag(l, flag);
+    for (Launch &l : p->unpack) set_launch_flag(l, flag);
+}

@@ -23,6 +23,9 @@ namespace {
 
 constexpr int kWidths[5] = {16, 8, 4, 2, 1};
 constexpr int kPoolRows = 0, kRowsPool = 1, kPoolPool = 2;
+// Rows per launch: the kernels index rows in 32 bits, and the last tile of a
+// launch (at most 512 rows) must still end below 2^32.
+constexpr uint64_t kMaxRows = UINT32_MAX - 4096u;
 const char *const kKindNames[3] = {"pool_rows", "rows_pool", "pool_pool"};
 
 }  // namespace
@@ -65,29 +68,29 @@ int32_t pool_side(const sgl_kv_pool_view *v, const sgl_kv_device_buffer *slots, 
     uint64_t need;
     if (mul_ovf(rows, 8, &need)) return shape_overflow();
     if (need > slots->byte_len) return out_of_bounds("slot_indices", 0, need, slots->byte_len);
-    uint64_t slot_count, tensor_page_bytes;
-    if (mul_ovf(v->page_size, v->page_count, &slot_count) ||
-        mul_ovf(v->page_size, v->row_bytes, &tensor_page_bytes))
-        return shape_overflow();
+    uint64_t slot_count, tensor_page_bytes[2] = {0, 0};
+    if (mul_ovf(v->page_size, v->page_count, &slot_count)) return shape_overflow();
+    for (uint32_t t = 0; t < v->tensor_count; ++t)
+        if (mul_ovf(v->page_size, view_row_bytes(*v, t), &tensor_page_bytes[t])) return shape_overflow();
     if (slot_count > UINT32_MAX) return too_large("slot_count", slot_count, UINT32_MAX);
     const char *names[2] = {v->tensor_count == 2 ? "key" : "latent", "value"};
     uint64_t ends[2] = {0, 0};
     for (uint32_t t = 0; t < v->tensor_count; ++t) {
-        if (add_ovf(v->tensor_offset[t], tensor_page_bytes, &ends[t])) return shape_overflow();
+        if (add_ovf(v->tensor_offset[t], tensor_page_bytes[t], &ends[t])) return shape_overflow();
         if (ends[t] > v->page_stride_bytes)
             return fail(SGL_KV_TENSOR_PAGE_REGION_OUT_OF_BOUNDS, names[t], v->tensor_offset[t],
-                        tensor_page_bytes, v->page_stride_bytes,
+                        tensor_page_bytes[t], v->page_stride_bytes,
                         "KV copy %s page region [%llu, %llu) exceeds page stride %llu", names[t],
                         (unsigned long long)v->tensor_offset[t], (unsigned long long)ends[t],
                         (unsigned long long)v->page_stride_bytes);
     }
     if (v->tensor_count == 2 && v->tensor_offset[0] < ends[1] && v->tensor_offset[1] < ends[0])
         return fail(SGL_KV_TENSOR_PAGE_REGIONS_OVERLAP, nullptr, v->tensor_offset[0],
-                    v->tensor_offset[1], tensor_page_bytes,
+                    v->tensor_offset[1], tensor_page_bytes[0],
                     "KV copy key/value page regions overlap: key offset %llu, value offset %llu, "
                     "tensor page size %llu bytes",
                     (unsigned long long)v->tensor_offset[0], (unsigned long long)v->tensor_offset[1],
-                    (unsigned long long)tensor_page_bytes);
+                    (unsigned long long)tensor_page_bytes[0]);
     // The pool must reach the end of the last slot's last tensor row
     // (CudaKvPairCopyPlan's pool_required_bytes, cuda_kv_kernels.rs:220-234).
     const uint64_t last_end = ends[0] > ends[1] ? ends[0] : ends[1];
@@ -97,7 +100,6 @@ int32_t pool_side(const sgl_kv_pool_view *v, const sgl_kv_device_buffer *slots, 
         return shape_overflow();
     if (required > v->byte_len) return out_of_bounds("pool", 0, required, v->byte_len);
 
-    const uint64_t chunk = shape.split ? shape.row_bytes / shape.heads : shape.row_bytes;
     const bool hnd = v->head_layout == SGL_KV_HND;
     memset(out, 0, sizeof *out);
     const uint64_t base = (uint64_t)(uintptr_t)v->base;
@@ -105,8 +107,12 @@ int32_t pool_side(const sgl_kv_pool_view *v, const sgl_kv_device_buffer *slots, 
     out->plane[1] = base + (v->tensor_count == 2 ? v->tensor_offset[1] : v->tensor_offset[0]);
     out->stride[0] = out->stride[1] = v->page_stride_bytes;
     out->slots = static_cast<const uint64_t *>(slots->ptr);
-    out->pos_mult = hnd ? chunk : v->row_bytes;
-    out->head_stride = hnd ? v->page_size * chunk : chunk;
+    for (uint32_t t = 0; t < 2; ++t) {
+        const uint32_t vt = t < v->tensor_count ? t : 0;
+        const uint64_t chunk = shape.chunk(vt);
+        out->pos_mult[t] = hnd ? chunk : view_row_bytes(*v, vt);
+        out->head_stride[t] = hnd ? v->page_size * chunk : chunk;
+    }
     out->slot_count = slot_count;
     out->page_size = (uint32_t)v->page_size;
     return SGL_KV_OK;
@@ -130,15 +136,31 @@ int32_t check_pool_shape(const sgl_kv_pool_view *v) {
     if (v->tensor_count > 2)
         return fail(SGL_KV_INVALID_ARGUMENT, "tensor_count", v->tensor_count, 2, 0,
                     "a pool view holds one or two tensors, not %u", v->tensor_count);
+    if (v->tensor_count == 1 && v->value_row_bytes)
+        return fail(SGL_KV_INVALID_ARGUMENT, "value_row_bytes", v->value_row_bytes, 0, 0,
+                    "a one-tensor pool view has no value width (%llu)",
+                    (unsigned long long)v->value_row_bytes);
     if (v->head_layout > SGL_KV_HND)
         return fail(SGL_KV_INVALID_ARGUMENT, "head_layout", v->head_layout, 0, 0,
                     "unknown head layout %u", v->head_layout);
     if (v->page_size > UINT32_MAX) return too_large("page_size", v->page_size, UINT32_MAX);
-    if (v->head_layout == SGL_KV_HND && v->row_bytes % v->heads)
-        return fail(SGL_KV_INVALID_ARGUMENT, "heads", v->heads, v->row_bytes, 0,
-                    "%u heads do not split a %llu-byte row evenly", v->heads,
-                    (unsigned long long)v->row_bytes);
+    for (uint32_t t = 0; t < v->tensor_count; ++t)
+        if (v->head_layout == SGL_KV_HND && view_row_bytes(*v, t) % v->heads)
+            return fail(SGL_KV_INVALID_ARGUMENT, "heads", v->heads, view_row_bytes(*v, t), 0,
+                        "%u heads do not split a %llu-byte row evenly", v->heads,
+                        (unsigned long long)view_row_bytes(*v, t));
     return SGL_KV_OK;
+}
+
+// The row geometry a pool view fixes for a copy.
+RowShape shape_of(const sgl_kv_pool_view &v, bool split, uint32_t heads) {
+    RowShape s;
+    s.row_bytes[0] = v.row_bytes;
+    s.row_bytes[1] = v.tensor_count == 2 ? view_row_bytes(v, 1) : v.row_bytes;
+    s.tensors = v.tensor_count;
+    s.heads = split ? heads : 1u;
+    s.split = split;
+    return s;
 }
 
 // Validates a transfer-rows side; `names` label the planes in errors.
@@ -147,34 +169,35 @@ int32_t rows_side(const sgl_kv_rows_view *v, uint64_t rows, const RowShape &shap
     if (!v) return fail(SGL_KV_INVALID_ARGUMENT, "rows", 0, 0, 0, "null rows view");
     memset(out, 0, sizeof *out);
     for (uint32_t t = 0; t < shape.tensors; ++t) {
+        const uint64_t rb = shape.row_bytes[t];
         if (!v->planes[t]) return fail(SGL_KV_INVALID_ARGUMENT, names[t], 0, 0, 0, "null plane");
-        if (v->row_stride[t] < shape.row_bytes)
-            return fail(SGL_KV_ROW_STRIDE_TOO_SMALL, names[t], shape.row_bytes, v->row_stride[t], 0,
+        if (v->row_stride[t] < rb)
+            return fail(SGL_KV_ROW_STRIDE_TOO_SMALL, names[t], rb, v->row_stride[t], 0,
                         "KV copy %s row stride %llu bytes is smaller than row width %llu bytes",
-                        names[t], (unsigned long long)v->row_stride[t],
-                        (unsigned long long)shape.row_bytes);
+                        names[t], (unsigned long long)v->row_stride[t], (unsigned long long)rb);
         uint64_t need;
-        if (mul_ovf(rows - 1, v->row_stride[t], &need) || add_ovf(need, shape.row_bytes, &need))
+        if (mul_ovf(rows - 1, v->row_stride[t], &need) || add_ovf(need, rb, &need))
             return shape_overflow();
         if (need > v->plane_bytes[t]) return out_of_bounds(names[t], 0, need, v->plane_bytes[t]);
         out->plane[t] = (uint64_t)(uintptr_t)v->planes[t];
         out->stride[t] = v->row_stride[t];
+        out->head_stride[t] = shape.chunk(t);
     }
     if (shape.tensors == 1) {
         out->plane[1] = out->plane[0];
         out->stride[1] = out->stride[0];
+        out->head_stride[1] = out->head_stride[0];
     }
-    out->head_stride = shape.split ? shape.row_bytes / shape.heads : shape.row_bytes;
     return SGL_KV_OK;
 }
 
 // Widest power-of-two access (<= 16 bytes) that divides every address and
 // stride either side computes.
-int vector_bytes(const sglkv_side &s, const sglkv_side &d, uint64_t chunk) {
-    uint64_t bits = chunk;
+int vector_bytes(const sglkv_side &s, const sglkv_side &d, const RowShape &shape) {
+    uint64_t bits = shape.chunk(0) | shape.chunk(shape.tensors - 1);
     for (const sglkv_side *x : {&s, &d})
-        bits |= x->plane[0] | x->plane[1] | x->stride[0] | x->stride[1] | x->pos_mult |
-                x->head_stride;
+        bits |= x->plane[0] | x->plane[1] | x->stride[0] | x->stride[1] | x->pos_mult[0] |
+                x->pos_mult[1] | x->head_stride[0] | x->head_stride[1];
     int vb = 16;
     while (vb > 1 && (bits & (uint64_t)(vb - 1))) vb >>= 1;
     return vb;
@@ -197,22 +220,77 @@ std::string default_code_object() {
 
 // Fills the launch geometry of a validated copy (vector width, tile) from
 // the context's code-object constants.
+// The byte-realigning kernel's launch: one thread per LDS vector of a row
+// (blockDim.x = vrow), SGLKV_REALIGN_ROWS_PER_THREAD rows per thread.
+// Returns false when a row's LDS footprint is too wide for it.
+bool plan_realign(const sgl_rocm_kv_ctx *ctx, Launch *l) {
+    const RowShape &shape = l->shape;
+    sglkv_realign_params &r = l->realign;
+    const uint64_t chunks = shape.split ? shape.heads : 1u;
+    uint64_t vrow = 0, vt0 = 0;
+    for (uint32_t t = 0; t < shape.tensors; ++t) {
+        const uint64_t c = shape.chunk(t);
+        const uint64_t seg = (c + 30) / 16;  // vectors covering c bytes at any alignment
+        if (c > UINT32_MAX || seg * chunks > SGLKV_REALIGN_MAX_ROW_VECTORS) return false;
+        r.chunk[t] = (uint32_t)c;
+        r.seg[t] = (uint32_t)seg;
+        vrow += seg * chunks;
+        if (t == 0) vt0 = vrow;
+    }
+    if (vrow > SGLKV_REALIGN_MAX_ROW_VECTORS) return false;
+    if (shape.tensors == 1) {
+        r.chunk[1] = r.chunk[0];
+        r.seg[1] = r.seg[0];
+    }
+    r.src = l->params.src;
+    r.dst = l->params.dst;
+    r.flag = ctx->flag;
+    r.scale_src = l->params.scale_src;
+    r.scale_dst = l->params.scale_dst;
+    r.scale_count = l->params.scale_count;
+    r.rows = (uint32_t)l->rows;
+    r.vt0 = (uint32_t)vt0;
+    r.vrow = (uint32_t)vrow;
+    r.rows_per_thread = SGLKV_REALIGN_ROWS_PER_THREAD;
+    r.zero = ctx->zero_row;
+    l->block_x = (uint32_t)vrow;
+    l->block_y = SGLKV_BLOCK_THREADS / l->block_x;
+    if (l->block_y > 64) l->block_y = 64;  // tiles of at most 512 rows
+    r.tile_rows = l->block_y * SGLKV_REALIGN_ROWS_PER_THREAD;
+    l->lds_bytes = SGLKV_REALIGN_LDS_BYTES(r.tile_rows, r.vrow);
+    if (l->lds_bytes > (uint32_t)ctx->max_lds_per_block) return false;
+    l->grid = (l->rows + r.tile_rows - 1) / r.tile_rows;
+    l->realigned = true;
+    return true;
+}
+
 int32_t finish_launch(const sgl_rocm_kv_ctx *ctx, Launch *l) {
     sglkv_copy_params &p = l->params;
     const RowShape &shape = l->shape;
-    if (l->rows > UINT32_MAX) return too_large("row_count", l->rows, UINT32_MAX);
-    const uint64_t chunk = shape.split ? shape.row_bytes / shape.heads : shape.row_bytes;
-    const int vb = vector_bytes(p.src, p.dst, chunk);
-    uint64_t row_vectors = shape.row_bytes / vb * shape.tensors;
-    if (row_vectors > (1ull << 31)) return too_large("row_bytes", shape.row_bytes, 1ull << 30);
+    if (l->rows > kMaxRows) return too_large("row_count", l->rows, kMaxRows);
+    const int vb = vector_bytes(p.src, p.dst, shape);
+    uint64_t row_vectors = 0;
+    for (uint32_t t = 0; t < shape.tensors; ++t) row_vectors += shape.row_bytes[t] / vb;
+    if (row_vectors > (1ull << 31)) return too_large("row_bytes", shape.row_bytes[0], 1ull << 30);
     int wi = 0;
     while (kWidths[wi] != vb) ++wi;
     l->width_index = wi;
+    l->realigned = false;
+    l->lds_bytes = 0;
     p.flag = ctx->flag;
     p.rows = (uint32_t)l->rows;
+    // Rows that do not fall on 16-byte vectors move through the realigning
+    // kernel: its accesses stay 16 bytes wide where the plain kernel's would
+    // narrow to the common alignment (down to single bytes for the odd
+    // 649-byte packed-MLA rows).
+    if (vb < 16 && plan_realign(ctx, l)) {
+        if (l->grid > INT32_MAX) return too_large("grid blocks", l->grid, INT32_MAX);
+        return SGL_KV_OK;
+    }
     p.vpr = (uint32_t)row_vectors;
-    p.vpt = (uint32_t)(shape.row_bytes / vb);
-    p.vpc = (uint32_t)(chunk / vb);
+    p.vpt = (uint32_t)(shape.row_bytes[0] / vb);
+    p.vpc[0] = (uint32_t)(shape.chunk(0) / vb);
+    p.vpc[1] = (uint32_t)(shape.chunk(shape.tensors - 1) / vb);
     l->block_x = p.vpr < SGLKV_BLOCK_THREADS ? p.vpr : SGLKV_BLOCK_THREADS;
     uint32_t by = SGLKV_BLOCK_THREADS / l->block_x;
     if (by > ctx->max_tile_rows / ctx->rows_per_thread) by = ctx->max_tile_rows / ctx->rows_per_thread;
@@ -315,7 +393,8 @@ int32_t pair_copy(sgl_rocm_kv_ctx *ctx, const sgl_kv_pair_copy_plan *plan,
 
     Launch l;
     memset(&l, 0, sizeof l);
-    l.shape = RowShape{plan->layout.row_bytes, 2, 1, false};
+    const uint64_t rb = plan->layout.row_bytes;
+    l.shape = RowShape{{rb, rb}, 2, 1, false};
     l.kind = scatter ? kRowsPool : kPoolRows;
     l.rows = plan->row_count;
     sglkv_copy_params &p = l.params;
@@ -325,25 +404,26 @@ int32_t pair_copy(sgl_rocm_kv_ctx *ctx, const sgl_kv_pair_copy_plan *plan,
     ps.plane[1] = pool + plan->layout.value_in_page_offset;
     ps.stride[0] = ps.stride[1] = plan->layout.page_stride_bytes;
     ps.slots = reinterpret_cast<const uint64_t *>(slots);
-    ps.pos_mult = plan->layout.row_bytes;
-    ps.head_stride = plan->layout.row_bytes;
+    ps.pos_mult[0] = ps.pos_mult[1] = rb;
+    ps.head_stride[0] = ps.head_stride[1] = rb;
     ps.slot_count = plan->slot_count;
     ps.page_size = (uint32_t)plan->layout.page_size;
     rs.plane[0] = keys;
     rs.plane[1] = values;
     rs.stride[0] = plan->key_row_stride_bytes;
     rs.stride[1] = plan->value_row_stride_bytes;
-    rs.head_stride = plan->layout.row_bytes;
+    rs.head_stride[0] = rs.head_stride[1] = rb;
     if ((rc = finish_launch(ctx, &l))) return rc;
+    // These drop-ins own an error word, as the reference's kernels object
+    // owns its flag (cuda_kv_kernels.rs:421, 550-551): clearing and reading
+    // it never touches the bits of the asynchronous calls.
+    set_launch_flag(l, ctx->pair_flag);
 
-    SGLKV_HIP(hipMemsetAsync(ctx->flag, 0, sizeof(uint32_t), stream));
+    SGLKV_HIP(hipMemsetAsync(ctx->pair_flag, 0, sizeof(uint32_t), stream));
     if ((rc = submit_launch(ctx, l, stream))) return rc;
     SGLKV_HIP(hipStreamSynchronize(stream));
     uint32_t flag = 0;
-    SGLKV_HIP(hipMemcpy(&flag, ctx->flag, sizeof flag, hipMemcpyDeviceToHost));
-    // A reported error is consumed, so that a later asynchronous call's
-    // check_errors does not report it again.
-    if (flag) SGLKV_HIP(hipMemset(ctx->flag, 0, sizeof(uint32_t)));
+    SGLKV_HIP(hipMemcpy(&flag, ctx->pair_flag, sizeof flag, hipMemcpyDeviceToHost));
     if (flag)
         return fail(SGL_KV_DEVICE_SLOT_INDEX_OUT_OF_RANGE, nullptr, plan->slot_count, 0, 0,
                     "KV copy device slot map contains an index outside %llu slots",
@@ -386,7 +466,13 @@ extern "C" int32_t sgl_rocm_kv_init(int32_t device, const char *code_object_path
                             "code object %s lacks kernel %s", path.c_str(), name);
             }
         }
-    err = hipModuleGetFunction(&ctx->resolve, ctx->module, "sglkv_resolve_spans");
+    const char *const realign_names[3] = {"sglkv_realign_pool_rows", "sglkv_realign_rows_pool",
+                                          "sglkv_realign_pool_pool"};
+    err = hipSuccess;
+    for (int k = 0; k < 3 && err == hipSuccess; ++k)
+        err = hipModuleGetFunction(&ctx->realign[k], ctx->module, realign_names[k]);
+    if (err == hipSuccess) err = hipModuleGetFunction(&ctx->resolve, ctx->module, "sglkv_resolve_spans");
+    if (err == hipSuccess) err = hipModuleGetFunction(&ctx->take_flags, ctx->module, "sglkv_take_flags");
     if (err == hipSuccess) err = hipModuleGetFunction(&ctx->fill, ctx->module, "sglkv_fill_synthetic");
     const char *const stream_names[3] = {"sglkv_stream_copy", "sglkv_stream_read", "sglkv_stream_write"};
     for (int i = 0; i < 3 && err == hipSuccess; ++i)
@@ -431,11 +517,16 @@ extern "C" int32_t sgl_rocm_kv_init(int32_t device, const char *code_object_path
     }
     if (err == hipSuccess && (ctx->rows_per_thread == 0 || ctx->rows_per_thread > ctx->max_tile_rows))
         err = hipErrorInvalidImage;
-    // One small block: the error word at offset 0, the zero row at 256.
+    // One small block: the error words at offsets 0, 64 and 128 (separate
+    // lines), check_errors' readout at 192, the zero row at 256.
     constexpr size_t kFlagBlock = 256 + SGLKV_ZERO_ROW_BYTES;
     if (err == hipSuccess) err = hipMalloc(reinterpret_cast<void **>(&ctx->flag), kFlagBlock);
     if (err == hipSuccess) err = hipMemset(ctx->flag, 0, kFlagBlock);
-    if (err == hipSuccess) ctx->zero_row = reinterpret_cast<const uint8_t *>(ctx->flag) + 256;
+    if (err == hipSuccess) {
+        ctx->attn_flag = ctx->flag + 16;
+        ctx->pair_flag = ctx->flag + 32;
+        ctx->zero_row = reinterpret_cast<const uint8_t *>(ctx->flag) + 256;
+    }
     if (err != hipSuccess) {
         if (ctx->flag) (void)hipFree(ctx->flag);
         (void)hipModuleUnload(ctx->module);
@@ -510,7 +601,7 @@ int32_t check_layer_span(const sgl_kv_pool_view *pool, bool pool_is_dst,
     if (pool_is_dst) {
         for (uint32_t t = 0; t < pool->tensor_count; ++t) {
             lo = pool->tensor_offset[t] < lo ? pool->tensor_offset[t] : lo;
-            const uint64_t end = pool->tensor_offset[t] + pool->page_size * pool->row_bytes;
+            const uint64_t end = pool->tensor_offset[t] + pool->page_size * view_row_bytes(*pool, t);
             hi = end > hi ? end : hi;
         }
         if (span.pool_stride < hi - lo)
@@ -520,7 +611,7 @@ int32_t check_layer_span(const sgl_kv_pool_view *pool, bool pool_is_dst,
     } else {
         for (uint32_t t = 0; t < shape.tensors; ++t) {
             const uint64_t b = (uint64_t)(uintptr_t)rows->planes[t];
-            const uint64_t end = b + (row_count - 1) * rows->row_stride[t] + shape.row_bytes;
+            const uint64_t end = b + (row_count - 1) * rows->row_stride[t] + shape.row_bytes[t];
             lo = b < lo ? b : lo;
             hi = end > hi ? end : hi;
         }
@@ -535,6 +626,8 @@ int32_t check_layer_span(const sgl_kv_pool_view *pool, bool pool_is_dst,
 int32_t prepare_pack(const sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src,
                      const sgl_kv_device_buffer *slots, uint64_t row_count,
                      const sgl_kv_rows_view *dst, Launch *l, LayerSpan span) {
+    // Row counts are checked first: the limit holds whatever the context.
+    if (row_count > kMaxRows) return too_large("row_count", row_count, kMaxRows);
     int32_t rc = check_ctx(ctx);
     if (!rc) rc = check_pool_shape(src);
     if (rc) return rc;
@@ -545,7 +638,7 @@ int32_t prepare_pack(const sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src,
     l->layers = span.count;
     if (row_count == 0) return SGL_KV_OK;
     const bool split = src->head_layout == SGL_KV_HND;
-    l->shape = RowShape{src->row_bytes, src->tensor_count, split ? src->heads : 1u, split};
+    l->shape = shape_of(*src, split, src->heads);
     const char *names[2] = {src->tensor_count == 2 ? "keys" : "rows", "values"};
     if ((rc = pool_side(src, slots, row_count, l->shape, &l->params.src)) ||
         (rc = rows_side(dst, row_count, l->shape, names, &l->params.dst)) ||
@@ -560,6 +653,8 @@ int32_t prepare_pack(const sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src,
 int32_t prepare_unpack(const sgl_rocm_kv_ctx *ctx, const sgl_kv_rows_view *src, uint64_t row_count,
                        const sgl_kv_pool_view *dst, const sgl_kv_device_buffer *slots, Launch *l,
                        LayerSpan span) {
+    // Row counts are checked first: the limit holds whatever the context.
+    if (row_count > kMaxRows) return too_large("row_count", row_count, kMaxRows);
     int32_t rc = check_ctx(ctx);
     if (!rc) rc = check_pool_shape(dst);
     if (rc) return rc;
@@ -570,7 +665,7 @@ int32_t prepare_unpack(const sgl_rocm_kv_ctx *ctx, const sgl_kv_rows_view *src, 
     l->layers = span.count;
     if (row_count == 0) return SGL_KV_OK;
     const bool split = dst->head_layout == SGL_KV_HND;
-    l->shape = RowShape{dst->row_bytes, dst->tensor_count, split ? dst->heads : 1u, split};
+    l->shape = shape_of(*dst, split, dst->heads);
     const char *names[2] = {dst->tensor_count == 2 ? "keys" : "rows", "values"};
     if ((rc = rows_side(src, row_count, l->shape, names, &l->params.src)) ||
         (rc = pool_side(dst, slots, row_count, l->shape, &l->params.dst)) ||
@@ -584,6 +679,12 @@ int32_t prepare_unpack(const sgl_rocm_kv_ctx *ctx, const sgl_kv_rows_view *src, 
 
 int32_t submit_launch(sgl_rocm_kv_ctx *ctx, Launch &l, hipStream_t stream) {
     if (l.rows == 0) return SGL_KV_OK;
+    if (l.realigned) {
+        void *args[] = {&l.realign};
+        SGLKV_HIP(hipModuleLaunchKernel(ctx->realign[l.kind], (unsigned)l.grid, l.layers ? l.layers : 1, 1,
+                                        l.block_x, l.block_y, 1, l.lds_bytes, stream, args, nullptr));
+        return SGL_KV_OK;
+    }
     void *args[] = {&l.params};
     SGLKV_HIP(hipModuleLaunchKernel(ctx->copy[l.width_index][l.kind], (unsigned)l.grid,
                                     l.layers ? l.layers : 1, 1, l.block_x, l.block_y, 1, 0, stream,
@@ -782,23 +883,28 @@ int32_t prepare_transfer(const sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src
                          const sgl_kv_pool_view *dst, const sgl_kv_device_buffer *dst_slots,
                          Launch *l, uint32_t layers, uint64_t src_layer_stride,
                          uint64_t dst_layer_stride) {
+    if (row_count > kMaxRows) return too_large("row_count", row_count, kMaxRows);
     int32_t rc = check_ctx(ctx);
     if (!rc) rc = check_pool_shape(src);
     if (!rc) rc = check_pool_shape(dst);
     if (rc) return rc;
-    if (src->row_bytes != dst->row_bytes || src->tensor_count != dst->tensor_count)
+    if (src->tensor_count != dst->tensor_count || src->row_bytes != dst->row_bytes ||
+        view_row_bytes(*src, 1) != view_row_bytes(*dst, 1))
         return fail(SGL_KV_INVALID_ARGUMENT, "dst", dst->row_bytes, src->row_bytes, 0,
-                    "destination rows (%llu bytes x %u tensors) differ from source rows (%llu x %u)",
-                    (unsigned long long)dst->row_bytes, dst->tensor_count,
-                    (unsigned long long)src->row_bytes, src->tensor_count);
+                    "destination rows (%llu + %llu bytes x %u tensors) differ from source rows "
+                    "(%llu + %llu x %u)",
+                    (unsigned long long)dst->row_bytes, (unsigned long long)view_row_bytes(*dst, 1),
+                    dst->tensor_count, (unsigned long long)src->row_bytes,
+                    (unsigned long long)view_row_bytes(*src, 1), src->tensor_count);
     const bool split = src->head_layout == SGL_KV_HND || dst->head_layout == SGL_KV_HND;
     if (split && src->heads != dst->heads)
         return fail(SGL_KV_INVALID_ARGUMENT, "heads", dst->heads, src->heads, 0,
                     "head-major relayout needs equal head counts (%u vs %u)", dst->heads, src->heads);
-    if (split && src->row_bytes % src->heads)
-        return fail(SGL_KV_INVALID_ARGUMENT, "heads", src->heads, src->row_bytes, 0,
-                    "%u heads do not split a %llu-byte row evenly", src->heads,
-                    (unsigned long long)src->row_bytes);
+    for (uint32_t t = 0; t < src->tensor_count; ++t)
+        if (split && view_row_bytes(*src, t) % src->heads)
+            return fail(SGL_KV_INVALID_ARGUMENT, "heads", src->heads, view_row_bytes(*src, t), 0,
+                        "%u heads do not split a %llu-byte row evenly", src->heads,
+                        (unsigned long long)view_row_bytes(*src, t));
     if (layers == 0 || layers > 65535)
         return fail(SGL_KV_INVALID_ARGUMENT, "layer_count", layers, 65535, 0,
                     "a launch covers 1 to 65535 layers, not %u", layers);
@@ -807,7 +913,7 @@ int32_t prepare_transfer(const sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src
     l->rows = row_count;
     l->layers = layers;
     if (row_count == 0) return SGL_KV_OK;
-    l->shape = RowShape{src->row_bytes, src->tensor_count, split ? src->heads : 1u, split};
+    l->shape = shape_of(*src, split, src->heads);
     if ((rc = pool_side(src, src_slots, row_count, l->shape, &l->params.src)) ||
         (rc = pool_side(dst, dst_slots, row_count, l->shape, &l->params.dst)))
         return rc;
@@ -828,7 +934,7 @@ int32_t prepare_transfer(const sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src
         uint64_t lo = UINT64_MAX, hi = 0;
         for (uint32_t t = 0; t < dst->tensor_count; ++t) {
             lo = dst->tensor_offset[t] < lo ? dst->tensor_offset[t] : lo;
-            const uint64_t end = dst->tensor_offset[t] + dst->page_size * dst->row_bytes;
+            const uint64_t end = dst->tensor_offset[t] + dst->page_size * view_row_bytes(*dst, t);
             hi = end > hi ? end : hi;
         }
         if (dst_layer_stride < hi - lo)
@@ -912,16 +1018,18 @@ extern "C" int32_t sgl_rocm_kv_resolve_spans(sgl_rocm_kv_ctx *ctx, uint64_t page
 }
 
 // Maps the device error word to the status (and detail record) it reports.
+// Span resolution's bits come first: a row it could not resolve also
+// reaches the copies as a bad slot, and the page table is the cause.
 int32_t sglkv::flag_status(uint32_t flag) {
-    if (flag & SGLKV_FLAG_SLOT)
-        return fail(SGL_KV_DEVICE_SLOT_INDEX_OUT_OF_RANGE, nullptr, 0, flag, 0,
-                    "KV copy device slot map contains an index outside the pool's slots");
     if (flag & SGLKV_FLAG_PAGE)
         return fail(SGL_KV_DEVICE_PAGE_INDEX_OUT_OF_RANGE, nullptr, 0, flag, 0,
                     "KV transfer page table holds an entry outside the table or the pool");
     if (flag & SGLKV_FLAG_SPAN)
         return fail(SGL_KV_DEVICE_SPAN_OUT_OF_RANGE, nullptr, 0, flag, 0,
                     "KV transfer row is not covered by any span");
+    if (flag & SGLKV_FLAG_SLOT)
+        return fail(SGL_KV_DEVICE_SLOT_INDEX_OUT_OF_RANGE, nullptr, 0, flag, 0,
+                    "KV copy device slot map contains an index outside the pool's slots");
     if (flag & SGLKV_FLAG_REQUEST)
         return fail(SGL_KV_DEVICE_REQUEST_OUT_OF_RANGE, nullptr, 0, flag, 0,
                     "KV page request lies outside its source or target region");
@@ -934,11 +1042,16 @@ extern "C" int32_t sgl_rocm_kv_check_errors(sgl_rocm_kv_ctx *ctx, void *stream) 
     DeviceScope scope(ctx->device);
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
     hipStream_t s = static_cast<hipStream_t>(stream);
+    // The copy word and the attention word (the asynchronous attention's
+    // metadata errors surface here too), each read and cleared atomically
+    // on `stream` after the work queued there.
+    uint32_t *out = ctx->flag + 48;
+    void *args[] = {&ctx->flag, &ctx->attn_flag, &out};
+    SGLKV_HIP(hipModuleLaunchKernel(ctx->take_flags, 1, 1, 1, 64, 1, 1, 0, s, args, nullptr));
+    uint32_t flags[2] = {0, 0};
+    SGLKV_HIP(hipMemcpyAsync(flags, out, sizeof flags, hipMemcpyDeviceToHost, s));
     SGLKV_HIP(hipStreamSynchronize(s));
-    uint32_t flag = 0;
-    SGLKV_HIP(hipMemcpy(&flag, ctx->flag, sizeof flag, hipMemcpyDeviceToHost));
-    if (flag) SGLKV_HIP(hipMemset(ctx->flag, 0, sizeof(uint32_t)));
-    return flag_status(flag);
+    return flag_status(flags[0] | flags[1]);
 }
 
 extern "C" int32_t sgl_rocm_kv_fill_synthetic(sgl_rocm_kv_ctx *ctx, const sgl_kv_device_buffer *buffer,

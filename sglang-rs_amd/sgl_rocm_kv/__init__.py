@@ -108,6 +108,13 @@ class _RuntimeLayout(ctypes.Structure):
                             "kv_tensors_per_token", "bytes_per_token", "page_size_bytes")]
 
 
+class _ModelLayout(ctypes.Structure):
+    _fields_ = [(n, _u64) for n in ("num_layers", "kv_heads", "head_dim", "kv_tensors_per_token",
+                                    "bytes_per_token_per_layer")] + [
+        ("geometry", ctypes.c_uint32), ("reserved", ctypes.c_uint32),
+        ("key_elements", _u64), ("value_elements", _u64)]
+
+
 class _PagedLayout(ctypes.Structure):
     _fields_ = [("runtime", _RuntimeLayout), ("page_count", _u64),
                 ("bytes_per_token_per_layer", _u64), ("bytes_per_layer_page", _u64),
@@ -188,7 +195,12 @@ class PoolView(ctypes.Structure):
                 ("page_stride_bytes", _u64), ("page_count", _u64), ("tensor_offset", _u64 * 2),
                 ("row_bytes", _u64), ("tensor_count", ctypes.c_uint32),
                 ("heads", ctypes.c_uint32), ("head_layout", ctypes.c_uint32),
-                ("reserved", ctypes.c_uint32), ("scale", ctypes.c_void_p)]
+                ("reserved", ctypes.c_uint32), ("scale", ctypes.c_void_p),
+                ("value_row_bytes", _u64)]
+
+    def tensor_row_bytes(self, tensor: int) -> int:
+        """Bytes per (token, tensor): the value width of a tensor pair may differ."""
+        return self.value_row_bytes if tensor == 1 and self.value_row_bytes else self.row_bytes
 
 
 class RowsView(ctypes.Structure):
@@ -269,6 +281,19 @@ _EXPORTS = {
     "sgl_kv_last_error": (None, [ctypes.POINTER(_ErrorDetail)]),
     "sgl_kv_status_name": (ctypes.c_char_p, [ctypes.c_int32]),
     "sgl_kv_dtype_bytes_per_element": (ctypes.c_size_t, [ctypes.c_int32]),
+    "sgl_kv_model_layout_multi_tensor": (ctypes.c_int32, [_u64, _u64, _u64, _u64, ctypes.POINTER(_ModelLayout)]),
+    "sgl_kv_model_layout_tensor_pair": (ctypes.c_int32, [_u64, _u64, _u64, _u64, _u64,
+                                                         ctypes.POINTER(_ModelLayout)]),
+    "sgl_kv_model_layout_packed_bytes_per_layer": (ctypes.c_int32, [_u64, _u64, ctypes.POINTER(_ModelLayout)]),
+    "sgl_kv_model_layout_packed_mla": (ctypes.c_int32, [_u64, _u64, _u64, ctypes.POINTER(_ModelLayout)]),
+    "sgl_kv_model_layout_elements_per_token": (ctypes.c_int32, [ctypes.POINTER(_ModelLayout), ctypes.POINTER(_u64),
+                                                                ctypes.POINTER(ctypes.c_uint32)]),
+    "sgl_kv_model_layout_token_size_bytes": (ctypes.c_int32, [ctypes.POINTER(_ModelLayout), ctypes.c_int32,
+                                                              ctypes.POINTER(_u64)]),
+    "sgl_kv_model_layout_tensor_pair_size_bytes": (ctypes.c_int32, [ctypes.POINTER(_ModelLayout), ctypes.c_int32,
+                                                                    _u64 * 2, ctypes.POINTER(ctypes.c_uint32)]),
+    "sgl_kv_paged_layout_for_model": (ctypes.c_int32, [ctypes.POINTER(_ModelLayout), ctypes.c_int32, _u64, _u64,
+                                                       ctypes.POINTER(_PagedLayout)]),
     "sgl_kv_paged_layout_new": (ctypes.c_int32, [ctypes.POINTER(_RuntimeLayout), _u64,
                                                  ctypes.POINTER(_PagedLayout)]),
     "sgl_kv_paged_layout_new_with_tensor_pair": (
@@ -385,6 +410,7 @@ _EXPORTS = {
                                                       ctypes.POINTER(_BackendMemory),
                                                       ctypes.POINTER(_BackendMemory)]),
     "sgl_rocm_kv_backend_submit": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_SpanDesc)]),
+    "sgl_rocm_kv_backend_submit_device_table": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_SpanDesc)]),
     "sgl_rocm_kv_backend_poll": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_TransferEvent),
                                                   _u64, ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
     "sgl_rocm_kv_backend_cancel": (ctypes.c_int32, [ctypes.c_void_p, _u64]),
@@ -515,6 +541,68 @@ class KvCacheRuntimeLayout:
                    bpt * page_size)
 
 
+class KvCacheModelLayout:
+    """KvCacheModelLayout (kv_cache.rs:68-225): a model's KV geometry before
+    the dtype and page size are chosen."""
+
+    def __init__(self, c: _ModelLayout):
+        self._c = c
+
+    @classmethod
+    def _build(cls, fn, *args) -> "KvCacheModelLayout":
+        out = _ModelLayout()
+        _call(fn, *args, ctypes.byref(out))
+        return cls(out)
+
+    @classmethod
+    def multi_tensor(cls, num_layers: int, kv_heads: int, head_dim: int, kv_tensors_per_token: int):
+        return cls._build(lib().sgl_kv_model_layout_multi_tensor, num_layers, kv_heads, head_dim,
+                          kv_tensors_per_token)
+
+    @classmethod
+    def tensor_pair(cls, num_layers: int, key_heads: int, key_head_dim: int, value_heads: int,
+                    value_head_dim: int):
+        return cls._build(lib().sgl_kv_model_layout_tensor_pair, num_layers, key_heads, key_head_dim,
+                          value_heads, value_head_dim)
+
+    @classmethod
+    def packed_bytes_per_layer(cls, num_layers: int, bytes_per_token_per_layer: int):
+        return cls._build(lib().sgl_kv_model_layout_packed_bytes_per_layer, num_layers,
+                          bytes_per_token_per_layer)
+
+    @classmethod
+    def packed_mla(cls, num_layers: int, qk_nope_head_dim: int, qk_rope_head_dim: int):
+        return cls._build(lib().sgl_kv_model_layout_packed_mla, num_layers, qk_nope_head_dim,
+                          qk_rope_head_dim)
+
+    num_layers = property(lambda self: self._c.num_layers)
+    kv_heads = property(lambda self: self._c.kv_heads)
+    head_dim = property(lambda self: self._c.head_dim)
+    kv_tensors_per_token = property(lambda self: self._c.kv_tensors_per_token)
+
+    @property
+    def bytes_per_token_per_layer(self):
+        return self._c.bytes_per_token_per_layer or None
+
+    def elements_per_token(self):
+        out, has = _u64(), ctypes.c_uint32()
+        _call(lib().sgl_kv_model_layout_elements_per_token, ctypes.byref(self._c), ctypes.byref(out),
+              ctypes.byref(has))
+        return out.value if has.value else None
+
+    def token_size_bytes(self, dtype: str) -> int:
+        out = _u64()
+        _call(lib().sgl_kv_model_layout_token_size_bytes, ctypes.byref(self._c), DTYPES[dtype],
+              ctypes.byref(out))
+        return out.value
+
+    def tensor_pair_size_bytes(self, dtype: str):
+        out, is_pair = (_u64 * 2)(), ctypes.c_uint32()
+        _call(lib().sgl_kv_model_layout_tensor_pair_size_bytes, ctypes.byref(self._c), DTYPES[dtype], out,
+              ctypes.byref(is_pair))
+        return [out[0], out[1]] if is_pair.value else None
+
+
 class PagedKvCacheLayout:
     """PagedKvCacheLayout (kv_cache.rs:436-823): page -> layer -> tensor -> token."""
 
@@ -527,6 +615,22 @@ class PagedKvCacheLayout:
         rt = runtime._c()
         _call(lib().sgl_kv_paged_layout_new, ctypes.byref(rt), page_count, ctypes.byref(out))
         return cls(out)
+
+    @classmethod
+    def for_model(cls, model: KvCacheModelLayout, dtype: str, page_size: int,
+                  slot_capacity: int) -> "PagedKvCacheLayout":
+        """paged_kv_cache_layout_for_model (backend_model.rs:348-382)."""
+        out = _PagedLayout()
+        _call(lib().sgl_kv_paged_layout_for_model, ctypes.byref(model._c), DTYPES[dtype], page_size,
+              slot_capacity, ctypes.byref(out))
+        return cls(out)
+
+    @property
+    def runtime(self) -> "KvCacheRuntimeLayout":
+        r = self._c.runtime
+        name = {v: k for k, v in DTYPES.items()}[r.dtype]
+        return KvCacheRuntimeLayout(name, r.page_size, r.num_layers, r.kv_heads, r.head_dim,
+                                    r.kv_tensors_per_token, r.bytes_per_token, r.page_size_bytes)
 
     @classmethod
     def new_with_tensor_pair(cls, runtime: KvCacheRuntimeLayout, page_count: int,
@@ -761,9 +865,12 @@ def rows_view(planes, plane_bytes, row_stride, scale: int | None = None) -> Rows
 
 def pool_view(base: int, byte_len: int, *, page_size: int, page_stride_bytes: int,
               page_count: int, tensor_offset, row_bytes: int, tensor_count: int, heads: int = 1,
-              head_layout: int = NHD, scale: int | None = None) -> PoolView:
-    """A pool view filled directly (for pools this library did not describe)."""
+              head_layout: int = NHD, scale: int | None = None,
+              value_row_bytes: int = 0) -> PoolView:
+    """A pool view filled directly (for pools this library did not describe);
+    value_row_bytes gives tensor 1's width when it differs from row_bytes."""
     v = PoolView()
+    v.value_row_bytes = value_row_bytes
     v.base, v.byte_len, v.page_size = base, byte_len, page_size
     v.page_stride_bytes, v.page_count = page_stride_bytes, page_count
     offs = list(tensor_offset) + [0, 0]
@@ -1075,14 +1182,30 @@ class RocmKvTransferBackend:
         token_offset.. ; the decode side holds them in `dst_page_table`."""
         slots = _u64_array(cache_slots)
         table = np.ascontiguousarray(np.asarray(dst_page_table, dtype=np.int32))
+        d = self._span(bootstrap_room, descriptor_checksum, token_offset, slots)
+        d.dst_page_table = table.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+        d.dst_page_table_len = len(table)
+        _call(lib().sgl_rocm_kv_backend_submit, self._h, ctypes.byref(d))
+
+    def submit_device_table(self, bootstrap_room: int, descriptor_checksum: str, token_offset: int,
+                            cache_slots, dst_page_table: "_DeviceBuffer", dst_page_table_len: int):
+        """As submit, with the decode page table in device memory (int32
+        entries): the decode slots are resolved on the device, and a bad entry
+        fails the span at poll (DevicePageIndexOutOfRange)."""
+        slots = _u64_array(cache_slots)
+        d = self._span(bootstrap_room, descriptor_checksum, token_offset, slots)
+        d.dst_page_table = ctypes.cast(ctypes.c_void_p(dst_page_table.ptr), ctypes.POINTER(ctypes.c_int32))
+        d.dst_page_table_len = dst_page_table_len
+        _call(lib().sgl_rocm_kv_backend_submit_device_table, self._h, ctypes.byref(d))
+
+    @staticmethod
+    def _span(bootstrap_room: int, descriptor_checksum: str, token_offset: int, slots: np.ndarray):
         d = _SpanDesc()
         d.bootstrap_room = bootstrap_room
         d.descriptor_checksum = descriptor_checksum.encode()[:64]
         d.token_offset, d.token_count = token_offset, len(slots)
         d.cache_slots = slots.ctypes.data_as(ctypes.POINTER(_u64))
-        d.dst_page_table = table.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
-        d.dst_page_table_len = len(table)
-        _call(lib().sgl_rocm_kv_backend_submit, self._h, ctypes.byref(d))
+        return d
 
     def poll(self, capacity: int = 256):
         """(events, pending_transfers), as KvTransferPoll (transfer.rs:1122-1143)."""

@@ -3,8 +3,13 @@ generators of request lengths, slot maps and page tables.
 
 Shapes follow the reference's model layouts: GQA models store K and V per
 token per layer (``KvCacheModelLayout::multi_tensor``, crates/sglang-srt/src/
-models/qwen.rs:234-239); the MLA workload stores one 576-wide latent row per
-token (a single-tensor layout). Slot maps stand in for the scheduler's
+models/qwen.rs:234-239). The MLA workloads come in the three forms the
+configurations and the reference use: one 576-wide latent row per token (a
+single-tensor layout, as BASELINE's C4 words it), the DeepSeek-V3 adapter's
+tensor pair of a 576-wide key and a 512-wide value
+(``KvCacheModelLayout::tensor_pair``, models/deepseek.rs:360-369), and the
+packed-MLA byte rows of 649 bytes (``KvCacheModelLayout::packed_mla``,
+models/deepseek.rs:1035-1037). Slot maps stand in for the scheduler's
 ``out_cache_pages`` (crates/sglang-srt/src/model_executor.rs:158-175), page
 tables for the decode side's ``dst_kv_indices``
 (crates/sglang-srt/src/pd_bootstrap.rs:416-494).
@@ -29,15 +34,27 @@ class Shape:
     head_dim: int
     elt_bytes: int
     tensors: int  # 2 = K/V, 1 = MLA latent row
+    value_head_dim: int = 0  # tensor 1's head dim when it differs (a tensor pair); 0 = head_dim
+
+    def tensor_row_bytes(self, tensor: int) -> int:
+        """Bytes per (token, layer) of `tensor`."""
+        hd = self.value_head_dim if tensor == 1 and self.value_head_dim else self.head_dim
+        return self.heads * hd * self.elt_bytes
 
     @property
     def row_bytes(self) -> int:
-        return self.heads * self.head_dim * self.elt_bytes
+        """Tensor 0's row (every tensor's, unless a pair of unequal widths)."""
+        return self.tensor_row_bytes(0)
+
+    @property
+    def layer_row_bytes(self) -> int:
+        """Bytes one token owns in one layer, all tensors."""
+        return sum(self.tensor_row_bytes(t) for t in range(self.tensors))
 
     @property
     def token_bytes(self) -> int:
         """Bytes one token owns across all layers and tensors."""
-        return self.layers * self.tensors * self.row_bytes
+        return self.layers * self.layer_row_bytes
 
 
 @dataclass
@@ -53,8 +70,9 @@ class PoolSpec:
         return self.page_count * self.page_stride(shape)
 
     def tensor_offsets(self, shape: Shape, layer: int):
-        """In-page offsets of the layer's tensor regions (kv_cache.rs:653-700)."""
-        per_layer = self.page_size * shape.tensors * shape.row_bytes
+        """In-page offsets of the layer's tensor regions (kv_cache.rs:653-700;
+        a pair's value region follows page_size key rows, :808-818)."""
+        per_layer = self.page_size * shape.layer_row_bytes
         return tuple(layer * per_layer + t * self.page_size * shape.row_bytes
                      for t in range(shape.tensors))
 
@@ -170,6 +188,38 @@ def c4(seed: int = 4, fp8: bool = False) -> Transfer:
     table, spans, dslots = _page_table_slots(rng, lengths, np.zeros(32, int), 64, dst.page_count)
     return Transfer("C4 mla-576" + (" fp8" if fp8 else ""), shape, src, dst, lengths, sslots,
                     dslots, table, spans, np.zeros(32, np.int64))
+
+
+def c4pair(seed: int = 4, fp8: bool = False, dst_page_size: int = 64) -> Transfer:
+    """C4's requests over the pool the DeepSeek-V3 adapter allocates: the
+    tensor pair of a 576-wide key (latent + rope) and a 512-wide value per
+    token per layer (models/deepseek.rs:360-369; 1,152 + 1,024 bytes in
+    bf16), page_size-64 source, destination page size `dst_page_size`."""
+    rng = np.random.default_rng(seed)
+    shape = Shape(61, 1, 576, 1 if fp8 else 2, 2, value_head_dim=512)
+    lengths = np.full(32, 8192)
+    src = PoolSpec(64, 4096)
+    dst = PoolSpec(dst_page_size, -(-4096 * 64 // dst_page_size))
+    _, _, sslots = _page_table_slots(rng, lengths, np.zeros(32, int), 64, src.page_count)
+    table, spans, dslots = _page_table_slots(rng, lengths, np.zeros(32, int), dst_page_size,
+                                             dst.page_count)
+    return Transfer("C4 deepseek-v3 mla pair 576/512" + (" fp8" if fp8 else ""), shape, src, dst,
+                    lengths, sslots, dslots, table, spans, np.zeros(32, np.int64))
+
+
+def c4packed(seed: int = 4) -> Transfer:
+    """C4's requests over packed-MLA rows: 649 bytes per token per layer
+    (packed_mla(61, 512, 64), kv_cache.rs:201-224, as build_mla_moe_definition
+    allocates it, models/deepseek.rs:1035-1037), page_size 64 on both sides."""
+    rng = np.random.default_rng(seed)
+    shape = Shape(61, 1, 649, 1, 1)
+    lengths = np.full(32, 8192)
+    src = PoolSpec(64, 4096)
+    dst = PoolSpec(64, 4096)
+    _, _, sslots = _page_table_slots(rng, lengths, np.zeros(32, int), 64, src.page_count)
+    table, spans, dslots = _page_table_slots(rng, lengths, np.zeros(32, int), 64, dst.page_count)
+    return Transfer("C4 packed-mla 649-byte rows", shape, src, dst, lengths, sslots, dslots, table,
+                    spans, np.zeros(32, np.int64))
 
 
 def c5(seed: int = 5, requests: int = 512) -> Transfer:

@@ -342,3 +342,61 @@ def test_bootstrap_frames_drive_the_backend(k, mode):
     pools.check()
     b.close()
     state.close()
+
+
+@pytest.mark.parametrize("mode", [kv.BACKEND_DIRECT, kv.BACKEND_STAGED])
+def test_device_table_failure_fails_only_its_span(k, mode):
+    """Two spans resolved on the device from device-resident decode page
+    tables. One table holds a page past the decode pool: the resolve kernel
+    flags that row and skips it (no fault), poll reports that room FAILED
+    with DevicePageIndexOutOfRange, its other rows still move, and the other
+    span (submitted before and after it) is COMPLETED with every byte moved
+    and the neighbouring bytes untouched. Each span owns its error word, so
+    the failure is charged to the right room (transfer.rs:2298-2329)."""
+    name = "direct" if mode == kv.BACKEND_DIRECT else "staged"
+    _say(f"backend {name}: per-span device failure")
+    rng = np.random.default_rng(900 + mode)
+    pools = _Pools(seed=30 + mode)
+    b = kv.RocmKvTransferBackend(k, mode, max_rows=512)
+    pools.register(b)
+    groups = rng.permutation(DECODE_PAGES).reshape(8, -1)
+    good_a = _span(rng, 16, 70, groups[0])
+    bad = _span(rng, 0, 90, groups[1])
+    good_b = _span(rng, 0, 33, groups[2])
+    bad_table = bad[1].copy()
+    bad_table[2] = DECODE_PAGES + 3           # tokens 32..47 have no page
+    tables = [hip.DeviceBuffer.from_array(t) for t in (good_a[1], bad_table, good_b[1])]
+    for room, (slots, _), table, off in ((21, good_a, tables[0], 16), (22, bad, tables[1], 0),
+                                         (23, good_b, tables[2], 0)):
+        b.submit_device_table(room, f"{room:064x}", off, slots, kv.device_buffer(table.ptr, table.nbytes),
+                              table.nbytes // 4)
+    pools.expect(16, *good_a)
+    pools.expect(0, *good_b)
+    # the failed span's rows whose page exists still move
+    keep = np.array([i for i in range(90) if i // P_DECODE != 2])
+    tok = keep.astype(np.uint64)
+    dslots = bad_table[tok // P_DECODE].astype(np.uint64) * P_DECODE + tok % P_DECODE
+    for layer in range(L):
+        sv = pools.pre.pool_view(pools.src.ptr, pools.src.nbytes, layer, kv.NHD, H)
+        dv = pools.dec.pool_view(pools.dst.ptr, pools.dst.nbytes, layer, kv.HND, H)
+        oracle.transfer(_opool(sv), pools.src_h, bad[0][keep], _opool(dv), pools.want, dslots)
+    b.wait()
+    events, pending = b.poll()
+    assert pending == 0
+    by_room = {e.bootstrap_room: e for e in events}
+    assert sorted(by_room) == [21, 22, 23]
+    assert by_room[21].status == kv.TRANSFER_COMPLETED and by_room[21].error_code == 0
+    assert by_room[23].status == kv.TRANSFER_COMPLETED and by_room[23].error_code == 0
+    assert by_room[22].status == kv.TRANSFER_FAILED
+    assert kv.status_name(by_room[22].error_code) == "DevicePageIndexOutOfRange"
+    pools.check()
+    # the words are clean for the next spans: a good span now completes
+    again = _span(rng, 0, 20, groups[3])
+    t4 = hip.DeviceBuffer.from_array(again[1])
+    b.submit_device_table(24, "0" * 64, 0, again[0], kv.device_buffer(t4.ptr, t4.nbytes), len(again[1]))
+    pools.expect(0, *again)
+    b.wait()
+    events, _ = b.poll()
+    assert [(e.bootstrap_room, e.status) for e in events] == [(24, kv.TRANSFER_COMPLETED)]
+    pools.check()
+    b.close()

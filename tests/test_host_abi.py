@@ -420,3 +420,27 @@ def test_sha256_matches_hashlib():
     for n in [0, 1, 55, 56, 63, 64, 65, 119, 120, 1000, 4096 + 3]:
         data = rng.integers(0, 256, n, dtype=np.uint8).tobytes()
         assert kv.sha256_hex(data) == hashlib.sha256(data).hexdigest(), n
+
+
+@pytest.mark.parametrize("rows", [2**32 - 1, 2**32 - 4096 + 1, 2**40])
+def test_row_counts_whose_last_tile_would_wrap_are_refused(rows):
+    """The copy kernels index rows in 32 bits and the last tile of a launch
+    must end below 2^32: the host refuses such row counts with a typed
+    DimensionTooLarge before any device work (checked ahead of the context,
+    so it holds on a host without a GPU)."""
+    import ctypes
+    v = kv.pool_view(0x1000, 1 << 40, page_size=1, page_stride_bytes=256, page_count=1 << 20,
+                     tensor_offset=[0, 128], row_bytes=128, tensor_count=2)
+    r = kv.rows_view([0x2000, 0x3000], [1 << 40, 1 << 40], [128, 128])
+    slots = kv.device_buffer(0x4000, 1 << 40)
+    lib = kv.lib()
+    for rc in (lib.sgl_rocm_kv_pack_layer(None, ctypes.byref(v), ctypes.byref(slots), rows,
+                                          ctypes.byref(r), None),
+               lib.sgl_rocm_kv_unpack_layer(None, ctypes.byref(r), rows, ctypes.byref(v),
+                                            ctypes.byref(slots), None),
+               lib.sgl_rocm_kv_transfer_layer(None, ctypes.byref(v), ctypes.byref(slots), rows,
+                                              ctypes.byref(v), ctypes.byref(slots), None)):
+        assert kv.status_name(rc) == "DimensionTooLarge"
+        d = kv._ErrorDetail()
+        lib.sgl_kv_last_error(ctypes.byref(d))
+        assert d.name == b"row_count" and d.a == rows and d.b == 2**32 - 1 - 4096

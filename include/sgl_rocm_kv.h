@@ -812,6 +812,25 @@ int32_t sgl_rocm_kv_paged_attention_async(sgl_rocm_kv_ctx *ctx, const sgl_kv_att
                                           const sgl_kv_attention_buffers *buffers,
                                           uint64_t max_sequence_length, void *stream);
 
+/* No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). sgl_rocm_kv_paged_attention_async with
+ * the split records in the library's static device workspace of
+ * SGL_KV_NOALLOC_WORKSPACE_BYTES bytes, instead of the context's buffer that
+ * grows on demand: it calls no hipMalloc, hipFree or other allocating
+ * routine. Each device the library runs on holds the workspace until the
+ * process ends (its address is resolved at sgl_rocm_kv_init). A launch whose
+ * records need more is rejected with SGL_KV_DIMENSION_TOO_LARGE (name
+ * "workspace", a = bytes needed, b = the maximum) before anything is
+ * enqueued. Every call on a device shares that device's workspace and the
+ * records a call leaves stay until the next one: calls that overlap in time
+ * on one device race, so issue them on one stream. Results equal those of
+ * sgl_rocm_kv_paged_attention_async on the same arguments. */
+#define SGL_KV_NOALLOC_WORKSPACE_BYTES (128ull << 20)
+int32_t sgl_rocm_kv_paged_attention_async_noalloc(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *plan,
+                                                  const sgl_kv_attention_buffers *buffers,
+                                                  uint64_t max_sequence_length, void *stream);
+
 /* ---- Bootstrap wire format: the decode side's page table and layout ----
  * The multipart frames a decode worker sends a prefill worker's bootstrap
  * listener (Mooncake protocol, crates/sglang-srt/src/pd_bootstrap.rs):

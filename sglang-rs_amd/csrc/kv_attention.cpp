@@ -238,9 +238,12 @@ uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
 
 // Validates, sizes the split and launches the attention (and, with
 // several splits, the combine pass) on `stream`; nothing waits.
+// `workspace` (fixed, `workspace_bytes` long) holds the split records when
+// given; otherwise the context's buffer, grown on demand.
 int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *plan,
                           const sgl_kv_attention_buffers *b, uint64_t max_sequence_length,
-                          hipStream_t s, bool clear_flag) {
+                          hipStream_t s, bool clear_flag, void *workspace = nullptr,
+                          uint64_t workspace_bytes = 0) {
     if (!ctx || !plan || !b)
         return fail(SGL_KV_INVALID_ARGUMENT, "ctx/plan/buffers", 0, 0, 0, "null argument");
     const sgl_kv_attention_plan_config &c = plan->config;
@@ -429,7 +432,13 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
         if (mul_ovf(c.query_count * c.query_head_count, splits, &bytes) ||
             mul_ovf(bytes, (uint64_t)SGLKV_ATTN_OPAD(p.dv) + 2, &bytes) || mul_ovf(bytes, 4, &bytes))
             return attn_overflow();
-        if (bytes > ctx->attention_partial_bytes) {
+        if (workspace) {
+            if (bytes > workspace_bytes)
+                return fail(SGL_KV_DIMENSION_TOO_LARGE, "workspace", bytes, workspace_bytes, 0,
+                            "paged attention needs %llu bytes of split records, more than the "
+                            "%llu-byte workspace",
+                            (unsigned long long)bytes, (unsigned long long)workspace_bytes);
+        } else if (bytes > ctx->attention_partial_bytes) {
             if (ctx->attention_partial) {
                 SGLKV_CHECK_HIP(hipDeviceSynchronize());
                 SGLKV_CHECK_HIP(hipFree(ctx->attention_partial));
@@ -439,7 +448,7 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
             SGLKV_CHECK_HIP(hipMalloc(&ctx->attention_partial, bytes));
             ctx->attention_partial_bytes = bytes;
         }
-        p.partial = static_cast<float *>(ctx->attention_partial);
+        p.partial = static_cast<float *>(workspace ? workspace : ctx->attention_partial);
     }
     if (clear_flag) SGLKV_CHECK_HIP(hipMemsetAsync(ctx->attn_flag, 0, sizeof(uint32_t), s));
     void *args[] = {&p};
@@ -480,5 +489,17 @@ extern "C" int32_t sgl_rocm_kv_paged_attention_async(sgl_rocm_kv_ctx *ctx,
     if (!ctx) return fail(SGL_KV_INVALID_ARGUMENT, "ctx", 0, 0, 0, "null argument");
     const int32_t rc =
         attention_enqueue(ctx, plan, b, max_sequence_length, static_cast<hipStream_t>(stream), false);
+    return rc ? rc : ok();
+}
+
+extern "C" int32_t sgl_rocm_kv_paged_attention_async_noalloc(sgl_rocm_kv_ctx *ctx,
+                                                             const sgl_kv_attention_plan *plan,
+                                                             const sgl_kv_attention_buffers *b,
+                                                             uint64_t max_sequence_length, void *stream) {
+    if (!ctx) return fail(SGL_KV_INVALID_ARGUMENT, "ctx", 0, 0, 0, "null argument");
+    if (!ctx->noalloc_workspace)
+        return fail(SGL_KV_MODULE, "workspace", 0, 0, 0, "the context has no workspace address");
+    const int32_t rc = attention_enqueue(ctx, plan, b, max_sequence_length, static_cast<hipStream_t>(stream),
+                                         false, ctx->noalloc_workspace, SGL_KV_NOALLOC_WORKSPACE_BYTES);
     return rc ? rc : ok();
 }

@@ -82,6 +82,9 @@ int32_t prepare_transfer(const sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src
 int32_t submit_launch(sgl_rocm_kv_ctx *ctx, Launch &l, hipStream_t stream);
 hipStream_t pipeline_final_stream(sgl_rocm_kv_pipeline *pipe);
 void pipeline_set_error_word(sgl_rocm_kv_pipeline *pipe, uint32_t *flag);
+// The device address of the static no-allocation workspace on `device`
+// (resolved once per device; kv_scratch.hip).
+int32_t noalloc_workspace(int device, void **out);
 int32_t hip_fail(hipError_t err, const char *call);
 int32_t flag_status(uint32_t flag);
 int32_t attention_flag_status(uint32_t flag);
@@ -142,6 +145,7 @@ struct sgl_rocm_kv_ctx {
     const uint8_t *zero_row;        // SGLKV_ZERO_ROW_BYTES of zeros inside that block
     void *attention_partial;        // split records, grown on demand
     uint64_t attention_partial_bytes;
+    void *noalloc_workspace;        // this device's static workspace (SGL_KV_NOALLOC_WORKSPACE_BYTES)
     uint32_t rows_per_thread;  // from the code object
     uint32_t max_tile_rows;
 };

@@ -533,6 +533,15 @@ extern "C" int32_t sgl_rocm_kv_init(int32_t device, const char *code_object_path
         delete ctx;
         return hip_fail(err, "sgl_rocm_kv_init");
     }
+    // The no-allocation entry point's workspace on this device, resolved
+    // here once so that the entry point itself does no set-up.
+    int32_t rc = noalloc_workspace(device, &ctx->noalloc_workspace);
+    if (rc) {
+        (void)hipFree(ctx->flag);
+        (void)hipModuleUnload(ctx->module);
+        delete ctx;
+        return rc;
+    }
     *out = ctx;
     return ok();
 }

@@ -430,6 +430,10 @@ _EXPORTS = {
                                                            ctypes.POINTER(_AttentionPlan),
                                                            ctypes.POINTER(_AttentionBuffers), _u64,
                                                            ctypes.c_void_p]),
+    "sgl_rocm_kv_paged_attention_async_noalloc": (ctypes.c_int32, [ctypes.c_void_p,
+                                                                   ctypes.POINTER(_AttentionPlan),
+                                                                   ctypes.POINTER(_AttentionBuffers), _u64,
+                                                                   ctypes.c_void_p]),
     "sgl_rocm_kv_execute_page_requests": (ctypes.c_int32, [ctypes.c_void_p,
                                                            ctypes.POINTER(_DeviceBuffer), _u64, _u64,
                                                            ctypes.POINTER(_DeviceBuffer),
@@ -1062,6 +1066,14 @@ class RocmKvPairCopyKernels:
         _paged_attention(lib().sgl_rocm_kv_paged_attention_async, self, plan, buffers,
                          max_sequence_length, stream)
 
+    def paged_attention_async_noalloc(self, plan: "PagedAttentionPlan", *, max_sequence_length: int = 0,
+                                      stream=None, **buffers):
+        """paged_attention_async with the split records in the library's
+        static device workspace (NOALLOC_WORKSPACE_BYTES per device): no
+        device allocation; launches needing more are refused."""
+        _paged_attention(lib().sgl_rocm_kv_paged_attention_async_noalloc, self, plan, buffers,
+                         max_sequence_length, stream)
+
     def check_errors(self, stream=None):
         _call(lib().sgl_rocm_kv_check_errors, self._h, _stream(stream))
 
@@ -1135,6 +1147,7 @@ class LayerPipeline:
 
 
 BACKEND_DIRECT, BACKEND_STAGED = 0, 1
+NOALLOC_WORKSPACE_BYTES = 128 << 20   # SGL_KV_NOALLOC_WORKSPACE_BYTES
 TRANSFER_COMPLETED, TRANSFER_FAILED, TRANSFER_CANCELED = 0, 1, 2
 
 

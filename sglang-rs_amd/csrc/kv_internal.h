@@ -148,6 +148,7 @@ struct sgl_rocm_kv_ctx {
     void *noalloc_workspace;        // this device's static workspace (SGL_KV_NOALLOC_WORKSPACE_BYTES)
     uint32_t rows_per_thread;  // from the code object
     uint32_t max_tile_rows;
+    uint32_t realign_rows_per_thread;
 };
 
 namespace sglkv {

@@ -40,6 +40,7 @@ typedef __attribute__((address_space(1))) char sglkv_gdst;
 // Tile constants of this code object, read by the launcher at load time.
 extern "C" __device__ uint32_t sglkv_rows_per_thread = SGLKV_ROWS_PER_THREAD;
 extern "C" __device__ uint32_t sglkv_max_tile_rows = SGLKV_MAX_TILE_ROWS;
+extern "C" __device__ uint32_t sglkv_realign_rows_per_thread = SGLKV_REALIGN_ROWS_PER_THREAD;
 
 // Cache policy of each copy direction, as bits: 1 = non-temporal loads,
 // 2 = non-temporal stores (they stream past the caches instead of
@@ -343,6 +344,16 @@ __device__ __forceinline__ void sglkv_realign_rows(const sglkv_realign_params &p
 
     // Phase 2: each aligned destination vector of each segment, shifted out
     // of LDS by the source/destination misalignment.
+    //
+    // Where a segment ends part-way into a 16-byte vector and the next tile
+    // row's same segment starts right there in the destination (consecutive
+    // positions of a page, contiguous transfer rows), the two share that
+    // vector: the next row's first lane writes it whole, with this row's
+    // last bytes, and this row's last lane writes nothing. Only segments of
+    // at least 16 bytes pair up (their first and last vectors are distinct
+    // lanes); both lanes decide from the same three facts (the rows are in
+    // this tile, both are valid, the destinations touch).
+    const uint32_t tile_rows = p.tile_rows;
 #pragma unroll 1
     for (uint32_t k = 0; k < RU; ++k) {
         const uint32_t i = threadIdx.y + k * blockDim.y;
@@ -354,7 +365,24 @@ __device__ __forceinline__ void sglkv_realign_rows(const sglkv_realign_params &p
         const uint32_t sa = static_cast<uint32_t>((src_base + so) & 15u);
         const uint64_t d = dst_base + dof;
         const uint32_t da = static_cast<uint32_t>(d & 15u);
-        if (m >= ((da + c + 15u) >> 4)) continue;
+        const uint32_t kvec = (da + c + 15u) >> 4;
+        if (m >= kvec) continue;
+        const uint32_t lo = m == 0 ? da : 0u;
+        const uint32_t end = da + c - 16u * m;
+        const uint32_t hi = end < 16u ? end : 16u;
+        // The neighbouring tile row's destination offset, when that row
+        // exists, is in this tile and is valid (else INVALID).
+        bool merge_prev = false;
+        if (c >= 16u && lo != 0 && i > 0) {
+            const uint64_t pso = SK == SGLKV_SIDE_POOL ? so_t[i - 1] : (r - 1) * src_stride;
+            const uint64_t pdo = DK == SGLKV_SIDE_POOL ? do_t[i - 1] : (r - 1) * dst_stride;
+            merge_prev = pso != SGLKV_INVALID_OFFSET && pdo != SGLKV_INVALID_OFFSET && pdo + c == dof;
+        }
+        if (c >= 16u && hi < 16u && m + 1 == kvec && i + 1 < tile_rows && r + 1 < p.rows) {
+            const uint64_t nso = SK == SGLKV_SIDE_POOL ? so_t[i + 1] : (r + 1) * src_stride;
+            const uint64_t ndo = DK == SGLKV_SIDE_POOL ? do_t[i + 1] : (r + 1) * dst_stride;
+            if (nso != SGLKV_INVALID_OFFSET && ndo != SGLKV_INVALID_OFFSET && dof + c == ndo) continue;
+        }
         // Segment byte b sits at LDS offset seg + sa + b; destination vector
         // m starts at segment byte 16 m - da. The offset is at least
         // seg - 15, inside the front pad for the first segment.
@@ -362,19 +390,40 @@ __device__ __forceinline__ void sglkv_realign_rows(const sglkv_realign_params &p
         const uint32_t *wp = reinterpret_cast<const uint32_t *>(data + (o & ~3));
         const uint32_t sh = static_cast<uint32_t>(o) & 3u;
         const uint32_t x0 = wp[0], x1 = wp[1], x2 = wp[2], x3 = wp[3], x4 = wp[4];
-        const uint32_t w0 = __builtin_amdgcn_alignbyte(x1, x0, sh);
-        const uint32_t w1 = __builtin_amdgcn_alignbyte(x2, x1, sh);
-        const uint32_t w2 = __builtin_amdgcn_alignbyte(x3, x2, sh);
-        const uint32_t w3 = __builtin_amdgcn_alignbyte(x4, x3, sh);
+        uint32_t w0 = __builtin_amdgcn_alignbyte(x1, x0, sh);
+        uint32_t w1 = __builtin_amdgcn_alignbyte(x2, x1, sh);
+        uint32_t w2 = __builtin_amdgcn_alignbyte(x3, x2, sh);
+        uint32_t w3 = __builtin_amdgcn_alignbyte(x4, x3, sh);
         const uint64_t dv = d - da + 16u * m;
-        const uint32_t lo = m == 0 ? da : 0u;
-        const uint32_t end = da + c - 16u * m;
-        const uint32_t hi = end < 16u ? end : 16u;
-        if (lo == 0 && hi == 16u) {
+        if (merge_prev) {
+            // Bytes [0, da) of the shared vector are the previous row's last
+            // da bytes, in its own LDS area.
+            const uint64_t pso = SK == SGLKV_SIDE_POOL ? so_t[i - 1] : (r - 1) * src_stride;
+            const uint32_t psa = static_cast<uint32_t>((src_base + pso) & 15u);
+            const uint32_t po = (i - 1) * row_lds + seg_lds + psa + c - da;
+            const uint32_t *pp = reinterpret_cast<const uint32_t *>(data + (po & ~3u));
+            const uint32_t psh = po & 3u;
+            const uint32_t y0 = pp[0], y1 = pp[1], y2 = pp[2], y3 = pp[3], y4 = pp[4];
+            const uint32_t v[4] = {__builtin_amdgcn_alignbyte(y1, y0, psh), __builtin_amdgcn_alignbyte(y2, y1, psh),
+                                   __builtin_amdgcn_alignbyte(y3, y2, psh), __builtin_amdgcn_alignbyte(y4, y3, psh)};
+            // byte j < da from the previous row
+#define SGLKV_MERGE(J, W)                                                                  \
+    {                                                                                      \
+        const uint32_t nb = da > 4u * (J) ? (da - 4u * (J) >= 4u ? 4u : da - 4u * (J)) : 0u; \
+        const uint32_t mask = nb == 4u ? 0xFFFFFFFFu : (1u << (8u * nb)) - 1u;            \
+        W = (v[J] & mask) | (W & ~mask);                                                   \
+    }
+            SGLKV_MERGE(0, w0)
+            SGLKV_MERGE(1, w1)
+            SGLKV_MERGE(2, w2)
+            SGLKV_MERGE(3, w3)
+#undef SGLKV_MERGE
+        }
+        if ((lo == 0 || merge_prev) && hi == 16u) {
             const sglkv_v4u v = {w0, w1, w2, w3};
             sglkv_store<sglkv_v4u, NT>(reinterpret_cast<gstore_t *>(dv), v);
         } else {
-            sglkv_store_partial<NT>(dv, lo, hi, w0, w1, w2, w3);
+            sglkv_store_partial<NT>(dv, merge_prev ? 0u : lo, hi, w0, w1, w2, w3);
         }
     }
 }
@@ -416,11 +465,25 @@ SGLKV_COPY_KERNELS(1)
         sglkv_realign_rows<SK, DK, NT, REMAP>(p);                                      \
     }
 
-SGLKV_REALIGN_KERNEL(SGLKV_SIDE_POOL, SGLKV_SIDE_ROWS, SGLKV_PACK_NT, SGLKV_PACK_REMAP,
+// Cache policy and tile order of the realigning kernels (bits as above).
+#ifndef SGLKV_REALIGN_PACK_NT
+#define SGLKV_REALIGN_PACK_NT SGLKV_PACK_NT
+#endif
+#ifndef SGLKV_REALIGN_UNPACK_NT
+#define SGLKV_REALIGN_UNPACK_NT SGLKV_UNPACK_NT
+#endif
+#ifndef SGLKV_REALIGN_TRANSFER_NT
+#define SGLKV_REALIGN_TRANSFER_NT SGLKV_TRANSFER_NT
+#endif
+#ifndef SGLKV_REALIGN_REMAP
+#define SGLKV_REALIGN_REMAP 1
+#endif
+
+SGLKV_REALIGN_KERNEL(SGLKV_SIDE_POOL, SGLKV_SIDE_ROWS, SGLKV_REALIGN_PACK_NT, SGLKV_PACK_REMAP,
                      sglkv_realign_pool_rows)
-SGLKV_REALIGN_KERNEL(SGLKV_SIDE_ROWS, SGLKV_SIDE_POOL, SGLKV_UNPACK_NT, SGLKV_UNPACK_REMAP,
+SGLKV_REALIGN_KERNEL(SGLKV_SIDE_ROWS, SGLKV_SIDE_POOL, SGLKV_REALIGN_UNPACK_NT, SGLKV_REALIGN_REMAP,
                      sglkv_realign_rows_pool)
-SGLKV_REALIGN_KERNEL(SGLKV_SIDE_POOL, SGLKV_SIDE_POOL, SGLKV_TRANSFER_NT, SGLKV_TRANSFER_REMAP,
+SGLKV_REALIGN_KERNEL(SGLKV_SIDE_POOL, SGLKV_SIDE_POOL, SGLKV_REALIGN_TRANSFER_NT, SGLKV_REALIGN_REMAP,
                      sglkv_realign_pool_pool)
 
 // Spans + page table -> one physical slot per row (the decode side's

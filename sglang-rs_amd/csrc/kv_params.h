@@ -123,13 +123,16 @@ typedef struct sglkv_realign_params {
                                with nothing to load */
 } sglkv_realign_params;
 
-/* Realigning kernel limits: rows a thread keeps in flight, and the LDS bytes
- * a workgroup's tile of rows may take (the launcher shrinks the tile to
- * fit; rows wider than SGLKV_REALIGN_MAX_ROW_VECTORS vectors use the plain
+/* Realigning kernel limits: rows a thread keeps in flight (the code object
+ * exports the value it was built with, sglkv_realign_rows_per_thread, and
+ * the launcher sizes tiles from it), and the widest row it takes (rows
+ * wider than SGLKV_REALIGN_MAX_ROW_VECTORS LDS vectors use the plain
  * kernels with narrower accesses). The LDS buffer carries 16 bytes of
  * padding before the first row and SGLKV_REALIGN_TAIL_PAD after the last,
  * so that the shifted reads of the first and last vectors stay inside it. */
-#define SGLKV_REALIGN_ROWS_PER_THREAD 8u
+#ifndef SGLKV_REALIGN_ROWS_PER_THREAD
+#define SGLKV_REALIGN_ROWS_PER_THREAD 4u  /* measured on MI355X (649-byte rows): 4 over 2, 8, 16 */
+#endif
 #define SGLKV_REALIGN_MAX_ROW_VECTORS 256u
 #define SGLKV_REALIGN_TAIL_PAD 32u
 /* Dynamic LDS of a realigning workgroup: the tile's staged row offsets

@@ -221,7 +221,7 @@ std::string default_code_object() {
 // Fills the launch geometry of a validated copy (vector width, tile) from
 // the context's code-object constants.
 // The byte-realigning kernel's launch: one thread per LDS vector of a row
-// (blockDim.x = vrow), SGLKV_REALIGN_ROWS_PER_THREAD rows per thread.
+// (blockDim.x = vrow), the code object's realign rows per thread.
 // Returns false when a row's LDS footprint is too wide for it.
 bool plan_realign(const sgl_rocm_kv_ctx *ctx, Launch *l) {
     const RowShape &shape = l->shape;
@@ -251,12 +251,13 @@ bool plan_realign(const sgl_rocm_kv_ctx *ctx, Launch *l) {
     r.rows = (uint32_t)l->rows;
     r.vt0 = (uint32_t)vt0;
     r.vrow = (uint32_t)vrow;
-    r.rows_per_thread = SGLKV_REALIGN_ROWS_PER_THREAD;
+    r.rows_per_thread = ctx->realign_rows_per_thread;
     r.zero = ctx->zero_row;
     l->block_x = (uint32_t)vrow;
     l->block_y = SGLKV_BLOCK_THREADS / l->block_x;
-    if (l->block_y > 64) l->block_y = 64;  // tiles of at most 512 rows
-    r.tile_rows = l->block_y * SGLKV_REALIGN_ROWS_PER_THREAD;
+    // Tiles of at most 512 rows.
+    if (l->block_y * r.rows_per_thread > 512) l->block_y = 512 / r.rows_per_thread;
+    r.tile_rows = l->block_y * r.rows_per_thread;
     l->lds_bytes = SGLKV_REALIGN_LDS_BYTES(r.tile_rows, r.vrow);
     if (l->lds_bytes > (uint32_t)ctx->max_lds_per_block) return false;
     l->grid = (l->rows + r.tile_rows - 1) / r.tile_rows;
@@ -506,16 +507,18 @@ extern "C" int32_t sgl_rocm_kv_init(int32_t device, const char *code_object_path
         err = hipModuleGetFunction(&ctx->attention_combine, ctx->module, "sglkv_paged_attention_combine");
     if (err == hipSuccess) err = hipDeviceGetAttribute(&ctx->cu_count, hipDeviceAttributeMultiprocessorCount, device);
     // The tile constants the kernels were compiled with.
-    const char *const constants[2] = {"sglkv_rows_per_thread", "sglkv_max_tile_rows"};
-    uint32_t *const values[2] = {&ctx->rows_per_thread, &ctx->max_tile_rows};
-    for (int i = 0; i < 2 && err == hipSuccess; ++i) {
+    const char *const constants[3] = {"sglkv_rows_per_thread", "sglkv_max_tile_rows",
+                                      "sglkv_realign_rows_per_thread"};
+    uint32_t *const values[3] = {&ctx->rows_per_thread, &ctx->max_tile_rows, &ctx->realign_rows_per_thread};
+    for (int i = 0; i < 3 && err == hipSuccess; ++i) {
         hipDeviceptr_t addr = nullptr;
         size_t bytes = 0;
         err = hipModuleGetGlobal(&addr, &bytes, ctx->module, constants[i]);
         if (err == hipSuccess && bytes != sizeof(uint32_t)) err = hipErrorInvalidSymbol;
         if (err == hipSuccess) err = hipMemcpyDtoH(values[i], addr, sizeof(uint32_t));
     }
-    if (err == hipSuccess && (ctx->rows_per_thread == 0 || ctx->rows_per_thread > ctx->max_tile_rows))
+    if (err == hipSuccess && (ctx->rows_per_thread == 0 || ctx->rows_per_thread > ctx->max_tile_rows ||
+                              ctx->realign_rows_per_thread == 0 || ctx->realign_rows_per_thread > 32))
         err = hipErrorInvalidImage;
     // One small block: the error words at offsets 0, 64 and 128 (separate
     // lines), check_errors' readout at 192, the zero row at 256.

@@ -264,7 +264,7 @@ def paged_attention(pool: np.ndarray, queries: np.ndarray, query_request_indices
                     query_sequence_lengths, request_slot_offsets, sequence_slots, *,
                     page_size: int, page_stride: int, key_offset: int, value_offset: int,
                     kv_heads: int, dk: int, dv: int, scale: float, slot_count: int,
-                    hnd: bool = False):
+                    hnd: bool = False, with_abs: bool = False):
     """sglang_paged_attention_bf16 (crates/sglang-kernel/src/cuda_attention.rs:
     14-155) in float64: for query q of request r, softmax(scale * q.k) . v over
     the first len_q slots of r's slot list; query head h reads KV head
@@ -275,7 +275,9 @@ def paged_attention(pool: np.ndarray, queries: np.ndarray, query_request_indices
     `pool` is the pool's bytes (uint8), `queries` bf16 bits [Q][QH][dk].
     Returns (out float64 [Q][QH][dv] with NaN rows for rejected queries,
     flags): the reference's metadata checks (:59-82) and slot check (:96-99)
-    set flag bits 1, 2, 4 and skip the query.
+    set flag bits 1, 2, 4 and skip the query. With `with_abs`, a third array
+    holds sum_i w_i |v_i| per output element (w the softmax weights): the
+    scale of the error that rounding the weights introduces.
     """
     q_bits = np.asarray(queries, dtype=np.uint16)
     nq, qh, _ = q_bits.shape
@@ -287,6 +289,7 @@ def paged_attention(pool: np.ndarray, queries: np.ndarray, query_request_indices
     slots_all = np.asarray(sequence_slots, dtype=np.uint64)
     request_count = len(rso) - 1
     out = np.full((nq, qh, dv), np.nan)
+    absw = np.full((nq, qh, dv), np.nan)
     flags = 0
     for q in range(nq):
         r = int(qri[q])
@@ -316,4 +319,5 @@ def paged_attention(pool: np.ndarray, queries: np.ndarray, query_request_indices
             s -= s.max(axis=1, keepdims=True)
             w = np.exp(s)
             out[q, g * group:(g + 1) * group] = (w @ v) / w.sum(axis=1, keepdims=True)
-    return out, flags
+            absw[q, g * group:(g + 1) * group] = (w @ np.abs(v)) / w.sum(axis=1, keepdims=True)
+    return (out, flags, absw) if with_abs else (out, flags)

@@ -17,7 +17,10 @@
 //    as B, so no cross-lane reduction is needed;
 //  - p.v is a second MFMA: the probabilities come out of the first one
 //    already in the A-operand layout of the second (lane l holds head l%16,
-//    tokens 8*(l/16)..+7); V is transposed through LDS into the B layout;
+//    tokens 8*(l/16)..+7); V is transposed through LDS into the B layout.
+//    Each probability enters as two bf16 values, hi + lo (two MFMAs), so
+//    the weights keep about 16 significant bits rather than bf16's 8; the
+//    latent body (MLA), whose matrix cores are its busiest unit, takes one;
 //  - long sequences are split over gridDim.y (flash-decoding): each split
 //    writes (max, sum, unnormalised output) and a combine kernel merges
 //    them, so a small batch still fills 256 CUs.
@@ -69,6 +72,19 @@ __device__ __forceinline__ sglkv_u16x8 attn_load8(uint64_t row, uint32_t dim, ui
 
 __device__ __forceinline__ uint16_t attn_to_bf16(float x) {
     return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
+}
+
+// A softmax weight as the sum of two bf16 values, hi = RN(x) and
+// lo = RN(x - hi): x - hi is exact in fp32 (|x - hi| <= 2^-8 |x|, at most
+// 16 significant bits), so |x - (hi + lo)| <= 2^-16 |x|. The p.v products
+// take hi.v + lo.v (two MFMAs into one fp32 accumulator), which keeps the
+// weights' error near fp32's instead of bf16's 2^-8; the reference weights
+// its values in fp32 (cuda_attention.rs:140-149).
+// Element i of the hi and lo operand vectors.
+__device__ __forceinline__ void attn_split_bf16(float x, sglkv_u16x8 &hi, sglkv_u16x8 &lo, uint32_t i) {
+    const __bf16 h = static_cast<__bf16>(x);
+    hi[i] = __builtin_bit_cast(uint16_t, h);
+    lo[i] = attn_to_bf16(x - static_cast<float>(h));
 }
 
 // Query-level metadata checks of the reference kernel (cuda_attention.rs:
@@ -193,13 +209,13 @@ __device__ __forceinline__ void attn_softmax_pv(const sglkv_attn_params &p, uint
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float m_new = fmaxf(st.m_run, mx);
     const float alpha = exp2f(st.m_run - m_new);
-    sglkv_u16x8 pbits;
+    sglkv_u16x8 phi, plo;
     float psum = 0.0f;
 #pragma unroll
     for (uint32_t i = 0; i < 8; ++i) {
         const float pi = exp2f(x[i] - m_new);
         psum += pi;
-        pbits[i] = attn_to_bf16(pi);
+        attn_split_bf16(pi, phi, plo, i);
     }
     st.l_part = st.l_part * alpha + psum;
     st.m_run = m_new;
@@ -214,13 +230,13 @@ __device__ __forceinline__ void attn_softmax_pv(const sglkv_attn_params &p, uint
         for (uint32_t e = 0; e < 4; ++e) st.o[j][e] *= arow[e];
 
     __builtin_amdgcn_wave_barrier();
-    // o[head 4g+e][dim 16j + r] += sum_t p[head][t] * v[t][dim].
+    // o[head 4g+e][dim 16j + r] += sum_t p[head][t] * v[t][dim], p = hi + lo.
 #pragma unroll
     for (uint32_t j = 0; j < NJ; ++j) {
         if (!FULL_DV && d0 + 16 * j >= p.dv) break;
         const sglkv_u16x8 vv = *reinterpret_cast<const sglkv_u16x8 *>(vt + (16 * j + r) * VTS + 8 * g);
-        st.o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(pbits), attn_as_bf16(vv), st.o[j], 0,
-                                                          0, 0);
+        st.o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(phi), attn_as_bf16(vv), st.o[j], 0, 0, 0);
+        st.o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(plo), attn_as_bf16(vv), st.o[j], 0, 0, 0);
     }
     __builtin_amdgcn_wave_barrier();
 }
@@ -825,7 +841,7 @@ __device__ __forceinline__ void attn_wide_pv(const sglkv_attn_params &p, const u
         }
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    sglkv_u16x8 pbits;
+    sglkv_u16x8 phi, plo;
     float psum = 0.0f;
     if (EXACT) {
         const float m_new = fmaxf(st.m_run, mx);
@@ -834,7 +850,7 @@ __device__ __forceinline__ void attn_wide_pv(const sglkv_attn_params &p, const u
         for (uint32_t i = 0; i < 8; ++i) {
             const float pi = exp2f(x[i] - m_new);
             psum += pi;
-            pbits[i] = attn_to_bf16(pi);
+            attn_split_bf16(pi, phi, plo, i);
         }
         st.l_part = st.l_part * alpha + psum;
         st.m_run = m_new;
@@ -855,7 +871,7 @@ __device__ __forceinline__ void attn_wide_pv(const sglkv_attn_params &p, const u
         for (uint32_t i = 0; i < 8; ++i) {
             const float pi = exp2f(fminf(x[i] - m_ref, SGLKV_ATTN_FIXED_MAX_LOG2));
             psum += pi;
-            pbits[i] = attn_to_bf16(pi);
+            attn_split_bf16(pi, phi, plo, i);
         }
         st.l_part += psum;
     }
@@ -873,16 +889,17 @@ __device__ __forceinline__ void attn_wide_pv(const sglkv_attn_params &p, const u
     for (uint32_t j = 0; j < G::NJH; ++j) {
         const sglkv_u16x8 vv = {(uint16_t)vlo[j][0], (uint16_t)vlo[j][1], (uint16_t)vlo[j][2], (uint16_t)vlo[j][3],
                                 (uint16_t)vhi[j][0], (uint16_t)vhi[j][1], (uint16_t)vhi[j][2], (uint16_t)vhi[j][3]};
-        st.o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(pbits), attn_as_bf16(vv), st.o[j], 0, 0, 0);
+        st.o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(phi), attn_as_bf16(vv), st.o[j], 0, 0, 0);
+        st.o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(plo), attn_as_bf16(vv), st.o[j], 0, 0, 0);
     }
     if (PIN) {
         __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * G::PV_AHEAD, 1);
 #pragma unroll
         for (uint32_t j = 0; j < G::NJH - G::PV_AHEAD; ++j) {
-            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 1);
+            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 1);
             __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 1);
         }
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, G::PV_AHEAD, 1);
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2 * G::PV_AHEAD, 1);
     }
 }
 
@@ -1623,13 +1640,13 @@ __device__ __forceinline__ void attn_stg_softmax_pv(const sglkv_attn_params &p, 
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float m_new = fmaxf(st.m_run, mx);
     const float alpha = exp2f(st.m_run - m_new);
-    sglkv_u16x8 pbits;
+    sglkv_u16x8 phi, plo;
     float psum = 0.0f;
 #pragma unroll
     for (uint32_t i = 0; i < 8; ++i) {
         const float pi = exp2f(x[i] - m_new);
         psum += pi;
-        pbits[i] = attn_to_bf16(pi);
+        attn_split_bf16(pi, phi, plo, i);
     }
     st.l_part = st.l_part * alpha + psum;
     st.m_run = m_new;
@@ -1649,7 +1666,8 @@ __device__ __forceinline__ void attn_stg_softmax_pv(const sglkv_attn_params &p, 
         const attn_i16x4 hi = attn_lat_vtr(vst + S::ROW * t1 + 16 * S::vpos(t1, pc) + half);
         const sglkv_u16x8 vv = {(uint16_t)lo[0], (uint16_t)lo[1], (uint16_t)lo[2], (uint16_t)lo[3],
                                 (uint16_t)hi[0], (uint16_t)hi[1], (uint16_t)hi[2], (uint16_t)hi[3]};
-        st.o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(pbits), attn_as_bf16(vv), st.o[j], 0, 0, 0);
+        st.o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(phi), attn_as_bf16(vv), st.o[j], 0, 0, 0);
+        st.o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(plo), attn_as_bf16(vv), st.o[j], 0, 0, 0);
     }
 }
 

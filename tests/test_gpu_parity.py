@@ -11,9 +11,7 @@ Cases:
   - edge cases: empty and single-row transfers, ragged tile tails,
     unaligned row strides (every vector width), out-of-range slots and page
     entries (typed errors, untouched bytes);
-  - C2 at full size (131,072 rows, 32 GiB pools) on three layers, checked
-    against the host copy of the synthetic source bytes and a
-    pack -> unpack -> re-pack round trip.
+  - (every benchmark configuration at full size: tests/test_gpu_full_size.py).
 """
 import numpy as np
 import pytest
@@ -413,48 +411,6 @@ def test_host_validation_errors(k):
     with pytest.raises(kv.KvError) as ei:
         k.pack_layer(_kpool(pool, spec, shape, 1), _db(sl), 8, rv_stride)
     assert ei.value.variant == "RowStrideTooSmall"
-
-
-# --- C2 at full size ----------------------------------------------------------------------------------
-
-def test_c2_full_size_three_layers(k):
-    """131,072 rows, 32 GiB source (P=1) and destination (P=64) pools. The
-    source is filled on the device with the reproducible splitmix64 stream,
-    so every packed byte is checked against host-computed source words; the
-    unpacked pool is checked by re-packing it with the destination slots."""
-    t = wl.c2()
-    sh = t.shape
-    rb, n = sh.row_bytes, t.rows
-    free, _ = hip.mem_info()
-    need = t.src.byte_len(sh) + t.dst.byte_len(sh) + 4 * n * rb + 16 * n
-    if free < need + (4 << 30):
-        pytest.skip(f"needs {need >> 30} GiB of device memory, {free >> 30} GiB free")
-    _say(f"C2 full size: {n} rows, pools {t.src.byte_len(sh) >> 30}+{t.dst.byte_len(sh) >> 30} GiB")
-    seed = 0x5EED
-    src, dst = hip.DeviceBuffer(t.src.byte_len(sh)), hip.DeviceBuffer(t.dst.byte_len(sh))
-    k.fill_synthetic(_db(src), seed, kv.FILL_BITS)
-    k.fill_synthetic(_db(dst), seed + 1, kv.FILL_BITS)
-    ss, ds = hip.DeviceBuffer.from_array(t.src_slots), hip.DeviceBuffer.from_array(t.dst_slots)
-    rows, again = hip.DeviceBuffer(2 * n * rb), hip.DeviceBuffer(2 * n * rb)
-    rv = kv.rows_view([rows.ptr, rows.ptr + n * rb], [n * rb] * 2, [rb, rb])
-    av = kv.rows_view([again.ptr, again.ptr + n * rb], [n * rb] * 2, [rb, rb])
-    wpr = rb // 8
-    for layer in (0, 17, 31):
-        _say(f"C2 full size: layer {layer}")
-        k.pack_layer(_kpool(src, t.src, sh, layer), _db(ss), n, rv)
-        k.unpack_layer(rv, n, _kpool(dst, t.dst, sh, layer), _db(ds))
-        k.pack_layer(_kpool(dst, t.dst, sh, layer), _db(ds), n, av)
-        k.check_errors()
-        got = rows.download(dtype=np.uint64).reshape(2, n, wpr)
-        for tns in range(2):
-            first = (t.src_slots.astype(np.uint64) * np.uint64(t.src.page_stride(sh))
-                     + np.uint64(t.src.tensor_offsets(sh, layer)[tns])) // np.uint64(8)
-            for lo in range(0, n, 16384):
-                hi = min(n, lo + 16384)
-                idx = first[lo:hi, None] + np.arange(wpr, dtype=np.uint64)[None, :]
-                want = kv.synthetic_words(seed, idx.reshape(-1))
-                np.testing.assert_array_equal(got[tns, lo:hi].reshape(-1), want)
-        assert np.array_equal(rows.download(), again.download()), "unpack -> re-pack round trip differs"
 
 
 # --- layer pipeline (pack -> pinned-host hop -> unpack) ----------------------------------------

@@ -142,9 +142,11 @@ def cpu_baseline(make, seconds: float = 10.0, rows: int | None = 8192, threads: 
     rb = [sh.tensor_row_bytes(i) for i in range(T)] + [0]
     lrb = sh.layer_row_bytes
     rng = np.random.default_rng(0)
-    # (the whole workload's pools: zeros, faulted in by the untimed pass;
-    # byte values do not change a copy's speed)
-    src = (np.zeros(t.src.byte_len(sh), np.uint8) if rows is None
+    # (the whole workload's source pool: one byte value written over every
+    # page, so each page is backed by its own memory; byte values do not
+    # change a copy's speed, but an array never written maps every page to
+    # the kernel's one zero page, whose reads hit in cache)
+    src = (np.full(t.src.byte_len(sh), 0xA5, np.uint8) if rows is None
            else rng.integers(0, 256, t.src.byte_len(sh), dtype=np.uint8))
     dst = np.zeros(t.dst.byte_len(sh), np.uint8)
     buf = np.zeros(sh.layers * n * lrb, np.uint8)

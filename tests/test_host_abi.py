@@ -145,6 +145,36 @@ def test_layout_agrees_with_the_oracle_on_random_shapes():
             assert rc == 0 and lay.tensor_slot_byte_range(layer, t, slot) == rngo
 
 
+def test_pair_layout_agrees_with_the_oracle_on_random_pair_shapes():
+    """Tensor-pair pools with unequal key and value widths (the MLA form,
+    kv_cache.rs:436-823 with key/value token bytes): every byte range the
+    product computes, and its pool view's per-tensor row widths, equal the
+    oracle's pair arithmetic (pinned by the asymmetric-pair goldens)."""
+    import oracle
+    rng = np.random.default_rng(7)
+    for _ in range(30):
+        P, L, pages = int(rng.choice([1, 2, 16, 64])), int(rng.integers(1, 6)), int(rng.integers(1, 5))
+        kb = 2 * int(rng.integers(1, 700))
+        vb = 2 * int(rng.integers(1, 700))
+        if kb == vb:
+            vb += 2
+        bpt = L * (kb + vb)
+        rt = kv.KvCacheRuntimeLayout("bf16", P, L, 1, kb // 2, 2, bpt, P * bpt)
+        lay = kv.PagedKvCacheLayout.new_with_tensor_pair(rt, pages, kb, vb)
+        olay = oracle.layout(P, L, 2, bpt, P * bpt, pages)
+        assert lay.total_byte_len == P * bpt * pages
+        for _ in range(12):
+            slot, layer, t = int(rng.integers(0, pages * P)), int(rng.integers(0, L)), int(rng.integers(0, 2))
+            rc, want = oracle.pair_tensor_token_byte_range(olay, kb, vb, slot // P, layer, t, slot % P)
+            assert rc == 0 and lay.tensor_slot_byte_range(layer, t, slot) == want, (P, L, kb, vb, slot, layer, t)
+        layer = int(rng.integers(0, L))
+        view = lay.pool_view(0x10000, lay.total_byte_len, layer, kv.NHD, 1)
+        assert view.tensor_row_bytes(0) == kb and view.tensor_row_bytes(1) == vb
+        for t in range(2):
+            rc, (s, _) = oracle.pair_tensor_token_byte_range(olay, kb, vb, 0, layer, t, 0)
+            assert rc == 0 and view.tensor_offset[t] == s
+
+
 def test_pair_copy_plan_goldens(goldens):
     g = goldens["pair_copy_plan"]
     lay = kv.KvPairCopyLayout(**g["layout"])

@@ -205,6 +205,14 @@ def test_oracle_attention_closed_forms_and_flags():
     np.testing.assert_array_equal(out[0, 0], vrow(2))
     np.testing.assert_allclose(out[1, 0], np.mean([vrow(s) for s in range(4)], axis=0), rtol=1e-12)
     assert flags == 0
+    # sum_i w_i |v_i| (the error model's weight term): |v| of the one
+    # token, the mean of |v| under equal keys; never below |out|.
+    out2, flags, absw = oracle.paged_attention(pool, q, [0, 0], [1, 4], [0, 4], [2, 1, 0, 3], with_abs=True,
+                                               **args)
+    np.testing.assert_array_equal(out2, out)
+    np.testing.assert_array_equal(absw[0, 0], np.abs(vrow(2)))
+    np.testing.assert_allclose(absw[1, 0], np.mean([np.abs(vrow(s)) for s in range(4)], axis=0), rtol=1e-12)
+    assert flags == 0 and (absw >= np.abs(out) - 1e-12).all()
     _, flags = oracle.paged_attention(pool, q, [1, 0], [1, 1], [0, 4], [0, 1, 2, 3], **args)
     assert flags == oracle.FLAG_ATTN_REQUEST
     _, flags = oracle.paged_attention(pool, q, [0, 0], [0, 5], [0, 4], [0, 1, 2, 3], **args)

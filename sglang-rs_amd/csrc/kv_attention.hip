@@ -1022,7 +1022,8 @@ __device__ __forceinline__ void attn_wide_body(const sglkv_attn_params &p) {
     }
     if (active && __any(over) && lane == 0) *redo = 1;
     __syncthreads();
-    if (*redo) {
+    // Read as a wave-uniform value, so the branch is a scalar one.
+    if (__builtin_amdgcn_readfirstlane(*redo)) {
         // A block outran the fixed reference by more than the bound: the
         // split again, one block at a time, with the running maximum.
         attn_state_init(st);
@@ -1439,7 +1440,8 @@ __device__ __forceinline__ void attn_latent_body(const sglkv_attn_params &p) {
     attn_lat_barrier<0>();
     if (active && __any(over) && lane == 0) *redo = 1;
     __syncthreads();
-    if (*redo) {
+    // Read as a wave-uniform value, so the branch is a scalar one.
+    if (__builtin_amdgcn_readfirstlane(*redo)) {
         // A block outran the fixed reference: each head's true maximum over
         // the split (q.k only), then the split again with that maximum as
         // the reference, which no block can outrun.
@@ -1472,18 +1474,34 @@ __device__ __forceinline__ void attn_latent_body(const sglkv_attn_params &p) {
 
     // Output (one split) or the split record [m, l, o[0..dv)]: o[n][r] is
     // head 8(r/4) + 4(l/32) + r%4, dim 32n + l%32; m and l of head l%32.
+    // dv is 512 (the host takes this body only then).
     const float l_tot = l_part + __shfl_xor(l_part, 32);
-    const uint32_t hl = lane & 31, hh = lane >> 5;
+    // The lane index as a fresh value: derived from the prologue's, it (and
+    // the head-row index computed from it there) would be kept live across
+    // the loop, where every register is taken, and so spilled.
+    uint32_t lane_e = lane;
+    asm volatile("" : "+v"(lane_e));
+    const uint32_t hl = lane_e & 31, hh = lane_e >> 5;
     if (p.splits == 1) {
+        float linv[16];
 #pragma unroll
-        for (uint32_t r = 0; r < 16; ++r) {
-            const uint32_t head = 8 * (r >> 2) + 4 * hh + (r & 3);
-            const float linv = 1.0f / __shfl(l_tot, head);
-            if (head >= nh) continue;
-            uint16_t *out = p.output + (q * p.query_heads + h0 + head) * p.dv;
+        for (uint32_t r = 0; r < 16; ++r) linv[r] = 1.0f / __shfl(l_tot, 8 * (r >> 2) + 4 * hh + (r & 3));
+        uint16_t *out = p.output + (q * p.query_heads + h0 + 4 * hh) * 512 + hl;
+        // Each accumulator is read out (v_accvgpr_read) right where it is
+        // scaled and stored. Left to the compiler, all 256 are copied to
+        // VGPRs at the loop's end, which do not hold them. The last MFMA
+        // writing them is at least 20 wait states back (the nops; an 8-pass
+        // 32x32 MFMA needs 18 before its result is read).
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3");
 #pragma unroll
-            for (uint32_t n = 0; n < kLatNT; ++n)
-                if (32 * n + hl < p.dv) out[32 * n + hl] = attn_to_bf16(o[n][r] * linv);
+        for (uint32_t n = 0; n < kLatNT; ++n) {
+#pragma unroll
+            for (uint32_t r = 0; r < 16; ++r) {
+                if (8 * (r >> 2) + 4 * hh + (r & 3) >= nh) continue;
+                float x;
+                asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(x) : "a"(o[n][r]));
+                out[(8 * (r >> 2) + (r & 3)) * 512 + 32 * n] = attn_to_bf16(x * linv[r]);
+            }
         }
     } else {
         if (hh == 0 && hl < nh) {
@@ -1497,8 +1515,7 @@ __device__ __forceinline__ void attn_latent_body(const sglkv_attn_params &p) {
             if (head >= nh) continue;
             float *pr = attn_rec_o(p, (q * p.query_heads + h0 + head) * p.splits + split);
 #pragma unroll
-            for (uint32_t n = 0; n < kLatNT; ++n)
-                if (32 * n + hl < p.dv) __builtin_nontemporal_store(o[n][r], pr + 32 * n + hl);
+            for (uint32_t n = 0; n < kLatNT; ++n) __builtin_nontemporal_store(o[n][r], pr + 32 * n + hl);
         }
     }
 }

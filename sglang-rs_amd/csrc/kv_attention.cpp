@@ -427,10 +427,13 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
     p.chunk_tokens = chunk;
     p.splits = (uint32_t)splits;
 
+    // The latent body writes scaled fp16 records (SGLKV_ATTN_HPAD), the
+    // others fp32 ones (SGLKV_ATTN_OPAD).
+    const bool half_records = which == 6;
     if (splits > 1) {
         uint64_t bytes;
-        if (mul_ovf(c.query_count * c.query_head_count, splits, &bytes) ||
-            mul_ovf(bytes, (uint64_t)SGLKV_ATTN_OPAD(p.dv) + 2, &bytes) || mul_ovf(bytes, 4, &bytes))
+        const uint64_t per_record = half_records ? 2ull * SGLKV_ATTN_HPAD(p.dv) + 16 : 4ull * (SGLKV_ATTN_OPAD(p.dv) + 2);
+        if (mul_ovf(c.query_count * c.query_head_count, splits, &bytes) || mul_ovf(bytes, per_record, &bytes))
             return attn_overflow();
         if (workspace) {
             if (bytes > workspace_bytes)
@@ -455,9 +458,9 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
     SGLKV_CHECK_HIP(hipModuleLaunchKernel(ctx->attention[which], (unsigned)base, (unsigned)splits, 1, threads,
                                           1, 1, lds, s, args, nullptr));
     if (splits > 1)
-        SGLKV_CHECK_HIP(hipModuleLaunchKernel(ctx->attention_combine,
-                                              (unsigned)(c.query_count * c.query_head_count), 1, 1, 128,
-                                              1, 1, 0, s, args, nullptr));
+        SGLKV_CHECK_HIP(hipModuleLaunchKernel(half_records ? ctx->attention_combine_h : ctx->attention_combine,
+                                              (unsigned)(c.query_count * c.query_head_count), 1, 1,
+                                              half_records ? 64 : 128, 1, 1, 0, s, args, nullptr));
     return SGL_KV_OK;
 }
 

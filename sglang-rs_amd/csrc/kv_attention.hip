@@ -253,6 +253,15 @@ __device__ __forceinline__ float *attn_rec_o(const sglkv_attn_params &p, uint64_
 __device__ __forceinline__ float *attn_rec_ml(const sglkv_attn_params &p, uint64_t i) {
     return p.partial + p.query_count * p.query_heads * p.splits * SGLKV_ATTN_OPAD(p.dv) + 2 * i;
 }
+// The latent body's scaled fp16 records: y row and (m, l, a, 0) of record i.
+__device__ __forceinline__ uint16_t *attn_rec_y(const sglkv_attn_params &p, uint64_t i) {
+    return reinterpret_cast<uint16_t *>(p.partial) + i * SGLKV_ATTN_HPAD(p.dv);
+}
+__device__ __forceinline__ float *attn_rec_mla(const sglkv_attn_params &p, uint64_t i) {
+    return reinterpret_cast<float *>(reinterpret_cast<uint16_t *>(p.partial) +
+                                     p.query_count * p.query_heads * p.splits * SGLKV_ATTN_HPAD(p.dv)) +
+           4 * i;
+}
 
 // Output (one split) or the split record (m, l, o[0..dv)).
 template <int NJ>
@@ -1504,18 +1513,39 @@ __device__ __forceinline__ void attn_latent_body(const sglkv_attn_params &p) {
             }
         }
     } else {
+        // Scaled fp16 record: a = max |o| over the head's 512 dims (the
+        // lane's 16 values, then the 32 lanes of its half-wave), y = o / a.
+        // y's rounding moves o by at most 2^-11 |o| + 2^-25 a.
         if (hh == 0 && hl < nh) {
-            float *pr = attn_rec_ml(p, (q * p.query_heads + h0 + hl) * p.splits + split);
+            float *pr = attn_rec_mla(p, (q * p.query_heads + h0 + hl) * p.splits + split);
             __builtin_nontemporal_store(m_run, pr);
             __builtin_nontemporal_store(l_tot, pr + 1);
         }
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3");
 #pragma unroll
         for (uint32_t r = 0; r < 16; ++r) {
             const uint32_t head = 8 * (r >> 2) + 4 * hh + (r & 3);
-            if (head >= nh) continue;
-            float *pr = attn_rec_o(p, (q * p.query_heads + h0 + head) * p.splits + split);
+            float a = 0.0f;
 #pragma unroll
-            for (uint32_t n = 0; n < kLatNT; ++n) __builtin_nontemporal_store(o[n][r], pr + 32 * n + hl);
+            for (uint32_t n = 0; n < kLatNT; ++n) {
+                float x;
+                asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(x) : "a"(o[n][r]));
+                a = fmaxf(a, fabsf(x));
+            }
+#pragma unroll
+            for (uint32_t d = 1; d < 32; d <<= 1) a = fmaxf(a, __shfl_xor(a, d));
+            if (head >= nh) continue;
+            const uint64_t rec = (q * p.query_heads + h0 + head) * p.splits + split;
+            if (hl == 0) __builtin_nontemporal_store(a, attn_rec_mla(p, rec) + 2);
+            const float inv = a > 0.0f ? 1.0f / a : 0.0f;
+            uint16_t *py = attn_rec_y(p, rec) + hl;
+#pragma unroll
+            for (uint32_t n = 0; n < kLatNT; ++n) {
+                float x;
+                asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(x) : "a"(o[n][r]));
+                __builtin_nontemporal_store(__builtin_bit_cast(uint16_t, static_cast<_Float16>(x * inv)),
+                                            py + 32 * n);
+            }
         }
     }
 }
@@ -1858,5 +1888,65 @@ extern "C" __global__ __launch_bounds__(128) void sglkv_paged_attention_combine(
 #pragma unroll
         for (uint32_t e = 0; e < 4; ++e)
             if (d + e < p.dv) out[d + e] = attn_to_bf16(o4[e] * linv);
+    }
+}
+
+// The latent body's records (scaled fp16, SGLKV_ATTN_HPAD): the merge
+// above with o_s = a_s y_s, the weight of split s being 2^(m_s - m*) a_s.
+// Thread t handles dims 8t .. 8t+7 (+512 ...), one 16-byte read per
+// split's y row (rows of whole 128-byte lines; dims past dv read the row's
+// padding and are not written).
+extern "C" __global__ __launch_bounds__(64) void sglkv_paged_attention_combine_h(sglkv_attn_params p) {
+    const uint64_t q = blockIdx.x / p.query_heads;
+    const uint32_t head = static_cast<uint32_t>(blockIdx.x % p.query_heads);
+    uint64_t start = 0, len = 0;
+    if (!attn_metadata(p, q, false, &start, &len)) return;
+    const uint32_t used = static_cast<uint32_t>((len + p.chunk_tokens - 1) / p.chunk_tokens);
+    const uint64_t i0 = (q * p.query_heads + head) * p.splits;
+    const float4 *mla = reinterpret_cast<const float4 *>(attn_rec_mla(p, i0));
+    const uint16_t *y = attn_rec_y(p, i0);
+    const uint32_t hpad = SGLKV_ATTN_HPAD(p.dv);
+    uint16_t *out = p.output + (q * p.query_heads + head) * p.dv;
+    for (uint32_t d = 8 * threadIdx.x; d < p.dv; d += 512) {
+        float m = -3.402823466e+38f, l = 0.0f;
+        float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+        for (uint32_t s0 = 0; s0 < used; s0 += 8) {
+            float4 r[8];
+            sglkv_u16x8 v[8];
+#pragma unroll
+            for (uint32_t j = 0; j < 8; ++j) {
+                const uint32_t s = s0 + j < used ? s0 + j : used - 1;
+                r[j] = mla[s];
+                v[j] = *reinterpret_cast<const sglkv_u16x8 *>(y + s * hpad + d);
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < 8; ++j) {
+                const bool ok = s0 + j < used;
+                const float m_new = ok ? fmaxf(m, r[j].x) : m;
+                const float a = exp2f(m - m_new);
+                const float w = ok ? exp2f(r[j].x - m_new) : 0.0f;
+                l = l * a + w * r[j].y;
+                const float wy = w * r[j].z;
+#pragma unroll
+                for (uint32_t e = 0; e < 8; ++e) {
+                    // (the element copied out first: hipcc bit-casts a
+                    // vector element operand as element 0)
+                    const uint16_t bits = v[j][e];
+                    acc[e] = acc[e] * a + wy * static_cast<float>(__builtin_bit_cast(_Float16, bits));
+                }
+                m = m_new;
+            }
+        }
+        const float linv = 1.0f / l;
+        sglkv_u16x8 o8;
+#pragma unroll
+        for (uint32_t e = 0; e < 8; ++e) o8[e] = attn_to_bf16(acc[e] * linv);
+        if (d + 8 <= p.dv && (reinterpret_cast<uintptr_t>(out + d) & 15u) == 0) {
+            *reinterpret_cast<sglkv_u16x8 *>(out + d) = o8;
+        } else {
+#pragma unroll
+            for (uint32_t e = 0; e < 8; ++e)
+                if (d + e < p.dv) out[d + e] = o8[e];
+        }
     }
 }

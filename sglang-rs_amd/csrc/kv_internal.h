@@ -132,6 +132,7 @@ struct sgl_rocm_kv_ctx {
     // staged (dims 128, rows in LDS) / staged (dims 64)
     hipFunction_t attention[9];
     hipFunction_t attention_combine;
+    hipFunction_t attention_combine_h;    // the latent body's scaled fp16 records
     uint32_t attention_occupancy[9];      // resident workgroups per CU of attention[i] ...
     uint32_t attention_occupancy_lds[9];  // ... at this LDS size (0 = not yet queried)
     int max_lds_per_block;                // device limit on a workgroup's LDS bytes

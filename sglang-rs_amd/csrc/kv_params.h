@@ -212,6 +212,12 @@ typedef struct sglkv_request_params {
  * (rows padded to whole 128-byte lines, so that the writes fill every line
  * they touch) and its m, l at partial + records * SGLKV_ATTN_OPAD(dv) + 2 i. */
 #define SGLKV_ATTN_OPAD(dv) (((dv) + 31u) & ~31u)
+/* The latent body's split records are scaled fp16: record i keeps
+ * y[dv] = o / a at partial + i * SGLKV_ATTN_HPAD(dv) halves (rows of whole
+ * 128-byte lines), a = max |o| over the record (so |y| <= 1), and
+ * (m, l, a, 0) as four floats at partial + records * SGLKV_ATTN_HPAD(dv)
+ * halves + 16 i bytes. sglkv_paged_attention_combine_h merges them. */
+#define SGLKV_ATTN_HPAD(dv) (((dv) + 63u) & ~63u)
 /* The wide bodies (many query heads per KV head, e.g. MLA): a workgroup of
  * SGLKV_ATTN_WIDE_WAVES waves serves SGLKV_ATTN_WIDE_GROUPS groups of
  * SGLKV_ATTN_HEADS heads, two waves per group; K dims padded to 32*DKC, V

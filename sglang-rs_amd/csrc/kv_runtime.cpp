@@ -505,6 +505,8 @@ extern "C" int32_t sgl_rocm_kv_init(int32_t device, const char *code_object_path
         err = hipDeviceGetAttribute(&ctx->max_lds_per_block, hipDeviceAttributeMaxSharedMemoryPerBlock, device);
     if (err == hipSuccess)
         err = hipModuleGetFunction(&ctx->attention_combine, ctx->module, "sglkv_paged_attention_combine");
+    if (err == hipSuccess)
+        err = hipModuleGetFunction(&ctx->attention_combine_h, ctx->module, "sglkv_paged_attention_combine_h");
     if (err == hipSuccess) err = hipDeviceGetAttribute(&ctx->cu_count, hipDeviceAttributeMultiprocessorCount, device);
     // The tile constants the kernels were compiled with.
     const char *const constants[3] = {"sglkv_rows_per_thread", "sglkv_max_tile_rows",

@@ -100,12 +100,13 @@ def test_noalloc_matches_the_allocating_entry_point_twice(k, shape):
 
 
 def test_noalloc_refuses_records_beyond_the_workspace(k):
-    """256 MLA decode queries over one 8,192-token request need 512 split
-    records per head (134.7 MB, past the 128 MiB workspace): the
+    """512 MLA decode queries over one 8,192-token request take two splits
+    each (the latent body's 4,096-token slot table): 131,072 scaled-fp16
+    split records of 1,040 bytes, 136.3 MB, past the 128 MiB workspace. The
     no-allocation entry point refuses with DimensionTooLarge naming the
     workspace and writes nothing, while the allocating one runs."""
     rng = np.random.default_rng(77)
-    case = _Decode(rng, 64, 1, 576, 512, 128, [8192] * 256, share=True)
+    case = _Decode(rng, 64, 1, 576, 512, 128, [8192] * 512, share=True)
     out = hip.DeviceBuffer(case.plan.output_required_bytes)
     out.fill(0xAB)
     with pytest.raises(kv.KvError) as ei:

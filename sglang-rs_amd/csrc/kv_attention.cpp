@@ -457,10 +457,14 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
     void *args[] = {&p};
     SGLKV_CHECK_HIP(hipModuleLaunchKernel(ctx->attention[which], (unsigned)base, (unsigned)splits, 1, threads,
                                           1, 1, lds, s, args, nullptr));
-    if (splits > 1)
-        SGLKV_CHECK_HIP(hipModuleLaunchKernel(half_records ? ctx->attention_combine_h : ctx->attention_combine,
-                                              (unsigned)(c.query_count * c.query_head_count), 1, 1,
-                                              half_records ? 64 : 128, 1, 1, 0, s, args, nullptr));
+    if (splits > 1 && half_records)  // 64 workgroups per 8 groups of 8 heads (the XCD map)
+        SGLKV_CHECK_HIP(hipModuleLaunchKernel(ctx->attention_combine_h,
+                                              (unsigned)(64 * ceil_div(c.query_count * ceil_div(c.query_head_count, 8), 8)),
+                                              1, 1, 64, 1, 1, 0, s, args, nullptr));
+    else if (splits > 1)
+        SGLKV_CHECK_HIP(hipModuleLaunchKernel(ctx->attention_combine,
+                                              (unsigned)(c.query_count * c.query_head_count), 1, 1, 128, 1, 1,
+                                              0, s, args, nullptr));
     return SGL_KV_OK;
 }
 

@@ -257,10 +257,13 @@ __device__ __forceinline__ float *attn_rec_ml(const sglkv_attn_params &p, uint64
 __device__ __forceinline__ uint16_t *attn_rec_y(const sglkv_attn_params &p, uint64_t i) {
     return reinterpret_cast<uint16_t *>(p.partial) + i * SGLKV_ATTN_HPAD(p.dv);
 }
-__device__ __forceinline__ float *attn_rec_mla(const sglkv_attn_params &p, uint64_t i) {
+// (m, l, a, 0) of (query q, split, head): ordered by (q, split, head), so
+// the heads of one workgroup's split are adjacent and go out in one store.
+__device__ __forceinline__ float *attn_rec_mla(const sglkv_attn_params &p, uint64_t q, uint32_t split,
+                                               uint64_t head) {
     return reinterpret_cast<float *>(reinterpret_cast<uint16_t *>(p.partial) +
                                      p.query_count * p.query_heads * p.splits * SGLKV_ATTN_HPAD(p.dv)) +
-           4 * i;
+           4 * ((q * p.splits + split) * p.query_heads + head);
 }
 
 // Output (one split) or the split record (m, l, o[0..dv)).
@@ -1516,11 +1519,11 @@ __device__ __forceinline__ void attn_latent_body(const sglkv_attn_params &p) {
         // Scaled fp16 record: a = max |o| over the head's 512 dims (the
         // lane's 16 values, then the 32 lanes of its half-wave), y = o / a.
         // y's rounding moves o by at most 2^-11 |o| + 2^-25 a.
-        if (hh == 0 && hl < nh) {
-            float *pr = attn_rec_mla(p, (q * p.query_heads + h0 + hl) * p.splits + split);
-            __builtin_nontemporal_store(m_run, pr);
-            __builtin_nontemporal_store(l_tot, pr + 1);
-        }
+        // a of each of the wave's heads meets its m and l in lane head (of
+        // the first half-wave) through 128 bytes of LDS per wave (the K
+        // stage, unused after the loop), and each head's (m, l, a, 0) goes
+        // out as one 16-byte store.
+        float *const a_lds = reinterpret_cast<float *>(k0) + 32 * w;
         asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3");
 #pragma unroll
         for (uint32_t r = 0; r < 16; ++r) {
@@ -1534,9 +1537,9 @@ __device__ __forceinline__ void attn_latent_body(const sglkv_attn_params &p) {
             }
 #pragma unroll
             for (uint32_t d = 1; d < 32; d <<= 1) a = fmaxf(a, __shfl_xor(a, d));
+            if (hl == 0) a_lds[head] = a;
             if (head >= nh) continue;
             const uint64_t rec = (q * p.query_heads + h0 + head) * p.splits + split;
-            if (hl == 0) __builtin_nontemporal_store(a, attn_rec_mla(p, rec) + 2);
             const float inv = a > 0.0f ? 1.0f / a : 0.0f;
             uint16_t *py = attn_rec_y(p, rec) + hl;
 #pragma unroll
@@ -1546,6 +1549,10 @@ __device__ __forceinline__ void attn_latent_body(const sglkv_attn_params &p) {
                 __builtin_nontemporal_store(__builtin_bit_cast(uint16_t, static_cast<_Float16>(x * inv)),
                                             py + 32 * n);
             }
+        }
+        if (hh == 0 && hl < nh) {
+            const sglkv_f32x4 mla = {m_run, l_tot, a_lds[hl], 0.0f};
+            __builtin_nontemporal_store(mla, reinterpret_cast<sglkv_f32x4 *>(attn_rec_mla(p, q, split, h0 + hl)));
         }
     }
 }
@@ -1893,21 +1900,33 @@ extern "C" __global__ __launch_bounds__(128) void sglkv_paged_attention_combine(
 
 // The latent body's records (scaled fp16, SGLKV_ATTN_HPAD): the merge
 // above with o_s = a_s y_s, the weight of split s being 2^(m_s - m*) a_s.
-// Thread t handles dims 8t .. 8t+7 (+512 ...), one 16-byte read per
+// A workgroup is one wave and one (query, head). Workgroups are handed to
+// the eight XCDs in turn (workgroup b to XCD b % 8), and g, the group of
+// eight adjacent heads 8k .. 8k+7 of a query (g = query * ceil(heads / 8)
+// + k), takes workgroups 64 (g / 8) + 8 m + g % 8 for m < 8: one XCD, so
+// the eight (m, l, a) of a split, which share a line, are fetched into one
+// L2 once. Lane t handles dims 8t .. 8t+7 (+512 ...), one 16-byte read per
 // split's y row (rows of whole 128-byte lines; dims past dv read the row's
 // padding and are not written).
 extern "C" __global__ __launch_bounds__(64) void sglkv_paged_attention_combine_h(sglkv_attn_params p) {
-    const uint64_t q = blockIdx.x / p.query_heads;
-    const uint32_t head = static_cast<uint32_t>(blockIdx.x % p.query_heads);
+    const uint32_t groups = (p.query_heads + 7) / 8;
+    const uint64_t t = blockIdx.x / 8;
+    const uint64_t g = 8 * (t / 8) + blockIdx.x % 8;
+    if (g >= p.query_count * groups) return;
+    const uint64_t q = g / groups;
+    const uint32_t head = 8 * static_cast<uint32_t>(g % groups) + static_cast<uint32_t>(t % 8);
+    if (head >= p.query_heads) return;
+    const uint32_t lane = threadIdx.x;
     uint64_t start = 0, len = 0;
     if (!attn_metadata(p, q, false, &start, &len)) return;
     const uint32_t used = static_cast<uint32_t>((len + p.chunk_tokens - 1) / p.chunk_tokens);
     const uint64_t i0 = (q * p.query_heads + head) * p.splits;
-    const float4 *mla = reinterpret_cast<const float4 *>(attn_rec_mla(p, i0));
+    const float4 *mla = reinterpret_cast<const float4 *>(attn_rec_mla(p, q, 0, head));
+    const uint64_t mla_split = p.query_heads;  // float4s from one split's (m, l, a) to the next's
     const uint16_t *y = attn_rec_y(p, i0);
     const uint32_t hpad = SGLKV_ATTN_HPAD(p.dv);
     uint16_t *out = p.output + (q * p.query_heads + head) * p.dv;
-    for (uint32_t d = 8 * threadIdx.x; d < p.dv; d += 512) {
+    for (uint32_t d = 8 * lane; d < p.dv; d += 512) {
         float m = -3.402823466e+38f, l = 0.0f;
         float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
         for (uint32_t s0 = 0; s0 < used; s0 += 8) {
@@ -1916,7 +1935,7 @@ extern "C" __global__ __launch_bounds__(64) void sglkv_paged_attention_combine_h
 #pragma unroll
             for (uint32_t j = 0; j < 8; ++j) {
                 const uint32_t s = s0 + j < used ? s0 + j : used - 1;
-                r[j] = mla[s];
+                r[j] = mla[s * mla_split];
                 v[j] = *reinterpret_cast<const sglkv_u16x8 *>(y + s * hpad + d);
             }
 #pragma unroll

@@ -216,7 +216,8 @@ typedef struct sglkv_request_params {
  * y[dv] = o / a at partial + i * SGLKV_ATTN_HPAD(dv) halves (rows of whole
  * 128-byte lines), a = max |o| over the record (so |y| <= 1), and
  * (m, l, a, 0) as four floats at partial + records * SGLKV_ATTN_HPAD(dv)
- * halves + 16 i bytes. sglkv_paged_attention_combine_h merges them. */
+ * halves + 16 j bytes, j = (query * splits + split) * query_heads + head
+ * (a split's heads adjacent). sglkv_paged_attention_combine_h merges them. */
 #define SGLKV_ATTN_HPAD(dv) (((dv) + 63u) & ~63u)
 /* The wide bodies (many query heads per KV head, e.g. MLA): a workgroup of
  * SGLKV_ATTN_WIDE_WAVES waves serves SGLKV_ATTN_WIDE_GROUPS groups of

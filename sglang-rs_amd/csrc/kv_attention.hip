@@ -1392,15 +1392,6 @@ __device__ __forceinline__ void attn_latent_body(const sglkv_attn_params &p) {
     const bool active = nh > 0;
     const uint64_t h0 = static_cast<uint64_t>(kvh) * p.group + hw;
 
-    // Queries: lane l holds head l%32, dims 16c + 8(l/32) .. +7 of step c.
-    sglkv_u16x8 qf[kLatKSteps];
-#pragma unroll
-    for (uint32_t c = 0; c < kLatKSteps; ++c) {
-        const uint32_t d = 16 * c + 8 * (lane >> 5);
-        qf[c] = sglkv_u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-        if ((lane & 31) < nh && d < p.dk)
-            qf[c] = *reinterpret_cast<const sglkv_u16x8 *>(p.queries + (q * p.query_heads + h0 + (lane & 31)) * p.dk + d);
-    }
     if (tid == 0) *redo = 0;
     for (uint32_t i = tid; i < nb * kLatB; i += kLatThreads) {
         const uint64_t tok = t0 + i;
@@ -1422,8 +1413,18 @@ __device__ __forceinline__ void attn_latent_body(const sglkv_attn_params &p) {
     attn_lat_issue_k(p, kbase, blk(0), true, w, lane, k0);
     attn_lat_issue_v(p, vbase, blk(0), true, w, lane, v0);
     attn_lat_issue_k(p, kbase, blk(1), 1 < nb, w, lane, k1);
-    // Every load so far (the queries, which the compiler tracks, and the
-    // first rows, which it does not) is complete before the loop, whose
+    // Queries, loaded while the first rows land: lane l holds head l%32,
+    // dims 16c + 8(l/32) .. +7 of step c.
+    sglkv_u16x8 qf[kLatKSteps];
+#pragma unroll
+    for (uint32_t c = 0; c < kLatKSteps; ++c) {
+        const uint32_t d = 16 * c + 8 * (lane >> 5);
+        qf[c] = sglkv_u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        if ((lane & 31) < nh && d < p.dk)
+            qf[c] = *reinterpret_cast<const sglkv_u16x8 *>(p.queries + (q * p.query_heads + h0 + (lane & 31)) * p.dk + d);
+    }
+    // Every load so far (the first rows, which the compiler does not track,
+    // and the queries, which it does) is complete before the loop, whose
     // waits then count the row loads alone (s_waitcnt vmcnt(0), lgkmcnt and
     // expcnt left at their maxima).
     __builtin_amdgcn_s_waitcnt(0x0F70);

@@ -904,8 +904,9 @@ def run_attention(args, config: str):
     log(f"attention avg {avg * 1e3:.1f} us per layer ({achieved:.0f} GB/s, "
         f"{launch_flops / avg / 1e9:.1f} TFLOP/s), wall {gbs:.0f} GB/s")
     k.close()
-    kernel = ("sglkv_paged_attention_latent" if mla else "sglkv_paged_attention_staged64" if D == 64
-              else "sglkv_paged_attention_staged128") + "+sglkv_paged_attention_combine"
+    kernel = ("sglkv_paged_attention_latent+sglkv_paged_attention_combine_h" if mla
+              else ("sglkv_paged_attention_staged64" if D == 64 else "sglkv_paged_attention_staged128")
+              + "+sglkv_paged_attention_combine")
     summary = "paged_attention_decode_" + ("mla" if mla else "hnd" if hnd else "dims64" if D == 64 else "nhd")
     extra = {"requests": nreq, "tokens_per_request": n, "layers": L, "kv_heads": H,
              "query_heads": qh, "key_dim": dk, "value_dim": dv, "page_size": P,

@@ -82,6 +82,12 @@ DESCRIPTIONS = {
                 "layer, kv_cache.rs:201-224, models/deepseek.rs:1035-1037), byte-realigning "
                 "kernels; 32 requests x 8192, page_size-64 -> page_size-64 with independent "
                 "random page tables",
+    "hnd64": "head chunks under 128 bytes: Llama-3.2-1B's KV shape (16 layers x 8 KV heads x 64) "
+             "in fp8, 512-byte rows of eight 64-byte head chunks, 64 requests x 2048 tokens; src "
+             "page_size-1 NHD pool of 262144 slots, dst page_size-64 HND pool with a random page "
+             "table (head-major pages written in 64-byte pieces)",
+    "nhd64": "as hnd64 with a page_size-64 NHD destination (whole 512-byte rows), the comparison "
+             "for hnd64",
     "c2pages": "C2 shape as the reference transfers it today: page-for-page copies between "
                "page_size-64 pools of equal layout (131072 tokens = 2048 pages of 8 MiB, random "
                "source and destination pages), built with sgl_kv_build_page_requests and run "
@@ -431,7 +437,8 @@ def run_coresident(t, config, args):
         f"kernel-sum {kernel_gbs:.0f} GB/s, wall {gbs:.0f} GB/s")
     del src, dst, xfer
     k.close()
-    payload_dtype = "fp8_e4m3" if fp8 else "packed_mla_bytes" if config == "c4packed" else "bf16"
+    payload_dtype = ("packed_mla_bytes" if config == "c4packed" else "fp8_e4m3" if sh.elt_bytes == 1
+                     else "bf16")
     extra = {"tokens": n, "layers": L, "kv_heads": sh.heads, "head_dim": sh.head_dim,
              "row_bytes": rb, "payload_dtype": payload_dtype,
              "payload_bytes": t.payload_bytes, "algorithmic_bytes_per_step": step_bytes,
@@ -1058,6 +1065,7 @@ def main():
     makers = {"c1": wl.c1, "c2": wl.c2, "c3": wl.c3, "c4": wl.c4,
               "c4fp8": lambda: wl.c4(fp8=True), "c4pair": wl.c4pair, "c4packed": wl.c4packed,
               "c5": wl.c5, "c2pages": wl.c2, "attn": wl.c2,
+              "hnd64": wl.chunks64, "nhd64": lambda: wl.chunks64(head_major=False),
               "attn_hnd": wl.c2, "attn_mla": wl.c4, "attn64": wl.c2, "ceilings": wl.c2, "c2direct": wl.c2}
     attention = args.config in ("attn", "attn_hnd", "attn_mla", "attn64")
     t = makers[args.config]()

@@ -176,7 +176,22 @@ __device__ __forceinline__ void sglkv_copy_rows(const sglkv_copy_params &p) {
     sglkv_copy_scales(p.scale_src, p.scale_dst, p.scale_count);
     const uint32_t layer = blockIdx.y;
 
-    for (uint32_t j = threadIdx.x; j < p.vpr; j += blockDim.x) {
+    // Thread (tx, ty): vector tx of rows ty + k * blockDim.y. Head-major
+    // pages with head chunks of under a cache line (line_rows = 128 / chunk
+    // bytes > 1) hold line_rows consecutive positions of a head chunk in one
+    // line. There the lanes are regrouped so that each run of line_rows *
+    // chunk-vectors lanes moves one chunk of line_rows consecutive rows:
+    // the line is then written (or read) whole by one wave, not in pieces
+    // by the waves of separate rows.
+    uint32_t tx = threadIdx.x, ty = threadIdx.y;
+    if (p.line_rows > 1) {
+        const uint32_t g = p.line_rows, cv = p.vpc[0], span = g * blockDim.x;
+        const uint32_t tid = threadIdx.y * blockDim.x + threadIdx.x, j = tid % span;
+        tx = (j / (g * cv)) * cv + j % cv;
+        ty = (tid / span) * g + (j / cv) % g;
+    }
+
+    for (uint32_t j = tx; j < p.vpr; j += blockDim.x) {
         // Select rather than index the kernel-argument arrays: a dynamic
         // index would copy the struct to scratch.
         const uint32_t t = j >= p.vpt;
@@ -205,13 +220,13 @@ __device__ __forceinline__ void sglkv_copy_rows(const sglkv_copy_params &p) {
         if (clean) {
 #pragma unroll
             for (uint32_t k = 0; k < RU; ++k) {
-                const uint32_t i = threadIdx.y + k * blockDim.y;
+                const uint32_t i = ty + k * blockDim.y;
                 const uint64_t so = SK == SGLKV_SIDE_POOL ? so_t[i] : (row0 + i) * src_stride;
                 buf[k] = sglkv_load<V, NT>(reinterpret_cast<gload_t *>(sb + so));
             }
 #pragma unroll
             for (uint32_t k = 0; k < RU; ++k) {
-                const uint32_t i = threadIdx.y + k * blockDim.y;
+                const uint32_t i = ty + k * blockDim.y;
                 const uint64_t dof = DK == SGLKV_SIDE_POOL ? do_t[i] : (row0 + i) * dst_stride;
                 sglkv_store<V, NT>(reinterpret_cast<gstore_t *>(db + dof), buf[k]);
             }
@@ -222,7 +237,7 @@ __device__ __forceinline__ void sglkv_copy_rows(const sglkv_copy_params &p) {
         // the clean path above.
 #pragma unroll 1
         for (uint32_t k = 0; k < RU; ++k) {
-            const uint32_t i = threadIdx.y + k * blockDim.y;
+            const uint32_t i = ty + k * blockDim.y;
             const uint64_t r = row0 + i;
             if (r >= p.rows) break;
             const uint64_t so = SK == SGLKV_SIDE_POOL ? so_t[i] : r * src_stride;

@@ -91,7 +91,10 @@ typedef struct sglkv_copy_params {
     uint32_t vpt;           /* vectors of tensor 0's row */
     uint32_t vpc[2];        /* vectors per head chunk of tensor t */
     uint32_t tile_rows;     /* rows per workgroup = blockDim.y * rows per thread */
-    uint32_t reserved;
+    uint32_t line_rows;     /* > 1: head-major pages with head chunks of 128 / line_rows
+                               bytes; lanes regrouped so that line_rows consecutive rows
+                               of one chunk (one cache line of a page) share a wave
+                               (blockDim.x == vpr, blockDim.y % line_rows == 0) */
 } sglkv_copy_params;
 
 /* Byte-realigning copy: for rows whose chunks are not whole 16-byte vectors

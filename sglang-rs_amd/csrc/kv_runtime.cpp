@@ -297,6 +297,15 @@ int32_t finish_launch(const sgl_rocm_kv_ctx *ctx, Launch *l) {
     if (by > ctx->max_tile_rows / ctx->rows_per_thread) by = ctx->max_tile_rows / ctx->rows_per_thread;
     l->block_y = by;
     p.tile_rows = by * ctx->rows_per_thread;
+    // A pool side with head-major pages whose head chunks are whole 16-byte
+    // vectors under a cache line (e.g. 64 bytes: fp8 x 64 dims, bf16 x 32):
+    // regroup the lanes so that a line's consecutive positions share a wave.
+    const uint64_t cb = shape.chunk(0);
+    auto head_major = [&](const sglkv_side &s) { return s.slots && s.head_stride[0] != cb; };
+    p.line_rows = 0;
+    if (vb == 16 && (head_major(p.src) || head_major(p.dst)) && cb < 128 && 128 % cb == 0 &&
+        shape.chunk(shape.tensors - 1) == cb && l->block_x == p.vpr && l->block_y % (128 / cb) == 0)
+        p.line_rows = (uint32_t)(128 / cb);
     l->grid = (l->rows + p.tile_rows - 1) / p.tile_rows;
     if (l->grid > INT32_MAX) return too_large("grid blocks", l->grid, INT32_MAX);
     return SGL_KV_OK;

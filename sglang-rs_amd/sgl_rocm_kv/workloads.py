@@ -222,6 +222,24 @@ def c4packed(seed: int = 4) -> Transfer:
                     spans, np.zeros(32, np.int64))
 
 
+def chunks64(seed: int = 6, head_major: bool = True) -> Transfer:
+    """Head chunks of 64 bytes: Llama-3.2-1B's KV shape (16 layers x 8 KV
+    heads x 64 dims) stored in fp8 (one byte per element), so a 512-byte row
+    is eight 64-byte head chunks. 64 requests x 2,048 tokens from a
+    page_size-1 NHD pool into a page_size-64 pool with a random page table,
+    head-major (HND: each head's chunks of a page contiguous, half a cache
+    line per token) or token-major (NHD)."""
+    rng = np.random.default_rng(seed)
+    shape = Shape(16, 8, 64, 1, 2)
+    lengths = np.full(64, 2048)
+    src = PoolSpec(1, 262144)
+    dst = PoolSpec(64, 4096, HND if head_major else NHD)
+    table, spans, dslots = _page_table_slots(rng, lengths, np.zeros(64, int), 64, dst.page_count)
+    return Transfer("llama-3.2-1b fp8, 64-byte head chunks, " + ("HND" if head_major else "NHD"),
+                    shape, src, dst, lengths, _token_slots(rng, int(lengths.sum()), src.page_count),
+                    dslots, table, spans, np.zeros(64, np.int64))
+
+
 def c5(seed: int = 5, requests: int = 512) -> Transfer:
     """Ragged radix-prefix transfer: log-uniform lengths, a page-aligned
     prefix of each request already cached on the decode side."""

@@ -168,6 +168,13 @@ def test_c4_full_size_every_layer(k, kind):
     _full_size(k, t, kind.upper())
 
 
+@pytest.mark.parametrize("kind", ["hnd64", "nhd64"])
+def test_64_byte_head_chunks_full_size(k, kind):
+    """The hnd64 / nhd64 bench configurations at 131,072 rows x 16 layers:
+    fp8 rows of eight 64-byte head chunks into page_size-64 HND or NHD pages."""
+    _full_size(k, wl.chunks64(head_major=kind == "hnd64"), kind.upper())
+
+
 def test_c5_waves_through_the_staged_pipeline(k):
     """C5: the ragged radix-prefix transfer in the request waves the bench
     runs (workloads.waves over a 262,144-slot source pool and a 4,096-page

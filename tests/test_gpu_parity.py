@@ -239,6 +239,17 @@ def test_hnd_with_eight_heads_both_directions(k):
         _run_pack_unpack(k, t, (0, 31), seed=src_p)
 
 
+@pytest.mark.parametrize("head_major", [True, False])
+def test_64_byte_head_chunks(k, head_major):
+    """Head chunks of 64 bytes (the hnd64 / nhd64 bench configurations:
+    Llama-3.2-1B's 8 KV heads x 64 dims in fp8): P=1 NHD -> P=64 HND, where
+    head-major pages are written half a cache line per token, and the same
+    into NHD, against the oracle on 3,000 rows of the first and last layers."""
+    t = wl.scaled(wl.chunks64(head_major=head_major), 3000, seed=8)
+    _say(f"64-byte head chunks, head-major {head_major}: {t.rows} rows")
+    _run_pack_unpack(k, t, (0, t.shape.layers - 1), seed=64)
+
+
 def test_transfer_layer_matches_oracle(k):
     """Pool -> pool in one pass, for co-resident pools (P=1 NHD -> P=64 HND,
     and MLA P=64 -> P=64)."""

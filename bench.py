@@ -982,6 +982,31 @@ def run_ceilings(args):
         ms = e0.elapsed_ms(e1) / 3
         out[name] = (n / (ms / 1e3) / 1e9, ms)
         log(f"{name}: {ms:.1f} ms per GiB, {out[name][0]:.1f} GB/s")
+    # Both directions at once (what the C5 pipeline asks of the link): a
+    # device-to-host and a host-to-device copy of 1 GiB on two streams,
+    # three of each; each direction's rate over its own span, from events
+    # on its stream.
+    host2 = hip.PinnedBuffer(n)
+    s2 = hip.Stream()
+    hip.memcpy_async(host.ptr, a.ptr, n, "d2h", s)
+    hip.memcpy_async(b.ptr, host2.ptr, n, "h2d", s2)
+    s.synchronize()
+    s2.synchronize()
+    d0, d1, h0, h1 = hip.Event(), hip.Event(), hip.Event(), hip.Event()
+    d0.record(s)
+    h0.record(s2)
+    for _ in range(3):
+        hip.memcpy_async(host.ptr, a.ptr, n, "d2h", s)
+        hip.memcpy_async(b.ptr, host2.ptr, n, "h2d", s2)
+    d1.record(s)
+    h1.record(s2)
+    d1.synchronize()
+    h1.synchronize()
+    for name, ev0, ev1 in (("link_both_d2h", d0, d1), ("link_both_h2d", h0, h1)):
+        ms = ev0.elapsed_ms(ev1) / 3
+        out[name] = (n / (ms / 1e3) / 1e9, ms)
+        log(f"{name} (both directions at once): {ms:.1f} ms per GiB, {out[name][0]:.1f} GB/s")
+    host2.free()
     host.free()
     # The same copy over 16 GiB: HBM reaches a lower rate once the footprint
     # is far larger than the last-level cache, which is the regime of
@@ -1016,6 +1041,10 @@ def run_ceilings(args):
         "copy_16gib_gbs": round(out["copy_16gib"][0], 1),
         "link_d2h_gbs": round(out["link_d2h"][0], 1),
         "link_h2d_gbs": round(out["link_h2d"][0], 1),
+        "link_both_d2h_gbs": round(out["link_both_d2h"][0], 1),
+        "link_both_h2d_gbs": round(out["link_both_h2d"][0], 1),
+        "copy_engines": "blit kernels (HSA_ENABLE_SDMA=0)" if os.environ.get("HSA_ENABLE_SDMA") == "0"
+                        else "SDMA engines (runtime default)",
         "roofline": {"bound": "hbm", "kernel": "sglkv_stream_copy", "achieved": round(gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": None, "algorithmic_bytes_per_launch": 2 * n},

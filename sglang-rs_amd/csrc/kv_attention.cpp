@@ -400,8 +400,8 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
     uint64_t base = c.query_count;
     if (mul_ovf(base, p.kv_heads, &base) || (wide && mul_ovf(base, hblocks, &base)) ||
         (!wide && (mul_ovf(base, p.head_groups, &base) || mul_ovf(base, p.dv_blocks, &base))) ||
-        base > INT32_MAX)
-        return too_large_dim("workgroups", base, INT32_MAX);
+        base > UINT32_MAX / threads)  // a dispatch counts its work-items in 32 bits
+        return too_large_dim("workgroups", base, UINT32_MAX / threads);
     if (ctx->attention_occupancy_lds[which] != lds) {
         int per_cu = 0;
         SGLKV_CHECK_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ctx->attention[which],
@@ -453,18 +453,25 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
         }
         p.partial = static_cast<float *>(workspace ? workspace : ctx->attention_partial);
     }
+    // The combine pass: one workgroup per (query, head); the fp16 one in
+    // blocks of 64 per 8 groups of 8 heads (its XCD map), padded.
+    uint64_t combine_grid = 0;
+    if (splits > 1) {
+        uint64_t heads;
+        if (mul_ovf(c.query_count, c.query_head_count, &heads)) return attn_overflow();
+        combine_grid = half_records ? 64 * ceil_div(c.query_count * ceil_div(c.query_head_count, 8), 8) : heads;
+        const uint64_t limit = UINT32_MAX / (half_records ? 64 : 128);  // work-items in 32 bits
+        if (heads > limit / 2 || combine_grid > limit)
+            return too_large_dim("combine workgroups", heads, limit / 2);
+    }
     if (clear_flag) SGLKV_CHECK_HIP(hipMemsetAsync(ctx->attn_flag, 0, sizeof(uint32_t), s));
     void *args[] = {&p};
     SGLKV_CHECK_HIP(hipModuleLaunchKernel(ctx->attention[which], (unsigned)base, (unsigned)splits, 1, threads,
                                           1, 1, lds, s, args, nullptr));
-    if (splits > 1 && half_records)  // 64 workgroups per 8 groups of 8 heads (the XCD map)
-        SGLKV_CHECK_HIP(hipModuleLaunchKernel(ctx->attention_combine_h,
-                                              (unsigned)(64 * ceil_div(c.query_count * ceil_div(c.query_head_count, 8), 8)),
-                                              1, 1, 64, 1, 1, 0, s, args, nullptr));
-    else if (splits > 1)
-        SGLKV_CHECK_HIP(hipModuleLaunchKernel(ctx->attention_combine,
-                                              (unsigned)(c.query_count * c.query_head_count), 1, 1, 128, 1, 1,
-                                              0, s, args, nullptr));
+    if (splits > 1)
+        SGLKV_CHECK_HIP(hipModuleLaunchKernel(half_records ? ctx->attention_combine_h : ctx->attention_combine,
+                                              (unsigned)combine_grid, 1, 1, half_records ? 64 : 128, 1, 1, 0, s,
+                                              args, nullptr));
     return SGL_KV_OK;
 }
 

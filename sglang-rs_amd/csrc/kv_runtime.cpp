@@ -285,7 +285,9 @@ int32_t finish_launch(const sgl_rocm_kv_ctx *ctx, Launch *l) {
     // narrow to the common alignment (down to single bytes for the odd
     // 649-byte packed-MLA rows).
     if (vb < 16 && plan_realign(ctx, l)) {
-        if (l->grid > INT32_MAX) return too_large("grid blocks", l->grid, INT32_MAX);
+        // A dispatch counts its work-items in 32 bits.
+        const uint64_t max_grid = UINT32_MAX / ((uint64_t)l->block_x * l->block_y);
+        if (l->grid > max_grid) return too_large("grid blocks", l->grid, max_grid);
         return SGL_KV_OK;
     }
     p.vpr = (uint32_t)row_vectors;
@@ -307,7 +309,8 @@ int32_t finish_launch(const sgl_rocm_kv_ctx *ctx, Launch *l) {
         shape.chunk(shape.tensors - 1) == cb && l->block_x == p.vpr && l->block_y % (128 / cb) == 0)
         p.line_rows = (uint32_t)(128 / cb);
     l->grid = (l->rows + p.tile_rows - 1) / p.tile_rows;
-    if (l->grid > INT32_MAX) return too_large("grid blocks", l->grid, INT32_MAX);
+    const uint64_t max_grid = UINT32_MAX / ((uint64_t)l->block_x * l->block_y);  // 32-bit work-item count
+    if (l->grid > max_grid) return too_large("grid blocks", l->grid, max_grid);
     return SGL_KV_OK;
 }
 

@@ -250,6 +250,46 @@ def test_64_byte_head_chunks(k, head_major):
     _run_pack_unpack(k, t, (0, t.shape.layers - 1), seed=64)
 
 
+@pytest.mark.parametrize("heads,head_dim,elt", [(8, 8, 2), (4, 32, 1), (8, 32, 2), (2, 16, 4)])
+def test_head_chunks_under_a_line_every_direction(k, heads, head_dim, elt):
+    """Head chunks of 16, 32 and 64 bytes, where the kernels regroup their
+    lanes so that a head-major line's consecutive positions share a wave:
+    P16 HND -> P64 NHD and P1 NHD -> P64 HND through pack and unpack, and
+    P64 HND -> P32 HND pool -> pool, against the oracle."""
+    sh = wl.Shape(3, heads, head_dim, elt, 2)
+    base = wl.scaled(wl.c2(), 1500, seed=9)
+    base.shape = sh
+    _say(f"head chunks of {head_dim * elt} B: {heads} heads, {base.rows} rows")
+    for src_layout, src_p, dst_layout, dst_p in ((kv.HND, 16, kv.NHD, 64), (kv.NHD, 1, kv.HND, 64)):
+        t = wl.scaled(base, 1500, seed=10)
+        t.shape = sh
+        pages = t.rows // src_p + 40
+        t.src = wl.PoolSpec(src_p, pages, src_layout)
+        t.src_slots = np.random.default_rng(11).permutation(pages * src_p)[:t.rows].astype(np.uint64)
+        t.dst = wl.PoolSpec(dst_p, t.dst.page_count, dst_layout)
+        _run_pack_unpack(k, t, (0, 2), seed=src_p + head_dim)
+    t = wl.scaled(base, 1500, seed=12)
+    t.shape = sh
+    t.src = wl.PoolSpec(64, -(-t.rows // 64) + 8, kv.HND)
+    _, _, t.src_slots = wl._page_table_slots(np.random.default_rng(13), t.lengths, np.zeros(len(t.lengths), int),
+                                             64, t.src.page_count)
+    dst_pages = -(-t.rows // 32) + 8
+    t.dst = wl.PoolSpec(32, dst_pages, kv.HND)
+    _, _, t.dst_slots = wl._page_table_slots(np.random.default_rng(14), t.lengths, np.zeros(len(t.lengths), int),
+                                             32, dst_pages)
+    rng = np.random.default_rng(15)
+    src_h = rng.integers(0, 256, t.src.byte_len(sh), dtype=np.uint8)
+    dst_h = rng.integers(0, 256, t.dst.byte_len(sh), dtype=np.uint8)
+    src, dst = hip.DeviceBuffer.from_array(src_h), hip.DeviceBuffer.from_array(dst_h)
+    ss, ds = hip.DeviceBuffer.from_array(t.src_slots), hip.DeviceBuffer.from_array(t.dst_slots)
+    for layer in range(sh.layers):
+        k.transfer_layer(_kpool(src, t.src, sh, layer), _db(ss), t.rows, _kpool(dst, t.dst, sh, layer), _db(ds))
+        oracle.transfer(_opool(t.src, sh, layer), src_h, t.src_slots, _opool(t.dst, sh, layer), dst_h,
+                        t.dst_slots, threads=4)
+    k.check_errors()
+    np.testing.assert_array_equal(dst.download(), dst_h)
+
+
 def test_transfer_layer_matches_oracle(k):
     """Pool -> pool in one pass, for co-resident pools (P=1 NHD -> P=64 HND,
     and MLA P=64 -> P=64)."""

@@ -1485,9 +1485,9 @@ __device__ __forceinline__ void attn_latent_body(const sglkv_attn_params &p) {
     if (!active) return;
     if (m_run == -INFINITY) m_run = -3.402823466e+38f;  // no valid token: the record's m as the other bodies leave it
 
-    // Output (one split) or the split record [m, l, o[0..dv)]: o[n][r] is
-    // head 8(r/4) + 4(l/32) + r%4, dim 32n + l%32; m and l of head l%32.
-    // dv is 512 (the host takes this body only then).
+    // Output (one split) or the split's scaled fp16 record: o[n][r] is head
+    // 8(r/4) + 4(l/32) + r%4, dim 32n + l%32; m and l of head l%32. dv is
+    // 512 (the host takes this body only then).
     const float l_tot = l_part + __shfl_xor(l_part, 32);
     // The lane index as a fresh value: derived from the prologue's, it (and
     // the head-row index computed from it there) would be kept live across
@@ -1520,10 +1520,10 @@ __device__ __forceinline__ void attn_latent_body(const sglkv_attn_params &p) {
         // Scaled fp16 record: a = max |o| over the head's 512 dims (the
         // lane's 16 values, then the 32 lanes of its half-wave), y = o / a.
         // y's rounding moves o by at most 2^-11 |o| + 2^-25 a.
-        // a of each of the wave's heads meets its m and l in lane head (of
-        // the first half-wave) through 128 bytes of LDS per wave (the K
-        // stage, unused after the loop), and each head's (m, l, a, 0) goes
-        // out as one 16-byte store.
+        // Head h's a reaches lane h of the first half-wave, which holds h's
+        // m and l, through 128 bytes of LDS per wave (the K stage, unused
+        // after the loop); each head's (m, l, a, 0) goes out as one 16-byte
+        // store.
         float *const a_lds = reinterpret_cast<float *>(k0) + 32 * w;
         asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3");
 #pragma unroll

@@ -460,7 +460,7 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
         uint64_t heads;
         if (mul_ovf(c.query_count, c.query_head_count, &heads)) return attn_overflow();
         combine_grid = half_records ? 64 * ceil_div(c.query_count * ceil_div(c.query_head_count, 8), 8) : heads;
-        const uint64_t limit = UINT32_MAX / (half_records ? 64 : 128);  // work-items in 32 bits
+        const uint64_t limit = UINT32_MAX / (half_records ? 256 : 128);  // work-items in 32 bits
         if (heads > limit / 2 || combine_grid > limit)
             return too_large_dim("combine workgroups", heads, limit / 2);
     }
@@ -468,10 +468,12 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
     void *args[] = {&p};
     SGLKV_CHECK_HIP(hipModuleLaunchKernel(ctx->attention[which], (unsigned)base, (unsigned)splits, 1, threads,
                                           1, 1, lds, s, args, nullptr));
+    // The fp16 combine: one wave per group of eight splits, up to four.
+    const unsigned combine_threads = half_records ? 64 * (unsigned)(splits > 24 ? 4 : ceil_div(splits, 8)) : 128;
     if (splits > 1)
         SGLKV_CHECK_HIP(hipModuleLaunchKernel(half_records ? ctx->attention_combine_h : ctx->attention_combine,
-                                              (unsigned)combine_grid, 1, 1, half_records ? 64 : 128, 1, 1, 0, s,
-                                              args, nullptr));
+                                              (unsigned)combine_grid, 1, 1, combine_threads, 1, 1, 0, s, args,
+                                              nullptr));
     return SGL_KV_OK;
 }
 

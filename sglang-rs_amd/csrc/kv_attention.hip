@@ -1901,23 +1901,28 @@ extern "C" __global__ __launch_bounds__(128) void sglkv_paged_attention_combine(
 
 // The latent body's records (scaled fp16, SGLKV_ATTN_HPAD): the merge
 // above with o_s = a_s y_s, the weight of split s being 2^(m_s - m*) a_s.
-// A workgroup is one wave and one (query, head). Workgroups are handed to
-// the eight XCDs in turn (workgroup b to XCD b % 8), and g, the group of
-// eight adjacent heads 8k .. 8k+7 of a query (g = query * ceil(heads / 8)
-// + k), takes workgroups 64 (g / 8) + 8 m + g % 8 for m < 8: one XCD, so
-// the eight (m, l, a) of a split, which share a line, are fetched into one
-// L2 once. Lane t handles dims 8t .. 8t+7 (+512 ...), one 16-byte read per
+// A workgroup is one (query, head), of blockDim.x / 64 waves (the host
+// gives 1 to 4, one per group of eight splits up to four groups): wave w
+// merges groups w, w + W, ... of the splits, then wave 0 merges the waves'
+// partial (m, l, o) through LDS, so a query with many splits waits for one
+// memory latency per W groups, not per group. Workgroups are handed to the
+// eight XCDs in turn (workgroup b to XCD b % 8), and g, the group of eight
+// adjacent heads 8k .. 8k+7 of a query (g = query * ceil(heads / 8) + k),
+// takes workgroups 64 (g / 8) + 8 m + g % 8 for m < 8: one XCD, so the
+// eight (m, l, a) of a split, which share a line, are fetched into one L2
+// once. Lane t handles dims 8t .. 8t+7 (+512 ...), one 16-byte read per
 // split's y row (rows of whole 128-byte lines; dims past dv read the row's
 // padding and are not written).
-extern "C" __global__ __launch_bounds__(64) void sglkv_paged_attention_combine_h(sglkv_attn_params p) {
+extern "C" __global__ __launch_bounds__(256) void sglkv_paged_attention_combine_h(sglkv_attn_params p) {
+    __shared__ float part[3][64][10];  // waves 1..3: m, l, o[8] per lane
     const uint32_t groups = (p.query_heads + 7) / 8;
     const uint64_t t = blockIdx.x / 8;
     const uint64_t g = 8 * (t / 8) + blockIdx.x % 8;
-    if (g >= p.query_count * groups) return;
+    if (g >= p.query_count * groups) return;  // uniform over the workgroup
     const uint64_t q = g / groups;
     const uint32_t head = 8 * static_cast<uint32_t>(g % groups) + static_cast<uint32_t>(t % 8);
     if (head >= p.query_heads) return;
-    const uint32_t lane = threadIdx.x;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
     uint64_t start = 0, len = 0;
     if (!attn_metadata(p, q, false, &start, &len)) return;
     const uint32_t used = static_cast<uint32_t>((len + p.chunk_tokens - 1) / p.chunk_tokens);
@@ -1927,10 +1932,10 @@ extern "C" __global__ __launch_bounds__(64) void sglkv_paged_attention_combine_h
     const uint16_t *y = attn_rec_y(p, i0);
     const uint32_t hpad = SGLKV_ATTN_HPAD(p.dv);
     uint16_t *out = p.output + (q * p.query_heads + head) * p.dv;
-    for (uint32_t d = 8 * lane; d < p.dv; d += 512) {
+    for (uint32_t d = 8 * lane; d < p.dv; d += 512) {  // the same trip count in every wave
         float m = -3.402823466e+38f, l = 0.0f;
         float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-        for (uint32_t s0 = 0; s0 < used; s0 += 8) {
+        for (uint32_t s0 = 8 * wave; s0 < used; s0 += 8 * waves) {
             float4 r[8];
             sglkv_u16x8 v[8];
 #pragma unroll
@@ -1957,6 +1962,31 @@ extern "C" __global__ __launch_bounds__(64) void sglkv_paged_attention_combine_h
                 m = m_new;
             }
         }
+        if (waves > 1) {
+            // A wave with no group keeps m = -FLT_MAX, l = 0, o = 0, which
+            // the merge weighs 0.
+            if (wave > 0) {
+                float *pw = part[wave - 1][lane];
+                pw[0] = m;
+                pw[1] = l;
+#pragma unroll
+                for (uint32_t e = 0; e < 8; ++e) pw[2 + e] = acc[e];
+            }
+            __syncthreads();
+            if (wave == 0) {
+                for (uint32_t w = 1; w < waves; ++w) {
+                    const float *pw = part[w - 1][lane];
+                    const float m_new = fmaxf(m, pw[0]);
+                    const float a = exp2f(m - m_new), b = exp2f(pw[0] - m_new);
+                    l = l * a + pw[1] * b;
+#pragma unroll
+                    for (uint32_t e = 0; e < 8; ++e) acc[e] = acc[e] * a + pw[2 + e] * b;
+                    m = m_new;
+                }
+            }
+            __syncthreads();
+        }
+        if (wave != 0) continue;
         const float linv = 1.0f / l;
         sglkv_u16x8 o8;
 #pragma unroll

@@ -413,7 +413,13 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
         (uint64_t)ctx->attention_occupancy[which] * (uint64_t)(ctx->cu_count > 0 ? ctx->cu_count : 256);
     const uint64_t want = base >= target ? 1 : target / base;
     uint64_t chunk = ceil_div(max_len, want);
-    chunk = ceil_div(chunk < 256 ? 256 : chunk, SGLKV_ATTN_TOKENS) * SGLKV_ATTN_TOKENS;
+    // At least 256 tokens a split; the latent body's smallest batches (one
+    // to three workgroups before splitting) go to 64 or 128, putting more
+    // CUs to work, since its combine merges up to 32 splits per memory
+    // round (measured, MLA over 8,192 tokens: 1 query 40.0 -> 33.2 us at
+    // 64, 2 queries 41.0 -> 35.2 us at 128; from 4 queries on 256 is best).
+    const uint64_t min_chunk = which == 6 && base < 4 ? (base <= 1 ? 64 : 128) : 256;
+    chunk = ceil_div(chunk < min_chunk ? min_chunk : chunk, SGLKV_ATTN_TOKENS) * SGLKV_ATTN_TOKENS;
     uint64_t splits = ceil_div(max_len, chunk);
     const uint64_t table = wide ? SGLKV_ATTN_WIDE_SLOTS : which >= 7 ? SGLKV_ATTN_STAGED_SLOTS : 0;
     if (table && chunk > table) {  // the slot table of the wide, latent and staged bodies

@@ -321,6 +321,22 @@ def test_mla_many_heads(k, qh, hnd):
     _check(got, want, c)
 
 
+@pytest.mark.parametrize("nq", [1, 2, 3])
+def test_latent_small_batches(k, nq):
+    """One to three MLA decode queries: the latent body's chunks shrink to
+    64 (one query) or 128 tokens, so a 3,000-token sequence takes up to 47
+    splits, which the combine merges four groups of eight at a time."""
+    rng = np.random.default_rng(nq + 90)
+    c = _Case(rng, P=64, L=2, H=1, dk=576, dv=512, qh=128, pages=160, layer=1)
+    lens = np.array([3000, 1777, 2500][:nq])
+    rso = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint64)
+    slots = rng.choice(c.layout.slot_count, size=int(rso[-1]), replace=False).astype(np.uint64)
+    q = _bf16_normal(rng, nq * 128 * 576).reshape(nq, 128, 576)
+    _say(f"latent small batch: {nq} queries, lengths {list(lens)}")
+    got, want = c.run(k, q, np.arange(nq), lens, rso, slots, 1.0 / math.sqrt(576), max_len=int(lens.max()))
+    _check(got, want, c)
+
+
 @pytest.mark.parametrize("H,qh,dk,hnd", [
     (2, 256, 576, False),   # two KV heads, a full 128-head block each
     (1, 160, 576, True),    # two head blocks, the second holding 32 heads

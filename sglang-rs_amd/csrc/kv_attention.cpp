@@ -413,12 +413,20 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
         (uint64_t)ctx->attention_occupancy[which] * (uint64_t)(ctx->cu_count > 0 ? ctx->cu_count : 256);
     const uint64_t want = base >= target ? 1 : target / base;
     uint64_t chunk = ceil_div(max_len, want);
-    // At least 256 tokens a split; the latent body's smallest batches (one
-    // to three workgroups before splitting) go to 64 or 128, putting more
-    // CUs to work, since its combine merges up to 32 splits per memory
-    // round (measured, MLA over 8,192 tokens: 1 query 40.0 -> 33.2 us at
-    // 64, 2 queries 41.0 -> 35.2 us at 128; from 4 queries on 256 is best).
-    const uint64_t min_chunk = which == 6 && base < 4 ? (base <= 1 ? 64 : 128) : 256;
+    // The shortest chunk a split takes. Small batches split further when
+    // the combine merges many splits per memory round (both combines spread
+    // a query's split groups over several waves or thread sets), which puts
+    // more CUs to work. Measured:
+    //  - staged bodies (GQA dims 128 / 64, 32 heads over 8 KV heads, 4,096
+    //    tokens): 1 query 23.3 -> 15.5 us / 16.7 -> 11.8 us at 64 tokens
+    //    against 256, 2 queries 24.6 -> 17.8 / 17.5 -> 12.2, 4 queries 26.4
+    //    -> 23.3 / 18.8 -> 15.9; from 16 queries on the split count is set
+    //    by the occupancy target, not by this minimum;
+    //  - latent body (MLA over 8,192 tokens): 64 tokens for one workgroup
+    //    before splitting, 128 for two or three (1 query 40.0 -> 33.2 us,
+    //    2 queries 41.0 -> 35.2 us), 256 from four on (best there);
+    //  - the other bodies keep 256 (not measured otherwise).
+    const uint64_t min_chunk = which >= 7 ? 64 : which == 6 && base < 4 ? (base <= 1 ? 64 : 128) : 256;
     chunk = ceil_div(chunk < min_chunk ? min_chunk : chunk, SGLKV_ATTN_TOKENS) * SGLKV_ATTN_TOKENS;
     uint64_t splits = ceil_div(max_len, chunk);
     const uint64_t table = wide ? SGLKV_ATTN_WIDE_SLOTS : which >= 7 ? SGLKV_ATTN_STAGED_SLOTS : 0;

@@ -1846,57 +1846,104 @@ extern "C" __global__ __launch_bounds__(64) void sglkv_paged_attention_pipe(sglk
     attn_pipe_body<false>(p);
 }
 
+// Merges splits s_begin, s_begin + s_step*8 (groups of eight) of one
+// (query, head)'s records into (m, l, acc) for dims d .. d+3, with a
+// running maximum: each group's (m, l) pairs and o pieces load at once.
+// Lanes of a group past the used splits reload the last used split and
+// weigh it 0.
+__device__ __forceinline__ void attn_combine_groups(const float2 *ml, const float *o, uint32_t opad, uint32_t d,
+                                                    uint32_t used, uint32_t s_begin, uint32_t s_step, float &m,
+                                                    float &l, float (&acc)[4]) {
+    for (uint32_t s0 = s_begin; s0 < used; s0 += s_step) {
+        float2 r[8];
+        float4 v[8];
+#pragma unroll
+        for (uint32_t j = 0; j < 8; ++j) {
+            const uint32_t s = s0 + j < used ? s0 + j : used - 1;
+            r[j] = ml[s];
+            v[j] = *reinterpret_cast<const float4 *>(o + s * opad + d);
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < 8; ++j) {
+            const bool ok = s0 + j < used;
+            const float m_new = ok ? fmaxf(m, r[j].x) : m;
+            const float a = exp2f(m - m_new);
+            const float w = ok ? exp2f(r[j].x - m_new) : 0.0f;
+            l = l * a + w * r[j].y;
+            acc[0] = acc[0] * a + w * v[j].x;
+            acc[1] = acc[1] * a + w * v[j].y;
+            acc[2] = acc[2] * a + w * v[j].z;
+            acc[3] = acc[3] * a + w * v[j].w;
+            m = m_new;
+        }
+    }
+}
+
 // Merges the split records of one (query, head): m* = max m_s,
-// out = sum_s 2^(m_s - m*) o_s / sum_s 2^(m_s - m*) l_s, with a running
-// maximum so that each group of eight splits' (m, l) pairs and o pieces is
-// loaded at once (one memory latency per group, not one for the maxima and
-// one for the rows). Thread t handles dims 4t .. 4t+3 (+512 ...), one
-// 16-byte read per split's o row (rows are 128-byte aligned; dims past dv
-// read the row's padding and are not written). Lanes of a group past the
-// used splits reload the last used split and weigh it 0.
+// out = sum_s 2^(m_s - m*) o_s / sum_s 2^(m_s - m*) l_s. Thread t handles
+// dims 4t .. 4t+3 of each split's o row (one 16-byte read; rows are
+// 128-byte aligned, dims past dv read the row's padding and are not
+// written). A row of dv < 512 dims needs only ceil(dv / 4) threads: the
+// workgroup's threads then form `sets` of that many, set i merging split
+// groups i, i + sets, ..., and set 0 merges the sets' partial (m, l, o)
+// through LDS, so a query split many ways waits for one memory latency per
+// `sets` groups of eight splits, not per group.
 extern "C" __global__ __launch_bounds__(128) void sglkv_paged_attention_combine(sglkv_attn_params p) {
+    __shared__ float part[128][6];  // m, l, o[4] of each thread of sets 1..
     const uint64_t q = blockIdx.x / p.query_heads;
     const uint32_t head = static_cast<uint32_t>(blockIdx.x % p.query_heads);
     uint64_t start = 0, len = 0;
-    if (!attn_metadata(p, q, false, &start, &len)) return;
+    if (!attn_metadata(p, q, false, &start, &len)) return;  // uniform over the workgroup
     const uint32_t used = static_cast<uint32_t>((len + p.chunk_tokens - 1) / p.chunk_tokens);
     const uint64_t i0 = (q * p.query_heads + head) * p.splits;
     const float2 *ml = reinterpret_cast<const float2 *>(attn_rec_ml(p, i0));
     const float *o = attn_rec_o(p, i0);
     const uint32_t opad = SGLKV_ATTN_OPAD(p.dv);
     uint16_t *out = p.output + (q * p.query_heads + head) * p.dv;
-    for (uint32_t d = 4 * threadIdx.x; d < p.dv; d += 512) {
-        float m = -3.402823466e+38f, l = 0.0f;
-        float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (uint32_t s0 = 0; s0 < used; s0 += 8) {
-            float2 r[8];
-            float4 v[8];
-#pragma unroll
-            for (uint32_t j = 0; j < 8; ++j) {
-                const uint32_t s = s0 + j < used ? s0 + j : used - 1;
-                r[j] = ml[s];
-                v[j] = *reinterpret_cast<const float4 *>(o + s * opad + d);
-            }
-#pragma unroll
-            for (uint32_t j = 0; j < 8; ++j) {
-                const bool ok = s0 + j < used;
-                const float m_new = ok ? fmaxf(m, r[j].x) : m;
-                const float a = exp2f(m - m_new);
-                const float w = ok ? exp2f(r[j].x - m_new) : 0.0f;
-                l = l * a + w * r[j].y;
-                acc.x = acc.x * a + w * v[j].x;
-                acc.y = acc.y * a + w * v[j].y;
-                acc.z = acc.z * a + w * v[j].z;
-                acc.w = acc.w * a + w * v[j].w;
-                m = m_new;
-            }
-        }
+    const uint32_t pieces = (p.dv + 3) / 4;
+    const uint32_t lanes = pieces < blockDim.x ? pieces : blockDim.x;
+    const uint32_t sets = blockDim.x / lanes, set = threadIdx.x / lanes, tl = threadIdx.x % lanes;
+    auto write = [&](uint32_t d, float m, float l, const float (&acc)[4]) {
+        (void)m;
         const float linv = 1.0f / l;
-        const float o4[4] = {acc.x, acc.y, acc.z, acc.w};
 #pragma unroll
         for (uint32_t e = 0; e < 4; ++e)
-            if (d + e < p.dv) out[d + e] = attn_to_bf16(o4[e] * linv);
+            if (d + e < p.dv) out[d + e] = attn_to_bf16(acc[e] * linv);
+    };
+    if (sets == 1 || used <= 8) {  // (uniform over the workgroup: one query's splits)
+        for (uint32_t d = 4 * threadIdx.x; d < p.dv; d += 4 * blockDim.x) {
+            float m = -3.402823466e+38f, l = 0.0f, acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            attn_combine_groups(ml, o, opad, d, used, 0, 8, m, l, acc);
+            write(d, m, l, acc);
+        }
+        return;
     }
+    // One 4-dim piece per thread (4 * lanes >= dv); threads past the last
+    // whole set (blockDim.x % lanes of them) only join the barrier. A set
+    // with no group keeps m = -FLT_MAX, l = 0, o = 0, which the merge
+    // weighs 0.
+    const uint32_t d = 4 * tl;
+    float m = -3.402823466e+38f, l = 0.0f, acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (set < sets) attn_combine_groups(ml, o, opad, d, used, 8 * set, 8 * sets, m, l, acc);
+    if (set > 0 && set < sets) {
+        float *pw = part[threadIdx.x];
+        pw[0] = m;
+        pw[1] = l;
+#pragma unroll
+        for (uint32_t e = 0; e < 4; ++e) pw[2 + e] = acc[e];
+    }
+    __syncthreads();
+    if (set != 0) return;
+    for (uint32_t k = 1; k < sets; ++k) {
+        const float *pw = part[k * lanes + tl];
+        const float m_new = fmaxf(m, pw[0]);
+        const float a = exp2f(m - m_new), b = exp2f(pw[0] - m_new);
+        l = l * a + pw[1] * b;
+#pragma unroll
+        for (uint32_t e = 0; e < 4; ++e) acc[e] = acc[e] * a + pw[2 + e] * b;
+        m = m_new;
+    }
+    write(d, m, l, acc);
 }
 
 // The latent body's records (scaled fp16, SGLKV_ATTN_HPAD): the merge
@@ -1905,7 +1952,8 @@ extern "C" __global__ __launch_bounds__(128) void sglkv_paged_attention_combine(
 // gives 1 to 4, one per group of eight splits up to four groups): wave w
 // merges groups w, w + W, ... of the splits, then wave 0 merges the waves'
 // partial (m, l, o) through LDS, so a query with many splits waits for one
-// memory latency per W groups, not per group. Workgroups are handed to the
+// memory latency per W groups, not per group (a query whose splits fit one
+// group takes wave 0 alone). Workgroups are handed to the
 // eight XCDs in turn (workgroup b to XCD b % 8), and g, the group of eight
 // adjacent heads 8k .. 8k+7 of a query (g = query * ceil(heads / 8) + k),
 // takes workgroups 64 (g / 8) + 8 m + g % 8 for m < 8: one XCD, so the
@@ -1926,6 +1974,10 @@ extern "C" __global__ __launch_bounds__(256) void sglkv_paged_attention_combine_
     uint64_t start = 0, len = 0;
     if (!attn_metadata(p, q, false, &start, &len)) return;
     const uint32_t used = static_cast<uint32_t>((len + p.chunk_tokens - 1) / p.chunk_tokens);
+    // One group of splits (a short sequence): wave 0 alone, no merge (the
+    // condition is the same for every wave of the workgroup).
+    if (used <= 8 && wave != 0) return;
+    const uint32_t nw = used <= 8 ? 1 : waves;
     const uint64_t i0 = (q * p.query_heads + head) * p.splits;
     const float4 *mla = reinterpret_cast<const float4 *>(attn_rec_mla(p, q, 0, head));
     const uint64_t mla_split = p.query_heads;  // float4s from one split's (m, l, a) to the next's
@@ -1935,7 +1987,7 @@ extern "C" __global__ __launch_bounds__(256) void sglkv_paged_attention_combine_
     for (uint32_t d = 8 * lane; d < p.dv; d += 512) {  // the same trip count in every wave
         float m = -3.402823466e+38f, l = 0.0f;
         float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-        for (uint32_t s0 = 8 * wave; s0 < used; s0 += 8 * waves) {
+        for (uint32_t s0 = 8 * wave; s0 < used; s0 += 8 * nw) {
             float4 r[8];
             sglkv_u16x8 v[8];
 #pragma unroll
@@ -1962,7 +2014,7 @@ extern "C" __global__ __launch_bounds__(256) void sglkv_paged_attention_combine_
                 m = m_new;
             }
         }
-        if (waves > 1) {
+        if (nw > 1) {
             // A wave with no group keeps m = -FLT_MAX, l = 0, o = 0, which
             // the merge weighs 0.
             if (wave > 0) {
@@ -1974,7 +2026,7 @@ extern "C" __global__ __launch_bounds__(256) void sglkv_paged_attention_combine_
             }
             __syncthreads();
             if (wave == 0) {
-                for (uint32_t w = 1; w < waves; ++w) {
+                for (uint32_t w = 1; w < nw; ++w) {
                     const float *pw = part[w - 1][lane];
                     const float m_new = fmaxf(m, pw[0]);
                     const float a = exp2f(m - m_new), b = exp2f(pw[0] - m_new);

@@ -321,6 +321,23 @@ def test_mla_many_heads(k, qh, hnd):
     _check(got, want, c)
 
 
+@pytest.mark.parametrize("D,nq", [(128, 1), (128, 2), (64, 1), (64, 3)])
+def test_staged_small_batches(k, D, nq):
+    """One to three GQA decode queries (32 heads over 8 KV heads): the
+    staged bodies split each 3,000-token sequence into 64-token chunks (up
+    to 47 splits), which the combine merges several groups of eight at a
+    time in parallel thread sets."""
+    rng = np.random.default_rng(D + nq)
+    c = _Case(rng, P=16, L=2, H=8, dk=D, dv=D, qh=32, pages=600, layer=1)
+    lens = np.array([3000, 1777, 2500][:nq])
+    rso = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint64)
+    slots = rng.choice(c.layout.slot_count, size=int(rso[-1]), replace=False).astype(np.uint64)
+    q = _bf16_normal(rng, nq * 32 * D).reshape(nq, 32, D)
+    _say(f"staged small batch: dims {D}, {nq} queries, lengths {list(lens)}")
+    got, want = c.run(k, q, np.arange(nq), lens, rso, slots, 1.0 / math.sqrt(D), max_len=int(lens.max()))
+    _check(got, want, c)
+
+
 @pytest.mark.parametrize("nq", [1, 2, 3])
 def test_latent_small_batches(k, nq):
     """One to three MLA decode queries: the latent body's chunks shrink to

@@ -747,9 +747,21 @@ typedef struct sgl_kv_attention_plan_config {  /* CudaBf16PagedAttentionPlanConf
     uint64_t query_key_head_dim;
     uint64_t value_head_dim;
     float scale;
-    uint32_t reserved;
+    uint32_t flags;            /* 0 or SGL_KV_ATTN_EXACT_WEIGHTS */
     sgl_kv_attention_layout layout;
 } sgl_kv_attention_plan_config;
+
+/* Plan flag with no counterpart in the reference (its config has no such
+ * field). The latent body (the MLA shape: 576-wide keys whose first 512
+ * dims are the values, one KV head) by default feeds the softmax weights to
+ * its P.V matrix products rounded to bf16, a relative error of at most 2^-8
+ * per weight; with this flag it feeds each weight as a hi + lo pair of bf16
+ * values (one more matrix product per tile), which brings that error to
+ * about 2^-16, as every other body does by default. It lengthens the
+ * latent launch by 4 % (one query of 8,192 tokens, 128 heads) to 20 %
+ * (64 such queries) on MI355X. Other bodies ignore it. Unknown bits are
+ * rejected by sgl_kv_attention_plan_new and at enqueue. */
+#define SGL_KV_ATTN_EXACT_WEIGHTS 1u
 
 typedef struct sgl_kv_attention_plan {  /* CudaBf16PagedAttentionPlan (:239-261) */
     sgl_kv_attention_plan_config config;

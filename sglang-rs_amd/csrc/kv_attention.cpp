@@ -115,6 +115,9 @@ extern "C" int32_t sgl_kv_attention_plan_new(const sgl_kv_attention_plan_config 
     if (lay.head_layout > SGL_KV_HND)
         return fail(SGL_KV_INVALID_ARGUMENT, "head_layout", lay.head_layout, 0, 0,
                     "unknown head layout %u", lay.head_layout);
+    if (c->flags & ~SGL_KV_ATTN_EXACT_WEIGHTS)
+        return fail(SGL_KV_INVALID_ARGUMENT, "flags", c->flags, SGL_KV_ATTN_EXACT_WEIGHTS, 0,
+                    "unknown attention plan flags 0x%x", c->flags);
 
     sgl_kv_attention_plan p;
     memset(&p, 0, sizeof p);
@@ -261,6 +264,10 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
     int32_t rc;
     for (const auto &a : all)
         if ((rc = check_device(ctx, a.name, *a.buf))) return rc;
+    // A plan is a plain struct the caller may have edited since plan_new.
+    if (c.flags & ~SGL_KV_ATTN_EXACT_WEIGHTS)
+        return fail(SGL_KV_INVALID_ARGUMENT, "flags", c.flags, SGL_KV_ATTN_EXACT_WEIGHTS, 0,
+                    "unknown attention plan flags 0x%x", c.flags);
     uint64_t qp, rip, slp, rop, ssp, poolp, outp;
     if ((rc = attn_ptr("queries", b->queries, b->queries_offset, plan->query_required_bytes, &qp)) ||
         (rc = attn_ptr("query_request_indices", b->query_request_indices, b->query_request_indices_offset,
@@ -402,15 +409,17 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
         (!wide && (mul_ovf(base, p.head_groups, &base) || mul_ovf(base, p.dv_blocks, &base))) ||
         base > UINT32_MAX / threads)  // a dispatch counts its work-items in 32 bits
         return too_large_dim("workgroups", base, UINT32_MAX / threads);
-    if (ctx->attention_occupancy_lds[which] != lds) {
+    // The latent body with hi + lo weights is a function of its own.
+    const int fn = which == 6 && (c.flags & SGL_KV_ATTN_EXACT_WEIGHTS) ? 9 : which;
+    if (ctx->attention_occupancy_lds[fn] != lds) {
         int per_cu = 0;
-        SGLKV_CHECK_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ctx->attention[which],
+        SGLKV_CHECK_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ctx->attention[fn],
                                                                            (int)threads, lds));
-        ctx->attention_occupancy[which] = per_cu > 0 ? (uint32_t)per_cu : 1;
-        ctx->attention_occupancy_lds[which] = lds;
+        ctx->attention_occupancy[fn] = per_cu > 0 ? (uint32_t)per_cu : 1;
+        ctx->attention_occupancy_lds[fn] = lds;
     }
     const uint64_t target =
-        (uint64_t)ctx->attention_occupancy[which] * (uint64_t)(ctx->cu_count > 0 ? ctx->cu_count : 256);
+        (uint64_t)ctx->attention_occupancy[fn] * (uint64_t)(ctx->cu_count > 0 ? ctx->cu_count : 256);
     const uint64_t want = base >= target ? 1 : target / base;
     uint64_t chunk = ceil_div(max_len, want);
     // The shortest chunk a split takes. Small batches split further when
@@ -480,7 +489,7 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
     }
     if (clear_flag) SGLKV_CHECK_HIP(hipMemsetAsync(ctx->attn_flag, 0, sizeof(uint32_t), s));
     void *args[] = {&p};
-    SGLKV_CHECK_HIP(hipModuleLaunchKernel(ctx->attention[which], (unsigned)base, (unsigned)splits, 1, threads,
+    SGLKV_CHECK_HIP(hipModuleLaunchKernel(ctx->attention[fn], (unsigned)base, (unsigned)splits, 1, threads,
                                           1, 1, lds, s, args, nullptr));
     // The fp16 combine: one wave per group of eight splits, up to four.
     const unsigned combine_threads = half_records ? 64 * (unsigned)(splits > 24 ? 4 : ceil_div(splits, 8)) : 128;

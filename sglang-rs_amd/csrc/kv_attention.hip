@@ -1287,9 +1287,11 @@ __device__ __forceinline__ attn_i16x4 attn_lat_vtr(const uint8_t *at) {
 }
 
 // o += P x V over the staged block (pa: the probabilities, bf16, as the A
-// operand of the two 16-token steps). MFMA j is tile j/2, step j%2; its B
+// operand of the two 16-token steps; EXACT: pa[2 + i] holds the lo halves,
+// each step taken twice, hi then lo). MFMA j is tile j/2, step j%2; its B
 // operand's two transposing reads run kLatAhead MFMAs ahead.
-__device__ __forceinline__ void attn_lat_pv(const uint8_t *vst, const sglkv_u16x8 (&pa)[2],
+template <bool EXACT>
+__device__ __forceinline__ void attn_lat_pv(const uint8_t *vst, const sglkv_u16x8 (&pa)[EXACT ? 4 : 2],
                                             sglkv_f32x16 (&o)[kLatNT], uint32_t lane) {
     const uint32_t L = lane & 15, c = (lane >> 4) & 1, h = lane >> 5;
     const uint8_t *va = vst + (4 * h + (L >> 2)) * kLatVP + 32 * c + 8 * (L & 3);
@@ -1308,6 +1310,7 @@ __device__ __forceinline__ void attn_lat_pv(const uint8_t *vst, const sglkv_u16x
         const sglkv_u16x8 b = vf[j % kLatAhead];
         if (j + kLatAhead < 2 * kLatNT) vf[j % kLatAhead] = vread(j + kLatAhead);
         o[j >> 1] = attn_mfma32(pa[j & 1], b, o[j >> 1]);
+        if (EXACT) o[j >> 1] = attn_mfma32(pa[2 + (j & 1)], b, o[j >> 1]);
     }
     __builtin_amdgcn_sched_barrier(0);
 }
@@ -1341,11 +1344,13 @@ __device__ __forceinline__ uint64_t attn_lat_valid(const uint32_t *sl, uint32_t 
 }
 
 // Softmax of one block against the fixed reference m_run (set by the first
-// valid block), l_part += the lane's p, pa = p in bf16; *over when the
-// block's maximum passes the reference by more than the bound.
+// valid block), l_part += the lane's p, pa = p in bf16 (EXACT: hi in pa[0..1],
+// lo in pa[2..3]); *over when the block's maximum passes the reference by
+// more than the bound.
+template <bool EXACT>
 __device__ __forceinline__ void attn_lat_softmax(const sglkv_attn_params &p, const sglkv_f32x16 &s, uint64_t vm,
                                                  uint32_t lane, float &m_run, float &l_part,
-                                                 sglkv_u16x8 (&pa)[2], bool &over) {
+                                                 sglkv_u16x8 (&pa)[EXACT ? 4 : 2], bool &over) {
     float x[16];
     const float mx = attn_lat_scores(p, s, vm, lane, x);
     if (m_run == -INFINITY) m_run = mx;
@@ -1358,11 +1363,15 @@ __device__ __forceinline__ void attn_lat_softmax(const sglkv_attn_params &p, con
         // token gives exactly 0).
         const float pr = __builtin_amdgcn_exp2f(fminf(x[r] - m_ref, SGLKV_ATTN_FIXED_MAX_LOG2));
         psum += pr;
-        pa[r >> 3][r & 7] = attn_to_bf16(pr);
+        if (EXACT)
+            attn_split_bf16(pr, pa[r >> 3], pa[2 + (r >> 3)], r & 7);
+        else
+            pa[r >> 3][r & 7] = attn_to_bf16(pr);
     }
     l_part += psum;
 }
 
+template <bool EXACT>
 __device__ __forceinline__ void attn_latent_body(const sglkv_attn_params &p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t attn_lat_lds[];
     uint8_t *const k0 = attn_lat_lds, *const k1 = attn_lat_lds + kLatK;
@@ -1443,9 +1452,9 @@ __device__ __forceinline__ void attn_latent_body(const sglkv_attn_params &p) {
         const sglkv_f32x16 s = attn_lat_qk(kc, qf, lane);
         attn_lat_barrier<kLatLoadsV + kLatLoadsK>();  // V(k) in LDS; q.k(k) done
         attn_lat_issue_k(p, kbase, blk(k + 2), k + 2 < nb, w, lane, kc);
-        sglkv_u16x8 pa[2];
-        attn_lat_softmax(p, s, attn_lat_valid(blk(k), lane), lane, m_run, l_part, pa, over);
-        attn_lat_pv(vc, pa, o, lane);
+        sglkv_u16x8 pa[EXACT ? 4 : 2];
+        attn_lat_softmax<EXACT>(p, s, attn_lat_valid(blk(k), lane), lane, m_run, l_part, pa, over);
+        attn_lat_pv<EXACT>(vc, pa, o, lane);
     }
     // Every row load (the zero rows issued past the chunk too) has landed:
     // __syncthreads would not wait for them (its fence orders LDS and
@@ -1475,10 +1484,10 @@ __device__ __forceinline__ void attn_latent_body(const sglkv_attn_params &p) {
             attn_lat_issue_k(p, kbase, blk(k), true, w, lane, k0);
             attn_lat_issue_v(p, vbase, blk(k), true, w, lane, v0);
             attn_lat_barrier<0>();
-            sglkv_u16x8 pa[2];
-            attn_lat_softmax(p, attn_lat_qk(k0, qf, lane), attn_lat_valid(blk(k), lane), lane, m_run, l_part, pa,
+            sglkv_u16x8 pa[EXACT ? 4 : 2];
+            attn_lat_softmax<EXACT>(p, attn_lat_qk(k0, qf, lane), attn_lat_valid(blk(k), lane), lane, m_run, l_part, pa,
                              over);
-            attn_lat_pv(v0, pa, o, lane);
+            attn_lat_pv<EXACT>(v0, pa, o, lane);
             __syncthreads();
         }
     }
@@ -1834,7 +1843,14 @@ extern "C" __global__ __launch_bounds__(256) void sglkv_paged_attention_latent(s
     // Naming an accumulator register keeps the compiler's MFMA accumulators
     // in AGPRs (the 256 of o), leaving the VGPRs to the queries and scores.
     asm volatile("" ::: "a0");
-    attn_latent_body(p);
+    attn_latent_body<false>(p);
+}
+
+// The same with each weight fed to p.v as hi + lo bf16 values, as the other
+// bodies always do (SGL_KV_ATTN_EXACT_WEIGHTS).
+extern "C" __global__ __launch_bounds__(256) void sglkv_paged_attention_latent_exact(sglkv_attn_params p) {
+    asm volatile("" ::: "a0");
+    attn_latent_body<true>(p);
 }
 
 // Head dims exactly 128 (no per-dim masks) / up to 128.

@@ -4,6 +4,7 @@ _for_layer) against the reference's own plan tests
 crates/sglang-srt/tests/cuda_attention.rs:70-168), transcribed into
 tests/golden/reference_goldens.json, plus the oracle's attention
 restatement pinned against torch's scaled_dot_product_attention."""
+import ctypes
 import math
 
 import numpy as np
@@ -62,6 +63,25 @@ def test_plan_region_errors_keep_the_reference_fields(goldens):
     with pytest.raises(kv.KvError) as ei:
         kv.PagedAttentionPlan.new(**_config(base, {"scale": float("nan")}))
     assert ei.value.variant == "InvalidScale"
+
+
+def test_plan_flags(goldens):
+    """ATTN_EXACT_WEIGHTS (no counterpart in the reference) is the one
+    plan flag: both constructors carry it, plan_new refuses other bits."""
+    g = goldens["paged_attention_plan"]
+    cfg = _config(g["base_config"], g["gqa"]["patch"])
+    assert kv.PagedAttentionPlan.new(**cfg).flags == 0
+    plan = kv.PagedAttentionPlan.new(**cfg, exact_weights=True)
+    assert plan.flags == kv.ATTN_EXACT_WEIGHTS == 1
+    f = g["from_layout"]
+    lay = kv.PagedKvCacheLayout.new(_runtime(f["runtime"]), f["page_count"])
+    assert kv.PagedAttentionPlan.for_layer(lay, 1, 5, 2, 5, 4, 0.5, exact_weights=True).flags == 1
+    for bad in (2, 0x80000000, 3):
+        plan._c.config.flags = bad
+        out = type(plan._c)()
+        with pytest.raises(kv.KvError) as ei:
+            kv._call(kv.lib().sgl_kv_attention_plan_new, ctypes.byref(plan._c.config), ctypes.byref(out))
+        assert ei.value.name == "flags" and ei.value.fields[:2] == (bad, 1)
 
 
 def _runtime(rt, dtype=None):

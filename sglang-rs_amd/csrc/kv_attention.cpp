@@ -383,9 +383,13 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
         }
     }
     // Dims 128 or 64 with one head group per KV head (the Llama/Qwen GQA
-    // decodes): the staged bodies, rows loaded straight into LDS.
+    // decodes): the staged bodies, rows loaded straight into LDS. They
+    // share one in-page offset between a token's K and V rows and form it
+    // with a 24-bit multiply.
     const bool d64 = which == 3 && p.dk == 64 && p.dv == 64;
     if ((which == 2 || d64) && qp % 16 == 0 && p.head_groups == 1 &&
+        p.key_token_stride == p.value_token_stride && p.key_token_stride < (1u << 24) &&
+        lay.page_size <= (1u << 24) &&
         max_len <= 65535ull * SGLKV_ATTN_STAGED_SLOTS &&
         SGLKV_ATTN_STAGED_LDS_BYTES(p.dk) <= (unsigned)ctx->max_lds_per_block) {
         which = d64 ? 8 : 7;

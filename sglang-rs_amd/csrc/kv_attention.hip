@@ -1144,6 +1144,39 @@ __device__ __forceinline__ void attn_lat_load(uint64_t src, const uint8_t *dst) 
         : "v"(src), "s"(attn_lat_lds_at(dst)));
 }
 
+// x of lane l ^ 16 and of lane l ^ 32 (a wave of 64): gfx950's row-swap
+// permutes (v_permlane16_swap_b32, v_permlane32_swap_b32), with no LDS
+// round trip. A swap of x with itself leaves the partner row's x in one of
+// the two results, chosen by the lane's own row.
+__device__ __forceinline__ float attn_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+}
+
+__device__ __forceinline__ float attn_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+
+// x = ok ? a : z and y = ok ? b : z per lane, as v_cndmask_b32s, which the
+// compiler cannot turn into a branch around the computation of a and b.
+__device__ __forceinline__ void attn_sel64x2(bool ok, uint64_t a, uint64_t b, uint64_t z, uint64_t &x,
+                                             uint64_t &y) {
+    const uint32_t m = ok ? 1u : 0u;
+    uint32_t xl, xh, yl, yh;
+    asm("v_cmp_ne_u32 vcc, 0, %4\n\t"
+        "v_cndmask_b32 %0, %5, %6, vcc\n\t"
+        "v_cndmask_b32 %1, %7, %8, vcc\n\t"
+        "v_cndmask_b32 %2, %5, %9, vcc\n\t"
+        "v_cndmask_b32 %3, %7, %10, vcc"
+        : "=&v"(xl), "=&v"(xh), "=&v"(yl), "=&v"(yh)
+        : "v"(m), "v"(static_cast<uint32_t>(z)), "v"(static_cast<uint32_t>(a)), "v"(static_cast<uint32_t>(z >> 32)),
+          "v"(static_cast<uint32_t>(a >> 32)), "v"(static_cast<uint32_t>(b)), "v"(static_cast<uint32_t>(b >> 32))
+        : "vcc");
+    x = (static_cast<uint64_t>(xh) << 32) | xl;
+    y = (static_cast<uint64_t>(yh) << 32) | yl;
+}
+
 // Eight rows: row i's 1 KiB from a[i] (the same in every lane; lane l's 16
 // bytes at a[i] + 16 l) into LDS at at + i * PITCH. The leading s_nop 4
 // covers a VALU (readlane) write of a[i] just before; each M0 write is one
@@ -1598,8 +1631,13 @@ __device__ __forceinline__ void attn_latent_body(const sglkv_attn_params &p) {
 //  - The slot table keeps token t of a block at entry (D/16)(t % T) + t/T
 //    (T = 512/D tokens per load), so the D/16 tokens Tj + c that lanes
 //    with c = lane / (D/8) load come in 16-byte reads.
-//  - Online softmax with per-block rescaling, as the pipelined body (o is
-//    D/4 registers).
+//  - Online softmax with lazy rescaling (o is D/4 registers): the
+//    reference maximum moves only when a block's maximum passes it by more
+//    than 8 log2 units.
+//  - Tokens past the sequence's end read the zero row and score -inf. A
+//    slot that fails its range check (which sets the error word, so the
+//    launch reports an error and its outputs carry no meaning) reads the
+//    zero row too.
 
 template <uint32_t D>
 struct attn_stg {
@@ -1648,15 +1686,14 @@ __device__ __forceinline__ void attn_lat_load8v(const uint64_t *a, uint32_t at) 
         : "scc");
 }
 
-// The 2 LOADS loads of a block (its 32 slot entries at tb; live false: past
-// the chunk, every lane reads the zero row) into a stage: K rows, then V
-// rows, 1 KiB each at consecutive LDS offsets.
+// The lane's LOADS slot entries of a block (table entries at tb), and the
+// block's 2 LOADS loads from them (live false: past the chunk, every lane
+// reads the zero row) into a stage: K rows, then V rows, 1 KiB each at
+// consecutive LDS offsets.
 template <uint32_t D>
-__device__ __forceinline__ void attn_stg_issue(const sglkv_attn_params &p, uint64_t kbase, uint64_t vbase,
-                                               const uint32_t *tb, bool live, uint32_t lane, const uint8_t *stage) {
+__device__ __forceinline__ void attn_stg_slots(const uint32_t *tb, uint32_t lane, uint32_t (&s)[attn_stg<D>::LOADS]) {
     typedef attn_stg<D> S;
-    const uint32_t c = lane / S::PIECES, pc = lane % S::PIECES;
-    uint32_t s[S::LOADS];
+    const uint32_t c = lane / S::PIECES;
 #pragma unroll
     for (uint32_t h = 0; h < S::LOADS / 4; ++h) {
         const uint4 v = *reinterpret_cast<const uint4 *>(tb + S::LOADS * c + 4 * h);
@@ -1665,18 +1702,31 @@ __device__ __forceinline__ void attn_stg_issue(const sglkv_attn_params &p, uint6
         s[4 * h + 2] = v.z;
         s[4 * h + 3] = v.w;
     }
+}
+
+template <uint32_t D>
+__device__ __forceinline__ void attn_stg_issue(const sglkv_attn_params &p, uint64_t kbase, uint64_t vbase,
+                                               const uint32_t (&s)[attn_stg<D>::LOADS], bool live, uint32_t lane,
+                                               const uint8_t *stage) {
+    typedef attn_stg<D> S;
+    const uint32_t c = lane / S::PIECES, pc = lane % S::PIECES;
     const uint64_t zero = reinterpret_cast<uint64_t>(p.zero_row) + 16 * pc;
     const uint32_t mask = (1u << p.page_shift) - 1;
+    // Each address is computed from a slot that is always in range (slot 0
+    // for dead tokens) and then selected: no branches. K and V rows share
+    // the token's offset (the host gives this body equal token strides, a
+    // page_size and token stride below 2^24 and pages of at most 4 GiB, so
+    // pos * stride fits a 24-bit multiply and 32 bits).
     uint64_t a[2 * S::LOADS];
 #pragma unroll
     for (uint32_t j = 0; j < S::LOADS; ++j) {
         const uint32_t t = S::TPL * j + c;
         const bool ok = live && s[j] != kAttnInvalidSlot;
-        const uint64_t page = static_cast<uint64_t>(s[j] >> p.page_shift) * p.page_stride32;
-        const uint32_t pos = s[j] & mask;
-        a[j] = ok ? kbase + page + static_cast<uint64_t>(pos) * p.key_token_stride32 + 16 * S::kpos(t, pc) : zero;
-        a[S::LOADS + j] =
-            ok ? vbase + page + static_cast<uint64_t>(pos) * p.value_token_stride32 + 16 * S::vpos(t, pc) : zero;
+        const uint32_t sj = ok ? s[j] : 0u;
+        const uint32_t in_page = __umul24(sj & mask, p.key_token_stride32);
+        const uint64_t off = static_cast<uint64_t>(sj >> p.page_shift) * p.page_stride32 + in_page;
+        attn_sel64x2(ok, kbase + off + 16 * S::kpos(t, pc), vbase + off + 16 * S::vpos(t, pc), zero, a[j],
+                     a[S::LOADS + j]);
     }
 #pragma unroll
     for (uint32_t h = 0; h < 2 * S::LOADS / 8; ++h) attn_lat_load8v<1024>(a + 8 * h, attn_lat_lds_at(stage + 8192 * h));
@@ -1686,52 +1736,68 @@ __device__ __forceinline__ void attn_stg_issue(const sglkv_attn_params &p, uint6
 // then o += p.v with V from the stage by transposing reads.
 template <uint32_t D>
 __device__ __forceinline__ void attn_stg_softmax_pv(const sglkv_attn_params &p, uint32_t g, uint32_t r,
-                                                    const sglkv_f32x4 (&sc)[2], uint64_t vb0, uint64_t vb1,
+                                                    const sglkv_f32x4 (&sc)[2], uint32_t nv,
                                                     const uint8_t *vst, attn_state_n<attn_stg<D>::NJ> &st) {
     typedef attn_stg<D> S;
-    float x[8];
-    float mx = -INFINITY;
-#pragma unroll
-    for (uint32_t b = 0; b < 2; ++b)
-#pragma unroll
-        for (uint32_t e = 0; e < 4; ++e) {
-            const bool ok = (((b ? vb1 : vb0) >> (4 * g + e)) & 1) != 0;
-            const float v = ok ? sc[b][e] * p.scale_log2 : -INFINITY;
-            x[4 * b + e] = v;
-            mx = fmaxf(mx, v);
-        }
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(st.m_run, mx);
-    const float alpha = exp2f(st.m_run - m_new);
-    sglkv_u16x8 phi, plo;
-    float psum = 0.0f;
-#pragma unroll
-    for (uint32_t i = 0; i < 8; ++i) {
-        const float pi = exp2f(x[i] - m_new);
-        psum += pi;
-        attn_split_bf16(pi, phi, plo, i);
-    }
-    st.l_part = st.l_part * alpha + psum;
-    st.m_run = m_new;
-    float arow[4];
-#pragma unroll
-    for (uint32_t e = 0; e < 4; ++e) arow[e] = __shfl(alpha, 4 * g + e);
-#pragma unroll
-    for (uint32_t j = 0; j < S::NJ; ++j)
-#pragma unroll
-        for (uint32_t e = 0; e < 4; ++e) st.o[j][e] *= arow[e];
-    // B operand of tile j: V[8g .. 8g+7][16j + r].
+    // The B operands of the p.v tiles (tile j: V[8g .. 8g+7][16j + r]) are
+    // read first, so their LDS latency passes under the softmax.
     const uint32_t t0 = 8 * g + (r >> 2), t1 = t0 + 4, d4 = r & 3;
+    sglkv_u16x8 vv[S::NJ];
 #pragma unroll
     for (uint32_t j = 0; j < S::NJ; ++j) {
         const uint32_t pc = 2 * j + (d4 >> 1), half = 8 * (d4 & 1);
         const attn_i16x4 lo = attn_lat_vtr(vst + S::ROW * t0 + 16 * S::vpos(t0, pc) + half);
         const attn_i16x4 hi = attn_lat_vtr(vst + S::ROW * t1 + 16 * S::vpos(t1, pc) + half);
-        const sglkv_u16x8 vv = {(uint16_t)lo[0], (uint16_t)lo[1], (uint16_t)lo[2], (uint16_t)lo[3],
-                                (uint16_t)hi[0], (uint16_t)hi[1], (uint16_t)hi[2], (uint16_t)hi[3]};
-        st.o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(phi), attn_as_bf16(vv), st.o[j], 0, 0, 0);
-        st.o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(plo), attn_as_bf16(vv), st.o[j], 0, 0, 0);
+        vv[j] = sglkv_u16x8{(uint16_t)lo[0], (uint16_t)lo[1], (uint16_t)lo[2], (uint16_t)lo[3],
+                            (uint16_t)hi[0], (uint16_t)hi[1], (uint16_t)hi[2], (uint16_t)hi[3]};
+    }
+    // Score row 4g + e of tile b is the block's token 8g + 4b + e; the
+    // first nv tokens of the block are the sequence's.
+    float x[8];
+#pragma unroll
+    for (uint32_t b = 0; b < 2; ++b)
+#pragma unroll
+        for (uint32_t e = 0; e < 4; ++e) x[4 * b + e] = sc[b][e] * p.scale_log2;
+    if (nv < kLatB) {
+#pragma unroll
+        for (uint32_t b = 0; b < 2; ++b)
+#pragma unroll
+            for (uint32_t e = 0; e < 4; ++e)
+                if (8 * g + 4 * b + e >= nv) x[4 * b + e] = -INFINITY;
+    }
+    float mx = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+    mx = fmaxf(mx, attn_xor16(mx));
+    mx = fmaxf(mx, attn_xor32(mx));
+    // Lazy rescaling: the reference m_run moves (and o and l are rescaled)
+    // only when some head's block maximum passes it by more than 8 log2
+    // units, so every weight is at most 2^8 and most blocks skip the
+    // rescale. The record's (m, l, o) stay relative to the same m.
+    if (__builtin_amdgcn_readfirstlane(__ballot(mx > st.m_run + 8.0f) != 0 ? 1u : 0u)) {
+        const float m_new = fmaxf(st.m_run, mx);
+        const float alpha = exp2f(st.m_run - m_new);
+        st.l_part *= alpha;
+        st.m_run = m_new;
+        float arow[4];
+#pragma unroll
+        for (uint32_t e = 0; e < 4; ++e) arow[e] = __shfl(alpha, 4 * g + e);
+#pragma unroll
+        for (uint32_t j = 0; j < S::NJ; ++j)
+#pragma unroll
+            for (uint32_t e = 0; e < 4; ++e) st.o[j][e] *= arow[e];
+    }
+    sglkv_u16x8 phi, plo;
+    float psum = 0.0f;
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) {
+        const float pi = __builtin_amdgcn_exp2f(x[i] - st.m_run);  // 0 for -inf; flushes below 2^-126
+        psum += pi;
+        attn_split_bf16(pi, phi, plo, i);
+    }
+    st.l_part += psum;
+#pragma unroll
+    for (uint32_t j = 0; j < S::NJ; ++j) {
+        st.o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(phi), attn_as_bf16(vv[j]), st.o[j], 0, 0, 0);
+        st.o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(plo), attn_as_bf16(vv[j]), st.o[j], 0, 0, 0);
     }
 }
 
@@ -1769,9 +1835,11 @@ __device__ __forceinline__ void attn_staged_body(const sglkv_attn_params &p) {
     const uint64_t vbase = pool + p.value_offset + w.kvh * p.value_head_stride;
     auto blk = [&](uint32_t b) { return table + (b < nb ? b : nb - 1) * kLatB; };
     auto stage = [&](uint32_t b) { return attn_stg_lds + (b % SGLKV_ATTN_STAGED_STAGES) * S::STAGE; };
-#pragma unroll
-    for (uint32_t b = 0; b + 1 < SGLKV_ATTN_STAGED_STAGES; ++b)
-        attn_stg_issue<D>(p, kbase, vbase, blk(b), b < nb, lane, stage(b));
+    static_assert(SGLKV_ATTN_STAGED_STAGES == 2, "one block in flight ahead");
+    uint32_t sl[S::LOADS];
+    attn_stg_slots<D>(blk(0), lane, sl);
+    attn_stg_issue<D>(p, kbase, vbase, sl, true, lane, stage(0));
+    attn_stg_slots<D>(blk(1), lane, sl);
     // The query and slot loads (which the compiler tracks) are complete
     // before the loop; the loop's waits count the row loads alone.
     __builtin_amdgcn_s_waitcnt(0x0F70);
@@ -1779,30 +1847,33 @@ __device__ __forceinline__ void attn_staged_body(const sglkv_attn_params &p) {
     attn_state_n<S::NJ> st;
     attn_state_init(st);
     for (uint32_t k = 0; k < nb; ++k) {
-        // Block k-1's LDS reads are done before block k+STAGES-1's rows
-        // overwrite its stage; then block k's loads (older than the newer
-        // blocks') have landed.
+        // Block k-1's LDS reads are done before block k+1's rows overwrite
+        // its stage; block k+1's slot entries were read one block ahead.
+        // Then block k's loads (older than block k+1's) have landed.
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        attn_stg_issue<D>(p, kbase, vbase, blk(k + SGLKV_ATTN_STAGED_STAGES - 1),
-                          k + SGLKV_ATTN_STAGED_STAGES - 1 < nb, lane, stage(k + SGLKV_ATTN_STAGED_STAGES - 1));
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * S::LOADS * (SGLKV_ATTN_STAGED_STAGES - 1)) : "memory");
+        attn_stg_issue<D>(p, kbase, vbase, sl, k + 1 < nb, lane, stage(k + 1));
+        attn_stg_slots<D>(blk(k + 2), lane, sl);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * S::LOADS) : "memory");
         const uint8_t *kst = stage(k);
-        sglkv_f32x4 sc[2] = {sglkv_f32x4{0.f, 0.f, 0.f, 0.f}, sglkv_f32x4{0.f, 0.f, 0.f, 0.f}};
-        uint32_t valid = 0;
+        // All K reads first, then the two score tiles' MFMA chains
+        // interleaved.
+        sglkv_u16x8 kf[2][S::KC];
 #pragma unroll
         for (uint32_t b = 0; b < 2; ++b) {
             const uint32_t t = 8 * (r >> 2) + 4 * b + (r & 3);
-            valid |= (blk(k)[S::entry(t)] != kAttnInvalidSlot ? 1u : 0u) << b;
 #pragma unroll
-            for (uint32_t c = 0; c < S::KC; ++c) {
-                const sglkv_u16x8 kf =
-                    *reinterpret_cast<const sglkv_u16x8 *>(kst + S::ROW * t + 16 * S::kpos(t, 4 * c + g));
-                sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(kf), attn_as_bf16(qf[c]), sc[b], 0, 0,
-                                                                0);
-            }
+            for (uint32_t c = 0; c < S::KC; ++c)
+                kf[b][c] = *reinterpret_cast<const sglkv_u16x8 *>(kst + S::ROW * t + 16 * S::kpos(t, 4 * c + g));
         }
-        const uint64_t vb0 = __ballot(valid & 1), vb1 = __ballot((valid >> 1) & 1);
-        attn_stg_softmax_pv<D>(p, g, r, sc, vb0, vb1, kst + S::V, st);
+        sglkv_f32x4 sc[2] = {sglkv_f32x4{0.f, 0.f, 0.f, 0.f}, sglkv_f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (uint32_t c = 0; c < S::KC; ++c)
+#pragma unroll
+            for (uint32_t b = 0; b < 2; ++b)
+                sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(kf[b][c]), attn_as_bf16(qf[c]), sc[b],
+                                                                0, 0, 0);
+        const uint64_t left = w.t1 - w.t0 - static_cast<uint64_t>(kLatB) * k;
+        attn_stg_softmax_pv<D>(p, g, r, sc, left < kLatB ? static_cast<uint32_t>(left) : kLatB, kst + S::V, st);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the zero-row loads issued past the chunk
     attn_finish(p, w, g, r, st);
@@ -1828,12 +1899,16 @@ extern "C" __global__ __launch_bounds__(512) void sglkv_paged_attention_wide128(
 }
 
 // K and V head dims 128 / 64, up to 16 query heads per KV head, rows
-// staged in LDS.
-extern "C" __global__ __launch_bounds__(64) void sglkv_paged_attention_staged128(sglkv_attn_params p) {
+// staged in LDS. A budget of 256 registers (two waves per SIMD, which LDS
+// does not allow anyway) makes the compiler keep the accumulators in
+// VGPRs instead of copying them between AGPRs and VGPRs every block.
+extern "C" __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void
+sglkv_paged_attention_staged128(sglkv_attn_params p) {
     attn_staged_body<128>(p);
 }
 
-extern "C" __global__ __launch_bounds__(64) void sglkv_paged_attention_staged64(sglkv_attn_params p) {
+extern "C" __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void
+sglkv_paged_attention_staged64(sglkv_attn_params p) {
     attn_staged_body<64>(p);
 }
 

@@ -31,7 +31,9 @@ paged-attention decode over the C2 decode pool (NHD or head-major pages),
 line carries its own metric (GB/s of K/V read). --config attn_mla does the
 same over the C4 pool in DeepSeek-V3's MLA form (K 576 / V 512 pair rows,
 128 query heads on one KV head); --config attn64 reads the C2 page table
-with head dims 64 (Llama-3.2-1B: 16 layers, 8 KV heads, 32 query heads).
+with head dims 64 (Llama-3.2-1B: 16 layers, 8 KV heads, 32 query heads) and
+--config attn256 with head dims 256 (Qwen3.5's full-attention layers: 2 KV
+heads, 8 query heads; 16 layers).
 
 Prints one JSON line (the driver's contract), with a `roofline` object for
 the dominant kernel and a `cpu_baseline` object: the CPU oracle
@@ -59,6 +61,7 @@ METRIC = "KV pack+unpack GB/s and % of HBM peak, Llama-3-8B shape; per-layer p50
 ATTN_METRIC = "paged-attention decode GB/s of K/V read and % of HBM peak, Llama-3-8B shape"
 MLA_METRIC = "paged-attention decode GB/s of K/V read and % of HBM peak, DeepSeek-V3 MLA shape"
 ATTN64_METRIC = "paged-attention decode GB/s of K/V read and % of HBM peak, Llama-3.2-1B shape"
+ATTN256_METRIC = "paged-attention decode GB/s of K/V read and % of HBM peak, Qwen3.5 head-dim-256 shape"
 DIRECT_METRIC = "KV pool-to-pool transfer GB/s (bytes read + written) and % of HBM peak, Llama-3-8B shape"
 
 DESCRIPTIONS = {
@@ -100,6 +103,10 @@ DESCRIPTIONS = {
               "Llama-3.2-1B shape, 16 layers x 8 KV heads x 64, bf16, page_size-64 NHD pool with "
               "a random page table, 64 requests x 2048 tokens, one decode query each with 32 "
               "query heads",
+    "attn256": "paged-attention decode with head dims 256 over the C2 decode pool's page table: "
+               "Qwen3.5 full-attention shape (the reference's qwen3_5 config: 2 KV heads x 256, "
+               "8 query heads), 16 layers, bf16, page_size-64 NHD pool with a random page table, "
+               "64 requests x 2048 tokens, one decode query each",
     "attn_mla": "paged-attention decode over the C4 decode pool as DeepSeek-V3's MLA decode reads "
                 "it: 61 layers of the reference's tensor-pair layout (576-wide latent+rope key, "
                 "512-wide latent value, bf16, one KV head), page_size 64 with a random page "
@@ -782,6 +789,8 @@ def _attention_geometry(config: str):
         return 61, 1, 576, 512, 64, 128, 1.0 / np.sqrt(192)
     if config == "attn64":  # Llama-3.2-1B
         return 16, 8, 64, 64, 64, 32, 1.0 / np.sqrt(64)
+    if config == "attn256":  # Qwen3.5's full-attention layers (model_registry.rs:628-660)
+        return 16, 2, 256, 256, 64, 8, 1.0 / np.sqrt(256)
     return 32, 8, 128, 128, 64, 32, 1.0 / np.sqrt(128)
 
 
@@ -838,6 +847,7 @@ def run_attention(args, config: str):
     """Decode attention over every layer of a decode pool: one async launch
     per layer on one stream. attn/attn_hnd read the C2 pool (Llama-3-8B GQA),
     attn64 the C2 page table at Llama-3.2-1B's head dims 64 (16 layers),
+    attn256 at Qwen3.5's head dims 256 (2 KV heads, 8 query heads),
     attn_mla the C4 pool in MLA tensor-pair form. Algorithmic bytes per
     launch = the K and V rows the queries attend (C2: 64 x 2048 tokens x
     2 x 2,048 B; MLA: 32 x 8192 tokens x (1,152 + 1,024) B) + queries +
@@ -850,7 +860,7 @@ def run_attention(args, config: str):
     t = wl.c4() if mla else wl.c2()
     L, H, dk, dv, P, qh, scale = _attention_geometry(config)
     D = dk
-    assert t.dst.page_size == P and (config == "attn64" or t.shape.layers == L)
+    assert t.dst.page_size == P and (config in ("attn64", "attn256") or t.shape.layers == L)
     nreq, n = len(t.lengths), int(t.lengths[0])
     layout = _attention_layout(kv, config, t.dst.page_count)
     k = kv.RocmKvPairCopyKernels(0)
@@ -912,9 +922,11 @@ def run_attention(args, config: str):
         f"{launch_flops / avg / 1e9:.1f} TFLOP/s), wall {gbs:.0f} GB/s")
     k.close()
     kernel = ("sglkv_paged_attention_latent+sglkv_paged_attention_combine_h" if mla
-              else ("sglkv_paged_attention_staged64" if D == 64 else "sglkv_paged_attention_staged128")
+              else ("sglkv_paged_attention_staged64" if D == 64 else "sglkv_paged_attention_staged256" if D == 256
+                    else "sglkv_paged_attention_staged128")
               + "+sglkv_paged_attention_combine")
-    summary = "paged_attention_decode_" + ("mla" if mla else "hnd" if hnd else "dims64" if D == 64 else "nhd")
+    summary = "paged_attention_decode_" + ("mla" if mla else "hnd" if hnd else "dims64" if D == 64
+                                           else "dims256" if D == 256 else "nhd")
     extra = {"requests": nreq, "tokens_per_request": n, "layers": L, "kv_heads": H,
              "query_heads": qh, "key_dim": dk, "value_dim": dv, "page_size": P,
              "head_layout": "HND" if hnd else "NHD",
@@ -1095,8 +1107,9 @@ def main():
               "c4fp8": lambda: wl.c4(fp8=True), "c4pair": wl.c4pair, "c4packed": wl.c4packed,
               "c5": wl.c5, "c2pages": wl.c2, "attn": wl.c2,
               "hnd64": wl.chunks64, "nhd64": lambda: wl.chunks64(head_major=False),
-              "attn_hnd": wl.c2, "attn_mla": wl.c4, "attn64": wl.c2, "ceilings": wl.c2, "c2direct": wl.c2}
-    attention = args.config in ("attn", "attn_hnd", "attn_mla", "attn64")
+              "attn_hnd": wl.c2, "attn_mla": wl.c4, "attn64": wl.c2, "attn256": wl.c2, "ceilings": wl.c2,
+              "c2direct": wl.c2}
+    attention = args.config in ("attn", "attn_hnd", "attn_mla", "attn64", "attn256")
     t = makers[args.config]()
     log(f"workload {t.name}: {t.rows} tokens moved, payload {t.payload_bytes / 2**30:.2f} GiB")
     if args.config == "c5":
@@ -1119,7 +1132,7 @@ def main():
     extra = r.pop("config_extra")
     out = {
         "metric": ((MLA_METRIC if args.config == "attn_mla" else ATTN64_METRIC if args.config == "attn64"
-                    else ATTN_METRIC) if attention
+                    else ATTN256_METRIC if args.config == "attn256" else ATTN_METRIC) if attention
                    else DIRECT_METRIC if args.config == "c2direct" else METRIC),
         "value": gbs,
         "unit": "GB/s",

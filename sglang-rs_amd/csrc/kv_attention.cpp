@@ -386,14 +386,19 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
     // decodes): the staged bodies, rows loaded straight into LDS. They
     // share one in-page offset between a token's K and V rows and form it
     // with a 24-bit multiply.
+    // Dims 256 (Qwen3.5's full-attention layers) take the staged body too,
+    // one wave covering all 256 value dims.
     const bool d64 = which == 3 && p.dk == 64 && p.dv == 64;
-    if ((which == 2 || d64) && qp % 16 == 0 && p.head_groups == 1 &&
+    const bool d256 = fast && p.dk == 256 && p.dv == 256;
+    if ((which == 2 || d64 || d256) && qp % 16 == 0 && p.head_groups == 1 &&
         p.key_token_stride == p.value_token_stride && p.key_token_stride < (1u << 24) &&
         lay.page_size <= (1u << 24) &&
         max_len <= 65535ull * SGLKV_ATTN_STAGED_SLOTS &&
         SGLKV_ATTN_STAGED_LDS_BYTES(p.dk) <= (unsigned)ctx->max_lds_per_block) {
-        which = d64 ? 8 : 7;
+        which = d64 ? 8 : d256 ? 10 : 7;
         lds = SGLKV_ATTN_STAGED_LDS_BYTES(p.dk);
+        threads = 64;
+        p.dv_blocks = 1;
     }
     p.zero_row = ctx->zero_row;
     p.page_stride32 = (uint32_t)lay.page_stride_bytes;
@@ -405,7 +410,7 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
     // Workgroups before splitting; split each query's sequence so that the
     // launch fills every CU with as many workgroups as stay resident at
     // once (the kernel's occupancy at this LDS size), in one round.
-    const bool wide = which >= 4 && which <= 6;  // the wide and latent bodies (7, 8: staged)
+    const bool wide = which >= 4 && which <= 6;  // the wide and latent bodies (7, 8, 10: staged)
     const uint64_t hblocks = which == 6 ? ceil_div(p.group, SGLKV_ATTN_LATENT_HEADS)
                                         : (p.head_groups + SGLKV_ATTN_WIDE_GROUPS - 1) / SGLKV_ATTN_WIDE_GROUPS;
     uint64_t base = c.query_count;

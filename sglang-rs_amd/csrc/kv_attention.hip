@@ -1177,6 +1177,23 @@ __device__ __forceinline__ void attn_sel64x2(bool ok, uint64_t a, uint64_t b, ui
     y = (static_cast<uint64_t>(yh) << 32) | yl;
 }
 
+// Four loads: lane l's 16 bytes of load i from a[i] to LDS at
+// at + i * PITCH + 16 l (non-temporal).
+template <uint32_t PITCH>
+__device__ __forceinline__ void attn_lat_load4v(const uint64_t *a, uint32_t at) {
+    uint32_t save;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %2, off nt\n\t"
+        "s_add_u32 m0, %1, %6\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %3, off nt\n\t"
+        "s_add_u32 m0, %1, %7\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %4, off nt\n\t"
+        "s_add_u32 m0, %1, %8\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %5, off nt\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(save)
+        : "s"(at), "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "n"(PITCH), "n"(2 * PITCH), "n"(3 * PITCH)
+        : "scc");
+}
+
 // Eight rows: row i's 1 KiB from a[i] (the same in every lane; lane l's 16
 // bytes at a[i] + 16 l) into LDS at at + i * PITCH. The leading s_nop 4
 // covers a VALU (readlane) write of a[i] just before; each M0 write is one
@@ -1649,15 +1666,18 @@ struct attn_stg {
     static constexpr uint32_t STAGE = 2 * V;                 // bytes of a stage
     static constexpr uint32_t KC = D / 32;                   // q.k steps
     static constexpr uint32_t NJ = D / 16;                   // p.v tiles
-    static_assert((D == 64 || D == 128) && STAGE * SGLKV_ATTN_STAGED_STAGES + 4 * SGLKV_ATTN_STAGED_SLOTS ==
-                                                SGLKV_ATTN_STAGED_LDS_BYTES(D),
+    static_assert((D == 64 || D == 128 || D == 256) &&
+                      STAGE * SGLKV_ATTN_STAGED_STAGES + 4 * SGLKV_ATTN_STAGED_SLOTS ==
+                          SGLKV_ATTN_STAGED_LDS_BYTES(D),
                   "stage layout");
     static_assert(2 * LOADS % 8 == 0, "whole groups of eight loads");
+    // Rows of 256 and 512 bytes both start on a 256-byte bank period, so
+    // dims 256 take the swizzles of dims 128 (their pieces' bit 4 is kept).
     static __device__ __forceinline__ uint32_t kpos(uint32_t t, uint32_t pc) {
-        return D == 128 ? pc ^ ((t & 3) | ((t >> 1) & 12)) : pc ^ (((t >> 1) & 1) | ((t >> 2) & 6));
+        return D >= 128 ? pc ^ ((t & 3) | ((t >> 1) & 12)) : pc ^ (((t >> 1) & 1) | ((t >> 2) & 6));
     }
     static __device__ __forceinline__ uint32_t vpos(uint32_t t, uint32_t pc) {
-        return D == 128 ? pc ^ (((t & 3) << 1) | (((t >> 3) & 1) << 3))
+        return D >= 128 ? pc ^ (((t & 3) << 1) | (((t >> 3) & 1) << 3))
                         : pc ^ ((((t >> 1) & 1) << 1) | (((t >> 3) & 1) << 2));
     }
     static __device__ __forceinline__ uint32_t entry(uint32_t t) { return LOADS * (t % TPL) + t / TPL; }
@@ -1717,19 +1737,25 @@ __device__ __forceinline__ void attn_stg_issue(const sglkv_attn_params &p, uint6
     // the token's offset (the host gives this body equal token strides, a
     // page_size and token stride below 2^24 and pages of at most 4 GiB, so
     // pos * stride fits a 24-bit multiply and 32 bits).
-    uint64_t a[2 * S::LOADS];
+    // Four loads' tokens at a time (K rows, then V rows), so at most eight
+    // addresses are live.
+    const uint32_t at = attn_lat_lds_at(stage);
 #pragma unroll
-    for (uint32_t j = 0; j < S::LOADS; ++j) {
-        const uint32_t t = S::TPL * j + c;
-        const bool ok = live && s[j] != kAttnInvalidSlot;
-        const uint32_t sj = ok ? s[j] : 0u;
-        const uint32_t in_page = __umul24(sj & mask, p.key_token_stride32);
-        const uint64_t off = static_cast<uint64_t>(sj >> p.page_shift) * p.page_stride32 + in_page;
-        attn_sel64x2(ok, kbase + off + 16 * S::kpos(t, pc), vbase + off + 16 * S::vpos(t, pc), zero, a[j],
-                     a[S::LOADS + j]);
+    for (uint32_t h = 0; h < S::LOADS / 4; ++h) {
+        uint64_t a[8];
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) {
+            const uint32_t j = 4 * h + i, t = S::TPL * j + c;
+            const bool ok = live && s[j] != kAttnInvalidSlot;
+            const uint32_t sj = ok ? s[j] : 0u;
+            const uint32_t in_page = __umul24(sj & mask, p.key_token_stride32);
+            const uint64_t off = static_cast<uint64_t>(sj >> p.page_shift) * p.page_stride32 + in_page;
+            attn_sel64x2(ok, kbase + off + 16 * S::kpos(t, pc), vbase + off + 16 * S::vpos(t, pc), zero, a[i],
+                         a[4 + i]);
+        }
+        attn_lat_load4v<1024>(a, at + 4096 * h);
+        attn_lat_load4v<1024>(a + 4, at + S::V + 4096 * h);
     }
-#pragma unroll
-    for (uint32_t h = 0; h < 2 * S::LOADS / 8; ++h) attn_lat_load8v<1024>(a + 8 * h, attn_lat_lds_at(stage + 8192 * h));
 }
 
 // Softmax of one block against the running maximum (rescaling o and l),
@@ -1739,18 +1765,21 @@ __device__ __forceinline__ void attn_stg_softmax_pv(const sglkv_attn_params &p, 
                                                     const sglkv_f32x4 (&sc)[2], uint32_t nv,
                                                     const uint8_t *vst, attn_state_n<attn_stg<D>::NJ> &st) {
     typedef attn_stg<D> S;
-    // The B operands of the p.v tiles (tile j: V[8g .. 8g+7][16j + r]) are
-    // read first, so their LDS latency passes under the softmax.
+    // The B operands of the p.v tiles (tile j: V[8g .. 8g+7][16j + r]) of
+    // the first group of (at most eight) tiles are read first, so their
+    // LDS latency passes under the softmax.
+    constexpr uint32_t VG = S::NJ > 8 ? 8 : S::NJ;
     const uint32_t t0 = 8 * g + (r >> 2), t1 = t0 + 4, d4 = r & 3;
-    sglkv_u16x8 vv[S::NJ];
-#pragma unroll
-    for (uint32_t j = 0; j < S::NJ; ++j) {
+    auto vread = [&](uint32_t j) {
         const uint32_t pc = 2 * j + (d4 >> 1), half = 8 * (d4 & 1);
         const attn_i16x4 lo = attn_lat_vtr(vst + S::ROW * t0 + 16 * S::vpos(t0, pc) + half);
         const attn_i16x4 hi = attn_lat_vtr(vst + S::ROW * t1 + 16 * S::vpos(t1, pc) + half);
-        vv[j] = sglkv_u16x8{(uint16_t)lo[0], (uint16_t)lo[1], (uint16_t)lo[2], (uint16_t)lo[3],
-                            (uint16_t)hi[0], (uint16_t)hi[1], (uint16_t)hi[2], (uint16_t)hi[3]};
-    }
+        return sglkv_u16x8{(uint16_t)lo[0], (uint16_t)lo[1], (uint16_t)lo[2], (uint16_t)lo[3],
+                           (uint16_t)hi[0], (uint16_t)hi[1], (uint16_t)hi[2], (uint16_t)hi[3]};
+    };
+    sglkv_u16x8 vv[VG];
+#pragma unroll
+    for (uint32_t j = 0; j < VG; ++j) vv[j] = vread(j);
     // Score row 4g + e of tile b is the block's token 8g + 4b + e; the
     // first nv tokens of the block are the sequence's.
     float x[8];
@@ -1795,9 +1824,18 @@ __device__ __forceinline__ void attn_stg_softmax_pv(const sglkv_attn_params &p, 
     }
     st.l_part += psum;
 #pragma unroll
-    for (uint32_t j = 0; j < S::NJ; ++j) {
-        st.o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(phi), attn_as_bf16(vv[j]), st.o[j], 0, 0, 0);
-        st.o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(plo), attn_as_bf16(vv[j]), st.o[j], 0, 0, 0);
+    for (uint32_t j0 = 0; j0 < S::NJ; j0 += VG) {
+        if (j0 > 0) {
+#pragma unroll
+            for (uint32_t j = 0; j < VG; ++j) vv[j] = vread(j0 + j);
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < VG; ++j) {
+            st.o[j0 + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(phi), attn_as_bf16(vv[j]),
+                                                                   st.o[j0 + j], 0, 0, 0);
+            st.o[j0 + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(plo), attn_as_bf16(vv[j]),
+                                                                   st.o[j0 + j], 0, 0, 0);
+        }
     }
 }
 
@@ -1855,23 +1893,29 @@ __device__ __forceinline__ void attn_staged_body(const sglkv_attn_params &p) {
         attn_stg_slots<D>(blk(k + 2), lane, sl);
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * S::LOADS) : "memory");
         const uint8_t *kst = stage(k);
-        // All K reads first, then the two score tiles' MFMA chains
-        // interleaved.
-        sglkv_u16x8 kf[2][S::KC];
-#pragma unroll
-        for (uint32_t b = 0; b < 2; ++b) {
-            const uint32_t t = 8 * (r >> 2) + 4 * b + (r & 3);
-#pragma unroll
-            for (uint32_t c = 0; c < S::KC; ++c)
-                kf[b][c] = *reinterpret_cast<const sglkv_u16x8 *>(kst + S::ROW * t + 16 * S::kpos(t, 4 * c + g));
-        }
+        // The K reads of a group of q.k steps first, then the two score
+        // tiles' MFMA chains interleaved (groups of 4 steps at dims 256, to
+        // bound the registers the reads hold).
+        constexpr uint32_t KG = S::KC > 4 ? 4 : S::KC;
         sglkv_f32x4 sc[2] = {sglkv_f32x4{0.f, 0.f, 0.f, 0.f}, sglkv_f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-        for (uint32_t c = 0; c < S::KC; ++c)
+        for (uint32_t c0 = 0; c0 < S::KC; c0 += KG) {
+            sglkv_u16x8 kf[2][KG];
 #pragma unroll
-            for (uint32_t b = 0; b < 2; ++b)
-                sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(kf[b][c]), attn_as_bf16(qf[c]), sc[b],
-                                                                0, 0, 0);
+            for (uint32_t b = 0; b < 2; ++b) {
+                const uint32_t t = 8 * (r >> 2) + 4 * b + (r & 3);
+#pragma unroll
+                for (uint32_t c = 0; c < KG; ++c)
+                    kf[b][c] = *reinterpret_cast<const sglkv_u16x8 *>(kst + S::ROW * t +
+                                                                      16 * S::kpos(t, 4 * (c0 + c) + g));
+            }
+#pragma unroll
+            for (uint32_t c = 0; c < KG; ++c)
+#pragma unroll
+                for (uint32_t b = 0; b < 2; ++b)
+                    sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(kf[b][c]), attn_as_bf16(qf[c0 + c]),
+                                                                    sc[b], 0, 0, 0);
+        }
         const uint64_t left = w.t1 - w.t0 - static_cast<uint64_t>(kLatB) * k;
         attn_stg_softmax_pv<D>(p, g, r, sc, left < kLatB ? static_cast<uint32_t>(left) : kLatB, kst + S::V, st);
     }
@@ -1910,6 +1954,13 @@ sglkv_paged_attention_staged128(sglkv_attn_params p) {
 extern "C" __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void
 sglkv_paged_attention_staged64(sglkv_attn_params p) {
     attn_staged_body<64>(p);
+}
+
+// Dims 256 (Qwen3.5's full-attention layers): 68 KiB of LDS, two
+// workgroups per CU.
+extern "C" __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void
+sglkv_paged_attention_staged256(sglkv_attn_params p) {
+    attn_staged_body<256>(p);
 }
 
 // MLA latent rows (K <= 576, V <= 512 dims), up to 128 query heads per

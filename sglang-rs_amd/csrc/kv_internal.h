@@ -129,12 +129,13 @@ struct sgl_rocm_kv_ctx {
     hipFunction_t stream_fn[3];     // streaming ceilings: copy, read, write
     // 16-byte vector / element-wise / pipelined dims 128 / pipelined dims <= 128 /
     // wide (K <= 576, V <= 512) / wide dims <= 128 / latent (MLA: K <= 576, V <= 512) /
-    // staged (dims 128, rows in LDS) / staged (dims 64) / latent with hi + lo weights
-    hipFunction_t attention[10];
+    // staged (dims 128, rows in LDS) / staged (dims 64) / latent with hi + lo weights /
+    // staged (dims 256)
+    hipFunction_t attention[11];
     hipFunction_t attention_combine;
     hipFunction_t attention_combine_h;    // the latent body's scaled fp16 records
-    uint32_t attention_occupancy[10];     // resident workgroups per CU of attention[i] ...
-    uint32_t attention_occupancy_lds[10]; // ... at this LDS size (0 = not yet queried)
+    uint32_t attention_occupancy[11];     // resident workgroups per CU of attention[i] ...
+    uint32_t attention_occupancy_lds[11]; // ... at this LDS size (0 = not yet queried)
     int max_lds_per_block;                // device limit on a workgroup's LDS bytes
     // Device error words, at the start of a small zeroed block: one per
     // consumer, as the reference keeps one flag per kernels object

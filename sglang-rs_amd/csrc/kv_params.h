@@ -247,7 +247,7 @@ typedef struct sglkv_request_params {
 #define SGLKV_ATTN_LATENT_VSTAGE (SGLKV_ATTN_TOKENS * 1088u)
 #define SGLKV_ATTN_LATENT_LDS_BYTES                                                            \
     (2u * (SGLKV_ATTN_LATENT_KSTAGE + SGLKV_ATTN_LATENT_VSTAGE) + 4u * SGLKV_ATTN_WIDE_SLOTS + 16u)
-/* The staged bodies (K and V head dims d = 64 or 128, at most
+/* The staged bodies (K and V head dims d = 64, 128 or 256, at most
  * SGLKV_ATTN_HEADS query heads per KV head): one wave per workgroup,
  * SGLKV_ATTN_STAGED_STAGES LDS stages of a 32-token block (64 d bytes of K
  * rows, then as many of V rows) and the chunk's slot table (at most

@@ -205,6 +205,26 @@ def test_dims64_decode(k, H, qh, P, hnd, nreq, max_len):
     _check(got, want, c)
 
 
+@pytest.mark.parametrize("H,qh,P,hnd,nreq,max_len", [
+    (2, 8, 64, False, 16, 1500),   # Qwen3.5's full-attention layers: 8 query heads over 2 KV heads
+    (2, 8, 16, True, 6, 4000),     # head-major pages, long sequences split several times
+    (2, 8, 64, False, 1, 3000),    # one query: 64-token chunks, many splits
+    (4, 64, 64, True, 3, 700),     # groups of 16 query heads
+])
+def test_dims256_decode(k, H, qh, P, hnd, nreq, max_len):
+    """Decode with K and V head dims 256 (the dims-256 staged body): the
+    reference's Qwen3.5 configuration (model_registry.rs:628-660) has
+    head_dim 256, 8 query heads and 2 KV heads."""
+    rng = np.random.default_rng(256 + P + qh + nreq)
+    pages = -(-nreq * max_len // P) + 4
+    c = _Case(rng, P=P, L=2, H=H, dk=256, dv=256, qh=qh, pages=pages, layer=1, hnd=hnd)
+    lens, rso, slots = _random_batch(rng, nreq, max_len, c.layout.slot_count)
+    q = _bf16_normal(rng, nreq * qh * 256).reshape(nreq, qh, 256)
+    _say(f"dims-256 decode H={H} qh={qh} P={P} hnd={hnd} tokens={int(rso[-1])}")
+    got, want = c.run(k, q, np.arange(nreq), lens, rso, slots, 1.0 / math.sqrt(256), max_len=max_len)
+    _check(got, want, c)
+
+
 def test_long_sequence_is_split_and_combined(k):
     """One request of 20,000 tokens (many splits through the combine kernel)
     and a short one in the same launch; the short query's sequence ends
@@ -225,7 +245,8 @@ def test_long_sequence_is_split_and_combined(k):
     _check(got2, want, c, 'no length hint')
 
 
-@pytest.mark.parametrize("dk,dv,qh,H", [(128, 128, 32, 8), (64, 64, 16, 2), (576, 512, 128, 1)])
+@pytest.mark.parametrize("dk,dv,qh,H", [(128, 128, 32, 8), (64, 64, 16, 2), (256, 256, 8, 2),
+                                        (576, 512, 128, 1)])
 def test_split_records_are_each_counted_once(k, dk, dv, qh, H):
     """Values that are constant over 256-token blocks (+-4 plus a little
     noise, a random sign per block) make each split's share of the output
@@ -233,7 +254,7 @@ def test_split_records_are_each_counted_once(k, dk, dv, qh, H):
     the output by about 4 x that split's weight, far past the error bound.
     24 queries over one 20,000-token request take every count of splits
     from 1 to all of them (so every remainder of the combine's groups of
-    eight), on the staged bodies (dims 128, 64) and the latent MLA body."""
+    eight), on the staged bodies (dims 128, 64, 256) and the latent MLA body."""
     rng = np.random.default_rng(dk + 31)
     n = 20000
     c = _Case(rng, P=64, L=1, H=H, dk=dk, dv=dv, qh=qh, pages=-(-n // 64) + 4, layer=0)
@@ -261,6 +282,7 @@ def test_split_records_are_each_counted_once(k, dk, dv, qh, H):
     (2, 64, 128, 128, False),    # group of 32: two head groups per KV head
     (1, 16, 576, 512, False),    # MLA widths (DeepSeek pair): dv spans 4 blocks
     (1, 20, 576, 512, True),     # MLA widths, head-major, group not a multiple of 16
+    (1, 32, 256, 256, False),    # dims 256, two head groups: the wide body
     (2, 6, 12, 4, False),        # odd widths: element-wise loads
     (3, 9, 40, 24, True),        # dims not multiples of 32
 ])
@@ -278,7 +300,7 @@ def test_shapes(k, H, qh, dk, dv, hnd):
     _check(got, want, c)
 
 
-@pytest.mark.parametrize("dk,dv,P", [(128, 128, 64), (64, 64, 16), (576, 512, 16)])
+@pytest.mark.parametrize("dk,dv,P", [(128, 128, 64), (64, 64, 16), (256, 256, 64), (576, 512, 16)])
 def test_slots_outside_the_sequences_hold_nan(k, dk, dv, P):
     """Every pool byte the queries do not attend is a NaN pattern: padded
     tokens of the last block (lengths not a multiple of 32) and split ends

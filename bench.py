@@ -923,7 +923,7 @@ def run_attention(args, config: str):
     k.close()
     kernel = ("sglkv_paged_attention_latent+sglkv_paged_attention_combine_h" if mla
               else ("sglkv_paged_attention_staged64" if D == 64 else "sglkv_paged_attention_staged256" if D == 256
-                    else "sglkv_paged_attention_staged128")
+                    else "sglkv_paged_attention_staged128k" if hnd else "sglkv_paged_attention_staged128")
               + "+sglkv_paged_attention_combine")
     summary = "paged_attention_decode_" + ("mla" if mla else "hnd" if hnd else "dims64" if D == 64
                                            else "dims256" if D == 256 else "nhd")

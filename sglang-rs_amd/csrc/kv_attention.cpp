@@ -397,6 +397,11 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
         SGLKV_ATTN_STAGED_LDS_BYTES(p.dk) <= (unsigned)ctx->max_lds_per_block) {
         which = d64 ? 8 : d256 ? 10 : 7;
         lds = SGLKV_ATTN_STAGED_LDS_BYTES(p.dk);
+        // Head-major pages at dims 128: K in registers, V alone in LDS.
+        if (which == 7 && lay.head_layout == SGL_KV_HND) {
+            which = 11;
+            lds = SGLKV_ATTN_KREG_LDS_BYTES(p.dk);
+        }
         threads = 64;
         p.dv_blocks = 1;
     }
@@ -410,7 +415,7 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
     // Workgroups before splitting; split each query's sequence so that the
     // launch fills every CU with as many workgroups as stay resident at
     // once (the kernel's occupancy at this LDS size), in one round.
-    const bool wide = which >= 4 && which <= 6;  // the wide and latent bodies (7, 8, 10: staged)
+    const bool wide = which >= 4 && which <= 6;  // the wide and latent bodies (7, 8, 10, 11: staged)
     const uint64_t hblocks = which == 6 ? ceil_div(p.group, SGLKV_ATTN_LATENT_HEADS)
                                         : (p.head_groups + SGLKV_ATTN_WIDE_GROUPS - 1) / SGLKV_ATTN_WIDE_GROUPS;
     uint64_t base = c.query_count;
@@ -439,12 +444,14 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
     //    tokens): 1 query 23.3 -> 15.5 us / 16.7 -> 11.8 us at 64 tokens
     //    against 256, 2 queries 24.6 -> 17.8 / 17.5 -> 12.2, 4 queries 26.4
     //    -> 23.3 / 18.8 -> 15.9; from 16 queries on the split count is set
-    //    by the occupancy target, not by this minimum;
+    //    by the occupancy target, not by this minimum. The dims-128 body
+    //    with K in registers (eight waves per CU) takes 128: at 64, 4
+    //    queries took 22.4 us against 20.6;
     //  - latent body (MLA over 8,192 tokens): 64 tokens for one workgroup
     //    before splitting, 128 for two or three (1 query 40.0 -> 33.2 us,
     //    2 queries 41.0 -> 35.2 us), 256 from four on (best there);
     //  - the other bodies keep 256 (not measured otherwise).
-    const uint64_t min_chunk = which >= 7 ? 64 : which == 6 && base < 4 ? (base <= 1 ? 64 : 128) : 256;
+    const uint64_t min_chunk = which == 11 ? 128 : which >= 7 ? 64 : which == 6 && base < 4 ? (base <= 1 ? 64 : 128) : 256;
     chunk = ceil_div(chunk < min_chunk ? min_chunk : chunk, SGLKV_ATTN_TOKENS) * SGLKV_ATTN_TOKENS;
     uint64_t splits = ceil_div(max_len, chunk);
     const uint64_t table = wide ? SGLKV_ATTN_WIDE_SLOTS : which >= 7 ? SGLKV_ATTN_STAGED_SLOTS : 0;

@@ -1144,6 +1144,20 @@ __device__ __forceinline__ void attn_lat_load(uint64_t src, const uint8_t *dst) 
         : "v"(src), "s"(attn_lat_lds_at(dst)));
 }
 
+// ok ? a : z per lane, as two v_cndmask_b32 (see attn_sel64x2).
+__device__ __forceinline__ uint64_t attn_sel64(bool ok, uint64_t a, uint64_t z) {
+    const uint32_t m = ok ? 1u : 0u;
+    uint32_t xl, xh;
+    asm("v_cmp_ne_u32 vcc, 0, %2\n\t"
+        "v_cndmask_b32 %0, %3, %4, vcc\n\t"
+        "v_cndmask_b32 %1, %5, %6, vcc"
+        : "=&v"(xl), "=&v"(xh)
+        : "v"(m), "v"(static_cast<uint32_t>(z)), "v"(static_cast<uint32_t>(a)), "v"(static_cast<uint32_t>(z >> 32)),
+          "v"(static_cast<uint32_t>(a >> 32))
+        : "vcc");
+    return (static_cast<uint64_t>(xh) << 32) | xl;
+}
+
 // x of lane l ^ 16 and of lane l ^ 32 (a wave of 64): gfx950's row-swap
 // permutes (v_permlane16_swap_b32, v_permlane32_swap_b32), with no LDS
 // round trip. A swap of x with itself leaves the partner row's x in one of
@@ -1923,6 +1937,186 @@ __device__ __forceinline__ void attn_staged_body(const sglkv_attn_params &p) {
     attn_finish(p, w, g, r, st);
 }
 
+// ---- The staged body with K in registers (dims 128, head-major pages) ----
+//
+// The staged layout for V (transposing reads need it in LDS), but each K
+// row piece goes straight from the pool into the VGPRs of the q.k A
+// operand: lane (g, r) of score tile b takes 16 bytes of token
+// 8(r >> 2) + 4b + (r & 3) at dims 32c + 8g for every q.k step c. A wave's
+// LDS is then its two V stages and its slot table (20 KiB at dims 128), so
+// twice as many waves share a CU (eight), each with two blocks of K and up
+// to two of V in flight. K loads are inline asm like the V loads (the
+// compiler would count only its own loads in its waits); their registers
+// pass through the wait that covers them, so no use moves above it. They
+// are cached loads: steps c and c + 1 read the two halves of one 128-byte
+// line, and the second finds it in L2 (with non-temporal K loads the body
+// measured 7 % slower than the LDS-staged one on NHD pages). On MI355X it
+// pays on head-major pages (a head's tokens are consecutive rows): 99.5
+// -> 94.7 us per launch on the 64-query bench; on token-major pages it
+// took 102.2 us against the LDS-staged body's 95.8, so those keep it.
+typedef unsigned int attn_u32x4 __attribute__((ext_vector_type(4)));
+
+template <uint32_t D>
+struct attn_kr {
+    typedef attn_stg<D> S;
+    static constexpr uint32_t VST = kLatB * S::ROW;  // one V stage
+    static constexpr uint32_t KL = 2 * S::KC;        // K register loads per block
+};
+
+__device__ __forceinline__ attn_u32x4 attn_kr_load(uint64_t a) {
+    attn_u32x4 v;
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(a) : "memory");
+    return v;
+}
+
+// K pieces of block `tb` (live false: past the chunk) into kr[b][c].
+template <uint32_t D>
+__device__ __forceinline__ void attn_kr_issue_k(const sglkv_attn_params &p, uint64_t kbase, const uint32_t *tb,
+                                                bool live, uint32_t g, uint32_t r,
+                                                attn_u32x4 (&kr)[2][attn_stg<D>::KC]) {
+    typedef attn_stg<D> S;
+    const uint32_t mask = (1u << p.page_shift) - 1;
+    const uint64_t zero = reinterpret_cast<uint64_t>(p.zero_row);
+#pragma unroll
+    for (uint32_t b = 0; b < 2; ++b) {
+        const uint32_t t = 8 * (r >> 2) + 4 * b + (r & 3);
+        const uint32_t s = tb[S::entry(t)];
+        const bool ok = live && s != kAttnInvalidSlot;
+        const uint32_t sj = ok ? s : 0u;
+        const uint32_t in_page = __umul24(sj & mask, p.key_token_stride32);
+        const uint64_t row = attn_sel64(
+            ok, kbase + static_cast<uint64_t>(sj >> p.page_shift) * p.page_stride32 + in_page, zero);
+#pragma unroll
+        for (uint32_t c = 0; c < S::KC; ++c) kr[b][c] = attn_kr_load(row + 16 * (4 * c + g));
+    }
+}
+
+// V rows of block `tb` into a V stage (the staged layout's V half).
+template <uint32_t D>
+__device__ __forceinline__ void attn_kr_issue_v(const sglkv_attn_params &p, uint64_t vbase, const uint32_t *tb,
+                                                bool live, uint32_t lane, const uint8_t *stage) {
+    typedef attn_stg<D> S;
+    uint32_t s[S::LOADS];
+    attn_stg_slots<D>(tb, lane, s);
+    const uint32_t c = lane / S::PIECES, pc = lane % S::PIECES;
+    const uint64_t zero = reinterpret_cast<uint64_t>(p.zero_row) + 16 * pc;
+    const uint32_t mask = (1u << p.page_shift) - 1;
+    uint64_t a[S::LOADS];
+#pragma unroll
+    for (uint32_t j = 0; j < S::LOADS; ++j) {
+        const uint32_t t = S::TPL * j + c;
+        const bool ok = live && s[j] != kAttnInvalidSlot;
+        const uint32_t sj = ok ? s[j] : 0u;
+        const uint32_t in_page = __umul24(sj & mask, p.value_token_stride32);
+        a[j] = attn_sel64(ok, vbase + static_cast<uint64_t>(sj >> p.page_shift) * p.page_stride32 + in_page +
+                                  16 * S::vpos(t, pc),
+                          zero);
+    }
+    const uint32_t at = attn_lat_lds_at(stage);
+    if constexpr (S::LOADS == 8)
+        attn_lat_load8v<1024>(a, at);
+    else
+        attn_lat_load4v<1024>(a, at);
+}
+
+// Waits until at most N vector-memory loads are outstanding; the K
+// registers of the block pass through it.
+template <uint32_t N, uint32_t KC>
+__device__ __forceinline__ void attn_kr_wait(attn_u32x4 (&kr)[2][KC]) {
+    if constexpr (KC == 4)
+        asm volatile("s_waitcnt vmcnt(%8)"
+                     : "+v"(kr[0][0]), "+v"(kr[0][1]), "+v"(kr[0][2]), "+v"(kr[0][3]), "+v"(kr[1][0]),
+                       "+v"(kr[1][1]), "+v"(kr[1][2]), "+v"(kr[1][3])
+                     : "n"(N)
+                     : "memory");
+    else
+        asm volatile("s_waitcnt vmcnt(%4)"
+                     : "+v"(kr[0][0]), "+v"(kr[0][1]), "+v"(kr[1][0]), "+v"(kr[1][1])
+                     : "n"(N)
+                     : "memory");
+}
+
+template <uint32_t D>
+__device__ __forceinline__ void attn_kr_block(const sglkv_attn_params &p, uint32_t g, uint32_t r,
+                                              const sglkv_u16x8 (&qf)[attn_stg<D>::KC],
+                                              const attn_u32x4 (&kr)[2][attn_stg<D>::KC], const uint8_t *vst,
+                                              uint32_t nv, attn_state_n<attn_stg<D>::NJ> &st) {
+    typedef attn_stg<D> S;
+    sglkv_f32x4 sc[2] = {sglkv_f32x4{0.f, 0.f, 0.f, 0.f}, sglkv_f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (uint32_t c = 0; c < S::KC; ++c)
+#pragma unroll
+        for (uint32_t b = 0; b < 2; ++b)
+            sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(attn_as_bf16(__builtin_bit_cast(sglkv_u16x8, kr[b][c])),
+                                                            attn_as_bf16(qf[c]), sc[b], 0, 0, 0);
+    attn_stg_softmax_pv<D>(p, g, r, sc, nv, vst, st);
+}
+
+template <uint32_t D>
+__device__ __forceinline__ void attn_kreg_body(const sglkv_attn_params &p) {
+    typedef attn_stg<D> S;
+    typedef attn_kr<D> K;
+    extern __shared__ __attribute__((aligned(16))) uint8_t attn_kr_lds[];
+    uint32_t *table = reinterpret_cast<uint32_t *>(attn_kr_lds + 2 * K::VST);
+    const uint32_t lane = threadIdx.x;
+    const uint32_t g = lane >> 4, r = lane & 15;
+    attn_work w;
+    if (!attn_decode(p, lane, &w)) return;
+    const uint32_t nb = static_cast<uint32_t>((w.t1 - w.t0 + kLatB - 1) / kLatB);
+
+    sglkv_u16x8 qf[S::KC];
+#pragma unroll
+    for (uint32_t c = 0; c < S::KC; ++c) {
+        qf[c] = sglkv_u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        if (r < w.nh)
+            qf[c] = *reinterpret_cast<const sglkv_u16x8 *>(p.queries + (w.q * p.query_heads + w.h0 + r) * D +
+                                                            32 * c + 8 * g);
+    }
+    for (uint32_t i = lane; i < nb * kLatB; i += 64) {
+        const uint64_t tok = w.t0 + i;
+        table[(i & ~31u) + S::entry(i & 31)] =
+            attn_wide_slot(p, tok < w.t1 ? p.sequence_slots[w.start + tok] : 0, tok, w.t1);
+    }
+    __syncthreads();
+
+    const uint64_t pool = reinterpret_cast<uint64_t>(p.pool);
+    const uint64_t kbase = pool + p.key_offset + w.kvh * p.key_head_stride;
+    const uint64_t vbase = pool + p.value_offset + w.kvh * p.value_head_stride;
+    auto blk = [&](uint32_t b) { return table + (b < nb ? b : nb - 1) * kLatB; };
+    uint8_t *const v0 = attn_kr_lds, *const v1 = attn_kr_lds + K::VST;
+    auto nvalid = [&](uint32_t k) {
+        const uint64_t left = w.t1 - w.t0 - static_cast<uint64_t>(kLatB) * k;
+        return left < kLatB ? static_cast<uint32_t>(left) : kLatB;
+    };
+    // Blocks alternate between register set A with stage v0 (even) and B
+    // with v1 (odd). Loads in issue order: K(k) V(k) per block; a block's
+    // wait leaves the next block's K.L + LOADS loads outstanding.
+    attn_u32x4 ka[2][S::KC], kb[2][S::KC];
+    attn_kr_issue_k<D>(p, kbase, blk(0), true, g, r, ka);
+    attn_kr_issue_v<D>(p, vbase, blk(0), true, lane, v0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // the query and slot loads (and block 0)
+
+    attn_state_n<S::NJ> st;
+    attn_state_init(st);
+    constexpr uint32_t AHEAD = K::KL + S::LOADS;
+    for (uint32_t k = 0; k < nb; k += 2) {
+        // p.v(k-1) read v1 before V(k+1) lands there.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        attn_kr_issue_k<D>(p, kbase, blk(k + 1), k + 1 < nb, g, r, kb);
+        attn_kr_issue_v<D>(p, vbase, blk(k + 1), k + 1 < nb, lane, v1);
+        attn_kr_wait<AHEAD, S::KC>(ka);
+        attn_kr_block<D>(p, g, r, qf, ka, v0, nvalid(k), st);
+        if (k + 1 >= nb) break;
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        attn_kr_issue_k<D>(p, kbase, blk(k + 2), k + 2 < nb, g, r, ka);
+        attn_kr_issue_v<D>(p, vbase, blk(k + 2), k + 2 < nb, lane, v0);
+        attn_kr_wait<AHEAD, S::KC>(kb);
+        attn_kr_block<D>(p, g, r, qf, kb, v1, nvalid(k + 1), st);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the loads issued past the chunk
+    attn_finish(p, w, g, r, st);
+}
+
 }  // namespace
 
 extern "C" __global__ __launch_bounds__(64) void sglkv_paged_attention_v16(sglkv_attn_params p) {
@@ -1943,12 +2137,18 @@ extern "C" __global__ __launch_bounds__(512) void sglkv_paged_attention_wide128(
 }
 
 // K and V head dims 128 / 64, up to 16 query heads per KV head, rows
-// staged in LDS. A budget of 256 registers (two waves per SIMD, which LDS
-// does not allow anyway) makes the compiler keep the accumulators in
-// VGPRs instead of copying them between AGPRs and VGPRs every block.
+// staged in LDS; for head-major pages, dims 128 also with K in registers
+// and V alone in LDS. A budget of 256 registers (two waves per SIMD) makes
+// the compiler keep the accumulators in VGPRs instead of copying them
+// between AGPRs and VGPRs every block.
 extern "C" __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void
 sglkv_paged_attention_staged128(sglkv_attn_params p) {
     attn_staged_body<128>(p);
+}
+
+extern "C" __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void
+sglkv_paged_attention_staged128k(sglkv_attn_params p) {
+    attn_kreg_body<128>(p);
 }
 
 extern "C" __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void

@@ -130,12 +130,12 @@ struct sgl_rocm_kv_ctx {
     // 16-byte vector / element-wise / pipelined dims 128 / pipelined dims <= 128 /
     // wide (K <= 576, V <= 512) / wide dims <= 128 / latent (MLA: K <= 576, V <= 512) /
     // staged (dims 128, rows in LDS) / staged (dims 64) / latent with hi + lo weights /
-    // staged (dims 256)
-    hipFunction_t attention[11];
+    // staged (dims 256) / staged (dims 128, K in registers: head-major pages)
+    hipFunction_t attention[12];
     hipFunction_t attention_combine;
     hipFunction_t attention_combine_h;    // the latent body's scaled fp16 records
-    uint32_t attention_occupancy[11];     // resident workgroups per CU of attention[i] ...
-    uint32_t attention_occupancy_lds[11]; // ... at this LDS size (0 = not yet queried)
+    uint32_t attention_occupancy[12];     // resident workgroups per CU of attention[i] ...
+    uint32_t attention_occupancy_lds[12]; // ... at this LDS size (0 = not yet queried)
     int max_lds_per_block;                // device limit on a workgroup's LDS bytes
     // Device error words, at the start of a small zeroed block: one per
     // consumer, as the reference keeps one flag per kernels object

@@ -255,6 +255,9 @@ typedef struct sglkv_request_params {
 #define SGLKV_ATTN_STAGED_STAGES 2u
 #define SGLKV_ATTN_STAGED_SLOTS 1024u
 #define SGLKV_ATTN_STAGED_LDS_BYTES(d) (SGLKV_ATTN_STAGED_STAGES * 128u * (d) + 4u * SGLKV_ATTN_STAGED_SLOTS)
+/* The dims-128 staged body keeps K in registers: two stages of V rows only
+ * (64 d bytes each) and the slot table. */
+#define SGLKV_ATTN_KREG_LDS_BYTES(d) (SGLKV_ATTN_STAGED_STAGES * 64u * (d) + 4u * SGLKV_ATTN_STAGED_SLOTS)
 
 typedef struct sglkv_attn_params {
     const uint16_t *queries;              /* bf16 [query][query_head][dk] */

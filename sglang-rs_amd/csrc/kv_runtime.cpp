@@ -518,6 +518,8 @@ extern "C" int32_t sgl_rocm_kv_init(int32_t device, const char *code_object_path
     if (err == hipSuccess)
         err = hipModuleGetFunction(&ctx->attention[10], ctx->module, "sglkv_paged_attention_staged256");
     if (err == hipSuccess)
+        err = hipModuleGetFunction(&ctx->attention[11], ctx->module, "sglkv_paged_attention_staged128k");
+    if (err == hipSuccess)
         err = hipDeviceGetAttribute(&ctx->max_lds_per_block, hipDeviceAttributeMaxSharedMemoryPerBlock, device);
     if (err == hipSuccess)
         err = hipModuleGetFunction(&ctx->attention_combine, ctx->module, "sglkv_paged_attention_combine");

@@ -300,14 +300,17 @@ def test_shapes(k, H, qh, dk, dv, hnd):
     _check(got, want, c)
 
 
-@pytest.mark.parametrize("dk,dv,P", [(128, 128, 64), (64, 64, 16), (256, 256, 64), (576, 512, 16)])
-def test_slots_outside_the_sequences_hold_nan(k, dk, dv, P):
+@pytest.mark.parametrize("dk,dv,P,hnd", [(128, 128, 64, False), (128, 128, 64, True), (64, 64, 16, False),
+                                         (256, 256, 64, False), (576, 512, 16, False)])
+def test_slots_outside_the_sequences_hold_nan(k, dk, dv, P, hnd):
     """Every pool byte the queries do not attend is a NaN pattern: padded
     tokens of the last block (lengths not a multiple of 32) and split ends
-    must contribute exact zeros, never garbage, on the pipelined body
-    (dims 128 and 64) and the generic one (MLA widths)."""
-    rng = np.random.default_rng(dk + P)
-    c = _Case(rng, P=P, L=1, H=1, dk=dk, dv=dv, qh=8, pages=120, layer=0)
+    must contribute exact zeros, never garbage, on the staged bodies (dims
+    128 with K in LDS and, head-major, in registers; 64; 256) and the latent
+    one (MLA widths). With one KV head, head-major and token-major pages
+    hold the same bytes."""
+    rng = np.random.default_rng(dk + P + hnd)
+    c = _Case(rng, P=P, L=1, H=1, dk=dk, dv=dv, qh=8, pages=120, layer=0, hnd=hnd)
     lens = np.array([1, 31, 33, 700, 1001])
     rso = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint64)
     slots = rng.choice(c.layout.slot_count, size=int(rso[-1]), replace=False).astype(np.uint64)
@@ -327,7 +330,7 @@ def test_slots_outside_the_sequences_hold_nan(k, dk, dv, P):
     pool16[nan_mask] = 0x7FC1
     c.pool.upload(c.pool_h)
     q = _bf16_normal(rng, 5 * 8 * dk).reshape(5, 8, dk)
-    _say(f"nan-filled pool dk={dk} dv={dv} P={P}")
+    _say(f"nan-filled pool dk={dk} dv={dv} P={P} hnd={hnd}")
     got, want = c.run(k, q, np.arange(5), lens, rso, slots, 1.0 / math.sqrt(dk), max_len=1001)
     assert np.isfinite(want).all() and np.isfinite(got).all()
     _check(got, want, c)
@@ -349,19 +352,21 @@ def test_mla_many_heads(k, qh, hnd):
     _check(got, want, c)
 
 
-@pytest.mark.parametrize("D,nq", [(128, 1), (128, 2), (64, 1), (64, 3)])
-def test_staged_small_batches(k, D, nq):
+@pytest.mark.parametrize("D,nq,hnd", [(128, 1, False), (128, 2, False), (64, 1, False), (64, 3, False),
+                                      (128, 1, True), (128, 3, True)])
+def test_staged_small_batches(k, D, nq, hnd):
     """One to three GQA decode queries (32 heads over 8 KV heads): the
     staged bodies split each 3,000-token sequence into 64-token chunks (up
-    to 47 splits), which the combine merges several groups of eight at a
-    time in parallel thread sets."""
-    rng = np.random.default_rng(D + nq)
-    c = _Case(rng, P=16, L=2, H=8, dk=D, dv=D, qh=32, pages=600, layer=1)
+    to 47 splits; 128-token chunks for the body with K in registers, which
+    head-major pages at dims 128 take), which the combine merges several
+    groups of eight at a time in parallel thread sets."""
+    rng = np.random.default_rng(D + nq + hnd)
+    c = _Case(rng, P=16, L=2, H=8, dk=D, dv=D, qh=32, pages=600, layer=1, hnd=hnd)
     lens = np.array([3000, 1777, 2500][:nq])
     rso = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint64)
     slots = rng.choice(c.layout.slot_count, size=int(rso[-1]), replace=False).astype(np.uint64)
     q = _bf16_normal(rng, nq * 32 * D).reshape(nq, 32, D)
-    _say(f"staged small batch: dims {D}, {nq} queries, lengths {list(lens)}")
+    _say(f"staged small batch: dims {D}, {nq} queries, hnd={hnd}, lengths {list(lens)}")
     got, want = c.run(k, q, np.arange(nq), lens, rso, slots, 1.0 / math.sqrt(D), max_len=int(lens.max()))
     _check(got, want, c)
 

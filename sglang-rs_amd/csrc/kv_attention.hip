@@ -1947,13 +1947,14 @@ __device__ __forceinline__ void attn_staged_body(const sglkv_attn_params &p) {
 // twice as many waves share a CU (eight), each with two blocks of K and up
 // to two of V in flight. K loads are inline asm like the V loads (the
 // compiler would count only its own loads in its waits); their registers
-// pass through the wait that covers them, so no use moves above it. They
-// are cached loads: steps c and c + 1 read the two halves of one 128-byte
-// line, and the second finds it in L2 (with non-temporal K loads the body
-// measured 7 % slower than the LDS-staged one on NHD pages). On MI355X it
-// pays on head-major pages (a head's tokens are consecutive rows): 99.5
-// -> 94.7 us per launch on the 64-query bench; on token-major pages it
-// took 102.2 us against the LDS-staged body's 95.8, so those keep it.
+// pass through the wait that covers them, so no use moves above it. Steps
+// c and c + 1 read the two halves of one 128-byte line. The loads carry
+// sc0 nt: measured on the head-major bench (alternating runs, GB/s wall),
+// 5,651 against 5,519 with the default policy, 5,601 with nt alone, 5,439
+// with sc0 and 5,327 with sc1. On MI355X this body pays on head-major
+// pages (a head's tokens are consecutive rows): 99.5 -> 94.3 us per launch
+// on the 64-query bench; on token-major pages it took 102-114 us against
+// the LDS-staged body's 95.8 whatever the policy, so those keep that one.
 typedef unsigned int attn_u32x4 __attribute__((ext_vector_type(4)));
 
 template <uint32_t D>
@@ -1965,7 +1966,7 @@ struct attn_kr {
 
 __device__ __forceinline__ attn_u32x4 attn_kr_load(uint64_t a) {
     attn_u32x4 v;
-    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(a) : "memory");
+    asm volatile("global_load_dwordx4 %0, %1, off sc0 nt" : "=v"(v) : "v"(a) : "memory");
     return v;
 }
 

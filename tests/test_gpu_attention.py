@@ -173,7 +173,7 @@ def test_reference_scheduler_metadata(k, goldens):
     _check(got, want, c)
 
 
-@pytest.mark.parametrize("hnd,P", [(False, 16), (True, 64), (False, 1)])
+@pytest.mark.parametrize("hnd,P", [(False, 16), (True, 64), (False, 1), (True, 16), (True, 2), (True, 48)])
 def test_llama3_8b_decode(k, hnd, P):
     """32 query heads over 8 KV heads of 128 dims; 16 requests of up to
     1,500 tokens, one decode query each (length = the whole sequence)."""

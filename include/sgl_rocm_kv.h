@@ -92,6 +92,7 @@ typedef enum sgl_kv_status {
     SGL_KV_PLAN_UNALIGNED_TOKEN_OFFSET = 43,    /* a = request index, b = token_offset, c = page_size */
     SGL_KV_PLAN_UNALIGNED_CACHE_SLOT = 44,      /* a = request index, b = cache_slot, c = page_size */
     SGL_KV_PLAN_NON_CONTIGUOUS_CACHE_SLOTS = 45,/* a = request index, b = expected, c = actual */
+    SGL_KV_PLAN_NON_PREFILL_BATCH = 46,
 
     SGL_KV_DEVICE_PAGE_INDEX_OUT_OF_RANGE = 50, /* a page-table entry is negative, past the table or past the pool */
     SGL_KV_DEVICE_SPAN_OUT_OF_RANGE = 51,       /* a row is not covered by its span list */
@@ -113,6 +114,8 @@ typedef enum sgl_kv_status {
     SGL_KV_ALLOC_ZERO_SLOT_CAPACITY = 71,
     SGL_KV_ALLOC_SLOT_CAPACITY_NOT_PAGE_ALIGNED = 72, /* a = slot_capacity, b = page_size */
     SGL_KV_ALLOC_OUT_OF_SLOTS = 73,                   /* a = requested, b = available */
+    /* RadixCacheError (cache.rs:38-44) */
+    SGL_KV_RADIX_TOKEN_PAGE_LENGTH_MISMATCH = 74,     /* a = token_count, b = cache_page_count */
 
     /* 80.. mirror CudaBf16PagedAttentionError (crates/sglang-kernel/src/cuda_attention.rs:518-564)
      * and CudaPagedAttentionError's plan variants (crates/sglang-srt/src/cuda_attention.rs:15-75);
@@ -390,6 +393,75 @@ int32_t sgl_kv_page_allocator_release(sgl_kv_page_allocator *allocator, const ui
                                       uint64_t count);
 /* CachePageAllocator::reset (cache.rs:468-471). */
 int32_t sgl_kv_page_allocator_reset(sgl_kv_page_allocator *allocator);
+
+/* Token-prefix cache (RadixCache, crates/sglang-srt/src/cache.rs:475-547):
+ * a trie over token ids whose nodes remember the KV slot ("cache page") of
+ * their token. The scheduler matches a prompt against it before it
+ * allocates, and the matched token count becomes the transfer span's
+ * token_offset (only the uncached suffix moves). Not thread-safe (the
+ * reference takes &mut). */
+typedef struct sgl_kv_radix_cache sgl_kv_radix_cache;
+int32_t sgl_kv_radix_cache_new(sgl_kv_radix_cache **out);
+int32_t sgl_kv_radix_cache_destroy(sgl_kv_radix_cache *cache);
+/* RadixCache::clear (cache.rs:481-483). */
+int32_t sgl_kv_radix_cache_clear(sgl_kv_radix_cache *cache);
+/* RadixCache::insert (cache.rs:485-504): every node on the path of
+ * input_ids takes the matching cache page (an existing node's page is
+ * replaced). TokenPageLengthMismatch when the lengths differ. */
+int32_t sgl_kv_radix_cache_insert(sgl_kv_radix_cache *cache, const uint32_t *input_ids, uint64_t token_count,
+                                  const uint64_t *cache_pages, uint64_t cache_page_count);
+/* RadixCache::match_prefix (cache.rs:506-530), and with page_size > 0 its
+ * page-aligned form match_prefix_page_aligned (:532-540): the match rounded
+ * down to whole pages (page_size 0 is InvalidArgument; the reference
+ * asserts). *matched_token_count receives the matched length m; the first m
+ * entries of out_cache_pages (capacity token_count) its cache pages. The
+ * remaining input ids are input_ids[m..]. page_size 1 is the plain match. */
+int32_t sgl_kv_radix_cache_match_prefix(const sgl_kv_radix_cache *cache, const uint32_t *input_ids,
+                                        uint64_t token_count, uint64_t page_size, uint64_t *matched_token_count,
+                                        uint64_t *out_cache_pages);
+
+/* The transfer-plan fields of a prefill ModelWorkerBatch
+ * (crates/sglang-srt/src/model_executor.rs:15-198): per request, in batch
+ * order, the tokens this forward computes (input_token_counts, the
+ * uncached suffix), the tokens already cached (cached_token_counts, the
+ * forward prefix) and whether it carries disaggregated params (a PD
+ * request; the others have no span); out_cache_pages are the forward's
+ * cache slots, the requests' runs concatenated. */
+typedef enum sgl_kv_forward_mode { SGL_KV_FORWARD_PREFILL = 0, SGL_KV_FORWARD_DECODE = 1 } sgl_kv_forward_mode;
+typedef struct sgl_kv_prefill_batch {
+    int32_t forward_mode;                     /* sgl_kv_forward_mode */
+    uint64_t request_count;
+    const uint64_t *input_token_counts;       /* request_count entries */
+    const uint64_t *cached_token_counts;      /* request_count entries */
+    const uint8_t *has_disaggregated_params;  /* request_count entries, 0 or 1 */
+    const uint64_t *out_cache_pages;
+    uint64_t out_cache_page_count;
+} sgl_kv_prefill_batch;
+
+/* One KvCacheTransferSpan (transfer.rs:495-505) as offsets into the batch
+ * and the plan's page-index array. */
+typedef struct sgl_kv_plan_span {
+    uint64_t request_index;      /* the request's position in the batch */
+    uint64_t token_offset;       /* cached_token_counts[request_index] */
+    uint64_t token_count;        /* input_token_counts[request_index] */
+    uint64_t cache_page_offset;  /* its slots: out_cache_pages[cache_page_offset .. + token_count) */
+    uint64_t page_index_offset;  /* its pages: page_indices[page_index_offset .. + page_index_count) */
+    uint64_t page_index_count;
+} sgl_kv_plan_span;
+
+/* KvCacheTransferPlan::from_prefill_worker_batch_with_page_size
+ * (transfer.rs:604-668): one span per request with disaggregated params,
+ * errors in the reference's order (NonPrefillBatch, ZeroPageSize, then per
+ * request CachePageCountMismatch and the transfer_page_indices errors, then
+ * TrailingCachePages). `spans` needs one entry per PD request (request_count
+ * is always enough); `page_indices` one per page of their slots
+ * (out_cache_page_count / page_size + request_count is always enough);
+ * too little room is InvalidArgument, checked after the plan's own errors.
+ * On success *span_count and *page_index_count receive the counts. */
+int32_t sgl_kv_transfer_plan_from_prefill_batch(const sgl_kv_prefill_batch *batch, uint64_t page_size,
+                                                sgl_kv_plan_span *spans, uint64_t span_capacity,
+                                                uint64_t *page_indices, uint64_t page_index_capacity,
+                                                uint64_t *span_count, uint64_t *page_index_count);
 
 /* KvCacheTransferSpan::descriptor_checksum (transfer.rs:548-570): lowercase
  * hex SHA-256 of the span's identifying fields, as /poll_transfers reports

@@ -241,6 +241,73 @@ def transfer_page_indices(token_offset: int, cache_slots, page_size: int):
     return rc, out[: n.value].tolist()
 
 
+# --- scheduler-side plan metadata (pure Python restatement, small cases) ---------------------
+
+PLAN_ZERO_PAGE_SIZE = 40
+PLAN_CACHE_PAGE_COUNT_MISMATCH = 41
+PLAN_TRAILING_CACHE_PAGES = 42
+PLAN_NON_PREFILL_BATCH = 46
+
+
+class RadixCache:
+    """RadixCache (crates/sglang-srt/src/cache.rs:475-547) as nested dicts:
+    a node is [cache_page or None, {token: child}]. insert (:485-504) gives
+    every node on the path its token's page; match_prefix (:506-530) walks
+    while the next token has a node with a page; match_prefix_page_aligned
+    (:532-540) rounds the match down to whole pages."""
+
+    def __init__(self):
+        self.root = [None, {}]
+
+    def insert(self, input_ids, cache_pages):
+        assert len(input_ids) == len(cache_pages)
+        node = self.root
+        for tok, page in zip(input_ids, cache_pages):
+            node = node[1].setdefault(int(tok), [None, {}])
+            node[0] = int(page)
+
+    def match_prefix_page_aligned(self, input_ids, page_size: int):
+        """(matched_token_count, cache_pages, remaining_input_ids)."""
+        assert page_size > 0
+        node, pages = self.root, []
+        for tok in input_ids:
+            child = node[1].get(int(tok))
+            if child is None or child[0] is None:
+                break
+            pages.append(child[0])
+            node = child
+        m = len(pages) // page_size * page_size
+        return m, pages[:m], [int(t) for t in input_ids[m:]]
+
+
+def transfer_plan_from_prefill_batch(input_token_counts, cached_token_counts, has_params, out_cache_pages,
+                                     page_size: int, prefill: bool = True):
+    """KvCacheTransferPlan::from_prefill_worker_batch_with_page_size
+    (crates/sglang-srt/src/transfer.rs:604-668). Returns (0, spans) with a
+    span = (request_index, token_offset, token_count, cache_pages,
+    page_indices), or (code, None) with the error's status code."""
+    if not prefill:
+        return PLAN_NON_PREFILL_BATCH, None
+    if page_size == 0:
+        return PLAN_ZERO_PAGE_SIZE, None
+    spans, offset = [], 0
+    for r, count in enumerate(input_token_counts):
+        end = offset + int(count)
+        if end > len(out_cache_pages):
+            return PLAN_CACHE_PAGE_COUNT_MISMATCH, None
+        slots = [int(s) for s in out_cache_pages[offset:end]]
+        offset = end
+        if not has_params[r]:
+            continue
+        rc, pages = transfer_page_indices(int(cached_token_counts[r]), slots, page_size)
+        if rc:
+            return rc, None
+        spans.append((r, int(cached_token_counts[r]), int(count), slots, pages))
+    if offset != len(out_cache_pages):
+        return PLAN_TRAILING_CACHE_PAGES, None
+    return 0, spans
+
+
 def f32_to_bf16(values: np.ndarray) -> np.ndarray:
     v = np.ascontiguousarray(values, dtype=np.float32)
     out = np.empty(v.shape, dtype=np.uint16)

@@ -105,6 +105,7 @@ extern "C" const char *sgl_kv_status_name(int32_t code) {
     case SGL_KV_PLAN_UNALIGNED_TOKEN_OFFSET: return "UnalignedTokenOffset";
     case SGL_KV_PLAN_UNALIGNED_CACHE_SLOT: return "UnalignedCacheSlot";
     case SGL_KV_PLAN_NON_CONTIGUOUS_CACHE_SLOTS: return "NonContiguousCacheSlots";
+    case SGL_KV_PLAN_NON_PREFILL_BATCH: return "NonPrefillBatch";
     case SGL_KV_DEVICE_PAGE_INDEX_OUT_OF_RANGE: return "DevicePageIndexOutOfRange";
     case SGL_KV_DEVICE_SPAN_OUT_OF_RANGE: return "DeviceSpanOutOfRange";
     case SGL_KV_DEVICE_REQUEST_OUT_OF_RANGE: return "DeviceRequestOutOfRange";
@@ -121,6 +122,7 @@ extern "C" const char *sgl_kv_status_name(int32_t code) {
     case SGL_KV_ALLOC_ZERO_SLOT_CAPACITY: return "ZeroSlotCapacity";
     case SGL_KV_ALLOC_SLOT_CAPACITY_NOT_PAGE_ALIGNED: return "SlotCapacityNotPageAligned";
     case SGL_KV_ALLOC_OUT_OF_SLOTS: return "OutOfSlots";
+    case SGL_KV_RADIX_TOKEN_PAGE_LENGTH_MISMATCH: return "TokenPageLengthMismatch";
     default: return "Unknown";
     }
 }

@@ -1,12 +1,16 @@
 // kv_plan.cpp -- host mirror of the scheduler-side producers of the transfer
 // path's metadata: the KV page allocator that hands out slot indices
-// (CachePageAllocator, crates/sglang-srt/src/cache.rs:340-473) and the
-// transfer span's descriptor checksum (KvCacheTransferSpan::
-// descriptor_checksum, crates/sglang-srt/src/transfer.rs:548-570), with a
-// SHA-256 written from FIPS 180-4. No HIP calls.
+// (CachePageAllocator, crates/sglang-srt/src/cache.rs:340-473), the
+// token-prefix cache whose match sets a span's token offset (RadixCache,
+// cache.rs:475-547), the transfer plan of a prefill batch
+// (KvCacheTransferPlan::from_prefill_worker_batch_with_page_size,
+// crates/sglang-srt/src/transfer.rs:604-668) and the transfer span's
+// descriptor checksum (KvCacheTransferSpan::descriptor_checksum,
+// transfer.rs:548-570), with a SHA-256 written from FIPS 180-4. No HIP calls.
 #include <string.h>
 
 #include <deque>
+#include <unordered_map>
 #include <vector>
 
 #include "kv_internal.h"
@@ -137,6 +141,165 @@ extern "C" int32_t sgl_kv_page_allocator_release(sgl_kv_page_allocator *a, const
 extern "C" int32_t sgl_kv_page_allocator_reset(sgl_kv_page_allocator *a) {
     if (!a) return fail(SGL_KV_INVALID_ARGUMENT, "allocator", 0, 0, 0, "null allocator");
     a->reset();
+    return ok();
+}
+
+// --- token-prefix cache --------------------------------------------------------------------
+
+// RadixCache (cache.rs:475-547). Nodes live in one vector and name their
+// children by index; node 0 is the root, which carries no page.
+struct sgl_kv_radix_cache {
+    struct Node {
+        uint64_t page = 0;
+        bool has_page = false;  // Option<CachePageId>: every u64 is a valid page
+        std::unordered_map<uint32_t, uint32_t> children;
+    };
+    std::vector<Node> nodes;
+
+    sgl_kv_radix_cache() { clear(); }
+    void clear() {
+        nodes.clear();
+        nodes.emplace_back();
+    }
+};
+
+extern "C" int32_t sgl_kv_radix_cache_new(sgl_kv_radix_cache **out) {
+    if (!out) return fail(SGL_KV_INVALID_ARGUMENT, "out", 0, 0, 0, "null argument");
+    *out = new sgl_kv_radix_cache();
+    return ok();
+}
+
+extern "C" int32_t sgl_kv_radix_cache_destroy(sgl_kv_radix_cache *cache) {
+    delete cache;
+    return SGL_KV_OK;
+}
+
+extern "C" int32_t sgl_kv_radix_cache_clear(sgl_kv_radix_cache *cache) {
+    if (!cache) return fail(SGL_KV_INVALID_ARGUMENT, "cache", 0, 0, 0, "null cache");
+    cache->clear();
+    return ok();
+}
+
+// RadixCache::insert (cache.rs:485-504).
+extern "C" int32_t sgl_kv_radix_cache_insert(sgl_kv_radix_cache *cache, const uint32_t *input_ids,
+                                             uint64_t token_count, const uint64_t *cache_pages,
+                                             uint64_t cache_page_count) {
+    if (!cache) return fail(SGL_KV_INVALID_ARGUMENT, "cache", 0, 0, 0, "null cache");
+    if (token_count != cache_page_count)
+        return fail(SGL_KV_RADIX_TOKEN_PAGE_LENGTH_MISMATCH, nullptr, token_count, cache_page_count, 0,
+                    "token count (%llu) must match cache page count (%llu)", (unsigned long long)token_count,
+                    (unsigned long long)cache_page_count);
+    if (token_count && (!input_ids || !cache_pages))
+        return fail(SGL_KV_INVALID_ARGUMENT, "input_ids/cache_pages", 0, 0, 0, "null argument");
+    if (cache->nodes.size() + token_count > UINT32_MAX)
+        return too_large_dim("radix_cache_nodes", cache->nodes.size() + token_count, UINT32_MAX);
+    uint32_t node = 0;
+    for (uint64_t i = 0; i < token_count; ++i) {
+        auto it = cache->nodes[node].children.find(input_ids[i]);
+        uint32_t child;
+        if (it == cache->nodes[node].children.end()) {
+            child = static_cast<uint32_t>(cache->nodes.size());
+            cache->nodes[node].children.emplace(input_ids[i], child);
+            cache->nodes.emplace_back();  // may move the vector: index, not reference, above
+        } else {
+            child = it->second;
+        }
+        cache->nodes[child].page = cache_pages[i];
+        cache->nodes[child].has_page = true;
+        node = child;
+    }
+    return ok();
+}
+
+// RadixCache::match_prefix (cache.rs:506-530): follow the prompt down the
+// trie while the next token has a node and that node a page; with page_size
+// > 1, match_prefix_page_aligned (:532-540) keeps the whole pages of it.
+extern "C" int32_t sgl_kv_radix_cache_match_prefix(const sgl_kv_radix_cache *cache, const uint32_t *input_ids,
+                                                   uint64_t token_count, uint64_t page_size,
+                                                   uint64_t *matched_token_count, uint64_t *out_cache_pages) {
+    if (!cache || !matched_token_count)
+        return fail(SGL_KV_INVALID_ARGUMENT, "cache/matched_token_count", 0, 0, 0, "null argument");
+    *matched_token_count = 0;
+    if (page_size == 0)
+        return fail(SGL_KV_INVALID_ARGUMENT, "page_size", 0, 0, 0, "KV cache page size must be non-zero");
+    if (token_count && (!input_ids || !out_cache_pages))
+        return fail(SGL_KV_INVALID_ARGUMENT, "input_ids/out_cache_pages", 0, 0, 0, "null argument");
+    uint64_t m = 0;
+    uint32_t node = 0;
+    while (m < token_count) {
+        const auto &children = cache->nodes[node].children;
+        auto it = children.find(input_ids[m]);
+        if (it == children.end()) break;
+        const auto &child = cache->nodes[it->second];
+        if (!child.has_page) break;
+        out_cache_pages[m++] = child.page;
+        node = it->second;
+    }
+    *matched_token_count = m / page_size * page_size;
+    return ok();
+}
+
+// --- transfer plan from a prefill batch ----------------------------------------------------
+
+// KvCacheTransferPlan::from_prefill_worker_batch_with_page_size
+// (transfer.rs:604-668) over the batch's plan fields; each span's page
+// indices come from transfer_page_indices (:679-720).
+extern "C" int32_t sgl_kv_transfer_plan_from_prefill_batch(const sgl_kv_prefill_batch *batch,
+                                                           uint64_t page_size, sgl_kv_plan_span *spans,
+                                                           uint64_t span_capacity, uint64_t *page_indices,
+                                                           uint64_t page_index_capacity, uint64_t *span_count,
+                                                           uint64_t *page_index_count) {
+    if (!batch || !span_count || !page_index_count)
+        return fail(SGL_KV_INVALID_ARGUMENT, "batch/span_count/page_index_count", 0, 0, 0, "null argument");
+    *span_count = *page_index_count = 0;
+    if (batch->forward_mode != SGL_KV_FORWARD_PREFILL)
+        return fail(SGL_KV_PLAN_NON_PREFILL_BATCH, nullptr, 0, 0, 0, "KV transfer plan requires prefill batch");
+    if (page_size == 0)
+        return fail(SGL_KV_PLAN_ZERO_PAGE_SIZE, nullptr, 0, 0, 0, "KV transfer page size must be non-zero");
+    const uint64_t n = batch->request_count;
+    if (n && (!batch->input_token_counts || !batch->cached_token_counts || !batch->has_disaggregated_params))
+        return fail(SGL_KV_INVALID_ARGUMENT, "batch", 0, 0, 0, "null per-request array");
+    if (batch->out_cache_page_count && !batch->out_cache_pages)
+        return fail(SGL_KV_INVALID_ARGUMENT, "out_cache_pages", 0, 0, 0, "null argument");
+    std::vector<sgl_kv_plan_span> out;
+    std::vector<uint64_t> pages;
+    uint64_t offset = 0;  // the next request's first cache page
+    for (uint64_t r = 0; r < n; ++r) {
+        const uint64_t count = batch->input_token_counts[r];
+        const uint64_t left = batch->out_cache_page_count - offset;
+        if (count > left)
+            return fail(SGL_KV_PLAN_CACHE_PAGE_COUNT_MISMATCH, nullptr, r, count, left,
+                        "request %llu has %llu input tokens but %llu cache pages available",
+                        (unsigned long long)r, (unsigned long long)count, (unsigned long long)left);
+        const uint64_t first = offset;
+        offset += count;
+        if (!batch->has_disaggregated_params[r]) continue;
+        const uint64_t token_offset = batch->cached_token_counts[r];
+        const uint64_t at = pages.size();
+        pages.resize(at + count / page_size + (count % page_size ? 1 : 0));
+        uint64_t got = 0;
+        const int32_t rc = sgl_kv_transfer_page_indices(r, token_offset, batch->out_cache_pages + first, count,
+                                                        page_size, pages.data() + at, &got);
+        if (rc) return rc;
+        pages.resize(at + got);
+        out.push_back(sgl_kv_plan_span{r, token_offset, count, first, at, got});
+    }
+    if (offset != batch->out_cache_page_count)
+        return fail(SGL_KV_PLAN_TRAILING_CACHE_PAGES, nullptr, offset, batch->out_cache_page_count, 0,
+                    "KV transfer plan consumed %llu cache pages but batch has %llu",
+                    (unsigned long long)offset, (unsigned long long)batch->out_cache_page_count);
+    if (out.size() > span_capacity || (out.size() && !spans))
+        return fail(SGL_KV_INVALID_ARGUMENT, "span_capacity", span_capacity, out.size(), 0,
+                    "%llu span entries for %llu spans", (unsigned long long)span_capacity,
+                    (unsigned long long)out.size());
+    if (pages.size() > page_index_capacity || (pages.size() && !page_indices))
+        return fail(SGL_KV_INVALID_ARGUMENT, "page_index_capacity", page_index_capacity, pages.size(), 0,
+                    "%llu page-index entries for %llu pages", (unsigned long long)page_index_capacity,
+                    (unsigned long long)pages.size());
+    if (!out.empty()) memcpy(spans, out.data(), out.size() * sizeof(sgl_kv_plan_span));
+    if (!pages.empty()) memcpy(page_indices, pages.data(), pages.size() * sizeof(uint64_t));
+    *span_count = out.size();
+    *page_index_count = pages.size();
     return ok();
 }
 

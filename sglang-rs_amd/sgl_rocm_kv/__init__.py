@@ -67,6 +67,11 @@ PLAN_ZERO_PAGE_SIZE = 40
 PLAN_UNALIGNED_TOKEN_OFFSET = 43
 PLAN_UNALIGNED_CACHE_SLOT = 44
 PLAN_NON_CONTIGUOUS_CACHE_SLOTS = 45
+PLAN_NON_PREFILL_BATCH = 46
+PLAN_CACHE_PAGE_COUNT_MISMATCH = 41
+PLAN_TRAILING_CACHE_PAGES = 42
+RADIX_TOKEN_PAGE_LENGTH_MISMATCH = 74
+FORWARD_PREFILL, FORWARD_DECODE = 0, 1
 DEVICE_PAGE_INDEX_OUT_OF_RANGE = 50
 DEVICE_SPAN_OUT_OF_RANGE = 51
 DEVICE_REQUEST_OUT_OF_RANGE = 52
@@ -277,6 +282,22 @@ class _AttentionBuffers(ctypes.Structure):
 PAGE_REQUEST_DTYPE = np.dtype([("source", "<u8"), ("target_offset", "<u8"), ("length", "<u8")])
 
 
+# sgl_kv_plan_span: one KvCacheTransferSpan as offsets into the batch and
+# the plan's page-index array.
+PLAN_SPAN_DTYPE = np.dtype([("request_index", "<u8"), ("token_offset", "<u8"), ("token_count", "<u8"),
+                            ("cache_page_offset", "<u8"), ("page_index_offset", "<u8"),
+                            ("page_index_count", "<u8")])
+
+
+class _PrefillBatch(ctypes.Structure):
+    _fields_ = [("forward_mode", ctypes.c_int32), ("request_count", ctypes.c_uint64),
+                ("input_token_counts", ctypes.POINTER(ctypes.c_uint64)),
+                ("cached_token_counts", ctypes.POINTER(ctypes.c_uint64)),
+                ("has_disaggregated_params", ctypes.POINTER(ctypes.c_uint8)),
+                ("out_cache_pages", ctypes.POINTER(ctypes.c_uint64)),
+                ("out_cache_page_count", ctypes.c_uint64)]
+
+
 SPAN_DTYPE = np.dtype([("row_start", "<u4"), ("token_offset", "<u4"), ("token_count", "<u4"),
                        ("page_table_start", "<u4")])
 
@@ -339,6 +360,17 @@ _EXPORTS = {
         ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_u64), _u64, _u64, ctypes.POINTER(_u64)]),
     "sgl_kv_page_allocator_release": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_u64), _u64]),
     "sgl_kv_page_allocator_reset": (ctypes.c_int32, [ctypes.c_void_p]),
+    "sgl_kv_radix_cache_new": (ctypes.c_int32, [ctypes.POINTER(ctypes.c_void_p)]),
+    "sgl_kv_radix_cache_destroy": (ctypes.c_int32, [ctypes.c_void_p]),
+    "sgl_kv_radix_cache_clear": (ctypes.c_int32, [ctypes.c_void_p]),
+    "sgl_kv_radix_cache_insert": (
+        ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint32), _u64, ctypes.POINTER(_u64), _u64]),
+    "sgl_kv_radix_cache_match_prefix": (
+        ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint32), _u64, _u64, ctypes.POINTER(_u64),
+                         ctypes.POINTER(_u64)]),
+    "sgl_kv_transfer_plan_from_prefill_batch": (
+        ctypes.c_int32, [ctypes.POINTER(_PrefillBatch), _u64, ctypes.c_void_p, _u64, ctypes.POINTER(_u64), _u64,
+                         ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
     "sgl_kv_transfer_span_checksum": (
         ctypes.c_int32, [ctypes.c_char_p, _u64, ctypes.c_char_p, _u64, ctypes.c_uint16, _u64,
                          ctypes.c_int32, _u64, _u64, _u64, ctypes.POINTER(_u64), _u64,
@@ -829,6 +861,92 @@ class CachePageAllocator:
                 self._h = None
         except Exception:
             pass
+
+
+@dataclass
+class PrefixMatch:
+    """PrefixMatch (cache.rs:31-36)."""
+    matched_token_count: int
+    cache_pages: list
+    remaining_input_ids: list
+
+
+def _u32_array(values) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(values, dtype=np.uint32))
+
+
+class RadixCache:
+    """RadixCache (crates/sglang-srt/src/cache.rs:475-547): token ids -> KV
+    slots of a cached prompt prefix."""
+
+    def __init__(self):
+        h = ctypes.c_void_p()
+        _call(lib().sgl_kv_radix_cache_new, ctypes.byref(h))
+        self._h = h.value
+
+    def clear(self):
+        _call(lib().sgl_kv_radix_cache_clear, self._h)
+
+    def insert(self, input_ids, cache_pages):
+        ids, pages = _u32_array(input_ids), _u64_array(cache_pages)
+        _call(lib().sgl_kv_radix_cache_insert, self._h,
+              ids.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), len(ids), _pu64(pages), len(pages))
+
+    def match_prefix_page_aligned(self, input_ids, page_size: int) -> PrefixMatch:
+        ids = _u32_array(input_ids)
+        out = np.zeros(max(1, len(ids)), dtype=np.uint64)
+        m = _u64()
+        _call(lib().sgl_kv_radix_cache_match_prefix, self._h,
+              ids.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), len(ids), page_size, ctypes.byref(m),
+              _pu64(out))
+        n = m.value
+        return PrefixMatch(n, out[:n].tolist(), ids[n:].tolist())
+
+    def match_prefix(self, input_ids) -> PrefixMatch:
+        return self.match_prefix_page_aligned(input_ids, 1)
+
+    def __del__(self):
+        try:
+            if self._h:
+                lib().sgl_kv_radix_cache_destroy(self._h)
+                self._h = None
+        except Exception:
+            pass
+
+
+@dataclass
+class PlanSpan:
+    """One span of KvCacheTransferPlan (transfer.rs:495-505) by request index."""
+    request_index: int
+    token_offset: int
+    token_count: int
+    cache_pages: list
+    page_indices: list
+
+
+def transfer_plan_from_prefill_batch(input_token_counts, cached_token_counts, has_disaggregated_params,
+                                     out_cache_pages, page_size: int = 1,
+                                     forward_mode: int = FORWARD_PREFILL) -> list:
+    """KvCacheTransferPlan::from_prefill_worker_batch_with_page_size
+    (transfer.rs:604-668) over a prefill batch's per-request token counts,
+    PD flags and concatenated cache slots: the spans, in batch order."""
+    inp, cached = _u64_array(input_token_counts), _u64_array(cached_token_counts)
+    pd = np.ascontiguousarray(np.asarray(has_disaggregated_params, dtype=np.uint8))
+    pages = _u64_array(out_cache_pages)
+    b = _PrefillBatch(forward_mode, len(inp), _pu64(inp), _pu64(cached),
+                      pd.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)), _pu64(pages), len(pages))
+    spans = np.zeros(max(1, len(inp)), dtype=PLAN_SPAN_DTYPE)
+    idx = np.zeros(max(1, len(pages) // max(page_size, 1) + len(inp)), dtype=np.uint64)
+    ns, ni = _u64(), _u64()
+    _call(lib().sgl_kv_transfer_plan_from_prefill_batch, ctypes.byref(b), page_size, spans.ctypes.data,
+          len(spans), _pu64(idx), len(idx), ctypes.byref(ns), ctypes.byref(ni))
+    out = []
+    for sp in spans[: ns.value]:
+        c0, p0 = int(sp["cache_page_offset"]), int(sp["page_index_offset"])
+        out.append(PlanSpan(int(sp["request_index"]), int(sp["token_offset"]), int(sp["token_count"]),
+                            pages[c0:c0 + int(sp["token_count"])].tolist(),
+                            idx[p0:p0 + int(sp["page_index_count"])].tolist()))
+    return out
 
 
 def transfer_span_checksum(request_id: str, bootstrap_host: str, bootstrap_port: int,

@@ -176,6 +176,68 @@ int main() {
     for (size_t n = 0; n < blob.size(); n += 1 + rng() % 97)
         CHECK(sgl_kv_sha256_hex(blob.data(), n, hex) == SGL_KV_OK && strlen(hex) == 64);
 
+    // The token-prefix cache under random inserts and matches: a match never
+    // exceeds the query, is a multiple of the page size, and reports pages
+    // for exactly the matched tokens (the rest of out_pages is untouched).
+    {
+        sgl_kv_radix_cache *c = nullptr;
+        CHECK(sgl_kv_radix_cache_new(&c) == SGL_KV_OK);
+        for (int it = 0; it < 3000; ++it) {
+            const uint64_t n = rng() % 24;
+            std::vector<uint32_t> toks(n);
+            std::vector<uint64_t> pages(n);
+            for (uint64_t i = 0; i < n; ++i) {
+                toks[i] = (uint32_t)(rng() % 3);
+                pages[i] = pick(rng);
+            }
+            if (rng() % 3 == 0) {
+                CHECK(sgl_kv_radix_cache_insert(c, toks.data(), n, pages.data(), n) == SGL_KV_OK);
+                if (n) CHECK(sgl_kv_radix_cache_insert(c, toks.data(), n, pages.data(), n - 1) ==
+                             SGL_KV_RADIX_TOKEN_PAGE_LENGTH_MISMATCH);
+            } else {
+                const uint64_t P = rng() % 5;
+                std::vector<uint64_t> out(n + 1, 0xA5A5A5A5A5A5A5A5ull);
+                uint64_t m = UINT64_MAX;
+                const int32_t rc = sgl_kv_radix_cache_match_prefix(c, toks.data(), n, P, &m, out.data());
+                if (P == 0) {
+                    CHECK(rc == SGL_KV_INVALID_ARGUMENT && m == 0);
+                } else {
+                    CHECK(rc == SGL_KV_OK && m <= n && m % P == 0);
+                    CHECK(out[n] == 0xA5A5A5A5A5A5A5A5ull);
+                }
+            }
+            if (rng() % 500 == 0) CHECK(sgl_kv_radix_cache_clear(c) == SGL_KV_OK);
+        }
+        sgl_kv_radix_cache_destroy(c);
+    }
+    // The prefill-batch plan on random (mostly malformed) batches: it returns
+    // a status and never writes past the capacities it was given.
+    for (int it = 0; it < 3000; ++it) {
+        const uint64_t reqs = rng() % 6, P = rng() % 5;
+        std::vector<uint64_t> inputs(reqs), cached(reqs);
+        std::vector<uint8_t> pd(reqs);
+        uint64_t total = 0;
+        for (uint64_t r = 0; r < reqs; ++r) {
+            inputs[r] = rng() % 3 == 0 ? pick(rng) : rng() % 9;
+            cached[r] = rng() % 2 ? (P ? P * (rng() % 3) : 0) : pick(rng);
+            pd[r] = (uint8_t)(rng() % 2);
+            if (inputs[r] < 64) total += inputs[r];
+        }
+        std::vector<uint64_t> slots(total + rng() % 3);
+        for (uint64_t i = 0; i < slots.size(); ++i) slots[i] = rng() % 2 ? i : pick(rng);
+        sgl_kv_prefill_batch b = {(int32_t)(rng() % 4 == 0), reqs, inputs.data(), cached.data(),
+                                  pd.data(), slots.data(), slots.size()};
+        const uint64_t span_cap = rng() % (reqs + 2), page_cap = rng() % (slots.size() + 3);
+        std::vector<sgl_kv_plan_span> spans(span_cap + 1);
+        std::vector<uint64_t> idx(page_cap + 1, 77);
+        spans[span_cap].request_index = 99;
+        uint64_t ns = 5, ni = 5;
+        const int32_t rc = sgl_kv_transfer_plan_from_prefill_batch(&b, P, spans.data(), span_cap, idx.data(),
+                                                                   page_cap, &ns, &ni);
+        CHECK(rc == SGL_KV_OK ? ns <= span_cap && ni <= page_cap : ns == 0 && ni == 0);
+        CHECK(spans[span_cap].request_index == 99 && idx[page_cap] == 77);
+    }
+
     if (failures) {
         fprintf(stderr, "%d checks failed\n", failures);
         return 1;

@@ -345,6 +345,66 @@ def test_bootstrap_frames_drive_the_backend(k, mode):
 
 
 @pytest.mark.parametrize("mode", [kv.BACKEND_DIRECT, kv.BACKEND_STAGED])
+def test_prefill_batch_plan_drives_the_backend(k, mode):
+    """The scheduler's route to the backend: prompts are matched against the
+    prefill side's token-prefix cache (RadixCache::match_prefix_page_aligned,
+    cache.rs:532-540), the uncached suffixes get slots from the page
+    allocator, the batch's plan (from_prefill_worker_batch_with_page_size,
+    transfer.rs:604-668) yields one span per PD request with its cached
+    prefix as the token offset, and each span goes to the backend under its
+    own decode page table. Requests without disaggregated params get no span
+    but still own slots in the batch. Every decode-pool byte matches the
+    oracle, and each event carries the checksum of its span's fields."""
+    rng = np.random.default_rng(400 + mode)
+    pools = _Pools(seed=40 + mode)
+    alloc = kv.CachePageAllocator(PREFILL_PAGES * P_PREFILL, P_PREFILL)
+    cache = kv.RadixCache()
+    # Two cached prompts: 48 and 21 tokens already in the prefill pool.
+    shared_a = [int(t) for t in rng.integers(0, 1000, 48)]
+    shared_b = [int(t) for t in rng.integers(1000, 2000, 21)]
+    for toks in (shared_a, shared_b):
+        cache.insert(toks, alloc.allocate(len(toks)))
+    prompts = [shared_a + [int(t) for t in rng.integers(0, 5000, 70)],   # 48 cached, 70 move
+               [int(t) for t in rng.integers(5000, 6000, 33)],           # nothing cached
+               shared_b[:9] + [int(t) for t in rng.integers(0, 5000, 5)],  # 9 cached, no params
+               shared_b + [int(t) for t in rng.integers(0, 5000, 200)],  # 21 cached, 200 move
+               shared_a[:16]]                                            # fully cached: nothing moves
+    has_params = [1, 1, 0, 1, 1]
+    cached, inputs, slots = [], [], []
+    for p in prompts:
+        m = cache.match_prefix_page_aligned(p, P_PREFILL)
+        cached.append(m.matched_token_count)
+        inputs.append(len(m.remaining_input_ids))
+        slots += alloc.allocate(len(m.remaining_input_ids))
+    assert cached == [48, 0, 9, 21, 16] and inputs == [70, 33, 5, 200, 0]
+    spans = kv.transfer_plan_from_prefill_batch(inputs, cached, has_params, slots, P_PREFILL)
+    assert [s.request_index for s in spans] == [0, 1, 3, 4]
+    _say(f"batch plan: {len(spans)} spans, {sum(s.token_count for s in spans)} tokens over {L} layers "
+         f"({'direct' if mode == kv.BACKEND_DIRECT else 'staged'})")
+    b = kv.RocmKvTransferBackend(k, mode, max_rows=256)
+    pools.register(b)
+    groups = rng.permutation(DECODE_PAGES).reshape(8, -1)
+    sums = {}
+    for i, s in enumerate(spans):
+        room = 60 + s.request_index
+        need = -(-(s.token_offset + s.token_count) // P_DECODE)
+        table = rng.choice(groups[i], size=need, replace=False).astype(np.int32)
+        sums[room] = kv.transfer_span_checksum(f"req-{room}", "10.0.0.8", 8200, room, 0, s.token_offset,
+                                               s.token_count, P_PREFILL, s.cache_pages, s.page_indices)
+        cache_slots = np.asarray(s.cache_pages, dtype=np.uint64)
+        b.submit(room, sums[room], s.token_offset, cache_slots, table)
+        if s.token_count:
+            pools.expect(s.token_offset, cache_slots, table)
+    b.wait()
+    events, pending = b.poll()
+    assert pending == 0 and [e.bootstrap_room for e in events] == sorted(sums)
+    for e in events:
+        assert e.status == kv.TRANSFER_COMPLETED and e.descriptor_checksum == sums[e.bootstrap_room]
+    pools.check()
+    b.close()
+
+
+@pytest.mark.parametrize("mode", [kv.BACKEND_DIRECT, kv.BACKEND_STAGED])
 def test_device_table_failure_fails_only_its_span(k, mode):
     """Two spans resolved on the device from device-resident decode page
     tables. One table holds a page past the decode pool: the resolve kernel

@@ -241,7 +241,7 @@ def _random_realign_case(rng):
     return T, H, w, rows, specs, strides
 
 
-@pytest.mark.parametrize("seed", range(16))
+@pytest.mark.parametrize("seed", range(48))
 def test_random_unequal_and_odd_widths(k, seed):
     """Random pair widths (unequal), odd widths and strides, HND chunks of
     odd size, page sizes 1-64: pack, unpack and pool to pool on one layer of

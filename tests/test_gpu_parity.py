@@ -634,7 +634,7 @@ def _random_case(rng):
     return shape, src, dst, ss, ds, rows, rb + extra
 
 
-@pytest.mark.parametrize("seed", range(24))
+@pytest.mark.parametrize("seed", range(64))
 def test_random_shapes_pack_unpack_transfer(k, seed):
     """Random T, heads, dim, element size, page sizes, NHD/HND on either
     side, row strides and row counts: pack, unpack and pool-to-pool against

@@ -160,6 +160,43 @@ def test_backend_poll_capacity_and_cancel(k):
     b.close()
 
 
+def test_backend_spans_in_flight_limit(k):
+    """Each span in flight holds one of the backend's 1,024 error words. The
+    1,025th unpolled span is refused on the host with a typed error and
+    nothing is enqueued for it; once poll has reported the finished spans,
+    their words are free and a new span moves and completes."""
+    rng = np.random.default_rng(6)
+    pools = _Pools(seed=9)
+    b = kv.RocmKvTransferBackend(k, kv.BACKEND_DIRECT, max_rows=16)
+    pools.register(b)
+    pages = rng.permutation(DECODE_PAGES)
+    _say("backend: 1,024 one-token spans in flight, then one more")
+    for i in range(1024):
+        table = [int(pages[i % DECODE_PAGES])]
+        slot = np.array([rng.integers(0, PREFILL_PAGES)], dtype=np.uint64)
+        b.submit(1000 + i, f"{i:064x}", i % P_DECODE, slot, table)
+        pools.expect(i % P_DECODE, slot, table)
+    with pytest.raises(kv.KvError) as e:
+        b.submit(5000, "0" * 64, 0, np.array([1], dtype=np.uint64), [0])
+    assert e.value.variant == "DimensionTooLarge" and e.value.name == "spans in flight"
+    b.wait()
+    events, pending = [], 1
+    while pending:
+        got, pending = b.poll(capacity=300)
+        events += got
+    assert [e.bootstrap_room for e in events] == [1000 + i for i in range(1024)]
+    assert all(e.status == kv.TRANSFER_COMPLETED for e in events)
+    slot = np.array([7], dtype=np.uint64)
+    table = [int(pages[-1])]
+    b.submit(5001, "1" * 64, 3, slot, table)
+    pools.expect(3, slot, table)
+    b.wait()
+    [done], pending = b.poll()
+    assert done.bootstrap_room == 5001 and done.status == kv.TRANSFER_COMPLETED and pending == 0
+    pools.check()
+    b.close()
+
+
 def test_backend_staged_spans_reuse_staging_in_order(k):
     """Staged spans share one set of staging buffers: many back-to-back
     submissions must each complete intact."""

@@ -150,7 +150,20 @@ typedef enum sgl_kv_status {
     SGL_KV_MODEL_INVALID_PACKED_MLA_NOPE_HEAD_DIM = 101, /* a = qk_nope_head_dim */
     SGL_KV_MODEL_ZERO_TENSOR_WIDTH = 102,
     SGL_KV_MODEL_SIZE_OVERFLOW = 103,
-    SGL_KV_MODEL_MISSING_CAPABILITY = 104       /* the message names the capability; a, b = values */
+    SGL_KV_MODEL_MISSING_CAPABILITY = 104,      /* the message names the capability; a, b = values */
+
+    /* 110.. mirror CudaKvStorageError (crates/sglang-srt/src/cuda_kv_cache.rs:20-40),
+     * KvCachePoolError (crates/sglang-srt/src/kv_cache.rs:830-833), CudaError::ZeroAllocation
+     * (crates/sglang-kernel/src/cuda.rs:121, 477-480) and MooncakeError::UnsupportedMemoryLocation
+     * (crates/sglang-srt/src/transfer.rs:1662-1676). Layout errors of the storage calls keep
+     * their codes 20..36, device copies 7, 9 and 11. */
+    SGL_KV_STORAGE_SIZE_MISMATCH = 110,         /* name = "storage" or "pool", a = expected, b = actual bytes */
+    SGL_KV_STORAGE_SLOT_MAP_CAPACITY_MISMATCH = 111, /* a = map_slot_count, b = layout_slot_count */
+    SGL_KV_STORAGE_PAGE_BUFFER_SIZE_MISMATCH = 112,  /* a = expected, b = actual bytes */
+    SGL_KV_STORAGE_SIZE_OVERFLOW = 113,
+    SGL_KV_ZERO_ALLOCATION = 114,
+    SGL_KV_UNSUPPORTED_MEMORY_LOCATION = 115,   /* a = sgl_kv_memory_location_kind, b = id */
+    SGL_KV_STORAGE_DESCRIPTOR = 116             /* name = what is wrong, a, b = values */
 } sgl_kv_status;
 
 /* Detail of the calling thread's most recent failure. */
@@ -1168,6 +1181,197 @@ int32_t sgl_rocm_kv_backend_wait(sgl_rocm_kv_backend *backend);
 /* Drains, releases every transfer and the staging, and forgets the pools. */
 int32_t sgl_rocm_kv_backend_shutdown(sgl_rocm_kv_backend *backend);
 int32_t sgl_rocm_kv_backend_destroy(sgl_rocm_kv_backend *backend);
+
+/* ---- KV storage: the pool's device memory (CudaKvStorage, crates/sglang-srt/src/cuda_kv_cache.rs:170-509) ----
+ * One library-owned device allocation holding a paged pool (page -> layer ->
+ * tensor -> token, PagedKvCacheLayout), zero-filled at allocation like
+ * CudaKvStorage::allocate (:177-189) and freed by sgl_rocm_kv_storage_destroy
+ * (the reference frees on Drop, crates/sglang-kernel/src/cuda.rs:693-708). A
+ * storage records the device of the context that allocated it and does not
+ * keep the context. Every call that takes a layout first checks it against
+ * the storage (validate_layout, :391-405): StorageSizeMismatch unless
+ * byte_len == layout.total_byte_len, then PageBufferSizeMismatch unless the
+ * storage's page_size_bytes == layout.runtime.page_size_bytes. Writes to one
+ * storage must not overlap other calls on it (the reference takes &mut self). */
+typedef struct sgl_rocm_kv_storage sgl_rocm_kv_storage;
+/* CudaKvCacheSlotMap (:109-140): a validated slot list uploaded as u64. */
+typedef struct sgl_rocm_kv_slot_map sgl_rocm_kv_slot_map;
+
+/* CudaContext::memory_info (crates/sglang-kernel/src/cuda.rs:496-511):
+ * hipMemGetInfo on the context's device. */
+int32_t sgl_rocm_kv_memory_info(const sgl_rocm_kv_ctx *ctx, uint64_t *free_bytes, uint64_t *total_bytes);
+/* CudaKvStorage::allocate (cuda_kv_cache.rs:177-189): byte_len bytes on the
+ * context's device, every byte zero when the call returns. byte_len 0 is
+ * ZeroAllocation (CudaContext::allocate, cuda.rs:477-480). page_size_bytes
+ * is recorded for validate_layout and the memory descriptor. */
+int32_t sgl_rocm_kv_storage_allocate(sgl_rocm_kv_ctx *ctx, uint64_t byte_len, uint64_t page_size_bytes,
+                                     sgl_rocm_kv_storage **out);
+/* allocate_cuda_kv_cache (cuda_kv_cache.rs:478-490): PagedKvCacheLayout::new
+ * (runtime, page_count), then a zero-filled storage of its total_byte_len and
+ * page_size_bytes; *layout receives the pool's layout (KvCachePool::layout). */
+int32_t sgl_rocm_kv_cache_allocate(sgl_rocm_kv_ctx *ctx, const sgl_kv_runtime_layout *runtime,
+                                   uint64_t page_count, sgl_kv_paged_layout *layout,
+                                   sgl_rocm_kv_storage **out);
+/* The same for a layout built elsewhere (a tensor pair from
+ * sgl_kv_paged_layout_new_with_tensor_pair or sgl_kv_paged_layout_for_model):
+ * CudaKvStorage::allocate of layout->total_byte_len, then KvCachePool::new's
+ * size check (kv_cache.rs:849-856). */
+int32_t sgl_rocm_kv_pool_allocate(sgl_rocm_kv_ctx *ctx, const sgl_kv_paged_layout *layout,
+                                  sgl_rocm_kv_storage **out);
+/* Frees the allocation; NULL is accepted. Slot maps uploaded through the
+ * storage stay valid (they own their memory). */
+int32_t sgl_rocm_kv_storage_destroy(sgl_rocm_kv_storage *storage);
+/* CudaKvStorage::allocation (:191-197): device pointer and byte length, the
+ * `pool` buffer of every copy entry point. */
+int32_t sgl_rocm_kv_storage_allocation(const sgl_rocm_kv_storage *storage, sgl_kv_device_buffer *out);
+/* KvCacheStorage::byte_len (kv_cache.rs:825-828; impl :444-447); 0 for NULL. */
+uint64_t sgl_rocm_kv_storage_byte_len(const sgl_rocm_kv_storage *storage);
+/* The page size the storage was allocated for; 0 for NULL. */
+uint64_t sgl_rocm_kv_storage_page_size_bytes(const sgl_rocm_kv_storage *storage);
+/* The storage's device ordinal (CudaDeviceAllocation::device_ordinal); -1 for NULL. */
+int32_t sgl_rocm_kv_storage_device(const sgl_rocm_kv_storage *storage);
+/* KvCacheStorage::clear (impl :449-452, allocation.fill(0)): every byte zero
+ * when the call returns. */
+int32_t sgl_rocm_kv_storage_clear(sgl_rocm_kv_storage *storage);
+/* CudaKvStorage::validate_layout (:391-405). */
+int32_t sgl_rocm_kv_storage_validate_layout(const sgl_rocm_kv_storage *storage,
+                                            const sgl_kv_paged_layout *layout);
+/* CudaKvStorage::write_page / read_page (:224-256): one whole page between
+ * host memory and the pool. `len` must equal layout.runtime.page_size_bytes
+ * (PageBufferSizeMismatch), the page must exist (PageOutOfRange). Both return
+ * when the copy is complete. */
+int32_t sgl_rocm_kv_storage_write_page(sgl_rocm_kv_storage *storage, const sgl_kv_paged_layout *layout,
+                                       uint64_t page_index, const void *bytes, uint64_t len);
+int32_t sgl_rocm_kv_storage_read_page(const sgl_rocm_kv_storage *storage, const sgl_kv_paged_layout *layout,
+                                      uint64_t page_index, void *bytes, uint64_t len);
+/* CudaKvStorage::write_tensor_slot_from_device / read_tensor_slot_to_device
+ * (:258-294): one (layer, tensor, slot)'s bytes (tensor_slot_byte_range)
+ * device to device. The other buffer must be on the storage's device
+ * (DeviceMismatch, CudaDeviceAllocation::copy_from_device, cuda.rs:827-857)
+ * and hold the range (AllocationOutOfBounds). Asynchronous on `stream`;
+ * sgl_rocm_kv_write_tensor_slots is the batched form. */
+int32_t sgl_rocm_kv_storage_write_tensor_slot(sgl_rocm_kv_storage *storage, const sgl_kv_paged_layout *layout,
+                                              uint64_t layer, uint64_t tensor, uint64_t slot,
+                                              const sgl_kv_device_buffer *source, uint64_t source_offset,
+                                              void *stream);
+int32_t sgl_rocm_kv_storage_read_tensor_slot(const sgl_rocm_kv_storage *storage, const sgl_kv_paged_layout *layout,
+                                             uint64_t layer, uint64_t tensor, uint64_t slot,
+                                             const sgl_kv_device_buffer *destination,
+                                             uint64_t destination_offset, void *stream);
+
+/* CudaKvCacheTensorLocation (:103-107). */
+typedef struct sgl_kv_tensor_location {
+    uint64_t device_ptr;
+    uint64_t byte_offset;
+    uint64_t byte_len;
+} sgl_kv_tensor_location;
+/* CudaKvStorage::tensor_location / slot_location (:376-403): the byte range
+ * of tensor_token_byte_range / tensor_slot_byte_range and its device address. */
+int32_t sgl_rocm_kv_storage_tensor_location(const sgl_rocm_kv_storage *storage,
+                                            const sgl_kv_paged_layout *layout, uint64_t page_index,
+                                            uint64_t layer, uint64_t tensor, uint64_t token,
+                                            sgl_kv_tensor_location *out);
+int32_t sgl_rocm_kv_storage_slot_location(const sgl_rocm_kv_storage *storage,
+                                          const sgl_kv_paged_layout *layout, uint64_t layer,
+                                          uint64_t tensor, uint64_t slot, sgl_kv_tensor_location *out);
+
+/* CudaKvStorage::upload_slot_map (:199-222): validate_layout, then the
+ * slots against the layout (validate_slot_indices: EmptySlotMap,
+ * BatchSlotOutOfRange), then a new device array of slot_len u64 slots. The
+ * map remembers the host slots and the layout's slot_count. */
+int32_t sgl_rocm_kv_storage_upload_slot_map(const sgl_rocm_kv_storage *storage,
+                                            const sgl_kv_paged_layout *layout, const uint64_t *slots,
+                                            uint64_t slot_len, sgl_rocm_kv_slot_map **out);
+int32_t sgl_rocm_kv_slot_map_destroy(sgl_rocm_kv_slot_map *map);
+/* CudaKvCacheSlotMap::allocation / len / slots (:126-140). */
+int32_t sgl_rocm_kv_slot_map_allocation(const sgl_rocm_kv_slot_map *map, sgl_kv_device_buffer *out);
+uint64_t sgl_rocm_kv_slot_map_len(const sgl_rocm_kv_slot_map *map);
+const uint64_t *sgl_rocm_kv_slot_map_slots(const sgl_rocm_kv_slot_map *map);
+
+/* The key and value rows of CudaKvSlotScatterLaunch / CudaKvSlotGatherLaunch
+ * (:142-166). */
+typedef struct sgl_kv_slot_rows {
+    sgl_kv_device_buffer keys;
+    uint64_t keys_offset;
+    uint64_t key_row_stride_bytes;
+    sgl_kv_device_buffer values;
+    uint64_t values_offset;
+    uint64_t value_row_stride_bytes;
+} sgl_kv_slot_rows;
+/* CudaKvStorage::write_kv_slots_from_device / read_kv_slots_to_device
+ * (:296-374): validate_slot_map (:407-421: validate_layout,
+ * SlotMapCapacityMismatch, the map's slots against the layout), the layer's
+ * pair-copy plan (kv_pair_copy_plan, :510-532: kv_pair_copy_geometry, then
+ * CudaKvPairCopyPlan::new with the map's length as row_count), then
+ * sgl_rocm_kv_pair_scatter / sgl_rocm_kv_pair_gather on `stream` with the
+ * storage as the pool (synchronous, as those are). */
+int32_t sgl_rocm_kv_storage_write_kv_slots(sgl_rocm_kv_ctx *ctx, sgl_rocm_kv_storage *storage,
+                                           const sgl_kv_paged_layout *layout, uint64_t layer,
+                                           const sgl_rocm_kv_slot_map *map, const sgl_kv_slot_rows *rows,
+                                           void *stream);
+int32_t sgl_rocm_kv_storage_read_kv_slots(sgl_rocm_kv_ctx *ctx, const sgl_rocm_kv_storage *storage,
+                                          const sgl_kv_paged_layout *layout, uint64_t layer,
+                                          const sgl_rocm_kv_slot_map *map, const sgl_kv_slot_rows *rows,
+                                          void *stream);
+
+/* KvCacheMemoryLocation (nexus-transfer; the variants named at
+ * crates/sglang-srt/src/transfer.rs:1662-1676). */
+typedef enum sgl_kv_memory_location_kind {
+    SGL_KV_LOCATION_CPU = 0,   /* id = numa_node */
+    SGL_KV_LOCATION_CUDA = 1,
+    SGL_KV_LOCATION_ROCM = 2,
+    SGL_KV_LOCATION_MUSA = 3,
+    SGL_KV_LOCATION_NPU = 4,
+    SGL_KV_LOCATION_METAL = 5,
+    SGL_KV_LOCATION_XPU = 6,
+    SGL_KV_LOCATION_HPU = 7
+} sgl_kv_memory_location_kind;
+
+/* TransferableKvCacheRegion (used at cuda_kv_cache.rs:464-468). */
+typedef struct sgl_kv_memory_region {
+    uint64_t base_addr;
+    uint64_t byte_len;
+    uint64_t page_size_bytes;
+} sgl_kv_memory_region;
+
+#define SGL_KV_MAX_MEMORY_REGIONS 8u
+/* TransferableKvCacheMemory (nexus-transfer, un-vendored: pinned at
+ * crates/sglang-srt/Cargo.toml:35): regions, the logical page size and the
+ * memory location. */
+typedef struct sgl_kv_transferable_memory {
+    sgl_kv_memory_region regions[SGL_KV_MAX_MEMORY_REGIONS];
+    uint64_t region_count;
+    uint64_t page_size_bytes;
+    int32_t location_kind;  /* sgl_kv_memory_location_kind */
+    int32_t location_id;    /* device id, or numa node for CPU */
+} sgl_kv_transferable_memory;
+
+/* KvCacheMemoryProvider::transferable_kv_cache_memory for the storage
+ * (impl :455-476), with location KvCacheMemoryLocation::Rocm { device_id }:
+ * one region {base, byte_len, page_size_bytes}. The descriptor's own checks
+ * live in nexus-transfer, which the reference tree does not hold; this
+ * library rejects (StorageDescriptor) a zero page size and a region that is
+ * not a whole number of pages, the conditions its consumers reject
+ * (model_executor.rs:687-692). */
+int32_t sgl_rocm_kv_storage_transferable_memory(const sgl_rocm_kv_storage *storage,
+                                                sgl_kv_transferable_memory *out);
+/* The storage as the transfer backend registers it (sgl_kv_backend_memory),
+ * after validate_layout. heads 0 = layout.runtime.kv_heads. */
+int32_t sgl_rocm_kv_storage_backend_memory(const sgl_rocm_kv_storage *storage,
+                                           const sgl_kv_paged_layout *layout, uint32_t head_layout,
+                                           uint64_t heads, sgl_kv_backend_memory *out);
+/* MooncakeMemoryLocationExt::mooncake_memory_location_label
+ * (transfer.rs:1662-1676): "cpu:{numa}", "cuda:{id}", "hip:{id}",
+ * "musa:{id}", "npu:{id}"; Metal, Xpu and Hpu are UnsupportedMemoryLocation. */
+int32_t sgl_kv_memory_location_label(int32_t location_kind, int32_t location_id, char out[32]);
+/* MooncakeKvCacheMemoryExt::mooncake_decode_remote_layout (transfer.rs:
+ * 1693-1703): dst_kv_ptrs = each region's base address (capacity entries
+ * available at dst_kv_ptrs; *ptr_count = region_count) and dst_kv_item_len =
+ * page_size_bytes / region_count. The indices are the caller's. A
+ * descriptor without regions is StorageDescriptor. */
+int32_t sgl_kv_transferable_memory_decode_remote_layout(const sgl_kv_transferable_memory *memory,
+                                                        uint64_t *dst_kv_ptrs, uint64_t capacity,
+                                                        uint64_t *ptr_count, uint64_t *dst_kv_item_len);
 
 /* After the work queued on `stream`, reads and clears (atomically, on the
  * device) the error words of the asynchronous calls: the copies' word and

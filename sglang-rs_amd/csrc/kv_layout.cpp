@@ -123,6 +123,13 @@ extern "C" const char *sgl_kv_status_name(int32_t code) {
     case SGL_KV_ALLOC_SLOT_CAPACITY_NOT_PAGE_ALIGNED: return "SlotCapacityNotPageAligned";
     case SGL_KV_ALLOC_OUT_OF_SLOTS: return "OutOfSlots";
     case SGL_KV_RADIX_TOKEN_PAGE_LENGTH_MISMATCH: return "TokenPageLengthMismatch";
+    case SGL_KV_STORAGE_SIZE_MISMATCH: return "StorageSizeMismatch";
+    case SGL_KV_STORAGE_SLOT_MAP_CAPACITY_MISMATCH: return "SlotMapCapacityMismatch";
+    case SGL_KV_STORAGE_PAGE_BUFFER_SIZE_MISMATCH: return "PageBufferSizeMismatch";
+    case SGL_KV_STORAGE_SIZE_OVERFLOW: return "SizeOverflow";
+    case SGL_KV_ZERO_ALLOCATION: return "ZeroAllocation";
+    case SGL_KV_UNSUPPORTED_MEMORY_LOCATION: return "UnsupportedMemoryLocation";
+    case SGL_KV_STORAGE_DESCRIPTOR: return "Descriptor";
     default: return "Unknown";
     }
 }

@@ -75,6 +75,16 @@ FORWARD_PREFILL, FORWARD_DECODE = 0, 1
 DEVICE_PAGE_INDEX_OUT_OF_RANGE = 50
 DEVICE_SPAN_OUT_OF_RANGE = 51
 DEVICE_REQUEST_OUT_OF_RANGE = 52
+STORAGE_SIZE_MISMATCH = 110
+STORAGE_SLOT_MAP_CAPACITY_MISMATCH = 111
+STORAGE_PAGE_BUFFER_SIZE_MISMATCH = 112
+STORAGE_SIZE_OVERFLOW = 113
+ZERO_ALLOCATION = 114
+UNSUPPORTED_MEMORY_LOCATION = 115
+STORAGE_DESCRIPTOR = 116
+# KvCacheMemoryLocation kinds (sgl_kv_memory_location_kind)
+LOCATION_CPU, LOCATION_CUDA, LOCATION_ROCM, LOCATION_MUSA = 0, 1, 2, 3
+LOCATION_NPU, LOCATION_METAL, LOCATION_XPU, LOCATION_HPU = 4, 5, 6, 7
 
 DTYPES = {"auto": 0, "float32": 1, "bf16": 2, "bfloat16": 2, "fp8_e4m3": 3, "fp8_e5m2": 4,
           "fp4_e2m1": 5}
@@ -232,6 +242,27 @@ class _BackendConfig(ctypes.Structure):
 class _BackendMemory(ctypes.Structure):
     _fields_ = [("layout", _PagedLayout), ("base", ctypes.c_void_p), ("byte_len", _u64),
                 ("head_layout", ctypes.c_uint32), ("reserved", ctypes.c_uint32), ("heads", _u64)]
+
+
+class _TensorLocation(ctypes.Structure):
+    _fields_ = [("device_ptr", _u64), ("byte_offset", _u64), ("byte_len", _u64)]
+
+
+class _SlotRows(ctypes.Structure):
+    _fields_ = [("keys", _DeviceBuffer), ("keys_offset", _u64), ("key_row_stride_bytes", _u64),
+                ("values", _DeviceBuffer), ("values_offset", _u64), ("value_row_stride_bytes", _u64)]
+
+
+class _MemoryRegion(ctypes.Structure):
+    _fields_ = [("base_addr", _u64), ("byte_len", _u64), ("page_size_bytes", _u64)]
+
+
+MAX_MEMORY_REGIONS = 8
+
+
+class _TransferableMemory(ctypes.Structure):
+    _fields_ = [("regions", _MemoryRegion * MAX_MEMORY_REGIONS), ("region_count", _u64),
+                ("page_size_bytes", _u64), ("location_kind", ctypes.c_int32), ("location_id", ctypes.c_int32)]
 
 
 class _SpanDesc(ctypes.Structure):
@@ -478,6 +509,55 @@ _EXPORTS = {
                                                     _u64, ctypes.c_uint32, ctypes.c_void_p]),
     "sgl_rocm_kv_stream": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_uint32, ctypes.POINTER(_DeviceBuffer),
                                             ctypes.POINTER(_DeviceBuffer), _u64, ctypes.c_void_p]),
+    "sgl_rocm_kv_memory_info": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
+    "sgl_rocm_kv_storage_allocate": (ctypes.c_int32, [ctypes.c_void_p, _u64, _u64, ctypes.POINTER(ctypes.c_void_p)]),
+    "sgl_rocm_kv_cache_allocate": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_RuntimeLayout), _u64,
+                                                    ctypes.POINTER(_PagedLayout), ctypes.POINTER(ctypes.c_void_p)]),
+    "sgl_rocm_kv_pool_allocate": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_PagedLayout),
+                                                   ctypes.POINTER(ctypes.c_void_p)]),
+    "sgl_rocm_kv_storage_destroy": (ctypes.c_int32, [ctypes.c_void_p]),
+    "sgl_rocm_kv_storage_allocation": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_DeviceBuffer)]),
+    "sgl_rocm_kv_storage_byte_len": (_u64, [ctypes.c_void_p]),
+    "sgl_rocm_kv_storage_page_size_bytes": (_u64, [ctypes.c_void_p]),
+    "sgl_rocm_kv_storage_device": (ctypes.c_int32, [ctypes.c_void_p]),
+    "sgl_rocm_kv_storage_clear": (ctypes.c_int32, [ctypes.c_void_p]),
+    "sgl_rocm_kv_storage_validate_layout": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_PagedLayout)]),
+    "sgl_rocm_kv_storage_write_page": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_PagedLayout), _u64,
+                                                        ctypes.c_void_p, _u64]),
+    "sgl_rocm_kv_storage_read_page": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_PagedLayout), _u64,
+                                                       ctypes.c_void_p, _u64]),
+    "sgl_rocm_kv_storage_write_tensor_slot": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_PagedLayout), _u64,
+                                                               _u64, _u64, ctypes.POINTER(_DeviceBuffer), _u64,
+                                                               ctypes.c_void_p]),
+    "sgl_rocm_kv_storage_read_tensor_slot": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_PagedLayout), _u64,
+                                                              _u64, _u64, ctypes.POINTER(_DeviceBuffer), _u64,
+                                                              ctypes.c_void_p]),
+    "sgl_rocm_kv_storage_tensor_location": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_PagedLayout), _u64,
+                                                             _u64, _u64, _u64, ctypes.POINTER(_TensorLocation)]),
+    "sgl_rocm_kv_storage_slot_location": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_PagedLayout), _u64,
+                                                           _u64, _u64, ctypes.POINTER(_TensorLocation)]),
+    "sgl_rocm_kv_storage_upload_slot_map": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_PagedLayout),
+                                                             ctypes.POINTER(_u64), _u64,
+                                                             ctypes.POINTER(ctypes.c_void_p)]),
+    "sgl_rocm_kv_slot_map_destroy": (ctypes.c_int32, [ctypes.c_void_p]),
+    "sgl_rocm_kv_slot_map_allocation": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_DeviceBuffer)]),
+    "sgl_rocm_kv_slot_map_len": (_u64, [ctypes.c_void_p]),
+    "sgl_rocm_kv_slot_map_slots": (ctypes.POINTER(_u64), [ctypes.c_void_p]),
+    "sgl_rocm_kv_storage_write_kv_slots": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_void_p,
+                                                            ctypes.POINTER(_PagedLayout), _u64, ctypes.c_void_p,
+                                                            ctypes.POINTER(_SlotRows), ctypes.c_void_p]),
+    "sgl_rocm_kv_storage_read_kv_slots": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_void_p,
+                                                           ctypes.POINTER(_PagedLayout), _u64, ctypes.c_void_p,
+                                                           ctypes.POINTER(_SlotRows), ctypes.c_void_p]),
+    "sgl_rocm_kv_storage_transferable_memory": (ctypes.c_int32, [ctypes.c_void_p,
+                                                                 ctypes.POINTER(_TransferableMemory)]),
+    "sgl_rocm_kv_storage_backend_memory": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_PagedLayout),
+                                                            ctypes.c_uint32, _u64, ctypes.POINTER(_BackendMemory)]),
+    "sgl_kv_memory_location_label": (ctypes.c_int32, [ctypes.c_int32, ctypes.c_int32, ctypes.c_char * 32]),
+    "sgl_kv_transferable_memory_decode_remote_layout": (ctypes.c_int32, [ctypes.POINTER(_TransferableMemory),
+                                                                         ctypes.POINTER(_u64), _u64,
+                                                                         ctypes.POINTER(_u64),
+                                                                         ctypes.POINTER(_u64)]),
     "sgl_kv_bootstrap_create": (ctypes.c_int32, [ctypes.POINTER(ctypes.c_void_p)]),
     "sgl_kv_bootstrap_destroy": (ctypes.c_int32, [ctypes.c_void_p]),
     "sgl_kv_bootstrap_ingest": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_FramePart), ctypes.c_uint32]),
@@ -1034,6 +1114,13 @@ class RocmKvPairCopyKernels:
     def cu_count(self) -> int:
         return lib().sgl_rocm_kv_cu_count(self._h)
 
+    def memory_info(self):
+        """CudaContext::memory_info (crates/sglang-kernel/src/cuda.rs:496-511):
+        (free_bytes, total_bytes) of the device."""
+        f, t = _u64(), _u64()
+        _call(lib().sgl_rocm_kv_memory_info, self._h, ctypes.byref(f), ctypes.byref(t))
+        return f.value, t.value
+
     def close(self):
         if self._h:
             _call(lib().sgl_rocm_kv_destroy, self._h)
@@ -1310,6 +1397,14 @@ class RocmKvTransferBackend:
         d = self._memory(decode, decode_base, decode_len, decode_head_layout, decode_heads)
         _call(lib().sgl_rocm_kv_backend_register, self._h, ctypes.byref(p), ctypes.byref(d))
 
+    def register_pools(self, prefill: "KvCachePool", decode: "KvCachePool", *,
+                       prefill_head_layout: int = NHD, prefill_heads: int = 0,
+                       decode_head_layout: int = NHD, decode_heads: int = 0):
+        """Registers two storage-backed pools (sgl_rocm_kv_storage_backend_memory)."""
+        p = prefill.storage().backend_memory(prefill.layout(), prefill_head_layout, prefill_heads)
+        d = decode.storage().backend_memory(decode.layout(), decode_head_layout, decode_heads)
+        _call(lib().sgl_rocm_kv_backend_register, self._h, ctypes.byref(p), ctypes.byref(d))
+
     def submit(self, bootstrap_room: int, descriptor_checksum: str, token_offset: int,
                cache_slots, dst_page_table):
         """Submits one span: prefill `cache_slots` hold the request's tokens
@@ -1370,6 +1465,307 @@ class RocmKvTransferBackend:
             self.close()
         except Exception:
             pass
+
+
+@dataclass
+class TransferableKvCacheRegion:
+    """TransferableKvCacheRegion (nexus-transfer, used at cuda_kv_cache.rs:464-468)."""
+    base_addr: int
+    byte_len: int
+    page_size_bytes: int
+
+
+@dataclass
+class MooncakeRemoteKvLayout:
+    """MooncakeRemoteKvLayout (crates/sglang-srt/src/transfer.rs:1651-1656)."""
+    dst_kv_ptrs: list
+    dst_kv_indices: list
+    dst_kv_item_len: int
+
+
+def memory_location_label(kind: int, location_id: int) -> str:
+    """mooncake_memory_location_label (transfer.rs:1662-1676): "hip:0" for
+    ROCm device 0; Metal, Xpu and Hpu raise UnsupportedMemoryLocation."""
+    out = (ctypes.c_char * 32)()
+    _call(lib().sgl_kv_memory_location_label, kind, location_id, out)
+    return out.value.decode()
+
+
+class TransferableKvCacheMemory:
+    """TransferableKvCacheMemory (nexus-transfer, un-vendored; pinned at
+    crates/sglang-srt/Cargo.toml:35): regions, logical page size, location."""
+
+    def __init__(self, regions, page_size_bytes: int, location_kind: int, location_id: int):
+        self._regions = [r if isinstance(r, TransferableKvCacheRegion) else TransferableKvCacheRegion(*r)
+                         for r in regions]
+        self._page_size_bytes = page_size_bytes
+        self._location = (location_kind, location_id)
+
+    @classmethod
+    def _from_c(cls, c: _TransferableMemory) -> "TransferableKvCacheMemory":
+        regions = [TransferableKvCacheRegion(r.base_addr, r.byte_len, r.page_size_bytes)
+                   for r in c.regions[: c.region_count]]
+        return cls(regions, c.page_size_bytes, c.location_kind, c.location_id)
+
+    def _c(self) -> _TransferableMemory:
+        c = _TransferableMemory()
+        for i, r in enumerate(self._regions[:MAX_MEMORY_REGIONS]):
+            c.regions[i] = _MemoryRegion(r.base_addr, r.byte_len, r.page_size_bytes)
+        c.region_count = len(self._regions)
+        c.page_size_bytes = self._page_size_bytes
+        c.location_kind, c.location_id = self._location
+        return c
+
+    def regions(self):
+        return list(self._regions)
+
+    def page_size_bytes(self) -> int:
+        return self._page_size_bytes
+
+    def location(self):
+        """(sgl_kv_memory_location_kind, device id or numa node)."""
+        return self._location
+
+    def location_label(self) -> str:
+        return memory_location_label(*self._location)
+
+    def mooncake_decode_remote_layout(self, dst_kv_indices) -> MooncakeRemoteKvLayout:
+        """mooncake_decode_remote_layout (transfer.rs:1693-1703)."""
+        c = self._c()
+        ptrs = (_u64 * MAX_MEMORY_REGIONS)()
+        n, item = _u64(), _u64()
+        _call(lib().sgl_kv_transferable_memory_decode_remote_layout, ctypes.byref(c), ptrs,
+              MAX_MEMORY_REGIONS, ctypes.byref(n), ctypes.byref(item))
+        return MooncakeRemoteKvLayout(list(ptrs[: n.value]), [int(i) for i in dst_kv_indices], item.value)
+
+
+@dataclass
+class KvCacheTensorLocation:
+    """CudaKvCacheTensorLocation (cuda_kv_cache.rs:103-107)."""
+    device_ptr: int
+    byte_offset: int
+    byte_len: int
+
+
+def _stream_handle(stream):
+    return None if stream is None else getattr(stream, "handle", stream)
+
+
+def _as_db(b) -> _DeviceBuffer:
+    return b if isinstance(b, _DeviceBuffer) else _DeviceBuffer(b.ptr, b.nbytes)
+
+
+class RocmKvSlotMap:
+    """CudaKvCacheSlotMap (cuda_kv_cache.rs:109-140): u64 slots on the device
+    plus the host slots they were validated with."""
+
+    def __init__(self, handle: int):
+        self._h = handle
+
+    def __len__(self) -> int:
+        return lib().sgl_rocm_kv_slot_map_len(self._h)
+
+    def slots(self) -> np.ndarray:
+        n = len(self)
+        ptr = lib().sgl_rocm_kv_slot_map_slots(self._h)
+        return np.ctypeslib.as_array(ptr, shape=(n,)).copy() if n else np.zeros(0, np.uint64)
+
+    def allocation(self) -> _DeviceBuffer:
+        b = _DeviceBuffer()
+        _call(lib().sgl_rocm_kv_slot_map_allocation, self._h, ctypes.byref(b))
+        return b
+
+    def close(self):
+        if self._h:
+            _call(lib().sgl_rocm_kv_slot_map_destroy, self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class RocmKvStorage:
+    """CudaKvStorage (cuda_kv_cache.rs:170-509) on MI355X: a library-owned,
+    zero-filled device allocation holding a paged pool."""
+
+    def __init__(self, handle: int):
+        self._h = handle
+
+    @classmethod
+    def allocate(cls, kernels: "RocmKvPairCopyKernels", byte_len: int, page_size_bytes: int) -> "RocmKvStorage":
+        """CudaKvStorage::allocate (:177-189)."""
+        h = ctypes.c_void_p()
+        _call(lib().sgl_rocm_kv_storage_allocate, kernels._h, byte_len, page_size_bytes, ctypes.byref(h))
+        return cls(h.value)
+
+    def allocation(self) -> _DeviceBuffer:
+        b = _DeviceBuffer()
+        _call(lib().sgl_rocm_kv_storage_allocation, self._h, ctypes.byref(b))
+        return b
+
+    @property
+    def device_ptr(self) -> int:
+        return self.allocation().ptr or 0
+
+    def byte_len(self) -> int:
+        return lib().sgl_rocm_kv_storage_byte_len(self._h)
+
+    def page_size_bytes(self) -> int:
+        return lib().sgl_rocm_kv_storage_page_size_bytes(self._h)
+
+    def device_ordinal(self) -> int:
+        return lib().sgl_rocm_kv_storage_device(self._h)
+
+    def clear(self):
+        """KvCacheStorage::clear (impl :449-452)."""
+        _call(lib().sgl_rocm_kv_storage_clear, self._h)
+
+    def validate_layout(self, layout: "PagedKvCacheLayout"):
+        _call(lib().sgl_rocm_kv_storage_validate_layout, self._h, ctypes.byref(layout._c))
+
+    def write_page(self, layout: "PagedKvCacheLayout", page_index: int, data):
+        """CudaKvStorage::write_page (:224-239)."""
+        a = np.ascontiguousarray(np.frombuffer(bytes(data), dtype=np.uint8)
+                                 if isinstance(data, (bytes, bytearray)) else np.asarray(data, dtype=np.uint8))
+        _call(lib().sgl_rocm_kv_storage_write_page, self._h, ctypes.byref(layout._c), page_index,
+              a.ctypes.data if a.size else None, a.size)
+
+    def read_page(self, layout: "PagedKvCacheLayout", page_index: int, nbytes: int | None = None) -> np.ndarray:
+        """CudaKvStorage::read_page (:241-256); nbytes defaults to the page size."""
+        n = layout.runtime.page_size_bytes if nbytes is None else nbytes
+        out = np.zeros(n, dtype=np.uint8)
+        _call(lib().sgl_rocm_kv_storage_read_page, self._h, ctypes.byref(layout._c), page_index,
+              out.ctypes.data if n else None, n)
+        return out
+
+    def write_tensor_slot_from_device(self, layout: "PagedKvCacheLayout", layer: int, tensor: int, slot: int,
+                                      source, source_offset: int = 0, stream=None):
+        """CudaKvStorage::write_tensor_slot_from_device (:258-274); asynchronous."""
+        src = _as_db(source)
+        _call(lib().sgl_rocm_kv_storage_write_tensor_slot, self._h, ctypes.byref(layout._c), layer, tensor, slot,
+              ctypes.byref(src), source_offset, _stream_handle(stream))
+
+    def read_tensor_slot_to_device(self, layout: "PagedKvCacheLayout", layer: int, tensor: int, slot: int,
+                                   destination, destination_offset: int = 0, stream=None):
+        """CudaKvStorage::read_tensor_slot_to_device (:276-294); asynchronous."""
+        dst = _as_db(destination)
+        _call(lib().sgl_rocm_kv_storage_read_tensor_slot, self._h, ctypes.byref(layout._c), layer, tensor, slot,
+              ctypes.byref(dst), destination_offset, _stream_handle(stream))
+
+    def tensor_location(self, layout: "PagedKvCacheLayout", page: int, layer: int, tensor: int,
+                        token: int) -> KvCacheTensorLocation:
+        out = _TensorLocation()
+        _call(lib().sgl_rocm_kv_storage_tensor_location, self._h, ctypes.byref(layout._c), page, layer, tensor,
+              token, ctypes.byref(out))
+        return KvCacheTensorLocation(out.device_ptr, out.byte_offset, out.byte_len)
+
+    def slot_location(self, layout: "PagedKvCacheLayout", layer: int, tensor: int, slot: int) -> KvCacheTensorLocation:
+        """CudaKvStorage::slot_location (:390-403)."""
+        out = _TensorLocation()
+        _call(lib().sgl_rocm_kv_storage_slot_location, self._h, ctypes.byref(layout._c), layer, tensor, slot,
+              ctypes.byref(out))
+        return KvCacheTensorLocation(out.device_ptr, out.byte_offset, out.byte_len)
+
+    def upload_slot_map(self, layout: "PagedKvCacheLayout", slots) -> RocmKvSlotMap:
+        """CudaKvStorage::upload_slot_map (:199-222)."""
+        a = _u64_array(slots)
+        h = ctypes.c_void_p()
+        _call(lib().sgl_rocm_kv_storage_upload_slot_map, self._h, ctypes.byref(layout._c),
+              _pu64(a) if a.size else None, a.size, ctypes.byref(h))
+        return RocmKvSlotMap(h.value)
+
+    @staticmethod
+    def _rows(keys, key_row_stride_bytes, values, value_row_stride_bytes, keys_offset, values_offset):
+        return _SlotRows(_as_db(keys), keys_offset, key_row_stride_bytes, _as_db(values), values_offset,
+                         value_row_stride_bytes)
+
+    def write_kv_slots_from_device(self, kernels: "RocmKvPairCopyKernels", layout: "PagedKvCacheLayout",
+                                   layer: int, slot_map: RocmKvSlotMap, *, keys, key_row_stride_bytes: int,
+                                   values, value_row_stride_bytes: int, keys_offset: int = 0,
+                                   values_offset: int = 0, stream=None):
+        """CudaKvStorage::write_kv_slots_from_device (:296-334)."""
+        r = self._rows(keys, key_row_stride_bytes, values, value_row_stride_bytes, keys_offset, values_offset)
+        _call(lib().sgl_rocm_kv_storage_write_kv_slots, kernels._h, self._h, ctypes.byref(layout._c), layer,
+              slot_map._h, ctypes.byref(r), _stream_handle(stream))
+
+    def read_kv_slots_to_device(self, kernels: "RocmKvPairCopyKernels", layout: "PagedKvCacheLayout",
+                                layer: int, slot_map: RocmKvSlotMap, *, keys, key_row_stride_bytes: int,
+                                values, value_row_stride_bytes: int, keys_offset: int = 0,
+                                values_offset: int = 0, stream=None):
+        """CudaKvStorage::read_kv_slots_to_device (:336-374)."""
+        r = self._rows(keys, key_row_stride_bytes, values, value_row_stride_bytes, keys_offset, values_offset)
+        _call(lib().sgl_rocm_kv_storage_read_kv_slots, kernels._h, self._h, ctypes.byref(layout._c), layer,
+              slot_map._h, ctypes.byref(r), _stream_handle(stream))
+
+    def transferable_kv_cache_memory(self) -> TransferableKvCacheMemory:
+        """impl KvCacheMemoryProvider for CudaKvStorage (:455-476), located on
+        KvCacheMemoryLocation::Rocm."""
+        c = _TransferableMemory()
+        _call(lib().sgl_rocm_kv_storage_transferable_memory, self._h, ctypes.byref(c))
+        return TransferableKvCacheMemory._from_c(c)
+
+    def backend_memory(self, layout: "PagedKvCacheLayout", head_layout: int = NHD, heads: int = 0):
+        m = _BackendMemory()
+        _call(lib().sgl_rocm_kv_storage_backend_memory, self._h, ctypes.byref(layout._c), head_layout, heads,
+              ctypes.byref(m))
+        return m
+
+    def close(self):
+        if self._h:
+            _call(lib().sgl_rocm_kv_storage_destroy, self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class KvCachePool:
+    """KvCachePool<RocmKvStorage> (kv_cache.rs:835-896): a layout and the
+    storage it addresses."""
+
+    def __init__(self, layout: "PagedKvCacheLayout", storage: RocmKvStorage):
+        self._layout, self._storage = layout, storage
+
+    def layout(self) -> "PagedKvCacheLayout":
+        return self._layout
+
+    def storage(self) -> RocmKvStorage:
+        return self._storage
+
+    storage_mut = storage
+
+    def clear(self):
+        self._storage.clear()
+
+    def transferable_kv_cache_memory(self) -> TransferableKvCacheMemory:
+        return self._storage.transferable_kv_cache_memory()
+
+    def close(self):
+        self._storage.close()
+
+
+def allocate_rocm_kv_cache(kernels: "RocmKvPairCopyKernels", runtime: KvCacheRuntimeLayout,
+                           page_count: int) -> KvCachePool:
+    """allocate_cuda_kv_cache (cuda_kv_cache.rs:478-490) on the kernels' device."""
+    out = _PagedLayout()
+    h = ctypes.c_void_p()
+    _call(lib().sgl_rocm_kv_cache_allocate, kernels._h, ctypes.byref(runtime._c()), page_count,
+          ctypes.byref(out), ctypes.byref(h))
+    return KvCachePool(PagedKvCacheLayout(out), RocmKvStorage(h.value))
+
+
+def allocate_rocm_kv_pool(kernels: "RocmKvPairCopyKernels", layout: "PagedKvCacheLayout") -> KvCachePool:
+    """A zero-filled storage for an existing layout (a tensor pair included),
+    checked as KvCachePool::new does (kv_cache.rs:849-856)."""
+    h = ctypes.c_void_p()
+    _call(lib().sgl_rocm_kv_pool_allocate, kernels._h, ctypes.byref(layout._c), ctypes.byref(h))
+    return KvCachePool(layout, RocmKvStorage(h.value))
 
 
 class PagedAttentionPlan:

@@ -832,21 +832,25 @@ typedef struct sgl_kv_attention_plan_config {  /* CudaBf16PagedAttentionPlanConf
     uint64_t query_key_head_dim;
     uint64_t value_head_dim;
     float scale;
-    uint32_t flags;            /* 0 or SGL_KV_ATTN_EXACT_WEIGHTS */
+    uint32_t flags;            /* 0, SGL_KV_ATTN_EXACT_WEIGHTS or SGL_KV_ATTN_FAST_WEIGHTS */
     sgl_kv_attention_layout layout;
 } sgl_kv_attention_plan_config;
 
-/* Plan flag with no counterpart in the reference (its config has no such
- * field). The latent body (the MLA shape: 576-wide keys whose first 512
- * dims are the values, one KV head) by default feeds the softmax weights to
- * its P.V matrix products rounded to bf16, a relative error of at most 2^-8
- * per weight; with this flag it feeds each weight as a hi + lo pair of bf16
- * values (one more matrix product per tile), which brings that error to
- * about 2^-16, as every other body does by default. It lengthens the
- * latent launch by 4 % (one query of 8,192 tokens, 128 heads) to 20 %
- * (64 such queries) on MI355X. Other bodies ignore it. Unknown bits are
- * rejected by sgl_kv_attention_plan_new and at enqueue. */
+/* Plan flags, with no counterpart in the reference (its config has no such
+ * field); 0 is the reference's behaviour. Every body feeds its softmax
+ * weights to the P.V matrix products as a hi + lo pair of bf16 values
+ * (relative error about 2^-16 per weight), so outputs stay within the
+ * reference's fp32-weight precision (cuda_attention.rs:138-149) up to the
+ * bf16 output rounding. SGL_KV_ATTN_FAST_WEIGHTS lets the latent body (the
+ * MLA shape: 576-wide keys whose first 512 dims are the values, one KV head)
+ * round each weight to one bf16 value instead (at most 2^-8 relative), which
+ * saves one matrix product per tile: 4 % (one query of 8,192 tokens, 128
+ * heads) to 20 % (64 such queries) of that launch on MI355X. Other bodies
+ * ignore it. SGL_KV_ATTN_EXACT_WEIGHTS names the default and is accepted
+ * for callers that set it; setting both, or any other bit, is rejected
+ * (InvalidArgument "flags") by sgl_kv_attention_plan_new and at enqueue. */
 #define SGL_KV_ATTN_EXACT_WEIGHTS 1u
+#define SGL_KV_ATTN_FAST_WEIGHTS 2u
 
 typedef struct sgl_kv_attention_plan {  /* CudaBf16PagedAttentionPlan (:239-261) */
     sgl_kv_attention_plan_config config;
@@ -886,9 +890,12 @@ int32_t sgl_kv_attention_plan_for_layer(const sgl_kv_paged_layout *layout, uint6
                                         float scale, uint32_t head_layout,
                                         sgl_kv_attention_plan *out);
 /* CudaBf16PagedAttentionKernels::forward (cuda_attention.rs:681-850):
- * checks devices and ranges, clears the error word, runs, synchronises
- * `stream` and reports bad metadata as SGL_KV_ATTN_DEVICE_METADATA_INVALID
- * (the outputs of the affected queries are then unspecified).
+ * checks devices and ranges, runs, synchronises `stream` and reports bad
+ * metadata as SGL_KV_ATTN_DEVICE_METADATA_INVALID (the outputs of the
+ * affected queries are then unspecified). It raises an error word of its
+ * own, which every call leaves clear, so asynchronous launches still
+ * running on other streams neither lose their errors to it nor report
+ * theirs through it.
  * max_sequence_length (0 = unknown, then sequence_slot_count) bounds the
  * query lengths and steers how sequences are split across workgroups; a
  * query longer than it is reported as a sequence error (flag 0x2), not
@@ -919,10 +926,18 @@ int32_t sgl_rocm_kv_paged_attention_async(sgl_rocm_kv_ctx *ctx, const sgl_kv_att
  * process ends (its address is resolved at sgl_rocm_kv_init). A launch whose
  * records need more is rejected with SGL_KV_DIMENSION_TOO_LARGE (name
  * "workspace", a = bytes needed, b = the maximum) before anything is
- * enqueued. Every call on a device shares that device's workspace and the
- * records a call leaves stay until the next one: calls that overlap in time
- * on one device race, so issue them on one stream. Results equal those of
- * sgl_rocm_kv_paged_attention_async on the same arguments. */
+ * enqueued. Every call on a device shares that device's workspace, and the
+ * records a call leaves stay until the next one. Calls are therefore ordered
+ * on the device: each call's launches wait for the previous call's combine
+ * (an event the library keeps per device, recorded after every call), on
+ * whatever stream and from whatever context of the process either was made,
+ * so concurrent calls run one after another instead of overwriting each
+ * other's records. A stream under graph capture skips that wait and record
+ * (an event recorded outside the capture cannot be waited on inside it):
+ * there the graph's own dependencies order the calls it holds, and the
+ * caller must not replay such a graph while another call that uses the
+ * workspace runs. Results equal those of sgl_rocm_kv_paged_attention_async
+ * on the same arguments. */
 #define SGL_KV_NOALLOC_WORKSPACE_BYTES (128ull << 20)
 int32_t sgl_rocm_kv_paged_attention_async_noalloc(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *plan,
                                                   const sgl_kv_attention_buffers *buffers,
@@ -1381,7 +1396,9 @@ int32_t sgl_kv_transferable_memory_decode_remote_layout(const sgl_kv_transferabl
  * also reaches the copies as a bad slot), then
  * SGL_KV_ATTN_DEVICE_METADATA_INVALID. The synchronous pair scatter/gather
  * and paged attention keep words of their own. Replaces the flag readback of
- * cuda_kv_kernels.rs:613-621 for the asynchronous calls. */
+ * cuda_kv_kernels.rs:613-621 for the asynchronous calls. The values are read
+ * back through one context-owned slot, so, like every call on a context,
+ * calls from different host threads must not overlap. */
 int32_t sgl_rocm_kv_check_errors(sgl_rocm_kv_ctx *ctx, void *stream);
 
 #ifdef __cplusplus

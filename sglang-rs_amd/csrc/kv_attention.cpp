@@ -7,6 +7,8 @@
 // device and range checks, clear the error word, launch, synchronise, read
 // the word).
 #include <hip/hip_runtime.h>
+
+#include <mutex>
 #include <math.h>
 #include <string.h>
 
@@ -15,6 +17,18 @@
 using namespace sglkv;
 
 namespace {
+
+// The plan flags: EXACT_WEIGHTS (the default, kept for callers that set it)
+// and FAST_WEIGHTS exclude each other; other bits are unknown.
+int32_t check_flags(uint32_t flags) {
+    constexpr uint32_t known = SGL_KV_ATTN_EXACT_WEIGHTS | SGL_KV_ATTN_FAST_WEIGHTS;
+    if (flags & ~known)
+        return fail(SGL_KV_INVALID_ARGUMENT, "flags", flags, known, 0, "unknown attention plan flags 0x%x", flags);
+    if ((flags & known) == known)
+        return fail(SGL_KV_INVALID_ARGUMENT, "flags", flags, known, 0,
+                    "attention plan flags 0x%x ask for exact and fast weights at once", flags);
+    return SGL_KV_OK;
+}
 
 int32_t attn_overflow() {
     return fail(SGL_KV_SHAPE_OVERFLOW, nullptr, 0, 0, 0, "CUDA paged attention shape overflowed");
@@ -115,9 +129,7 @@ extern "C" int32_t sgl_kv_attention_plan_new(const sgl_kv_attention_plan_config 
     if (lay.head_layout > SGL_KV_HND)
         return fail(SGL_KV_INVALID_ARGUMENT, "head_layout", lay.head_layout, 0, 0,
                     "unknown head layout %u", lay.head_layout);
-    if (c->flags & ~SGL_KV_ATTN_EXACT_WEIGHTS)
-        return fail(SGL_KV_INVALID_ARGUMENT, "flags", c->flags, SGL_KV_ATTN_EXACT_WEIGHTS, 0,
-                    "unknown attention plan flags 0x%x", c->flags);
+    if ((rc = check_flags(c->flags))) return rc;
 
     sgl_kv_attention_plan p;
     memset(&p, 0, sizeof p);
@@ -240,12 +252,13 @@ int32_t attn_ptr(const char *name, const sgl_kv_device_buffer &b, uint64_t offse
 uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
 
 // Validates, sizes the split and launches the attention (and, with
-// several splits, the combine pass) on `stream`; nothing waits.
-// `workspace` (fixed, `workspace_bytes` long) holds the split records when
-// given; otherwise the context's buffer, grown on demand.
+// several splits, the combine pass) on `stream`; nothing waits. Metadata
+// errors raise `flag_word`. `workspace` (fixed, `workspace_bytes` long)
+// holds the split records when given; otherwise the context's buffer,
+// grown on demand.
 int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *plan,
                           const sgl_kv_attention_buffers *b, uint64_t max_sequence_length,
-                          hipStream_t s, bool clear_flag, void *workspace = nullptr,
+                          hipStream_t s, uint32_t *flag_word, void *workspace = nullptr,
                           uint64_t workspace_bytes = 0) {
     if (!ctx || !plan || !b)
         return fail(SGL_KV_INVALID_ARGUMENT, "ctx/plan/buffers", 0, 0, 0, "null argument");
@@ -265,9 +278,7 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
     for (const auto &a : all)
         if ((rc = check_device(ctx, a.name, *a.buf))) return rc;
     // A plan is a plain struct the caller may have edited since plan_new.
-    if (c.flags & ~SGL_KV_ATTN_EXACT_WEIGHTS)
-        return fail(SGL_KV_INVALID_ARGUMENT, "flags", c.flags, SGL_KV_ATTN_EXACT_WEIGHTS, 0,
-                    "unknown attention plan flags 0x%x", c.flags);
+    if ((rc = check_flags(c.flags))) return rc;
     uint64_t qp, rip, slp, rop, ssp, poolp, outp;
     if ((rc = attn_ptr("queries", b->queries, b->queries_offset, plan->query_required_bytes, &qp)) ||
         (rc = attn_ptr("query_request_indices", b->query_request_indices, b->query_request_indices_offset,
@@ -302,7 +313,7 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
     p.sequence_slots = reinterpret_cast<const uint64_t *>(ssp);
     p.pool = reinterpret_cast<const uint8_t *>(poolp);
     p.output = reinterpret_cast<uint16_t *>(outp);
-    p.flag = ctx->attn_flag;
+    p.flag = flag_word;
     p.query_count = c.query_count;
     p.request_count = c.request_count;
     p.sequence_slot_count = c.sequence_slot_count;
@@ -423,8 +434,9 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
         (!wide && (mul_ovf(base, p.head_groups, &base) || mul_ovf(base, p.dv_blocks, &base))) ||
         base > UINT32_MAX / threads)  // a dispatch counts its work-items in 32 bits
         return too_large_dim("workgroups", base, UINT32_MAX / threads);
-    // The latent body with hi + lo weights is a function of its own.
-    const int fn = which == 6 && (c.flags & SGL_KV_ATTN_EXACT_WEIGHTS) ? 9 : which;
+    // The latent body has two functions: hi + lo weights (the default, as
+    // precise as the other bodies) and, on request, bf16 weights.
+    const int fn = which == 6 && !(c.flags & SGL_KV_ATTN_FAST_WEIGHTS) ? 9 : which;
     if (ctx->attention_occupancy_lds[fn] != lds) {
         int per_cu = 0;
         SGLKV_CHECK_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ctx->attention[fn],
@@ -503,7 +515,6 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
         if (heads > limit / 2 || combine_grid > limit)
             return too_large_dim("combine workgroups", heads, limit / 2);
     }
-    if (clear_flag) SGLKV_CHECK_HIP(hipMemsetAsync(ctx->attn_flag, 0, sizeof(uint32_t), s));
     void *args[] = {&p};
     SGLKV_CHECK_HIP(hipModuleLaunchKernel(ctx->attention[fn], (unsigned)base, (unsigned)splits, 1, threads,
                                           1, 1, lds, s, args, nullptr));
@@ -523,17 +534,20 @@ extern "C" int32_t sgl_rocm_kv_paged_attention(sgl_rocm_kv_ctx *ctx, const sgl_k
                                                uint64_t max_sequence_length, void *stream) {
     if (!ctx) return fail(SGL_KV_INVALID_ARGUMENT, "ctx", 0, 0, 0, "null argument");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    int32_t rc = attention_enqueue(ctx, plan, b, max_sequence_length, s, true);
+    // The synchronous forward has an error word of its own, as the
+    // reference's kernels object has its flag (cuda_attention.rs:667,
+    // 706-707): asynchronous launches still running on other streams raise
+    // the asynchronous word, so nothing here can take or clear their bits.
+    // Calls on one context do not overlap, so the word is clean on entry:
+    // every synchronous call leaves it zero.
+    int32_t rc = attention_enqueue(ctx, plan, b, max_sequence_length, s, ctx->sync_attn_flag);
     if (rc) return rc;
     DeviceScope scope(ctx->device);
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
     SGLKV_CHECK_HIP(hipStreamSynchronize(s));
     uint32_t flag = 0;
-    SGLKV_CHECK_HIP(hipMemcpy(&flag, ctx->attn_flag, sizeof flag, hipMemcpyDeviceToHost));
-    // A reported error is consumed, as sgl_rocm_kv_check_errors does. The
-    // attention word is its own (the copies raise another), so this read
-    // and clear takes no copy error away from check_errors.
-    if (flag) SGLKV_CHECK_HIP(hipMemset(ctx->attn_flag, 0, sizeof(uint32_t)));
+    SGLKV_CHECK_HIP(hipMemcpy(&flag, ctx->sync_attn_flag, sizeof flag, hipMemcpyDeviceToHost));
+    if (flag) SGLKV_CHECK_HIP(hipMemset(ctx->sync_attn_flag, 0, sizeof(uint32_t)));
     return attention_flag_status(flag);
 }
 
@@ -543,7 +557,7 @@ extern "C" int32_t sgl_rocm_kv_paged_attention_async(sgl_rocm_kv_ctx *ctx,
                                                      uint64_t max_sequence_length, void *stream) {
     if (!ctx) return fail(SGL_KV_INVALID_ARGUMENT, "ctx", 0, 0, 0, "null argument");
     const int32_t rc =
-        attention_enqueue(ctx, plan, b, max_sequence_length, static_cast<hipStream_t>(stream), false);
+        attention_enqueue(ctx, plan, b, max_sequence_length, static_cast<hipStream_t>(stream), ctx->attn_flag);
     return rc ? rc : ok();
 }
 
@@ -552,9 +566,28 @@ extern "C" int32_t sgl_rocm_kv_paged_attention_async_noalloc(sgl_rocm_kv_ctx *ct
                                                              const sgl_kv_attention_buffers *b,
                                                              uint64_t max_sequence_length, void *stream) {
     if (!ctx) return fail(SGL_KV_INVALID_ARGUMENT, "ctx", 0, 0, 0, "null argument");
-    if (!ctx->noalloc_workspace)
+    if (!ctx->noalloc_workspace || !ctx->noalloc_order)
         return fail(SGL_KV_MODULE, "workspace", 0, 0, 0, "the context has no workspace address");
-    const int32_t rc = attention_enqueue(ctx, plan, b, max_sequence_length, static_cast<hipStream_t>(stream),
-                                         false, ctx->noalloc_workspace, SGL_KV_NOALLOC_WORKSPACE_BYTES);
-    return rc ? rc : ok();
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    // Every call on this device shares the workspace. The device's event
+    // marks the end of the last call that used it: this call's launches
+    // wait for it on `s`, and the event then moves past this call's
+    // combine. The lock makes wait, launch and record one step for all
+    // host threads and contexts, so calls on any streams run in the order
+    // they were made. Under stream capture the graph's own dependencies
+    // order its launches (an event recorded outside the capture cannot be
+    // waited on there), so the event is left alone.
+    NoallocOrder *order = ctx->noalloc_order;
+    std::lock_guard<std::mutex> guard(order->lock);
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    SGLKV_CHECK_HIP(hipStreamIsCapturing(s, &capture));
+    const bool ordered = capture == hipStreamCaptureStatusNone;
+    if (ordered) SGLKV_CHECK_HIP(hipStreamWaitEvent(s, order->last, 0));
+    const int32_t rc = attention_enqueue(ctx, plan, b, max_sequence_length, s, ctx->attn_flag,
+                                         ctx->noalloc_workspace, SGL_KV_NOALLOC_WORKSPACE_BYTES);
+    if (rc) return rc;
+    if (ordered) SGLKV_CHECK_HIP(hipEventRecord(order->last, s));
+    return ok();
 }

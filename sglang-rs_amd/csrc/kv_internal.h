@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "kv_params.h"
 
 // The C ABI is the library's only exported surface (built with
@@ -82,9 +84,16 @@ int32_t prepare_transfer(const sgl_rocm_kv_ctx *ctx, const sgl_kv_pool_view *src
 int32_t submit_launch(sgl_rocm_kv_ctx *ctx, Launch &l, hipStream_t stream);
 hipStream_t pipeline_final_stream(sgl_rocm_kv_pipeline *pipe);
 void pipeline_set_error_word(sgl_rocm_kv_pipeline *pipe, uint32_t *flag);
-// The device address of the static no-allocation workspace on `device`
-// (resolved once per device; kv_scratch.hip).
-int32_t noalloc_workspace(int device, void **out);
+// The no-allocation entry point's workspace on one device (kv_scratch.hip):
+// `lock` makes a call's wait + launch + record one step among host threads,
+// `last` is recorded after the last call that used the workspace.
+struct NoallocOrder {
+    std::mutex lock;
+    hipEvent_t last = nullptr;
+};
+// The device address of the static no-allocation workspace on `device` and
+// its ordering (resolved once per device).
+int32_t noalloc_workspace(int device, void **out, NoallocOrder **order);
 int32_t hip_fail(hipError_t err, const char *call);
 int32_t flag_status(uint32_t flag);
 int32_t attention_flag_status(uint32_t flag);
@@ -142,12 +151,14 @@ struct sgl_rocm_kv_ctx {
     // (cuda_kv_kernels.rs:421, 460-461; cuda_attention.rs:667, 706-707), so that one
     // consumer's read-and-clear never takes another's bits.
     uint32_t *flag;                 // asynchronous copies, span resolution, page requests
-    uint32_t *attn_flag;            // paged attention
+    uint32_t *attn_flag;            // asynchronous paged attention
     uint32_t *pair_flag;            // the synchronous pair scatter/gather drop-ins
+    uint32_t *sync_attn_flag;       // the synchronous paged attention
     const uint8_t *zero_row;        // SGLKV_ZERO_ROW_BYTES of zeros inside that block
     void *attention_partial;        // split records, grown on demand
     uint64_t attention_partial_bytes;
     void *noalloc_workspace;        // this device's static workspace (SGL_KV_NOALLOC_WORKSPACE_BYTES)
+    sglkv::NoallocOrder *noalloc_order;  // its ordering across streams and contexts
     uint32_t rows_per_thread;  // from the code object
     uint32_t max_tile_rows;
     uint32_t realign_rows_per_thread;

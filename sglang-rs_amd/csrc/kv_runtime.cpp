@@ -540,15 +540,16 @@ extern "C" int32_t sgl_rocm_kv_init(int32_t device, const char *code_object_path
     if (err == hipSuccess && (ctx->rows_per_thread == 0 || ctx->rows_per_thread > ctx->max_tile_rows ||
                               ctx->realign_rows_per_thread == 0 || ctx->realign_rows_per_thread > 32))
         err = hipErrorInvalidImage;
-    // One small block: the error words at offsets 0, 64 and 128 (separate
-    // lines), check_errors' readout at 192, the zero row at 256.
-    constexpr size_t kFlagBlock = 256 + SGLKV_ZERO_ROW_BYTES;
+    // One small block: the error words at offsets 0, 64, 128 and 256
+    // (separate lines), check_errors' readout at 192, the zero row at 320.
+    constexpr size_t kFlagBlock = 320 + SGLKV_ZERO_ROW_BYTES;
     if (err == hipSuccess) err = hipMalloc(reinterpret_cast<void **>(&ctx->flag), kFlagBlock);
     if (err == hipSuccess) err = hipMemset(ctx->flag, 0, kFlagBlock);
     if (err == hipSuccess) {
         ctx->attn_flag = ctx->flag + 16;
         ctx->pair_flag = ctx->flag + 32;
-        ctx->zero_row = reinterpret_cast<const uint8_t *>(ctx->flag) + 256;
+        ctx->sync_attn_flag = ctx->flag + 64;
+        ctx->zero_row = reinterpret_cast<const uint8_t *>(ctx->flag) + 320;
     }
     if (err != hipSuccess) {
         if (ctx->flag) (void)hipFree(ctx->flag);
@@ -558,7 +559,7 @@ extern "C" int32_t sgl_rocm_kv_init(int32_t device, const char *code_object_path
     }
     // The no-allocation entry point's workspace on this device, resolved
     // here once so that the entry point itself does no set-up.
-    int32_t rc = noalloc_workspace(device, &ctx->noalloc_workspace);
+    int32_t rc = noalloc_workspace(device, &ctx->noalloc_workspace, &ctx->noalloc_order);
     if (rc) {
         (void)hipFree(ctx->flag);
         (void)hipModuleUnload(ctx->module);

@@ -21,11 +21,13 @@ static __device__ __align__(256) uint8_t scratch[SGL_KV_NOALLOC_WORKSPACE_BYTES]
 constexpr int kMaxDevices = 64;
 std::mutex g_lock;
 void *g_address[kMaxDevices];
+sglkv::NoallocOrder g_order[kMaxDevices];
 
 }  // namespace
 
-int32_t sglkv::noalloc_workspace(int device, void **out) {
+int32_t sglkv::noalloc_workspace(int device, void **out, NoallocOrder **order) {
     *out = nullptr;
+    *order = nullptr;
     if (device < 0 || device >= kMaxDevices)
         return fail(SGL_KV_INVALID_ARGUMENT, "device", (uint64_t)(int64_t)device, kMaxDevices, 0,
                     "device %d is past the %d devices the workspace table covers", device, kMaxDevices);
@@ -37,8 +39,16 @@ int32_t sglkv::noalloc_workspace(int device, void **out) {
         const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
         if (err != hipSuccess) return hip_fail(err, "hipGetSymbolAddress");
         if (!ptr) return fail(SGL_KV_MODULE, "hipGetSymbolAddress", 0, 0, 0, "the workspace has no device address");
+        // The ordering event, created once here so that the entry point
+        // itself creates nothing; kept, like the workspace, until the
+        // process ends.
+        hipEvent_t last = nullptr;
+        const hipError_t eerr = hipEventCreateWithFlags(&last, hipEventDisableTiming);
+        if (eerr != hipSuccess) return hip_fail(eerr, "hipEventCreateWithFlags");
+        g_order[device].last = last;
         g_address[device] = ptr;
     }
     *out = g_address[device];
+    *order = &g_order[device];
     return SGL_KV_OK;
 }

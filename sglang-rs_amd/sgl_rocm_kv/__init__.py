@@ -89,9 +89,11 @@ LOCATION_NPU, LOCATION_METAL, LOCATION_XPU, LOCATION_HPU = 4, 5, 6, 7
 DTYPES = {"auto": 0, "float32": 1, "bf16": 2, "bfloat16": 2, "fp8_e4m3": 3, "fp8_e5m2": 4,
           "fp4_e2m1": 5}
 NHD, HND = 0, 1
-# Attention plan flag (no counterpart in the reference): the latent (MLA)
-# body feeds its softmax weights as hi + lo bf16 pairs instead of one bf16.
+# Attention plan flags (no counterpart in the reference): hi + lo bf16
+# softmax weights are the default in every body (EXACT names it); FAST lets
+# the latent (MLA) body round each weight to one bf16 instead.
 ATTN_EXACT_WEIGHTS = 1
+ATTN_FAST_WEIGHTS = 2
 FILL_BITS, FILL_BF16_NORMAL, FILL_BF16_UNIFORM = 0, 1, 2
 STREAM_COPY, STREAM_READ, STREAM_WRITE = 0, 1, 2
 
@@ -1781,10 +1783,11 @@ class PagedAttentionPlan:
             value_head_dim: int, scale: float, page_size: int, page_stride_bytes: int,
             key_in_page_offset: int, value_in_page_offset: int, key_row_bytes: int,
             value_row_bytes: int, head_layout: int = NHD,
-            exact_weights: bool = False) -> "PagedAttentionPlan":
+            exact_weights: bool = False, fast_weights: bool = False) -> "PagedAttentionPlan":
+        flags = (ATTN_EXACT_WEIGHTS if exact_weights else 0) | (ATTN_FAST_WEIGHTS if fast_weights else 0)
         cfg = _AttentionPlanConfig(query_count, request_count, sequence_slot_count, slot_count,
                                    query_head_count, kv_head_count, query_key_head_dim,
-                                   value_head_dim, scale, ATTN_EXACT_WEIGHTS if exact_weights else 0,
+                                   value_head_dim, scale, flags,
                                    _AttentionLayout(page_size, page_stride_bytes,
                                                     key_in_page_offset, value_in_page_offset,
                                                     key_row_bytes, value_row_bytes, head_layout, 0))
@@ -1796,16 +1799,19 @@ class PagedAttentionPlan:
     def for_layer(cls, layout: PagedKvCacheLayout, layer: int, query_count: int,
                   request_count: int, sequence_slot_count: int, query_head_count: int,
                   scale: float, head_layout: int = NHD,
-                  exact_weights: bool = False) -> "PagedAttentionPlan":
+                  exact_weights: bool = False, fast_weights: bool = False) -> "PagedAttentionPlan":
         """CudaBf16PagedAttentionExecutor::plan / build_plan
-        (crates/sglang-srt/src/cuda_attention.rs:438-572). `exact_weights`
-        sets ATTN_EXACT_WEIGHTS on the plan the C entry point returns."""
+        (crates/sglang-srt/src/cuda_attention.rs:438-572). `exact_weights` /
+        `fast_weights` set ATTN_EXACT_WEIGHTS / ATTN_FAST_WEIGHTS on the plan
+        the C entry point returns."""
         out = _AttentionPlan()
         _call(lib().sgl_kv_attention_plan_for_layer, ctypes.byref(layout._c), layer, query_count,
               request_count, sequence_slot_count, query_head_count, scale, head_layout,
               ctypes.byref(out))
         if exact_weights:
             out.config.flags |= ATTN_EXACT_WEIGHTS
+        if fast_weights:
+            out.config.flags |= ATTN_FAST_WEIGHTS
         return cls(out)
 
     def __getattr__(self, name):

@@ -66,22 +66,26 @@ def test_plan_region_errors_keep_the_reference_fields(goldens):
 
 
 def test_plan_flags(goldens):
-    """ATTN_EXACT_WEIGHTS (no counterpart in the reference) is the one
-    plan flag: both constructors carry it, plan_new refuses other bits."""
+    """The plan flags (no counterpart in the reference): 0 is the default
+    (hi + lo weights everywhere), ATTN_EXACT_WEIGHTS names it and
+    ATTN_FAST_WEIGHTS asks the latent body for one bf16 per weight; both
+    constructors carry them, plan_new refuses unknown bits and the pair."""
     g = goldens["paged_attention_plan"]
     cfg = _config(g["base_config"], g["gqa"]["patch"])
     assert kv.PagedAttentionPlan.new(**cfg).flags == 0
     plan = kv.PagedAttentionPlan.new(**cfg, exact_weights=True)
     assert plan.flags == kv.ATTN_EXACT_WEIGHTS == 1
+    assert kv.PagedAttentionPlan.new(**cfg, fast_weights=True).flags == kv.ATTN_FAST_WEIGHTS == 2
     f = g["from_layout"]
     lay = kv.PagedKvCacheLayout.new(_runtime(f["runtime"]), f["page_count"])
     assert kv.PagedAttentionPlan.for_layer(lay, 1, 5, 2, 5, 4, 0.5, exact_weights=True).flags == 1
-    for bad in (2, 0x80000000, 3):
+    assert kv.PagedAttentionPlan.for_layer(lay, 1, 5, 2, 5, 4, 0.5, fast_weights=True).flags == 2
+    for bad in (4, 0x80000000, 3, 7):
         plan._c.config.flags = bad
         out = type(plan._c)()
         with pytest.raises(kv.KvError) as ei:
             kv._call(kv.lib().sgl_kv_attention_plan_new, ctypes.byref(plan._c.config), ctypes.byref(out))
-        assert ei.value.name == "flags" and ei.value.fields[:2] == (bad, 1)
+        assert ei.value.name == "flags" and ei.value.fields[:2] == (bad, 3)
 
 
 def _runtime(rt, dtype=None):

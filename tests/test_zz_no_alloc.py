@@ -3,9 +3,11 @@ sgl_rocm_kv_paged_attention_async_noalloc, through the C ABI: on two calls in
 a row (the second smaller), its outputs equal those of
 sgl_rocm_kv_paged_attention_async on the same arguments, bit for bit (same
 kernels, same splits; only where the split records live differs), for a GQA
-decode and an MLA decode whose sequences are split across workgroups; and a
-launch whose split records exceed the static workspace is refused before
-anything is enqueued.
+decode and an MLA decode whose sequences are split across workgroups; calls
+made back to back on two streams and from two contexts of one device (which
+share that device's workspace) are ordered on the device and each still
+equals the allocating entry point's result; and a launch whose split records
+exceed the static workspace is refused before anything is enqueued.
 """
 import numpy as np
 import pytest
@@ -97,6 +99,43 @@ def test_noalloc_matches_the_allocating_entry_point_twice(k, shape):
     # and the first shape again after the smaller one (the workspace keeps
     # the last call's records; nothing depends on them)
     np.testing.assert_array_equal(big.run(k, noalloc=True), big.run(k, noalloc=False))
+
+
+def test_noalloc_calls_on_two_streams_and_two_contexts_are_ordered(k):
+    """Twelve no-allocation decodes issued back to back, with no host wait,
+    alternating between two streams and two contexts of one device, GQA
+    (fp32 split records) and MLA (scaled fp16 records) in turn: all of them
+    write their records at the start of the one workspace. Each call waits
+    on the device for the previous call's combine, so every output equals
+    the allocating entry point's, bit for bit."""
+    rng = np.random.default_rng(515)
+    gqa = _Decode(rng, 64, 8, 128, 128, 32, [4096, 3000, 4096, 2500, 4096, 1234])
+    mla = _Decode(rng, 64, 1, 576, 512, 128, [8192, 6000, 8192, 4097])
+    want = {id(gqa): gqa.run(k, noalloc=False), id(mla): mla.run(k, noalloc=False)}
+    k2 = kv.RocmKvPairCopyKernels(0)
+    s1, s2 = hip.Stream(), hip.Stream()
+    order = [(gqa, k, s1), (mla, k2, s2), (gqa, k2, s2), (mla, k, s1), (mla, k2, s1), (gqa, k, s2)] * 2
+    # every output is allocated and filled before the first launch: a fill
+    # on the null stream would otherwise wait for the streams' work
+    outs = []
+    for case, _, _ in order:
+        out = hip.DeviceBuffer(case.plan.output_required_bytes)
+        out.fill(0xFF)
+        outs.append(out)
+    hip.synchronize()
+    _say("noalloc: 12 decodes on two streams and two contexts")
+    for (case, ctx, s), out in zip(order, outs):
+        ctx.paged_attention_async_noalloc(case.plan, max_sequence_length=case.max_len, output=out, stream=s,
+                                          **case.bufs)
+    s1.synchronize()
+    s2.synchronize()
+    k.check_errors()
+    k2.check_errors()
+    for i, ((case, _, _), out) in enumerate(zip(order, outs)):
+        np.testing.assert_array_equal(out.download(dtype=np.uint16), want[id(case)], err_msg=f"call {i}")
+    s1.destroy()
+    s2.destroy()
+    k2.close()
 
 
 def test_noalloc_refuses_records_beyond_the_workspace(k):

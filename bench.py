@@ -877,7 +877,8 @@ def run_attention(args, config: str):
                 sequence_slots=hip.DeviceBuffer.from_array(t.dst_slots), pool=pool)
     outs = [hip.DeviceBuffer(nreq * qh * dv * 2) for _ in range(L)]
     plans = [kv.PagedAttentionPlan.for_layer(layout, l, nreq, nreq, len(t.dst_slots), qh,
-                                             scale, kv.HND if hnd else kv.NHD)
+                                             scale, kv.HND if hnd else kv.NHD,
+                                             fast_weights=args.fast_weights)
              for l in range(L)]
     s = hip.Stream()
     hip.synchronize()
@@ -921,7 +922,8 @@ def run_attention(args, config: str):
     log(f"attention avg {avg * 1e3:.1f} us per layer ({achieved:.0f} GB/s, "
         f"{launch_flops / avg / 1e9:.1f} TFLOP/s), wall {gbs:.0f} GB/s")
     k.close()
-    kernel = ("sglkv_paged_attention_latent+sglkv_paged_attention_combine_h" if mla
+    latent = "sglkv_paged_attention_latent" if args.fast_weights else "sglkv_paged_attention_latent_exact"
+    kernel = (latent + "+sglkv_paged_attention_combine_h" if mla
               else ("sglkv_paged_attention_staged64" if D == 64 else "sglkv_paged_attention_staged256" if D == 256
                     else "sglkv_paged_attention_staged128k" if hnd else "sglkv_paged_attention_staged128")
               + "+sglkv_paged_attention_combine")
@@ -930,6 +932,7 @@ def run_attention(args, config: str):
     extra = {"requests": nreq, "tokens_per_request": n, "layers": L, "kv_heads": H,
              "query_heads": qh, "key_dim": dk, "value_dim": dv, "page_size": P,
              "head_layout": "HND" if hnd else "NHD",
+             "softmax_weights": "one bf16 (ATTN_FAST_WEIGHTS)" if args.fast_weights else "hi + lo bf16 (default)",
              "algorithmic_bytes_per_step": launch_bytes * L}
     return {
         "value": round(gbs, 1),
@@ -1089,6 +1092,9 @@ def main():
                     help="time the all-core CPU baseline on the whole workload (when host RAM "
                          "holds both pools and the rows) instead of its first 8192 tokens")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--fast-weights", action="store_true",
+                    help="attention configs: plans with ATTN_FAST_WEIGHTS (the MLA latent body rounds "
+                         "each softmax weight to one bf16 instead of a hi + lo pair)")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="after timing, run 3 hipMemcpyDtoD copies of exactly 1 GiB: a plain copy "
                          "kernel of known size that calibrates rocprofv3's FETCH_SIZE/WRITE_SIZE")

@@ -481,6 +481,11 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
     // The latent body writes scaled fp16 records (SGLKV_ATTN_HPAD), the
     // others fp32 ones (SGLKV_ATTN_OPAD).
     const bool half_records = which == 6;
+    // The fp16 records and their combine are laid out for the latent body's
+    // 512-wide values (SGLKV_ATTN_HPAD); nothing else selects that body.
+    if (half_records && p.dv != 512)
+        return fail(SGL_KV_INVALID_ARGUMENT, "value_head_dim", p.dv, 512, 0,
+                    "the latent body's fp16 split records need 512-wide values, not %u", (unsigned)p.dv);
     if (splits > 1) {
         uint64_t bytes;
         const uint64_t per_record = half_records ? 2ull * SGLKV_ATTN_HPAD(p.dv) + 16 : 4ull * (SGLKV_ATTN_OPAD(p.dv) + 2);

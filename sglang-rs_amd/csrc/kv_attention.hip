@@ -56,16 +56,27 @@ template <bool VEC>
 __device__ __forceinline__ sglkv_u16x8 attn_load8(uint64_t row, uint32_t dim, uint32_t limit,
                                                   bool valid) {
     sglkv_u16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (!valid) return v;
     if (VEC) {
-        if (dim < limit)
+        if (valid && dim < limit)
             v = *reinterpret_cast<__attribute__((address_space(1))) const sglkv_u16x8 *>(row + 2ull * dim);
     } else {
+        // Branch- and compare-free: an element past the row (or of an
+        // invalid token) loads the row's element 0 and is masked to zero.
+        // The caller's row always addresses pool memory (an invalid token's
+        // row is slot 0's), so the load stays in bounds. The masks are
+        // vector values: (i - limit) >> 31 (arithmetic) is all ones exactly
+        // when i < limit (both below 2^31); a compare per element would keep
+        // a 64-bit lane mask per load alive in scalar registers until its
+        // data returns, more than the SGPR file holds.
         const __attribute__((address_space(1))) uint16_t *p =
             reinterpret_cast<__attribute__((address_space(1))) const uint16_t *>(row);
+        const uint32_t vm = valid ? 0xFFFFFFFFu : 0u;
 #pragma unroll
-        for (uint32_t e = 0; e < 8; ++e)
-            if (dim + e < limit) v[e] = p[dim + e];
+        for (uint32_t e = 0; e < 8; ++e) {
+            const uint32_t i = dim + e;
+            const uint32_t keep = static_cast<uint32_t>(static_cast<int32_t>(i - limit) >> 31) & vm;
+            v[e] = static_cast<uint16_t>(p[i & keep] & keep);
+        }
     }
     return v;
 }
@@ -364,14 +375,18 @@ __device__ __forceinline__ void attn_body(const sglkv_attn_params &p) {
             vrow[b] = vbase + page * p.page_stride + pos * p.value_token_stride;
             valid[b] = ok;
         }
-        // Value pieces first, so their loads are in flight during q.k: lane
-        // (g, r) loads dims d0 + 8*(g + 4s) .. +7 of its two tokens.
+        // Lane (g, r) loads value dims d0 + 8*(g + 4s) .. +7 of its two
+        // tokens. 16-byte pieces are issued first, so their loads are in
+        // flight during q.k; element-wise pieces (64 separate 2-byte loads)
+        // after it, where they do not hold registers across the q.k loop.
         sglkv_u16x8 vpiece[2][4];
+        if (VEC) {
 #pragma unroll
-        for (uint32_t b = 0; b < 2; ++b)
+            for (uint32_t b = 0; b < 2; ++b)
 #pragma unroll
-            for (uint32_t s = 0; s < 4; ++s)
-                vpiece[b][s] = attn_load8<VEC>(vrow[b], w.d0 + 8 * (g + 4 * s), p.dv, valid[b]);
+                for (uint32_t s = 0; s < 4; ++s)
+                    vpiece[b][s] = attn_load8<VEC>(vrow[b], w.d0 + 8 * (g + 4 * s), p.dv, valid[b]);
+        }
 
         // Scores: s[b][e] = q(head r) . k(token of row 4g+e of block b).
         sglkv_f32x4 sc[2] = {sglkv_f32x4{0.f, 0.f, 0.f, 0.f}, sglkv_f32x4{0.f, 0.f, 0.f, 0.f}};
@@ -385,6 +400,13 @@ __device__ __forceinline__ void attn_body(const sglkv_attn_params &p) {
             }
         }
 
+        if (!VEC) {
+#pragma unroll
+            for (uint32_t b = 0; b < 2; ++b)
+#pragma unroll
+                for (uint32_t s = 0; s < 4; ++s)
+                    vpiece[b][s] = attn_load8<VEC>(vrow[b], w.d0 + 8 * (g + 4 * s), p.dv, valid[b]);
+        }
         // Transposed values into LDS: vt[dim][token - tb].
 #pragma unroll
         for (uint32_t b = 0; b < 2; ++b) {
@@ -891,6 +913,15 @@ __device__ __forceinline__ void attn_wide_pv(const sglkv_attn_params &p, const u
     // value block is computed: staged dims past dv are zero, and the finish
     // writes none of them.
     const uint16_t *v0 = vs + (4 * g + (r >> 2)) * G::VS + 4 * (r & 3) + 16 * j0;
+    if (EXACT) {
+        // The exact path runs in a loop of its own (the rare recompute of a
+        // split): an opaque base keeps the compiler from hoisting the
+        // 2 * NJH read addresses out of that loop into registers it then
+        // has to spill; it forms them per block instead.
+        uintptr_t a = reinterpret_cast<uintptr_t>(v0);
+        asm volatile("" : "+v"(a));
+        v0 = reinterpret_cast<const uint16_t *>(a);
+    }
     attn_i16x4 vlo[G::NJH], vhi[G::NJH];
 #pragma unroll
     for (uint32_t j = 0; j < G::NJH; ++j) {
@@ -966,14 +997,17 @@ __device__ __forceinline__ void attn_wide_body(const sglkv_attn_params &p) {
     // This half's queries: lane (g, r) holds head r, dims 32(kc0 + c) + 8g
     // .. +7 (zero past the group or past dk); the host requires 16-byte
     // aligned queries.
-    sglkv_u16x8 qf[G::KH];
+    auto load_queries = [&](sglkv_u16x8(&qv)[G::KH]) {
 #pragma unroll
-    for (uint32_t c = 0; c < G::KH; ++c) {
-        const uint32_t d = 32 * (kc0 + c) + 8 * g;
-        qf[c] = sglkv_u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-        if (r < w.nh && d < p.dk)
-            qf[c] = *reinterpret_cast<const sglkv_u16x8 *>(p.queries + (q * p.query_heads + w.h0 + r) * p.dk + d);
-    }
+        for (uint32_t c = 0; c < G::KH; ++c) {
+            const uint32_t d = 32 * (kc0 + c) + 8 * g;
+            qv[c] = sglkv_u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+            if (r < w.nh && d < p.dk)
+                qv[c] = *reinterpret_cast<const sglkv_u16x8 *>(p.queries + (q * p.query_heads + w.h0 + r) * p.dk + d);
+        }
+    };
+    sglkv_u16x8 qf[G::KH];
+    load_queries(qf);
 
     // The chunk's slots, checked once; tokens past t1 are invalid.
     if (tid == 0) *redo = 0;
@@ -986,11 +1020,19 @@ __device__ __forceinline__ void attn_wide_body(const sglkv_attn_params &p) {
     const uint64_t pool = reinterpret_cast<uint64_t>(p.pool);
     const uint64_t kbase = pool + p.key_offset + kvh * p.key_head_stride;
     const uint64_t vbase = pool + p.value_offset + kvh * p.value_head_stride;
-    attn_wide_stage<DKC, NJ> ra, rb;  // K rows: two stages; V rows: ra.v
+    // K rows in registers: two stages where the register file has room
+    // (block k+2's rows load while block k+1's wait for LDS); one stage for
+    // 576-wide keys, where two stages with the 16 value accumulators and the
+    // queries would not fit a wave's 256 registers (8 waves per workgroup,
+    // two per SIMD): there block k+2's rows load only once block k+1's are
+    // in LDS. V rows: ra.v.
+    constexpr bool two_stages = DKC < 18;
+    attn_wide_stage<DKC, NJ> ra, rb;
     attn_wide_load_k<DKC, NJ>(p, kbase, slots, tid, ra);
     attn_wide_load_v<DKC, NJ>(p, vbase, slots, tid, ra);
-    attn_wide_load_k<DKC, NJ>(p, kbase, slots + (nb > 1 ? B : 0), tid, rb);
+    if (two_stages) attn_wide_load_k<DKC, NJ>(p, kbase, slots + (nb > 1 ? B : 0), tid, rb);
     attn_wide_store_k<DKC, NJ>(ks, tid, ra);
+    if (!two_stages) attn_wide_load_k<DKC, NJ>(p, kbase, slots + (nb > 1 ? B : 0), tid, ra);
     __syncthreads();
 
     attn_state_n<G::NJH> st;
@@ -1008,22 +1050,28 @@ __device__ __forceinline__ void attn_wide_body(const sglkv_attn_params &p) {
     // skips it are never written.
     auto step = [&](uint32_t k, attn_wide_stage<DKC, NJ> &fr, attn_wide_stage<DKC, NJ> &next) {
         const uint32_t k1 = k + 1 < nb ? k + 1 : nb - 1, k2 = k + 2 < nb ? k + 2 : nb - 1;
-        attn_wide_load_k<DKC, NJ>(p, kbase, slots + k2 * B, tid, fr);
+        if (two_stages) attn_wide_load_k<DKC, NJ>(p, kbase, slots + k2 * B, tid, fr);
         sglkv_f32x4 sc[2];
         attn_wide_qk<DKC, NJ, false>(ks, qf, kc0, g, r, lane, sc, sxw);
         attn_wide_store_v<DKC, NJ>(vs, tid, ra);
         attn_wide_load_v<DKC, NJ>(p, vbase, slots + k1 * B, tid, ra);
-        // Slot reads, then K-row loads between the q.k MFMAs, LDS reads of
-        // K running QK_AHEAD k-steps ahead.
+        // Slot reads, then row loads (K with two stages, V with one) between
+        // the q.k MFMAs, LDS reads of K running QK_AHEAD k-steps ahead.
+        constexpr uint32_t vmem = two_stages ? G::KPT + (G::RTHREADS ? 1 : 0) : G::VPT;
         __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 + 2 * G::QK_AHEAD, 0);
 #pragma unroll
         for (uint32_t c = 0; c < G::KH; ++c) {
             __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
-            if (c < G::KPT + (G::RTHREADS ? 1 : 0)) __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
+            if (c < vmem) __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
             if (c + G::QK_AHEAD < G::KH) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
         }
         __syncthreads();
-        attn_wide_store_k<DKC, NJ>(ks, tid, next);
+        if (two_stages) {
+            attn_wide_store_k<DKC, NJ>(ks, tid, next);
+        } else {  // the one stage: block k+1's rows to LDS, then block k+2's loads
+            attn_wide_store_k<DKC, NJ>(ks, tid, ra);
+            attn_wide_load_k<DKC, NJ>(p, kbase, slots + k2 * B, tid, ra);
+        }
         if (active) attn_wide_pv<false, DKC, NJ, false>(p, vs, sc, sxo, slots + k * B, j0, g, r, lane, st, &over);
         __syncthreads();
     };
@@ -1037,8 +1085,12 @@ __device__ __forceinline__ void attn_wide_body(const sglkv_attn_params &p) {
     // Read as a wave-uniform value, so the branch is a scalar one.
     if (__builtin_amdgcn_readfirstlane(*redo)) {
         // A block outran the fixed reference by more than the bound: the
-        // split again, one block at a time, with the running maximum.
+        // split again, one block at a time, with the running maximum. The
+        // queries are read again rather than kept from the main loop, whose
+        // registers are then free for this path's exact p.v.
         attn_state_init(st);
+        sglkv_u16x8 qr[G::KH];
+        load_queries(qr);
         for (uint32_t k = 0; k < nb; ++k) {
             attn_wide_load_k<DKC, NJ>(p, kbase, slots + k * B, tid, ra);
             attn_wide_load_v<DKC, NJ>(p, vbase, slots + k * B, tid, ra);
@@ -1046,7 +1098,7 @@ __device__ __forceinline__ void attn_wide_body(const sglkv_attn_params &p) {
             attn_wide_store_v<DKC, NJ>(vs, tid, ra);
             __syncthreads();
             sglkv_f32x4 sc[2];
-            if (active) attn_wide_qk<DKC, NJ>(ks, qf, kc0, g, r, lane, sc, sxw);
+            if (active) attn_wide_qk<DKC, NJ>(ks, qr, kc0, g, r, lane, sc, sxw);
             __syncthreads();
             if (active) attn_wide_pv<true, DKC, NJ>(p, vs, sc, sxo, slots + k * B, j0, g, r, lane, st, &over);
             __syncthreads();
@@ -2124,7 +2176,8 @@ extern "C" __global__ __launch_bounds__(64) void sglkv_paged_attention_v16(sglkv
     attn_body<true>(p);
 }
 
-extern "C" __global__ __launch_bounds__(64) void sglkv_paged_attention_v2(sglkv_attn_params p) {
+extern "C" __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void
+sglkv_paged_attention_v2(sglkv_attn_params p) {
     attn_body<false>(p);
 }
 
@@ -2327,7 +2380,11 @@ extern "C" __global__ __launch_bounds__(256) void sglkv_paged_attention_combine_
     const uint16_t *y = attn_rec_y(p, i0);
     const uint32_t hpad = SGLKV_ATTN_HPAD(p.dv);
     uint16_t *out = p.output + (q * p.query_heads + head) * p.dv;
-    for (uint32_t d = 8 * lane; d < p.dv; d += 512) {  // the same trip count in every wave
+    // Every lane of every wave runs the same iterations (the barriers below
+    // need that); a lane past the row loads element 0 and stores nothing.
+    for (uint32_t d0 = 0; d0 < p.dv; d0 += 512) {
+        const bool active = d0 + 8 * lane < p.dv;
+        const uint32_t d = active ? d0 + 8 * lane : 0;
         float m = -3.402823466e+38f, l = 0.0f;
         float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
         for (uint32_t s0 = 8 * wave; s0 < used; s0 += 8 * nw) {
@@ -2381,7 +2438,7 @@ extern "C" __global__ __launch_bounds__(256) void sglkv_paged_attention_combine_
             }
             __syncthreads();
         }
-        if (wave != 0) continue;
+        if (wave != 0 || !active) continue;
         const float linv = 1.0f / l;
         sglkv_u16x8 o8;
 #pragma unroll

@@ -44,6 +44,33 @@ def test_code_object_is_built_for_gfx950():
     assert int.from_bytes(head[48:52], "little") & 0xFF == 0x4F
 
 
+def test_code_object_kernels_spill_nothing():
+    """Every kernel of the code object keeps its state in registers and LDS:
+    no private (scratch) segment and no VGPR or SGPR spills, read from the
+    code object's metadata notes (llvm-readelf --notes, from the ROCm
+    toolchain)."""
+    import re
+    import shutil
+    import subprocess
+    readelf = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "llvm", "bin", "llvm-readelf")
+    if not os.path.exists(readelf):
+        readelf = shutil.which("llvm-readelf")
+    if not readelf:
+        pytest.skip("llvm-readelf is not available to read the code object's notes")
+    notes = subprocess.run([readelf, "--notes", kv.CODE_OBJECT_PATH], capture_output=True, text=True,
+                           check=True).stdout
+    kernels = re.split(r"\n\s+- \.agpr_count:", notes)[1:]
+    assert len(kernels) >= 40, len(kernels)
+    bad = []
+    for k in kernels:
+        name = re.search(r"\.name:\s+(\S+)", k).group(1)
+        fields = {f: int(re.search(rf"\.{f}:\s+(\d+)", k).group(1))
+                  for f in ("private_segment_fixed_size", "vgpr_spill_count", "sgpr_spill_count")}
+        if any(fields.values()):
+            bad.append((name, fields))
+    assert not bad, bad
+
+
 def _runtime(d, **patch):
     r = dict(d)
     r.update(patch)

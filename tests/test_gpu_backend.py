@@ -38,9 +38,10 @@ def k():
     ctx.close()
 
 
-def _layouts():
-    pre = kv.PagedKvCacheLayout.new(kv.KvCacheRuntimeLayout.for_model("bf16", P_PREFILL, L, H, D),
-                                    PREFILL_PAGES)
+def _layouts(p_prefill=P_PREFILL):
+    """The prefill pool holds PREFILL_PAGES * P_PREFILL slots at any page size."""
+    pre = kv.PagedKvCacheLayout.new(kv.KvCacheRuntimeLayout.for_model("bf16", p_prefill, L, H, D),
+                                    PREFILL_PAGES * P_PREFILL // p_prefill)
     dec = kv.PagedKvCacheLayout.new(kv.KvCacheRuntimeLayout.for_model("bf16", P_DECODE, L, H, D),
                                     DECODE_PAGES)
     return pre, dec
@@ -57,8 +58,8 @@ class _Pools:
     """Seeded prefill and decode pools on the device, with host copies of
     what the decode pool must hold after the submitted spans."""
 
-    def __init__(self, seed):
-        self.pre, self.dec = _layouts()
+    def __init__(self, seed, p_prefill=P_PREFILL):
+        self.pre, self.dec = _layouts(p_prefill)
         rng = np.random.default_rng(seed)
         self.src_h = rng.integers(0, 256, self.pre.total_byte_len, dtype=np.uint8)
         self.dst_h = rng.integers(0, 256, self.dec.total_byte_len, dtype=np.uint8)
@@ -432,6 +433,79 @@ def test_prefill_batch_plan_drives_the_backend(k, mode):
         b.submit(room, sums[room], s.token_offset, cache_slots, table)
         if s.token_count:
             pools.expect(s.token_offset, cache_slots, table)
+    b.wait()
+    events, pending = b.poll()
+    assert pending == 0 and [e.bootstrap_room for e in events] == sorted(sums)
+    for e in events:
+        assert e.status == kv.TRANSFER_COMPLETED and e.descriptor_checksum == sums[e.bootstrap_room]
+    pools.check()
+    b.close()
+
+
+@pytest.mark.parametrize("mode", [kv.BACKEND_DIRECT, kv.BACKEND_STAGED])
+@pytest.mark.parametrize("p_prefill", [16, 64])
+def test_prefill_batch_plan_with_prefill_pages(k, mode, p_prefill):
+    """The same route with prefill pages of 16 and 64 tokens, where the
+    plan's page rules bite (transfer.rs:679-720): cached prefixes are matched
+    page-aligned (match_prefix_page_aligned rounds 50 cached tokens down to
+    whole pages), each uncached suffix starts on a fresh page of the
+    allocator, so its slots are page-aligned and contiguous within each page,
+    and the span's page indices are those pages. A batch whose cached prefix
+    is not a whole number of prefill pages (the plain match) is refused with
+    UnalignedTokenOffset before anything reaches the backend, and the decode
+    pool is unchanged by it. Every decode-pool byte matches the oracle."""
+    P = p_prefill
+    rng = np.random.default_rng(500 + P + mode)
+    pools = _Pools(seed=50 + P + mode, p_prefill=P)
+    slots_total = PREFILL_PAGES * P_PREFILL
+    alloc = kv.CachePageAllocator(slots_total, P)
+    cache = kv.RadixCache()
+    shared = [int(t) for t in rng.integers(0, 1000, 2 * P + P // 2 + 3)]   # cached: two pages and a part
+    cache.insert(shared, alloc.allocate(len(shared)))
+    prompts = [shared + [int(t) for t in rng.integers(0, 5000, 3 * P + 5)],   # two pages cached
+               [int(t) for t in rng.integers(5000, 6000, P + 7)],             # nothing cached
+               shared[:P + 3] + [int(t) for t in rng.integers(0, 5000, 40)]]  # one page cached
+    has_params = [1, 1, 1]
+    cached, inputs, slots = [], [], []
+    for p in prompts:
+        m = cache.match_prefix_page_aligned(p, P)
+        cached.append(m.matched_token_count)
+        inputs.append(len(m.remaining_input_ids))
+        slots += alloc.allocate(len(m.remaining_input_ids))
+    assert cached == [2 * P, 0, P]
+    spans = kv.transfer_plan_from_prefill_batch(inputs, cached, has_params, slots, P)
+    assert [s.token_offset for s in spans] == cached
+    for s in spans:   # whole pages of the allocator: the first slot page-aligned, pages contiguous
+        pages = np.asarray(s.cache_pages, np.int64)
+        assert pages[0] % P == 0 and (np.diff(pages)[np.arange(1, len(pages)) % P != 0] == 1).all()
+        assert list(s.page_indices) == sorted(set((pages // P).tolist()), key=list(pages // P).index)
+    _say(f"batch plan, prefill pages of {P}: {len(spans)} spans, {sum(s.token_count for s in spans)} tokens "
+         f"({'direct' if mode == kv.BACKEND_DIRECT else 'staged'})")
+    b = kv.RocmKvTransferBackend(k, mode, max_rows=512)
+    pools.register(b)
+
+    # A batch with an unaligned cached prefix (the plain match): refused by the plan.
+    m = cache.match_prefix(prompts[0])
+    assert m.matched_token_count == len(shared) and m.matched_token_count % P
+    bad_slots = alloc.allocate(len(m.remaining_input_ids))
+    with pytest.raises(kv.KvError) as ei:
+        kv.transfer_plan_from_prefill_batch([len(m.remaining_input_ids)], [m.matched_token_count], [1],
+                                            bad_slots, P)
+    assert ei.value.variant == "UnalignedTokenOffset"
+    assert ei.value.fields == (0, m.matched_token_count, P)
+    assert b.poll() == ([], 0)
+
+    groups = rng.permutation(DECODE_PAGES).reshape(8, -1)
+    sums = {}
+    for i, s in enumerate(spans):
+        room = 70 + s.request_index
+        need = -(-(s.token_offset + s.token_count) // P_DECODE)
+        table = rng.choice(groups[i], size=need, replace=False).astype(np.int32)
+        sums[room] = kv.transfer_span_checksum(f"req-{room}", "10.0.0.8", 8200, room, 0, s.token_offset,
+                                               s.token_count, P, s.cache_pages, s.page_indices)
+        cache_slots = np.asarray(s.cache_pages, dtype=np.uint64)
+        b.submit(room, sums[room], s.token_offset, cache_slots, table)
+        pools.expect(s.token_offset, cache_slots, table)
     b.wait()
     events, pending = b.poll()
     assert pending == 0 and [e.bootstrap_room for e in events] == sorted(sums)

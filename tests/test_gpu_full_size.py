@@ -10,13 +10,21 @@ decode pool and packs every layer again from the decode pool. Then:
   - the packed rows of the first, middle and last layers equal the source
     words recomputed on the host at each row's source slot, for every row;
   - a random sample of rows of every other layer does too;
+  - the destination pool itself, read back region by region with plain
+    copies and addressed on the host: every row of the first, middle and
+    last layers sits at its destination slot (NHD or HND) holding the
+    source words, every other byte of those layers' regions in the pages
+    the destination table names still holds the destination's own fill,
+    and a seeded sample of 64 pages the table does not name is unchanged
+    in full (on C2 these reads reach offsets past 2^32 bytes);
   - the re-packed rows equal the packed rows on every layer (the unpack
     placed every row where the destination slots say, as the re-pack reads
     them; the unpack itself is compared with the oracle on the same shapes
     at reduced size in tests/test_gpu_parity.py and test_gpu_mla_pools.py).
 
-Source byte addresses come from the workload's own page-major arithmetic
-(workloads.PoolSpec, restating kv_cache.rs:653-700), not from the product.
+Source and destination byte addresses come from the workload's own
+page-major arithmetic (workloads.PoolSpec, restating kv_cache.rs:653-700),
+not from the product.
 
 C5 runs its request waves (workloads.waves) through the staged layer
 pipeline (pack -> pinned host -> unpack on four streams) and checks, wave by
@@ -105,6 +113,83 @@ def _check_layer_rows(rows_buf, t, sh, layer, seed, sample=None, rng=None):
         plane += n * rb
 
 
+def _fill_bytes(seed, start, nbytes):
+    """Bytes [start, start + nbytes) of a buffer filled with the FILL_BITS
+    stream of `seed`."""
+    w0 = start // 8
+    nw = (start + nbytes + 7) // 8 - w0
+    words = kv.synthetic_words(seed, np.arange(w0, w0 + nw, dtype=np.uint64))
+    return words.view(np.uint8)[start - 8 * w0: start - 8 * w0 + nbytes]
+
+
+def _check_destination(dst, t, sh, layer, label):
+    """Every row of `layer` read straight from the destination pool at its
+    destination slot (host arithmetic, head chunk by head chunk on HND
+    pages), against the source words; every other byte of the layer's
+    regions in the pages the rows touch against the destination fill.
+    Returns the largest pool offset read."""
+    spec, P = t.dst, t.dst.page_size
+    region_bytes = P * sh.layer_row_bytes        # the layer's tensors, consecutive in a page
+    region0 = spec.tensor_offsets(sh, layer)[0]
+    dslots = np.asarray(t.dst_slots, np.int64)
+    pages, where = np.unique(dslots // P, return_inverse=True)
+    got = np.empty((len(pages), region_bytes), np.uint8)
+    top = 0
+    for i, page in enumerate(pages):
+        off = int(page) * spec.page_stride(sh) + region0
+        got[i] = dst.download(region_bytes, off)
+        top = max(top, off + region_bytes)
+    written = np.zeros_like(got, dtype=bool)
+    pos = dslots % P
+    for tensor in range(sh.tensors):
+        rb = sh.tensor_row_bytes(tensor)
+        toff = spec.tensor_offsets(sh, layer)[tensor] - region0
+        chunks = sh.heads if spec.head_layout == kv.HND else 1
+        c = rb // chunks
+        for lo in range(0, t.rows, 16384):
+            hi = min(t.rows, lo + 16384)
+            want = _source_bytes(SEED, t.src, sh, layer, tensor, t.src_slots[lo:hi])
+            for h in range(chunks):
+                if spec.head_layout == kv.HND:
+                    at = toff + (h * P + pos[lo:hi]) * c
+                else:
+                    at = toff + pos[lo:hi] * rb + h * c
+                idx = at[:, None] + np.arange(c)[None, :]
+                rows = where[lo:hi][:, None]
+                np.testing.assert_array_equal(got[rows, idx], want[:, h * c:(h + 1) * c],
+                                              err_msg=f"{label} layer {layer} tensor {tensor} head {h} rows {lo}..{hi}")
+                written[rows, idx] = True
+    # the rest of those regions: the destination's own fill, untouched
+    for i, page in enumerate(pages):
+        if written[i].all():
+            continue
+        off = int(page) * spec.page_stride(sh) + region0
+        fill = _fill_bytes(SEED + 1, off, region_bytes)
+        keep = ~written[i]
+        assert np.array_equal(got[i][keep], fill[keep]), f"{label} layer {layer} page {page}: stray write"
+    return top
+
+
+def _check_untouched_pages(dst, t, sh, label, count=64, seed=17):
+    """`count` seeded pages that no destination slot names, each compared in
+    full with the destination's fill. Returns the largest offset read."""
+    spec = t.dst
+    used = np.unique(np.asarray(t.dst_slots, np.int64) // spec.page_size)
+    free = np.setdiff1d(np.arange(spec.page_count), used)
+    if not len(free):   # C4: 262,144 rows fill all 4,096 pages; the region checks cover them
+        _say(f"{label}: the destination table names every page")
+        return 0
+    rng = np.random.default_rng(seed)
+    top = 0
+    for page in rng.choice(free, size=min(count, len(free)), replace=False):
+        off = int(page) * spec.page_stride(sh)
+        n = spec.page_stride(sh)
+        assert np.array_equal(dst.download(n, off), _fill_bytes(SEED + 1, off, n)), \
+            f"{label}: page {page} outside the destination table changed"
+        top = max(top, off + n)
+    return top
+
+
 def _equal_on_host(a, b, nbytes, chunk=1 << 30):
     for off in range(0, nbytes, chunk):
         m = min(chunk, nbytes - off)
@@ -134,7 +219,7 @@ def _full_size(k, t, label):
     k.unpack_layers(pa, n * lrb, L, n, _view(dst, t.dst, sh, 0), dstride, _db(ds))
     k.pack_layers(_view(dst, t.dst, sh, 0), dstride, L, _db(ds), n, pb, n * lrb)
     k.check_errors()
-    del src, dst
+    del src
     rng = np.random.default_rng(3)
     full = sorted({0, L // 2, L - 1})
     for layer in range(L):
@@ -143,14 +228,24 @@ def _full_size(k, t, label):
             _check_layer_rows(packed, t, sh, layer, SEED)
         else:
             _check_layer_rows(packed, t, sh, layer, SEED, sample=64, rng=rng)
+    top = 0
+    for layer in full:
+        _say(f"{label}: layer {layer} read straight from the destination pool")
+        top = max(top, _check_destination(dst, t, sh, layer, label))
+    _say(f"{label}: 64 pages outside the destination table")
+    top = max(top, _check_untouched_pages(dst, t, sh, label))
+    del dst
     _say(f"{label}: pack -> unpack -> re-pack on all {L} layers")
     bad = _equal_on_host(packed, again, rows_bytes)
     assert bad is None, f"re-packed rows differ in the GiB at byte {bad}"
+    return top
 
 
 def test_c2_full_size_every_layer(k):
-    """C2: 131,072 rows x 32 layers (16 GiB of rows), P1 -> P64."""
-    _full_size(k, wl.c2(), "C2")
+    """C2: 131,072 rows x 32 layers (16 GiB of rows), P1 -> P64; the
+    destination reads reach past 2^32 bytes of the 32 GiB pool."""
+    top = _full_size(k, wl.c2(), "C2")
+    assert top > 1 << 32
 
 
 def test_c3_full_size_every_layer(k):

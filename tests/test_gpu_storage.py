@@ -11,6 +11,8 @@ values are the reference's literals (tests/golden/reference_goldens.json).
 The slot-map copies are checked against the oracle's literal restatement of
 the reference's scatter/gather kernels (oracle/kv_oracle.c).
 """
+import math
+
 import numpy as np
 import pytest
 
@@ -278,3 +280,102 @@ def test_storage_pools_drive_the_transfer_backend(k):
     be.close()
     decode.close()
     prefill.close()
+
+
+def _bf16(values) -> np.ndarray:
+    """f32 -> bf16 bits, round to nearest even (the reference's test helper,
+    crates/sglang-srt/tests/cuda_backend.rs:125-129, restated by the oracle)."""
+    return oracle.f32_to_bf16(np.asarray(values, np.float32))
+
+
+def test_reference_attention_over_physical_slots(k):
+    """cuda_bf16_paged_attention_reads_mooncake_registered_physical_kv_slots
+    (cuda_backend.rs:641-781): a scheduler's two-request prefill ([10, 11, 12]
+    and [20, 21] from a fresh 8-slot page allocator, page size 1) gives causal
+    metadata over its physical slots; keys (i - 11) * 0.03125 and values
+    (17 - i) * 0.046875 go into a 2-page P4 L1 H2 D4 pool through an uploaded
+    slot map (write_kv_slots_from_device); queries ((7 i mod 29) - 14) *
+    0.0625, 4 query heads, scale 1/2. The attention reads the very allocation
+    the Mooncake descriptor registers. Checked against the float64 oracle
+    within the reference's 0.02 and within bf16 rounding of the output."""
+    _say("reference attention over physical slots")
+    P, L, H, D, qh = 4, 1, 2, 4, 4
+    rt = kv.KvCacheRuntimeLayout("bf16", P, L, H, D, 2, L * H * D * 2 * 2, P * L * H * D * 2 * 2)
+    pool = kv.allocate_rocm_kv_cache(k, rt, 2)
+    layout = pool.layout()
+    # the scheduler's slots: CachePageAllocator::new(8) hands out 0, 1, 2 then 3, 4
+    alloc = kv.CachePageAllocator(8, 1)
+    a = alloc.allocate_for_sequence([], 3)
+    b = alloc.allocate_for_sequence([], 2)
+    slots = np.concatenate([a, b]).astype(np.uint64)
+    np.testing.assert_array_equal(slots, np.arange(5))
+    qri = np.array([0, 0, 0, 1, 1], np.uint32)       # one query per prefill token
+    qsl = np.array([1, 2, 3, 1, 2], np.uint64)       # causal: position + 1
+    rso = np.array([0, 3, 5], np.uint64)
+    smap = pool.storage().upload_slot_map(layout, slots)
+    n = len(slots) * H * D
+    keys_h = _bf16((np.arange(n) - 11.0) * 0.03125)
+    values_h = _bf16((17.0 - np.arange(n)) * 0.046875)
+    row = H * D * 2
+    keys, values = hip.DeviceBuffer.from_array(keys_h), hip.DeviceBuffer.from_array(values_h)
+    pool.storage_mut().write_kv_slots_from_device(k, layout, 0, smap, keys=keys, key_row_stride_bytes=row,
+                                                  values=values, value_row_stride_bytes=row)
+    q_h = _bf16(((np.arange(5 * qh * D) * 7 % 29) - 14.0) * 0.0625)
+    mem = pool.transferable_kv_cache_memory()
+    assert mem.regions()[0].base_addr == pool.storage().device_ptr
+    plan = kv.PagedAttentionPlan.for_layer(layout, 0, 5, 2, 5, qh, 1.0 / math.sqrt(D))
+    out = hip.DeviceBuffer(plan.output_required_bytes)
+    k.paged_attention(plan, queries=hip.DeviceBuffer.from_array(q_h),
+                      query_request_indices=hip.DeviceBuffer.from_array(qri),
+                      query_sequence_lengths=hip.DeviceBuffer.from_array(qsl),
+                      request_slot_offsets=hip.DeviceBuffer.from_array(rso),
+                      sequence_slots=hip.DeviceBuffer.from_array(slots),
+                      pool=pool.storage().allocation(), output=out)
+    got = oracle.bf16_to_f32(out.download().view(np.uint16)).reshape(5, qh, D)
+    pool_bytes = np.concatenate([pool.storage().read_page(layout, p) for p in range(2)])
+    want, flags = oracle.paged_attention(
+        pool_bytes, q_h.reshape(5, qh, D), qri, qsl, rso, slots, page_size=P,
+        page_stride=plan.page_stride_bytes, key_offset=plan.key_in_page_offset,
+        value_offset=plan.value_in_page_offset, kv_heads=H, dk=D, dv=D, scale=1.0 / math.sqrt(D),
+        slot_count=layout.slot_count, hnd=False)
+    assert flags == 0
+    err = np.abs(got - want)
+    assert err.max() <= 0.02                                        # the reference's tolerance
+    assert (err <= 2.0 ** -8 * np.abs(want) + 1e-3).all(), err.max()  # bf16 rounding of the output
+    smap.close()
+    pool.close()
+
+
+def test_reference_asymmetric_compressed_mla(k):
+    """cuda_bf16_paged_attention_executes_asymmetric_compressed_mla_kv
+    (cuda_backend.rs:783-882): a 1-page P4 pool of the tensor-pair layout with
+    3-dim keys (6 bytes) and 2-dim values (4 bytes); slot 0 holds key [1, 0, 0]
+    and value [10, 20], slot 1 key [0, 1, 0] and value [30, 40], each written
+    with write_tensor_slot_from_device; one query [1, 0, 0] over both slots
+    (for_single_query), scale 1. The output is w [10, 20] + (1 - w) [30, 40]
+    with w = e / (e + 1): within the reference's 0.05, and within the bf16
+    rounding of the output."""
+    _say("reference asymmetric compressed MLA")
+    rt = kv.KvCacheRuntimeLayout("bf16", 4, 1, 1, 3, 2, 10, 40)
+    layout = kv.PagedKvCacheLayout.new_with_tensor_pair(rt, 1, 6, 4)
+    storage = kv.RocmKvStorage.allocate(k, layout.total_byte_len, layout.runtime.page_size_bytes)
+    for slot, key, value in ((0, [1.0, 0.0, 0.0], [10.0, 20.0]), (1, [0.0, 1.0, 0.0], [30.0, 40.0])):
+        kb, vb = hip.DeviceBuffer.from_array(_bf16(key)), hip.DeviceBuffer.from_array(_bf16(value))
+        storage.write_tensor_slot_from_device(layout, 0, 0, slot, kb, 0)
+        storage.write_tensor_slot_from_device(layout, 0, 1, slot, vb, 0)
+        hip.synchronize()
+    slots = np.array([0, 1], np.uint64)            # CudaPagedAttentionMetadata::for_single_query
+    plan = kv.PagedAttentionPlan.for_layer(layout, 0, 1, 1, 2, 1, 1.0)
+    assert (plan.key_row_bytes, plan.value_row_bytes) == (6, 4)
+    out = hip.DeviceBuffer(plan.output_required_bytes)
+    k.paged_attention(plan, queries=hip.DeviceBuffer.from_array(_bf16([1.0, 0.0, 0.0])),
+                      query_request_indices=hip.DeviceBuffer.from_array(np.zeros(1, np.uint32)),
+                      query_sequence_lengths=hip.DeviceBuffer.from_array(np.array([2], np.uint64)),
+                      request_slot_offsets=hip.DeviceBuffer.from_array(np.array([0, 2], np.uint64)),
+                      sequence_slots=hip.DeviceBuffer.from_array(slots), pool=storage.allocation(), output=out)
+    got = oracle.bf16_to_f32(out.download().view(np.uint16))
+    w = math.e / (math.e + 1.0)
+    want = np.array([w * 10 + (1 - w) * 30, w * 20 + (1 - w) * 40])
+    assert np.abs(got - want).max() <= 0.05                          # the reference's tolerance
+    assert (np.abs(got - want) <= 2.0 ** -8 * np.abs(want) + 1e-3).all(), (got, want)
+    storage.close()

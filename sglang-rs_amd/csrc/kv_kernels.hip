@@ -57,13 +57,22 @@ extern "C" __device__ uint32_t sglkv_realign_rows_per_thread = SGLKV_REALIGN_ROW
 #endif
 // Workgroups are dispatched round-robin over the 8 XCDs (workgroup b runs
 // on XCD b % 8). A remapped direction instead gives each XCD one contiguous
-// eighth of the row tiles, so the lines of a destination page are written
-// through one L2 (measured: +2 % for unpack, -1 % for pack on MI355X).
+// eighth of the row tiles. The unpack keeps the round-robin order: the rows
+// pack has just written are still partly in the Infinity Cache (the later
+// part of each layer's rows), and round-robin tiles give every XCD an equal
+// share of cached and uncached rows, where contiguous eighths leave the XCDs
+// with the uncached first half the long pole (read latency twice that of
+// the other half in rocprofv3's per-XCD counters). Measured on MI355X, one
+// process per line with both orders on the same pools: unpack per layer C2
+// 208.1 -> 206.0 us (180.0 -> 174.7 in the other placement cluster), C3
+// 107.9 -> 90.4, C4 117.5 -> 94.9, the C4 key/value pair 192.6 -> 183.8;
+// the 64-byte-chunk HND unpack is unchanged. Pack: contiguous eighths were
+// 1 % slower.
 #ifndef SGLKV_PACK_REMAP
 #define SGLKV_PACK_REMAP 0
 #endif
 #ifndef SGLKV_UNPACK_REMAP
-#define SGLKV_UNPACK_REMAP 1
+#define SGLKV_UNPACK_REMAP 0
 #endif
 #ifndef SGLKV_TRANSFER_REMAP
 #define SGLKV_TRANSFER_REMAP 1
@@ -490,6 +499,8 @@ SGLKV_COPY_KERNELS(1)
 #ifndef SGLKV_REALIGN_TRANSFER_NT
 #define SGLKV_REALIGN_TRANSFER_NT SGLKV_TRANSFER_NT
 #endif
+// The byte-realigning unpack (649-byte packed-MLA rows) keeps contiguous
+// eighths: round-robin tiles measured 1.5 % slower there (67.6 -> 68.6 us).
 #ifndef SGLKV_REALIGN_REMAP
 #define SGLKV_REALIGN_REMAP 1
 #endif

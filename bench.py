@@ -235,6 +235,40 @@ def _views(kv, buf, spec, sh, layer, scale=None):
                         sh.tensor_row_bytes(1) != sh.row_bytes else 0)
 
 
+class _Span:
+    """A device range (ptr, nbytes), optionally keeping its owner alive."""
+
+    def __init__(self, ptr: int, nbytes: int, owner=None):
+        self.ptr, self.nbytes, self.owner = ptr, nbytes, owner
+
+    def download(self, nbytes: int, offset: int = 0) -> np.ndarray:
+        from sgl_rocm_kv import hip
+        assert offset + nbytes <= self.nbytes, "download past the end of the range"
+        out = np.empty(nbytes, dtype=np.uint8)
+        hip.memcpy_async(out.ctypes.data, self.ptr + offset, nbytes, "d2h")
+        hip.synchronize()
+        return out
+
+
+def _placed_pool(kv, k, spec, sh, probe_rows, candidates: int):
+    """The destination pool from the library's placement probe
+    (sgl_rocm_kv_storage_allocate_placed): `candidates` allocations held at
+    once, each probed by packing one layer's rows into `probe_rows` (scratch,
+    overwritten) and timing their unpack back, the fastest kept and
+    zero-filled. The same build's unpack into a pool runs
+    at one of two speeds on MI355X depending on where the allocation lands in
+    physical memory; the probe costs ~4 ms per candidate, outside the timed
+    steps."""
+    nbytes = spec.byte_len(sh)
+    view = _views(kv, _Span(0, nbytes), spec, sh, 0)
+    storage, report = kv.RocmKvStorage.allocate_placed(k, nbytes, spec.page_stride(sh), view,
+                                                       probe_rows, candidates)
+    b = storage.allocation()
+    log(f"destination pool: {report['candidates']} placement candidates, probe unpack "
+        f"{report['probe_us']} us over {report['probe_rows']} rows, kept #{report['chosen']}")
+    return _Span(b.ptr, b.byte_len, storage), report
+
+
 def _kernel_family(sh):
     """The copy kernels a shape's rows take: the 16-byte-vector kernels when
     every row width is a whole number of 16-byte vectors (every address and
@@ -299,8 +333,8 @@ def run_coresident(t, config, args):
     fp8 = config == "c4fp8"
     k = kv.RocmKvPairCopyKernels(0)
     src = hip.DeviceBuffer(t.src.byte_len(sh))
-    dst = hip.DeviceBuffer(t.dst.byte_len(sh))
     xfer = hip.DeviceBuffer(L * n * lrb)
+    dst, placement = _placed_pool(kv, k, t.dst, sh, kv.device_buffer(xfer.ptr, xfer.nbytes), args.placement)
     kind = kv.FILL_BITS if sh.elt_bytes == 1 else kv.FILL_BF16_NORMAL
     k.fill_synthetic(kv.device_buffer(src.ptr, src.nbytes), 2024, kind)
     k.fill_synthetic(kv.device_buffer(dst.ptr, dst.nbytes), 2025, kind)
@@ -463,6 +497,7 @@ def run_coresident(t, config, args):
         "unpack_us_avg": round(avg_unpack * 1e3, 2),
         "kernel_sum_gbs": round(kernel_gbs, 1),
         "verified_rows": checked,
+        "placement": placement,
         "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      # the committed counter summaries were taken with --launch auto
@@ -651,7 +686,10 @@ def run_direct(t, args):
     sh = t.shape
     rb, n, L, T = sh.row_bytes, t.rows, sh.layers, sh.tensors
     k = kv.RocmKvPairCopyKernels(0)
-    src, dst = hip.DeviceBuffer(t.src.byte_len(sh)), hip.DeviceBuffer(t.dst.byte_len(sh))
+    src = hip.DeviceBuffer(t.src.byte_len(sh))
+    # The probe uses the source pool's first bytes as its rows scratch; the
+    # pool is filled after it.
+    dst, placement = _placed_pool(kv, k, t.dst, sh, kv.device_buffer(src.ptr, src.nbytes), args.placement)
     k.fill_synthetic(kv.device_buffer(src.ptr, src.nbytes), 2024, kv.FILL_BF16_NORMAL)
     ss, ds = hip.DeviceBuffer.from_array(t.src_slots), hip.DeviceBuffer.from_array(t.dst_slots)
     ssb, dsb = kv.device_buffer(ss.ptr, ss.nbytes), kv.device_buffer(ds.ptr, ds.nbytes)
@@ -701,6 +739,7 @@ def run_direct(t, args):
         "config_extra": {"tokens": n, "layers": L, "payload_bytes": payload,
                          "algorithmic_bytes_per_step": 2 * payload},
         "per_layer_p50_us": round(float(np.percentile(layer_ms, 50)) * 1e3, 2),
+        "placement": placement,
         "roofline": {"bound": "hbm", "kernel": "sglkv_copy_pool_pool_v16", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "algorithmic_bytes_per_launch": launch_bytes},
@@ -1083,6 +1122,11 @@ def main():
                     help="c2/c3/c4: pack and unpack each layer in this many pieces through one reused "
                          "transfer region (co-resident schedule; rows re-read from the Infinity Cache). "
                          "Default 1: whole layers, every layer's rows in its own region")
+    ap.add_argument("--placement", type=int, default=3,
+                    help="c1-c4, hnd64, nhd64, c2direct: allocate the destination pool this many times "
+                         "at once, time one layer's unpack into each and keep the fastest "
+                         "(sgl_rocm_kv_storage_allocate_placed; 1 = a single allocation, still probed "
+                         "and reported)")
     ap.add_argument("--cpu-seconds", type=float, default=6.0,
                     help="seconds of CPU work per CPU-baseline figure")
     ap.add_argument("--cpu-threads", type=int, default=_usable_cores(),

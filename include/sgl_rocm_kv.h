@@ -1233,6 +1233,39 @@ int32_t sgl_rocm_kv_cache_allocate(sgl_rocm_kv_ctx *ctx, const sgl_kv_runtime_la
  * size check (kv_cache.rs:849-856). */
 int32_t sgl_rocm_kv_pool_allocate(sgl_rocm_kv_ctx *ctx, const sgl_kv_paged_layout *layout,
                                   sgl_rocm_kv_storage **out);
+
+/* What sgl_rocm_kv_storage_allocate_placed measured. */
+#define SGL_KV_PLACEMENT_MAX_CANDIDATES 8u
+typedef struct sgl_kv_placement_report {
+    uint32_t candidates;  /* allocations probed (fewer than asked when the device ran out) */
+    uint32_t chosen;      /* index of the one kept */
+    uint64_t probe_rows;  /* rows each probe scattered */
+    float probe_us[SGL_KV_PLACEMENT_MAX_CANDIDATES]; /* median probe launch per candidate, µs */
+} sgl_kv_placement_report;
+
+/* No counterpart in the reference, which allocates one pool
+ * (CudaKvStorage::allocate, cuda_kv_cache.rs:177-189). On MI355X the same
+ * scatter into a pool runs at one of two speeds depending on where the
+ * allocation lands in physical memory (Llama-3-8B-shape unpack: 177-183 or
+ * 205-211 µs per layer), fixed for the allocation's lifetime, and no HIP
+ * allocation call selects it. This call allocates `candidates` (1..8) buffers
+ * of byte_len bytes at once and probes each: up to 131,072 rows of the layer
+ * `probe_view` describes (its base and byte_len replaced by the candidate's;
+ * the rows' pages a fixed permutation of the pool's pages) are packed into
+ * `probe_rows` and unpacked back, one warm-up and five timed rounds on
+ * `stream`, and the median unpack is kept. It keeps the fastest candidate,
+ * frees the others, and zero-fills the one it returns, as
+ * sgl_rocm_kv_storage_allocate does. `probe_rows` is scratch for the probe
+ * (its contents are overwritten): pass the buffer the caller will unpack
+ * from, at least one row of the view's tensors. Past the first candidate, an
+ * allocation the device cannot satisfy ends the probing instead of failing
+ * the call. Peak device memory during the call is candidates x byte_len.
+ * `report` may be NULL. */
+int32_t sgl_rocm_kv_storage_allocate_placed(sgl_rocm_kv_ctx *ctx, uint64_t byte_len,
+                                            uint64_t page_size_bytes, const sgl_kv_pool_view *probe_view,
+                                            const sgl_kv_device_buffer *probe_rows, uint32_t candidates,
+                                            void *stream, sgl_rocm_kv_storage **out,
+                                            sgl_kv_placement_report *report);
 /* Frees the allocation; NULL is accepted. Slot maps uploaded through the
  * storage stay valid (they own their memory). */
 int32_t sgl_rocm_kv_storage_destroy(sgl_rocm_kv_storage *storage);

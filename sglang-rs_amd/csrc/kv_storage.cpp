@@ -13,6 +13,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <vector>
 
 #include "kv_internal.h"
@@ -244,6 +245,183 @@ extern "C" int32_t sgl_rocm_kv_pool_allocate(sgl_rocm_kv_ctx *ctx, const sgl_kv_
         return rc;
     }
     *out = s;
+    return ok();
+}
+
+namespace {
+
+constexpr uint64_t kProbeMaxRows = 131072;
+constexpr int kProbeTimed = 5;
+
+uint64_t gcd64(uint64_t a, uint64_t b) {
+    while (b) {
+        const uint64_t t = a % b;
+        a = b;
+        b = t;
+    }
+    return a;
+}
+
+// The probe's slot map: rows r of a fixed permutation of the pool's pages,
+// r % page_size within its page, the way a decode page table spreads a
+// request over the pool. The permutation is affine (i -> (a i + c) mod
+// pages with a coprime to pages), so nothing proportional to the page count
+// is built.
+std::vector<uint64_t> probe_slots(uint64_t rows, uint64_t page_size, uint64_t pages) {
+    uint64_t a = 0x9E3779B97F4A7C15ull % pages;
+    if (a == 0) a = 1;
+    while (gcd64(a, pages) != 1) a = a + 1 < pages ? a + 1 : 1;
+    const uint64_t c = pages / 3;
+    std::vector<uint64_t> slots(rows);
+    for (uint64_t r = 0; r < rows; ++r) {
+        const uint64_t i = r / page_size;
+        const uint64_t page = (uint64_t)(((unsigned __int128)a * i + c) % pages);
+        slots[r] = page * page_size + r % page_size;
+    }
+    return slots;
+}
+
+// Frees every candidate but `keep` (-1: all of them).
+void free_candidates(std::vector<void *> &bases, int keep) {
+    for (size_t i = 0; i < bases.size(); ++i)
+        if ((int)i != keep && bases[i]) (void)hipFree(bases[i]);
+}
+
+}  // namespace
+
+extern "C" int32_t sgl_rocm_kv_storage_allocate_placed(sgl_rocm_kv_ctx *ctx, uint64_t byte_len,
+                                                       uint64_t page_size_bytes, const sgl_kv_pool_view *probe_view,
+                                                       const sgl_kv_device_buffer *probe_rows, uint32_t candidates,
+                                                       void *stream, sgl_rocm_kv_storage **out,
+                                                       sgl_kv_placement_report *report) {
+    if (!out) return null_arg("out");
+    *out = nullptr;
+    if (!ctx) return null_arg("ctx");
+    if (!probe_view) return null_arg("probe_view");
+    if (!probe_rows || !probe_rows->ptr) return null_arg("probe_rows");
+    if (candidates < 1 || candidates > SGL_KV_PLACEMENT_MAX_CANDIDATES)
+        return fail(SGL_KV_INVALID_ARGUMENT, "candidates", candidates, SGL_KV_PLACEMENT_MAX_CANDIDATES, 0,
+                    "placement candidates must be 1..%u, got %u", SGL_KV_PLACEMENT_MAX_CANDIDATES, candidates);
+    if (byte_len == 0)
+        return fail(SGL_KV_ZERO_ALLOCATION, nullptr, 0, 0, 0, "ROCm allocation of zero bytes");
+    const sgl_kv_pool_view &v = *probe_view;
+    if (v.tensor_count < 1 || v.tensor_count > 2)
+        return fail(SGL_KV_INVALID_ARGUMENT, "tensor_count", v.tensor_count, 2, 0,
+                    "probe view tensor_count must be 1 or 2, got %u", v.tensor_count);
+    if (v.page_size == 0 || v.page_count == 0)
+        return fail(SGL_KV_INVALID_ARGUMENT, "page_size/page_count", v.page_size, v.page_count, 0,
+                    "probe view has no slots");
+    const uint64_t rb0 = v.row_bytes;
+    const uint64_t rb1 = v.tensor_count == 2 ? (v.value_row_bytes ? v.value_row_bytes : v.row_bytes) : 0;
+    const uint64_t token_bytes = rb0 + rb1;
+    uint64_t slot_count;
+    if (__builtin_mul_overflow(v.page_size, v.page_count, &slot_count)) slot_count = UINT64_MAX;
+    uint64_t rows = token_bytes ? probe_rows->byte_len / token_bytes : 0;
+    if (rows > slot_count) rows = slot_count;
+    if (rows > kProbeMaxRows) rows = kProbeMaxRows;
+    if (rows == 0)
+        return fail(SGL_KV_INVALID_ARGUMENT, "probe_rows", probe_rows->byte_len, token_bytes, 0,
+                    "probe rows of %llu bytes hold no row of %llu bytes",
+                    (unsigned long long)probe_rows->byte_len, (unsigned long long)token_bytes);
+
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+
+    // All candidates are held at once: a freed allocation would come back at
+    // the same physical memory.
+    std::vector<void *> bases;
+    for (uint32_t i = 0; i < candidates; ++i) {
+        void *base = nullptr;
+        const hipError_t err = hipMalloc(&base, byte_len);
+        if (err != hipSuccess) {
+            (void)hipGetLastError();
+            if (i == 0) return hip_fail(err, "hipMalloc");
+            break;  // probe what fits
+        }
+        bases.push_back(base);
+    }
+
+    const std::vector<uint64_t> host_slots = probe_slots(rows, v.page_size, v.page_count);
+    void *slot_dev = nullptr;
+    hipEvent_t ev[kProbeTimed + 1] = {};
+    int32_t rc = SGL_KV_OK;
+    std::vector<float> probe_us(bases.size(), 0.0f);
+    auto cleanup = [&](int keep) {
+        for (hipEvent_t &e : ev)
+            if (e) (void)hipEventDestroy(e);
+        if (slot_dev) (void)hipFree(slot_dev);
+        free_candidates(bases, keep);
+    };
+    hipError_t err = hipMalloc(&slot_dev, rows * sizeof(uint64_t));
+    if (err == hipSuccess)
+        err = hipMemcpy(slot_dev, host_slots.data(), rows * sizeof(uint64_t), hipMemcpyHostToDevice);
+    for (int i = 0; err == hipSuccess && i <= kProbeTimed; ++i) err = hipEventCreate(&ev[i]);
+    if (err != hipSuccess) {
+        cleanup(-1);
+        return hip_fail(err, "probe set-up");
+    }
+    const sgl_kv_device_buffer slots{slot_dev, rows * sizeof(uint64_t)};
+    sgl_kv_rows_view rv;
+    memset(&rv, 0, sizeof rv);
+    uint8_t *p = static_cast<uint8_t *>(probe_rows->ptr);
+    rv.planes[0] = p;
+    rv.plane_bytes[0] = rows * rb0;
+    rv.row_stride[0] = rb0;
+    if (v.tensor_count == 2) {
+        rv.planes[1] = p + rows * rb0;
+        rv.plane_bytes[1] = rows * rb1;
+        rv.row_stride[1] = rb1;
+    }
+    for (size_t c = 0; c < bases.size() && rc == SGL_KV_OK; ++c) {
+        sgl_kv_pool_view pv = v;
+        pv.base = bases[c];
+        pv.byte_len = byte_len;
+        pv.scale = nullptr;  // the probe moves bytes only
+        // Each round packs the candidate's rows into probe_rows and unpacks
+        // them back, so that the timed unpack reads rows just written, as
+        // one that follows a transfer's pack or receive does; only the
+        // unpack is timed.
+        rc = sgl_rocm_kv_pack_layer(ctx, &pv, &slots, rows, &rv, s);  // warm-up
+        if (rc == SGL_KV_OK) rc = sgl_rocm_kv_unpack_layer(ctx, &rv, rows, &pv, &slots, s);
+        float t[kProbeTimed];
+        for (int i = 0; i < kProbeTimed && rc == SGL_KV_OK; ++i) {
+            if ((rc = sgl_rocm_kv_pack_layer(ctx, &pv, &slots, rows, &rv, s)) != SGL_KV_OK) break;
+            if ((err = hipEventRecord(ev[i], s)) != hipSuccess) break;
+            rc = sgl_rocm_kv_unpack_layer(ctx, &rv, rows, &pv, &slots, s);
+            if (rc == SGL_KV_OK && (err = hipEventRecord(ev[i + 1], s)) != hipSuccess) break;
+            if (rc == SGL_KV_OK && (err = hipEventSynchronize(ev[i + 1])) != hipSuccess) break;
+            if (rc == SGL_KV_OK && (err = hipEventElapsedTime(&t[i], ev[i], ev[i + 1])) != hipSuccess) break;
+        }
+        if (rc == SGL_KV_OK && err != hipSuccess) rc = hip_fail(err, "probe timing");
+        if (rc != SGL_KV_OK) break;
+        std::sort(t, t + kProbeTimed);
+        probe_us[c] = t[kProbeTimed / 2] * 1000.0f;
+    }
+    if (rc == SGL_KV_OK && (err = hipStreamSynchronize(s)) != hipSuccess) rc = hip_fail(err, "hipStreamSynchronize");
+    if (rc != SGL_KV_OK) {
+        cleanup(-1);
+        return rc;
+    }
+    size_t best = 0;
+    for (size_t c = 1; c < bases.size(); ++c)
+        if (probe_us[c] < probe_us[best]) best = c;
+    void *base = bases[best];
+    cleanup((int)best);
+    err = hipMemsetAsync(base, 0, byte_len, nullptr);
+    if (err == hipSuccess) err = hipStreamSynchronize(nullptr);
+    if (err != hipSuccess) {
+        (void)hipFree(base);
+        return hip_fail(err, "hipMemsetAsync");
+    }
+    if (report) {
+        memset(report, 0, sizeof *report);
+        report->candidates = (uint32_t)bases.size();
+        report->chosen = (uint32_t)best;
+        report->probe_rows = rows;
+        for (size_t c = 0; c < bases.size(); ++c) report->probe_us[c] = probe_us[c];
+    }
+    *out = new sgl_rocm_kv_storage{ctx->device, base, byte_len, page_size_bytes};
     return ok();
 }
 

@@ -267,6 +267,14 @@ class _TransferableMemory(ctypes.Structure):
                 ("page_size_bytes", _u64), ("location_kind", ctypes.c_int32), ("location_id", ctypes.c_int32)]
 
 
+PLACEMENT_MAX_CANDIDATES = 8
+
+
+class _PlacementReport(ctypes.Structure):
+    _fields_ = [("candidates", ctypes.c_uint32), ("chosen", ctypes.c_uint32), ("probe_rows", _u64),
+                ("probe_us", ctypes.c_float * PLACEMENT_MAX_CANDIDATES)]
+
+
 class _SpanDesc(ctypes.Structure):
     _fields_ = [("bootstrap_room", _u64), ("descriptor_checksum", ctypes.c_char * 65),
                 ("reserved", ctypes.c_char * 7), ("token_offset", _u64), ("token_count", _u64),
@@ -517,6 +525,10 @@ _EXPORTS = {
                                                     ctypes.POINTER(_PagedLayout), ctypes.POINTER(ctypes.c_void_p)]),
     "sgl_rocm_kv_pool_allocate": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_PagedLayout),
                                                    ctypes.POINTER(ctypes.c_void_p)]),
+    "sgl_rocm_kv_storage_allocate_placed": (ctypes.c_int32, [ctypes.c_void_p, _u64, _u64, ctypes.POINTER(PoolView),
+                                                             ctypes.POINTER(_DeviceBuffer), ctypes.c_uint32,
+                                                             ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p),
+                                                             ctypes.POINTER(_PlacementReport)]),
     "sgl_rocm_kv_storage_destroy": (ctypes.c_int32, [ctypes.c_void_p]),
     "sgl_rocm_kv_storage_allocation": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_DeviceBuffer)]),
     "sgl_rocm_kv_storage_byte_len": (_u64, [ctypes.c_void_p]),
@@ -1602,6 +1614,22 @@ class RocmKvStorage:
         h = ctypes.c_void_p()
         _call(lib().sgl_rocm_kv_storage_allocate, kernels._h, byte_len, page_size_bytes, ctypes.byref(h))
         return cls(h.value)
+
+    @classmethod
+    def allocate_placed(cls, kernels: "RocmKvPairCopyKernels", byte_len: int, page_size_bytes: int,
+                        probe_view: "PoolView", probe_rows: _DeviceBuffer, candidates: int,
+                        stream=None) -> tuple["RocmKvStorage", dict]:
+        """allocate(), keeping the fastest of `candidates` allocations for the
+        scatter `probe_view` describes (no counterpart in the reference).
+        Returns the storage and the probe report."""
+        h = ctypes.c_void_p()
+        r = _PlacementReport()
+        _call(lib().sgl_rocm_kv_storage_allocate_placed, kernels._h, byte_len, page_size_bytes,
+              ctypes.byref(probe_view), ctypes.byref(probe_rows), candidates, _stream(stream),
+              ctypes.byref(h), ctypes.byref(r))
+        report = {"candidates": r.candidates, "chosen": r.chosen, "probe_rows": r.probe_rows,
+                  "probe_us": [round(float(r.probe_us[i]), 2) for i in range(r.candidates)]}
+        return cls(h.value), report
 
     def allocation(self) -> _DeviceBuffer:
         b = _DeviceBuffer()

@@ -379,3 +379,86 @@ def test_reference_asymmetric_compressed_mla(k):
     assert np.abs(got - want).max() <= 0.05                          # the reference's tolerance
     assert (np.abs(got - want) <= 2.0 ** -8 * np.abs(want) + 1e-3).all(), (got, want)
     storage.close()
+
+
+def test_placed_allocation_keeps_the_fastest_candidate(k):
+    """sgl_rocm_kv_storage_allocate_placed (no counterpart in the reference):
+    three allocations probed with one layer's unpack, the fastest kept,
+    zero-filled and of the requested size, the others given back; the kept
+    pool is an ordinary pool (an unpack into it equals the oracle's)."""
+    _say("placed allocation")
+    P, L, H, D, pages = 64, 2, 8, 128, 128
+    rb = H * D * 2
+    rt = kv.KvCacheRuntimeLayout("bf16", P, L, H, D, 2, L * 2 * rb, P * L * 2 * rb)
+    layout = kv.PagedKvCacheLayout.new(rt, pages)
+    nbytes, psb = layout.total_byte_len, rt.page_size_bytes
+    rows_n = 3000
+    probe_rows = hip.DeviceBuffer(rows_n * 2 * rb)
+    k.fill_synthetic(kv.device_buffer(probe_rows.ptr, probe_rows.nbytes), 11)
+    hip.synchronize()
+    view = layout.pool_view(0, nbytes, 1)
+    free_before, _ = k.memory_info()
+    storage, rep = kv.RocmKvStorage.allocate_placed(k, nbytes, psb, view,
+                                                    kv.device_buffer(probe_rows.ptr, probe_rows.nbytes), 3)
+    free_after, _ = k.memory_info()
+    _say(f"placement report {rep}")
+    assert rep["candidates"] == 3 and rep["probe_rows"] == rows_n
+    assert len(rep["probe_us"]) == 3 and min(rep["probe_us"]) > 0
+    assert rep["chosen"] == int(np.argmin(rep["probe_us"]))
+    assert storage.byte_len() == nbytes and storage.page_size_bytes() == psb
+    # one pool's worth held (allocation granularity aside), not three
+    assert nbytes // 2 <= free_before - free_after < 2 * nbytes
+    whole = np.concatenate([storage.read_page(layout, p) for p in range(pages)])
+    assert not whole.any(), "the kept pool is zero-filled after the probe"
+
+    # an ordinary pool: unpack rows into layer 0 and compare with the oracle
+    rng = np.random.default_rng(5)
+    n = 777
+    slots = rng.choice(layout.slot_count, size=n, replace=False).astype(np.uint64)
+    rows = rng.integers(0, 256, size=(2, n, rb), dtype=np.uint8)
+    rows_dev = hip.DeviceBuffer.from_array(rows)
+    slots_dev = hip.DeviceBuffer.from_array(slots)
+    b = storage.allocation()
+    rv = kv.rows_view([rows_dev.ptr, rows_dev.ptr + n * rb], [n * rb, n * rb], [rb, rb])
+    k.unpack_layer(rv, n, layout.pool_view(b.ptr, b.byte_len, 0), kv.device_buffer(slots_dev.ptr, slots_dev.nbytes))
+    hip.synchronize()
+    k.check_errors()
+    got = np.concatenate([storage.read_page(layout, p) for p in range(pages)])
+    offs = tuple(layout.pool_view(0, nbytes, 0).tensor_offset[t] for t in range(2))
+    pool = oracle.Pool(P, psb, pages, offs, rb, 2, H, False)
+    want = np.zeros(nbytes, np.uint8)
+    oracle.unpack(pool, want, slots, rows[0], rows[1], rb, rb)
+    np.testing.assert_array_equal(got, want)
+    storage.close()
+    free_released, _ = k.memory_info()
+    assert free_released > free_after
+
+
+def test_placed_allocation_errors(k):
+    """Candidate counts outside 1..8, probe rows too small for one row and a
+    missing view are refused before anything is allocated."""
+    _say("placed allocation errors")
+    P, L, H, D = 16, 1, 2, 64
+    rb = H * D * 2
+    rt = kv.KvCacheRuntimeLayout("bf16", P, L, H, D, 2, L * 2 * rb, P * L * 2 * rb)
+    layout = kv.PagedKvCacheLayout.new(rt, 4)
+    nbytes = layout.total_byte_len
+    rows = hip.DeviceBuffer(4 * 2 * rb)
+    view = layout.pool_view(0, nbytes, 0)
+    db = kv.device_buffer(rows.ptr, rows.nbytes)
+    for bad in (0, 9):
+        with pytest.raises(kv.KvError) as e:
+            kv.RocmKvStorage.allocate_placed(k, nbytes, rt.page_size_bytes, view, db, bad)
+        assert e.value.code == kv.INVALID_ARGUMENT and e.value.name == "candidates"
+    with pytest.raises(kv.KvError) as e:
+        kv.RocmKvStorage.allocate_placed(k, nbytes, rt.page_size_bytes, view,
+                                         kv.device_buffer(rows.ptr, 2 * rb - 1), 2)
+    assert e.value.code == kv.INVALID_ARGUMENT and e.value.name == "probe_rows"
+    with pytest.raises(kv.KvError) as e:
+        kv.RocmKvStorage.allocate_placed(k, 0, rt.page_size_bytes, view, db, 2)
+    assert e.value.code == kv.ZERO_ALLOCATION
+    # a single candidate is an ordinary probed allocation
+    storage, rep = kv.RocmKvStorage.allocate_placed(k, nbytes, rt.page_size_bytes, view, db, 1)
+    assert rep["candidates"] == 1 and rep["chosen"] == 0 and rep["probe_rows"] == 4
+    assert storage.byte_len() == nbytes
+    storage.close()

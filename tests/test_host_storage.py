@@ -83,6 +83,15 @@ def test_storage_entry_points_reject_null_without_a_gpu():
     assert lib.sgl_rocm_kv_storage_clear(None) == kv.INVALID_ARGUMENT
     assert lib.sgl_rocm_kv_storage_validate_layout(None, None) == kv.INVALID_ARGUMENT
     assert lib.sgl_rocm_kv_memory_info(None, None, None) == kv.INVALID_ARGUMENT
+    assert lib.sgl_rocm_kv_storage_allocate_placed(None, 64, 64, None, None, 3, None,
+                                                   ctypes.byref(out), None) == kv.INVALID_ARGUMENT
+    assert out.value is None
+
+
+def test_placement_report_matches_the_header():
+    """sgl_kv_placement_report: two u32, a u64 and SGL_KV_PLACEMENT_MAX_CANDIDATES floats."""
+    assert kv.PLACEMENT_MAX_CANDIDATES == 8
+    assert ctypes.sizeof(kv._PlacementReport) == 4 + 4 + 8 + 4 * 8
 
 
 def test_storage_status_names():

@@ -263,6 +263,7 @@ def _placed_pool(kv, k, spec, sh, probe_rows, candidates: int):
     view = _views(kv, _Span(0, nbytes), spec, sh, 0)
     storage, report = kv.RocmKvStorage.allocate_placed(k, nbytes, spec.page_stride(sh), view,
                                                        probe_rows, candidates)
+    report["probe_us"] = [round(x, 2) for x in report["probe_us"]]
     b = storage.allocation()
     log(f"destination pool: {report['candidates']} placement candidates, probe unpack "
         f"{report['probe_us']} us over {report['probe_rows']} rows, kept #{report['chosen']}")

@@ -326,6 +326,13 @@ extern "C" int32_t sgl_rocm_kv_storage_allocate_placed(sgl_rocm_kv_ctx *ctx, uin
 
     DeviceScope scope(ctx->device);
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    {
+        // The probe's kernels read and write probe_rows: it must be memory
+        // of the context's device.
+        const sgl_rocm_kv_storage probe_owner{ctx->device, nullptr, 0, 0};
+        const int32_t rc = same_device(&probe_owner, "probe_rows", *probe_rows);
+        if (rc) return rc;
+    }
     hipStream_t s = static_cast<hipStream_t>(stream);
 
     // All candidates are held at once: a freed allocation would come back at

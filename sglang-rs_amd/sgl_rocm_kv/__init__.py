@@ -1628,7 +1628,7 @@ class RocmKvStorage:
               ctypes.byref(probe_view), ctypes.byref(probe_rows), candidates, _stream(stream),
               ctypes.byref(h), ctypes.byref(r))
         report = {"candidates": r.candidates, "chosen": r.chosen, "probe_rows": r.probe_rows,
-                  "probe_us": [round(float(r.probe_us[i]), 2) for i in range(r.candidates)]}
+                  "probe_us": [float(r.probe_us[i]) for i in range(r.candidates)]}
         return cls(h.value), report
 
     def allocation(self) -> _DeviceBuffer:

@@ -404,7 +404,7 @@ def test_placed_allocation_keeps_the_fastest_candidate(k):
     _say(f"placement report {rep}")
     assert rep["candidates"] == 3 and rep["probe_rows"] == rows_n
     assert len(rep["probe_us"]) == 3 and min(rep["probe_us"]) > 0
-    assert rep["chosen"] == int(np.argmin(rep["probe_us"]))
+    assert rep["probe_us"][rep["chosen"]] == min(rep["probe_us"])
     assert storage.byte_len() == nbytes and storage.page_size_bytes() == psb
     # one pool's worth held (allocation granularity aside), not three
     assert nbytes // 2 <= free_before - free_after < 2 * nbytes
@@ -457,6 +457,12 @@ def test_placed_allocation_errors(k):
     with pytest.raises(kv.KvError) as e:
         kv.RocmKvStorage.allocate_placed(k, 0, rt.page_size_bytes, view, db, 2)
     assert e.value.code == kv.ZERO_ALLOCATION
+    # probe rows in host memory are not the context's device memory
+    host = np.zeros(4 * 2 * rb, np.uint8)
+    with pytest.raises(kv.KvError) as e:
+        kv.RocmKvStorage.allocate_placed(k, nbytes, rt.page_size_bytes, view,
+                                         kv.device_buffer(host.ctypes.data, host.nbytes), 2)
+    assert e.value.variant == "DeviceMismatch" and e.value.name == "probe_rows"
     # a single candidate is an ordinary probed allocation
     storage, rep = kv.RocmKvStorage.allocate_placed(k, nbytes, rt.page_size_bytes, view, db, 1)
     assert rep["candidates"] == 1 and rep["chosen"] == 0 and rep["probe_rows"] == 4

@@ -468,3 +468,54 @@ def test_placed_allocation_errors(k):
     assert rep["candidates"] == 1 and rep["chosen"] == 0 and rep["probe_rows"] == 4
     assert storage.byte_len() == nbytes
     storage.close()
+
+
+@pytest.mark.parametrize("form", ["pair", "packed", "hnd"])
+def test_placed_allocation_probes_every_pool_form(k, form):
+    """The placement probe packs and unpacks through the view it is given:
+    DeepSeek-V3's key/value pair of unequal widths (1,152 / 1,024 B), the
+    649-byte packed-MLA rows (the byte-realigning kernels) and head-major
+    pages. Each kept pool is zero-filled and round-trips rows."""
+    _say(f"placed allocation, {form} view")
+    P, L, pages = 16, 2, 64
+    if form == "pair":
+        kb, vb, T, H, hl = 1152, 1024, 2, 1, kv.NHD
+    elif form == "packed":
+        kb, vb, T, H, hl = 649, 0, 1, 1, kv.NHD
+    else:
+        kb, vb, T, H, hl = 1024, 1024, 2, 8, kv.HND
+    token = kb + vb
+    stride = P * L * token
+    nbytes = pages * stride
+
+    def view(base):
+        return kv.pool_view(base, nbytes, page_size=P, page_stride_bytes=stride, page_count=pages,
+                            tensor_offset=[0, P * kb][:T], row_bytes=kb, tensor_count=T, heads=H,
+                            head_layout=hl, value_row_bytes=vb if form == "pair" else 0)
+
+    probe = hip.DeviceBuffer(600 * token)
+    storage, rep = kv.RocmKvStorage.allocate_placed(k, nbytes, stride, view(0),
+                                                    kv.device_buffer(probe.ptr, probe.nbytes), 2)
+    assert rep["candidates"] == 2 and rep["probe_rows"] == 600 and min(rep["probe_us"]) > 0
+    b = storage.allocation()
+    assert b.byte_len == nbytes
+    whole = np.zeros(nbytes, np.uint8)
+    hip.memcpy_async(whole.ctypes.data, b.ptr, nbytes, "d2h")
+    hip.synchronize()
+    assert not whole.any()
+    rng = np.random.default_rng(9)
+    n = 300
+    slots = rng.choice(P * pages, size=n, replace=False).astype(np.uint64)
+    widths = [kb, vb][:T]
+    rows = [rng.integers(0, 256, size=n * w, dtype=np.uint8) for w in widths]
+    src = [hip.DeviceBuffer.from_array(r) for r in rows]
+    back = [hip.DeviceBuffer(n * w) for w in widths]
+    sd = hip.DeviceBuffer.from_array(slots)
+    sdb = kv.device_buffer(sd.ptr, sd.nbytes)
+    k.unpack_layer(kv.rows_view([x.ptr for x in src], [n * w for w in widths], widths), n, view(b.ptr), sdb)
+    k.pack_layer(view(b.ptr), sdb, n, kv.rows_view([x.ptr for x in back], [n * w for w in widths], widths))
+    hip.synchronize()
+    k.check_errors()
+    for r, x in zip(rows, back):
+        np.testing.assert_array_equal(x.download(), r)
+    storage.close()

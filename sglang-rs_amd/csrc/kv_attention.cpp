@@ -592,7 +592,10 @@ extern "C" int32_t sgl_rocm_kv_paged_attention_async_noalloc(sgl_rocm_kv_ctx *ct
     if (ordered) SGLKV_CHECK_HIP(hipStreamWaitEvent(s, order->last, 0));
     const int32_t rc = attention_enqueue(ctx, plan, b, max_sequence_length, s, ctx->attn_flag,
                                          ctx->noalloc_workspace, SGL_KV_NOALLOC_WORKSPACE_BYTES);
+    // Recorded whatever the enqueue returned: a failure after its first
+    // launch still leaves work on `s` that uses the workspace.
+    const hipError_t rec = ordered ? hipEventRecord(order->last, s) : hipSuccess;
     if (rc) return rc;
-    if (ordered) SGLKV_CHECK_HIP(hipEventRecord(order->last, s));
+    if (rec != hipSuccess) return hip_fail(rec, "hipEventRecord");
     return ok();
 }

@@ -470,28 +470,34 @@ def test_placed_allocation_errors(k):
     storage.close()
 
 
-@pytest.mark.parametrize("form", ["pair", "packed", "hnd"])
+@pytest.mark.parametrize("form", ["pair", "packed", "hnd", "fp8"])
 def test_placed_allocation_probes_every_pool_form(k, form):
     """The placement probe packs and unpacks through the view it is given:
     DeepSeek-V3's key/value pair of unequal widths (1,152 / 1,024 B), the
-    649-byte packed-MLA rows (the byte-realigning kernels) and head-major
-    pages. Each kept pool is zero-filled and round-trips rows."""
+    649-byte packed-MLA rows (the byte-realigning kernels), head-major pages
+    and fp8 rows whose view carries a per-layer scale (the probe moves bytes
+    only and leaves the scale alone). Each kept pool is zero-filled and
+    round-trips rows (and the scale)."""
     _say(f"placed allocation, {form} view")
     P, L, pages = 16, 2, 64
     if form == "pair":
         kb, vb, T, H, hl = 1152, 1024, 2, 1, kv.NHD
     elif form == "packed":
         kb, vb, T, H, hl = 649, 0, 1, 1, kv.NHD
+    elif form == "fp8":
+        kb, vb, T, H, hl = 576, 0, 1, 1, kv.NHD
     else:
         kb, vb, T, H, hl = 1024, 1024, 2, 8, kv.HND
     token = kb + vb
     stride = P * L * token
     nbytes = pages * stride
+    pool_scale = hip.DeviceBuffer.from_array(np.array([-7.0], np.float32))
 
     def view(base):
         return kv.pool_view(base, nbytes, page_size=P, page_stride_bytes=stride, page_count=pages,
                             tensor_offset=[0, P * kb][:T], row_bytes=kb, tensor_count=T, heads=H,
-                            head_layout=hl, value_row_bytes=vb if form == "pair" else 0)
+                            head_layout=hl, value_row_bytes=vb if form == "pair" else 0,
+                            scale=pool_scale.ptr if form == "fp8" else None)
 
     probe = hip.DeviceBuffer(600 * token)
     storage, rep = kv.RocmKvStorage.allocate_placed(k, nbytes, stride, view(0),
@@ -512,10 +518,20 @@ def test_placed_allocation_probes_every_pool_form(k, form):
     back = [hip.DeviceBuffer(n * w) for w in widths]
     sd = hip.DeviceBuffer.from_array(slots)
     sdb = kv.device_buffer(sd.ptr, sd.nbytes)
-    k.unpack_layer(kv.rows_view([x.ptr for x in src], [n * w for w in widths], widths), n, view(b.ptr), sdb)
-    k.pack_layer(view(b.ptr), sdb, n, kv.rows_view([x.ptr for x in back], [n * w for w in widths], widths))
+    # the probe left the pool's scale as it was
+    np.testing.assert_array_equal(pool_scale.download(dtype=np.float32), [-7.0])
+    rows_scale = hip.DeviceBuffer.from_array(np.array([0.375], np.float32))
+    back_scale = hip.DeviceBuffer.from_array(np.array([0.0], np.float32))
+    fp8 = form == "fp8"
+    k.unpack_layer(kv.rows_view([x.ptr for x in src], [n * w for w in widths], widths,
+                                rows_scale.ptr if fp8 else None), n, view(b.ptr), sdb)
+    k.pack_layer(view(b.ptr), sdb, n, kv.rows_view([x.ptr for x in back], [n * w for w in widths], widths,
+                                                   back_scale.ptr if fp8 else None))
     hip.synchronize()
     k.check_errors()
     for r, x in zip(rows, back):
         np.testing.assert_array_equal(x.download(), r)
+    if fp8:
+        np.testing.assert_array_equal(pool_scale.download(dtype=np.float32), [0.375])
+        np.testing.assert_array_equal(back_scale.download(dtype=np.float32), [0.375])
     storage.close()

@@ -250,19 +250,20 @@ class _Span:
         return out
 
 
-def _placed_pool(kv, k, spec, sh, probe_rows, candidates: int):
+def _placed_pool(kv, k, spec, sh, probe_rows, candidates: int, probe_source=None):
     """The destination pool from the library's placement probe
     (sgl_rocm_kv_storage_allocate_placed): `candidates` allocations held at
     once, each probed by packing one layer's rows into `probe_rows` (scratch,
     overwritten) and timing their unpack back, the fastest kept and
-    zero-filled. The same build's unpack into a pool runs
+    zero-filled; with `probe_source` (a pool view) each candidate is timed on
+    a pool-to-pool transfer from it instead. The same build's unpack into a pool runs
     at one of two speeds on MI355X depending on where the allocation lands in
     physical memory; the probe costs ~4 ms per candidate, outside the timed
     steps."""
     nbytes = spec.byte_len(sh)
     view = _views(kv, _Span(0, nbytes), spec, sh, 0)
     storage, report = kv.RocmKvStorage.allocate_placed(k, nbytes, spec.page_stride(sh), view,
-                                                       probe_rows, candidates)
+                                                       probe_rows, candidates, probe_source=probe_source)
     report["probe_us"] = [round(x, 2) for x in report["probe_us"]]
     b = storage.allocation()
     log(f"destination pool: {report['candidates']} placement candidates, probe unpack "
@@ -688,10 +689,11 @@ def run_direct(t, args):
     rb, n, L, T = sh.row_bytes, t.rows, sh.layers, sh.tensors
     k = kv.RocmKvPairCopyKernels(0)
     src = hip.DeviceBuffer(t.src.byte_len(sh))
-    # The probe uses the source pool's first bytes as its rows scratch; the
-    # pool is filled after it.
-    dst, placement = _placed_pool(kv, k, t.dst, sh, kv.device_buffer(src.ptr, src.nbytes), args.placement)
     k.fill_synthetic(kv.device_buffer(src.ptr, src.nbytes), 2024, kv.FILL_BF16_NORMAL)
+    # Each destination candidate is probed with a pool-to-pool transfer from
+    # the source pool's first layer (the source is only read).
+    dst, placement = _placed_pool(kv, k, t.dst, sh, None, args.placement,
+                                  probe_source=_views(kv, src, t.src, sh, 0))
     ss, ds = hip.DeviceBuffer.from_array(t.src_slots), hip.DeviceBuffer.from_array(t.dst_slots)
     ssb, dsb = kv.device_buffer(ss.ptr, ss.nbytes), kv.device_buffer(ds.ptr, ds.nbytes)
     sviews = [_views(kv, src, t.src, sh, l) for l in range(L)]

@@ -1257,13 +1257,18 @@ typedef struct sgl_kv_placement_report {
  * frees the others, and zero-fills the one it returns, as
  * sgl_rocm_kv_storage_allocate does. `probe_rows` is scratch for the probe
  * (its contents are overwritten): pass the buffer the caller will unpack
- * from, at least one row of the view's tensors. Past the first candidate, an
- * allocation the device cannot satisfy ends the probing instead of failing
- * the call. Peak device memory during the call is candidates x byte_len.
- * `report` may be NULL. */
+ * from, at least one row of the view's tensors. A caller that will fill the
+ * pool from another pool on the device (sgl_rocm_kv_transfer_layer) passes
+ * that pool's layer as `probe_source` instead: each round is then one timed
+ * pool-to-pool transfer of up to 131,072 rows (a fixed permutation of the
+ * source's pages) into the candidate, the source only read, and probe_rows
+ * may be NULL. Past the first candidate, an allocation the device cannot
+ * satisfy ends the probing instead of failing the call. Peak device memory
+ * during the call is candidates x byte_len. `report` may be NULL. */
 int32_t sgl_rocm_kv_storage_allocate_placed(sgl_rocm_kv_ctx *ctx, uint64_t byte_len,
                                             uint64_t page_size_bytes, const sgl_kv_pool_view *probe_view,
-                                            const sgl_kv_device_buffer *probe_rows, uint32_t candidates,
+                                            const sgl_kv_device_buffer *probe_rows,
+                                            const sgl_kv_pool_view *probe_source, uint32_t candidates,
                                             void *stream, sgl_rocm_kv_storage **out,
                                             sgl_kv_placement_report *report);
 /* Frees the allocation; NULL is accepted. Slot maps uploaded through the

@@ -291,42 +291,52 @@ void free_candidates(std::vector<void *> &bases, int keep) {
 
 extern "C" int32_t sgl_rocm_kv_storage_allocate_placed(sgl_rocm_kv_ctx *ctx, uint64_t byte_len,
                                                        uint64_t page_size_bytes, const sgl_kv_pool_view *probe_view,
-                                                       const sgl_kv_device_buffer *probe_rows, uint32_t candidates,
+                                                       const sgl_kv_device_buffer *probe_rows,
+                                                       const sgl_kv_pool_view *probe_source, uint32_t candidates,
                                                        void *stream, sgl_rocm_kv_storage **out,
                                                        sgl_kv_placement_report *report) {
     if (!out) return null_arg("out");
     *out = nullptr;
     if (!ctx) return null_arg("ctx");
     if (!probe_view) return null_arg("probe_view");
-    if (!probe_rows || !probe_rows->ptr) return null_arg("probe_rows");
+    if (!probe_source && (!probe_rows || !probe_rows->ptr)) return null_arg("probe_rows");
     if (candidates < 1 || candidates > SGL_KV_PLACEMENT_MAX_CANDIDATES)
         return fail(SGL_KV_INVALID_ARGUMENT, "candidates", candidates, SGL_KV_PLACEMENT_MAX_CANDIDATES, 0,
                     "placement candidates must be 1..%u, got %u", SGL_KV_PLACEMENT_MAX_CANDIDATES, candidates);
     if (byte_len == 0)
         return fail(SGL_KV_ZERO_ALLOCATION, nullptr, 0, 0, 0, "ROCm allocation of zero bytes");
     const sgl_kv_pool_view &v = *probe_view;
-    if (v.tensor_count < 1 || v.tensor_count > 2)
-        return fail(SGL_KV_INVALID_ARGUMENT, "tensor_count", v.tensor_count, 2, 0,
-                    "probe view tensor_count must be 1 or 2, got %u", v.tensor_count);
-    if (v.page_size == 0 || v.page_count == 0)
-        return fail(SGL_KV_INVALID_ARGUMENT, "page_size/page_count", v.page_size, v.page_count, 0,
-                    "probe view has no slots");
+    for (const sgl_kv_pool_view *w : {probe_view, probe_source}) {
+        if (!w) continue;
+        if (w->tensor_count < 1 || w->tensor_count > 2)
+            return fail(SGL_KV_INVALID_ARGUMENT, "tensor_count", w->tensor_count, 2, 0,
+                        "probe view tensor_count must be 1 or 2, got %u", w->tensor_count);
+        if (w->page_size == 0 || w->page_count == 0)
+            return fail(SGL_KV_INVALID_ARGUMENT, "page_size/page_count", w->page_size, w->page_count, 0,
+                        "probe view has no slots");
+    }
+    auto slot_count = [](const sgl_kv_pool_view &w) {
+        uint64_t n;
+        return __builtin_mul_overflow(w.page_size, w.page_count, &n) ? UINT64_MAX : n;
+    };
     const uint64_t rb0 = v.row_bytes;
     const uint64_t rb1 = v.tensor_count == 2 ? (v.value_row_bytes ? v.value_row_bytes : v.row_bytes) : 0;
     const uint64_t token_bytes = rb0 + rb1;
-    uint64_t slot_count;
-    if (__builtin_mul_overflow(v.page_size, v.page_count, &slot_count)) slot_count = UINT64_MAX;
-    uint64_t rows = token_bytes ? probe_rows->byte_len / token_bytes : 0;
-    if (rows > slot_count) rows = slot_count;
-    if (rows > kProbeMaxRows) rows = kProbeMaxRows;
-    if (rows == 0)
-        return fail(SGL_KV_INVALID_ARGUMENT, "probe_rows", probe_rows->byte_len, token_bytes, 0,
-                    "probe rows of %llu bytes hold no row of %llu bytes",
-                    (unsigned long long)probe_rows->byte_len, (unsigned long long)token_bytes);
+    uint64_t rows = slot_count(v);
+    if (probe_source) {
+        rows = std::min(rows, slot_count(*probe_source));
+    } else {
+        rows = std::min(rows, token_bytes ? probe_rows->byte_len / token_bytes : 0);
+        if (rows == 0)
+            return fail(SGL_KV_INVALID_ARGUMENT, "probe_rows", probe_rows->byte_len, token_bytes, 0,
+                        "probe rows of %llu bytes hold no row of %llu bytes",
+                        (unsigned long long)probe_rows->byte_len, (unsigned long long)token_bytes);
+    }
+    rows = std::min(rows, kProbeMaxRows);
 
     DeviceScope scope(ctx->device);
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
-    {
+    if (!probe_source) {
         // The probe's kernels read and write probe_rows: it must be memory
         // of the context's device.
         const sgl_rocm_kv_storage probe_owner{ctx->device, nullptr, 0, 0};
@@ -349,53 +359,77 @@ extern "C" int32_t sgl_rocm_kv_storage_allocate_placed(sgl_rocm_kv_ctx *ctx, uin
         bases.push_back(base);
     }
 
-    const std::vector<uint64_t> host_slots = probe_slots(rows, v.page_size, v.page_count);
+    // Slot maps: the candidate's rows at [0, rows), the source's (pool to
+    // pool) at [rows, 2 rows).
+    std::vector<uint64_t> host_slots = probe_slots(rows, v.page_size, v.page_count);
+    if (probe_source) {
+        const std::vector<uint64_t> src = probe_slots(rows, probe_source->page_size, probe_source->page_count);
+        host_slots.insert(host_slots.end(), src.begin(), src.end());
+    }
     void *slot_dev = nullptr;
     hipEvent_t ev[kProbeTimed + 1] = {};
     int32_t rc = SGL_KV_OK;
     std::vector<float> probe_us(bases.size(), 0.0f);
     auto cleanup = [&](int keep) {
+        // Nothing may still be writing a candidate when it is freed.
+        (void)hipStreamSynchronize(s);
         for (hipEvent_t &e : ev)
             if (e) (void)hipEventDestroy(e);
         if (slot_dev) (void)hipFree(slot_dev);
         free_candidates(bases, keep);
     };
-    hipError_t err = hipMalloc(&slot_dev, rows * sizeof(uint64_t));
+    hipError_t err = hipMalloc(&slot_dev, host_slots.size() * sizeof(uint64_t));
     if (err == hipSuccess)
-        err = hipMemcpy(slot_dev, host_slots.data(), rows * sizeof(uint64_t), hipMemcpyHostToDevice);
+        err = hipMemcpy(slot_dev, host_slots.data(), host_slots.size() * sizeof(uint64_t), hipMemcpyHostToDevice);
     for (int i = 0; err == hipSuccess && i <= kProbeTimed; ++i) err = hipEventCreate(&ev[i]);
     if (err != hipSuccess) {
         cleanup(-1);
         return hip_fail(err, "probe set-up");
     }
     const sgl_kv_device_buffer slots{slot_dev, rows * sizeof(uint64_t)};
+    const sgl_kv_device_buffer src_slots{static_cast<uint64_t *>(slot_dev) + rows, rows * sizeof(uint64_t)};
     sgl_kv_rows_view rv;
     memset(&rv, 0, sizeof rv);
-    uint8_t *p = static_cast<uint8_t *>(probe_rows->ptr);
-    rv.planes[0] = p;
-    rv.plane_bytes[0] = rows * rb0;
-    rv.row_stride[0] = rb0;
-    if (v.tensor_count == 2) {
-        rv.planes[1] = p + rows * rb0;
-        rv.plane_bytes[1] = rows * rb1;
-        rv.row_stride[1] = rb1;
+    if (!probe_source) {
+        uint8_t *p = static_cast<uint8_t *>(probe_rows->ptr);
+        rv.planes[0] = p;
+        rv.plane_bytes[0] = rows * rb0;
+        rv.row_stride[0] = rb0;
+        if (v.tensor_count == 2) {
+            rv.planes[1] = p + rows * rb0;
+            rv.plane_bytes[1] = rows * rb1;
+            rv.row_stride[1] = rb1;
+        }
+    }
+    sgl_kv_pool_view sv;
+    if (probe_source) {
+        sv = *probe_source;
+        sv.scale = nullptr;
     }
     for (size_t c = 0; c < bases.size() && rc == SGL_KV_OK; ++c) {
         sgl_kv_pool_view pv = v;
         pv.base = bases[c];
         pv.byte_len = byte_len;
         pv.scale = nullptr;  // the probe moves bytes only
-        // Each round packs the candidate's rows into probe_rows and unpacks
-        // them back, so that the timed unpack reads rows just written, as
-        // one that follows a transfer's pack or receive does; only the
-        // unpack is timed.
-        rc = sgl_rocm_kv_pack_layer(ctx, &pv, &slots, rows, &rv, s);  // warm-up
-        if (rc == SGL_KV_OK) rc = sgl_rocm_kv_unpack_layer(ctx, &rv, rows, &pv, &slots, s);
+        // Rows mode: each round packs the candidate's rows into probe_rows
+        // and unpacks them back, so that the timed unpack reads rows just
+        // written, as one that follows a transfer's pack or receive does;
+        // only the unpack is timed. Pool-to-pool mode: each round is one
+        // timed transfer from the source pool into the candidate.
+        auto prepare = [&]() {
+            return probe_source ? SGL_KV_OK : sgl_rocm_kv_pack_layer(ctx, &pv, &slots, rows, &rv, s);
+        };
+        auto timed = [&]() {
+            return probe_source ? sgl_rocm_kv_transfer_layer(ctx, &sv, &src_slots, rows, &pv, &slots, s)
+                                : sgl_rocm_kv_unpack_layer(ctx, &rv, rows, &pv, &slots, s);
+        };
+        rc = prepare();  // warm-up round
+        if (rc == SGL_KV_OK) rc = timed();
         float t[kProbeTimed];
         for (int i = 0; i < kProbeTimed && rc == SGL_KV_OK; ++i) {
-            if ((rc = sgl_rocm_kv_pack_layer(ctx, &pv, &slots, rows, &rv, s)) != SGL_KV_OK) break;
+            if ((rc = prepare()) != SGL_KV_OK) break;
             if ((err = hipEventRecord(ev[i], s)) != hipSuccess) break;
-            rc = sgl_rocm_kv_unpack_layer(ctx, &rv, rows, &pv, &slots, s);
+            rc = timed();
             if (rc == SGL_KV_OK && (err = hipEventRecord(ev[i + 1], s)) != hipSuccess) break;
             if (rc == SGL_KV_OK && (err = hipEventSynchronize(ev[i + 1])) != hipSuccess) break;
             if (rc == SGL_KV_OK && (err = hipEventElapsedTime(&t[i], ev[i], ev[i + 1])) != hipSuccess) break;

@@ -526,7 +526,8 @@ _EXPORTS = {
     "sgl_rocm_kv_pool_allocate": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(_PagedLayout),
                                                    ctypes.POINTER(ctypes.c_void_p)]),
     "sgl_rocm_kv_storage_allocate_placed": (ctypes.c_int32, [ctypes.c_void_p, _u64, _u64, ctypes.POINTER(PoolView),
-                                                             ctypes.POINTER(_DeviceBuffer), ctypes.c_uint32,
+                                                             ctypes.POINTER(_DeviceBuffer), ctypes.POINTER(PoolView),
+                                                             ctypes.c_uint32,
                                                              ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p),
                                                              ctypes.POINTER(_PlacementReport)]),
     "sgl_rocm_kv_storage_destroy": (ctypes.c_int32, [ctypes.c_void_p]),
@@ -1617,15 +1618,18 @@ class RocmKvStorage:
 
     @classmethod
     def allocate_placed(cls, kernels: "RocmKvPairCopyKernels", byte_len: int, page_size_bytes: int,
-                        probe_view: "PoolView", probe_rows: _DeviceBuffer, candidates: int,
-                        stream=None) -> tuple["RocmKvStorage", dict]:
+                        probe_view: "PoolView", probe_rows: _DeviceBuffer | None, candidates: int,
+                        stream=None, probe_source: "PoolView | None" = None) -> tuple["RocmKvStorage", dict]:
         """allocate(), keeping the fastest of `candidates` allocations for the
-        scatter `probe_view` describes (no counterpart in the reference).
-        Returns the storage and the probe report."""
+        scatter `probe_view` describes: an unpack from `probe_rows` (scratch),
+        or a pool-to-pool transfer from `probe_source` when given (no
+        counterpart in the reference). Returns the storage and the probe
+        report."""
         h = ctypes.c_void_p()
         r = _PlacementReport()
         _call(lib().sgl_rocm_kv_storage_allocate_placed, kernels._h, byte_len, page_size_bytes,
-              ctypes.byref(probe_view), ctypes.byref(probe_rows), candidates, _stream(stream),
+              ctypes.byref(probe_view), None if probe_rows is None else ctypes.byref(probe_rows),
+              None if probe_source is None else ctypes.byref(probe_source), candidates, _stream(stream),
               ctypes.byref(h), ctypes.byref(r))
         report = {"candidates": r.candidates, "chosen": r.chosen, "probe_rows": r.probe_rows,
                   "probe_us": [float(r.probe_us[i]) for i in range(r.candidates)]}

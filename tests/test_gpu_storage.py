@@ -535,3 +535,65 @@ def test_placed_allocation_probes_every_pool_form(k, form):
         np.testing.assert_array_equal(pool_scale.download(dtype=np.float32), [0.375])
         np.testing.assert_array_equal(back_scale.download(dtype=np.float32), [0.375])
     storage.close()
+
+
+def test_placed_allocation_probes_pool_to_pool(k):
+    """With a source pool's view instead of probe rows, each candidate is
+    timed on a pool-to-pool transfer from it; the source is only read, and
+    the kept pool then takes a transfer whose bytes equal the oracle's."""
+    _say("placed allocation, pool-to-pool probe")
+    L, H, D = 2, 2, 64
+    rb = H * D * 2
+    src_rt = kv.KvCacheRuntimeLayout("bf16", 1, L, H, D, 2, L * 2 * rb, L * 2 * rb)
+    dst_rt = kv.KvCacheRuntimeLayout("bf16", 16, L, H, D, 2, L * 2 * rb, 16 * L * 2 * rb)
+    src_l, dst_l = kv.PagedKvCacheLayout.new(src_rt, 4096), kv.PagedKvCacheLayout.new(dst_rt, 128)
+    src = kv.RocmKvStorage.allocate(k, src_l.total_byte_len, src_rt.page_size_bytes)
+    sb = src.allocation()
+    k.fill_synthetic(sb, 31)
+    hip.synchronize()
+    before = np.zeros(sb.byte_len, np.uint8)
+    hip.memcpy_async(before.ctypes.data, sb.ptr, sb.byte_len, "d2h")
+    hip.synchronize()
+    with pytest.raises(kv.KvError) as e:   # neither rows nor a source to probe with
+        kv.RocmKvStorage.allocate_placed(k, dst_l.total_byte_len, dst_rt.page_size_bytes,
+                                         dst_l.pool_view(0, dst_l.total_byte_len, 0), None, 2)
+    assert e.value.code == kv.INVALID_ARGUMENT and e.value.name == "probe_rows"
+    dst, rep = kv.RocmKvStorage.allocate_placed(
+        k, dst_l.total_byte_len, dst_rt.page_size_bytes, dst_l.pool_view(0, dst_l.total_byte_len, 0), None, 3,
+        probe_source=src_l.pool_view(sb.ptr, sb.byte_len, 0))
+    _say(f"placement report {rep}")
+    assert rep["candidates"] == 3 and rep["probe_rows"] == 2048 and min(rep["probe_us"]) > 0
+    assert rep["probe_us"][rep["chosen"]] == min(rep["probe_us"])
+    after = np.zeros(sb.byte_len, np.uint8)
+    hip.memcpy_async(after.ctypes.data, sb.ptr, sb.byte_len, "d2h")
+    hip.synchronize()
+    np.testing.assert_array_equal(after, before)   # the probe only read the source
+    db = dst.allocation()
+    got0 = np.zeros(db.byte_len, np.uint8)
+    hip.memcpy_async(got0.ctypes.data, db.ptr, db.byte_len, "d2h")
+    hip.synchronize()
+    assert not got0.any()
+    rng = np.random.default_rng(13)
+    n = 500
+    s_slots = rng.choice(4096, size=n, replace=False).astype(np.uint64)
+    d_slots = rng.choice(2048, size=n, replace=False).astype(np.uint64)
+    ss, ds = hip.DeviceBuffer.from_array(s_slots), hip.DeviceBuffer.from_array(d_slots)
+    for layer in range(L):
+        k.transfer_layer(src_l.pool_view(sb.ptr, sb.byte_len, layer), kv.device_buffer(ss.ptr, ss.nbytes), n,
+                         dst_l.pool_view(db.ptr, db.byte_len, layer), kv.device_buffer(ds.ptr, ds.nbytes))
+    hip.synchronize()
+    k.check_errors()
+    got = np.zeros(db.byte_len, np.uint8)
+    hip.memcpy_async(got.ctypes.data, db.ptr, db.byte_len, "d2h")
+    hip.synchronize()
+    src_lay = oracle.layout(1, L, 2, src_rt.bytes_per_token, src_rt.page_size_bytes, 4096)
+    dst_lay = oracle.layout(16, L, 2, dst_rt.bytes_per_token, dst_rt.page_size_bytes, 128)
+    want = np.zeros_like(got)
+    for layer in range(L):
+        def pool(lay, rt, pages):
+            offs = tuple(oracle.tensor_token_byte_range(lay, 0, layer, t, 0)[1][0] for t in range(2))
+            return oracle.Pool(rt.page_size, rt.page_size_bytes, pages, offs, rb, 2, H, False)
+        oracle.transfer(pool(src_lay, src_rt, 4096), before, s_slots, pool(dst_lay, dst_rt, 128), want, d_slots)
+    np.testing.assert_array_equal(got, want)
+    dst.close()
+    src.close()

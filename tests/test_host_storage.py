@@ -83,7 +83,7 @@ def test_storage_entry_points_reject_null_without_a_gpu():
     assert lib.sgl_rocm_kv_storage_clear(None) == kv.INVALID_ARGUMENT
     assert lib.sgl_rocm_kv_storage_validate_layout(None, None) == kv.INVALID_ARGUMENT
     assert lib.sgl_rocm_kv_memory_info(None, None, None) == kv.INVALID_ARGUMENT
-    assert lib.sgl_rocm_kv_storage_allocate_placed(None, 64, 64, None, None, 3, None,
+    assert lib.sgl_rocm_kv_storage_allocate_placed(None, 64, 64, None, None, None, 3, None,
                                                    ctypes.byref(out), None) == kv.INVALID_ARGUMENT
     assert out.value is None
 

@@ -31,7 +31,8 @@ paged-attention decode over the C2 decode pool (NHD or head-major pages),
 line carries its own metric (GB/s of K/V read). --config attn_mla does the
 same over the C4 pool in DeepSeek-V3's MLA form (K 576 / V 512 pair rows,
 128 query heads on one KV head); --config attn64 reads the C2 page table
-with head dims 64 (Llama-3.2-1B: 16 layers, 8 KV heads, 32 query heads) and
+with head dims 64 (Llama-3.2-1B: 16 layers, 8 KV heads, 32 query heads;
+attn64_hnd over head-major pages) and
 --config attn256 with head dims 256 (Qwen3.5's full-attention layers: 2 KV
 heads, 8 query heads; 16 layers).
 
@@ -103,6 +104,8 @@ DESCRIPTIONS = {
               "Llama-3.2-1B shape, 16 layers x 8 KV heads x 64, bf16, page_size-64 NHD pool with "
               "a random page table, 64 requests x 2048 tokens, one decode query each with 32 "
               "query heads",
+    "attn64_hnd": "paged-attention decode as attn64, over head-major (HND) pages (the layout the unpack "
+                  "writes for a relayouting decode pool)",
     "attn256": "paged-attention decode with head dims 256 over the C2 decode pool's page table: "
                "Qwen3.5 full-attention shape (the reference's qwen3_5 config: 2 KV heads x 256, "
                "8 query heads), 16 layers, bf16, page_size-64 NHD pool with a random page table, "
@@ -829,7 +832,7 @@ def _attention_geometry(config: str):
     360-369`) read by DeepSeek-V3's 128 heads at its qk head dim (192)."""
     if config == "attn_mla":
         return 61, 1, 576, 512, 64, 128, 1.0 / np.sqrt(192)
-    if config == "attn64":  # Llama-3.2-1B
+    if config in ("attn64", "attn64_hnd"):  # Llama-3.2-1B
         return 16, 8, 64, 64, 64, 32, 1.0 / np.sqrt(64)
     if config == "attn256":  # Qwen3.5's full-attention layers (model_registry.rs:628-660)
         return 16, 2, 256, 256, 64, 8, 1.0 / np.sqrt(256)
@@ -851,7 +854,7 @@ def attention_cpu_baseline(seconds: float, config: str):
     on a host pool holding just those pages."""
     import oracle
     import sgl_rocm_kv as kv
-    hnd = config == "attn_hnd"
+    hnd = config in ("attn_hnd", "attn64_hnd")
     L, H, dk, dv, P, qh, scale = _attention_geometry(config)
     n, nq = 2048, 2
     D = dk
@@ -898,11 +901,11 @@ def run_attention(args, config: str):
     import sgl_rocm_kv as kv
     from sgl_rocm_kv import hip
     from sgl_rocm_kv import workloads as wl
-    hnd, mla = config == "attn_hnd", config == "attn_mla"
+    hnd, mla = config in ("attn_hnd", "attn64_hnd"), config == "attn_mla"
     t = wl.c4() if mla else wl.c2()
     L, H, dk, dv, P, qh, scale = _attention_geometry(config)
     D = dk
-    assert t.dst.page_size == P and (config in ("attn64", "attn256") or t.shape.layers == L)
+    assert t.dst.page_size == P and (config in ("attn64", "attn64_hnd", "attn256") or t.shape.layers == L)
     nreq, n = len(t.lengths), int(t.lengths[0])
     layout = _attention_layout(kv, config, t.dst.page_count)
     k = kv.RocmKvPairCopyKernels(0)
@@ -966,11 +969,12 @@ def run_attention(args, config: str):
     k.close()
     latent = "sglkv_paged_attention_latent" if args.fast_weights else "sglkv_paged_attention_latent_exact"
     kernel = (latent + "+sglkv_paged_attention_combine_h" if mla
-              else ("sglkv_paged_attention_staged64" if D == 64 else "sglkv_paged_attention_staged256" if D == 256
+              else ("sglkv_paged_attention_staged64" if D == 64
+                    else "sglkv_paged_attention_staged256" if D == 256
                     else "sglkv_paged_attention_staged128k" if hnd else "sglkv_paged_attention_staged128")
               + "+sglkv_paged_attention_combine")
-    summary = "paged_attention_decode_" + ("mla" if mla else "hnd" if hnd else "dims64" if D == 64
-                                           else "dims256" if D == 256 else "nhd")
+    summary = "paged_attention_decode_" + ("mla" if mla else ("dims64_hnd" if hnd else "dims64") if D == 64
+                                           else "hnd" if hnd else "dims256" if D == 256 else "nhd")
     extra = {"requests": nreq, "tokens_per_request": n, "layers": L, "kv_heads": H,
              "query_heads": qh, "key_dim": dk, "value_dim": dv, "page_size": P,
              "head_layout": "HND" if hnd else "NHD",
@@ -1160,9 +1164,9 @@ def main():
               "c4fp8": lambda: wl.c4(fp8=True), "c4pair": wl.c4pair, "c4packed": wl.c4packed,
               "c5": wl.c5, "c2pages": wl.c2, "attn": wl.c2,
               "hnd64": wl.chunks64, "nhd64": lambda: wl.chunks64(head_major=False),
-              "attn_hnd": wl.c2, "attn_mla": wl.c4, "attn64": wl.c2, "attn256": wl.c2, "ceilings": wl.c2,
+              "attn_hnd": wl.c2, "attn_mla": wl.c4, "attn64": wl.c2, "attn64_hnd": wl.c2, "attn256": wl.c2, "ceilings": wl.c2,
               "c2direct": wl.c2}
-    attention = args.config in ("attn", "attn_hnd", "attn_mla", "attn64", "attn256")
+    attention = args.config in ("attn", "attn_hnd", "attn_mla", "attn64", "attn64_hnd", "attn256")
     t = makers[args.config]()
     log(f"workload {t.name}: {t.rows} tokens moved, payload {t.payload_bytes / 2**30:.2f} GiB")
     if args.config == "c5":
@@ -1184,7 +1188,7 @@ def main():
     gbs = r.pop("value")
     extra = r.pop("config_extra")
     out = {
-        "metric": ((MLA_METRIC if args.config == "attn_mla" else ATTN64_METRIC if args.config == "attn64"
+        "metric": ((MLA_METRIC if args.config == "attn_mla" else ATTN64_METRIC if args.config in ("attn64", "attn64_hnd")
                     else ATTN256_METRIC if args.config == "attn256" else ATTN_METRIC) if attention
                    else DIRECT_METRIC if args.config == "c2direct" else METRIC),
         "value": gbs,

@@ -409,6 +409,8 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
         which = d64 ? 8 : d256 ? 10 : 7;
         lds = SGLKV_ATTN_STAGED_LDS_BYTES(p.dk);
         // Head-major pages at dims 128: K in registers, V alone in LDS.
+        // (Dims 64 keep K in LDS: the same body with K in registers,
+        // 125 VGPRs, measured no faster on head-major pages.)
         if (which == 7 && lay.head_layout == SGL_KV_HND) {
             which = 11;
             lds = SGLKV_ATTN_KREG_LDS_BYTES(p.dk);
@@ -463,7 +465,10 @@ int32_t attention_enqueue(sgl_rocm_kv_ctx *ctx, const sgl_kv_attention_plan *pla
     //    before splitting, 128 for two or three (1 query 40.0 -> 33.2 us,
     //    2 queries 41.0 -> 35.2 us), 256 from four on (best there);
     //  - the other bodies keep 256 (not measured otherwise).
-    const uint64_t min_chunk = which == 11 ? 128 : which >= 7 ? 64 : which == 6 && base < 4 ? (base <= 1 ? 64 : 128) : 256;
+    const uint64_t min_chunk = which == 11                 ? 128
+                               : which >= 7                ? 64
+                               : which == 6 && base < 4    ? (base <= 1 ? 64 : 128)
+                                                           : 256;
     chunk = ceil_div(chunk < min_chunk ? min_chunk : chunk, SGLKV_ATTN_TOKENS) * SGLKV_ATTN_TOKENS;
     uint64_t splits = ceil_div(max_len, chunk);
     const uint64_t table = wide ? SGLKV_ATTN_WIDE_SLOTS : which >= 7 ? SGLKV_ATTN_STAGED_SLOTS : 0;

@@ -501,3 +501,22 @@ def test_row_counts_whose_last_tile_would_wrap_are_refused(rows):
         d = kv._ErrorDetail()
         lib.sgl_kv_last_error(ctypes.byref(d))
         assert d.name == b"row_count" and d.a == rows and d.b == 2**32 - 1 - 4096
+
+
+def test_header_compiles_as_c99_and_cpp17(tmp_path):
+    """include/sgl_rocm_kv.h is the C ABI a binding generator or a C caller
+    reads: it must compile on its own as strict C99 and as C++17, without a
+    warning."""
+    import shutil
+    import subprocess
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    inc = os.path.join(root, "include")
+    for compiler, std, ext in (("gcc", "c99", "c"), ("g++", "c++17", "cpp")):
+        if shutil.which(compiler) is None:
+            pytest.skip(f"{compiler} not found")
+        src = tmp_path / f"use_header.{ext}"
+        src.write_text('#include "sgl_rocm_kv.h"\nint main(void) { return (int)sizeof(sgl_kv_pool_view) == 0; }\n')
+        r = subprocess.run([compiler, f"-std={std}", "-Wall", "-Wextra", "-pedantic", "-Werror", "-I", inc,
+                            "-c", str(src), "-o", str(tmp_path / f"use_header_{ext}.o")],
+                           capture_output=True, text=True)
+        assert r.returncode == 0, r.stderr
